@@ -1,0 +1,231 @@
+/*
+ * sglang_neuron_amd — C ABI of the MI355X (gfx950) paged decode-attention path.
+ *
+ * The library is libsglang_neuron_amd.so, built with hipcc for gfx950 from sglang_neuron_amd/csrc/. Every
+ * function takes raw device pointers, int32/int64 sizes, and a hipStream_t passed as `void *`. Each returns an int
+ * status: SNA_OK (0), or a negative code with a message that sna_last_error() gives back on the calling thread.
+ * Nothing throws across the ABI, and no function allocates device memory. Kernels are enqueued on the caller's
+ * stream in call order, so a store followed by a decode on one stream sees the store. The library keeps no device
+ * state between calls; the only state is the thread-local error string.
+ *
+ * Conventions (sglang-neuron, reference paths under /root/reference/sglang_neuron):
+ *   - A token slot is page * page_size + offset; page = slot / page_size (attention/backend.py:6-7).
+ *   - Page 0 is reserved: a pool of `size` slots has size / page_size + 1 pages (mem_cache/memory_pool.py:20-21,
+ *     106-107).
+ *   - Block tables are int32 [B, width] with -1 past a row's pages (attention/backend.py:114-130).
+ *   - seq_lens count the prefix plus the new token (attention/backend.py:36). The new token sits at position
+ *     seq_len - 1 and is attended in-band, as the reference appends it (attention_decode_paged.py:167-169,
+ *     attention_decode.py:262-269).
+ *   - MHA caches are head-major, [num_blocks, kv_heads, page_size, head_dim] (memory_pool.py:186-191). FP8 K is
+ *     stored unpacked (fp8_packed_k = False; the reference's packed [.., page/2, d, 2] K is a Trainium-kernel
+ *     layout, attention_decode.py:207-223).
+ *   - FP8 is OCP e4m3fn. A stored value is e4m3fn_RNE(clamp(float(x) / s, -448, 448)), where s is the
+ *     dequantization scale (swa_fused.py:73-75, qkv.py:69-70, mla_decode_attention_torch.py:216-220).
+ */
+#ifndef SGLANG_NEURON_AMD_H_
+#define SGLANG_NEURON_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---- */
+#define SNA_OK 0
+#define SNA_ERR_INVALID_ARGUMENT (-1) /* a null pointer, a bad shape or size, an unsupported combination */
+#define SNA_ERR_WORKSPACE (-2)        /* the workspace is smaller than the plan needs */
+#define SNA_ERR_LAUNCH (-3)           /* the HIP runtime refused a launch */
+#define SNA_ERR_UNSUPPORTED (-4)      /* a dtype or head layout this build has no kernel for */
+
+/* ---- dtypes of cache storage ---- */
+#define SNA_DTYPE_BF16 0
+#define SNA_DTYPE_FP8_E4M3FN 1
+
+/* Library ABI version (major * 100 + minor). */
+int sna_version(void);
+
+/* The message of the calling thread's last failing call ("" if none). The pointer is valid until the thread's
+ * next call into the library. */
+const char *sna_last_error(void);
+
+/* =====================================================================================================
+ * KV-pool stores
+ * ===================================================================================================== */
+
+/* Store one token per entry of `slots` into an MHA pool layer.
+ *   k, v        [n_tokens, num_kv_heads, head_dim] bf16, contiguous.
+ *   slots       [n_tokens] int64 token slots. A slot < 0 or >= num_blocks * page_size is written to slot 0, the
+ *               reserved padding page (attention_decode.py:288-291; transformer/model.py:99-102).
+ *   k_scale, v_scale
+ *               [num_kv_heads] fp32 dequantization scales. Required for an FP8 cache and ignored for bf16.
+ *   k_cache, v_cache
+ *               [num_blocks, num_kv_heads, page_size, head_dim], of dtype cache_dtype.
+ * FP8 cache: byte = e4m3fn_RNE(clamp(float(x) / scale[h], +-448)), bit-exact with the reference's quantize-then-cast
+ * (attention_decode.py:259-260, qkv.py:69-79). bf16 cache: a copy (attention_decode_paged.py:174-176).
+ * Replaces: the pool write that the reference's compiled graphs do. The reference pool's own set_kv_buffer refuses
+ * (mem_cache/memory_pool.py:178-179); this is upstream SGLang's
+ * MHATokenToKVPool.set_kv_buffer(layer, loc, cache_k, cache_v, k_scale, v_scale) for this pool layout. */
+int sna_kv_store_mha(const void *k, const void *v, const int64_t *slots, int64_t n_tokens, const float *k_scale,
+                     const float *v_scale, void *k_cache, void *v_cache, int64_t num_blocks, int32_t num_kv_heads,
+                     int32_t page_size, int32_t head_dim, int32_t cache_dtype, void *stream);
+
+/* Per-head absmax scales, s[h] = max |x[:, h, :]| / 448, or 1 for an all-zero head.
+ *   x         [n_tokens, num_heads, head_dim] bf16.
+ *   scale_out [num_heads] fp32.
+ *   workspace at least sna_absmax_workspace_bytes(n_tokens, num_heads) bytes of device memory.
+ * This has no reference counterpart. The reference's FP8 KV scale is one per-tensor value from the checkpoint
+ * (gpt_oss/mxfp4/common.py:475-487), while the per-KV-head calibration is this path's extension. */
+int64_t sna_absmax_workspace_bytes(int64_t n_tokens, int32_t num_heads);
+int sna_kv_absmax_scale(const void *x, int64_t n_tokens, int32_t num_heads, int32_t head_dim, float *scale_out,
+                        void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Store absorbed-MLA compact rows [latent(512) | k_pe(64)] into an MLA pool layer with one scale per token.
+ *   rows      [n_tokens, row_dim] bf16, with row_dim = 576 (deepseek_v2/model.py:101-111 builds them).
+ *   slots     [n_tokens] int64. Out-of-pool or negative slots go to slot 0 (deepseek_v2/model.py:64-70).
+ *   cache     [num_slots, row_dim] of cache_dtype (FP8: uint8 storage, memory_pool.py:313-315).
+ *   row_scale [num_slots] fp32. FP8: written with s_t = max|row_t| / 448 (or 1 for a zero row), and each byte is
+ *             e4m3fn_RNE(clamp(x / s_t)). Ignored for bf16.
+ * Replaces: _write_rows (deepseek_v2/model.py:64-70); the pool's set_mla_kv_buffer refuses in the reference
+ * (memory_pool.py:417-418). Per-token scales are this path's extension (the reference has none). */
+int sna_kv_store_mla(const void *rows, const int64_t *slots, int64_t n_tokens, int32_t row_dim, void *cache,
+                     float *row_scale, int64_t num_slots, int32_t cache_dtype, void *stream);
+
+/* Quantize, pack and scatter DSA cache rows in the reference's 640-byte layout:
+ *   bytes [0, 128)   k_pe: 64 bf16 = bf16_RNE(x / kv_scale)
+ *   bytes [128, 640) latent: 512 e4m3fn = e4m3fn_RNE(clamp(x / kv_scale)); latent dim c = 256a + 128b + p is at byte
+ *                    128 + 256a + 2p + b (kv_row_layout.py:62-84).
+ *   rows   [n_tokens, 576] bf16 in [k_pe(64) | latent(512)] order (mla_decode_attention_torch.py:42).
+ *   slots  [n_tokens] int64 flat row ids. A slot < 0 or >= num_rows is skipped (_scatter,
+ *          mla_decode_attention_torch.py:193-201).
+ *   cache  [num_rows, 640] uint8.
+ * Replaces: pack_kv_rows + _scatter (mla_decode_attention_torch.py:193-221). */
+int sna_kv_store_dsa(const void *rows, const int64_t *slots, int64_t n_tokens, float kv_scale, void *cache,
+                     int64_t num_rows, void *stream);
+
+/* =====================================================================================================
+ * Split-K planning (host side; no device access)
+ * ===================================================================================================== */
+
+/* The split plan of a decode launch. `split_tiles` is how many key tiles each split covers. `n_work` is the number of
+ * (sequence, split) items, which is what the workspace holds. */
+typedef struct {
+  int32_t split_tiles;
+  int32_t n_work;
+  int32_t tile;         /* keys per tile of the kernel family: 32 (GQA) or 16 (MLA, DSA) */
+  int32_t target_ctas;  /* the workgroup count the plan aimed for */
+} sna_split_plan;
+
+/* Plan a decode from host copies of seq_lens (exact) or, with host_seq_lens == NULL, from an upper bound
+ * max_seq_len for every row (then n_work bounds the device's count and the workspace is sized for it).
+ * `kind`: 0 GQA, 1 MLA, 2 DSA. For DSA, seq_lens are ignored: `n_keys_per_row` (the index-list length) is the
+ * row's key count. `window` is the sliding window (0 = full). `ctas_per_item` is the number of workgroups that
+ * one (sequence, split) item launches: num_kv_heads for GQA, and 1 for MLA and DSA. `num_cus` is the device's CU
+ * count (0 = 256). Returns SNA_OK and fills *plan. Host and device seq_lens must agree: a device length past the
+ * host's leaves its extra splits unread, though all reads stay inside the workspace. */
+int sna_plan_decode(int32_t kind, const int32_t *host_seq_lens, int32_t B, int32_t max_seq_len, int32_t window,
+                    int32_t n_keys_per_row, int32_t ctas_per_item, int32_t num_cus, sna_split_plan *plan);
+
+/* Workspace bytes a decode with this plan needs: n_work * heads * (head_dim_v + 2) * 4. */
+int64_t sna_decode_workspace_bytes(const sna_split_plan *plan, int32_t num_q_heads, int32_t head_dim_v);
+
+/* =====================================================================================================
+ * Decode attention
+ * ===================================================================================================== */
+
+/* GQA paged decode over an MHA pool layer, with the step's own token attended in-band and optionally stored.
+ *   q            [B, num_q_heads, head_dim] bf16 (after projection, QK norm and RoPE).
+ *   k_cache, v_cache
+ *                [num_blocks, num_kv_heads, page_size, head_dim] of cache_dtype.
+ *   k_scale, v_scale
+ *                [num_kv_heads] fp32 dequantization scales (FP8 only; NULL for bf16).
+ *   block_table  [B, table_stride] int32, of which `table_width` columns are valid; -1 marks no page.
+ *   seq_lens     [B] int32, prefix plus the new token (>= 1).
+ *   k_new, v_new [B, num_kv_heads, head_dim] bf16: the step's token. With an FP8 cache it is attended as
+ *                dequant(quant(x)), the value the store writes (attention_decode.py:259-269).
+ *   new_slots    [B] int64 or NULL. If not NULL, the combine pass also stores k_new / v_new at these slots,
+ *                bit-exact with sna_kv_store_mha. Positions < seq_len - 1 are read, so the store never races the
+ *                reads.
+ *   sinks        [num_q_heads] fp32 or NULL. exp(sink_h - max) joins the softmax denominator
+ *                (attention_decode.py:274-275).
+ *   window       0 for full attention, or W > 0: keys at positions [seq_len - W, seq_len - 1], the new one
+ *                included (gpt_oss/attention_masks.py:47-52; swa_fused.py:115).
+ *   sm_scale     softmax scale applied to q.k (dequantized k).
+ *   out          [B, num_q_heads, head_dim] bf16.
+ *   plan, workspace
+ *                from sna_plan_decode(kind 0) and at least sna_decode_workspace_bytes(plan, num_q_heads, head_dim).
+ * A key at position p < seq_len - 1 is visible iff its table entry is >= 0, lies in [0, num_blocks), and p is in
+ * the window. This is the reference's mask (attention_decode_paged.py:165-166, attention_decode_mask.py:64-81).
+ * Scores, softmax and accumulation are fp32. The group num_q_heads / num_kv_heads must be <= 16.
+ * Replaces: the attention core of _torch_attention_decode_paged (attention_decode_paged.py:159-177) and of
+ * _torch_attention_decode (attention_decode.py:259-300), which nkilib's attention_block_tkg runs on Trainium
+ * (attention_decode_paged.py:63-126). */
+int sna_paged_decode_gqa(const void *q, const void *k_cache, const void *v_cache, const float *k_scale,
+                         const float *v_scale, const int32_t *block_table, int64_t table_stride, int32_t table_width,
+                         const int32_t *seq_lens, const void *k_new, const void *v_new, const int64_t *new_slots,
+                         const float *sinks, int32_t window, float sm_scale, void *out, int32_t B,
+                         int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                         int64_t num_blocks, int32_t cache_dtype, const sna_split_plan *plan, void *workspace,
+                         int64_t workspace_bytes, void *stream);
+
+/* Absorbed-MLA paged decode over an MLA pool layer of compact rows [latent(512) | k_pe(64)].
+ *   ql_nope      [B, num_heads, 512] bf16 (W_UK folded in); q_pe [B, num_heads, 64] bf16 (RoPE'd).
+ *   cache        [num_blocks * page_size, 576] of cache_dtype; row_scale [num_blocks * page_size] fp32 (FP8).
+ *   block_table, seq_lens
+ *                as for GQA. History keys are positions < seq_len - 1 (mla.py:48-50).
+ *   compact_new  [B, 576] bf16: the step's own row, attended in-band as dequant(quant(row)) with its own
+ *                per-token scale.
+ *   new_slots    [B] int64 or NULL: also store compact_new there, bit-exact with sna_kv_store_mla.
+ *   out          [B, num_heads, 512] bf16. Scores are fp32 sm_scale * (ql_nope . latent + q_pe . k_pe), softmax is
+ *                fp32, out = probs . latent.
+ * Replaces: mla_decode (ops/attention/mla.py:32-53). On Trainium that is paged_absorbed_mla
+ * (nki/deepseek_mla_decode.py:510-557). */
+int sna_mla_decode(const void *ql_nope, const void *q_pe, const void *cache, const float *row_scale,
+                   const int32_t *block_table, int64_t table_stride, int32_t table_width, const int32_t *seq_lens,
+                   const void *compact_new, const int64_t *new_slots, float sm_scale, void *out, int32_t B,
+                   int32_t num_heads, int32_t page_size, int64_t num_blocks, int32_t cache_dtype,
+                   const sna_split_plan *plan, void *workspace, int64_t workspace_bytes, void *stream);
+
+/* DSA sparse absorbed-MLA decode over 640-byte packed rows (one query token per sequence, one CP rank).
+ *   q_absorbed   [B, num_heads, 512] bf16; q_pe [B, num_heads, 64] bf16.
+ *   cache        [num_blocks * page_size, 640] uint8 (sna_kv_store_dsa's layout); kv_scale is per tensor.
+ *   indices      [B, n_indices] int32 global token positions; < 0 entries are empty.
+ *   block_table  [B, table_stride] int32 (logical block -> physical block); `table_width` valid columns.
+ *   positions    [B] int32, the query token's absolute position.
+ *   own_rows     [B, 576] bf16 in [k_pe | latent] order: the step's rows, attended in-band from their packed bytes
+ *                (mla_decode_attention_torch.py:181-190). The caller stores them first with sna_kv_store_dsa, so an
+ *                index equal to a row's own position reads the stored row, as in the reference (steps 0-1 precede
+ *                the gather there).
+ *   ctx_out      [B, num_heads, 512] bf16; lse_out [B, num_heads] fp32 (natural log), or NULL.
+ * Position pos resolves to row table[pos / page_size] * page_size + pos % page_size. It is dropped when pos < 0,
+ * its block is outside the table or unallocated, or the row is outside the cache. A resolved key is kept iff
+ * pos <= position, and the own row always is.
+ * Replaces: mla_decode_attention_torch_ref with spec = 1, cp_degree = 1 (mla_decode_attention_torch.py:38-130).
+ * On Trainium that is mla_decode_attention (models/glm52/kernels/decode/attention/mla/mla_decode_attention.py:207). */
+int sna_mla_decode_sparse(const void *q_absorbed, const void *q_pe, const void *cache, float kv_scale,
+                          const int32_t *indices, int32_t n_indices, const int32_t *block_table, int64_t table_stride,
+                          int32_t table_width, const int32_t *positions, const void *own_rows, float sm_scale,
+                          void *ctx_out, float *lse_out, int32_t B, int32_t num_heads, int32_t page_size,
+                          int64_t num_blocks, const sna_split_plan *plan, void *workspace, int64_t workspace_bytes,
+                          void *stream);
+
+/* Log-sum-exp merge of partial attention results, e.g. one per decode-context-parallel rank:
+ *   o_parts   [n_parts, n_rows, dim] fp32, each normalized by its own softmax sum.
+ *   lse_parts [n_parts, n_rows] fp32 natural-log LSE (-inf for an empty part).
+ *   out       [n_rows, dim] bf16 = sum_i exp(lse_i - LSE) o_i, LSE = logsumexp_i lse_i. lse_out [n_rows] or NULL.
+ * Replaces: the DCP merge (attention_decode.py:277-285) and the CP softmax combine of
+ * models/glm52/kernels/decode/attention_layer.py:653. */
+int sna_lse_combine(const float *o_parts, const float *lse_parts, int32_t n_parts, int64_t n_rows, int32_t dim,
+                    void *out, float *lse_out, void *stream);
+
+/* ---- diagnostics ---- */
+
+/* Decode n e4m3fn bytes to bf16 bits with the conversion instruction the decode kernels use for gathered pages. It
+ * lets a test compare that instruction with the exact decoding on all 256 byte values. */
+int sna_diag_fp8_to_bf16(const uint8_t *in, uint16_t *out, int64_t n, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SGLANG_NEURON_AMD_H_ */

@@ -1,0 +1,107 @@
+"""ctypes binding of libsglang_neuron_amd.so (the C ABI declared in include/sglang_neuron_amd.h).
+
+torch is imported first on purpose: the library links libamdhip64.so.7, and with torch's copy of that runtime already
+loaded under the same soname, the dynamic loader binds the library to it, so torch's streams and allocations are valid
+in the library's calls. There is no fallback: a missing library raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch  # noqa: F401  (see the module docstring)
+
+LIB_PATH = Path(__file__).resolve().parent / "libsglang_neuron_amd.so"
+
+SNA_OK = 0
+SNA_ERR_INVALID_ARGUMENT = -1
+SNA_ERR_WORKSPACE = -2
+SNA_ERR_LAUNCH = -3
+SNA_ERR_UNSUPPORTED = -4
+
+DTYPE_BF16 = 0
+DTYPE_FP8_E4M3FN = 1
+
+KIND_GQA = 0
+KIND_MLA = 1
+KIND_DSA = 2
+
+
+class SplitPlan(ctypes.Structure):
+    """sna_split_plan."""
+
+    _fields_ = [("split_tiles", ctypes.c_int32), ("n_work", ctypes.c_int32), ("tile", ctypes.c_int32),
+                ("target_ctas", ctypes.c_int32)]
+
+    def __repr__(self) -> str:
+        return (f"SplitPlan(split_tiles={self.split_tiles}, n_work={self.n_work}, tile={self.tile}, "
+                f"target_ctas={self.target_ctas})")
+
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+_F32 = ctypes.c_float
+
+# name -> (restype, argtypes); the exact declarations of include/sglang_neuron_amd.h
+SIGNATURES = {
+    "sna_version": (_I32, []),
+    "sna_last_error": (ctypes.c_char_p, []),
+    "sna_kv_store_mha": (_I32, [_P, _P, _P, _I64, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P]),
+    "sna_absmax_workspace_bytes": (_I64, [_I64, _I32]),
+    "sna_kv_absmax_scale": (_I32, [_P, _I64, _I32, _I32, _P, _P, _I64, _P]),
+    "sna_kv_store_mla": (_I32, [_P, _P, _I64, _I32, _P, _P, _I64, _I32, _P]),
+    "sna_kv_store_dsa": (_I32, [_P, _P, _I64, _F32, _P, _I64, _P]),
+    "sna_plan_decode": (_I32, [_I32, _P, _I32, _I32, _I32, _I32, _I32, _I32, ctypes.POINTER(SplitPlan)]),
+    "sna_decode_workspace_bytes": (_I64, [ctypes.POINTER(SplitPlan), _I32, _I32]),
+    "sna_paged_decode_gqa": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _I32, _F32, _P, _I32,
+                                    _I32, _I32, _I32, _I32, _I64, _I32, ctypes.POINTER(SplitPlan), _P, _I64, _P]),
+    "sna_mla_decode": (_I32, [_P, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _F32, _P, _I32, _I32, _I32, _I64, _I32,
+                              ctypes.POINTER(SplitPlan), _P, _I64, _P]),
+    "sna_mla_decode_sparse": (_I32, [_P, _P, _P, _F32, _P, _I32, _P, _I64, _I32, _P, _P, _F32, _P, _P, _I32, _I32,
+                                     _I32, _I64, ctypes.POINTER(SplitPlan), _P, _I64, _P]),
+    "sna_lse_combine": (_I32, [_P, _P, _I32, _I64, _I32, _P, _P, _P]),
+    "sna_diag_fp8_to_bf16": (_I32, [_P, _P, _I64, _P]),
+}
+
+_lib = None
+
+
+class SnaError(RuntimeError):
+    """A launch the HIP runtime refused."""
+
+
+def load(path: os.PathLike | str | None = None) -> ctypes.CDLL:
+    """The loaded library, with every declared symbol typed. Raises if it is not built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise FileNotFoundError(f"{p} is not built: run `python -m sglang_neuron_amd.build` (hipcc, gfx950)")
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    msg = load().sna_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    """Map a status code to the exception the reference raises for the same condition (ValueError for bad inputs,
+    RuntimeError for launch failures)."""
+    if rc == SNA_OK:
+        return
+    msg = last_error() or f"{what} failed with status {rc}"
+    if rc in (SNA_ERR_INVALID_ARGUMENT, SNA_ERR_WORKSPACE, SNA_ERR_UNSUPPORTED):
+        raise ValueError(msg)
+    raise SnaError(msg)

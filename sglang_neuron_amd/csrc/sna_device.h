@@ -1,0 +1,212 @@
+// Device helpers shared by the KV-store and decode kernels (gfx950 / CDNA4).
+//
+// Number formats follow the public specifications, not any library's code:
+//   * bf16   : IEEE binary32 with the low 16 mantissa bits dropped; float -> bf16 rounds to nearest even.
+//   * e4m3fn : OCP FP8 E4M3 ("fn": no infinities, one NaN code per sign, 0x7F / 0xFF). Bias 7, 3 mantissa bits,
+//              max finite 448 = 1.75 * 2^8, min normal 2^-6, subnormals m * 2^-9.
+// The store's arithmetic is  q = e4m3fn_RNE(clamp(float(x_bf16) / s, -448, 448))  with an IEEE-correct fp32
+// division (the HIP default; this code is never built with fast-math).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sna {
+
+constexpr float kFp8Max = 448.0f;
+constexpr float kLog2e = 1.4426950408889634f;
+// Running-max sentinel: finite, so exp2(m_old - m_new) never evaluates (-inf) - (-inf).
+constexpr float kNegBig = -1.0e30f;
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// float -> bf16 bits, round to nearest even; NaN -> 0x7FC0.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// float -> e4m3fn byte, round to nearest even. A magnitude that rounds above 448 (infinity included) and NaN give
+// the NaN code with the input's sign, which is what a plain cast does; the store clamps first, so only NaN reaches
+// that branch there.
+__device__ __forceinline__ uint32_t f32_to_e4m3fn(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;
+  if (a < 0x3c800000u) {
+    // |x| < 2^-6: the subnormal grid has step 2^-9. |x| * 512 is exact; rint rounds half to even. A result of 8 is
+    // the encoding of 2^-6 (exponent 1, mantissa 0), so the carry into the exponent is free.
+    return sign | (uint32_t)__builtin_rintf(__uint_as_float(a) * 512.0f);
+  }
+  // Normal: keep 3 of 23 mantissa bits with round-half-even at bit 20, then rebias the exponent 127 -> 7
+  // (120 << 3 = 960). A mantissa carry moves into the exponent by the addition itself.
+  uint32_t r = ((a + 0x7ffffu + ((a >> 20) & 1u)) >> 20) - 960u;
+  if (r > 0x7eu) return sign | 0x7fu;
+  return sign | r;
+}
+
+// e4m3fn byte -> float (exact).
+__device__ __forceinline__ float e4m3fn_to_f32(uint32_t b) {
+  const uint32_t sign = (b & 0x80u) << 24;
+  const uint32_t e = (b >> 3) & 0xfu;
+  const uint32_t m = b & 7u;
+  if (e == 15u && m == 7u) return __uint_as_float(sign | 0x7fc00000u);
+  if (e == 0u) return __uint_as_float(sign | __float_as_uint((float)m * 0.001953125f));  // m * 2^-9
+  return __uint_as_float(sign | ((e + 120u) << 23) | (m << 20));
+}
+
+// NaN-preserving clamp to the e4m3fn range: comparisons with NaN are false, so NaN passes through.
+__device__ __forceinline__ float clamp_fp8(float x) {
+  return x > kFp8Max ? kFp8Max : (x < -kFp8Max ? -kFp8Max : x);
+}
+
+// The store's quantizer: one bf16 element (its bits) and the dequantization scale s.
+__device__ __forceinline__ uint32_t quantize_e4m3fn(uint32_t bf16_bits, float s) {
+  return f32_to_e4m3fn(clamp_fp8(bf16_bits_to_f32(bf16_bits) / s));
+}
+
+// The scale rule for per-head and per-token scales: absmax / 448, or 1 for an all-zero operand (whose bytes are then
+// all zero), so no division by zero can happen.
+__device__ __forceinline__ float scale_from_absmax(float amax) { return amax > 0.0f ? amax / kFp8Max : 1.0f; }
+
+// Slot sanitising of the MHA pool write and of the MLA row write: a negative slot or one past the pool goes to
+// slot 0, the reserved padding page.
+__device__ __forceinline__ int64_t redirect_slot(int64_t slot, int64_t num_slots) {
+  return (slot < 0 || slot >= num_slots) ? 0 : slot;
+}
+
+// ---- MFMA operand types (gfx950) ----
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Four e4m3fn bytes of a dword to four bf16 values in order (bytes 0..3). Exact: every e4m3fn value is a bf16 value.
+__device__ __forceinline__ void fp8x4_to_bf16x4(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+  bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
+  lo = __builtin_bit_cast(uint32_t, a);
+  hi = __builtin_bit_cast(uint32_t, b);
+}
+
+// Two floats to a packed pair of bf16 (round to nearest even), low half first.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  bf16x2_t v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ f32x4_t mfma_16x16x32_bf16(const uint32_t (&a)[4], const uint32_t (&b)[4], f32x4_t c) {
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  u32x4_t av = {a[0], a[1], a[2], a[3]};
+  u32x4_t bv = {b[0], b[1], b[2], b[3]};
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av), __builtin_bit_cast(bf16x8_t, bv),
+                                                  c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4_t mfma_16x16x16_bf16(const uint32_t (&a)[2], const uint32_t (&b)[2], f32x4_t c) {
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  u32x2_t av = {a[0], a[1]};
+  u32x2_t bv = {b[0], b[1]};
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, av), __builtin_bit_cast(s16x4_t, bv),
+                                                    c, 0, 0, 0);
+}
+
+// 16-, 8- and 4-byte global loads of raw bits.
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ uint2 ld8(const void* p) { return *reinterpret_cast<const uint2*>(p); }
+__device__ __forceinline__ uint32_t ld4(const void* p) { return *reinterpret_cast<const uint32_t*>(p); }
+
+// Wave64 reductions across the four 16-lane groups (lanes l, l^16, l^32, l^48 hold the same MFMA column).
+__device__ __forceinline__ float max_across_groups(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+__device__ __forceinline__ float sum_across_groups(float v) {
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+// ---- split-K work decomposition ----
+// Sequence b's keys from the pool are positions [lo_b, hi_b): hi_b = seq_len_b - 1 (the step's own token is attended
+// in-band by the combine pass), lo_b = max(0, seq_len_b - window) for a sliding window of `window` keys (the new one
+// included), else 0. Keys are processed in tiles of TILE positions aligned to absolute position multiples of TILE;
+// a split is `split_tiles` consecutive tiles. The flattened work index runs over (sequence, split) in sequence order.
+struct KeyRange {
+  int32_t lo, hi;
+};
+
+__device__ __forceinline__ KeyRange key_range(int32_t seq_len, int32_t window) {
+  KeyRange r;
+  r.hi = seq_len - 1;
+  r.lo = (window > 0 && seq_len - window > 0) ? seq_len - window : 0;
+  if (r.hi < r.lo) r.hi = r.lo;
+  return r;
+}
+
+template <int TILE>
+__device__ __forceinline__ int32_t splits_of(int32_t seq_len, int32_t window, int32_t split_tiles) {
+  if (seq_len <= 1) return 0;
+  KeyRange r = key_range(seq_len, window);
+  if (r.hi <= r.lo) return 0;
+  int32_t t0 = r.lo / TILE, t1 = (r.hi + TILE - 1) / TILE;
+  return (t1 - t0 + split_tiles - 1) / split_tiles;
+}
+
+// Wave-cooperative search: the (sequence, split) of flattened work index w, and the sequence's first work index.
+// Every lane of the calling wave returns the same values; b = -1 when w is past the last split.
+template <int TILE>
+__device__ __forceinline__ void locate_work(const int32_t* __restrict__ seq_lens, int32_t B, int32_t window,
+                                            int32_t split_tiles, int32_t w, int32_t& b_out, int32_t& split_out) {
+  const int lane = threadIdx.x & 63;
+  int32_t base = 0;
+  b_out = -1;
+  split_out = 0;
+  for (int32_t b0 = 0; b0 < B; b0 += 64) {
+    int32_t b = b0 + lane;
+    int32_t n = b < B ? splits_of<TILE>(seq_lens[b], window, split_tiles) : 0;
+    // inclusive scan over the wave
+    int32_t incl = n;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      int32_t t = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += t;
+    }
+    int32_t excl = incl - n;
+    int32_t total = __shfl(incl, 63, 64);
+    if (w < base + total) {
+      bool mine = (w >= base + excl) && (w < base + incl);
+      unsigned long long ballot = __ballot(mine);
+      int src = __ffsll((long long)ballot) - 1;
+      int32_t e = __shfl(excl, src, 64);
+      b_out = b0 + src;
+      split_out = w - base - e;
+      return;
+    }
+    base += total;
+  }
+}
+
+// First flattened work index of sequence b (same decomposition), computed by one wave.
+template <int TILE>
+__device__ __forceinline__ int32_t work_base_of(const int32_t* __restrict__ seq_lens, int32_t b, int32_t window,
+                                                int32_t split_tiles) {
+  const int lane = threadIdx.x & 63;
+  int32_t acc = 0;
+  for (int32_t b0 = 0; b0 < b; b0 += 64) {
+    int32_t bb = b0 + lane;
+    int32_t n = bb < b ? splits_of<TILE>(seq_lens[bb], window, split_tiles) : 0;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) n += __shfl_xor(n, off, 64);
+    acc += n;
+  }
+  return acc;
+}
+
+}  // namespace sna

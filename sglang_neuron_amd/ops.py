@@ -1,0 +1,349 @@
+"""Tensor-level entry points of the HIP path. Each checks shapes, dtypes and devices on the host, then calls the C ABI
+on torch's current stream. There is no CPU or eager fallback: without the built library, or with CPU tensors, these
+raise.
+
+Reference interfaces each function stands in for are cited per function (paths under
+/root/reference/sglang_neuron).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence, Union
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+FP8 = torch.float8_e4m3fn
+_cu_count: dict[int, int] = {}
+
+
+def _ptr(t: Optional[Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _num_cus(device: torch.device) -> int:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _cu_count:
+        _cu_count[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return _cu_count[idx]
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _on_gpu(*ts: Optional[Tensor]) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        _need(t.is_cuda, "the HIP path takes device tensors (got a CPU tensor); there is no CPU fallback")
+        if dev is None:
+            dev = t.device
+        _need(t.device == dev, f"tensors on {t.device} and {dev}")
+    assert dev is not None
+    return dev
+
+
+def _contig(t: Tensor, name: str, dtype: Optional[torch.dtype] = None) -> Tensor:
+    if dtype is not None:
+        _need(t.dtype == dtype, f"{name} must be {dtype}, got {t.dtype}")
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def cache_dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.bfloat16:
+        return _lib.DTYPE_BF16
+    if dtype in (FP8, torch.uint8):
+        return _lib.DTYPE_FP8_E4M3FN
+    raise ValueError(f"unsupported cache dtype {dtype} (bf16 or float8_e4m3fn)")
+
+
+# ------------------------------------------------------------------------------------------------------------------
+# stores
+# ------------------------------------------------------------------------------------------------------------------
+
+def kv_store_mha(k: Tensor, v: Tensor, slots: Tensor, k_cache: Tensor, v_cache: Tensor,
+                 k_scale: Optional[Tensor] = None, v_scale: Optional[Tensor] = None) -> None:
+    """Write the tokens' K/V [T, kv_heads, d] bf16 into one layer's caches [blocks, kv_heads, page, d] at ``slots``
+    [T] (int64); FP8 caches quantize with the per-head dequantization scales [kv_heads]. Out-of-pool slots write slot
+    0, as the reference's write does (ops/attention/attention_decode.py:288-300)."""
+    dev = _on_gpu(k, v, slots, k_cache, v_cache, k_scale, v_scale)
+    nb, G, P, d = k_cache.shape
+    _need(v_cache.shape == k_cache.shape and v_cache.dtype == k_cache.dtype, "K and V caches differ")
+    k = _contig(k.reshape(-1, G, d), "k", torch.bfloat16)
+    v = _contig(v.reshape(-1, G, d), "v", torch.bfloat16)
+    _need(k.shape == v.shape, f"k {tuple(k.shape)} and v {tuple(v.shape)} differ")
+    slots = _contig(slots.reshape(-1).to(torch.int64), "slots")
+    _need(slots.numel() == k.shape[0], f"{slots.numel()} slots for {k.shape[0]} tokens")
+    code = cache_dtype_code(k_cache.dtype)
+    if code == _lib.DTYPE_FP8_E4M3FN:
+        _need(k_scale is not None and v_scale is not None, "an FP8 cache needs k_scale and v_scale")
+        k_scale = _contig(k_scale.reshape(-1).float(), "k_scale")
+        v_scale = _contig(v_scale.reshape(-1).float(), "v_scale")
+        _need(k_scale.numel() == G and v_scale.numel() == G, f"scales must have {G} entries (one per KV head)")
+    _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
+    rc = _lib.load().sna_kv_store_mha(_ptr(k), _ptr(v), _ptr(slots), k.shape[0], _ptr(k_scale), _ptr(v_scale),
+                                      _ptr(k_cache), _ptr(v_cache), nb, G, P, d, code, _stream(dev))
+    _lib.check(rc, "kv_store_mha")
+
+
+def kv_absmax_scale(x: Tensor) -> Tensor:
+    """Per-head dequantization scales [H] fp32 of x [T, H, d] bf16: absmax / 448, or 1 for an all-zero head."""
+    dev = _on_gpu(x)
+    _need(x.dim() == 3, f"x must be [T, H, d], got {tuple(x.shape)}")
+    x = _contig(x, "x", torch.bfloat16)
+    T, H, d = x.shape
+    lib = _lib.load()
+    ws = torch.empty(max(int(lib.sna_absmax_workspace_bytes(T, H)), 4), dtype=torch.uint8, device=dev)
+    out = torch.empty(H, dtype=torch.float32, device=dev)
+    rc = lib.sna_kv_absmax_scale(_ptr(x), T, H, d, _ptr(out), _ptr(ws), ws.numel(), _stream(dev))
+    _lib.check(rc, "kv_absmax_scale")
+    return out
+
+
+def kv_store_mla(rows: Tensor, slots: Tensor, cache: Tensor, row_scale: Optional[Tensor] = None) -> None:
+    """Write compact MLA rows [T, 576] bf16 into a layer's rows [slots, 576] (or [slots, 1, 576]) at ``slots``; an
+    FP8 (uint8-stored) cache gets one scale per token in ``row_scale`` [slots]. Out-of-pool slots write slot 0
+    (models/deepseek_v2/model.py:64-70)."""
+    dev = _on_gpu(rows, slots, cache, row_scale)
+    flat = cache.reshape(cache.shape[0], -1)
+    n_slots, dim = flat.shape
+    rows = _contig(rows.reshape(-1, dim), "rows", torch.bfloat16)
+    slots = _contig(slots.reshape(-1).to(torch.int64), "slots")
+    _need(slots.numel() == rows.shape[0], f"{slots.numel()} slots for {rows.shape[0]} rows")
+    code = cache_dtype_code(cache.dtype)
+    if code == _lib.DTYPE_FP8_E4M3FN:
+        _need(row_scale is not None and row_scale.numel() == n_slots and row_scale.dtype == torch.float32
+              and row_scale.is_contiguous(), f"an FP8 MLA cache needs a contiguous fp32 row_scale of {n_slots}")
+    _need(cache.is_contiguous(), "cache must be contiguous")
+    rc = _lib.load().sna_kv_store_mla(_ptr(rows), _ptr(slots), rows.shape[0], dim, _ptr(cache), _ptr(row_scale),
+                                      n_slots, code, _stream(dev))
+    _lib.check(rc, "kv_store_mla")
+
+
+def kv_store_dsa(rows: Tensor, slots: Tensor, cache: Tensor, kv_scale: float) -> None:
+    """Pack rows [T, 576] bf16 ([k_pe 64 | latent 512]) into the 640-byte layout and scatter them to ``slots``
+    (flat rows of ``cache`` [..., 640] uint8); a negative or out-of-cache slot is skipped
+    (models/glm52/kernels/decode/attention/mla/mla_decode_attention_torch.py:193-221)."""
+    dev = _on_gpu(rows, slots, cache)
+    _need(cache.dtype == torch.uint8 and cache.shape[-1] == 640 and cache.is_contiguous(),
+          "the DSA cache is contiguous uint8 [..., 640]")
+    rows = _contig(rows.reshape(-1, 576), "rows", torch.bfloat16)
+    slots = _contig(slots.reshape(-1).to(torch.int64), "slots")
+    _need(slots.numel() == rows.shape[0], f"{slots.numel()} slots for {rows.shape[0]} rows")
+    n_rows = cache.numel() // 640
+    rc = _lib.load().sna_kv_store_dsa(_ptr(rows), _ptr(slots), rows.shape[0], float(kv_scale), _ptr(cache), n_rows,
+                                      _stream(dev))
+    _lib.check(rc, "kv_store_dsa")
+
+
+# ------------------------------------------------------------------------------------------------------------------
+# planning
+# ------------------------------------------------------------------------------------------------------------------
+
+def plan_decode(kind: int, B: int, *, host_seq_lens: Union[Tensor, Sequence[int], None] = None,
+                max_seq_len: int = -1, window: int = 0, n_keys_per_row: int = 0, ctas_per_item: int = 1,
+                num_cus: int = 0) -> _lib.SplitPlan:
+    """The split-K plan of a decode launch (sna_plan_decode): exact from host seq_lens, or a bound from
+    ``max_seq_len``."""
+    plan = _lib.SplitPlan()
+    arr = None
+    if host_seq_lens is not None:
+        t = torch.as_tensor(host_seq_lens, dtype=torch.int32).reshape(-1).cpu().contiguous()
+        _need(t.numel() == B, f"{t.numel()} host seq_lens for {B} rows")
+        arr = t
+    rc = _lib.load().sna_plan_decode(kind, None if arr is None else arr.data_ptr(), B, max_seq_len, window,
+                                     n_keys_per_row, ctas_per_item, num_cus, plan)
+    _lib.check(rc, "plan_decode")
+    return plan
+
+
+def workspace_bytes(plan: _lib.SplitPlan, heads: int, dim_v: int) -> int:
+    return int(_lib.load().sna_decode_workspace_bytes(plan, heads, dim_v))
+
+
+def _host_lens(seq_lens: Tensor, host_seq_lens) -> Optional[Tensor]:
+    if host_seq_lens is not None:
+        return torch.as_tensor(host_seq_lens, dtype=torch.int32).reshape(-1)
+    if not seq_lens.is_cuda:
+        return seq_lens.reshape(-1).to(torch.int32)
+    return None
+
+
+# ------------------------------------------------------------------------------------------------------------------
+# decode attention
+# ------------------------------------------------------------------------------------------------------------------
+
+def paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: Tensor, seq_lens: Tensor,
+                     k_new: Tensor, v_new: Tensor, *, sm_scale: float, k_scale: Optional[Tensor] = None,
+                     v_scale: Optional[Tensor] = None, sinks: Optional[Tensor] = None, window: int = 0,
+                     new_slots: Optional[Tensor] = None, out: Optional[Tensor] = None,
+                     host_seq_lens=None, plan: Optional[_lib.SplitPlan] = None) -> Tensor:
+    """GQA decode of q [B, H, d] over a layer's paged caches [blocks, G, page, d], the step's token k_new / v_new
+    [B, G, d] attended in-band (and stored at ``new_slots`` when given). Returns [B, H, d] bf16.
+
+    Stands in for the attention core of _torch_attention_decode_paged (ops/attention/attention_decode_paged.py:
+    159-177) and _torch_attention_decode (ops/attention/attention_decode.py:259-300)."""
+    dev = _on_gpu(q, k_cache, v_cache, block_table, seq_lens, k_new, v_new, k_scale, v_scale, sinks, new_slots, out)
+    _need(q.dim() == 3, f"q must be [B, H, d], got {tuple(q.shape)}")
+    B, H, d = q.shape
+    nb, G, P, dk = k_cache.shape
+    _need(dk == d and v_cache.shape == k_cache.shape and v_cache.dtype == k_cache.dtype,
+          f"caches {tuple(k_cache.shape)} / {tuple(v_cache.shape)} do not match q's head_dim {d}")
+    _need(H % G == 0, f"{H} query heads over {G} KV heads")
+    code = cache_dtype_code(k_cache.dtype)
+    q = _contig(q, "q", torch.bfloat16)
+    k_new = _contig(k_new.reshape(B, G, d), "k_new", torch.bfloat16)
+    v_new = _contig(v_new.reshape(B, G, d), "v_new", torch.bfloat16)
+    _need(block_table.dim() == 2 and block_table.shape[0] == B, f"block_table must be [{B}, width]")
+    table = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
+    _need(table.stride(1) == 1, "block_table rows must be contiguous")
+    lens = _contig(seq_lens.reshape(-1).to(torch.int32), "seq_lens")
+    _need(lens.numel() == B, f"{lens.numel()} seq_lens for {B} rows")
+    if code == _lib.DTYPE_FP8_E4M3FN:
+        _need(k_scale is not None and v_scale is not None, "an FP8 cache needs k_scale and v_scale")
+        k_scale = _contig(k_scale.reshape(-1).float(), "k_scale")
+        v_scale = _contig(v_scale.reshape(-1).float(), "v_scale")
+        _need(k_scale.numel() == G and v_scale.numel() == G, "one k/v scale per KV head")
+    if sinks is not None:
+        sinks = _contig(sinks.reshape(-1).float(), "sinks")
+        _need(sinks.numel() == H, f"{sinks.numel()} sinks for {H} heads")
+    if new_slots is not None:
+        new_slots = _contig(new_slots.reshape(-1).to(torch.int64), "new_slots")
+        _need(new_slots.numel() == B, f"{new_slots.numel()} new slots for {B} rows")
+    if out is None:
+        out = torch.empty(B, H, d, dtype=torch.bfloat16, device=dev)
+    _need(out.shape == (B, H, d) and out.dtype == torch.bfloat16 and out.is_contiguous(), "bad out tensor")
+    if plan is None:
+        hl = _host_lens(seq_lens, host_seq_lens)
+        plan = plan_decode(_lib.KIND_GQA, B, host_seq_lens=hl, max_seq_len=table.shape[1] * P, window=window,
+                           ctas_per_item=G, num_cus=_num_cus(dev))
+    ws = torch.empty(max(workspace_bytes(plan, H, d), 16), dtype=torch.uint8, device=dev)
+    rc = _lib.load().sna_paged_decode_gqa(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), _ptr(table), table.stride(0),
+        table.shape[1], _ptr(lens), _ptr(k_new), _ptr(v_new), _ptr(new_slots), _ptr(sinks), int(window),
+        float(sm_scale), _ptr(out), B, H, G, d, P, nb, code, plan, _ptr(ws), ws.numel(), _stream(dev))
+    _lib.check(rc, "paged_decode_gqa")
+    return out
+
+
+def mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: Tensor, block_table: Tensor,
+               seq_lens: Tensor, compact_new: Tensor, *, sm_scale: float, page_size: int,
+               new_slots: Optional[Tensor] = None, out: Optional[Tensor] = None, host_seq_lens=None,
+               plan: Optional[_lib.SplitPlan] = None) -> Tensor:
+    """Absorbed-MLA decode of ql_nope [B, H, 512] / q_pe [B, H, 64] over a layer's FP8 rows [slots, 576] (uint8 or
+    float8 storage) with per-token scales ``row_scale`` [slots], the history through ``block_table`` and the own row
+    ``compact_new`` [B, 576] in-band (stored at ``new_slots`` when given). Returns [B, H, 512] bf16.
+
+    Stands in for mla_decode (ops/attention/mla.py:32-53)."""
+    dev = _on_gpu(ql_nope, q_pe, cache, row_scale, block_table, seq_lens, compact_new, new_slots, out)
+    B, H, lat = ql_nope.shape
+    _need(lat == 512 and q_pe.shape == (B, H, 64), "ql_nope [B, H, 512] and q_pe [B, H, 64]")
+    # rows as the pool holds them: [slots, 576], [slots, 1, 576] or the block view [blocks, page, 576]
+    _need(cache.shape[-1] == 576 and cache.is_contiguous(), f"MLA rows must be contiguous [.., 576], got "
+          f"{tuple(cache.shape)}")
+    code = cache_dtype_code(cache.dtype)
+    _need(code == _lib.DTYPE_FP8_E4M3FN, "the HIP MLA decode reads the FP8 row pool")
+    n_slots = cache.numel() // 576
+    P = int(page_size)
+    _need(n_slots % P == 0, f"{n_slots} rows are not whole pages of {P}")
+    nb = n_slots // P
+    _need(row_scale.numel() == n_slots and row_scale.dtype == torch.float32 and row_scale.is_contiguous(),
+          "row_scale must be contiguous fp32 with one entry per row")
+    ql_nope = _contig(ql_nope, "ql_nope", torch.bfloat16)
+    q_pe = _contig(q_pe, "q_pe", torch.bfloat16)
+    compact_new = _contig(compact_new.reshape(B, 576), "compact_new", torch.bfloat16)
+    table = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
+    _need(table.dim() == 2 and table.shape[0] == B and table.stride(1) == 1, f"block_table must be [{B}, width]")
+    lens = _contig(seq_lens.reshape(-1).to(torch.int32), "seq_lens")
+    if new_slots is not None:
+        new_slots = _contig(new_slots.reshape(-1).to(torch.int64), "new_slots")
+    if out is None:
+        out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
+    if plan is None:
+        hl = _host_lens(seq_lens, host_seq_lens)
+        plan = plan_decode(_lib.KIND_MLA, B, host_seq_lens=hl, max_seq_len=table.shape[1] * P,
+                           ctas_per_item=(H + 15) // 16, num_cus=_num_cus(dev))
+    ws = torch.empty(max(workspace_bytes(plan, H, 512), 16), dtype=torch.uint8, device=dev)
+    rc = _lib.load().sna_mla_decode(
+        _ptr(ql_nope), _ptr(q_pe), _ptr(cache), _ptr(row_scale), _ptr(table), table.stride(0), table.shape[1],
+        _ptr(lens), _ptr(compact_new), _ptr(new_slots), float(sm_scale), _ptr(out), B, H, P, nb, code, plan,
+        _ptr(ws), ws.numel(), _stream(dev))
+    _lib.check(rc, "mla_decode")
+    return out
+
+
+def mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, kv_scale: float, indices: Tensor,
+                      block_table: Tensor, positions: Tensor, own_rows: Tensor, *, sm_scale: float, page_size: int,
+                      plan: Optional[_lib.SplitPlan] = None) -> tuple[Tensor, Tensor]:
+    """DSA sparse decode: q_absorbed [B, H, 512], q_pe [B, H, 64], the 640-byte row cache, ``indices`` [B, K] int32
+    global positions (-1 empty), ``block_table`` [B, W], ``positions`` [B], own rows [B, 576] ([k_pe | latent],
+    already stored by kv_store_dsa). Returns (ctx [B, H, 512] bf16, lse [B, H] fp32).
+
+    Stands in for mla_decode_attention_torch_ref with one token per sequence and one CP rank
+    (models/glm52/kernels/decode/attention/mla/mla_decode_attention_torch.py:38-130)."""
+    dev = _on_gpu(q_absorbed, q_pe, cache, indices, block_table, positions, own_rows)
+    B, H, lat = q_absorbed.shape
+    _need(lat == 512 and q_pe.shape == (B, H, 64), "q_absorbed [B, H, 512] and q_pe [B, H, 64]")
+    _need(cache.dtype == torch.uint8 and cache.shape[-1] == 640 and cache.is_contiguous(), "cache [..., 640] uint8")
+    n_rows = cache.numel() // 640
+    P = int(page_size)
+    _need(n_rows % P == 0, f"{n_rows} rows are not whole pages of {P}")
+    q_absorbed = _contig(q_absorbed, "q_absorbed", torch.bfloat16)
+    q_pe = _contig(q_pe, "q_pe", torch.bfloat16)
+    own_rows = _contig(own_rows.reshape(B, 576), "own_rows", torch.bfloat16)
+    idx = _contig(indices.reshape(B, -1).to(torch.int32), "indices")
+    K = idx.shape[1]
+    table = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
+    _need(table.dim() == 2 and table.shape[0] == B and table.stride(1) == 1, f"block_table must be [{B}, width]")
+    pos = _contig(positions.reshape(-1).to(torch.int32), "positions")
+    _need(pos.numel() == B, f"{pos.numel()} positions for {B} rows")
+    if plan is None:
+        plan = plan_decode(_lib.KIND_DSA, B, n_keys_per_row=K, ctas_per_item=(H + 15) // 16, num_cus=_num_cus(dev))
+    ws = torch.empty(max(workspace_bytes(plan, H, 512), 16), dtype=torch.uint8, device=dev)
+    ctx = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B, H, dtype=torch.float32, device=dev)
+    rc = _lib.load().sna_mla_decode_sparse(
+        _ptr(q_absorbed), _ptr(q_pe), _ptr(cache), float(kv_scale), _ptr(idx), K, _ptr(table), table.stride(0),
+        table.shape[1], _ptr(pos), _ptr(own_rows), float(sm_scale), _ptr(ctx), _ptr(lse), B, H, P, n_rows // P, plan,
+        _ptr(ws), ws.numel(), _stream(dev))
+    _lib.check(rc, "mla_decode_sparse")
+    return ctx, lse
+
+
+def lse_combine(o_parts: Tensor, lse_parts: Tensor) -> tuple[Tensor, Tensor]:
+    """Merge partial attention results o_parts [n, rows, dim] fp32 (each normalized) with their natural-log LSEs
+    [n, rows]: out = sum_i exp(lse_i - LSE) o_i. The reference's DCP merge (ops/attention/attention_decode.py:
+    277-285)."""
+    dev = _on_gpu(o_parts, lse_parts)
+    n, rows, dim = o_parts.shape
+    o_parts = _contig(o_parts, "o_parts", torch.float32)
+    lse_parts = _contig(lse_parts.reshape(n, rows), "lse_parts", torch.float32)
+    out = torch.empty(rows, dim, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(rows, dtype=torch.float32, device=dev)
+    rc = _lib.load().sna_lse_combine(_ptr(o_parts), _ptr(lse_parts), n, rows, dim, _ptr(out), _ptr(lse), _stream(dev))
+    _lib.check(rc, "lse_combine")
+    return out, lse
+
+
+def diag_fp8_to_bf16(x: Tensor) -> Tensor:
+    """The gathered-page conversion instruction applied to bytes x (uint8): bf16 bits as int16 view."""
+    dev = _on_gpu(x)
+    x = _contig(x.reshape(-1), "x", torch.uint8)
+    out = torch.empty(x.numel(), dtype=torch.int16, device=dev)
+    rc = _lib.load().sna_diag_fp8_to_bf16(_ptr(x), _ptr(out), x.numel(), _stream(dev))
+    _lib.check(rc, "diag_fp8_to_bf16")
+    return out
+
+
+def default_sm_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)

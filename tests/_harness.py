@@ -1,0 +1,80 @@
+"""Shared builders for the parity tests: the same seeded case materialized twice, in the CPU oracle and through the HIP
+path, and the comparison bar (bit-exact stores; max-abs 2e-2 and mean-abs 2e-3 for bf16 attention outputs with fp32
+accumulation, the tolerance BASELINE.json's north star states)."""
+
+from __future__ import annotations
+
+import torch
+
+from oracle import attention as oatt
+from oracle import fp8 as ofp8
+from oracle import store as ost
+from sglang_neuron_amd import ops, workloads
+
+MAX_ABS = 2e-2
+MEAN_ABS = 2e-3
+
+
+def assert_close_attn(got: torch.Tensor, want: torch.Tensor, what: str = "") -> None:
+    g = got.detach().float().cpu()
+    w = want.detach().float().cpu()
+    assert g.shape == w.shape, (g.shape, w.shape)
+    assert bool(torch.isfinite(g).all()), f"{what}: non-finite output"
+    diff = (g - w).abs()
+    mx, mean = float(diff.max()) if diff.numel() else 0.0, float(diff.mean()) if diff.numel() else 0.0
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, f"{what}: max-abs {mx:.3e} (bar {MAX_ABS}), mean-abs {mean:.3e} " \
+                                               f"(bar {MEAN_ABS})"
+
+
+# ---- GQA ----
+
+def gqa_scales(case: workloads.GqaCase):
+    """Per-KV-head absmax scales over every K (V) token of the case, prior and new (oracle)."""
+    k_all = torch.cat([case.k_prior.cpu(), case.k_new.cpu()], dim=0)
+    v_all = torch.cat([case.v_prior.cpu(), case.v_new.cpu()], dim=0)
+    return ofp8.absmax_scale(k_all, dims=(0, 2)), ofp8.absmax_scale(v_all, dims=(0, 2))
+
+
+def gqa_oracle(case: workloads.GqaCase):
+    """(out [B, H, d], k_cache, v_cache, k_scale, v_scale) on the CPU: prefill store, decode, then the new token's store."""
+    G, d, P, nb = case.G, case.d, case.P, case.num_blocks
+    dt = torch.uint8 if case.fp8 else torch.bfloat16
+    kc = torch.zeros(nb, G, P, d, dtype=dt)
+    vc = torch.zeros(nb, G, P, d, dtype=dt)
+    ks = vs = None
+    if case.fp8:
+        ks, vs = gqa_scales(case)
+    ost.kv_store_mha(case.k_prior.cpu(), case.v_prior.cpu(), case.prior_slots.cpu(), kc, vc, ks, vs)
+    out = oatt.paged_decode_gqa(case.q.cpu(), kc, vc, case.block_table, case.seq_lens, case.k_new.cpu(),
+                                case.v_new.cpu(), sm_scale=case.sm_scale, k_scale=ks, v_scale=vs,
+                                sinks=case.sinks, window=case.window)
+    ost.kv_store_mha(case.k_new.cpu(), case.v_new.cpu(), case.new_slots.cpu(), kc, vc, ks, vs)
+    return out, kc, vc, ks, vs
+
+
+def gqa_gpu_pool(case: workloads.GqaCase, dev="cuda"):
+    """(k_cache, v_cache, k_scale, v_scale) on the GPU, filled by the HIP store (scales by the HIP absmax kernel)."""
+    G, d, P, nb = case.G, case.d, case.P, case.num_blocks
+    dt = torch.float8_e4m3fn if case.fp8 else torch.bfloat16
+    kc = torch.zeros(nb, G, P, d, dtype=dt, device=dev)
+    vc = torch.zeros(nb, G, P, d, dtype=dt, device=dev)
+    ks = vs = None
+    kp, vp = case.k_prior.to(dev), case.v_prior.to(dev)
+    if case.fp8:
+        ks = ops.kv_absmax_scale(torch.cat([kp, case.k_new.to(dev)], dim=0))
+        vs = ops.kv_absmax_scale(torch.cat([vp, case.v_new.to(dev)], dim=0))
+    if kp.shape[0]:
+        ops.kv_store_mha(kp, vp, case.prior_slots.to(dev), kc, vc, ks, vs)
+    return kc, vc, ks, vs
+
+
+def gqa_gpu_decode(case: workloads.GqaCase, kc, vc, ks, vs, dev="cuda", store_new=True):
+    return ops.paged_decode_gqa(case.q.to(dev), kc, vc, case.block_table.to(dev), case.seq_lens.to(dev),
+                                case.k_new.to(dev), case.v_new.to(dev), sm_scale=case.sm_scale, k_scale=ks,
+                                v_scale=vs, sinks=None if case.sinks is None else case.sinks.to(dev),
+                                window=case.window, new_slots=case.new_slots.to(dev) if store_new else None,
+                                host_seq_lens=case.seq_lens)
+
+
+def cache_bytes(c: torch.Tensor) -> torch.Tensor:
+    return c.detach().cpu().contiguous().view(torch.uint8)

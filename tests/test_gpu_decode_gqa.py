@@ -1,0 +1,82 @@
+"""GQA decode parity: the HIP split-K decode (+ combine + fused store) against the oracle on seeded cases of cfg1,
+cfg2 and cfg4 (full and sliding-window layers), plus the edge cases the reference's path has."""
+
+import pytest
+import torch
+
+from sglang_neuron_amd import workloads
+from tests.conftest import announce
+from tests._harness import assert_close_attn, cache_bytes, gqa_gpu_decode, gqa_gpu_pool, gqa_oracle
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    ("cfg1", 1, {}),                                                     # full size: B8 H16 G8 d128 bf16
+    ("cfg2-small", 2, {"B": 4, "lens": (4096, 4096)}),                    # FP8 per-head, L=4096, 4 rows
+    ("cfg2-ragged", 2, {"B": 6, "lens": (1, 700)}),
+    ("cfg4-full", 4, {"B": 6}),                                          # sinks, d64, group 8
+    ("cfg4-swa", 4, {"B": 6, "window": workloads.SWA_WINDOW}),
+    ("cfg4-swa-short", 4, {"B": 5, "window": 128, "lens": (1, 200)}),
+    ("bf16-d64-g1", 1, {"B": 3, "H": 4, "G": 4, "d": 64, "lens": (2, 300)}),
+    ("fp8-g16", 2, {"B": 2, "H": 32, "G": 2, "lens": (33, 900)}),
+    ("fp8-page64", 2, {"B": 3, "P": 64, "lens": (50, 1500)}),
+]
+
+
+@pytest.mark.parametrize("name,cfg,over", CASES, ids=[c[0] for c in CASES])
+def test_gqa_decode_matches_oracle(name, cfg, over):
+    case = workloads.gqa_case(cfg, overrides=over)
+    want, kc_o, vc_o, ks_o, vs_o = gqa_oracle(case)
+    announce(f"gqa {name}: B={case.B} H={case.H} G={case.G} d={case.d} P={case.P} fp8={case.fp8} "
+             f"window={case.window} lens={case.seq_lens.tolist()[:8]}")
+    kc, vc, ks, vs = gqa_gpu_pool(case)
+    if case.fp8:
+        assert torch.equal(ks.cpu(), ks_o) and torch.equal(vs.cpu(), vs_o)
+    out = gqa_gpu_decode(case, kc, vc, ks, vs)
+    torch.cuda.synchronize()
+    assert_close_attn(out, want, name)
+    # the pool after the step (prefill + the fused store of the new token) is bit-exact
+    assert torch.equal(cache_bytes(kc), cache_bytes(kc_o)), "K pool differs"
+    assert torch.equal(cache_bytes(vc), cache_bytes(vc_o)), "V pool differs"
+
+
+def test_gqa_single_token_rows():
+    """seq_len 1 (a padding row reading nothing but its own token): the output is the new token's value."""
+    case = workloads.gqa_case(2, overrides={"B": 3, "lens": (1, 1)})
+    announce("gqa seq_len 1")
+    want, *_ = gqa_oracle(case)
+    kc, vc, ks, vs = gqa_gpu_pool(case)
+    out = gqa_gpu_decode(case, kc, vc, ks, vs)
+    assert_close_attn(out, want, "seq_len 1")
+
+
+def test_gqa_page_permutation_invariance():
+    """Moving pages to other physical ids (and the table with them) leaves the output bit-identical."""
+    case = workloads.gqa_case(2, overrides={"B": 3, "lens": (500, 1200)})
+    announce("gqa page permutation")
+    kc, vc, ks, vs = gqa_gpu_pool(case)
+    out1 = gqa_gpu_decode(case, kc, vc, ks, vs, store_new=False)
+    perm = torch.randperm(case.num_blocks - 1, generator=torch.Generator().manual_seed(3)) + 1
+    inv = torch.zeros(case.num_blocks, dtype=torch.int64)
+    inv[perm] = torch.arange(1, case.num_blocks)
+    kc2 = kc.clone()
+    vc2 = vc.clone()
+    kc2[inv[1:].cuda()] = kc[1:]
+    vc2[inv[1:].cuda()] = vc[1:]
+    t = case.block_table.clone().to(torch.int64)
+    t = torch.where(t > 0, inv[t.clamp(min=0)], t).to(torch.int32)
+    case.block_table = t
+    out2 = gqa_gpu_decode(case, kc2, vc2, ks, vs, store_new=False)
+    assert torch.equal(out1.cpu(), out2.cpu())
+
+
+def test_gqa_invalid_pages_are_masked():
+    """-1 table entries inside a row's range hide those keys, as the reference's visibility mask does."""
+    case = workloads.gqa_case(1, overrides={"B": 2, "lens": (300, 300)})
+    case.block_table[0, 3] = -1
+    case.block_table[1, 0] = -1
+    want, *_ = gqa_oracle(case)
+    announce("gqa -1 pages")
+    kc, vc, ks, vs = gqa_gpu_pool(case)
+    out = gqa_gpu_decode(case, kc, vc, ks, vs)
+    assert_close_attn(out, want, "-1 pages")

@@ -249,7 +249,8 @@ class DsaCase:
     def fill_rows(self, store: Callable[[Tensor, Tensor], None], gen_device="cpu", chunk: int = 1 << 18) -> None:
         """Fill every prior position of every row (positions < the pool's per-sequence size, except each row's own
         position) through ``store(rows [n, 576] bf16, slots [n])``, in chunks."""
-        g = gen(5, gen_device)
+        g = torch.Generator(device=gen_device)
+        g.manual_seed(2005)
         B, P = self.B, self.P
         per = self.pool_positions
         for b in range(B):

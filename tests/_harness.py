@@ -78,3 +78,60 @@ def gqa_gpu_decode(case: workloads.GqaCase, kc, vc, ks, vs, dev="cuda", store_ne
 
 def cache_bytes(c: torch.Tensor) -> torch.Tensor:
     return c.detach().cpu().contiguous().view(torch.uint8)
+
+
+# ---- MLA ----
+
+def mla_oracle(case: workloads.MlaCase):
+    """(out, cache, row_scale) on the CPU: prefill rows, decode, then the own row's store."""
+    n = case.num_blocks * case.P
+    cache = torch.zeros(n, 576, dtype=torch.uint8)
+    scale = torch.zeros(n, dtype=torch.float32)
+    ost.kv_store_mla(case.prior_rows.cpu(), case.prior_slots.cpu(), cache, scale)
+    out = oatt.mla_decode(case.ql_nope.cpu(), case.q_pe.cpu(), cache, scale, case.block_table, case.seq_lens,
+                          case.compact_new.cpu(), sm_scale=case.sm_scale, page_size=case.P)
+    ost.kv_store_mla(case.compact_new.cpu(), case.new_slots.cpu(), cache, scale)
+    return out, cache, scale
+
+
+def mla_gpu_pool(case: workloads.MlaCase, dev="cuda"):
+    n = case.num_blocks * case.P
+    cache = torch.zeros(n, 576, dtype=torch.uint8, device=dev)
+    scale = torch.zeros(n, dtype=torch.float32, device=dev)
+    if case.prior_slots.numel():
+        ops.kv_store_mla(case.prior_rows.to(dev), case.prior_slots.to(dev), cache, scale)
+    return cache, scale
+
+
+def mla_gpu_decode(case: workloads.MlaCase, cache, scale, dev="cuda", store_new=True):
+    return ops.mla_decode(case.ql_nope.to(dev), case.q_pe.to(dev), cache, scale, case.block_table.to(dev),
+                          case.seq_lens.to(dev), case.compact_new.to(dev), sm_scale=case.sm_scale, page_size=case.P,
+                          new_slots=case.new_slots.to(dev) if store_new else None, host_seq_lens=case.seq_lens)
+
+
+# ---- DSA ----
+
+def dsa_oracle(case: workloads.DsaCase):
+    """(ctx, lse, cache) on the CPU: every prior row stored, then the reference's six steps."""
+    n = case.num_blocks * case.P
+    cache = torch.zeros(n, 640, dtype=torch.uint8)
+    case.fill_rows(lambda v, s: ost.kv_store_dsa(v, s, cache, case.kv_scale))
+    ctx, lse, cache2 = oatt.mla_decode_sparse(case.q_absorbed.cpu(), case.q_pe.cpu(), cache, case.kv_scale,
+                                              case.indices, case.block_table, case.positions, case.own_rows.cpu(),
+                                              case.new_slots.cpu(), sm_scale=case.sm_scale, page_size=case.P)
+    return ctx, lse, cache2
+
+
+def dsa_gpu_pool(case: workloads.DsaCase, dev="cuda", gen_device="cpu"):
+    n = case.num_blocks * case.P
+    cache = torch.zeros(n, 640, dtype=torch.uint8, device=dev)
+    case.fill_rows(lambda v, s: ops.kv_store_dsa(v.to(dev), s.to(dev), cache, case.kv_scale), gen_device=gen_device)
+    return cache
+
+
+def dsa_gpu_step(case: workloads.DsaCase, cache, dev="cuda"):
+    """The step as the path runs it: store the own rows, then the sparse decode."""
+    ops.kv_store_dsa(case.own_rows.to(dev), case.new_slots.to(dev), cache, case.kv_scale)
+    return ops.mla_decode_sparse(case.q_absorbed.to(dev), case.q_pe.to(dev), cache, case.kv_scale,
+                                 case.indices.to(dev), case.block_table.to(dev), case.positions.to(dev),
+                                 case.own_rows.to(dev), sm_scale=case.sm_scale, page_size=case.P)

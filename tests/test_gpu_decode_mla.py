@@ -1,0 +1,71 @@
+"""Absorbed-MLA decode parity (cfg3 shapes) and DSA sparse decode parity (cfg5 shapes): the HIP kernels against the
+oracle on seeded cases, with the pools compared bit-exact after the step."""
+
+import pytest
+import torch
+
+from sglang_neuron_amd import workloads
+from tests.conftest import announce
+from tests._harness import (assert_close_attn, dsa_gpu_pool, dsa_gpu_step, dsa_oracle, mla_gpu_decode, mla_gpu_pool,
+                            mla_oracle)
+
+pytestmark = pytest.mark.gpu
+
+MLA_CASES = [
+    ("cfg3-small", {"B": 4, "lens": (1024, 4096)}),
+    ("cfg3-ragged", {"B": 6, "lens": (1, 300)}),
+    ("cfg3-long", {"B": 2, "lens": (16000, 16384)}),
+    ("heads-8", {"B": 3, "H": 8, "lens": (20, 2000)}),
+    ("heads-20", {"B": 2, "H": 20, "lens": (100, 1000)}),
+    ("page-16", {"B": 3, "P": 16, "lens": (40, 900)}),
+]
+
+
+@pytest.mark.parametrize("name,over", MLA_CASES, ids=[c[0] for c in MLA_CASES])
+def test_mla_decode_matches_oracle(name, over):
+    case = workloads.mla_case(overrides=over)
+    want, cache_o, scale_o = mla_oracle(case)
+    announce(f"mla {name}: B={case.B} H={case.H} P={case.P} lens={case.seq_lens.tolist()[:8]}")
+    cache, scale = mla_gpu_pool(case)
+    out = mla_gpu_decode(case, cache, scale)
+    torch.cuda.synchronize()
+    assert_close_attn(out, want, name)
+    assert torch.equal(cache.cpu(), cache_o), "row pool differs"
+    assert torch.equal(scale.cpu(), scale_o), "row scales differ"
+
+
+DSA_CASES = [
+    ("cfg5-small", {"B": 4, "pool_positions": 4096, "n_indices": 512, "recent": 128, "short_rows": (100, 300)}),
+    ("cfg5-wide", {"B": 2, "pool_positions": 8192, "n_indices": 2048, "recent": 128, "short_rows": (1500,)}),
+    ("page-16", {"B": 3, "P": 16, "pool_positions": 2048, "n_indices": 100, "recent": 16, "short_rows": (40,)}),
+]
+
+
+@pytest.mark.parametrize("name,over", DSA_CASES, ids=[c[0] for c in DSA_CASES])
+def test_dsa_decode_matches_oracle(name, over):
+    case = workloads.dsa_case(overrides=over)
+    want_ctx, want_lse, cache_o = dsa_oracle(case)
+    announce(f"dsa {name}: B={case.B} H={case.H} P={case.P} K={case.indices.shape[1]}")
+    cache = dsa_gpu_pool(case)
+    ctx, lse = dsa_gpu_step(case, cache)
+    torch.cuda.synchronize()
+    assert_close_attn(ctx, want_ctx, name)
+    assert torch.allclose(lse.cpu(), want_lse, atol=2e-3, rtol=1e-4), (lse.cpu() - want_lse).abs().max()
+    assert torch.equal(cache.cpu(), cache_o), "row pool differs"
+
+
+def test_dsa_invalid_indices_are_dropped():
+    """Indices past the table, into unallocated blocks, or after the query's position are dropped; -1 is empty."""
+    case = workloads.dsa_case(overrides={"B": 2, "pool_positions": 1024, "n_indices": 64, "recent": 8,
+                                         "short_rows": ()})
+    case.indices[0, 5] = 10 ** 6            # past the table
+    case.indices[0, 6] = -1
+    case.block_table[1, 2] = -1            # unallocated block: drops indices in [128, 192)
+    case.indices[1, 7] = 150
+    case.indices[1, 8] = int(case.positions[1]) + 5  # after the query position (not kept)
+    want_ctx, want_lse, _ = dsa_oracle(case)
+    announce("dsa invalid indices")
+    cache = dsa_gpu_pool(case)
+    ctx, lse = dsa_gpu_step(case, cache)
+    assert_close_attn(ctx, want_ctx, "invalid indices")
+    assert torch.allclose(lse.cpu(), want_lse, atol=2e-3, rtol=1e-4)

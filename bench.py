@@ -1,0 +1,388 @@
+#!/usr/bin/env python
+"""Benchmark of the paged decode-attention step on one MI355X (the metric of BASELINE.json).
+
+A step is one decode of the whole batch with the default workload cfg2 (Qwen3-8B-shaped GQA, FP8 e4m3fn KV with
+per-KV-head scales, B64 H32 G8 d128, L=4096, page 16). That covers the new token's store, the split-K decode and the
+combine pass. Inputs are already resident in HBM. The pool is rotated over copies whose total exceeds the 256 MB
+Infinity Cache several times, so every step reads cold HBM.
+
+One JSON line on stdout:
+  value         algorithmic HBM bytes of the step / step time, GB/s (higher is better); ms_per_step beside it.
+  roofline      the split-K decode kernel alone: its algorithmic bytes per launch / its average launch duration,
+                measured with HIP events on the launch stream (the library's diagnostics timer) over the timed
+                steps, against MI355X's 8 TB/s. traffic = FETCH_SIZE + WRITE_SIZE per launch from the committed
+                rocprofv3 counter summary when one exists for the workload, else null.
+  cpu_baseline  the CPU oracle (a torch restatement of the reference's torch path) on a bounded sample of the same
+                workload, timed on this host's cores.
+
+Options: --config {1,2,3,4,4swa,5} picks another workload (the default line is cfg2); --all prints one line per
+workload; --gpus above 1 is refused, because this build measures one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "decode-attn µs/step + achieved HBM GB/s (% of peak), FP8 KV, 1 MI355X"
+PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0
+COLD_BYTES = 1 << 30  # rotate pool copies until the rotation spans this much (4x the Infinity Cache)
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def _copies(touched_bytes: int, pool_bytes: int, cap: int) -> int:
+    n = max(2, math.ceil(COLD_BYTES / max(touched_bytes, 1)))
+    n = min(n, cap, max(2, (64 << 30) // max(pool_bytes, 1)))
+    return n
+
+
+def _traffic(workload: str):
+    """FETCH_SIZE + WRITE_SIZE bytes per launch from profiles/traffic_<workload>.json, if measured."""
+    p = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        d = json.load(f)
+    return d.get("bytes_per_launch")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# workloads: each returns (steps [Prepared per pool copy], description dict, alg bytes of the step, alg bytes and
+# MFMA flops of the split-K kernel launch, a CPU-baseline callable)
+# ---------------------------------------------------------------------------------------------------------------
+
+def setup_gqa(cfg: int, window: int, dev):
+    import torch
+
+    from sglang_neuron_amd import ops, workloads
+
+    over = {"window": window} if window else {}
+    t0 = time.time()
+    case = workloads.gqa_case(cfg, gen_device=dev, overrides=over)
+    kc, vc, ks, vs = workloads.gqa_pool(case, dev)
+    pool_bytes = kc.numel() * kc.element_size() * 2
+    touched = case.kv_bytes_per_step()
+    n = _copies(touched, pool_bytes, 64)
+    pools = [(kc, vc)] + [(kc.clone(), vc.clone()) for _ in range(n - 1)]
+    torch.cuda.synchronize()
+    log(f"cfg{cfg}{' swa' if window else ''}: B={case.B} H={case.H} G={case.G} d={case.d} P={case.P} "
+        f"tokens={int(case.seq_lens.sum())} pool={pool_bytes / 1e6:.1f} MB x {n} copies, built in {time.time() - t0:.1f}s")
+    q, table, lens = case.q, case.block_table.to(dev), case.seq_lens.to(dev)
+    kn, vn, slots = case.k_new.to(dev), case.v_new.to(dev), case.new_slots.to(dev)
+    sinks = None if case.sinks is None else case.sinks.to(dev)
+    plan = ops.plan_decode(0, case.B, host_seq_lens=case.seq_lens, window=case.window, ctas_per_item=case.G,
+                           num_cus=ops._num_cus(q.device))
+    out = torch.empty(case.B, case.H, case.d, dtype=torch.bfloat16, device=dev)
+    steps = [ops.prepare_paged_decode_gqa(q, k, v, table, lens, kn, vn, sm_scale=case.sm_scale, k_scale=ks,
+                                          v_scale=vs, sinks=sinks, window=case.window, new_slots=slots, out=out,
+                                          plan=plan) for (k, v) in pools]
+    esz = 1 if case.fp8 else 2
+    keys = sum(min(L - 1, case.window - 1) if case.window else L - 1 for L in case.seq_lens.tolist())
+    pages = sum(-(-(min(L - 1, case.window - 1) if case.window else L - 1) // case.P) for L in case.seq_lens.tolist())
+    split_bytes = keys * case.G * case.d * esz * 2 + case.B * case.H * case.d * 2 + pages * 4
+    tiles = 0
+    for L in case.seq_lens.tolist():
+        hi = L - 1
+        lo = max(0, L - case.window) if case.window else 0
+        if hi > lo:
+            tiles += -(-hi // 32) - lo // 32
+    steps_qk, dt = case.d // 32, case.d // 16
+    mfma_flops = tiles * case.G * (2 * steps_qk + dt) * (16 * 16 * 32 * 2)
+    name = {1: "qwen3-0.6b-gqa-bf16", 2: "qwen3-8b-gqa-fp8", 4: "gpt-oss-120b-share-fp8"}[cfg]
+    desc = {"workload": f"cfg{cfg}{'-swa' + str(window) if window else ''}: {name}", "batch": case.B,
+            "q_heads": case.H, "kv_heads": case.G, "head_dim": case.d, "page_size": case.P,
+            "kv_dtype": "fp8_e4m3fn per-KV-head scale" if case.fp8 else "bf16",
+            "seq_len": "4096" if cfg == 2 else f"U{list(workloads.GQA_CONFIGS[cfg]['lens'])}",
+            "window": case.window or None, "sinks": case.sinks is not None, "pool_copies": n,
+            "split_plan": {"split_tiles": plan.split_tiles, "n_work": plan.n_work}}
+
+    def cpu_baseline(budget_s: float):
+        from oracle import attention as oatt
+        from oracle import store as ost
+
+        kcpu = pools[0][0].cpu().view(torch.uint8) if case.fp8 else pools[0][0].cpu()
+        vcpu = pools[0][1].cpu().view(torch.uint8) if case.fp8 else pools[0][1].cpu()
+        kss = None if ks is None else ks.cpu()
+        vss = None if vs is None else vs.cpu()
+        qc, knc, vnc = q.cpu(), kn.cpu(), vn.cpu()
+        sk = None if sinks is None else sinks.cpu()
+
+        def run(nrows):
+            oatt.paged_decode_gqa(qc[:nrows], kcpu, vcpu, case.block_table[:nrows], case.seq_lens[:nrows],
+                                  knc[:nrows], vnc[:nrows], sm_scale=case.sm_scale, k_scale=kss, v_scale=vss,
+                                  sinks=sk, window=case.window)
+            ost.kv_store_mha(knc[:nrows], vnc[:nrows], case.new_slots[:nrows], kcpu, vcpu, kss, vss)
+
+        return _time_rows(run, case.B, budget_s)
+
+    return steps, desc, case.kv_bytes_per_step(), split_bytes, mfma_flops, cpu_baseline
+
+
+def setup_mla(dev):
+    import torch
+
+    from sglang_neuron_amd import ops, workloads
+
+    t0 = time.time()
+    case = workloads.mla_case(gen_device=dev)
+    cache, scale = workloads.mla_pool(case, dev)
+    pool_bytes = cache.numel() + scale.numel() * 4
+    n = _copies(case.kv_bytes_per_step(), pool_bytes, 64)
+    pools = [(cache, scale)] + [(cache.clone(), scale.clone()) for _ in range(n - 1)]
+    torch.cuda.synchronize()
+    log(f"cfg3: B={case.B} H={case.H} P={case.P} tokens={int(case.seq_lens.sum())} pool={pool_bytes / 1e6:.1f} MB x "
+        f"{n} copies, built in {time.time() - t0:.1f}s")
+    table, lens = case.block_table.to(dev), case.seq_lens.to(dev)
+    plan = ops.plan_decode(1, case.B, host_seq_lens=case.seq_lens, ctas_per_item=1, num_cus=ops._num_cus(table.device))
+    out = torch.empty(case.B, case.H, 512, dtype=torch.bfloat16, device=dev)
+    steps = [ops.prepare_mla_decode(case.ql_nope, case.q_pe, c, s, table, lens, case.compact_new,
+                                    sm_scale=case.sm_scale, page_size=case.P, new_slots=case.new_slots.to(dev),
+                                    out=out, plan=plan) for (c, s) in pools]
+    keys = int((case.seq_lens - 1).sum())
+    pages = int(((case.seq_lens - 1 + case.P - 1) // case.P).sum())
+    split_bytes = keys * 580 + case.B * case.H * 576 * 2 + pages * 4
+    tiles = int(((case.seq_lens - 1 + 15) // 16).sum())
+    mfma_flops = tiles * (18 * 16 * 16 * 32 * 2 + 32 * 16 * 16 * 16 * 2)
+    desc = {"workload": "cfg3: deepseek-v2-lite absorbed MLA", "batch": case.B, "q_heads": case.H,
+            "qk_dim": 576, "v_dim": 512, "page_size": case.P, "kv_dtype": "fp8_e4m3fn per-token scale",
+            "seq_len": "U[1024, 16384]", "pool_copies": n,
+            "split_plan": {"split_tiles": plan.split_tiles, "n_work": plan.n_work}}
+
+    def cpu_baseline(budget_s: float):
+        from oracle import attention as oatt
+        from oracle import store as ost
+
+        c0, s0 = pools[0][0].cpu(), pools[0][1].cpu()
+        ql, qp, cn = case.ql_nope.cpu(), case.q_pe.cpu(), case.compact_new.cpu()
+
+        def run(nrows):
+            oatt.mla_decode(ql[:nrows], qp[:nrows], c0, s0, case.block_table[:nrows], case.seq_lens[:nrows],
+                            cn[:nrows], sm_scale=case.sm_scale, page_size=case.P)
+            ost.kv_store_mla(cn[:nrows], case.new_slots[:nrows], c0, s0)
+
+        return _time_rows(run, case.B, budget_s)
+
+    return steps, desc, case.kv_bytes_per_step(), split_bytes, mfma_flops, cpu_baseline
+
+
+def setup_dsa(dev):
+    import torch
+
+    from sglang_neuron_amd import ops, workloads
+
+    t0 = time.time()
+    case = workloads.dsa_case(gen_device=dev)
+    cache = workloads.dsa_pool(case, dev, gen_device=dev)
+    pool_bytes = cache.numel()
+    n = _copies(case.kv_bytes_per_step(), pool_bytes, 16)
+    pools = [cache] + [cache.clone() for _ in range(n - 1)]
+    torch.cuda.synchronize()
+    log(f"cfg5: B={case.B} H={case.H} K={case.indices.shape[1]} pool={pool_bytes / 1e9:.2f} GB x {n} copies, "
+        f"built in {time.time() - t0:.1f}s")
+    idx, table, pos = case.indices.to(dev), case.block_table.to(dev), case.positions.to(dev)
+    plan = ops.plan_decode(2, case.B, n_keys_per_row=case.indices.shape[1], ctas_per_item=1,
+                           num_cus=ops._num_cus(idx.device))
+    steps = [ops.prepare_mla_decode_sparse(case.q_absorbed, case.q_pe, c, case.kv_scale, idx, table, pos,
+                                           case.own_rows, sm_scale=case.sm_scale, page_size=case.P,
+                                           new_slots=case.new_slots.to(dev), plan=plan) for c in pools]
+    valid = int((case.indices >= 0).sum())
+    split_bytes = valid * (640 + 4 + 4) + int((case.indices < 0).sum()) * 4 + case.B * case.H * 576 * 2
+    tiles = case.B * (-(-case.indices.shape[1] // 16))
+    mfma_flops = tiles * (18 * 16 * 16 * 32 * 2 + 32 * 16 * 16 * 16 * 2)
+    desc = {"workload": "cfg5: glm-5.2-style DSA absorbed MLA", "batch": case.B, "q_heads": case.H,
+            "indices_per_row": case.indices.shape[1], "pool_positions_per_seq": case.pool_positions,
+            "page_size": case.P, "kv_dtype": "fp8_e4m3fn latent + bf16 rope, 640-byte rows, kv_scale 2^-6",
+            "short_rows": list(workloads.DSA_CONFIG["short_rows"]), "pool_copies": n,
+            "split_plan": {"split_tiles": plan.split_tiles, "n_work": plan.n_work}}
+
+    def cpu_baseline(budget_s: float):
+        from oracle import attention as oatt
+
+        c0 = pools[0].cpu()
+        qa, qp, own = case.q_absorbed.cpu(), case.q_pe.cpu(), case.own_rows.cpu()
+
+        def run(nrows):
+            oatt.mla_decode_sparse(qa[:nrows], qp[:nrows], c0, case.kv_scale, case.indices[:nrows],
+                                   case.block_table[:nrows], case.positions[:nrows], own[:nrows],
+                                   case.new_slots[:nrows], sm_scale=case.sm_scale, page_size=case.P, inplace=True)
+
+        return _time_rows(run, case.B, budget_s)
+
+    return steps, desc, case.kv_bytes_per_step(), split_bytes, mfma_flops, cpu_baseline
+
+
+def _time_rows(run, B: int, budget_s: float):
+    """Time the CPU oracle on the first n rows (n sized to the budget), median of 3, scaled to the whole batch."""
+    import torch
+
+    t = time.perf_counter()
+    run(1)
+    t1 = time.perf_counter() - t
+    nrows = max(1, min(B, int(budget_s / 3 / max(t1, 1e-6))))
+    times = []
+    for _ in range(3):
+        t = time.perf_counter()
+        run(nrows)
+        times.append(time.perf_counter() - t)
+    med = statistics.median(times)
+    return {"value": med * (B / nrows) * 1e6, "unit": "us/step", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"rows 0..{nrows - 1} of {B} (median of 3 runs, scaled x{B / nrows:.2f} to the batch)",
+            "cpu": cpu_model()}
+
+
+# ---------------------------------------------------------------------------------------------------------------
+
+def run_one(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> dict:
+    import ctypes
+
+    import torch
+
+    from sglang_neuron_amd import _lib
+
+    if key in ("1", "2", "4"):
+        built = setup_gqa(int(key), 0, dev)
+    elif key == "4swa":
+        from sglang_neuron_amd import workloads
+
+        built = setup_gqa(4, workloads.SWA_WINDOW, dev)
+    elif key == "3":
+        built = setup_mla(dev)
+    elif key == "5":
+        built = setup_dsa(dev)
+    else:
+        raise SystemExit(f"unknown config {key}")
+    steps, desc, step_bytes, split_bytes, mfma_flops, cpu_fn = built
+    n = len(steps)
+    lib = _lib.load()
+
+    for i in range(warmup):
+        steps[i % n]()
+    torch.cuda.synchronize()
+    log(f"warmup {warmup} done; timing {steps_n} steps")
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter()
+    start.record()
+    for i in range(steps_n):
+        steps[i % n]()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall
+    ms = start.elapsed_time(end) / steps_n
+    log(f"timed: {ms * 1e3:.2f} us/step ({wall * 1e6 / steps_n:.2f} us/step by the host clock)")
+
+    # the split-K kernel alone, with the library's HIP-event timer on the launch stream
+    lib.sna_diag_kernel_timing(1)
+    for i in range(steps_n):
+        steps[i % n]()
+    split_ms, comb_ms, launches = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
+    _lib.check(lib.sna_diag_kernel_timing_read(ctypes.byref(split_ms), ctypes.byref(comb_ms), ctypes.byref(launches)),
+               "kernel_timing_read")
+    lib.sna_diag_kernel_timing(0)
+    avg_split_ms = split_ms.value / max(launches.value, 1)
+    avg_comb_ms = comb_ms.value / max(launches.value, 1)
+    achieved = split_bytes / (avg_split_ms * 1e-3) / 1e9 if avg_split_ms > 0 else 0.0
+    log(f"split-K kernel: {avg_split_ms * 1e3:.2f} us/launch ({achieved:.0f} GB/s), combine {avg_comb_ms * 1e3:.2f} us")
+
+    value = step_bytes / (ms * 1e-3) / 1e9
+    wl = desc["workload"].split(":")[0]
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps_n,
+        "warmup": warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3fn" if "fp8" in desc.get("kv_dtype", "") else "bf16",
+        "data": "synthetic: seeded N(0,1) values (torch.Generator seed 1000+cfg), random page permutation",
+        "config": desc,
+        "us_per_step": round(ms * 1e3, 3),
+        "step_alg_bytes": step_bytes,
+        "step_hbm_frac": round(value / PEAK_HBM_GBS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "split-K decode (gqa_decode_kernel / mla_decode_kernel)",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": _traffic(wl),
+            "alg_bytes_per_launch": split_bytes,
+            "avg_launch_us": round(avg_split_ms * 1e3, 3),
+            "combine_avg_launch_us": round(avg_comb_ms * 1e3, 3),
+            "launches_timed": launches.value,
+            "mfma_tflops": round(mfma_flops / (avg_split_ms * 1e-3) / 1e12, 2) if avg_split_ms > 0 else None,
+            "mfma_util_of_bf16_dense_peak": round(mfma_flops / (avg_split_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)
+            if avg_split_ms > 0 else None,
+        },
+        "cpu_baseline": None,
+    }
+    if cpu:
+        log("CPU baseline (oracle on the host cores)")
+        line["cpu_baseline"] = cpu_fn(cpu_budget)
+        log(f"CPU baseline: {line['cpu_baseline']['value']:.0f} us/step on {line['cpu_baseline']['cores']} threads")
+    return line
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="2", help="1, 2, 3, 4, 4swa or 5 (default 2, the metric's workload)")
+    ap.add_argument("--all", action="store_true", help="one line per workload")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work for the baseline sample")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: this build runs no collectives (asked for {max(args.gpus, world)} GPUs). "
+              "The single-GPU number is the per-GPU share; see DESIGN.md for how the path shards.", file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    keys = ["1", "2", "3", "4", "4swa", "5"] if args.all else [args.config]
+    for k in keys:
+        line = run_one(k, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
+        print(json.dumps(line), flush=True)
+        torch.cuda.empty_cache()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -6,7 +6,7 @@
  * status: SNA_OK (0), or a negative code with a message that sna_last_error() gives back on the calling thread.
  * Nothing throws across the ABI, and no function allocates device memory. Kernels are enqueued on the caller's
  * stream in call order, so a store followed by a decode on one stream sees the store. The library keeps no device
- * state between calls; the only state is the thread-local error string.
+ * state between calls. Its only state is the thread-local error string and the diagnostics timer (off by default).
  *
  * Conventions (sglang-neuron, reference paths under /root/reference/sglang_neuron):
  *   - A token slot is page * page_size + offset; page = slot / page_size (attention/backend.py:6-7).
@@ -108,12 +108,19 @@ int sna_kv_store_dsa(const void *rows, const int64_t *slots, int64_t n_tokens, f
  * ===================================================================================================== */
 
 /* The split plan of a decode launch. `split_tiles` is how many key tiles each split covers. `n_work` is the number of
- * (sequence, split) items, which is what the workspace holds. */
+ * (sequence, split) items the split-K kernel runs. Partials are kept per (row, split): the workspace holds
+ * batch * max_splits of them. A plan whose rows all fit one split (max_splits <= 1) needs no workspace, because its
+ * split-K kernel writes the final output and no combine pass runs. */
 typedef struct {
   int32_t split_tiles;
   int32_t n_work;
   int32_t tile;         /* keys per tile of the kernel family: 32 (GQA) or 16 (MLA, DSA) */
   int32_t target_ctas;  /* the workgroup count the plan aimed for */
+  int32_t max_splits;   /* the most splits any row has */
+  int32_t batch;        /* rows the plan was made for */
+  int32_t empty_rows;   /* rows with no prior key (seq_len 1), or -1 when planned from a bound */
+  int32_t depth;        /* GQA: tiles each wave keeps in its register ring (2: two waves per SIMD; 4: one wave per
+                           SIMD with three tiles in flight). The planner picks it; splits were sized for it. */
 } sna_split_plan;
 
 /* Plan a decode from host copies of seq_lens (exact) or, with host_seq_lens == NULL, from an upper bound
@@ -126,7 +133,8 @@ typedef struct {
 int sna_plan_decode(int32_t kind, const int32_t *host_seq_lens, int32_t B, int32_t max_seq_len, int32_t window,
                     int32_t n_keys_per_row, int32_t ctas_per_item, int32_t num_cus, sna_split_plan *plan);
 
-/* Workspace bytes a decode with this plan needs: n_work * heads * (head_dim_v + 2) * 4. */
+/* Workspace bytes a decode with this plan needs: batch * max_splits * heads * (head_dim_v + 2) * 4, or 0 when
+ * max_splits <= 1. */
 int64_t sna_decode_workspace_bytes(const sna_split_plan *plan, int32_t num_q_heads, int32_t head_dim_v);
 
 /* =====================================================================================================
@@ -219,6 +227,14 @@ int sna_lse_combine(const float *o_parts, const float *lse_parts, int32_t n_part
                     void *out, float *lse_out, void *stream);
 
 /* ---- diagnostics ---- */
+
+/* Per-kernel timing of the decode entry points, for the benchmark's roofline figure. With timing on, each decode call
+ * records HIP events on its stream around its split-K kernel and around its combine pass (up to 4096 calls after the
+ * switch). sna_diag_kernel_timing_read waits for the last event and returns the summed milliseconds of each kernel
+ * and the number of calls timed. The events are the library's only state besides the error string. The timer is not
+ * thread-safe and is off by default. */
+int sna_diag_kernel_timing(int enable);
+int sna_diag_kernel_timing_read(double *split_ms, double *combine_ms, int64_t *launches);
 
 /* Decode n e4m3fn bytes to bf16 bits with the conversion instruction the decode kernels use for gathered pages. It
  * lets a test compare that instruction with the exact decoding on all 256 byte values. */

@@ -44,8 +44,6 @@ def paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: T
     nb, G, P, _ = k_cache.shape
     group = H // G
     Wt = block_table.shape[1]
-    kf = _dequant_cache(k_cache, k_scale, G)
-    vf = _dequant_cache(v_cache, v_scale, G)
     table = block_table.to(torch.int64)
     out = torch.empty(B, H, d, dtype=torch.bfloat16)
     key_pos = torch.arange(Wt * P)
@@ -54,8 +52,8 @@ def paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: T
         tb = table[b]
         page_ok = (tb >= 0) & (tb < nb)
         rows = tb.clamp(min=0, max=nb - 1)
-        keys = kf[rows].permute(1, 0, 2, 3).reshape(G, Wt * P, d)   # [G, W*P, d]
-        vals = vf[rows].permute(1, 0, 2, 3).reshape(G, Wt * P, d)
+        keys = _dequant_cache(k_cache[rows], k_scale, G).permute(1, 0, 2, 3).reshape(G, Wt * P, d)  # [G, W*P, d]
+        vals = _dequant_cache(v_cache[rows], v_scale, G).permute(1, 0, 2, 3).reshape(G, Wt * P, d)
         visible = page_ok.repeat_interleave(P) & (key_pos < L - 1)
         if window > 0:
             visible &= key_pos >= L - window
@@ -125,7 +123,7 @@ def mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: Optional
 
 def mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, kv_scale: float, indices: Tensor,
                       block_table: Tensor, positions: Tensor, own_rows: Tensor, new_slots: Tensor, *,
-                      sm_scale: float, page_size: int) -> tuple[Tensor, Tensor, Tensor]:
+                      sm_scale: float, page_size: int, inplace: bool = False) -> tuple[Tensor, Tensor, Tensor]:
     """(ctx [B, H, 512] bf16, lse [B, H] fp32, cache) of the DSA absorbed-MLA decode with one query token per
     sequence and one CP rank: mla_decode_attention_torch_ref (models/glm52/kernels/decode/attention/mla/
     mla_decode_attention_torch.py:38-130) with spec = 1, cp_degree = 1, cp_rank = 0.
@@ -135,10 +133,12 @@ def mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, kv_scale:
     (_gather_token_keys, :162-179; dropped when its block is past the table, unallocated, or the row is outside the
     cache), and appends the own row from its packed bytes (:185-189). Step 4 keeps key_pos <= position. Step 5 gives
     ctx = softmax . latent and lse = max + log(sum) (:117-121); a row with no kept key gives ctx 0 and lse -inf
-    (:122-128)."""
+    (:122-128). ``inplace`` writes the own rows into ``cache`` itself instead of a copy (the reference copies,
+    :193-196; the CPU baseline times the in-place form)."""
     B, H, _ = q_absorbed.shape
     P = page_size
-    cache = cache.clone()
+    if not inplace:
+        cache = cache.clone()
     st.kv_store_dsa(own_rows, new_slots, cache, kv_scale)
     flat = cache.reshape(-1, st.ROW_BYTES)
     n_rows = flat.shape[0]

@@ -33,11 +33,13 @@ class SplitPlan(ctypes.Structure):
     """sna_split_plan."""
 
     _fields_ = [("split_tiles", ctypes.c_int32), ("n_work", ctypes.c_int32), ("tile", ctypes.c_int32),
-                ("target_ctas", ctypes.c_int32)]
+                ("target_ctas", ctypes.c_int32), ("max_splits", ctypes.c_int32), ("batch", ctypes.c_int32),
+                ("empty_rows", ctypes.c_int32), ("depth", ctypes.c_int32)]
 
     def __repr__(self) -> str:
         return (f"SplitPlan(split_tiles={self.split_tiles}, n_work={self.n_work}, tile={self.tile}, "
-                f"target_ctas={self.target_ctas})")
+                f"target_ctas={self.target_ctas}, max_splits={self.max_splits}, batch={self.batch}, "
+                f"empty_rows={self.empty_rows}, depth={self.depth})")
 
 
 _P = ctypes.c_void_p
@@ -64,6 +66,9 @@ SIGNATURES = {
                                      _I32, _I64, ctypes.POINTER(SplitPlan), _P, _I64, _P]),
     "sna_lse_combine": (_I32, [_P, _P, _I32, _I64, _I32, _P, _P, _P]),
     "sna_diag_fp8_to_bf16": (_I32, [_P, _P, _I64, _P]),
+    "sna_diag_kernel_timing": (_I32, [_I32]),
+    "sna_diag_kernel_timing_read": (_I32, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+                                           ctypes.POINTER(ctypes.c_int64)]),
 }
 
 _lib = None

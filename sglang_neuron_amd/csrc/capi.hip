@@ -27,6 +27,29 @@ int32_t host_tiles(int32_t seq_len, int32_t window, int32_t tile) { return host_
 
 }  // namespace
 
+// ---- diagnostics timer ----
+namespace {
+constexpr int kMaxTimed = 4096;
+bool g_timing = false;
+int g_timed = 0;
+hipEvent_t g_events[kMaxTimed][3];
+bool g_made[kMaxTimed] = {};
+}  // namespace
+
+void timing_mark(int phase, hipStream_t s) {
+  if (!g_timing || g_timed >= kMaxTimed) return;
+  if (!g_made[g_timed]) {
+    for (int i = 0; i < 3; ++i)
+      if (hipEventCreate(&g_events[g_timed][i]) != hipSuccess) {
+        g_timing = false;
+        return;
+      }
+    g_made[g_timed] = true;
+  }
+  (void)hipEventRecord(g_events[g_timed][phase], s);
+  if (phase == 2) ++g_timed;
+}
+
 // ---- LSE merge of partials (decode-context-parallel style) ----
 __global__ __launch_bounds__(256) void lse_combine_kernel(const float* __restrict__ o_parts,
                                                           const float* __restrict__ lse_parts, int32_t n_parts,
@@ -65,9 +88,37 @@ int sna_version(void) { return 100; }
 
 const char* sna_last_error(void) { return error_buffer(); }
 
+int sna_diag_kernel_timing(int enable) {
+  ApiGuard guard;
+  g_timing = enable != 0;
+  if (g_timing) g_timed = 0;
+  return SNA_OK;
+}
+
+int sna_diag_kernel_timing_read(double* split_ms, double* combine_ms, int64_t* launches) {
+  ApiGuard guard;
+  if (!split_ms || !combine_ms || !launches) return fail(SNA_ERR_INVALID_ARGUMENT, "kernel_timing_read: null pointer");
+  *split_ms = 0.0;
+  *combine_ms = 0.0;
+  *launches = g_timed;
+  if (g_timed == 0) return SNA_OK;
+  if (hipEventSynchronize(g_events[g_timed - 1][2]) != hipSuccess)
+    return fail(SNA_ERR_LAUNCH, "kernel_timing_read: event synchronize failed");
+  for (int i = 0; i < g_timed; ++i) {
+    float a = 0.f, b = 0.f;
+    if (hipEventElapsedTime(&a, g_events[i][0], g_events[i][1]) != hipSuccess ||
+        hipEventElapsedTime(&b, g_events[i][1], g_events[i][2]) != hipSuccess)
+      return fail(SNA_ERR_LAUNCH, "kernel_timing_read: elapsed time failed");
+    *split_ms += a;
+    *combine_ms += b;
+  }
+  return SNA_OK;
+}
+
 int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32_t max_seq_len, int32_t window,
                     int32_t n_keys_per_row, int32_t ctas_per_item, int32_t num_cus, sna_split_plan* plan) {
   ApiGuard guard;
+  const int32_t gqa_depth = plan ? plan->depth : 0;  // a caller may preset the ring depth it wants (2 or 4)
   if (!plan) return fail(SNA_ERR_INVALID_ARGUMENT, "plan_decode: null plan");
   if (kind < 0 || kind > 2) return fail(SNA_ERR_INVALID_ARGUMENT, "plan_decode: unknown kind %d", kind);
   if (B < 0 || ctas_per_item < 1 || window < 0)
@@ -80,9 +131,11 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
   const int32_t tile = kind == 0 ? 32 : 16;
   const int32_t waves = 4;
   const int32_t cus = num_cus > 0 ? num_cus : 256;
-  // Resident workgroups the launch aims for: GQA runs several 4-wave workgroups per CU; the MLA kernels hold
-  // one per CU (their register budget), and the ragged tail is cut by aiming slightly under a full wave of CUs.
-  const int64_t target = kind == 0 ? (int64_t)cus * 8 : (int64_t)cus;
+  // Resident workgroups the launch aims for. GQA with the deep register ring (depth 4) holds one 4-wave workgroup
+  // per CU and gets two rounds of them; the shallow ring (depth 2) holds two per CU and gets four rounds. The MLA
+  // kernels hold one per CU (their register budget) and aim for a single round.
+  const int32_t depth = gqa_depth > 0 ? gqa_depth : 4;
+  const int64_t target = kind == 0 ? (int64_t)cus * (depth >= 4 ? 2 : 8) : (int64_t)cus;
   auto len_of = [&](int32_t b) -> int32_t {
     if (kind == 2) return n_keys_per_row + 1;  // the index list as "prior keys" + the own row
     return host_seq_lens ? host_seq_lens[b] : max_seq_len;
@@ -98,27 +151,52 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
   const int64_t items_target = std::max<int64_t>(1, target / ctas_per_item);
   int32_t split_tiles = (int32_t)std::max<int64_t>(waves, (total_tiles + items_target - 1) / items_target);
   if (kind != 0) {
-    // MLA: grow the split until the item count fits the resident target, so no workgroup waits for a second round
-    while (true) {
+    // MLA: grow the split until the item count fits the resident target, so no workgroup waits for a second round.
+    // A split's row ids live in the kernel's LDS, which caps it at kMlaMaxSplitTiles tiles.
+    constexpr int32_t kMlaMaxSplitTiles = 256;
+    split_tiles = std::min(split_tiles, kMlaMaxSplitTiles);
+    while (split_tiles < kMlaMaxSplitTiles) {
       int64_t n = 0;
       for (int32_t b = 0; b < B; ++b) n += host_splits(len_of(b), win, tile, split_tiles);
       if (n * ctas_per_item <= target || split_tiles >= std::max(max_tiles, waves)) break;
-      split_tiles += waves;
+      split_tiles = std::min(split_tiles + waves, kMlaMaxSplitTiles);
     }
   }
+  // the combine passes hold at most kMaxSplits weights per row: grow the split until every row fits
+  while (true) {
+    int32_t worst = 0;
+    for (int32_t b = 0; b < B; ++b) worst = std::max(worst, host_splits(len_of(b), win, tile, split_tiles));
+    if (worst <= kMaxSplits) break;
+    split_tiles = std::max(split_tiles + 1, (max_tiles + kMaxSplits - 1) / kMaxSplits);
+  }
+  if (kind != 0 && split_tiles * tile > 4096)
+    return fail(SNA_ERR_UNSUPPORTED, "plan_decode: a row of %d tiles needs splits beyond the MLA kernel's capacity",
+                max_tiles);
   int64_t n_work = 0;
-  for (int32_t b = 0; b < B; ++b) n_work += host_splits(len_of(b), win, tile, split_tiles);
-  if (n_work > INT32_MAX / 2) return fail(SNA_ERR_INVALID_ARGUMENT, "plan_decode: too many splits");
+  int32_t max_splits = 0, empty = 0;
+  for (int32_t b = 0; b < B; ++b) {
+    const int32_t n = host_splits(len_of(b), win, tile, split_tiles);
+    n_work += n;
+    max_splits = std::max(max_splits, n);
+    empty += n == 0;
+  }
+  if (n_work > INT32_MAX / 2 || (int64_t)B * max_splits > INT32_MAX / 2)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "plan_decode: too many splits");
   plan->split_tiles = split_tiles;
   plan->n_work = (int32_t)n_work;
   plan->tile = tile;
   plan->target_ctas = (int32_t)target;
+  plan->max_splits = max_splits;
+  plan->batch = B;
+  // a plan from a bound cannot know which rows are only their new token
+  plan->empty_rows = (kind != 2 && !host_seq_lens) ? -1 : empty;
+  plan->depth = kind == 0 ? depth : 0;
   return SNA_OK;
 }
 
 int64_t sna_decode_workspace_bytes(const sna_split_plan* plan, int32_t num_q_heads, int32_t head_dim_v) {
-  if (!plan || num_q_heads < 1 || head_dim_v < 1) return 0;
-  return (int64_t)std::max(plan->n_work, 1) * num_q_heads * ((int64_t)head_dim_v + 2) * (int64_t)sizeof(float);
+  if (!plan || num_q_heads < 1 || head_dim_v < 1 || plan->max_splits <= 1) return 0;
+  return (int64_t)plan->batch * plan->max_splits * num_q_heads * ((int64_t)head_dim_v + 2) * (int64_t)sizeof(float);
 }
 
 int sna_lse_combine(const float* o_parts, const float* lse_parts, int32_t n_parts, int64_t n_rows, int32_t dim,

@@ -1,8 +1,10 @@
-// GQA paged decode: split-K online softmax over the block table, MFMA for QK^T and PV, then a combine pass that adds
-// the step's own token (and the sink), normalizes, and optionally stores the token into the pool.
+// GQA paged decode: split-K online softmax over the block table with MFMA for QK^T and PV. The workgroup of a
+// row's first split also attends the step's own token in-band and stores it into the pool. A row with one split
+// writes its final output; otherwise a combine pass merges the splits and adds the sink.
 //
-// Work: one workgroup of 4 waves per (sequence, split, KV head). A wave takes 32-key tiles round-robin. The tile
-// is two half-tiles of 16 keys, each inside one page (page_size is a multiple of 16).
+// Work: one workgroup of 4 waves per (sequence, split, KV head). A wave takes 32-key tiles round-robin, loading the
+// next tile while it computes the current one. A tile is two half-tiles of 16 keys, each inside one page (page_size
+// is a multiple of 16).
 //
 // Lane roles in a wave (lane = 16 * g4 + li):
 //   QK   S^T[key, head] = K[key, :] . Q[head, :]   with v_mfma_f32_16x16x32_bf16, M = 16 keys, N = 16 heads (the
@@ -16,50 +18,40 @@
 //        D/16 contiguous elements V[key, D/16 * li ...] of its 8 keys and regroups them in registers so that the
 //        d-tile t operand holds V[8 keys, D/16 * li + t].
 //   acc  lane (g4, j), d-tile t, row r accumulates O[head j, D/16 * (4 g4 + r) + t].
+//
+// Softmax state per head is (m, l, acc) in the log2 domain. m moves only when a tile's maximum passes it by more than
+// 8 (a factor of 256), so the accumulators are rescaled rarely. Probabilities stay <= 256, which bf16 and fp32
+// hold without loss of relative precision.
 #include "sna_device.h"
 #include "sna_host.h"
 
 namespace sna {
 
+constexpr float kRescaleSlack = 8.0f;
+
 struct GqaArgs {
   const uint16_t* q;
-  const uint8_t* k_cache;
-  const uint8_t* v_cache;
+  uint8_t* k_cache;
+  uint8_t* v_cache;
   const float* k_scale;
   const float* v_scale;
   const int32_t* table;
   int64_t table_stride;
   int32_t table_width;
   const int32_t* seq_lens;
-  int32_t B, H, G, group, P;
-  int64_t num_blocks;
-  int32_t window;
-  float sm_scale;
-  int32_t split_tiles;
-  int32_t n_work;
-  float* ws_o;   // [n_work, H, D]  unnormalized partial outputs (V dequantized)
-  float* ws_ml;  // [n_work, H, 2]  running max (log2 domain) and softmax sum
-};
-
-struct GqaCombineArgs {
-  const uint16_t* q;
   const uint16_t* k_new;
   const uint16_t* v_new;
   const int64_t* new_slots;
-  uint8_t* k_cache;
-  uint8_t* v_cache;
-  const float* k_scale;
-  const float* v_scale;
   const float* sinks;
-  const int32_t* seq_lens;
   int32_t B, H, G, group, P;
   int64_t num_blocks;
   int32_t window;
   float sm_scale;
   int32_t split_tiles;
   int32_t n_work;
-  const float* ws_o;
-  const float* ws_ml;
+  int32_t max_splits;
+  float* ws_o;   // [B, max_splits, H, D]  unnormalized partials (V dequantized)
+  float* ws_ml;  // [B, max_splits, H, 2]  reference max (log2 domain) and softmax sum
   uint16_t* out;
 };
 
@@ -85,28 +77,44 @@ __device__ __forceinline__ void load_bytes(const uint8_t* p, uint32_t (&dst)[NB 
   }
 }
 
-template <int D, bool FP8, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void gqa_decode_kernel(GqaArgs a) {
-  constexpr int ESZ = FP8 ? 1 : 2;
-  constexpr int STEPS = D / 32;        // QK MFMA steps
-  constexpr int KE = D / 4;            // K elements per lane per key
-  constexpr int KB = KE * ESZ;         // K bytes per lane per key
-  constexpr int VE = D / 16;           // V elements per lane per key (= PV d-tiles)
-  constexpr int VB = VE * ESZ;         // V bytes per lane per key
-  constexpr int DT = D / 16;           // PV d-tiles
+template <int D, bool FP8>
+struct GqaTile {
+  static constexpr int ESZ = FP8 ? 1 : 2;
+  static constexpr int KB = D / 4 * ESZ;   // K bytes per lane per key
+  static constexpr int VB = D / 16 * ESZ;  // V bytes per lane per key
+  uint32_t k[2][KB / 4];
+  uint32_t v[8][VB / 4];
+  int32_t T0;
+  bool pvalid[2];
+};
+
+template <int D, bool FP8, int WAVES, bool FINAL, int DEPTH>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(DEPTH >= 4 ? 1 : 2)))
+void gqa_decode_kernel(GqaArgs a) {
+  using Tile = GqaTile<D, FP8>;
+  constexpr int ESZ = Tile::ESZ;
+  constexpr int STEPS = D / 32;  // QK MFMA steps
+  constexpr int KE = D / 4;      // K elements per lane per key
+  constexpr int KB = Tile::KB;
+  constexpr int VE = D / 16;     // V elements per lane per key (= PV d-tiles)
+  constexpr int VB = Tile::VB;
+  constexpr int DT = D / 16;     // PV d-tiles
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
 
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform, so tile and page indices stay scalar
+  const int lane = tid & 63;
   const int g4 = lane >> 4;
   const int li = lane & 15;
   const int g = blockIdx.y;
 
   int32_t b, split;
   locate_work<32>(a.seq_lens, a.B, a.window, a.split_tiles, (int32_t)blockIdx.x, b, split);
+  b = __builtin_amdgcn_readfirstlane(b);
+  split = __builtin_amdgcn_readfirstlane(split);
   if (b < 0) return;  // uniform across the workgroup
 
-  const int32_t L = a.seq_lens[b];
+  const int32_t L = ld_const(a.seq_lens + b);
   const KeyRange kr = key_range(L, a.window);
   const int32_t t_first = kr.lo / 32 + split * a.split_tiles;
   const int32_t t_last = min(t_first + a.split_tiles, (kr.hi + 31) / 32);
@@ -133,45 +141,31 @@ __global__ __launch_bounds__(64 * WAVES) void gqa_decode_kernel(GqaArgs a) {
   const int64_t head_stride = (int64_t)a.P * D * ESZ;  // bytes of one (page, head) block
   const int32_t* trow = a.table + (int64_t)b * a.table_stride;
 
-  float m_run = kNegBig;
-  float l_run = 0.0f;
+  auto load_tile = [&](Tile& T, int32_t tile) {
+    T.T0 = __builtin_amdgcn_readfirstlane(tile * 32);  // uniform: the page lookups below are scalar loads
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      // page of the half-tile (uniform); an entry outside the table or the pool reads page 0 and is masked
+      const int32_t col = (T.T0 + 16 * hf) / a.P;
+      const int32_t e = col < a.table_width ? ld_const(trow + col) : -1;
+      T.pvalid[hf] = e >= 0 && (int64_t)e < a.num_blocks;
+      const int32_t pg = T.pvalid[hf] ? e : 0;
+      const int64_t blk = ((int64_t)pg * a.G + g) * head_stride + (int64_t)((T.T0 + 16 * hf) % a.P) * D * ESZ;
+      load_bytes<KB>(a.k_cache + blk + (int64_t)li * D * ESZ + KB * g4, T.k[hf]);
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4)
+        load_bytes<VB>(a.v_cache + blk + (int64_t)(4 * g4 + e4) * D * ESZ + VB * li, T.v[4 * hf + e4]);
+    }
+  };
+
+  float m_ref = kNegBig;  // the reference maximum of this lane's head
+  float l_run = 0.0f;     // this lane's share of the softmax sum
   f32x4_t acc[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int32_t tile = t_first + wave; tile < t_last; tile += WAVES) {
-    const int32_t T0 = tile * 32;
-    // page of each half-tile (uniform across the wave); an entry outside the table or pool reads page 0, masked
-    int32_t pg[2];
-    bool pvalid[2];
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      const int32_t col = (T0 + 16 * hf) / a.P;
-      int32_t e = col < a.table_width ? trow[col] : -1;
-      pvalid[hf] = e >= 0 && (int64_t)e < a.num_blocks;
-      pg[hf] = pvalid[hf] ? e : 0;
-    }
-    const uint8_t* kbase[2];
-    const uint8_t* vbase[2];
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      const int64_t blk = ((int64_t)pg[hf] * a.G + g) * head_stride + (int64_t)((T0 + 16 * hf) % a.P) * D * ESZ;
-      kbase[hf] = a.k_cache + blk;
-      vbase[hf] = a.v_cache + blk;
-    }
-
-    // ---- loads ----
-    uint32_t kraw[2][KB / 4];
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) load_bytes<KB>(kbase[hf] + (int64_t)li * D * ESZ + KB * g4, kraw[hf]);
-    uint32_t vraw[8][VB / 4];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int hf = e >> 2;
-      const int key = 4 * g4 + (e & 3);
-      load_bytes<VB>(vbase[hf] + (int64_t)key * D * ESZ + VB * li, vraw[e]);
-    }
-
+  auto compute_tile = [&](Tile& T) {
+    const bool full = T.pvalid[0] && T.pvalid[1] && T.T0 >= kr.lo && T.T0 + 32 <= kr.hi;
     // ---- S^T = K Q^T ----
     f32x4_t sc[2];
 #pragma unroll
@@ -181,58 +175,55 @@ __global__ __launch_bounds__(64 * WAVES) void gqa_decode_kernel(GqaArgs a) {
       for (int st = 0; st < STEPS; ++st) {
         uint32_t op[4];
         if constexpr (FP8) {
-          fp8x4_to_bf16x4(kraw[hf][2 * st], op[0], op[1]);
-          fp8x4_to_bf16x4(kraw[hf][2 * st + 1], op[2], op[3]);
+          fp8x4_to_bf16x4(T.k[hf][2 * st], op[0], op[1]);
+          fp8x4_to_bf16x4(T.k[hf][2 * st + 1], op[2], op[3]);
         } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) op[i] = kraw[hf][4 * st + i];
+          for (int i = 0; i < 4; ++i) op[i] = T.k[hf][4 * st + i];
         }
         s = mfma_16x16x32_bf16(op, qv[st], s);
       }
       sc[hf] = s;
     }
-
-    // ---- mask and online softmax (log2 domain) ----
+    // ---- mask (boundary tiles only), online softmax ----
     float x[8];
     float tmax = -INFINITY;
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
+    for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int32_t pos = T0 + 16 * hf + 4 * g4 + r;
-        const bool ok = pvalid[hf] && pos >= kr.lo && pos < kr.hi;
-        const float v = ok ? sc[hf][r] * qk_scale : -INFINITY;
-        x[4 * hf + r] = v;
-        tmax = fmaxf(tmax, v);
-      }
+      for (int r = 0; r < 4; ++r) x[4 * hf + r] = sc[hf][r] * qk_scale;
+    if (!full) {
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int32_t pos = T.T0 + 16 * hf + 4 * g4 + r;
+          const bool ok = T.pvalid[hf] && pos >= kr.lo && pos < kr.hi;
+          x[4 * hf + r] = ok ? x[4 * hf + r] : -INFINITY;
+#pragma unroll
+          for (int i = 0; i < VB / 4; ++i) T.v[4 * hf + r][i] = ok ? T.v[4 * hf + r][i] : 0u;
+        }
     }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) tmax = fmaxf(tmax, x[i]);
     tmax = max_across_groups(tmax);
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = exp2f(m_run - m_new);
-    m_run = m_new;
+    const bool bump = tmax > m_ref + kRescaleSlack;
+    if (__any(bump)) {
+      const float m_new = bump ? tmax : m_ref;
+      const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new);
+      m_ref = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) acc[t] *= alpha;
+    }
     float p[8];
-    float psum = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      p[i] = exp2f(x[i] - m_new);
-      psum += p[i];
+      p[i] = __builtin_amdgcn_exp2f(x[i] - m_ref);
+      l_run += p[i];
     }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int t = 0; t < DT; ++t) acc[t] *= alpha;
-    uint32_t pop[4] = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
-                       pack_bf16x2(p[6], p[7])};
-
-    // ---- zero the V of keys outside the pages (a stale NaN there would survive p = 0) ----
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int hf = e >> 2;
-      const int32_t pos = T0 + 16 * hf + 4 * g4 + (e & 3);
-      const bool ok = pvalid[hf] && pos >= kr.lo && pos < kr.hi;
-#pragma unroll
-      for (int i = 0; i < VB / 4; ++i) vraw[e][i] = ok ? vraw[e][i] : 0u;
-    }
-
+    const uint32_t pop[4] = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                             pack_bf16x2(p[6], p[7])};
     // ---- O^T += V^T P^T, one MFMA per 16-wide d-tile ----
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
@@ -242,8 +233,8 @@ __global__ __launch_bounds__(64 * WAVES) void gqa_decode_kernel(GqaArgs a) {
         uint32_t lo = 0, hi = 0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          lo |= ((vraw[e][t >> 2] >> (8 * (t & 3))) & 0xffu) << (8 * e);
-          hi |= ((vraw[e + 4][t >> 2] >> (8 * (t & 3))) & 0xffu) << (8 * e);
+          lo |= ((T.v[e][t >> 2] >> (8 * (t & 3))) & 0xffu) << (8 * e);
+          hi |= ((T.v[e + 4][t >> 2] >> (8 * (t & 3))) & 0xffu) << (8 * e);
         }
         fp8x4_to_bf16x4(lo, op[0], op[1]);
         fp8x4_to_bf16x4(hi, op[2], op[3]);
@@ -251,16 +242,84 @@ __global__ __launch_bounds__(64 * WAVES) void gqa_decode_kernel(GqaArgs a) {
         // 16-bit element t of each key's run
 #pragma unroll
         for (int pr = 0; pr < 4; ++pr) {
-          const uint32_t e0 = (vraw[2 * pr][t >> 1] >> (16 * (t & 1))) & 0xffffu;
-          const uint32_t e1 = (vraw[2 * pr + 1][t >> 1] >> (16 * (t & 1))) & 0xffffu;
+          const uint32_t e0 = (T.v[2 * pr][t >> 1] >> (16 * (t & 1))) & 0xffffu;
+          const uint32_t e1 = (T.v[2 * pr + 1][t >> 1] >> (16 * (t & 1))) & 0xffffu;
           op[pr] = e0 | (e1 << 16);
         }
       }
       acc[t] = mfma_16x16x32_bf16(op, pop, acc[t]);
     }
+  };
+
+  // ---- the tile loop: a ring of DEPTH register tiles, DEPTH - 1 of them in flight ahead of the one computed ----
+  {
+    Tile ring[DEPTH];
+    const int32_t t0 = t_first + wave;
+#pragma unroll
+    for (int i = 0; i < DEPTH - 1; ++i)
+      if (t0 + i * WAVES < t_last) load_tile(ring[i], t0 + i * WAVES);
+    for (int32_t base = 0;; base += DEPTH) {
+      bool done = false;
+#pragma unroll
+      for (int k = 0; k < DEPTH; ++k) {
+        const int32_t cur = t0 + (base + k) * WAVES;
+        if (cur >= t_last) {
+          done = true;
+          break;
+        }
+        const int32_t nxt = cur + (DEPTH - 1) * WAVES;
+        if (nxt < t_last) load_tile(ring[(k + DEPTH - 1) % DEPTH], nxt);
+        compute_tile(ring[k]);
+      }
+      if (done) break;
+    }
   }
 
-  // ---- merge the waves' partials in LDS and write this split's partial ----
+  // ---- the step's own token, attended in-band by the row's first split (and stored) ----
+  __shared__ float sm_kn[D], sm_vn[D], sm_sn[16];
+  const bool own = split == 0;  // uniform
+  if (own) {
+    if (tid < D) {
+      const int64_t src = ((int64_t)b * a.G + g) * D + tid;
+      const uint32_t kb = a.k_new[src], vb = a.v_new[src];
+      float kd, vd;
+      int64_t dst = -1;
+      if (a.new_slots) {
+        const int64_t slot = redirect_slot(a.new_slots[b], a.num_blocks * a.P);
+        dst = (((slot / a.P) * a.G + g) * a.P + slot % a.P) * D + tid;
+      }
+      if constexpr (FP8) {
+        const uint32_t kq = quantize_e4m3fn(kb, kscale), vq = quantize_e4m3fn(vb, vscale);
+        kd = e4m3fn_to_f32(kq) * kscale;
+        vd = e4m3fn_to_f32(vq) * vscale;
+        if (dst >= 0) {
+          a.k_cache[dst] = (uint8_t)kq;
+          a.v_cache[dst] = (uint8_t)vq;
+        }
+      } else {
+        kd = bf16_bits_to_f32(kb);
+        vd = bf16_bits_to_f32(vb);
+        if (dst >= 0) {
+          reinterpret_cast<uint16_t*>(a.k_cache)[dst] = (uint16_t)kb;
+          reinterpret_cast<uint16_t*>(a.v_cache)[dst] = (uint16_t)vb;
+        }
+      }
+      sm_kn[tid] = kd;
+      sm_vn[tid] = vd;
+    }
+    __syncthreads();
+    for (int j = wave; j < a.group; j += WAVES) {
+      const uint16_t* qp = a.q + ((int64_t)b * a.H + g * a.group + j) * D;
+      float s = 0.0f;
+#pragma unroll
+      for (int d = lane; d < D; d += 64) s += bf16_bits_to_f32(qp[d]) * sm_kn[d];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+      if (lane == 0) sm_sn[j] = s * a.sm_scale * kLog2e;
+    }
+  }
+
+  // ---- merge the waves (and the own token) in LDS; write the output or this split's partial ----
   __shared__ float sm_o[WAVES][16][D + 1];
   __shared__ float sm_m[WAVES][16];
   __shared__ float sm_l[WAVES][16];
@@ -270,117 +329,158 @@ __global__ __launch_bounds__(64 * WAVES) void gqa_decode_kernel(GqaArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) sm_o[wave][li][VE * (4 * g4 + r) + t] = acc[t][r];
   if (g4 == 0) {
-    sm_m[wave][li] = m_run;
+    sm_m[wave][li] = m_ref;
     sm_l[wave][li] = l_tot;
   }
   __syncthreads();
-  const int64_t wbase = (int64_t)blockIdx.x * a.H + (int64_t)g * a.group;
-  for (int idx = threadIdx.x; idx < a.group * D; idx += 64 * WAVES) {
+  const int32_t S = a.max_splits;
+  for (int idx = tid; idx < a.group * D; idx += 64 * WAVES) {
     const int j = idx / D, d = idx % D;
-    float M = sm_m[0][j];
+    const int32_t h = g * a.group + j;
+    float M = own ? sm_sn[j] : -INFINITY;
 #pragma unroll
-    for (int w = 1; w < WAVES; ++w) M = fmaxf(M, sm_m[w][j]);
-    float o = 0.0f;
+    for (int w = 0; w < WAVES; ++w) M = fmaxf(M, sm_m[w][j]);
+    float o = 0.0f, l = 0.0f;
 #pragma unroll
-    for (int w = 0; w < WAVES; ++w) o += exp2f(sm_m[w][j] - M) * sm_o[w][j][d];
-    a.ws_o[(wbase + j) * D + d] = o * vscale;
-    if (d == 0) {
-      float l = 0.0f;
-#pragma unroll
-      for (int w = 0; w < WAVES; ++w) l += exp2f(sm_m[w][j] - M) * sm_l[w][j];
-      a.ws_ml[(wbase + j) * 2] = M;
-      a.ws_ml[(wbase + j) * 2 + 1] = l;
+    for (int w = 0; w < WAVES; ++w) {
+      const float e = __builtin_amdgcn_exp2f(sm_m[w][j] - M);
+      o += e * sm_o[w][j][d];
+      l += e * sm_l[w][j];
+    }
+    o *= vscale;
+    if (own) {
+      const float e = __builtin_amdgcn_exp2f(sm_sn[j] - M);
+      o += e * sm_vn[d];
+      l += e;
+    }
+    if constexpr (FINAL) {
+      if (a.sinks) l += __builtin_amdgcn_exp2f(a.sinks[h] * kLog2e - M);
+      a.out[((int64_t)b * a.H + h) * D + d] = (uint16_t)f32_to_bf16_bits(o / l);
+    } else {
+      const int64_t row = ((int64_t)b * S + split) * a.H + h;
+      a.ws_o[row * D + d] = o;
+      if (d == 0) {
+        a.ws_ml[row * 2] = M;
+        a.ws_ml[row * 2 + 1] = l;
+      }
     }
   }
 }
 
-// One workgroup per (sequence, KV head): the step's token in-band (and its store), the sink, the split merge.
-template <int D, bool FP8>
-__global__ __launch_bounds__(256) void gqa_combine_kernel(GqaCombineArgs a) {
-  constexpr int ESZ = FP8 ? 1 : 2;
-  const int b = blockIdx.x, g = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  __shared__ float sm_k[D], sm_v[D], sm_s[16];
-  __shared__ int32_t sm_work[2];
-
-  const int32_t L = a.seq_lens[b];
-  if (wave == 0) {
-    int32_t n = splits_of<32>(L, a.window, a.split_tiles);
-    int32_t base = work_base_of<32>(a.seq_lens, b, a.window, a.split_tiles);
-    if (base > a.n_work) base = a.n_work;
-    if (base + n > a.n_work) n = a.n_work - base;
-    if (lane == 0) {
-      sm_work[0] = base;
-      sm_work[1] = n;
-    }
+// Merge of a row's splits per (row, KV head): out = sum_s e_s o_s / (sum_s e_s l_s + e_sink), with
+// e_s = exp2(m_s - M). The (m, l) pairs of the group's heads load into LDS in one round and each head's weights are
+// formed once. Every thread then sums its outputs over the splits with independent loads.
+template <int D>
+__global__ __launch_bounds__(256) void gqa_combine_kernel(GqaArgs a) {
+  const int b = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+  const int32_t S = a.max_splits;
+  const int32_t n = min(splits_of<32>(ld_const(a.seq_lens + b), a.window, a.split_tiles), S);
+  __shared__ float sm_w[16][kMaxSplits + 1];
+  __shared__ float sm_l[16][kMaxSplits + 1];
+  __shared__ float sm_inv[16];
+  const int64_t base = (int64_t)b * S * a.H + (int64_t)g * a.group;  // row of (b, split 0, head g * group)
+  for (int e = tid; e < a.group * n; e += blockDim.x) {
+    const int j = e / n, s = e % n;
+    const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + (base + (int64_t)s * a.H + j) * 2);
+    sm_w[j][s] = ml.x;
+    sm_l[j][s] = ml.y;
   }
+  __syncthreads();
+  if (tid < a.group) {
+    const int j = tid;
+    const int32_t h = g * a.group + j;
+    const float sink = a.sinks ? a.sinks[h] * kLog2e : -INFINITY;
+    float M = sink;
+    for (int32_t s = 0; s < n; ++s) M = fmaxf(M, sm_w[j][s]);
+    float den = a.sinks ? __builtin_amdgcn_exp2f(sink - M) : 0.0f;
+    for (int32_t s = 0; s < n; ++s) {
+      const float w = __builtin_amdgcn_exp2f(sm_w[j][s] - M);
+      sm_w[j][s] = w;
+      den += w * sm_l[j][s];
+    }
+    sm_inv[j] = 1.0f / den;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < a.group * D; idx += blockDim.x) {
+    const int j = idx / D, d = idx % D;
+    const float* op = a.ws_o + (base + j) * D + d;
+    float num = 0.0f;
+#pragma unroll 8
+    for (int32_t s = 0; s < n; ++s) num += sm_w[j][s] * op[(int64_t)s * a.H * D];
+    a.out[((int64_t)b * a.H + g * a.group + j) * D + d] = (uint16_t)f32_to_bf16_bits(num * sm_inv[j]);
+  }
+}
+
+// Rows with no split at all (seq_len 1) get their output from this pass: only the own token (and the sink).
+template <int D, bool FP8>
+__global__ __launch_bounds__(128) void gqa_lone_token_kernel(GqaArgs a) {
+  const int b = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+  if (splits_of<32>(a.seq_lens[b], a.window, a.split_tiles) > 0) return;
+  __shared__ float sm_kn[D], sm_vn[D];
+  const float kscale = FP8 ? a.k_scale[g] : 1.0f, vscale = FP8 ? a.v_scale[g] : 1.0f;
   if (tid < D) {
     const int64_t src = ((int64_t)b * a.G + g) * D + tid;
     const uint32_t kb = a.k_new[src], vb = a.v_new[src];
-    float kd, vd;
+    int64_t dst = -1;
+    if (a.new_slots) {
+      const int64_t slot = redirect_slot(a.new_slots[b], a.num_blocks * a.P);
+      dst = (((slot / a.P) * a.G + g) * a.P + slot % a.P) * D + tid;
+    }
     if constexpr (FP8) {
-      const float ks = a.k_scale[g], vs = a.v_scale[g];
-      const uint32_t kq = quantize_e4m3fn(kb, ks), vq = quantize_e4m3fn(vb, vs);
-      kd = e4m3fn_to_f32(kq) * ks;
-      vd = e4m3fn_to_f32(vq) * vs;
-      if (a.new_slots) {
-        const int64_t slot = redirect_slot(a.new_slots[b], a.num_blocks * a.P);
-        const int64_t dst = (((slot / a.P) * a.G + g) * a.P + slot % a.P) * D + tid;
+      const uint32_t kq = quantize_e4m3fn(kb, kscale), vq = quantize_e4m3fn(vb, vscale);
+      sm_kn[tid] = e4m3fn_to_f32(kq) * kscale;
+      sm_vn[tid] = e4m3fn_to_f32(vq) * vscale;
+      if (dst >= 0) {
         a.k_cache[dst] = (uint8_t)kq;
         a.v_cache[dst] = (uint8_t)vq;
       }
     } else {
-      kd = bf16_bits_to_f32(kb);
-      vd = bf16_bits_to_f32(vb);
-      if (a.new_slots) {
-        const int64_t slot = redirect_slot(a.new_slots[b], a.num_blocks * a.P);
-        const int64_t dst = (((slot / a.P) * a.G + g) * a.P + slot % a.P) * D + tid;
+      sm_kn[tid] = bf16_bits_to_f32(kb);
+      sm_vn[tid] = bf16_bits_to_f32(vb);
+      if (dst >= 0) {
         reinterpret_cast<uint16_t*>(a.k_cache)[dst] = (uint16_t)kb;
         reinterpret_cast<uint16_t*>(a.v_cache)[dst] = (uint16_t)vb;
       }
     }
-    (void)ESZ;
-    sm_k[tid] = kd;
-    sm_v[tid] = vd;
   }
   __syncthreads();
-  // score of the new token per head, in the log2 domain
-  for (int j = wave; j < a.group; j += 4) {
+  const int wave = tid >> 6, lane = tid & 63;
+  for (int j = wave; j < a.group; j += 2) {
     const int32_t h = g * a.group + j;
     const uint16_t* qp = a.q + ((int64_t)b * a.H + h) * D;
     float s = 0.0f;
-    for (int d = lane; d < D; d += 64) s += bf16_bits_to_f32(qp[d]) * sm_k[d];
+    for (int d = lane; d < D; d += 64) s += bf16_bits_to_f32(qp[d]) * sm_kn[d];
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-    if (lane == 0) sm_s[j] = s * a.sm_scale * kLog2e;
-  }
-  __syncthreads();
-  const int32_t base = sm_work[0], n = sm_work[1];
-  for (int idx = tid; idx < a.group * D; idx += 256) {
-    const int j = idx / D, d = idx % D;
-    const int32_t h = g * a.group + j;
-    const float s_new = sm_s[j];
-    const float sink = a.sinks ? a.sinks[h] * kLog2e : -INFINITY;
-    float M = fmaxf(s_new, sink);
-    for (int32_t i = 0; i < n; ++i) M = fmaxf(M, a.ws_ml[((int64_t)(base + i) * a.H + h) * 2]);
-    const float w_new = exp2f(s_new - M);
-    float den = w_new + (a.sinks ? exp2f(sink - M) : 0.0f);
-    float num = w_new * sm_v[d];
-    for (int32_t i = 0; i < n; ++i) {
-      const int64_t row = (int64_t)(base + i) * a.H + h;
-      const float w = exp2f(a.ws_ml[row * 2] - M);
-      den += w * a.ws_ml[row * 2 + 1];
-      num += w * a.ws_o[row * D + d];
+    s *= a.sm_scale * kLog2e;
+    float M = s, den = 1.0f;
+    if (a.sinks) {
+      const float sk = a.sinks[h] * kLog2e;
+      M = fmaxf(s, sk);
+      den = __builtin_amdgcn_exp2f(s - M) + __builtin_amdgcn_exp2f(sk - M);
     }
-    a.out[((int64_t)b * a.H + h) * D + d] = (uint16_t)f32_to_bf16_bits(num / den);
+    const float w = __builtin_amdgcn_exp2f(s - M) / den;
+    for (int d = lane; d < D; d += 64) a.out[((int64_t)b * a.H + h) * D + d] = (uint16_t)f32_to_bf16_bits(w * sm_vn[d]);
   }
 }
 
 template <int D, bool FP8>
-static void launch_gqa(const GqaArgs& da, const GqaCombineArgs& ca, hipStream_t s) {
-  if (da.n_work > 0)
-    hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4>), dim3(da.n_work, da.G), dim3(256), 0, s, da);
-  hipLaunchKernelGGL((gqa_combine_kernel<D, FP8>), dim3(ca.B, ca.G), dim3(256), 0, s, ca);
+static void launch_gqa(const GqaArgs& a, int depth, bool any_lone, hipStream_t s) {
+  timing_mark(0, s);
+  if (a.n_work > 0) {
+    const dim3 grid(a.n_work, a.G);
+    if (depth >= 4) {
+      if (a.max_splits <= 1) hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, true, 4>), grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, false, 4>), grid, dim3(256), 0, s, a);
+    } else {
+      if (a.max_splits <= 1) hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, true, 2>), grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, false, 2>), grid, dim3(256), 0, s, a);
+    }
+  }
+  timing_mark(1, s);
+  if (a.max_splits > 1) hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.B, a.G), dim3(256), 0, s, a);
+  if (any_lone) hipLaunchKernelGGL((gqa_lone_token_kernel<D, FP8>), dim3(a.B, a.G), dim3(128), 0, s, a);
+  timing_mark(2, s);
 }
 
 }  // namespace sna
@@ -411,79 +511,62 @@ extern "C" int sna_paged_decode_gqa(const void* q, const void* k_cache, const vo
   if (window < 0 || table_width < 0 || table_stride < table_width || num_blocks < 1 || !(sm_scale > 0.0f))
     return fail(SNA_ERR_INVALID_ARGUMENT, "paged_decode_gqa: bad window %d, table %d/%lld, blocks %lld or scale %g",
                 window, table_width, (long long)table_stride, (long long)num_blocks, (double)sm_scale);
-  if (!plan || plan->tile != 32 || plan->split_tiles < 1 || plan->n_work < 0)
-    return fail(SNA_ERR_INVALID_ARGUMENT, "paged_decode_gqa: missing or foreign split plan");
+  if (!plan || plan->tile != 32 || plan->split_tiles < 1 || plan->n_work < 0 || plan->max_splits < 0 ||
+      plan->batch != B)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "paged_decode_gqa: missing or foreign split plan (made for %d rows)",
+                plan ? plan->batch : -1);
   if (B == 0) return SNA_OK;
   const bool fp8 = cache_dtype == SNA_DTYPE_FP8_E4M3FN;
+  const int64_t need = sna_decode_workspace_bytes(plan, num_q_heads, head_dim);
   if (!q || !k_cache || !v_cache || !block_table || !seq_lens || !k_new || !v_new || !out ||
-      (fp8 && (!k_scale || !v_scale)) || (plan->n_work > 0 && !workspace))
+      (fp8 && (!k_scale || !v_scale)) || (need > 0 && !workspace))
     return fail(SNA_ERR_INVALID_ARGUMENT, "paged_decode_gqa: null pointer");
   if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
     return fail(SNA_ERR_INVALID_ARGUMENT, "paged_decode_gqa: q and caches must be 16-byte aligned");
-  const int64_t need = sna_decode_workspace_bytes(plan, num_q_heads, head_dim);
-  if (plan->n_work > 0 && workspace_bytes < need)
+  if (workspace_bytes < need)
     return fail(SNA_ERR_WORKSPACE, "paged_decode_gqa: workspace of %lld bytes, the plan needs %lld",
                 (long long)workspace_bytes, (long long)need);
-  if ((int64_t)plan->n_work > 2147483647LL || num_kv_heads > 65535 || B > 2147483647)
-    return fail(SNA_ERR_INVALID_ARGUMENT, "paged_decode_gqa: grid too large");
+  if (num_kv_heads > 65535) return fail(SNA_ERR_INVALID_ARGUMENT, "paged_decode_gqa: grid too large");
 
+  GqaArgs a;
+  a.q = (const uint16_t*)q;
+  a.k_cache = (uint8_t*)k_cache;
+  a.v_cache = (uint8_t*)v_cache;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
+  a.table = block_table;
+  a.table_stride = table_stride;
+  a.table_width = table_width;
+  a.seq_lens = seq_lens;
+  a.k_new = (const uint16_t*)k_new;
+  a.v_new = (const uint16_t*)v_new;
+  a.new_slots = new_slots;
+  a.sinks = sinks;
+  a.B = B;
+  a.H = num_q_heads;
+  a.G = num_kv_heads;
+  a.group = group;
+  a.P = page_size;
+  a.num_blocks = num_blocks;
+  a.window = window;
+  a.sm_scale = sm_scale;
+  a.split_tiles = plan->split_tiles;
+  a.n_work = plan->n_work;
+  a.max_splits = plan->max_splits;
   float* ws = (float*)workspace;
-  const int64_t n_o = (int64_t)plan->n_work * num_q_heads * head_dim;
-  GqaArgs da;
-  da.q = (const uint16_t*)q;
-  da.k_cache = (const uint8_t*)k_cache;
-  da.v_cache = (const uint8_t*)v_cache;
-  da.k_scale = k_scale;
-  da.v_scale = v_scale;
-  da.table = block_table;
-  da.table_stride = table_stride;
-  da.table_width = table_width;
-  da.seq_lens = seq_lens;
-  da.B = B;
-  da.H = num_q_heads;
-  da.G = num_kv_heads;
-  da.group = group;
-  da.P = page_size;
-  da.num_blocks = num_blocks;
-  da.window = window;
-  da.sm_scale = sm_scale;
-  da.split_tiles = plan->split_tiles;
-  da.n_work = plan->n_work;
-  da.ws_o = ws;
-  da.ws_ml = ws ? ws + n_o : nullptr;
-
-  GqaCombineArgs ca;
-  ca.q = (const uint16_t*)q;
-  ca.k_new = (const uint16_t*)k_new;
-  ca.v_new = (const uint16_t*)v_new;
-  ca.new_slots = new_slots;
-  ca.k_cache = (uint8_t*)k_cache;
-  ca.v_cache = (uint8_t*)v_cache;
-  ca.k_scale = k_scale;
-  ca.v_scale = v_scale;
-  ca.sinks = sinks;
-  ca.seq_lens = seq_lens;
-  ca.B = B;
-  ca.H = num_q_heads;
-  ca.G = num_kv_heads;
-  ca.group = group;
-  ca.P = page_size;
-  ca.num_blocks = num_blocks;
-  ca.window = window;
-  ca.sm_scale = sm_scale;
-  ca.split_tiles = plan->split_tiles;
-  ca.n_work = plan->n_work;
-  ca.ws_o = da.ws_o;
-  ca.ws_ml = da.ws_ml;
-  ca.out = (uint16_t*)out;
+  a.ws_o = need > 0 ? ws : nullptr;
+  a.ws_ml = need > 0 ? ws + (int64_t)B * plan->max_splits * num_q_heads * head_dim : nullptr;
+  a.out = (uint16_t*)out;
+  // a row with no prior key has no split: the lone-token pass writes it (launched unless the plan rules it out)
+  const bool any_lone = plan->empty_rows != 0;
 
   hipStream_t s = (hipStream_t)stream;
   if (head_dim == 128) {
-    if (fp8) launch_gqa<128, true>(da, ca, s);
-    else launch_gqa<128, false>(da, ca, s);
+    if (fp8) launch_gqa<128, true>(a, plan->depth, any_lone, s);
+    else launch_gqa<128, false>(a, plan->depth, any_lone, s);
   } else {
-    if (fp8) launch_gqa<64, true>(da, ca, s);
-    else launch_gqa<64, false>(da, ca, s);
+    if (fp8) launch_gqa<64, true>(a, plan->depth, any_lone, s);
+    else launch_gqa<64, false>(a, plan->depth, any_lone, s);
   }
   return check_launch("paged_decode_gqa");
 }

@@ -1,16 +1,21 @@
 // Absorbed-MLA decode (paged, per-token FP8 scale) and DSA sparse decode (index lists over 640-byte packed rows):
-// split-K online softmax with all of a row's 16 heads in one wave, MFMA for QK^T and PV, and a combine pass that adds
-// the step's own row, normalizes and (paged) stores the row.
+// split-K online softmax with all 16 heads of a head group in one wave, MFMA for QK^T and PV. The workgroup of a
+// row's first split also attends the row's own new token in-band (and, paged, stores it). A row with one split
+// writes its final output; otherwise a combine pass merges the splits.
 //
 // Row formats:
 //   ROWS576  [latent 512 | k_pe 64] e4m3fn, one fp32 dequantization scale per token slot (row_scale).
 //   ROWS640  [k_pe 64 bf16 | latent 512 e4m3fn, permuted], one per-tensor kv_scale. Latent dim c = 256a + 128b + p
 //            sits at latent byte 256a + 2p + b.
 //
+// Work: one workgroup of 4 waves per (row, split, 16-head group). The workgroup first resolves the row id of every
+// key of its split into LDS (the block-table walk, or for DSA the index -> block -> row walk). Each wave then takes
+// 16-key tiles round-robin, the next tile's loads in flight while it computes one.
+//
 // Lane roles (lane = 16 * g4 + li), 16-key tiles:
 //   QK   S^T[key, head] = K[key, :] . Q[head, :]   v_mfma_f32_16x16x32_bf16, 18 steps over the 576 dims. Lane
 //        (g4, li) feeds 144 (ROWS576) or 160 (ROWS640) bytes of key li's row, loaded straight from HBM, and head li's
-//        query elements under the same K-index map.
+//        query elements under the same K-index map. The query operand lives in LDS in lane order.
 //   PV   O^T[latent byte, head] = V^T[byte, keys] . P^T[keys, head]   v_mfma_f32_16x16x16_bf16, K = the 16 keys,
 //        lane (g4, *) supplying keys 4 g4 .. 4 g4 + 3, the S^T rows it holds. The latent bytes of the tile go
 //        through LDS. For d-tile (q, r), lane (g4, i) reads dword (64 q + 4 i) of rows 4 g4 .. 4 g4 + 3, transposes
@@ -25,14 +30,16 @@ enum { ROWS576 = 0, ROWS640 = 1 };
 
 constexpr int kLatent = 512;
 constexpr int kRope = 64;
-constexpr int kLdsRow = 528;  // latent bytes of one key row in LDS, padded so row 4 apart hit other banks
+constexpr int kLdsRow = 528;        // latent bytes of one key row in LDS, padded so rows 4 apart hit other banks
+constexpr int kMaxSplitKeys = 4096;  // keys one split may cover (its row ids live in LDS)
+constexpr float kMlaRescaleSlack = 8.0f;
 
 struct MlaArgs {
   const uint16_t* ql;    // [B, H, 512]
   const uint16_t* qpe;   // [B, H, 64]
-  const uint8_t* cache;  // rows
-  const float* row_scale;
-  float kv_scale;
+  uint8_t* cache;        // rows
+  float* row_scale;      // ROWS576
+  float kv_scale;        // ROWS640
   const int32_t* table;
   int64_t table_stride;
   int32_t table_width;
@@ -40,30 +47,14 @@ struct MlaArgs {
   const int32_t* indices;    // sparse [B, n_indices]
   int32_t n_indices;
   const int32_t* positions;  // sparse [B]
+  const uint16_t* own;       // [B, 576] bf16: ROWS576 [latent | rope], ROWS640 [rope | latent]
+  const int64_t* new_slots;  // paged: store the own row there (NULL: no store)
   int32_t B, H, P;
   int64_t num_blocks;
   float sm_scale;
-  int32_t split_tiles, n_work;
-  float* ws_o;   // [n_work, H, 512]  unnormalized partials, latent-byte order
-  float* ws_ml;  // [n_work, H, 2]
-};
-
-struct MlaCombineArgs {
-  const uint16_t* ql;
-  const uint16_t* qpe;
-  const uint16_t* own;  // [B, 576] bf16: ROWS576 [latent | rope], ROWS640 [rope | latent]
-  const int64_t* new_slots;
-  uint8_t* cache;
-  float* row_scale;
-  float kv_scale;
-  const int32_t* seq_lens;
-  int32_t n_indices;
-  int32_t B, H, P;
-  int64_t num_blocks;
-  float sm_scale;
-  int32_t split_tiles, n_work;
-  const float* ws_o;
-  const float* ws_ml;
+  int32_t split_tiles, n_work, max_splits;
+  float* ws_o;   // [B, max_splits, H, 512]  unnormalized partials, latent-byte order
+  float* ws_ml;  // [B, max_splits, H, 2]
   uint16_t* out;
   float* lse_out;
 };
@@ -102,22 +93,119 @@ __device__ __forceinline__ int chunk_offset(int g4, int c) {
   }
 }
 
-template <int FMT, int WAVES>
+// Latent byte offset of chunk c of lane group g4, or -1 for a rope chunk.
+template <int FMT>
+__device__ __forceinline__ int chunk_latent(int g4, int c) {
+  if constexpr (FMT == ROWS576) {
+    const int off = 144 * g4 + 16 * c;
+    return off < kLatent ? off : -1;
+  } else {
+    return c < 2 ? -1 : 128 * g4 + 16 * (c - 2);
+  }
+}
+
+// The query element pair-block of step s, lane group g4 for head row qlp/qpp (8 bf16, packed).
+template <int FMT>
+__device__ __forceinline__ uint4 query_chunk(const uint16_t* qlp, const uint16_t* qpp, int g4, int s) {
+  if constexpr (FMT == ROWS576) {
+    const int dim = 144 * g4 + 8 * s;  // natural order: latent then rope
+    return dim < kLatent ? ld16(qlp + dim) : ld16(qpp + (dim - kLatent));
+  } else {
+    if (s < 2) return ld16(qpp + 16 * g4 + 8 * s);
+    uint32_t e[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) e[i] = qlp[latent_dim_of_byte(128 * g4 + 8 * (s - 2) + i)];
+    return make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
+  }
+}
+
+template <int FMT>
+struct MlaRing {
+  uint32_t raw[RowFmt<FMT>::kLaneChunks][4];
+  float kscale[4];
+  uint32_t vmask;  // bit k: key k of the tile is valid
+};
+
+// The own row of sequence b, dequantized in natural order [latent 512 | rope 64] into sm_row, stored into the
+// pool when paged and st is set. Every thread of the workgroup calls it. ROWS576 quantizes with the row's own
+// per-token scale, ROWS640 with kv_scale and the row's bf16 rope.
+template <int FMT, int NT>
+__device__ void own_row_dequant(const MlaArgs& a, int b, bool st, float* sm_row, float* sm_red) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint16_t* own = a.own + (int64_t)b * 576;
+  if constexpr (FMT == ROWS576) {
+    float m = 0.0f;
+    for (int i = tid; i < 576; i += NT) m = fmaxf(m, fabsf(bf16_bits_to_f32(own[i])));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if (lane == 0) sm_red[wave] = m;
+    __syncthreads();
+    float mm = sm_red[0];
+    for (int w = 1; w < NT / 64; ++w) mm = fmaxf(mm, sm_red[w]);
+    const float s = scale_from_absmax(mm);
+    int64_t slot = -1;
+    if (st && a.new_slots) slot = redirect_slot(a.new_slots[b], a.num_blocks * a.P);
+    for (int i = tid; i < 576; i += NT) {
+      const uint32_t qb = quantize_e4m3fn(own[i], s);
+      sm_row[i] = e4m3fn_to_f32(qb) * s;
+      if (slot >= 0) a.cache[slot * 576 + i] = (uint8_t)qb;
+    }
+    if (slot >= 0 && tid == 0) a.row_scale[slot] = s;
+  } else {
+    for (int i = tid; i < 576; i += NT) {
+      const uint32_t bits = own[i];
+      if (i < kRope)
+        sm_row[kLatent + i] = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(bits) / a.kv_scale)) * a.kv_scale;
+      else
+        sm_row[i - kRope] = e4m3fn_to_f32(quantize_e4m3fn(bits, a.kv_scale)) * a.kv_scale;
+    }
+  }
+  __syncthreads();
+}
+
+// Score of the own row for heads [16 hg, 16 hg + nh), log2 domain, into sm_sn.
+template <int NT>
+__device__ void own_row_scores(const MlaArgs& a, int b, int hg, int nh, const float* sm_row, float* sm_sn) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int j = wave; j < nh; j += NT / 64) {
+    const int32_t h = 16 * hg + j;
+    const uint16_t* qlp = a.ql + ((int64_t)b * a.H + h) * kLatent;
+    const uint16_t* qpp = a.qpe + ((int64_t)b * a.H + h) * kRope;
+    float s = 0.0f;
+    for (int d = lane; d < kLatent; d += 64) s += bf16_bits_to_f32(qlp[d]) * sm_row[d];
+    s += bf16_bits_to_f32(qpp[lane]) * sm_row[kLatent + lane];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if (lane == 0) sm_sn[j] = s * a.sm_scale * kLog2e;
+  }
+  __syncthreads();
+}
+
+template <int FMT, int WAVES, bool FINAL>
 __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
   constexpr int NCH = RowFmt<FMT>::kLaneChunks;
   constexpr int ROWB = RowFmt<FMT>::kRowBytes;
   constexpr bool SPARSE = FMT == ROWS640;
+  constexpr int NT = 64 * WAVES;
+  using Ring = MlaRing<FMT>;
 
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform, so tile indices stay scalar
+  const int lane = tid & 63;
   const int g4 = lane >> 4;
   const int li = lane & 15;
   const int hg = blockIdx.y;  // 16-head group
+  const int nh = min(16, a.H - 16 * hg);
 
+  __shared__ uint4 sm_q[18][64];                                    // query operand, lane order
+  __shared__ int32_t sm_rowid[kMaxSplitKeys];                       // row id of each key of the split, -1 = none
   __shared__ __attribute__((aligned(16))) uint8_t sm_lat[WAVES][16 * kLdsRow];
   __shared__ float sm_o[16][kLatent + 4];
   __shared__ float sm_m[WAVES][16];
   __shared__ float sm_l[WAVES][16];
+  __shared__ float sm_row[576];
+  __shared__ float sm_sn[16];
+  __shared__ float sm_red[WAVES];
 
   // Paged: keys are positions [0, seq_len - 1). Sparse: keys are index-list entries [0, n_indices), modelled as a
   // "sequence" of n_indices + 1 so the same decomposition applies (every row has the same split count).
@@ -131,197 +219,180 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
     }
   } else {
     locate_work<16>(a.seq_lens, a.B, 0, a.split_tiles, (int32_t)blockIdx.x, b, split);
+    b = __builtin_amdgcn_readfirstlane(b);
+    split = __builtin_amdgcn_readfirstlane(split);
   }
   if (b < 0) return;
 
-  int32_t klo = 0, khi;
-  if constexpr (SPARSE) {
-    khi = a.n_indices;
-  } else {
-    khi = a.seq_lens[b] - 1;
-  }
+  const int32_t khi = SPARSE ? a.n_indices : a.seq_lens[b] - 1;
   const int32_t t_first = split * a.split_tiles;
   const int32_t t_last = min(t_first + a.split_tiles, (khi + 15) / 16);
+  const int32_t kbase = t_first * 16;
+  const int32_t nkeys = (t_last - t_first) * 16;
 
-  // ---- query operand: 18 steps x 8 elements for head (16 hg + li) ----
-  uint32_t qv[18][4];
-  {
-    const int32_t h = 16 * hg + li;
-    const bool live = h < a.H;
-    const uint16_t* qlp = a.ql + ((int64_t)b * a.H + (live ? h : 0)) * kLatent;
-    const uint16_t* qpp = a.qpe + ((int64_t)b * a.H + (live ? h : 0)) * kRope;
-#pragma unroll
-    for (int s = 0; s < 18; ++s) {
-      uint4 w = make_uint4(0, 0, 0, 0);
-      if (live) {
-        if constexpr (FMT == ROWS576) {
-          const int dim = 144 * g4 + 8 * s;  // natural order: latent then rope
-          w = dim < kLatent ? ld16(qlp + dim) : ld16(qpp + (dim - kLatent));
-        } else {
-          if (s < 2) {
-            w = ld16(qpp + 16 * g4 + 8 * s);
-          } else {
-            uint32_t e[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) e[i] = qlp[latent_dim_of_byte(128 * g4 + 8 * (s - 2) + i)];
-            w = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
-          }
-        }
-      }
-      qv[s][0] = w.x;
-      qv[s][1] = w.y;
-      qv[s][2] = w.z;
-      qv[s][3] = w.w;
+  // ---- the query operand into LDS, and every key's row id ----
+  for (int e = tid; e < 18 * 64; e += NT) {
+    const int s = e >> 6, ln = e & 63;
+    const int32_t h = 16 * hg + (ln & 15);
+    uint4 w = make_uint4(0, 0, 0, 0);
+    if (h < a.H) {
+      const uint16_t* qlp = a.ql + ((int64_t)b * a.H + h) * kLatent;
+      const uint16_t* qpp = a.qpe + ((int64_t)b * a.H + h) * kRope;
+      w = query_chunk<FMT>(qlp, qpp, ln >> 4, s);
     }
+    sm_q[s][ln] = w;
   }
-
-  const float base_scale = a.sm_scale * kLog2e * (SPARSE ? a.kv_scale : 1.0f);
   const int32_t* trow = a.table + (int64_t)b * a.table_stride;
   const int64_t n_rows = a.num_blocks * a.P;
   int32_t qpos = 0;
   if constexpr (SPARSE) qpos = a.positions[b];
+  for (int k = tid; k < nkeys; k += NT) {
+    const int32_t key = kbase + k;
+    int32_t row = -1;
+    if constexpr (SPARSE) {
+      const int32_t pos = key < khi ? a.indices[(int64_t)b * a.n_indices + key] : -1;
+      if (pos >= 0 && pos <= qpos) {
+        const int32_t blk = pos / a.P;
+        if (blk < a.table_width) {
+          const int32_t e = trow[blk];
+          if (e >= 0 && (int64_t)e < a.num_blocks) {
+            const int64_t r = (int64_t)e * a.P + pos % a.P;
+            if (r < n_rows) row = (int32_t)r;
+          }
+        }
+      }
+    } else {
+      if (key < khi) {
+        const int32_t col = key / a.P;
+        const int32_t e = col < a.table_width ? trow[col] : -1;
+        if (e >= 0 && (int64_t)e < a.num_blocks) row = e * a.P + key % a.P;
+      }
+    }
+    sm_rowid[k] = row;
+  }
+  __syncthreads();
 
-  float m_run = kNegBig;
+  const float base_scale = a.sm_scale * kLog2e * (SPARSE ? a.kv_scale : 1.0f);
+
+  auto issue = [&](Ring& R, int32_t tile) {
+    const int32_t k0 = tile * 16 - kbase;
+    const int32_t row = sm_rowid[k0 + li];
+    const bool kvalid = row >= 0;
+    R.vmask = (uint32_t)(__ballot(kvalid) & 0xffffull);
+    const uint8_t* rp = a.cache + (int64_t)(kvalid ? row : 0) * ROWB;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const uint4 w = ld16(rp + chunk_offset<FMT>(g4, c));
+      R.raw[c][0] = w.x;
+      R.raw[c][1] = w.y;
+      R.raw[c][2] = w.z;
+      R.raw[c][3] = w.w;
+    }
+    if constexpr (!SPARSE) {
+      // per-token scales of keys 4 g4 .. 4 g4 + 3: consecutive slots of one page
+      const int32_t srow = sm_rowid[k0 + 4 * g4];
+      const float4 s4 = *reinterpret_cast<const float4*>(a.row_scale + (srow >= 0 ? srow : 0));
+      R.kscale[0] = s4.x;
+      R.kscale[1] = s4.y;
+      R.kscale[2] = s4.z;
+      R.kscale[3] = s4.w;
+    }
+  };
+
+  float m_ref = kNegBig;
   float l_run = 0.0f;
   f32x4_t acc[8][4];
 #pragma unroll
   for (int q = 0; q < 8; ++q)
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[q][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
   uint8_t* lds = sm_lat[wave];
 
-  for (int32_t tile = t_first + wave; tile < t_last; tile += WAVES) {
-    const int32_t T0 = tile * 16;
-    // ---- the row of key li (this lane's load) and the validity of every key of the tile ----
-    int64_t row = 0;
-    bool kvalid;
-    if constexpr (SPARSE) {
-      const int32_t k = T0 + li;
-      const int32_t pos = k < khi ? a.indices[(int64_t)b * a.n_indices + k] : -1;
-      kvalid = false;
-      if (pos >= 0 && pos <= qpos) {
-        const int32_t blk = pos / a.P;
-        if (blk < a.table_width) {
-          const int32_t e = trow[blk];
-          if (e >= 0 && (int64_t)e < a.num_blocks) {
-            row = (int64_t)e * a.P + pos % a.P;
-            kvalid = row < n_rows;
-            if (!kvalid) row = 0;
-          }
-        }
-      }
-    } else {
-      const int32_t col = T0 / a.P;
-      const int32_t e = col < a.table_width ? trow[col] : -1;
-      const bool pv = e >= 0 && (int64_t)e < a.num_blocks;
-      const int32_t pos = T0 + li;
-      kvalid = pv && pos >= klo && pos < khi;
-      row = (pv ? (int64_t)e * a.P : 0) + (T0 % a.P) + li;
+  auto compute = [&](Ring& R) {
+    const bool full = R.vmask == 0xffffu;
+    if (!full) {
+      // a masked key's bytes are zeroed (a stale NaN there would survive p = 0)
+      const bool mine = (R.vmask >> li) & 1u;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) R.raw[c][i] = mine ? R.raw[c][i] : 0u;
     }
-    const uint32_t vmask = (uint32_t)(__ballot(kvalid) & 0xffffull);  // bit k: key k of the tile is valid
-
-    // ---- loads: NCH 16-byte chunks of row `row` ----
-    uint32_t raw[NCH][4];
-    const uint8_t* rp = a.cache + row * ROWB;
+    // latent bytes to LDS for the PV transpose
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      const uint4 w = ld16(rp + chunk_offset<FMT>(g4, c));
-      raw[c][0] = kvalid ? w.x : 0u;
-      raw[c][1] = kvalid ? w.y : 0u;
-      raw[c][2] = kvalid ? w.z : 0u;
-      raw[c][3] = kvalid ? w.w : 0u;
-    }
-    float kscale[4] = {1.f, 1.f, 1.f, 1.f};
-    if constexpr (!SPARSE) {
-      // per-token scales of keys 4 g4 .. 4 g4 + 3: four consecutive slots of one page
-      const int32_t col = T0 / a.P;
-      const int32_t e = col < a.table_width ? trow[col] : -1;
-      const bool pv = e >= 0 && (int64_t)e < a.num_blocks;
-      const int64_t srow = (pv ? (int64_t)e * a.P : 0) + (T0 % a.P) + 4 * g4;
-      const float4 s4 = *reinterpret_cast<const float4*>(a.row_scale + srow);
-      kscale[0] = s4.x;
-      kscale[1] = s4.y;
-      kscale[2] = s4.z;
-      kscale[3] = s4.w;
-    }
-
-    // ---- latent bytes to LDS for the PV transpose ----
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      int lat;  // latent byte offset of the chunk, or -1
-      if constexpr (FMT == ROWS576) {
-        const int off = chunk_offset<FMT>(g4, c);
-        lat = off < kLatent ? off : -1;
-      } else {
-        lat = c < 2 ? -1 : 128 * g4 + 16 * (c - 2);
-      }
+      const int lat = chunk_latent<FMT>(g4, c);
       if (lat >= 0)
-        *reinterpret_cast<uint4*>(lds + li * kLdsRow + lat) = make_uint4(raw[c][0], raw[c][1], raw[c][2], raw[c][3]);
+        *reinterpret_cast<uint4*>(lds + li * kLdsRow + lat) = make_uint4(R.raw[c][0], R.raw[c][1], R.raw[c][2],
+                                                                          R.raw[c][3]);
     }
-
-    // ---- S^T = K Q^T ----
+    // S^T = K Q^T
     f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 18; ++s) {
       uint32_t op[4];
       if constexpr (FMT == ROWS576) {
         const int c = s >> 1, hf = s & 1;
-        fp8x4_to_bf16x4(raw[c][2 * hf], op[0], op[1]);
-        fp8x4_to_bf16x4(raw[c][2 * hf + 1], op[2], op[3]);
+        fp8x4_to_bf16x4(R.raw[c][2 * hf], op[0], op[1]);
+        fp8x4_to_bf16x4(R.raw[c][2 * hf + 1], op[2], op[3]);
       } else {
         if (s < 2) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) op[i] = raw[s][i];
+          for (int i = 0; i < 4; ++i) op[i] = R.raw[s][i];
         } else {
           const int c = 2 + ((s - 2) >> 1), hf = (s - 2) & 1;
-          fp8x4_to_bf16x4(raw[c][2 * hf], op[0], op[1]);
-          fp8x4_to_bf16x4(raw[c][2 * hf + 1], op[2], op[3]);
+          fp8x4_to_bf16x4(R.raw[c][2 * hf], op[0], op[1]);
+          fp8x4_to_bf16x4(R.raw[c][2 * hf + 1], op[2], op[3]);
         }
       }
-      sc = mfma_16x16x32_bf16(op, qv[s], sc);
+      const uint4 qw = sm_q[s][lane];
+      const uint32_t qop[4] = {qw.x, qw.y, qw.z, qw.w};
+      sc = mfma_16x16x32_bf16(op, qop, sc);
     }
-
-    // ---- mask, online softmax ----
+    // mask, online softmax with a lazily moved reference maximum
     float x[4];
     float tmax = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const bool ok = (vmask >> (4 * g4 + r)) & 1u;
-      const float v = ok ? sc[r] * base_scale * kscale[r] : -INFINITY;
-      x[r] = v;
-      tmax = fmaxf(tmax, v);
+      const bool ok = (R.vmask >> (4 * g4 + r)) & 1u;
+      const float ks = SPARSE ? 1.0f : R.kscale[r];
+      x[r] = ok ? sc[r] * base_scale * ks : -INFINITY;
+      tmax = fmaxf(tmax, x[r]);
     }
     tmax = max_across_groups(tmax);
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = exp2f(m_run - m_new);
-    m_run = m_new;
-    float p[4], psum = 0.0f;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p[r] = exp2f(x[r] - m_new);
-      psum += p[r];
-    }
-    l_run = l_run * alpha + psum;
-    if (alpha != 1.0f) {
+    const bool bump = tmax > m_ref + kMlaRescaleSlack;
+    if (__any(bump)) {
+      const float m_new = bump ? tmax : m_ref;
+      const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new);
+      m_ref = m_new;
+      l_run *= alpha;
 #pragma unroll
       for (int q = 0; q < 8; ++q)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[q][r] *= alpha;
     }
-    // V is dequantized through P: p' = p * scale(key) (a masked key has p = 0 and a zeroed row)
-    const bool ok0 = (vmask >> (4 * g4)) & 1u, ok1 = (vmask >> (4 * g4 + 1)) & 1u;
-    const bool ok2 = (vmask >> (4 * g4 + 2)) & 1u, ok3 = (vmask >> (4 * g4 + 3)) & 1u;
-    const uint32_t pop[2] = {pack_bf16x2(ok0 ? p[0] * kscale[0] : 0.f, ok1 ? p[1] * kscale[1] : 0.f),
-                             pack_bf16x2(ok2 ? p[2] * kscale[2] : 0.f, ok3 ? p[3] * kscale[3] : 0.f)};
-
-    // ---- O^T += V^T P^T over 32 d-tiles ----
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = __builtin_amdgcn_exp2f(x[r] - m_ref);
+      l_run += p[r];
+    }
+    // V is dequantized through P: p' = p * scale(key) (a masked key has p = 0 and zeroed bytes)
+    float pv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool ok = (R.vmask >> (4 * g4 + r)) & 1u;
+      pv[r] = ok ? p[r] * (SPARSE ? 1.0f : R.kscale[r]) : 0.0f;
+    }
+    const uint32_t pop[2] = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
+    // O^T += V^T P^T over 32 d-tiles
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       uint32_t w[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) w[e] = *reinterpret_cast<const uint32_t*>(lds + (4 * g4 + e) * kLdsRow + 64 * q + 4 * li);
+      for (int e = 0; e < 4; ++e)
+        w[e] = *reinterpret_cast<const uint32_t*>(lds + (4 * g4 + e) * kLdsRow + 64 * q + 4 * li);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const uint32_t xr = ((w[0] >> (8 * r)) & 0xffu) | (((w[1] >> (8 * r)) & 0xffu) << 8) |
@@ -332,19 +403,42 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
       }
     }
     __builtin_amdgcn_wave_barrier();
+  };
+
+  // ---- the tile loop: two register buffers, the next tile's loads in flight while one computes ----
+  {
+    Ring R0, R1;
+    int32_t t = t_first + wave;
+    if (t < t_last) issue(R0, t);
+    while (t < t_last) {
+      if (t + WAVES < t_last) issue(R1, t + WAVES);
+      compute(R0);
+      t += WAVES;
+      if (t >= t_last) break;
+      if (t + WAVES < t_last) issue(R0, t + WAVES);
+      compute(R1);
+      t += WAVES;
+    }
   }
 
-  // ---- merge the waves: common max, then sum the rescaled accumulators through LDS ----
+  // ---- the own row, attended in-band by the row's first split (paged: and stored, by head group 0) ----
+  const bool own = split == 0;  // uniform
+  if (own) {
+    own_row_dequant<FMT, NT>(a, b, hg == 0, sm_row, sm_red);
+    own_row_scores<NT>(a, b, hg, nh, sm_row, sm_sn);
+  }
+
+  // ---- merge: a common maximum per head, then the waves' rescaled accumulators summed through LDS ----
   const float l_tot = sum_across_groups(l_run);
   if (g4 == 0) {
-    sm_m[wave][li] = m_run;
+    sm_m[wave][li] = m_ref;
     sm_l[wave][li] = l_tot;
   }
   __syncthreads();
-  float M = sm_m[0][li];
+  float M = own ? sm_sn[li] : -INFINITY;
 #pragma unroll
-  for (int w = 1; w < WAVES; ++w) M = fmaxf(M, sm_m[w][li]);
-  const float f = exp2f(m_run - M);
+  for (int w = 0; w < WAVES; ++w) M = fmaxf(M, sm_m[w][li]);
+  const float f = __builtin_amdgcn_exp2f(m_ref - M);
 #pragma unroll
   for (int w = 0; w < WAVES; ++w) {
     if (wave == w) {
@@ -362,117 +456,128 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
     }
     __syncthreads();
   }
-  const int64_t wrow = (int64_t)blockIdx.x * a.H + 16 * hg;
   const float oscale = SPARSE ? a.kv_scale : 1.0f;
-  const int nh = min(16, a.H - 16 * hg);
-  for (int idx = threadIdx.x; idx < nh * kLatent; idx += 64 * WAVES) {
-    const int j = idx / kLatent, beta = idx % kLatent;
-    a.ws_o[(wrow + j) * kLatent + beta] = sm_o[j][beta] * oscale;
-  }
-  if (threadIdx.x < nh) {
-    const int j = threadIdx.x;
-    float Mj = sm_m[0][j];
-    for (int w = 1; w < WAVES; ++w) Mj = fmaxf(Mj, sm_m[w][j]);
-    float l = 0.0f;
-    for (int w = 0; w < WAVES; ++w) l += exp2f(sm_m[w][j] - Mj) * sm_l[w][j];
-    a.ws_ml[(wrow + j) * 2] = Mj;
-    a.ws_ml[(wrow + j) * 2 + 1] = l;
-  }
-}
-
-// One workgroup per (sequence, 16-head group): the own row in-band (and its store), then the split merge.
-template <int FMT>
-__global__ __launch_bounds__(256) void mla_combine_kernel(MlaCombineArgs a) {
-  constexpr bool SPARSE = FMT == ROWS640;
-  const int b = blockIdx.x, hg = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  __shared__ float sm_row[576];  // the own row, dequantized, natural order [latent 512 | rope 64]
-  __shared__ float sm_s[16];
-  __shared__ float sm_red[4];
-  __shared__ int32_t sm_work[2];
-  const int nh = min(16, a.H - 16 * hg);
-
-  if (wave == 0) {
-    int32_t n, base;
-    if constexpr (SPARSE) {
-      n = splits_of<16>(a.n_indices + 1, 0, a.split_tiles);
-      base = b * n;
-    } else {
-      n = splits_of<16>(a.seq_lens[b], 0, a.split_tiles);
-      base = work_base_of<16>(a.seq_lens, b, 0, a.split_tiles);
-    }
-    if (base > a.n_work) base = a.n_work;
-    if (base + n > a.n_work) n = a.n_work - base;
-    if (lane == 0) {
-      sm_work[0] = base;
-      sm_work[1] = n;
-    }
-  }
-  // ---- own row: quantize -> dequantize (and store) ----
-  const uint16_t* own = a.own + (int64_t)b * 576;
-  if constexpr (!SPARSE) {
-    float m = 0.0f;
-    for (int i = tid; i < 576; i += 256) m = fmaxf(m, fabsf(bf16_bits_to_f32(own[i])));
+  const int32_t S = a.max_splits;
+  for (int idx = tid; idx < nh * kLatent; idx += NT) {
+    const int j = idx / kLatent, c = idx % kLatent;  // c: the latent dim written (FINAL), or byte (partial)
+    const int32_t h = 16 * hg + j;
+    float Mj = own ? sm_sn[j] : -INFINITY;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    if (lane == 0) sm_red[wave] = m;
-    __syncthreads();
-    const float s = scale_from_absmax(fmaxf(fmaxf(sm_red[0], sm_red[1]), fmaxf(sm_red[2], sm_red[3])));
-    const bool store = a.new_slots != nullptr && hg == 0;
-    const int64_t slot = store ? redirect_slot(a.new_slots[b], a.num_blocks * a.P) : 0;
-    for (int i = tid; i < 576; i += 256) {
-      const uint32_t qb = quantize_e4m3fn(own[i], s);
-      sm_row[i] = e4m3fn_to_f32(qb) * s;
-      if (store) a.cache[slot * 576 + i] = (uint8_t)qb;
-    }
-    if (store && tid == 0) a.row_scale[slot] = s;
-  } else {
-    // [rope 64 | latent 512] in, as the 640-byte row would hold it, dequantized back with kv_scale
-    for (int i = tid; i < 576; i += 256) {
-      const uint32_t bits = own[i];
-      float v;
-      if (i < kRope) {
-        v = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(bits) / a.kv_scale)) * a.kv_scale;
-        sm_row[kLatent + i] = v;
-      } else {
-        v = e4m3fn_to_f32(quantize_e4m3fn(bits, a.kv_scale)) * a.kv_scale;
-        sm_row[i - kRope] = v;
+    for (int w = 0; w < WAVES; ++w) Mj = fmaxf(Mj, sm_m[w][j]);
+    float l = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) l += __builtin_amdgcn_exp2f(sm_m[w][j] - Mj) * sm_l[w][j];
+    const float e_own = own ? __builtin_amdgcn_exp2f(sm_sn[j] - Mj) : 0.0f;
+    l += e_own;
+    if constexpr (FINAL) {
+      const int beta = SPARSE ? latent_byte_of_dim(c) : c;
+      float o = sm_o[j][beta] * oscale;
+      if (own) o += e_own * sm_row[c];
+      a.out[((int64_t)b * a.H + h) * kLatent + c] = (uint16_t)f32_to_bf16_bits(o / l);
+      if (a.lse_out && c == 0) a.lse_out[(int64_t)b * a.H + h] = (Mj + __log2f(l)) * 0.6931471805599453f;
+    } else {
+      const int beta = c;
+      float o = sm_o[j][beta] * oscale;
+      if (own) o += e_own * sm_row[SPARSE ? latent_dim_of_byte(beta) : beta];
+      const int64_t row = ((int64_t)b * S + split) * a.H + h;
+      a.ws_o[row * kLatent + beta] = o;
+      if (beta == 0) {
+        a.ws_ml[row * 2] = Mj;
+        a.ws_ml[row * 2 + 1] = l;
       }
     }
   }
-  __syncthreads();
-  // ---- the own row's score per head (log2 domain) ----
-  for (int j = wave; j < nh; j += 4) {
-    const int32_t h = 16 * hg + j;
-    const uint16_t* qlp = a.ql + ((int64_t)b * a.H + h) * kLatent;
-    const uint16_t* qpp = a.qpe + ((int64_t)b * a.H + h) * kRope;
-    float s = 0.0f;
-    for (int d = lane; d < kLatent; d += 64) s += bf16_bits_to_f32(qlp[d]) * sm_row[d];
-    s += bf16_bits_to_f32(qpp[lane]) * sm_row[kLatent + lane];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-    if (lane == 0) sm_s[j] = s * a.sm_scale * kLog2e;
+}
+
+// Merge of a row's splits per (row, head): out = sum_s e_s o_s / sum_s e_s l_s, lse = M + log(sum), with
+// e_s = exp2(m_s - M) formed once per head in LDS.
+template <int FMT>
+__global__ __launch_bounds__(128) void mla_combine_kernel(MlaArgs a) {
+  constexpr bool SPARSE = FMT == ROWS640;
+  const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int32_t n = min(SPARSE ? splits_of<16>(a.n_indices + 1, 0, a.split_tiles)
+                               : splits_of<16>(ld_const(a.seq_lens + b), 0, a.split_tiles),
+                        a.max_splits);
+  __shared__ float sm_w[kMaxSplits];
+  __shared__ float sm_l[kMaxSplits];
+  __shared__ float sm_inv, sm_lse;
+  const int64_t row0 = (int64_t)b * a.max_splits * a.H + h;
+  for (int s = tid; s < n; s += blockDim.x) {
+    const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + (row0 + (int64_t)s * a.H) * 2);
+    sm_w[s] = ml.x;
+    sm_l[s] = ml.y;
   }
   __syncthreads();
-  const int32_t base = sm_work[0], n = sm_work[1];
-  for (int idx = tid; idx < nh * kLatent; idx += 256) {
+  if (tid == 0) {
+    float M = -INFINITY;
+    for (int32_t s = 0; s < n; ++s) M = fmaxf(M, sm_w[s]);
+    float den = 0.0f;
+    for (int32_t s = 0; s < n; ++s) {
+      const float w = __builtin_amdgcn_exp2f(sm_w[s] - M);
+      sm_w[s] = w;
+      den += w * sm_l[s];
+    }
+    sm_inv = 1.0f / den;
+    sm_lse = (M + __log2f(den)) * 0.6931471805599453f;
+  }
+  __syncthreads();
+  const float* ob = a.ws_o + row0 * kLatent;
+  for (int c = tid; c < kLatent; c += blockDim.x) {
+    const int beta = SPARSE ? latent_byte_of_dim(c) : c;
+    float num = 0.0f;
+#pragma unroll 8
+    for (int32_t s = 0; s < n; ++s) num += sm_w[s] * ob[(int64_t)s * a.H * kLatent + beta];
+    a.out[((int64_t)b * a.H + h) * kLatent + c] = (uint16_t)f32_to_bf16_bits(num * sm_inv);
+  }
+  if (a.lse_out && tid == 0) a.lse_out[(int64_t)b * a.H + h] = sm_lse;
+}
+
+// A row with no prior key (paged seq_len 1, or an empty index list): the output is its own row's latent.
+template <int FMT>
+__global__ __launch_bounds__(256) void mla_lone_row_kernel(MlaArgs a) {
+  constexpr bool SPARSE = FMT == ROWS640;
+  const int b = blockIdx.x, hg = blockIdx.y;
+  const int32_t n = SPARSE ? splits_of<16>(a.n_indices + 1, 0, a.split_tiles)
+                           : splits_of<16>(a.seq_lens[b], 0, a.split_tiles);
+  if (n > 0) return;
+  __shared__ float sm_row[576];
+  __shared__ float sm_sn[16];
+  __shared__ float sm_red[4];
+  const int nh = min(16, a.H - 16 * hg);
+  own_row_dequant<FMT, 256>(a, b, hg == 0, sm_row, sm_red);
+  own_row_scores<256>(a, b, hg, nh, sm_row, sm_sn);
+  for (int idx = threadIdx.x; idx < nh * kLatent; idx += 256) {
     const int j = idx / kLatent, c = idx % kLatent;
     const int32_t h = 16 * hg + j;
-    const int beta = SPARSE ? latent_byte_of_dim(c) : c;
-    const float s_new = sm_s[j];
-    float M = s_new;
-    for (int32_t i = 0; i < n; ++i) M = fmaxf(M, a.ws_ml[((int64_t)(base + i) * a.H + h) * 2]);
-    const float w_new = exp2f(s_new - M);
-    float den = w_new, num = w_new * sm_row[c];
-    for (int32_t i = 0; i < n; ++i) {
-      const int64_t r = (int64_t)(base + i) * a.H + h;
-      const float w = exp2f(a.ws_ml[r * 2] - M);
-      den += w * a.ws_ml[r * 2 + 1];
-      num += w * a.ws_o[r * kLatent + beta];
-    }
-    a.out[((int64_t)b * a.H + h) * kLatent + c] = (uint16_t)f32_to_bf16_bits(num / den);
-    if (a.lse_out && c == 0) a.lse_out[(int64_t)b * a.H + h] = (M + log2f(den)) * 0.6931471805599453f;
+    a.out[((int64_t)b * a.H + h) * kLatent + c] = (uint16_t)f32_to_bf16_bits(sm_row[c]);
+    if (a.lse_out && c == 0) a.lse_out[(int64_t)b * a.H + h] = sm_sn[j] * 0.6931471805599453f;
   }
+}
+
+template <int FMT>
+static void launch_mla(const MlaArgs& a, int32_t groups, int32_t grid_x, bool any_lone, hipStream_t s) {
+  timing_mark(0, s);
+  if (grid_x > 0) {
+    if (a.max_splits <= 1)
+      hipLaunchKernelGGL((mla_decode_kernel<FMT, 4, true>), dim3(grid_x, groups), dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((mla_decode_kernel<FMT, 4, false>), dim3(grid_x, groups), dim3(256), 0, s, a);
+  }
+  timing_mark(1, s);
+  if (a.max_splits > 1) hipLaunchKernelGGL((mla_combine_kernel<FMT>), dim3(a.B, a.H), dim3(128), 0, s, a);
+  if (any_lone) hipLaunchKernelGGL((mla_lone_row_kernel<FMT>), dim3(a.B, groups), dim3(256), 0, s, a);
+  timing_mark(2, s);
+}
+
+static int check_plan(const sna_split_plan* plan, int32_t B, const char* what) {
+  if (!plan || plan->tile != 16 || plan->split_tiles < 1 || plan->n_work < 0 || plan->max_splits < 0 ||
+      plan->batch != B)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "%s: missing or foreign split plan (made for %d rows)", what,
+                plan ? plan->batch : -1);
+  if (plan->split_tiles * 16 > kMaxSplitKeys)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "%s: a split of %d keys exceeds the kernel's %d", what,
+                plan->split_tiles * 16, kMaxSplitKeys);
+  return SNA_OK;
 }
 
 }  // namespace sna
@@ -490,67 +595,48 @@ extern "C" int sna_mla_decode(const void* ql_nope, const void* q_pe, const void*
     return fail(SNA_ERR_UNSUPPORTED, "mla_decode: only the FP8 per-token-scale row pool is built (dtype %d)",
                 cache_dtype);
   if (B < 0 || num_heads < 1 || page_size < 16 || page_size % 16 || num_blocks < 1 || table_width < 0 ||
-      table_stride < table_width || !(sm_scale > 0.0f))
+      table_stride < table_width || !(sm_scale > 0.0f) || num_blocks * page_size > INT32_MAX)
     return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode: bad sizes (B %d, heads %d, page %d (a multiple of 16), blocks "
                 "%lld, table %d/%lld)", B, num_heads, page_size, (long long)num_blocks, table_width,
                 (long long)table_stride);
-  if (!plan || plan->tile != 16 || plan->split_tiles < 1 || plan->n_work < 0)
-    return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode: missing or foreign split plan");
+  if (int rc = check_plan(plan, B, "mla_decode")) return rc;
   if (B == 0) return SNA_OK;
+  const int64_t need = sna_decode_workspace_bytes(plan, num_heads, kLatent);
   if (!ql_nope || !q_pe || !cache || !row_scale || !block_table || !seq_lens || !compact_new || !out ||
-      (plan->n_work > 0 && !workspace))
+      (need > 0 && !workspace))
     return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode: null pointer");
   if (!aligned(ql_nope, 16) || !aligned(q_pe, 16) || !aligned(cache, 16) || !aligned(row_scale, 16))
     return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode: q, cache and row_scale must be 16-byte aligned");
-  const int32_t groups = (num_heads + 15) / 16;
-  const int64_t need = sna_decode_workspace_bytes(plan, num_heads, kLatent);
-  if (plan->n_work > 0 && workspace_bytes < need)
+  if (workspace_bytes < need)
     return fail(SNA_ERR_WORKSPACE, "mla_decode: workspace of %lld bytes, the plan needs %lld",
                 (long long)workspace_bytes, (long long)need);
+  const int32_t groups = (num_heads + 15) / 16;
   float* ws = (float*)workspace;
-  MlaArgs da{};
-  da.ql = (const uint16_t*)ql_nope;
-  da.qpe = (const uint16_t*)q_pe;
-  da.cache = (const uint8_t*)cache;
-  da.row_scale = row_scale;
-  da.kv_scale = 1.0f;
-  da.table = block_table;
-  da.table_stride = table_stride;
-  da.table_width = table_width;
-  da.seq_lens = seq_lens;
-  da.B = B;
-  da.H = num_heads;
-  da.P = page_size;
-  da.num_blocks = num_blocks;
-  da.sm_scale = sm_scale;
-  da.split_tiles = plan->split_tiles;
-  da.n_work = plan->n_work;
-  da.ws_o = ws;
-  da.ws_ml = ws ? ws + (int64_t)plan->n_work * num_heads * kLatent : nullptr;
-  MlaCombineArgs ca{};
-  ca.ql = da.ql;
-  ca.qpe = da.qpe;
-  ca.own = (const uint16_t*)compact_new;
-  ca.new_slots = new_slots;
-  ca.cache = (uint8_t*)cache;
-  ca.row_scale = (float*)row_scale;
-  ca.kv_scale = 1.0f;
-  ca.seq_lens = seq_lens;
-  ca.B = B;
-  ca.H = num_heads;
-  ca.P = page_size;
-  ca.num_blocks = num_blocks;
-  ca.sm_scale = sm_scale;
-  ca.split_tiles = plan->split_tiles;
-  ca.n_work = plan->n_work;
-  ca.ws_o = da.ws_o;
-  ca.ws_ml = da.ws_ml;
-  ca.out = (uint16_t*)out;
-  ca.lse_out = nullptr;
-  hipStream_t s = (hipStream_t)stream;
-  if (plan->n_work > 0)
-    hipLaunchKernelGGL((mla_decode_kernel<ROWS576, 4>), dim3(plan->n_work, groups), dim3(256), 0, s, da);
-  hipLaunchKernelGGL((mla_combine_kernel<ROWS576>), dim3(B, groups), dim3(256), 0, s, ca);
+  MlaArgs a{};
+  a.ql = (const uint16_t*)ql_nope;
+  a.qpe = (const uint16_t*)q_pe;
+  a.cache = (uint8_t*)cache;
+  a.row_scale = (float*)row_scale;
+  a.kv_scale = 1.0f;
+  a.table = block_table;
+  a.table_stride = table_stride;
+  a.table_width = table_width;
+  a.seq_lens = seq_lens;
+  a.own = (const uint16_t*)compact_new;
+  a.new_slots = new_slots;
+  a.B = B;
+  a.H = num_heads;
+  a.P = page_size;
+  a.num_blocks = num_blocks;
+  a.sm_scale = sm_scale;
+  a.split_tiles = plan->split_tiles;
+  a.n_work = plan->n_work;
+  a.max_splits = plan->max_splits;
+  a.ws_o = need > 0 ? ws : nullptr;
+  a.ws_ml = need > 0 ? ws + (int64_t)B * plan->max_splits * num_heads * kLatent : nullptr;
+  a.out = (uint16_t*)out;
+  a.lse_out = nullptr;
+  launch_mla<ROWS576>(a, groups, plan->n_work, plan->empty_rows != 0, (hipStream_t)stream);
   return check_launch("mla_decode");
 }
 
@@ -563,70 +649,54 @@ extern "C" int sna_mla_decode_sparse(const void* q_absorbed, const void* q_pe, c
                                      void* stream) {
   ApiGuard guard;
   if (B < 0 || num_heads < 1 || n_indices < 0 || page_size < 1 || num_blocks < 1 || table_width < 0 ||
-      table_stride < table_width || !(sm_scale > 0.0f) || !(kv_scale > 0.0f))
+      table_stride < table_width || !(sm_scale > 0.0f) || !(kv_scale > 0.0f) || num_blocks * page_size > INT32_MAX)
     return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode_sparse: bad sizes (B %d, heads %d, indices %d, page %d, blocks "
                 "%lld, table %d/%lld, kv_scale %g)", B, num_heads, n_indices, page_size, (long long)num_blocks,
                 table_width, (long long)table_stride, (double)kv_scale);
-  if (!plan || plan->tile != 16 || plan->split_tiles < 1 || plan->n_work < 0)
-    return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode_sparse: missing or foreign split plan");
+  if (int rc = check_plan(plan, B, "mla_decode_sparse")) return rc;
   if (B == 0) return SNA_OK;
+  const int64_t need = sna_decode_workspace_bytes(plan, num_heads, kLatent);
   if (!q_absorbed || !q_pe || !cache || !block_table || !positions || !own_rows || !ctx_out ||
-      (n_indices > 0 && !indices) || (plan->n_work > 0 && !workspace))
+      (n_indices > 0 && !indices) || (need > 0 && !workspace))
     return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode_sparse: null pointer");
   if (!aligned(q_absorbed, 16) || !aligned(q_pe, 16) || !aligned(cache, 16))
     return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode_sparse: q and cache must be 16-byte aligned");
-  const int32_t per = (n_indices + 15) / 16 == 0 ? 0 : ((n_indices + 15) / 16 + plan->split_tiles - 1) / plan->split_tiles;
-  if ((int64_t)per * B > plan->n_work)
-    return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode_sparse: the plan holds %d items, the index lists need %lld",
-                plan->n_work, (long long)per * B);
-  const int32_t groups = (num_heads + 15) / 16;
-  const int64_t need = sna_decode_workspace_bytes(plan, num_heads, kLatent);
-  if (plan->n_work > 0 && workspace_bytes < need)
+  const int32_t tiles = (n_indices + 15) / 16;
+  const int32_t per = tiles == 0 ? 0 : (tiles + plan->split_tiles - 1) / plan->split_tiles;
+  if (per > plan->max_splits || (int64_t)per * B > plan->n_work)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode_sparse: the plan holds %d splits per row, the index lists need "
+                "%d", plan->max_splits, per);
+  if (workspace_bytes < need)
     return fail(SNA_ERR_WORKSPACE, "mla_decode_sparse: workspace of %lld bytes, the plan needs %lld",
                 (long long)workspace_bytes, (long long)need);
+  const int32_t groups = (num_heads + 15) / 16;
   float* ws = (float*)workspace;
-  MlaArgs da{};
-  da.ql = (const uint16_t*)q_absorbed;
-  da.qpe = (const uint16_t*)q_pe;
-  da.cache = (const uint8_t*)cache;
-  da.row_scale = nullptr;
-  da.kv_scale = kv_scale;
-  da.table = block_table;
-  da.table_stride = table_stride;
-  da.table_width = table_width;
-  da.indices = indices;
-  da.n_indices = n_indices;
-  da.positions = positions;
-  da.B = B;
-  da.H = num_heads;
-  da.P = page_size;
-  da.num_blocks = num_blocks;
-  da.sm_scale = sm_scale;
-  da.split_tiles = plan->split_tiles;
-  da.n_work = plan->n_work;
-  da.ws_o = ws;
-  da.ws_ml = ws ? ws + (int64_t)plan->n_work * num_heads * kLatent : nullptr;
-  MlaCombineArgs ca{};
-  ca.ql = da.ql;
-  ca.qpe = da.qpe;
-  ca.own = (const uint16_t*)own_rows;
-  ca.new_slots = nullptr;
-  ca.kv_scale = kv_scale;
-  ca.n_indices = n_indices;
-  ca.B = B;
-  ca.H = num_heads;
-  ca.P = page_size;
-  ca.num_blocks = num_blocks;
-  ca.sm_scale = sm_scale;
-  ca.split_tiles = plan->split_tiles;
-  ca.n_work = plan->n_work;
-  ca.ws_o = da.ws_o;
-  ca.ws_ml = da.ws_ml;
-  ca.out = (uint16_t*)ctx_out;
-  ca.lse_out = lse_out;
-  hipStream_t s = (hipStream_t)stream;
-  if (per * B > 0)
-    hipLaunchKernelGGL((mla_decode_kernel<ROWS640, 4>), dim3(per * B, groups), dim3(256), 0, s, da);
-  hipLaunchKernelGGL((mla_combine_kernel<ROWS640>), dim3(B, groups), dim3(256), 0, s, ca);
+  MlaArgs a{};
+  a.ql = (const uint16_t*)q_absorbed;
+  a.qpe = (const uint16_t*)q_pe;
+  a.cache = (uint8_t*)cache;
+  a.row_scale = nullptr;
+  a.kv_scale = kv_scale;
+  a.table = block_table;
+  a.table_stride = table_stride;
+  a.table_width = table_width;
+  a.indices = indices;
+  a.n_indices = n_indices;
+  a.positions = positions;
+  a.own = (const uint16_t*)own_rows;
+  a.new_slots = nullptr;
+  a.B = B;
+  a.H = num_heads;
+  a.P = page_size;
+  a.num_blocks = num_blocks;
+  a.sm_scale = sm_scale;
+  a.split_tiles = plan->split_tiles;
+  a.n_work = plan->n_work;
+  a.max_splits = plan->max_splits;
+  a.ws_o = need > 0 ? ws : nullptr;
+  a.ws_ml = need > 0 ? ws + (int64_t)B * plan->max_splits * num_heads * kLatent : nullptr;
+  a.out = (uint16_t*)ctx_out;
+  a.lse_out = lse_out;
+  launch_mla<ROWS640>(a, groups, per * B, per == 0, (hipStream_t)stream);
   return check_launch("mla_decode_sparse");
 }

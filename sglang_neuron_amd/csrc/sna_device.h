@@ -17,6 +17,8 @@ constexpr float kFp8Max = 448.0f;
 constexpr float kLog2e = 1.4426950408889634f;
 // Running-max sentinel: finite, so exp2(m_old - m_new) never evaluates (-inf) - (-inf).
 constexpr float kNegBig = -1.0e30f;
+// The most splits a row may have (the combine passes hold one weight per split in LDS); the planner keeps to it.
+constexpr int kMaxSplits = 64;
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
@@ -116,6 +118,14 @@ __device__ __forceinline__ f32x4_t mfma_16x16x16_bf16(const uint32_t (&a)[2], co
                                                     c, 0, 0, 0);
 }
 
+// A wave-uniform read of memory no kernel of the launch writes (block tables, index lists, seq_lens): through the
+// constant address space, so the compiler may use a scalar load, which waits on lgkmcnt and leaves the vector loads
+// in flight alone.
+template <typename T>
+__device__ __forceinline__ T ld_const(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)(p);
+}
+
 // 16-, 8- and 4-byte global loads of raw bits.
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ uint2 ld8(const void* p) { return *reinterpret_cast<const uint2*>(p); }
@@ -179,14 +189,15 @@ __device__ __forceinline__ void locate_work(const int32_t* __restrict__ seq_lens
       if (lane >= off) incl += t;
     }
     int32_t excl = incl - n;
-    int32_t total = __shfl(incl, 63, 64);
+    const int32_t total = __builtin_amdgcn_readfirstlane(__shfl(incl, 63, 64));  // uniform loop exit
     if (w < base + total) {
       bool mine = (w >= base + excl) && (w < base + incl);
       unsigned long long ballot = __ballot(mine);
       int src = __ffsll((long long)ballot) - 1;
       int32_t e = __shfl(excl, src, 64);
-      b_out = b0 + src;
-      split_out = w - base - e;
+      // the same for every lane: made scalar, so what is indexed by them stays in scalar registers
+      b_out = __builtin_amdgcn_readfirstlane(b0 + src);
+      split_out = __builtin_amdgcn_readfirstlane(w - base - e);
       return;
     }
     base += total;

@@ -35,4 +35,8 @@ inline int check_launch(const char* what) {
 
 inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
+// Diagnostics timer (capi.hip): when sna_diag_kernel_timing(1) has switched it on, a decode launcher records an event
+// before its split-K kernel (phase 0), between it and the combine pass (phase 1) and after the combine (phase 2).
+void timing_mark(int phase, hipStream_t s);
+
 }  // namespace sna

@@ -152,10 +152,11 @@ def kv_store_dsa(rows: Tensor, slots: Tensor, cache: Tensor, kv_scale: float) ->
 
 def plan_decode(kind: int, B: int, *, host_seq_lens: Union[Tensor, Sequence[int], None] = None,
                 max_seq_len: int = -1, window: int = 0, n_keys_per_row: int = 0, ctas_per_item: int = 1,
-                num_cus: int = 0) -> _lib.SplitPlan:
+                num_cus: int = 0, gqa_depth: int = 0) -> _lib.SplitPlan:
     """The split-K plan of a decode launch (sna_plan_decode): exact from host seq_lens, or a bound from
-    ``max_seq_len``."""
+    ``max_seq_len``. ``gqa_depth`` (2 or 4) asks for a GQA register-ring depth; 0 lets the planner pick."""
     plan = _lib.SplitPlan()
+    plan.depth = int(gqa_depth)
     arr = None
     if host_seq_lens is not None:
         t = torch.as_tensor(host_seq_lens, dtype=torch.int32).reshape(-1).cpu().contiguous()
@@ -183,22 +184,38 @@ def _host_lens(seq_lens: Tensor, host_seq_lens) -> Optional[Tensor]:
 # decode attention
 # ------------------------------------------------------------------------------------------------------------------
 
-def paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: Tensor, seq_lens: Tensor,
-                     k_new: Tensor, v_new: Tensor, *, sm_scale: float, k_scale: Optional[Tensor] = None,
-                     v_scale: Optional[Tensor] = None, sinks: Optional[Tensor] = None, window: int = 0,
-                     new_slots: Optional[Tensor] = None, out: Optional[Tensor] = None,
-                     host_seq_lens=None, plan: Optional[_lib.SplitPlan] = None) -> Tensor:
-    """GQA decode of q [B, H, d] over a layer's paged caches [blocks, G, page, d], the step's token k_new / v_new
-    [B, G, d] attended in-band (and stored at ``new_slots`` when given). Returns [B, H, d] bf16.
+class Prepared:
+    """One or more C-ABI calls with validated, bound arguments, launched again on every call. It keeps its tensors
+    (inputs, outputs, workspace) alive and returns its outputs. The bench runs its timed loop through these, so host
+    work stays out of the timing, and every public decode function below is prepare + one launch."""
 
-    Stands in for the attention core of _torch_attention_decode_paged (ops/attention/attention_decode_paged.py:
-    159-177) and _torch_attention_decode (ops/attention/attention_decode.py:259-300)."""
+    def __init__(self, calls, keep, outputs, what):
+        self._calls = calls        # [(fn, args)]
+        self._keep = keep
+        self.outputs = outputs
+        self._what = what
+
+    def __call__(self):
+        for fn, args in self._calls:
+            rc = fn(*args)
+            if rc:
+                _lib.check(rc, self._what)
+        return self.outputs
+
+
+def prepare_paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: Tensor, seq_lens: Tensor,
+                             k_new: Tensor, v_new: Tensor, *, sm_scale: float, k_scale: Optional[Tensor] = None,
+                             v_scale: Optional[Tensor] = None, sinks: Optional[Tensor] = None, window: int = 0,
+                             new_slots: Optional[Tensor] = None, out: Optional[Tensor] = None,
+                             host_seq_lens=None, plan: Optional[_lib.SplitPlan] = None) -> Prepared:
+    """paged_decode_gqa's checks and argument binding, launched by calling the result."""
     dev = _on_gpu(q, k_cache, v_cache, block_table, seq_lens, k_new, v_new, k_scale, v_scale, sinks, new_slots, out)
     _need(q.dim() == 3, f"q must be [B, H, d], got {tuple(q.shape)}")
     B, H, d = q.shape
     nb, G, P, dk = k_cache.shape
     _need(dk == d and v_cache.shape == k_cache.shape and v_cache.dtype == k_cache.dtype,
           f"caches {tuple(k_cache.shape)} / {tuple(v_cache.shape)} do not match q's head_dim {d}")
+    _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
     _need(H % G == 0, f"{H} query heads over {G} KV heads")
     code = cache_dtype_code(k_cache.dtype)
     q = _contig(q, "q", torch.bfloat16)
@@ -228,23 +245,30 @@ def paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: T
         plan = plan_decode(_lib.KIND_GQA, B, host_seq_lens=hl, max_seq_len=table.shape[1] * P, window=window,
                            ctas_per_item=G, num_cus=_num_cus(dev))
     ws = torch.empty(max(workspace_bytes(plan, H, d), 16), dtype=torch.uint8, device=dev)
-    rc = _lib.load().sna_paged_decode_gqa(
-        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), _ptr(table), table.stride(0),
-        table.shape[1], _ptr(lens), _ptr(k_new), _ptr(v_new), _ptr(new_slots), _ptr(sinks), int(window),
-        float(sm_scale), _ptr(out), B, H, G, d, P, nb, code, plan, _ptr(ws), ws.numel(), _stream(dev))
-    _lib.check(rc, "paged_decode_gqa")
-    return out
+    lib = _lib.load()
+    args = (_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), _ptr(table), table.stride(0),
+            table.shape[1], _ptr(lens), _ptr(k_new), _ptr(v_new), _ptr(new_slots), _ptr(sinks), int(window),
+            float(sm_scale), _ptr(out), B, H, G, d, P, nb, code, plan, _ptr(ws), ws.numel(), _stream(dev))
+    keep = (q, k_cache, v_cache, k_scale, v_scale, table, lens, k_new, v_new, new_slots, sinks, out, ws, plan)
+    return Prepared([(lib.sna_paged_decode_gqa, args)], keep, out, "paged_decode_gqa")
 
 
-def mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: Tensor, block_table: Tensor,
-               seq_lens: Tensor, compact_new: Tensor, *, sm_scale: float, page_size: int,
-               new_slots: Optional[Tensor] = None, out: Optional[Tensor] = None, host_seq_lens=None,
-               plan: Optional[_lib.SplitPlan] = None) -> Tensor:
-    """Absorbed-MLA decode of ql_nope [B, H, 512] / q_pe [B, H, 64] over a layer's FP8 rows [slots, 576] (uint8 or
-    float8 storage) with per-token scales ``row_scale`` [slots], the history through ``block_table`` and the own row
-    ``compact_new`` [B, 576] in-band (stored at ``new_slots`` when given). Returns [B, H, 512] bf16.
+def paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: Tensor, seq_lens: Tensor,
+                     k_new: Tensor, v_new: Tensor, **kw) -> Tensor:
+    """GQA decode of q [B, H, d] over a layer's paged caches [blocks, G, page, d], the step's token k_new / v_new
+    [B, G, d] attended in-band (and stored at ``new_slots`` when given). Keyword arguments: sm_scale, k_scale,
+    v_scale (FP8), sinks, window, new_slots, out, host_seq_lens, plan. Returns [B, H, d] bf16.
 
-    Stands in for mla_decode (ops/attention/mla.py:32-53)."""
+    Stands in for the attention core of _torch_attention_decode_paged (ops/attention/attention_decode_paged.py:
+    159-177) and _torch_attention_decode (ops/attention/attention_decode.py:259-300)."""
+    return prepare_paged_decode_gqa(q, k_cache, v_cache, block_table, seq_lens, k_new, v_new, **kw)()
+
+
+def prepare_mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: Tensor, block_table: Tensor,
+                       seq_lens: Tensor, compact_new: Tensor, *, sm_scale: float, page_size: int,
+                       new_slots: Optional[Tensor] = None, out: Optional[Tensor] = None, host_seq_lens=None,
+                       plan: Optional[_lib.SplitPlan] = None) -> Prepared:
+    """mla_decode's checks and argument binding, launched by calling the result."""
     dev = _on_gpu(ql_nope, q_pe, cache, row_scale, block_table, seq_lens, compact_new, new_slots, out)
     B, H, lat = ql_nope.shape
     _need(lat == 512 and q_pe.shape == (B, H, 64), "ql_nope [B, H, 512] and q_pe [B, H, 64]")
@@ -265,33 +289,44 @@ def mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: Tensor, 
     table = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
     _need(table.dim() == 2 and table.shape[0] == B and table.stride(1) == 1, f"block_table must be [{B}, width]")
     lens = _contig(seq_lens.reshape(-1).to(torch.int32), "seq_lens")
+    _need(lens.numel() == B, f"{lens.numel()} seq_lens for {B} rows")
     if new_slots is not None:
         new_slots = _contig(new_slots.reshape(-1).to(torch.int64), "new_slots")
+        _need(new_slots.numel() == B, f"{new_slots.numel()} new slots for {B} rows")
     if out is None:
         out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
+    _need(out.shape == (B, H, 512) and out.dtype == torch.bfloat16 and out.is_contiguous(), "bad out tensor")
     if plan is None:
         hl = _host_lens(seq_lens, host_seq_lens)
         plan = plan_decode(_lib.KIND_MLA, B, host_seq_lens=hl, max_seq_len=table.shape[1] * P,
                            ctas_per_item=(H + 15) // 16, num_cus=_num_cus(dev))
     ws = torch.empty(max(workspace_bytes(plan, H, 512), 16), dtype=torch.uint8, device=dev)
-    rc = _lib.load().sna_mla_decode(
-        _ptr(ql_nope), _ptr(q_pe), _ptr(cache), _ptr(row_scale), _ptr(table), table.stride(0), table.shape[1],
-        _ptr(lens), _ptr(compact_new), _ptr(new_slots), float(sm_scale), _ptr(out), B, H, P, nb, code, plan,
-        _ptr(ws), ws.numel(), _stream(dev))
-    _lib.check(rc, "mla_decode")
-    return out
+    lib = _lib.load()
+    args = (_ptr(ql_nope), _ptr(q_pe), _ptr(cache), _ptr(row_scale), _ptr(table), table.stride(0), table.shape[1],
+            _ptr(lens), _ptr(compact_new), _ptr(new_slots), float(sm_scale), _ptr(out), B, H, P, nb, code, plan,
+            _ptr(ws), ws.numel(), _stream(dev))
+    keep = (ql_nope, q_pe, cache, row_scale, table, lens, compact_new, new_slots, out, ws, plan)
+    return Prepared([(lib.sna_mla_decode, args)], keep, out, "mla_decode")
 
 
-def mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, kv_scale: float, indices: Tensor,
-                      block_table: Tensor, positions: Tensor, own_rows: Tensor, *, sm_scale: float, page_size: int,
-                      plan: Optional[_lib.SplitPlan] = None) -> tuple[Tensor, Tensor]:
-    """DSA sparse decode: q_absorbed [B, H, 512], q_pe [B, H, 64], the 640-byte row cache, ``indices`` [B, K] int32
-    global positions (-1 empty), ``block_table`` [B, W], ``positions`` [B], own rows [B, 576] ([k_pe | latent],
-    already stored by kv_store_dsa). Returns (ctx [B, H, 512] bf16, lse [B, H] fp32).
+def mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: Tensor, block_table: Tensor,
+               seq_lens: Tensor, compact_new: Tensor, **kw) -> Tensor:
+    """Absorbed-MLA decode of ql_nope [B, H, 512] / q_pe [B, H, 64] over a layer's FP8 rows [slots, 576] (uint8 or
+    float8 storage) with per-token scales ``row_scale`` [slots], the history through ``block_table`` and the own row
+    ``compact_new`` [B, 576] in-band (stored at ``new_slots`` when given). Keyword arguments: sm_scale, page_size,
+    new_slots, out, host_seq_lens, plan. Returns [B, H, 512] bf16.
 
-    Stands in for mla_decode_attention_torch_ref with one token per sequence and one CP rank
-    (models/glm52/kernels/decode/attention/mla/mla_decode_attention_torch.py:38-130)."""
-    dev = _on_gpu(q_absorbed, q_pe, cache, indices, block_table, positions, own_rows)
+    Stands in for mla_decode (ops/attention/mla.py:32-53)."""
+    return prepare_mla_decode(ql_nope, q_pe, cache, row_scale, block_table, seq_lens, compact_new, **kw)()
+
+
+def prepare_mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, kv_scale: float, indices: Tensor,
+                              block_table: Tensor, positions: Tensor, own_rows: Tensor, *, sm_scale: float,
+                              page_size: int, new_slots: Optional[Tensor] = None,
+                              plan: Optional[_lib.SplitPlan] = None) -> Prepared:
+    """mla_decode_sparse's checks and argument binding (with ``new_slots``, the own rows' store first), launched by
+    calling the result."""
+    dev = _on_gpu(q_absorbed, q_pe, cache, indices, block_table, positions, own_rows, new_slots)
     B, H, lat = q_absorbed.shape
     _need(lat == 512 and q_pe.shape == (B, H, 64), "q_absorbed [B, H, 512] and q_pe [B, H, 64]")
     _need(cache.dtype == torch.uint8 and cache.shape[-1] == 640 and cache.is_contiguous(), "cache [..., 640] uint8")
@@ -312,12 +347,32 @@ def mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, kv_scale:
     ws = torch.empty(max(workspace_bytes(plan, H, 512), 16), dtype=torch.uint8, device=dev)
     ctx = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
     lse = torch.empty(B, H, dtype=torch.float32, device=dev)
-    rc = _lib.load().sna_mla_decode_sparse(
+    lib = _lib.load()
+    calls = []
+    if new_slots is not None:
+        new_slots = _contig(new_slots.reshape(-1).to(torch.int64), "new_slots")
+        _need(new_slots.numel() == B, f"{new_slots.numel()} new slots for {B} rows")
+        calls.append((lib.sna_kv_store_dsa, (_ptr(own_rows), _ptr(new_slots), B, float(kv_scale), _ptr(cache),
+                                             n_rows, _stream(dev))))
+    calls.append((lib.sna_mla_decode_sparse, (
         _ptr(q_absorbed), _ptr(q_pe), _ptr(cache), float(kv_scale), _ptr(idx), K, _ptr(table), table.stride(0),
         table.shape[1], _ptr(pos), _ptr(own_rows), float(sm_scale), _ptr(ctx), _ptr(lse), B, H, P, n_rows // P, plan,
-        _ptr(ws), ws.numel(), _stream(dev))
-    _lib.check(rc, "mla_decode_sparse")
-    return ctx, lse
+        _ptr(ws), ws.numel(), _stream(dev))))
+    keep = (q_absorbed, q_pe, cache, idx, table, pos, own_rows, new_slots, ctx, lse, ws, plan)
+    return Prepared(calls, keep, (ctx, lse), "mla_decode_sparse")
+
+
+def mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, kv_scale: float, indices: Tensor,
+                      block_table: Tensor, positions: Tensor, own_rows: Tensor, **kw) -> tuple[Tensor, Tensor]:
+    """DSA sparse decode: q_absorbed [B, H, 512], q_pe [B, H, 64], the 640-byte row cache, ``indices`` [B, K] int32
+    global positions (-1 empty), ``block_table`` [B, W], ``positions`` [B], own rows [B, 576] ([k_pe | latent]).
+    With ``new_slots`` the own rows are stored first (the reference's steps 0-1); without, the caller has stored them.
+    Keyword arguments: sm_scale, page_size, new_slots, plan. Returns (ctx [B, H, 512] bf16, lse [B, H] fp32).
+
+    Stands in for mla_decode_attention_torch_ref with one token per sequence and one CP rank
+    (models/glm52/kernels/decode/attention/mla/mla_decode_attention_torch.py:38-130)."""
+    return prepare_mla_decode_sparse(q_absorbed, q_pe, cache, kv_scale, indices, block_table, positions, own_rows,
+                                     **kw)()
 
 
 def lse_combine(o_parts: Tensor, lse_parts: Tensor) -> tuple[Tensor, Tensor]:

@@ -296,3 +296,46 @@ def dsa_case(*, gen_device="cpu", overrides: Optional[dict] = None) -> DsaCase:
     return DsaCase(B=B, H=H, P=P, kv_scale=spec["kv_scale"], sm_scale=spec["sm_scale"], positions=positions,
                    block_table=table, num_blocks=nb, indices=idx, q_absorbed=qa, q_pe=qpe, own_rows=own,
                    new_slots=new_slots, pool_positions=per)
+
+
+# ---- pools on the GPU, filled through the HIP store kernels ----
+
+def gqa_pool(case: GqaCase, device="cuda"):
+    """(k_cache, v_cache, k_scale, v_scale) of one layer on ``device``: per-KV-head scales calibrated over every K (V)
+    token of the case (prior and new) by the HIP absmax kernel, then the prior tokens stored by the HIP store."""
+    from . import ops
+
+    dt = torch.float8_e4m3fn if case.fp8 else torch.bfloat16
+    kc = torch.zeros(case.num_blocks, case.G, case.P, case.d, dtype=dt, device=device)
+    vc = torch.zeros_like(kc)
+    ks = vs = None
+    kp, vp = case.k_prior.to(device), case.v_prior.to(device)
+    if case.fp8:
+        ks = ops.kv_absmax_scale(torch.cat([kp, case.k_new.to(device)], dim=0))
+        vs = ops.kv_absmax_scale(torch.cat([vp, case.v_new.to(device)], dim=0))
+    if kp.shape[0]:
+        ops.kv_store_mha(kp, vp, case.prior_slots.to(device), kc, vc, ks, vs)
+    return kc, vc, ks, vs
+
+
+def mla_pool(case: MlaCase, device="cuda"):
+    """(rows [slots, 576] uint8, row_scale [slots]) of one layer on ``device``, the prior rows stored by the HIP
+    per-token FP8 store."""
+    from . import ops
+
+    n = case.num_blocks * case.P
+    cache = torch.zeros(n, 576, dtype=torch.uint8, device=device)
+    scale = torch.zeros(n, dtype=torch.float32, device=device)
+    if case.prior_slots.numel():
+        ops.kv_store_mla(case.prior_rows.to(device), case.prior_slots.to(device), cache, scale)
+    return cache, scale
+
+
+def dsa_pool(case: DsaCase, device="cuda", gen_device="cpu"):
+    """The 640-byte row cache of one layer on ``device``, every prior position filled by the HIP DSA store."""
+    from . import ops
+
+    cache = torch.zeros(case.num_blocks * case.P, 640, dtype=torch.uint8, device=device)
+    case.fill_rows(lambda v, s: ops.kv_store_dsa(v.to(device), s.to(device), cache, case.kv_scale),
+                   gen_device=gen_device)
+    return cache

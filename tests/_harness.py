@@ -54,18 +54,7 @@ def gqa_oracle(case: workloads.GqaCase):
 
 def gqa_gpu_pool(case: workloads.GqaCase, dev="cuda"):
     """(k_cache, v_cache, k_scale, v_scale) on the GPU, filled by the HIP store (scales by the HIP absmax kernel)."""
-    G, d, P, nb = case.G, case.d, case.P, case.num_blocks
-    dt = torch.float8_e4m3fn if case.fp8 else torch.bfloat16
-    kc = torch.zeros(nb, G, P, d, dtype=dt, device=dev)
-    vc = torch.zeros(nb, G, P, d, dtype=dt, device=dev)
-    ks = vs = None
-    kp, vp = case.k_prior.to(dev), case.v_prior.to(dev)
-    if case.fp8:
-        ks = ops.kv_absmax_scale(torch.cat([kp, case.k_new.to(dev)], dim=0))
-        vs = ops.kv_absmax_scale(torch.cat([vp, case.v_new.to(dev)], dim=0))
-    if kp.shape[0]:
-        ops.kv_store_mha(kp, vp, case.prior_slots.to(dev), kc, vc, ks, vs)
-    return kc, vc, ks, vs
+    return workloads.gqa_pool(case, dev)
 
 
 def gqa_gpu_decode(case: workloads.GqaCase, kc, vc, ks, vs, dev="cuda", store_new=True):
@@ -95,12 +84,7 @@ def mla_oracle(case: workloads.MlaCase):
 
 
 def mla_gpu_pool(case: workloads.MlaCase, dev="cuda"):
-    n = case.num_blocks * case.P
-    cache = torch.zeros(n, 576, dtype=torch.uint8, device=dev)
-    scale = torch.zeros(n, dtype=torch.float32, device=dev)
-    if case.prior_slots.numel():
-        ops.kv_store_mla(case.prior_rows.to(dev), case.prior_slots.to(dev), cache, scale)
-    return cache, scale
+    return workloads.mla_pool(case, dev)
 
 
 def mla_gpu_decode(case: workloads.MlaCase, cache, scale, dev="cuda", store_new=True):
@@ -123,10 +107,7 @@ def dsa_oracle(case: workloads.DsaCase):
 
 
 def dsa_gpu_pool(case: workloads.DsaCase, dev="cuda", gen_device="cpu"):
-    n = case.num_blocks * case.P
-    cache = torch.zeros(n, 640, dtype=torch.uint8, device=dev)
-    case.fill_rows(lambda v, s: ops.kv_store_dsa(v.to(dev), s.to(dev), cache, case.kv_scale), gen_device=gen_device)
-    return cache
+    return workloads.dsa_pool(case, dev, gen_device)
 
 
 def dsa_gpu_step(case: workloads.DsaCase, cache, dev="cuda"):

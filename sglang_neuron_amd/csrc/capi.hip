@@ -131,11 +131,6 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
   const int32_t tile = kind == 0 ? 32 : 16;
   const int32_t waves = 4;
   const int32_t cus = num_cus > 0 ? num_cus : 256;
-  // Resident workgroups the launch aims for. GQA with the deep register ring (depth 4) holds one 4-wave workgroup
-  // per CU and gets two rounds of them; the shallow ring (depth 2) holds two per CU and gets four rounds. The MLA
-  // kernels hold one per CU (their register budget) and aim for a single round.
-  const int32_t depth = gqa_depth > 0 ? gqa_depth : 4;
-  const int64_t target = kind == 0 ? (int64_t)cus * (depth >= 4 ? 2 : 8) : (int64_t)cus;
   auto len_of = [&](int32_t b) -> int32_t {
     if (kind == 2) return n_keys_per_row + 1;  // the index list as "prior keys" + the own row
     return host_seq_lens ? host_seq_lens[b] : max_seq_len;
@@ -148,18 +143,29 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
     total_tiles += t;
     max_tiles = std::max(max_tiles, t);
   }
+  // GQA register-ring depth: the deep ring (4) when there is enough work to fill the chip with long splits; the
+  // shallow ring (2) keeps small launches short.
+  const int32_t depth = gqa_depth > 0 ? gqa_depth : (total_tiles * ctas_per_item >= (int64_t)cus * 32 ? 4 : 2);
+  // Resident workgroups the launch aims for, and whether it must fit them in one round. GQA with the deep ring holds
+  // two 4-wave workgroups per CU and runs one round; the shallow ring holds about three and runs a few rounds. The
+  // MLA kernels hold one per CU (their register and LDS budget) and run one round.
+  const bool one_round = kind != 0 || depth >= 4;
+  const int64_t target = kind == 0 ? (int64_t)cus * (depth >= 4 ? 2 : 8) : (int64_t)cus;
   const int64_t items_target = std::max<int64_t>(1, target / ctas_per_item);
   int32_t split_tiles = (int32_t)std::max<int64_t>(waves, (total_tiles + items_target - 1) / items_target);
-  if (kind != 0) {
-    // MLA: grow the split until the item count fits the resident target, so no workgroup waits for a second round.
-    // A split's row ids live in the kernel's LDS, which caps it at kMlaMaxSplitTiles tiles.
-    constexpr int32_t kMlaMaxSplitTiles = 256;
-    split_tiles = std::min(split_tiles, kMlaMaxSplitTiles);
-    while (split_tiles < kMlaMaxSplitTiles) {
+  // short rows (a sliding window, a few pages) stay whole: one split, no combine pass
+  split_tiles = std::max(split_tiles, std::min(max_tiles, 2 * waves));
+  // A MLA split's row ids live in the kernel's LDS, which caps it at kMlaMaxSplitTiles tiles.
+  constexpr int32_t kMlaMaxSplitTiles = kMlaMaxSplitKeys / 16;
+  const int32_t cap = kind != 0 ? kMlaMaxSplitTiles : std::max(max_tiles, waves);
+  split_tiles = std::min(split_tiles, cap);
+  if (one_round) {
+    // grow the split until the item count fits the resident target, so no workgroup waits for a second round
+    while (split_tiles < cap) {
       int64_t n = 0;
       for (int32_t b = 0; b < B; ++b) n += host_splits(len_of(b), win, tile, split_tiles);
-      if (n * ctas_per_item <= target || split_tiles >= std::max(max_tiles, waves)) break;
-      split_tiles = std::min(split_tiles + waves, kMlaMaxSplitTiles);
+      if (n * ctas_per_item <= target) break;
+      split_tiles = std::min(split_tiles + (kind != 0 ? waves : 1), cap);
     }
   }
   // the combine passes hold at most kMaxSplits weights per row: grow the split until every row fits
@@ -169,7 +175,7 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
     if (worst <= kMaxSplits) break;
     split_tiles = std::max(split_tiles + 1, (max_tiles + kMaxSplits - 1) / kMaxSplits);
   }
-  if (kind != 0 && split_tiles * tile > 4096)
+  if (kind != 0 && split_tiles * tile > kMlaMaxSplitKeys)
     return fail(SNA_ERR_UNSUPPORTED, "plan_decode: a row of %d tiles needs splits beyond the MLA kernel's capacity",
                 max_tiles);
   int64_t n_work = 0;

@@ -10,7 +10,8 @@
 //
 // Work: one workgroup of 4 waves per (row, split, 16-head group). The workgroup first resolves the row id of every
 // key of its split into LDS (the block-table walk, or for DSA the index -> block -> row walk). Each wave then takes
-// 16-key tiles round-robin, the next tile's loads in flight while it computes one.
+// 16-key tiles round-robin through a ring of 3 LDS slots, filled by global->LDS DMA: two tiles are in flight while
+// it computes a third, and the in-flight bytes cost no registers.
 //
 // Lane roles (lane = 16 * g4 + li), 16-key tiles:
 //   QK   S^T[key, head] = K[key, :] . Q[head, :]   v_mfma_f32_16x16x32_bf16, 18 steps over the 576 dims. Lane
@@ -31,7 +32,7 @@ enum { ROWS576 = 0, ROWS640 = 1 };
 constexpr int kLatent = 512;
 constexpr int kRope = 64;
 constexpr int kLdsRow = 528;        // latent bytes of one key row in LDS, padded so rows 4 apart hit other banks
-constexpr int kMaxSplitKeys = 4096;  // keys one split may cover (its row ids live in LDS)
+constexpr int kMlaRingDepth = 3;    // LDS tile slots per wave
 constexpr float kMlaRescaleSlack = 8.0f;
 
 struct MlaArgs {
@@ -119,13 +120,6 @@ __device__ __forceinline__ uint4 query_chunk(const uint16_t* qlp, const uint16_t
   }
 }
 
-template <int FMT>
-struct MlaRing {
-  uint32_t raw[RowFmt<FMT>::kLaneChunks][4];
-  float kscale[4];
-  uint32_t vmask;  // bit k: key k of the tile is valid
-};
-
 // The own row of sequence b, dequantized in natural order [latent 512 | rope 64] into sm_row, stored into the
 // pool when paged and st is set. Every thread of the workgroup calls it. ROWS576 quantizes with the row's own
 // per-token scale, ROWS640 with kv_scale and the row's bf16 rope.
@@ -181,31 +175,63 @@ __device__ void own_row_scores(const MlaArgs& a, int b, int hg, int nh, const fl
   __syncthreads();
 }
 
+// Tile geometry in LDS. A tile is 16 rows of CH 16-byte chunks, loaded by NDMA wave-wide global->LDS DMAs (lane i of
+// DMA j fills LDS chunk 64 j + i). Logical chunk c of row r sits at LDS chunk r * CH + (c + r / ROT) % CH: the per-row
+// rotation spreads the rows a QK read touches over all LDS banks. Each lane's global address absorbs the rotation, so
+// it costs nothing at load time.
+template <int FMT>
+struct TileGeo {
+  static constexpr int CH = FMT == ROWS576 ? 36 : 40;
+  static constexpr int NDMA = CH * 16 / 64;  // 9 or 10
+  static constexpr int SLOT = NDMA * 1024;   // bytes of one ring slot
+  static constexpr int ROT = FMT == ROWS576 ? 4 : 2;
+  __device__ static int lds_chunk(int r, int c) {
+    int x = c + r / ROT;
+    x = x >= CH ? x - CH : x;
+    return r * CH + x;
+  }
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 template <int FMT, int WAVES, bool FINAL>
 __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
-  constexpr int NCH = RowFmt<FMT>::kLaneChunks;
+  using Geo = TileGeo<FMT>;
+  constexpr int CH = Geo::CH;
+  constexpr int NDMA = Geo::NDMA;
+  constexpr int SLOT = Geo::SLOT;
   constexpr int ROWB = RowFmt<FMT>::kRowBytes;
   constexpr bool SPARSE = FMT == ROWS640;
   constexpr int NT = 64 * WAVES;
-  using Ring = MlaRing<FMT>;
+  constexpr int DEPTH = kMlaRingDepth;
+  // VMEM operations one tile issues: its DMAs, plus the per-token scale load of the paged format
+  constexpr int PER_TILE = NDMA + (SPARSE ? 0 : 1);
+  typedef __attribute__((address_space(3))) void lds_void;
 
   const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform, so tile indices stay scalar
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int g4 = lane >> 4;
   const int li = lane & 15;
   const int hg = blockIdx.y;  // 16-head group
   const int nh = min(16, a.H - 16 * hg);
 
-  __shared__ uint4 sm_q[18][64];                                    // query operand, lane order
-  __shared__ int32_t sm_rowid[kMaxSplitKeys];                       // row id of each key of the split, -1 = none
-  __shared__ __attribute__((aligned(16))) uint8_t sm_lat[WAVES][16 * kLdsRow];
-  __shared__ float sm_o[16][kLatent + 4];
+  // LDS: the query operand, the split's row ids, and each wave's ring of DEPTH tile slots. After the tile loop the
+  // ring's space holds the merge buffers.
+  __shared__ uint4 sm_q[18][64];
+  __shared__ int32_t sm_rowid[kMlaMaxSplitKeys];
+  __shared__ __attribute__((aligned(1024))) uint8_t sm_ring[WAVES][DEPTH][SLOT];
   __shared__ float sm_m[WAVES][16];
   __shared__ float sm_l[WAVES][16];
   __shared__ float sm_row[576];
   __shared__ float sm_sn[16];
   __shared__ float sm_red[WAVES];
+  static_assert(sizeof(float) * 16 * (kLatent + 4) <= sizeof(sm_ring), "the merge buffer lives in the ring");
+  float(*sm_o)[kLatent + 4] = reinterpret_cast<float(*)[kLatent + 4]>(&sm_ring[0][0][0]);
 
   // Paged: keys are positions [0, seq_len - 1). Sparse: keys are index-list entries [0, n_indices), modelled as a
   // "sequence" of n_indices + 1 so the same decomposition applies (every row has the same split count).
@@ -224,7 +250,7 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
   }
   if (b < 0) return;
 
-  const int32_t khi = SPARSE ? a.n_indices : a.seq_lens[b] - 1;
+  const int32_t khi = SPARSE ? a.n_indices : ld_const(a.seq_lens + b) - 1;
   const int32_t t_first = split * a.split_tiles;
   const int32_t t_last = min(t_first + a.split_tiles, (khi + 15) / 16);
   const int32_t kbase = t_first * 16;
@@ -271,34 +297,52 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
     sm_rowid[k] = row;
   }
   __syncthreads();
-
-  const float base_scale = a.sm_scale * kLog2e * (SPARSE ? a.kv_scale : 1.0f);
-
-  auto issue = [&](Ring& R, int32_t tile) {
-    const int32_t k0 = tile * 16 - kbase;
-    const int32_t row = sm_rowid[k0 + li];
-    const bool kvalid = row >= 0;
-    R.vmask = (uint32_t)(__ballot(kvalid) & 0xffffull);
-    const uint8_t* rp = a.cache + (int64_t)(kvalid ? row : 0) * ROWB;
+  // the query operand in registers for the whole tile loop
+  uint32_t qv[18][4];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const uint4 w = ld16(rp + chunk_offset<FMT>(g4, c));
-      R.raw[c][0] = w.x;
-      R.raw[c][1] = w.y;
-      R.raw[c][2] = w.z;
-      R.raw[c][3] = w.w;
+  for (int s = 0; s < 18; ++s) {
+    const uint4 w = sm_q[s][lane];
+    qv[s][0] = w.x;
+    qv[s][1] = w.y;
+    qv[s][2] = w.z;
+    qv[s][3] = w.w;
+  }
+
+  // Each lane's (row, chunk) for every DMA of a tile: fixed by the layout.
+  int dma_row[NDMA], dma_off[NDMA];
+#pragma unroll
+  for (int j = 0; j < NDMA; ++j) {
+    const int o = 64 * j + lane;
+    const int r = o / CH, sl = o % CH;
+    int c = sl - r / Geo::ROT;
+    c = c < 0 ? c + CH : c;
+    dma_row[j] = r;
+    dma_off[j] = 16 * c;
+  }
+
+  float kscale_ring[DEPTH][4];
+  // Issue the loads of tile `tile` into ring slot `slot`: NDMA DMAs, and the per-token scales into registers.
+  auto issue = [&](int slot, int32_t tile, float (&ks)[4]) {
+    const int32_t k0 = tile * 16 - kbase;
+    uint8_t* dst = sm_ring[wave][slot];
+#pragma unroll
+    for (int j = 0; j < NDMA; ++j) {
+      const int32_t row = sm_rowid[k0 + dma_row[j]];
+      const uint8_t* src = a.cache + (int64_t)(row >= 0 ? row : 0) * ROWB + dma_off[j];
+      __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(dst + 1024 * j), 16, 0, 0);
     }
     if constexpr (!SPARSE) {
       // per-token scales of keys 4 g4 .. 4 g4 + 3: consecutive slots of one page
       const int32_t srow = sm_rowid[k0 + 4 * g4];
       const float4 s4 = *reinterpret_cast<const float4*>(a.row_scale + (srow >= 0 ? srow : 0));
-      R.kscale[0] = s4.x;
-      R.kscale[1] = s4.y;
-      R.kscale[2] = s4.z;
-      R.kscale[3] = s4.w;
+      ks[0] = s4.x;
+      ks[1] = s4.y;
+      ks[2] = s4.z;
+      ks[3] = s4.w;
     }
   };
 
+  const float base_scale = a.sm_scale * kLog2e * (SPARSE ? a.kv_scale : 1.0f);
   float m_ref = kNegBig;
   float l_run = 0.0f;
   f32x4_t acc[8][4];
@@ -306,57 +350,49 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
   for (int q = 0; q < 8; ++q)
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[q][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  uint8_t* lds = sm_lat[wave];
 
-  auto compute = [&](Ring& R) {
-    const bool full = R.vmask == 0xffffu;
-    if (!full) {
-      // a masked key's bytes are zeroed (a stale NaN there would survive p = 0)
-      const bool mine = (R.vmask >> li) & 1u;
+  auto compute = [&](int slot, int32_t tile, const float (&ks)[4]) {
+    const uint8_t* T = sm_ring[wave][slot];
+    const int32_t k0 = tile * 16 - kbase;
+    // validity of the tile's keys (bit k: key k)
+    const uint32_t vmask = (uint32_t)(__ballot(sm_rowid[k0 + li] >= 0) & 0xffffull);
+    // S^T = K Q^T from the slot: lane (g4, li) reads its chunks of row li. Three accumulators keep three
+    // independent MFMA chains in flight; they are summed at the end.
+    f32x4_t scp[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-      for (int c = 0; c < NCH; ++c)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) R.raw[c][i] = mine ? R.raw[c][i] : 0u;
-    }
-    // latent bytes to LDS for the PV transpose
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const int lat = chunk_latent<FMT>(g4, c);
-      if (lat >= 0)
-        *reinterpret_cast<uint4*>(lds + li * kLdsRow + lat) = make_uint4(R.raw[c][0], R.raw[c][1], R.raw[c][2],
-                                                                          R.raw[c][3]);
-    }
-    // S^T = K Q^T
-    f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 18; ++s) {
-      uint32_t op[4];
-      if constexpr (FMT == ROWS576) {
-        const int c = s >> 1, hf = s & 1;
-        fp8x4_to_bf16x4(R.raw[c][2 * hf], op[0], op[1]);
-        fp8x4_to_bf16x4(R.raw[c][2 * hf + 1], op[2], op[3]);
-      } else {
-        if (s < 2) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) op[i] = R.raw[s][i];
-        } else {
-          const int c = 2 + ((s - 2) >> 1), hf = (s - 2) & 1;
-          fp8x4_to_bf16x4(R.raw[c][2 * hf], op[0], op[1]);
-          fp8x4_to_bf16x4(R.raw[c][2 * hf + 1], op[2], op[3]);
+    for (int s = 0; s < 18; s += 2) {
+      // the two MFMA steps s, s + 1 share one 16-byte chunk
+      f32x4_t& sc = scp[(s / 2) % 3];
+      if constexpr (FMT == ROWS640) {
+        if (s == 0) {
+          // steps 0 and 1: the bf16 rope, one chunk each
+          const uint4 w0 = *reinterpret_cast<const uint4*>(T + 16 * Geo::lds_chunk(li, 2 * g4));
+          const uint4 w1 = *reinterpret_cast<const uint4*>(T + 16 * Geo::lds_chunk(li, 2 * g4 + 1));
+          const uint32_t a0[4] = {w0.x, w0.y, w0.z, w0.w}, a1[4] = {w1.x, w1.y, w1.z, w1.w};
+          sc = mfma_16x16x32_bf16(a0, qv[0], sc);
+          sc = mfma_16x16x32_bf16(a1, qv[1], sc);
+          continue;
         }
       }
-      const uint4 qw = sm_q[s][lane];
-      const uint32_t qop[4] = {qw.x, qw.y, qw.z, qw.w};
-      sc = mfma_16x16x32_bf16(op, qop, sc);
+      const int c = FMT == ROWS576 ? 9 * g4 + s / 2 : 8 + 8 * g4 + (s - 2) / 2;
+      const uint4 w = *reinterpret_cast<const uint4*>(T + 16 * Geo::lds_chunk(li, c));
+      uint32_t op0[4], op1[4];
+      fp8x4_to_bf16x4(w.x, op0[0], op0[1]);
+      fp8x4_to_bf16x4(w.y, op0[2], op0[3]);
+      fp8x4_to_bf16x4(w.z, op1[0], op1[1]);
+      fp8x4_to_bf16x4(w.w, op1[2], op1[3]);
+      sc = mfma_16x16x32_bf16(op0, qv[s], sc);
+      sc = mfma_16x16x32_bf16(op1, qv[s + 1], sc);
     }
+    const f32x4_t sc = scp[0] + scp[1] + scp[2];
     // mask, online softmax with a lazily moved reference maximum
     float x[4];
     float tmax = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const bool ok = (R.vmask >> (4 * g4 + r)) & 1u;
-      const float ks = SPARSE ? 1.0f : R.kscale[r];
-      x[r] = ok ? sc[r] * base_scale * ks : -INFINITY;
+      const bool ok = (vmask >> (4 * g4 + r)) & 1u;
+      const float kscl = SPARSE ? 1.0f : ks[r];
+      x[r] = ok ? sc[r] * base_scale * kscl : -INFINITY;
       tmax = fmaxf(tmax, x[r]);
     }
     tmax = max_across_groups(tmax);
@@ -371,58 +407,76 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[q][r] *= alpha;
     }
-    float p[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p[r] = __builtin_amdgcn_exp2f(x[r] - m_ref);
-      l_run += p[r];
-    }
-    // V is dequantized through P: p' = p * scale(key) (a masked key has p = 0 and zeroed bytes)
     float pv[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const bool ok = (R.vmask >> (4 * g4 + r)) & 1u;
-      pv[r] = ok ? p[r] * (SPARSE ? 1.0f : R.kscale[r]) : 0.0f;
+      const bool ok = (vmask >> (4 * g4 + r)) & 1u;
+      const float p = __builtin_amdgcn_exp2f(x[r] - m_ref);
+      l_run += p;
+      // V is dequantized through P: p' = p * scale(key); a masked key has p = 0
+      pv[r] = ok ? p * (SPARSE ? 1.0f : ks[r]) : 0.0f;
     }
     const uint32_t pop[2] = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
-    // O^T += V^T P^T over 32 d-tiles
-    __builtin_amdgcn_wave_barrier();
+    const bool full = vmask == 0xffffu;
+    // O^T += V^T P^T over 32 d-tiles: lane (g4, i) reads latent dword 64 q + 4 i of rows 4 g4 .. 4 g4 + 3
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       uint32_t w[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        w[e] = *reinterpret_cast<const uint32_t*>(lds + (4 * g4 + e) * kLdsRow + 64 * q + 4 * li);
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * g4 + e;
+        const int rb = (SPARSE ? 128 : 0) + 64 * q + 4 * li;  // the dword's byte within the row
+        w[e] = *reinterpret_cast<const uint32_t*>(T + 16 * Geo::lds_chunk(r, rb >> 4) + (rb & 15));
+        // a masked key's bytes may be anything (a stale NaN would survive p = 0): zero them
+        if (!full) w[e] = ((vmask >> r) & 1u) ? w[e] : 0u;
+      }
+      uint32_t xr[4];
+      transpose4x4_bytes(w, xr);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const uint32_t xr = ((w[0] >> (8 * r)) & 0xffu) | (((w[1] >> (8 * r)) & 0xffu) << 8) |
-                            (((w[2] >> (8 * r)) & 0xffu) << 16) | (((w[3] >> (8 * r)) & 0xffu) << 24);
         uint32_t op[2];
-        fp8x4_to_bf16x4(xr, op[0], op[1]);
+        fp8x4_to_bf16x4(xr[r], op[0], op[1]);
         acc[q][r] = mfma_16x16x16_bf16(op, pop, acc[q][r]);
       }
     }
-    __builtin_amdgcn_wave_barrier();
   };
 
-  // ---- the tile loop: two register buffers, the next tile's loads in flight while one computes ----
+  // ---- the tile loop: DEPTH ring slots per wave, DEPTH - 1 tiles' loads in flight while one computes ----
   {
-    Ring R0, R1;
-    int32_t t = t_first + wave;
-    if (t < t_last) issue(R0, t);
-    while (t < t_last) {
-      if (t + WAVES < t_last) issue(R1, t + WAVES);
-      compute(R0);
-      t += WAVES;
-      if (t >= t_last) break;
-      if (t + WAVES < t_last) issue(R0, t + WAVES);
-      compute(R1);
-      t += WAVES;
+    const int32_t t0 = t_first + wave;
+#pragma unroll
+    for (int i = 0; i < DEPTH - 1; ++i)
+      if (t0 + i * WAVES < t_last) issue(i, t0 + i * WAVES, kscale_ring[i]);
+    for (int32_t base = 0;; base += DEPTH) {
+      bool done = false;
+#pragma unroll
+      for (int k = 0; k < DEPTH; ++k) {
+        const int32_t cur = t0 + (base + k) * WAVES;
+        if (cur >= t_last) {
+          done = true;
+          break;
+        }
+        // issue the tile DEPTH - 1 ahead, then wait until this tile's loads have landed: the ones issued after it
+        // (up to DEPTH - 1 tiles' worth) may stay in flight
+        const int32_t nxt = cur + (DEPTH - 1) * WAVES;
+        if (nxt < t_last) {
+          issue((k + DEPTH - 1) % DEPTH, nxt, kscale_ring[(k + DEPTH - 1) % DEPTH]);
+          wait_vmcnt<(DEPTH - 1) * PER_TILE>();
+        } else if (nxt - WAVES < t_last && DEPTH > 2) {
+          wait_vmcnt<(DEPTH - 2) * PER_TILE>();
+        } else {
+          wait_vmcnt<0>();
+        }
+        compute(k, cur, kscale_ring[k]);
+      }
+      if (done) break;
     }
+    wait_vmcnt<0>();
   }
 
   // ---- the own row, attended in-band by the row's first split (paged: and stored, by head group 0) ----
   const bool own = split == 0;  // uniform
+  __syncthreads();  // every wave is done with the ring before its space becomes the merge buffer
   if (own) {
     own_row_dequant<FMT, NT>(a, b, hg == 0, sm_row, sm_red);
     own_row_scores<NT>(a, b, hg, nh, sm_row, sm_sn);
@@ -574,9 +628,9 @@ static int check_plan(const sna_split_plan* plan, int32_t B, const char* what) {
       plan->batch != B)
     return fail(SNA_ERR_INVALID_ARGUMENT, "%s: missing or foreign split plan (made for %d rows)", what,
                 plan ? plan->batch : -1);
-  if (plan->split_tiles * 16 > kMaxSplitKeys)
+  if (plan->split_tiles * 16 > kMlaMaxSplitKeys)
     return fail(SNA_ERR_INVALID_ARGUMENT, "%s: a split of %d keys exceeds the kernel's %d", what,
-                plan->split_tiles * 16, kMaxSplitKeys);
+                plan->split_tiles * 16, kMlaMaxSplitKeys);
   return SNA_OK;
 }
 

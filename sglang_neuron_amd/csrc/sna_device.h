@@ -19,6 +19,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegBig = -1.0e30f;
 // The most splits a row may have (the combine passes hold one weight per split in LDS); the planner keeps to it.
 constexpr int kMaxSplits = 64;
+// The most keys one MLA / DSA split may cover (the split's row ids live in the kernel's LDS); the planner keeps to it.
+constexpr int kMlaMaxSplitKeys = 2048;
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
@@ -94,6 +96,19 @@ __device__ __forceinline__ void fp8x4_to_bf16x4(uint32_t w, uint32_t& lo, uint32
   bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
   lo = __builtin_bit_cast(uint32_t, a);
   hi = __builtin_bit_cast(uint32_t, b);
+}
+
+// 4x4 byte transpose with v_perm_b32 (its 8 source bytes are {S1 bytes 0-3, S0 bytes 0-3} for selector values 0-7):
+// byte r of w[e] becomes byte e of x[r].
+__device__ __forceinline__ void transpose4x4_bytes(const uint32_t (&w)[4], uint32_t (&x)[4]) {
+  const uint32_t t01l = __builtin_amdgcn_perm(w[1], w[0], 0x05010400u);  // w0.b0 w1.b0 w0.b1 w1.b1
+  const uint32_t t01h = __builtin_amdgcn_perm(w[1], w[0], 0x07030602u);  // w0.b2 w1.b2 w0.b3 w1.b3
+  const uint32_t t23l = __builtin_amdgcn_perm(w[3], w[2], 0x05010400u);
+  const uint32_t t23h = __builtin_amdgcn_perm(w[3], w[2], 0x07030602u);
+  x[0] = __builtin_amdgcn_perm(t23l, t01l, 0x05040100u);
+  x[1] = __builtin_amdgcn_perm(t23l, t01l, 0x07060302u);
+  x[2] = __builtin_amdgcn_perm(t23h, t01h, 0x05040100u);
+  x[3] = __builtin_amdgcn_perm(t23h, t01h, 0x07060302u);
 }
 
 // Two floats to a packed pair of bf16 (round to nearest even), low half first.

@@ -229,10 +229,11 @@ int sna_lse_combine(const float *o_parts, const float *lse_parts, int32_t n_part
 /* ---- diagnostics ---- */
 
 /* Per-kernel timing of the decode entry points, for the benchmark's roofline figure. With timing on, each decode call
- * records HIP events on its stream around its split-K kernel and around its combine pass (up to 4096 calls after the
- * switch). sna_diag_kernel_timing_read waits for the last event and returns the summed milliseconds of each kernel
- * and the number of calls timed. The events are the library's only state besides the error string. The timer is not
- * thread-safe and is off by default. */
+ * launches its split-K kernel and its combine kernel through hipExtLaunchKernel with a start/stop event pair, so the
+ * kernels' own dispatch packets stamp the times and no marker packet runs between them (up to 4096 calls after the
+ * switch). sna_diag_kernel_timing_read waits for the events and returns the summed milliseconds of each kernel and
+ * the number of split-K launches timed. The events are the library's only state besides the error string. The timer
+ * is not thread-safe and is off by default. */
 int sna_diag_kernel_timing(int enable);
 int sna_diag_kernel_timing_read(double *split_ms, double *combine_ms, int64_t *launches);
 

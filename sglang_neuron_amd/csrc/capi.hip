@@ -32,22 +32,32 @@ namespace {
 constexpr int kMaxTimed = 4096;
 bool g_timing = false;
 int g_timed = 0;
-hipEvent_t g_events[kMaxTimed][3];
+hipEvent_t g_events[kMaxTimed][2][2];  // [call][split, combine][start, stop]
 bool g_made[kMaxTimed] = {};
+bool g_used[kMaxTimed][2] = {};
 }  // namespace
 
-void timing_mark(int phase, hipStream_t s) {
-  if (!g_timing || g_timed >= kMaxTimed) return;
+void timing_events(int phase, hipEvent_t* start, hipEvent_t* stop) {
+  *start = nullptr;
+  *stop = nullptr;
+  if (!g_timing || g_timed >= kMaxTimed || phase < 0 || phase > 1) return;
   if (!g_made[g_timed]) {
-    for (int i = 0; i < 3; ++i)
-      if (hipEventCreate(&g_events[g_timed][i]) != hipSuccess) {
-        g_timing = false;
-        return;
-      }
+    for (int p = 0; p < 2; ++p)
+      for (int i = 0; i < 2; ++i)
+        if (hipEventCreate(&g_events[g_timed][p][i]) != hipSuccess) {
+          g_timing = false;
+          return;
+        }
     g_made[g_timed] = true;
   }
-  (void)hipEventRecord(g_events[g_timed][phase], s);
-  if (phase == 2) ++g_timed;
+  g_used[g_timed][phase] = true;
+  *start = g_events[g_timed][phase][0];
+  *stop = g_events[g_timed][phase][1];
+}
+
+void timing_end_call() {
+  if (!g_timing || g_timed >= kMaxTimed) return;
+  if (g_used[g_timed][0] || g_used[g_timed][1]) ++g_timed;
 }
 
 // ---- LSE merge of partials (decode-context-parallel style) ----
@@ -91,7 +101,10 @@ const char* sna_last_error(void) { return error_buffer(); }
 int sna_diag_kernel_timing(int enable) {
   ApiGuard guard;
   g_timing = enable != 0;
-  if (g_timing) g_timed = 0;
+  if (g_timing) {
+    g_timed = 0;
+    for (int i = 0; i < kMaxTimed; ++i) g_used[i][0] = g_used[i][1] = false;
+  }
   return SNA_OK;
 }
 
@@ -100,17 +113,17 @@ int sna_diag_kernel_timing_read(double* split_ms, double* combine_ms, int64_t* l
   if (!split_ms || !combine_ms || !launches) return fail(SNA_ERR_INVALID_ARGUMENT, "kernel_timing_read: null pointer");
   *split_ms = 0.0;
   *combine_ms = 0.0;
-  *launches = g_timed;
-  if (g_timed == 0) return SNA_OK;
-  if (hipEventSynchronize(g_events[g_timed - 1][2]) != hipSuccess)
-    return fail(SNA_ERR_LAUNCH, "kernel_timing_read: event synchronize failed");
+  *launches = 0;
   for (int i = 0; i < g_timed; ++i) {
-    float a = 0.f, b = 0.f;
-    if (hipEventElapsedTime(&a, g_events[i][0], g_events[i][1]) != hipSuccess ||
-        hipEventElapsedTime(&b, g_events[i][1], g_events[i][2]) != hipSuccess)
-      return fail(SNA_ERR_LAUNCH, "kernel_timing_read: elapsed time failed");
-    *split_ms += a;
-    *combine_ms += b;
+    for (int p = 0; p < 2; ++p) {
+      if (!g_used[i][p]) continue;
+      float ms = 0.f;
+      if (hipEventSynchronize(g_events[i][p][1]) != hipSuccess ||
+          hipEventElapsedTime(&ms, g_events[i][p][0], g_events[i][p][1]) != hipSuccess)
+        return fail(SNA_ERR_LAUNCH, "kernel_timing_read: elapsed time failed");
+      (p == 0 ? *split_ms : *combine_ms) += ms;
+    }
+    *launches += g_used[i][0];
   }
   return SNA_OK;
 }

@@ -8,19 +8,21 @@
 //   ROWS640  [k_pe 64 bf16 | latent 512 e4m3fn, permuted], one per-tensor kv_scale. Latent dim c = 256a + 128b + p
 //            sits at latent byte 256a + 2p + b.
 //
-// Work: one workgroup of 4 waves per (row, split, 16-head group). The workgroup first resolves the row id of every
-// key of its split into LDS (the block-table walk, or for DSA the index -> block -> row walk). Each wave then takes
-// 16-key tiles round-robin through a ring of 3 LDS slots, filled by global->LDS DMA: two tiles are in flight while
-// it computes a third, and the in-flight bytes cost no registers.
+// Work: one workgroup of 4 waves per (row, split, 16-head group). Each wave takes the split's 16-key tiles
+// round-robin through its own ring of LDS slots, filled by global->LDS DMA, so the in-flight bytes cost no
+// registers. Paged: a tile is 16 consecutive slots of one page (the page size is a multiple of 16), one contiguous
+// 9 KB run of HBM; the split's block-table entries sit in two VGPRs and a tile's page is a readlane. Sparse: the
+// workgroup first resolves every index of its split to a row id in LDS (index -> block -> row). The own row is
+// quantized as the store quantizes it and attended as a one-key tile by one wave of the row's first split.
 //
 // Lane roles (lane = 16 * g4 + li), 16-key tiles:
-//   QK   S^T[key, head] = K[key, :] . Q[head, :]   v_mfma_f32_16x16x32_bf16, 18 steps over the 576 dims. Lane
-//        (g4, li) feeds 144 (ROWS576) or 160 (ROWS640) bytes of key li's row, loaded straight from HBM, and head li's
-//        query elements under the same K-index map. The query operand lives in LDS in lane order.
+//   QK   S^T[key, head] = K[key, :] . Q[head, :]   v_mfma_f32_16x16x32_bf16, 18 steps over the 576 dims. In step pair
+//        k lane (g4, li) feeds the 16 bytes of chunk 4 k + g4 of key li's row (ROWS640: the rope chunks 4 s + g4
+//        first, then the latent chunks 8 + 4 (k - 1) + g4), and head li's query elements of the same dims, held in
+//        registers for the whole split.
 //   PV   O^T[latent byte, head] = V^T[byte, keys] . P^T[keys, head]   v_mfma_f32_16x16x16_bf16, K = the 16 keys,
-//        lane (g4, *) supplying keys 4 g4 .. 4 g4 + 3, the S^T rows it holds. The latent bytes of the tile go
-//        through LDS. For d-tile (q, r), lane (g4, i) reads dword (64 q + 4 i) of rows 4 g4 .. 4 g4 + 3, transposes
-//        the 4x4 bytes and feeds byte r of each.
+//        lane (g4, *) supplying keys 4 g4 .. 4 g4 + 3, the S^T rows it holds. For d-tile (q, r), lane (g4, i) reads
+//        dword (64 q + 4 i) of rows 4 g4 .. 4 g4 + 3, transposes the 4x4 bytes and feeds byte r of each.
 //   acc  lane (g4, j) accumulates head j at latent bytes 64 q + 16 g4 + 4 r' + r  (q < 8, r < 4, r' < 4).
 #include "sna_device.h"
 #include "sna_host.h"
@@ -31,8 +33,6 @@ enum { ROWS576 = 0, ROWS640 = 1 };
 
 constexpr int kLatent = 512;
 constexpr int kRope = 64;
-constexpr int kLdsRow = 528;        // latent bytes of one key row in LDS, padded so rows 4 apart hit other banks
-constexpr int kMlaRingDepth = 3;    // LDS tile slots per wave
 constexpr float kMlaRescaleSlack = 8.0f;
 
 struct MlaArgs {
@@ -83,42 +83,6 @@ struct RowFmt<ROWS640> {
   static constexpr int kRowBytes = 640;
   static constexpr int kLaneChunks = 10;
 };
-
-// Byte offset within the row of chunk c of lane group g4.
-template <int FMT>
-__device__ __forceinline__ int chunk_offset(int g4, int c) {
-  if constexpr (FMT == ROWS576) {
-    return 144 * g4 + 16 * c;
-  } else {
-    return c < 2 ? 32 * g4 + 16 * c : 128 + 128 * g4 + 16 * (c - 2);
-  }
-}
-
-// Latent byte offset of chunk c of lane group g4, or -1 for a rope chunk.
-template <int FMT>
-__device__ __forceinline__ int chunk_latent(int g4, int c) {
-  if constexpr (FMT == ROWS576) {
-    const int off = 144 * g4 + 16 * c;
-    return off < kLatent ? off : -1;
-  } else {
-    return c < 2 ? -1 : 128 * g4 + 16 * (c - 2);
-  }
-}
-
-// The query element pair-block of step s, lane group g4 for head row qlp/qpp (8 bf16, packed).
-template <int FMT>
-__device__ __forceinline__ uint4 query_chunk(const uint16_t* qlp, const uint16_t* qpp, int g4, int s) {
-  if constexpr (FMT == ROWS576) {
-    const int dim = 144 * g4 + 8 * s;  // natural order: latent then rope
-    return dim < kLatent ? ld16(qlp + dim) : ld16(qpp + (dim - kLatent));
-  } else {
-    if (s < 2) return ld16(qpp + 16 * g4 + 8 * s);
-    uint32_t e[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) e[i] = qlp[latent_dim_of_byte(128 * g4 + 8 * (s - 2) + i)];
-    return make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
-  }
-}
 
 // The own row of sequence b, dequantized in natural order [latent 512 | rope 64] into sm_row, stored into the
 // pool when paged and st is set. Every thread of the workgroup calls it. ROWS576 quantizes with the row's own
@@ -175,22 +139,26 @@ __device__ void own_row_scores(const MlaArgs& a, int b, int hg, int nh, const fl
   __syncthreads();
 }
 
-// Tile geometry in LDS. A tile is 16 rows of CH 16-byte chunks, loaded by NDMA wave-wide global->LDS DMAs (lane i of
-// DMA j fills LDS chunk 64 j + i). Logical chunk c of row r sits at LDS chunk r * CH + (c + r / ROT) % CH: the per-row
-// rotation spreads the rows a QK read touches over all LDS banks. Each lane's global address absorbs the rotation, so
-// it costs nothing at load time.
+// Tile geometry in LDS. A tile is 16 key rows; chunk c (16 bytes) of row r sits at LDS chunk r * STRIDE + c, with
+// STRIDE = CHUNKS + 1: the pad chunk puts rows 1 apart 20 (ROWS576) or 36 (ROWS640) banks apart and rows 4 apart 16
+// banks apart, so the QK reads (16 rows, one 16-byte chunk each) and the PV reads (4 rows x 64 bytes per lane group)
+// are free of bank conflicts, and every LDS address is a per-lane base plus a constant. NDMA wave-wide DMAs fill a
+// slot: lane i of DMA j fills LDS chunk 64 j + i. A pad chunk loads a duplicate of its row's last chunk; the lanes of
+// the last DMA past the tile are switched off. ROWS576 tiles bring their 16 per-token scales along in one more DMA.
 template <int FMT>
 struct TileGeo {
-  static constexpr int CH = FMT == ROWS576 ? 36 : 40;
-  static constexpr int NDMA = CH * 16 / 64;  // 9 or 10
-  static constexpr int SLOT = NDMA * 1024;   // bytes of one ring slot
-  static constexpr int ROT = FMT == ROWS576 ? 4 : 2;
-  __device__ static int lds_chunk(int r, int c) {
-    int x = c + r / ROT;
-    x = x >= CH ? x - CH : x;
-    return r * CH + x;
-  }
+  static constexpr int CHUNKS = FMT == ROWS576 ? 36 : 40;
+  static constexpr int STRIDE = CHUNKS + 1;
+  static constexpr int RS = 16 * STRIDE;                        // LDS row stride, bytes
+  static constexpr int NDMA = (16 * STRIDE + 63) / 64;          // 10 or 11
+  static constexpr int TAIL = 16 * STRIDE - 64 * (NDMA - 1);    // active lanes of the last DMA
+  static constexpr int SCALES = 16 * RS;                        // offset of the 16 per-token scales (ROWS576)
+  static constexpr int SLOT = 16 * RS + 64;                     // bytes of one ring slot
+  static constexpr int DEPTH = FMT == ROWS576 ? 4 : 3;          // ring slots per wave
 };
+
+// Dword 3 of a raw buffer resource on gfx9-family chips (no format conversion, no swizzle).
+constexpr int kBufferFlags = 0x00020000;
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -198,19 +166,42 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int FMT, int WAVES, bool FINAL>
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Two query dwords of a ROWS640 latent step: bytes 2i + bb of the step hold dim (bb ? y : x)[i], i < 4, from the
+// bf16 pairs x = x0 | x1 << 16 and y = y0 | y1 << 16.
+__device__ __forceinline__ void interleave_pairs(uint32_t x, uint32_t y, uint32_t& d0, uint32_t& d1) {
+  d0 = (x & 0xffffu) | (y << 16);
+  d1 = (x >> 16) | (y & 0xffff0000u);
+}
+
+// WIDE: a sparse pool past 4 GiB, whose rows take 64-bit addresses (every other pool is read through 32-bit buffer
+// offsets).
+template <int FMT, int WAVES, bool FINAL, bool WIDE>
 __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
   using Geo = TileGeo<FMT>;
-  constexpr int CH = Geo::CH;
   constexpr int NDMA = Geo::NDMA;
   constexpr int SLOT = Geo::SLOT;
+  constexpr int RS = Geo::RS;
+  constexpr int DEPTH = Geo::DEPTH;
   constexpr int ROWB = RowFmt<FMT>::kRowBytes;
   constexpr bool SPARSE = FMT == ROWS640;
   constexpr int NT = 64 * WAVES;
-  constexpr int DEPTH = kMlaRingDepth;
-  // VMEM operations one tile issues: its DMAs, plus the per-token scale load of the paged format
+  // VMEM operations one tile issues: its DMAs, plus the per-token scale DMA of the paged format
   constexpr int PER_TILE = NDMA + (SPARSE ? 0 : 1);
+  static_assert((DEPTH - 1) * PER_TILE < 64, "vmcnt range");
+  static_assert(WAVES == 4, "the merge splits the 8 latent blocks over 4 waves");
   typedef __attribute__((address_space(3))) void lds_void;
+  typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -220,18 +211,15 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
   const int hg = blockIdx.y;  // 16-head group
   const int nh = min(16, a.H - 16 * hg);
 
-  // LDS: the query operand, the split's row ids, and each wave's ring of DEPTH tile slots. After the tile loop the
-  // ring's space holds the merge buffers.
-  __shared__ uint4 sm_q[18][64];
-  __shared__ int32_t sm_rowid[kMlaMaxSplitKeys];
-  __shared__ __attribute__((aligned(1024))) uint8_t sm_ring[WAVES][DEPTH][SLOT];
+  // LDS: each wave's ring of DEPTH tile slots (after the tile loop: the merge exchange), the sparse row ids, and the
+  // waves' softmax statistics.
+  __shared__ __attribute__((aligned(16))) uint8_t sm_ring[WAVES][DEPTH][SLOT];
+  __shared__ int32_t sm_rowid[SPARSE ? kMlaMaxSplitKeys : 1];
   __shared__ float sm_m[WAVES][16];
   __shared__ float sm_l[WAVES][16];
-  __shared__ float sm_row[576];
-  __shared__ float sm_sn[16];
-  __shared__ float sm_red[WAVES];
-  static_assert(sizeof(float) * 16 * (kLatent + 4) <= sizeof(sm_ring), "the merge buffer lives in the ring");
-  float(*sm_o)[kLatent + 4] = reinterpret_cast<float(*)[kLatent + 4]>(&sm_ring[0][0][0]);
+  __shared__ __attribute__((aligned(16))) uint16_t sm_own[576];  // the own row (bf16), DMA'd during the prologue
+  static_assert(sizeof(float4) * WAVES * 6 * 4 * 64 <= sizeof(sm_ring), "the merge exchange lives in the ring");
+  float4* sm_x = reinterpret_cast<float4*>(&sm_ring[0][0][0]);
 
   // Paged: keys are positions [0, seq_len - 1). Sparse: keys are index-list entries [0, n_indices), modelled as a
   // "sequence" of n_indices + 1 so the same decomposition applies (every row has the same split count).
@@ -245,100 +233,168 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
     }
   } else {
     locate_work<16>(a.seq_lens, a.B, 0, a.split_tiles, (int32_t)blockIdx.x, b, split);
-    b = __builtin_amdgcn_readfirstlane(b);
-    split = __builtin_amdgcn_readfirstlane(split);
   }
+  b = __builtin_amdgcn_readfirstlane(b);
+  split = __builtin_amdgcn_readfirstlane(split);
   if (b < 0) return;
 
   const int32_t khi = SPARSE ? a.n_indices : ld_const(a.seq_lens + b) - 1;
   const int32_t t_first = split * a.split_tiles;
   const int32_t t_last = min(t_first + a.split_tiles, (khi + 15) / 16);
   const int32_t kbase = t_first * 16;
-  const int32_t nkeys = (t_last - t_first) * 16;
-
-  // ---- the query operand into LDS, and every key's row id ----
-  for (int e = tid; e < 18 * 64; e += NT) {
-    const int s = e >> 6, ln = e & 63;
-    const int32_t h = 16 * hg + (ln & 15);
-    uint4 w = make_uint4(0, 0, 0, 0);
-    if (h < a.H) {
-      const uint16_t* qlp = a.ql + ((int64_t)b * a.H + h) * kLatent;
-      const uint16_t* qpp = a.qpe + ((int64_t)b * a.H + h) * kRope;
-      w = query_chunk<FMT>(qlp, qpp, ln >> 4, s);
-    }
-    sm_q[s][ln] = w;
-  }
   const int32_t* trow = a.table + (int64_t)b * a.table_stride;
-  const int64_t n_rows = a.num_blocks * a.P;
-  int32_t qpos = 0;
-  if constexpr (SPARSE) qpos = a.positions[b];
-  for (int k = tid; k < nkeys; k += NT) {
-    const int32_t key = kbase + k;
-    int32_t row = -1;
+
+  // ---- prologue: the split's block-table entries (paged), the query operand, the own row ----
+  int32_t pg0 = -1, pg1 = -1, col0 = 0;
+  if constexpr (!SPARSE) {
+    // a split spans at most 128 table columns: at most 2048 keys, pages of at least 16
+    col0 = kbase / a.P;
+    const int32_t col_end = min((t_last * 16 - 1) / a.P + 1, a.table_width);
+    if (col0 + lane < col_end) pg0 = trow[col0 + lane];
+    if (col0 + 64 + lane < col_end) pg1 = trow[col0 + 64 + lane];
+  }
+  uint32_t qv[18][4];
+  {
+    const int32_t h = min(16 * hg + li, a.H - 1);  // lanes of absent heads read a real head; their results are dropped
+    const uint16_t* qlp = a.ql + ((int64_t)b * a.H + h) * kLatent;
+    const uint16_t* qpp = a.qpe + ((int64_t)b * a.H + h) * kRope;
+    if constexpr (FMT == ROWS576) {
+#pragma unroll
+      for (int k = 0; k < 9; ++k) {
+        const int d = 16 * (4 * k + g4);  // chunk 4 k + g4 = dims d .. d + 15: latent for k < 8, rope for k = 8
+        const uint16_t* src = k < 8 ? qlp + d : qpp + (d - kLatent);
+        const uint4 x = ld16(src), y = ld16(src + 8);
+        qv[2 * k][0] = x.x, qv[2 * k][1] = x.y, qv[2 * k][2] = x.z, qv[2 * k][3] = x.w;
+        qv[2 * k + 1][0] = y.x, qv[2 * k + 1][1] = y.y, qv[2 * k + 1][2] = y.z, qv[2 * k + 1][3] = y.w;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {  // rope chunk 4 s + g4: dims 8 (4 s + g4) .. + 7, bf16 on both sides
+        const uint4 x = ld16(qpp + 8 * (4 * s + g4));
+        qv[s][0] = x.x, qv[s][1] = x.y, qv[s][2] = x.z, qv[s][3] = x.w;
+      }
+#pragma unroll
+      for (int k = 1; k < 9; ++k) {
+        // latent chunk m = 4 (k - 1) + g4: bytes 16 m .. 16 m + 15 = dims 256 a + 128 bb + p0 + i, byte 2 i + bb
+        const int m = 4 * (k - 1) + g4;
+        const int a0 = (16 * m) >> 8, p0 = ((16 * m) & 255) >> 1;
+        const uint4 x = ld16(qlp + 256 * a0 + p0), y = ld16(qlp + 256 * a0 + 128 + p0);
+        interleave_pairs(x.x, y.x, qv[2 * k][0], qv[2 * k][1]);
+        interleave_pairs(x.y, y.y, qv[2 * k][2], qv[2 * k][3]);
+        interleave_pairs(x.z, y.z, qv[2 * k + 1][0], qv[2 * k + 1][1]);
+        interleave_pairs(x.w, y.w, qv[2 * k + 1][2], qv[2 * k + 1][3]);
+      }
+    }
+  }
+  // The own row is attended by one wave of the row's first split, after its tiles: the wave with the fewest.
+  const int32_t ntiles = t_last - t_first;
+  const bool own_wave = split == 0 && wave == ((ntiles % WAVES) == 0 ? WAVES - 1 : ntiles % WAVES);
+  // Its bytes land in LDS while the tiles stream: issued first, they are complete once the first tile's are.
+  if (own_wave) {
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.own + (int64_t)b * 576);
+    __builtin_amdgcn_global_load_lds((const void*)(src + 16u * (uint32_t)lane), (lds_void*)&sm_own[0], 16, 0, 0);
+    if (lane < 8)
+      __builtin_amdgcn_global_load_lds((const void*)(src + 1024u + 16u * (uint32_t)lane), (lds_void*)&sm_own[512], 16,
+                                       0, 0);
+  }
+
+  // Sparse: every index of the split to a row id (-1: skipped), all loads of a stage in flight together.
+  if constexpr (SPARSE) {
+    constexpr int KPT = kMlaMaxSplitKeys / NT;
+    const int32_t nkeys = (t_last - t_first) * 16;
+    const int32_t qpos = a.positions[b];
+    const int64_t n_rows = a.num_blocks * a.P;
+    int32_t pos[KPT];
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int32_t k = tid + i * NT, key = kbase + k;
+      pos[i] = (k < nkeys && key < khi) ? a.indices[(int64_t)b * a.n_indices + key] : -1;
+    }
+    int32_t ent[KPT];
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      ent[i] = -1;
+      if (pos[i] >= 0 && pos[i] <= qpos && pos[i] / a.P < a.table_width) ent[i] = trow[pos[i] / a.P];
+    }
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int32_t k = tid + i * NT;
+      if (k >= nkeys) continue;
+      int32_t row = -1;
+      if (ent[i] >= 0 && (int64_t)ent[i] < a.num_blocks) {
+        const int64_t r = (int64_t)ent[i] * a.P + pos[i] % a.P;
+        if (r < n_rows) row = (int32_t)r;
+      }
+      sm_rowid[k] = row;
+    }
+    __syncthreads();
+  }
+
+  // Each lane's source chunk for every DMA of a tile: LDS chunk o = 64 j + lane is chunk o % STRIDE of row
+  // o / STRIDE (the pad chunk repeats the row's last chunk; rows past the tile only occur on switched-off lanes).
+  // Offsets are 32-bit against a uniform base, so the DMAs take the scalar-base + vector-offset address form.
+  uint32_t dma_src[NDMA];
+#pragma unroll
+  for (int j = 0; j < NDMA; ++j) {
+    const uint32_t o = 64 * j + lane;
+    const uint32_t r = min(o / Geo::STRIDE, 15u);
+    const uint32_t c = min(o % Geo::STRIDE, (uint32_t)Geo::CHUNKS - 1);
+    dma_src[j] = SPARSE ? (r << 16) | (16 * c) : r * ROWB + 16 * c;
+  }
+
+  // Paged: the first slot of tile `tile` and whether its page is real (uniform).
+  auto tile_row0 = [&](int32_t tile, bool& ok) -> int64_t {
+    const int32_t key0 = tile * 16;
+    const int32_t col = key0 / a.P - col0;  // < 128
+    const int32_t page = __builtin_amdgcn_readlane(col < 64 ? pg0 : pg1, col & 63);
+    ok = page >= 0 && (int64_t)page < a.num_blocks;
+    return ok ? (int64_t)page * a.P + key0 % a.P : 0;
+  };
+  // The valid keys of tile `tile` (bit k: key k), uniform.
+  auto tile_mask = [&](int32_t tile) -> uint32_t {
     if constexpr (SPARSE) {
-      const int32_t pos = key < khi ? a.indices[(int64_t)b * a.n_indices + key] : -1;
-      if (pos >= 0 && pos <= qpos) {
-        const int32_t blk = pos / a.P;
-        if (blk < a.table_width) {
-          const int32_t e = trow[blk];
-          if (e >= 0 && (int64_t)e < a.num_blocks) {
-            const int64_t r = (int64_t)e * a.P + pos % a.P;
-            if (r < n_rows) row = (int32_t)r;
-          }
+      return (uint32_t)(__ballot(sm_rowid[tile * 16 - kbase + li] >= 0) & 0xffffull);
+    } else {
+      bool ok;
+      (void)tile_row0(tile, ok);
+      const int32_t nvalid = ok ? min(16, khi - tile * 16) : 0;
+      return nvalid >= 16 ? 0xffffu : (1u << nvalid) - 1u;
+    }
+  };
+  // Issue the loads of tile `tile` into the ring slot at dst: NDMA DMAs, and the per-token scales (paged).
+  // The DMAs read through buffer resources (a uniform base and size in SGPRs, a 32-bit offset per lane); the
+  // sparse rows of a pool past 4 GiB take 64-bit addresses instead.
+  const __amdgpu_buffer_rsrc_t pool_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.cache, (short)0, WIDE ? 0 : (int)(uint32_t)(a.num_blocks * a.P * ROWB), kBufferFlags);
+  auto issue = [&](lds_void* dst, int32_t tile) {
+    lds_u8* d = (lds_u8*)dst;
+    if constexpr (SPARSE) {
+      const int32_t k0 = tile * 16 - kbase;
+#pragma unroll
+      for (int j = 0; j < NDMA; ++j) {
+        const int32_t row = max(sm_rowid[k0 + (int32_t)(dma_src[j] >> 16)], 0);
+        if (j < NDMA - 1 || lane < Geo::TAIL) {
+          if constexpr (!WIDE)
+            buffer_load_lds16(pool_rsrc, (lds_void*)(d + 1024 * j), (uint32_t)row * ROWB + (dma_src[j] & 0xffffu));
+          else
+            __builtin_amdgcn_global_load_lds((const void*)(a.cache + (int64_t)row * ROWB + (dma_src[j] & 0xffffu)),
+                                             (lds_void*)(d + 1024 * j), 16, 0, 0);
         }
       }
     } else {
-      if (key < khi) {
-        const int32_t col = key / a.P;
-        const int32_t e = col < a.table_width ? trow[col] : -1;
-        if (e >= 0 && (int64_t)e < a.num_blocks) row = e * a.P + key % a.P;
-      }
-    }
-    sm_rowid[k] = row;
-  }
-  __syncthreads();
-  // the query operand in registers for the whole tile loop
-  uint32_t qv[18][4];
+      bool ok;
+      const int64_t row0 = tile_row0(tile, ok);
+      const __amdgpu_buffer_rsrc_t rk =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(a.cache + row0 * ROWB), (short)0, 16 * ROWB, kBufferFlags);
 #pragma unroll
-  for (int s = 0; s < 18; ++s) {
-    const uint4 w = sm_q[s][lane];
-    qv[s][0] = w.x;
-    qv[s][1] = w.y;
-    qv[s][2] = w.z;
-    qv[s][3] = w.w;
-  }
-
-  // Each lane's (row, chunk) for every DMA of a tile: fixed by the layout.
-  int dma_row[NDMA], dma_off[NDMA];
-#pragma unroll
-  for (int j = 0; j < NDMA; ++j) {
-    const int o = 64 * j + lane;
-    const int r = o / CH, sl = o % CH;
-    int c = sl - r / Geo::ROT;
-    c = c < 0 ? c + CH : c;
-    dma_row[j] = r;
-    dma_off[j] = 16 * c;
-  }
-
-  float kscale_ring[DEPTH][4];
-  // Issue the loads of tile `tile` into ring slot `slot`: NDMA DMAs, and the per-token scales into registers.
-  auto issue = [&](int slot, int32_t tile, float (&ks)[4]) {
-    const int32_t k0 = tile * 16 - kbase;
-    uint8_t* dst = sm_ring[wave][slot];
-#pragma unroll
-    for (int j = 0; j < NDMA; ++j) {
-      const int32_t row = sm_rowid[k0 + dma_row[j]];
-      const uint8_t* src = a.cache + (int64_t)(row >= 0 ? row : 0) * ROWB + dma_off[j];
-      __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(dst + 1024 * j), 16, 0, 0);
-    }
-    if constexpr (!SPARSE) {
-      // per-token scales of keys 4 g4 .. 4 g4 + 3: consecutive slots of one page
-      const int32_t srow = sm_rowid[k0 + 4 * g4];
-      const float4 s4 = *reinterpret_cast<const float4*>(a.row_scale + (srow >= 0 ? srow : 0));
-      ks[0] = s4.x;
-      ks[1] = s4.y;
-      ks[2] = s4.z;
-      ks[3] = s4.w;
+      for (int j = 0; j < NDMA; ++j)
+        if (j < NDMA - 1 || lane < Geo::TAIL)
+          buffer_load_lds16(rk, (lds_void*)(d + 1024 * j), dma_src[j]);
+      // the tile's 16 per-token scales, consecutive like its rows
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(a.row_scale + row0), (short)0, 64, kBufferFlags);
+      if (lane < 16)
+        buffer_load_lds4(rs, (lds_void*)(d + Geo::SCALES), 4u * (uint32_t)lane);
     }
   };
 
@@ -351,38 +407,60 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[q][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int slot, int32_t tile, const float (&ks)[4]) {
-    const uint8_t* T = sm_ring[wave][slot];
-    const int32_t k0 = tile * 16 - kbase;
-    // validity of the tile's keys (bit k: key k)
-    const uint32_t vmask = (uint32_t)(__ballot(sm_rowid[k0 + li] >= 0) & 0xffffull);
-    // S^T = K Q^T from the slot: lane (g4, li) reads its chunks of row li. Three accumulators keep three
-    // independent MFMA chains in flight; they are summed at the end.
+  // PV of one tile: O^T += V^T P^T over 32 d-tiles. A masked key's bytes may be anything (a stale NaN would survive
+  // p = 0), so a tile with masked keys zeroes them.
+  auto pv = [&](const uint8_t* T, const uint32_t (&pop)[2], uint32_t vmask, auto masked) {
+    const uint8_t* Tv = T + 4 * g4 * RS + 4 * li + (SPARSE ? 128 : 0);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        w[e] = *reinterpret_cast<const uint32_t*>(Tv + e * RS + 64 * q);
+        if constexpr (decltype(masked)::value) w[e] = ((vmask >> (4 * g4 + e)) & 1u) ? w[e] : 0u;
+      }
+      uint32_t xr[4];
+      transpose4x4_bytes(w, xr);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        uint32_t op[2];
+        fp8x4_to_bf16x4(xr[r], op[0], op[1]);
+        acc[q][r] = mfma_16x16x16_bf16(op, pop, acc[q][r]);
+      }
+    }
+  };
+
+  auto compute = [&](const uint8_t* T, uint32_t vmask) {
+    float ks[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    if constexpr (!SPARSE) {  // scales of keys 4 g4 .. 4 g4 + 3
+      const float4 s4 = *reinterpret_cast<const float4*>(T + Geo::SCALES + 16 * g4);
+      ks[0] = s4.x, ks[1] = s4.y, ks[2] = s4.z, ks[3] = s4.w;
+    }
+    // S^T = K Q^T: three accumulators keep three independent MFMA chains in flight
+    const uint8_t* Tq = T + li * RS + 16 * g4;
     f32x4_t scp[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-    for (int s = 0; s < 18; s += 2) {
-      // the two MFMA steps s, s + 1 share one 16-byte chunk
-      f32x4_t& sc = scp[(s / 2) % 3];
-      if constexpr (FMT == ROWS640) {
-        if (s == 0) {
+    for (int k = 0; k < 9; ++k) {
+      f32x4_t& sc = scp[k % 3];
+      if constexpr (SPARSE) {
+        if (k == 0) {
           // steps 0 and 1: the bf16 rope, one chunk each
-          const uint4 w0 = *reinterpret_cast<const uint4*>(T + 16 * Geo::lds_chunk(li, 2 * g4));
-          const uint4 w1 = *reinterpret_cast<const uint4*>(T + 16 * Geo::lds_chunk(li, 2 * g4 + 1));
+          const uint4 w0 = *reinterpret_cast<const uint4*>(Tq);
+          const uint4 w1 = *reinterpret_cast<const uint4*>(Tq + 64);
           const uint32_t a0[4] = {w0.x, w0.y, w0.z, w0.w}, a1[4] = {w1.x, w1.y, w1.z, w1.w};
           sc = mfma_16x16x32_bf16(a0, qv[0], sc);
           sc = mfma_16x16x32_bf16(a1, qv[1], sc);
           continue;
         }
       }
-      const int c = FMT == ROWS576 ? 9 * g4 + s / 2 : 8 + 8 * g4 + (s - 2) / 2;
-      const uint4 w = *reinterpret_cast<const uint4*>(T + 16 * Geo::lds_chunk(li, c));
+      const uint4 w = *reinterpret_cast<const uint4*>(Tq + (SPARSE ? 128 + 64 * (k - 1) : 64 * k));
       uint32_t op0[4], op1[4];
       fp8x4_to_bf16x4(w.x, op0[0], op0[1]);
       fp8x4_to_bf16x4(w.y, op0[2], op0[3]);
       fp8x4_to_bf16x4(w.z, op1[0], op1[1]);
       fp8x4_to_bf16x4(w.w, op1[2], op1[3]);
-      sc = mfma_16x16x32_bf16(op0, qv[s], sc);
-      sc = mfma_16x16x32_bf16(op1, qv[s + 1], sc);
+      sc = mfma_16x16x32_bf16(op0, qv[2 * k], sc);
+      sc = mfma_16x16x32_bf16(op1, qv[2 * k + 1], sc);
     }
     const f32x4_t sc = scp[0] + scp[1] + scp[2];
     // mask, online softmax with a lazily moved reference maximum
@@ -391,8 +469,7 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const bool ok = (vmask >> (4 * g4 + r)) & 1u;
-      const float kscl = SPARSE ? 1.0f : ks[r];
-      x[r] = ok ? sc[r] * base_scale * kscl : -INFINITY;
+      x[r] = ok ? sc[r] * base_scale * (SPARSE ? 1.0f : ks[r]) : -INFINITY;
       tmax = fmaxf(tmax, x[r]);
     }
     tmax = max_across_groups(tmax);
@@ -407,183 +484,252 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[q][r] *= alpha;
     }
-    float pv[4];
+    float pw[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const bool ok = (vmask >> (4 * g4 + r)) & 1u;
       const float p = __builtin_amdgcn_exp2f(x[r] - m_ref);
       l_run += p;
       // V is dequantized through P: p' = p * scale(key); a masked key has p = 0
-      pv[r] = ok ? p * (SPARSE ? 1.0f : ks[r]) : 0.0f;
+      pw[r] = ok ? p * (SPARSE ? 1.0f : ks[r]) : 0.0f;
     }
-    const uint32_t pop[2] = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
-    const bool full = vmask == 0xffffu;
-    // O^T += V^T P^T over 32 d-tiles: lane (g4, i) reads latent dword 64 q + 4 i of rows 4 g4 .. 4 g4 + 3
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      uint32_t w[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = 4 * g4 + e;
-        const int rb = (SPARSE ? 128 : 0) + 64 * q + 4 * li;  // the dword's byte within the row
-        w[e] = *reinterpret_cast<const uint32_t*>(T + 16 * Geo::lds_chunk(r, rb >> 4) + (rb & 15));
-        // a masked key's bytes may be anything (a stale NaN would survive p = 0): zero them
-        if (!full) w[e] = ((vmask >> r) & 1u) ? w[e] : 0u;
-      }
-      uint32_t xr[4];
-      transpose4x4_bytes(w, xr);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        uint32_t op[2];
-        fp8x4_to_bf16x4(xr[r], op[0], op[1]);
-        acc[q][r] = mfma_16x16x16_bf16(op, pop, acc[q][r]);
-      }
-    }
+    const uint32_t pop[2] = {pack_bf16x2(pw[0], pw[1]), pack_bf16x2(pw[2], pw[3])};
+    if (vmask == 0xffffu) pv(T, pop, vmask, std::false_type{});
+    else pv(T, pop, vmask, std::true_type{});
   };
 
-  // ---- the tile loop: DEPTH ring slots per wave, DEPTH - 1 tiles' loads in flight while one computes ----
+  // ---- the tile loop: wave w takes tiles t_first + w + WAVES i through its ring of DEPTH slots; DEPTH - 1 tiles'
+  // loads are in flight while one computes ----
   {
     const int32_t t0 = t_first + wave;
+    const int32_t mine = t0 < t_last ? (t_last - t0 + WAVES - 1) / WAVES : 0;
+    uint8_t* ring = &sm_ring[wave][0][0];
+    lds_u8* ring_lds = (lds_u8*)(&sm_ring[wave][0][0]);
 #pragma unroll
     for (int i = 0; i < DEPTH - 1; ++i)
-      if (t0 + i * WAVES < t_last) issue(i, t0 + i * WAVES, kscale_ring[i]);
-    for (int32_t base = 0;; base += DEPTH) {
-      bool done = false;
-#pragma unroll
-      for (int k = 0; k < DEPTH; ++k) {
-        const int32_t cur = t0 + (base + k) * WAVES;
-        if (cur >= t_last) {
-          done = true;
-          break;
-        }
-        // issue the tile DEPTH - 1 ahead, then wait until this tile's loads have landed: the ones issued after it
-        // (up to DEPTH - 1 tiles' worth) may stay in flight
-        const int32_t nxt = cur + (DEPTH - 1) * WAVES;
-        if (nxt < t_last) {
-          issue((k + DEPTH - 1) % DEPTH, nxt, kscale_ring[(k + DEPTH - 1) % DEPTH]);
-          wait_vmcnt<(DEPTH - 1) * PER_TILE>();
-        } else if (nxt - WAVES < t_last && DEPTH > 2) {
-          wait_vmcnt<(DEPTH - 2) * PER_TILE>();
-        } else {
-          wait_vmcnt<0>();
-        }
-        compute(k, cur, kscale_ring[k]);
+      if (i < mine) issue((lds_void*)(ring_lds + i * SLOT), t0 + i * WAVES);
+    int slot = 0;
+    for (int32_t i = 0; i < mine; ++i) {
+      // issue tile i + DEPTH - 1, then wait until tile i's loads have landed: those issued after it may stay in flight
+      const int32_t ahead = mine - 1 - i;  // tiles after this one
+      if (ahead >= DEPTH - 1) {
+        const int nslot = slot == 0 ? DEPTH - 1 : slot - 1;  // (slot + DEPTH - 1) % DEPTH
+        issue((lds_void*)(ring_lds + nslot * SLOT), t0 + (i + DEPTH - 1) * WAVES);
+        wait_vmcnt<(DEPTH - 1) * PER_TILE>();
+      } else if (DEPTH > 2 && ahead == DEPTH - 2) {
+        wait_vmcnt<(DEPTH > 2 ? DEPTH - 2 : 0) * PER_TILE>();
+      } else if (DEPTH > 3 && ahead == DEPTH - 3) {
+        wait_vmcnt<(DEPTH > 3 ? DEPTH - 3 : 0) * PER_TILE>();
+      } else {
+        wait_vmcnt<0>();
       }
-      if (done) break;
+      const int32_t cur = t0 + i * WAVES;
+      compute(ring + slot * SLOT, tile_mask(cur));
+      slot = slot == DEPTH - 1 ? 0 : slot + 1;
     }
     wait_vmcnt<0>();
   }
 
-  // ---- the own row, attended in-band by the row's first split (paged: and stored, by head group 0) ----
-  const bool own = split == 0;  // uniform
-  __syncthreads();  // every wave is done with the ring before its space becomes the merge buffer
-  if (own) {
-    own_row_dequant<FMT, NT>(a, b, hg == 0, sm_row, sm_red);
-    own_row_scores<NT>(a, b, hg, nh, sm_row, sm_sn);
+  // ---- the own row: quantized as the store quantizes it, written into slot 0 as key 0 of a one-key tile ----
+  if (own_wave) {
+    uint8_t* T = &sm_ring[wave][0][0];
+    // 8-element chunks lane and lane + 64 of the own row
+    const uint4 own0 = *reinterpret_cast<const uint4*>(&sm_own[8 * lane]);
+    const uint4 own1 = lane < 8 ? *reinterpret_cast<const uint4*>(&sm_own[8 * (lane + 64)]) : make_uint4(0, 0, 0, 0);
+    const uint32_t w[8] = {own0.x, own0.y, own0.z, own0.w, own1.x, own1.y, own1.z, own1.w};
+    if constexpr (FMT == ROWS576) {
+      float m = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        m = fmaxf(m, fabsf(bf16_bits_to_f32(w[j] & 0xffffu)));
+        m = fmaxf(m, fabsf(bf16_bits_to_f32(w[j] >> 16)));
+      }
+      const float s = scale_from_absmax(wave_max(m));
+      int64_t slot = -1;
+      if (hg == 0 && a.new_slots) slot = redirect_slot(a.new_slots[b], a.num_blocks * a.P);
+#pragma unroll
+      for (int part = 0; part < 2; ++part) {
+        if (part == 1 && lane >= 8) continue;
+        uint32_t o[2] = {0, 0};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t bits = (w[part * 4 + (i >> 1)] >> ((i & 1) * 16)) & 0xffffu;
+          o[i >> 2] |= quantize_e4m3fn(bits, s) << ((i & 3) * 8);
+        }
+        const int byte = 8 * (lane + 64 * part);
+        *reinterpret_cast<uint2*>(T + byte) = make_uint2(o[0], o[1]);
+        if (slot >= 0) *reinterpret_cast<uint2*>(a.cache + slot * 576 + byte) = make_uint2(o[0], o[1]);
+      }
+      if (slot >= 0 && lane == 0) a.row_scale[slot] = s;
+      if (lane < 16) reinterpret_cast<float*>(T + Geo::SCALES)[lane] = s;
+    } else {
+      // [rope 64 | latent 512] bf16 -> [bf16(rope / kv_scale) | e4m3fn(latent / kv_scale), permuted]
+#pragma unroll
+      for (int part = 0; part < 2; ++part) {
+        if (part == 1 && lane >= 8) continue;
+        const int ch = lane + 64 * part;  // 8-element chunk of the own row
+        if (ch < 8) {
+          uint32_t o[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = f32_to_bf16_bits(bf16_bits_to_f32(w[part * 4 + i] & 0xffffu) / a.kv_scale);
+            const uint32_t hi = f32_to_bf16_bits(bf16_bits_to_f32(w[part * 4 + i] >> 16) / a.kv_scale);
+            o[i] = lo | (hi << 16);
+          }
+          *reinterpret_cast<uint4*>(T + 16 * ch) = make_uint4(o[0], o[1], o[2], o[3]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const uint32_t bits = (w[part * 4 + (i >> 1)] >> ((i & 1) * 16)) & 0xffffu;
+            T[128 + latent_byte_of_dim(8 * (ch - 8) + i)] = (uint8_t)quantize_e4m3fn(bits, a.kv_scale);
+          }
+        }
+      }
+    }
+    compute(T, 1u);
   }
 
-  // ---- merge: a common maximum per head, then the waves' rescaled accumulators summed through LDS ----
-  const float l_tot = sum_across_groups(l_run);
+  // ---- merge: a common maximum per head; wave w sums latent blocks 2 w, 2 w + 1 over the waves and writes them ----
+  const float l_w = sum_across_groups(l_run);
   if (g4 == 0) {
     sm_m[wave][li] = m_ref;
-    sm_l[wave][li] = l_tot;
+    sm_l[wave][li] = l_w;
+  }
+  __syncthreads();  // every wave is past its tile loop: the ring's space is free for the exchange
+  float M = sm_m[0][li];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) M = fmaxf(M, sm_m[w][li]);
+  float L = 0.0f;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) L += __builtin_amdgcn_exp2f(sm_m[w][li] - M) * sm_l[w][li];
+  const float f = __builtin_amdgcn_exp2f(m_ref - M);
+  // exchange slot of (sender w, block q not its own): [w][q < 2 w ? q : q - 2][r][lane]
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    if (q / 2 == wave) continue;
+    const int idx = q < 2 * wave ? q : q - 2;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const f32x4_t v = acc[q][r] * f;
+      sm_x[((wave * 6 + idx) * 4 + r) * 64 + lane] = make_float4(v[0], v[1], v[2], v[3]);
+    }
   }
   __syncthreads();
-  float M = own ? sm_sn[li] : -INFINITY;
-#pragma unroll
-  for (int w = 0; w < WAVES; ++w) M = fmaxf(M, sm_m[w][li]);
-  const float f = __builtin_amdgcn_exp2f(m_ref - M);
-#pragma unroll
-  for (int w = 0; w < WAVES; ++w) {
-    if (wave == w) {
-#pragma unroll
-      for (int q = 0; q < 8; ++q)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            const int beta = 64 * q + 16 * g4 + 4 * rr + r;
-            const float v = acc[q][r][rr] * f;
-            if (w == 0) sm_o[li][beta] = v;
-            else sm_o[li][beta] += v;
-          }
-    }
-    __syncthreads();
-  }
-  const float oscale = SPARSE ? a.kv_scale : 1.0f;
+  const int32_t h = 16 * hg + li;
   const int32_t S = a.max_splits;
-  for (int idx = tid; idx < nh * kLatent; idx += NT) {
-    const int j = idx / kLatent, c = idx % kLatent;  // c: the latent dim written (FINAL), or byte (partial)
-    const int32_t h = 16 * hg + j;
-    float Mj = own ? sm_sn[j] : -INFINITY;
+  const float oscale = SPARSE ? a.kv_scale : 1.0f;
 #pragma unroll
-    for (int w = 0; w < WAVES; ++w) Mj = fmaxf(Mj, sm_m[w][j]);
-    float l = 0.0f;
+  for (int q = 0; q < 8; ++q) {
+    if (q / 2 != wave) continue;
+    f32x4_t v[4];
 #pragma unroll
-    for (int w = 0; w < WAVES; ++w) l += __builtin_amdgcn_exp2f(sm_m[w][j] - Mj) * sm_l[w][j];
-    const float e_own = own ? __builtin_amdgcn_exp2f(sm_sn[j] - Mj) : 0.0f;
-    l += e_own;
-    if constexpr (FINAL) {
-      const int beta = SPARSE ? latent_byte_of_dim(c) : c;
-      float o = sm_o[j][beta] * oscale;
-      if (own) o += e_own * sm_row[c];
-      a.out[((int64_t)b * a.H + h) * kLatent + c] = (uint16_t)f32_to_bf16_bits(o / l);
-      if (a.lse_out && c == 0) a.lse_out[(int64_t)b * a.H + h] = (Mj + __log2f(l)) * 0.6931471805599453f;
-    } else {
-      const int beta = c;
-      float o = sm_o[j][beta] * oscale;
-      if (own) o += e_own * sm_row[SPARSE ? latent_dim_of_byte(beta) : beta];
-      const int64_t row = ((int64_t)b * S + split) * a.H + h;
-      a.ws_o[row * kLatent + beta] = o;
-      if (beta == 0) {
-        a.ws_ml[row * 2] = Mj;
-        a.ws_ml[row * 2 + 1] = l;
+    for (int r = 0; r < 4; ++r) {
+      v[r] = acc[q][r] * f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        if (w == wave) continue;
+        const int idx = q < 2 * w ? q : q - 2;
+        const float4 t = sm_x[((w * 6 + idx) * 4 + r) * 64 + lane];
+        v[r][0] += t.x;
+        v[r][1] += t.y;
+        v[r][2] += t.z;
+        v[r][3] += t.w;
       }
+    }
+    if (li >= nh) continue;
+    // o[t]: latent byte 64 q + 16 g4 + t, t = 4 r' + r
+    float o[16];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) o[4 * rr + r] = v[r][rr] * oscale;
+    const int beta0 = 64 * q + 16 * g4;
+    // the 16 bytes' dims: ROWS576 beta0 + t; ROWS640 two runs of 8, base + i (t = 2 i) and base + 128 + i (t = 2 i + 1)
+    const int dim0 = SPARSE ? 256 * (beta0 >> 8) + ((beta0 & 255) >> 1) : beta0;
+    float run[2][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      run[0][i] = SPARSE ? o[2 * i] : o[i];
+      run[1][i] = SPARSE ? o[2 * i + 1] : o[8 + i];
+    }
+    const int run_off = SPARSE ? 128 : 8;
+    if constexpr (FINAL) {
+      const float inv = 1.0f / L;
+      uint16_t* dst = a.out + ((int64_t)b * a.H + h) * kLatent + dim0;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        uint32_t pk[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pk[i] = pack_bf16x2(run[u][2 * i] * inv, run[u][2 * i + 1] * inv);
+        *reinterpret_cast<uint4*>(dst + u * run_off) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+      }
+      if (a.lse_out && q == 0 && g4 == 0) a.lse_out[(int64_t)b * a.H + h] = (M + __log2f(L)) * 0.6931471805599453f;
+    } else {
+      const int64_t row = ((int64_t)b * S + split) * a.H + h;
+      float* dst = a.ws_o + row * kLatent + dim0;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        *reinterpret_cast<float4*>(dst + u * run_off) = make_float4(run[u][0], run[u][1], run[u][2], run[u][3]);
+        *reinterpret_cast<float4*>(dst + u * run_off + 4) = make_float4(run[u][4], run[u][5], run[u][6], run[u][7]);
+      }
+      if (q == 0 && g4 == 0) *reinterpret_cast<float2*>(a.ws_ml + row * 2) = make_float2(M, L);
     }
   }
 }
 
-// Merge of a row's splits per (row, head): out = sum_s e_s o_s / sum_s e_s l_s, lse = M + log(sum), with
-// e_s = exp2(m_s - M) formed once per head in LDS.
+// Merge of a row's splits, one wave per (row, head): out = sum_s e_s o_s / sum_s e_s l_s, lse = M + log(sum), with
+// e_s = exp2(m_s - M); lane s holds split s's weight and lane i the latent dims 8 i .. 8 i + 7.
 template <int FMT>
-__global__ __launch_bounds__(128) void mla_combine_kernel(MlaArgs a) {
+__global__ __launch_bounds__(64) void mla_combine_kernel(MlaArgs a) {
   constexpr bool SPARSE = FMT == ROWS640;
-  const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
   const int32_t n = min(SPARSE ? splits_of<16>(a.n_indices + 1, 0, a.split_tiles)
                                : splits_of<16>(ld_const(a.seq_lens + b), 0, a.split_tiles),
                         a.max_splits);
-  __shared__ float sm_w[kMaxSplits];
-  __shared__ float sm_l[kMaxSplits];
-  __shared__ float sm_inv, sm_lse;
+  if (n == 0) return;  // a row with no prior key: the lone-row kernel writes it
   const int64_t row0 = (int64_t)b * a.max_splits * a.H + h;
-  for (int s = tid; s < n; s += blockDim.x) {
-    const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + (row0 + (int64_t)s * a.H) * 2);
-    sm_w[s] = ml.x;
-    sm_l[s] = ml.y;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float M = -INFINITY;
-    for (int32_t s = 0; s < n; ++s) M = fmaxf(M, sm_w[s]);
-    float den = 0.0f;
-    for (int32_t s = 0; s < n; ++s) {
-      const float w = __builtin_amdgcn_exp2f(sm_w[s] - M);
-      sm_w[s] = w;
-      den += w * sm_l[s];
+  const float* ob = a.ws_o + row0 * kLatent + 8 * lane;
+  const int64_t sstride = (int64_t)a.H * kLatent;
+  constexpr int PRE = 8;  // splits whose partials load before the weights are known
+  float4 pre[PRE][2];
+#pragma unroll
+  for (int s = 0; s < PRE; ++s) {
+    if (s < n) {
+      pre[s][0] = *reinterpret_cast<const float4*>(ob + s * sstride);
+      pre[s][1] = *reinterpret_cast<const float4*>(ob + s * sstride + 4);
     }
-    sm_inv = 1.0f / den;
-    sm_lse = (M + __log2f(den)) * 0.6931471805599453f;
   }
-  __syncthreads();
-  const float* ob = a.ws_o + row0 * kLatent;
-  for (int c = tid; c < kLatent; c += blockDim.x) {
-    const int beta = SPARSE ? latent_byte_of_dim(c) : c;
-    float num = 0.0f;
-#pragma unroll 8
-    for (int32_t s = 0; s < n; ++s) num += sm_w[s] * ob[(int64_t)s * a.H * kLatent + beta];
-    a.out[((int64_t)b * a.H + h) * kLatent + c] = (uint16_t)f32_to_bf16_bits(num * sm_inv);
+  float m = -INFINITY, l = 0.0f;
+  if (lane < n) {
+    const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + (row0 + (int64_t)lane * a.H) * 2);
+    m = ml.x;
+    l = ml.y;
   }
-  if (a.lse_out && tid == 0) a.lse_out[(int64_t)b * a.H + h] = sm_lse;
+  const float M = wave_max(m);
+  const float e = lane < n ? __builtin_amdgcn_exp2f(m - M) : 0.0f;
+  const float den = wave_sum(e * l);
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < PRE; ++s) {
+    if (s < n) {
+      const float es = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), s));
+      o[0] += es * pre[s][0].x, o[1] += es * pre[s][0].y, o[2] += es * pre[s][0].z, o[3] += es * pre[s][0].w;
+      o[4] += es * pre[s][1].x, o[5] += es * pre[s][1].y, o[6] += es * pre[s][1].z, o[7] += es * pre[s][1].w;
+    }
+  }
+  for (int32_t s = PRE; s < n; ++s) {
+    const float es = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), s));
+    const float4 x0 = *reinterpret_cast<const float4*>(ob + s * sstride);
+    const float4 x1 = *reinterpret_cast<const float4*>(ob + s * sstride + 4);
+    o[0] += es * x0.x, o[1] += es * x0.y, o[2] += es * x0.z, o[3] += es * x0.w;
+    o[4] += es * x1.x, o[5] += es * x1.y, o[6] += es * x1.z, o[7] += es * x1.w;
+  }
+  const float inv = 1.0f / den;
+  uint32_t pk[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) pk[i] = pack_bf16x2(o[2 * i] * inv, o[2 * i + 1] * inv);
+  *reinterpret_cast<uint4*>(a.out + ((int64_t)b * a.H + h) * kLatent + 8 * lane) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  if (a.lse_out && lane == 0) a.lse_out[(int64_t)b * a.H + h] = (M + __log2f(den)) * 0.6931471805599453f;
 }
 
 // A row with no prior key (paged seq_len 1, or an empty index list): the output is its own row's latent.
@@ -610,17 +756,27 @@ __global__ __launch_bounds__(256) void mla_lone_row_kernel(MlaArgs a) {
 
 template <int FMT>
 static void launch_mla(const MlaArgs& a, int32_t groups, int32_t grid_x, bool any_lone, hipStream_t s) {
-  timing_mark(0, s);
+  hipEvent_t t0, t1;
   if (grid_x > 0) {
-    if (a.max_splits <= 1)
-      hipLaunchKernelGGL((mla_decode_kernel<FMT, 4, true>), dim3(grid_x, groups), dim3(256), 0, s, a);
-    else
-      hipLaunchKernelGGL((mla_decode_kernel<FMT, 4, false>), dim3(grid_x, groups), dim3(256), 0, s, a);
+    timing_events(0, &t0, &t1);
+    const dim3 grid(grid_x, groups);
+    // only a sparse pool can take the 64-bit kernel (W is false for the paged format)
+    constexpr bool W = FMT == ROWS640;
+    const bool wide = W && a.num_blocks * a.P * (int64_t)RowFmt<FMT>::kRowBytes > 0xffffffffll;
+    if (a.max_splits <= 1) {
+      if (wide) hipExtLaunchKernelGGL((mla_decode_kernel<FMT, 4, true, W>), grid, dim3(256), 0, s, t0, t1, 0, a);
+      else hipExtLaunchKernelGGL((mla_decode_kernel<FMT, 4, true, false>), grid, dim3(256), 0, s, t0, t1, 0, a);
+    } else {
+      if (wide) hipExtLaunchKernelGGL((mla_decode_kernel<FMT, 4, false, W>), grid, dim3(256), 0, s, t0, t1, 0, a);
+      else hipExtLaunchKernelGGL((mla_decode_kernel<FMT, 4, false, false>), grid, dim3(256), 0, s, t0, t1, 0, a);
+    }
   }
-  timing_mark(1, s);
-  if (a.max_splits > 1) hipLaunchKernelGGL((mla_combine_kernel<FMT>), dim3(a.B, a.H), dim3(128), 0, s, a);
+  if (a.max_splits > 1) {
+    timing_events(1, &t0, &t1);
+    hipExtLaunchKernelGGL((mla_combine_kernel<FMT>), dim3(a.B, a.H), dim3(64), 0, s, t0, t1, 0, a);
+  }
   if (any_lone) hipLaunchKernelGGL((mla_lone_row_kernel<FMT>), dim3(a.B, groups), dim3(256), 0, s, a);
-  timing_mark(2, s);
+  timing_end_call();
 }
 
 static int check_plan(const sna_split_plan* plan, int32_t B, const char* what) {

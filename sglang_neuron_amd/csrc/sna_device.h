@@ -98,6 +98,17 @@ __device__ __forceinline__ void fp8x4_to_bf16x4(uint32_t w, uint32_t& lo, uint32
   hi = __builtin_bit_cast(uint32_t, b);
 }
 
+// Buffer loads straight into LDS (lane i's bytes land at d + size * i), through a buffer resource: a uniform base and
+// size in SGPRs and a 32-bit offset per lane. Reads past the resource's size return zeros. Kept in helpers: the
+// builtin written inside a kernel template's body has cost the template its host-side launch stub.
+typedef __attribute__((address_space(3))) void lds_ptr_t;
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t r, lds_ptr_t* d, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, d, 16, voff, 0, 0, 0);
+}
+__device__ __forceinline__ void buffer_load_lds4(__amdgpu_buffer_rsrc_t r, lds_ptr_t* d, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, d, 4, voff, 0, 0, 0);
+}
+
 // 4x4 byte transpose with v_perm_b32 (its 8 source bytes are {S1 bytes 0-3, S0 bytes 0-3} for selector values 0-7):
 // byte r of w[e] becomes byte e of x[r].
 __device__ __forceinline__ void transpose4x4_bytes(const uint32_t (&w)[4], uint32_t (&x)[4]) {

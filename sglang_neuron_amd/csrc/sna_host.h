@@ -1,6 +1,7 @@
 // Host-side helpers of the C ABI: the thread-local error message, argument checks and launch checks.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdint.h>
@@ -35,8 +36,11 @@ inline int check_launch(const char* what) {
 
 inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
-// Diagnostics timer (capi.hip): when sna_diag_kernel_timing(1) has switched it on, a decode launcher records an event
-// before its split-K kernel (phase 0), between it and the combine pass (phase 1) and after the combine (phase 2).
-void timing_mark(int phase, hipStream_t s);
+// Diagnostics timer (capi.hip). When sna_diag_kernel_timing(1) has switched it on, timing_events hands a decode
+// launcher the start/stop events of its split-K kernel (phase 0) or its combine kernel (phase 1), and the launcher
+// passes them to hipExtLaunchKernelGGL, so the dispatch packet itself stamps them: no marker packet sits between
+// the kernels. Both events are null when the timer is off. timing_end_call closes the launcher's call.
+void timing_events(int phase, hipEvent_t* start, hipEvent_t* stop);
+void timing_end_call();
 
 }  // namespace sna

@@ -33,6 +33,12 @@ HIP_FLAGS = [
 ]
 
 
+# Per-source additions. decode_mla.hip: MFMA accumulators in VGPRs. Its split-K kernel holds 128 fp32 accumulators per
+# lane and rescales them in the online softmax; with the accumulators in AGPRs the compiler copies the whole set
+# between register files around that (rare) rescale branch on every tile.
+EXTRA_FLAGS = {"decode_mla.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and os.path.exists(cand):
@@ -46,7 +52,7 @@ def sources() -> list[Path]:
 
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIP_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}\n{res.stderr}")

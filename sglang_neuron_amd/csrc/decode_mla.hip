@@ -154,17 +154,11 @@ struct TileGeo {
   static constexpr int TAIL = 16 * STRIDE - 64 * (NDMA - 1);    // active lanes of the last DMA
   static constexpr int SCALES = 16 * RS;                        // offset of the 16 per-token scales (ROWS576)
   static constexpr int SLOT = 16 * RS + 64;                     // bytes of one ring slot
-  static constexpr int DEPTH = FMT == ROWS576 ? 4 : 3;          // ring slots per wave
+  static constexpr int DEPTH = 3;                               // ring slots per wave
 };
 
 // Dword 3 of a raw buffer resource on gfx9-family chips (no format conversion, no swizzle).
 constexpr int kBufferFlags = 0x00020000;
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -196,9 +190,6 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
   constexpr int ROWB = RowFmt<FMT>::kRowBytes;
   constexpr bool SPARSE = FMT == ROWS640;
   constexpr int NT = 64 * WAVES;
-  // VMEM operations one tile issues: its DMAs, plus the per-token scale DMA of the paged format
-  constexpr int PER_TILE = NDMA + (SPARSE ? 0 : 1);
-  static_assert((DEPTH - 1) * PER_TILE < 64, "vmcnt range");
   static_assert(WAVES == 4, "the merge splits the 8 latent blocks over 4 waves");
   typedef __attribute__((address_space(3))) void lds_void;
   typedef __attribute__((address_space(3))) uint8_t lds_u8;
@@ -218,8 +209,10 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
   __shared__ float sm_m[WAVES][16];
   __shared__ float sm_l[WAVES][16];
   __shared__ __attribute__((aligned(16))) uint16_t sm_own[576];  // the own row (bf16), DMA'd during the prologue
-  static_assert(sizeof(float4) * WAVES * 6 * 4 * 64 <= sizeof(sm_ring), "the merge exchange lives in the ring");
-  float4* sm_x = reinterpret_cast<float4*>(&sm_ring[0][0][0]);
+  __shared__ uint4 sm_q[18][64];
+  // The merge exchange: block idx < 6 of sender w, 256 float4.
+  static_assert(sizeof(float4) * WAVES * 6 * 256 <= sizeof(sm_ring), "the merge exchange lives in the ring");
+  auto xchg = [&](int w, int idx) -> float4* { return reinterpret_cast<float4*>(&sm_ring[0][0][0]) + (w * 6 + idx) * 256; };
 
   // Paged: keys are positions [0, seq_len - 1). Sparse: keys are index-list entries [0, n_indices), modelled as a
   // "sequence" of n_indices + 1 so the same decomposition applies (every row has the same split count).
@@ -253,38 +246,34 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
     if (col0 + lane < col_end) pg0 = trow[col0 + lane];
     if (col0 + 64 + lane < col_end) pg1 = trow[col0 + 64 + lane];
   }
-  uint32_t qv[18][4];
-  {
-    const int32_t h = min(16 * hg + li, a.H - 1);  // lanes of absent heads read a real head; their results are dropped
+  // The query operand of every QK step, in lane order: sm_q[s][lane] holds the 8 bf16 lane (g4, li) feeds in step s
+  // (head li). ROWS576: step pair k is chunk 4 k + g4 = dims 16 (4 k + g4) .. + 15 (rope for k = 8). ROWS640: steps
+  // 0, 1 are rope chunk 4 s + g4 (dims 8 (4 s + g4) .. + 7); step pair k > 0 is latent chunk m = 4 (k - 1) + g4,
+  // whose byte 2 i + bb holds dim 256 a + 128 bb + p0 + i.
+  for (int e = tid; e < 18 * 64; e += NT) {
+    const int s = e >> 6, ln = e & 63, eg4 = ln >> 4;
+    const int32_t h = min(16 * hg + (ln & 15), a.H - 1);  // absent heads read a real head; their results are dropped
     const uint16_t* qlp = a.ql + ((int64_t)b * a.H + h) * kLatent;
     const uint16_t* qpp = a.qpe + ((int64_t)b * a.H + h) * kRope;
+    uint4 w;
     if constexpr (FMT == ROWS576) {
-#pragma unroll
-      for (int k = 0; k < 9; ++k) {
-        const int d = 16 * (4 * k + g4);  // chunk 4 k + g4 = dims d .. d + 15: latent for k < 8, rope for k = 8
-        const uint16_t* src = k < 8 ? qlp + d : qpp + (d - kLatent);
-        const uint4 x = ld16(src), y = ld16(src + 8);
-        qv[2 * k][0] = x.x, qv[2 * k][1] = x.y, qv[2 * k][2] = x.z, qv[2 * k][3] = x.w;
-        qv[2 * k + 1][0] = y.x, qv[2 * k + 1][1] = y.y, qv[2 * k + 1][2] = y.z, qv[2 * k + 1][3] = y.w;
-      }
+      const int d = 16 * (4 * (s >> 1) + eg4) + 8 * (s & 1);
+      w = d < kLatent ? ld16(qlp + d) : ld16(qpp + (d - kLatent));
+    } else if (s < 2) {
+      w = ld16(qpp + 8 * (4 * s + eg4));
     } else {
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {  // rope chunk 4 s + g4: dims 8 (4 s + g4) .. + 7, bf16 on both sides
-        const uint4 x = ld16(qpp + 8 * (4 * s + g4));
-        qv[s][0] = x.x, qv[s][1] = x.y, qv[s][2] = x.z, qv[s][3] = x.w;
-      }
-#pragma unroll
-      for (int k = 1; k < 9; ++k) {
-        // latent chunk m = 4 (k - 1) + g4: bytes 16 m .. 16 m + 15 = dims 256 a + 128 bb + p0 + i, byte 2 i + bb
-        const int m = 4 * (k - 1) + g4;
-        const int a0 = (16 * m) >> 8, p0 = ((16 * m) & 255) >> 1;
-        const uint4 x = ld16(qlp + 256 * a0 + p0), y = ld16(qlp + 256 * a0 + 128 + p0);
-        interleave_pairs(x.x, y.x, qv[2 * k][0], qv[2 * k][1]);
-        interleave_pairs(x.y, y.y, qv[2 * k][2], qv[2 * k][3]);
-        interleave_pairs(x.z, y.z, qv[2 * k + 1][0], qv[2 * k + 1][1]);
-        interleave_pairs(x.w, y.w, qv[2 * k + 1][2], qv[2 * k + 1][3]);
+      const int m = 4 * ((s >> 1) - 1) + eg4;
+      const int a0 = (16 * m) >> 8, p0 = ((16 * m) & 255) >> 1;
+      const uint4 x = ld16(qlp + 256 * a0 + p0), y = ld16(qlp + 256 * a0 + 128 + p0);
+      if (s & 1) {
+        interleave_pairs(x.z, y.z, w.x, w.y);
+        interleave_pairs(x.w, y.w, w.z, w.w);
+      } else {
+        interleave_pairs(x.x, y.x, w.x, w.y);
+        interleave_pairs(x.y, y.y, w.z, w.w);
       }
     }
+    sm_q[s][ln] = w;
   }
   // The own row is attended by one wave of the row's first split, after its tiles: the wave with the fewest.
   const int32_t ntiles = t_last - t_first;
@@ -292,10 +281,9 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
   // Its bytes land in LDS while the tiles stream: issued first, they are complete once the first tile's are.
   if (own_wave) {
     const uint8_t* src = reinterpret_cast<const uint8_t*>(a.own + (int64_t)b * 576);
-    __builtin_amdgcn_global_load_lds((const void*)(src + 16u * (uint32_t)lane), (lds_void*)&sm_own[0], 16, 0, 0);
-    if (lane < 8)
-      __builtin_amdgcn_global_load_lds((const void*)(src + 1024u + 16u * (uint32_t)lane), (lds_void*)&sm_own[512], 16,
-                                       0, 0);
+    const uint32_t dst = lds_address((lds_void*)(lds_u8*)&sm_own[0]);
+    dma_global16(src + 16u * (uint32_t)lane, dst);
+    if (lane < 8) dma_global16(src + 1024u + 16u * (uint32_t)lane, dst + 1024);
   }
 
   // Sparse: every index of the split to a row id (-1: skipped), all loads of a stage in flight together.
@@ -332,6 +320,8 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
 
   // Each lane's source chunk for every DMA of a tile: LDS chunk o = 64 j + lane is chunk o % STRIDE of row
   // o / STRIDE (the pad chunk repeats the row's last chunk; rows past the tile only occur on switched-off lanes).
+  if constexpr (!SPARSE) __syncthreads();  // sm_q complete (the sparse row ids' barrier covers it there)
+
   // Offsets are 32-bit against a uniform base, so the DMAs take the scalar-base + vector-offset address form.
   uint32_t dma_src[NDMA];
 #pragma unroll
@@ -366,8 +356,7 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
   // sparse rows of a pool past 4 GiB take 64-bit addresses instead.
   const __amdgpu_buffer_rsrc_t pool_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)a.cache, (short)0, WIDE ? 0 : (int)(uint32_t)(a.num_blocks * a.P * ROWB), kBufferFlags);
-  auto issue = [&](lds_void* dst, int32_t tile) {
-    lds_u8* d = (lds_u8*)dst;
+  auto issue = [&](uint32_t d, int32_t tile) {  // d: the slot's LDS address
     if constexpr (SPARSE) {
       const int32_t k0 = tile * 16 - kbase;
 #pragma unroll
@@ -375,10 +364,9 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
         const int32_t row = max(sm_rowid[k0 + (int32_t)(dma_src[j] >> 16)], 0);
         if (j < NDMA - 1 || lane < Geo::TAIL) {
           if constexpr (!WIDE)
-            buffer_load_lds16(pool_rsrc, (lds_void*)(d + 1024 * j), (uint32_t)row * ROWB + (dma_src[j] & 0xffffu));
+            dma_buffer16(pool_rsrc, d + 1024 * j, (uint32_t)row * ROWB + (dma_src[j] & 0xffffu));
           else
-            __builtin_amdgcn_global_load_lds((const void*)(a.cache + (int64_t)row * ROWB + (dma_src[j] & 0xffffu)),
-                                             (lds_void*)(d + 1024 * j), 16, 0, 0);
+            dma_global16(a.cache + (int64_t)row * ROWB + (dma_src[j] & 0xffffu), d + 1024 * j);
         }
       }
     } else {
@@ -389,12 +377,12 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
 #pragma unroll
       for (int j = 0; j < NDMA; ++j)
         if (j < NDMA - 1 || lane < Geo::TAIL)
-          buffer_load_lds16(rk, (lds_void*)(d + 1024 * j), dma_src[j]);
+          dma_buffer16(rk, d + 1024 * j, dma_src[j]);
       // the tile's 16 per-token scales, consecutive like its rows
       const __amdgpu_buffer_rsrc_t rs =
           __builtin_amdgcn_make_buffer_rsrc((void*)(a.row_scale + row0), (short)0, 64, kBufferFlags);
       if (lane < 16)
-        buffer_load_lds4(rs, (lds_void*)(d + Geo::SCALES), 4u * (uint32_t)lane);
+        dma_buffer4(rs, d + Geo::SCALES, 4u * (uint32_t)lane);
     }
   };
 
@@ -407,9 +395,18 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[q][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // PV of one tile: O^T += V^T P^T over 32 d-tiles. A masked key's bytes may be anything (a stale NaN would survive
-  // p = 0), so a tile with masked keys zeroes them.
-  auto pv = [&](const uint8_t* T, const uint32_t (&pop)[2], uint32_t vmask, auto masked) {
+  // A masked key's latent bytes may be anything, and a stale NaN or Inf would survive p = 0 in PV: a tile with masked
+  // keys has their latent bytes zeroed in LDS first (its scores and scales are masked by selects).
+  auto sanitize = [&](uint8_t* T, uint32_t vmask) {
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int idx = lane + 64 * it, r = idx >> 5, c = idx & 31;
+      if (!((vmask >> r) & 1u))
+        *reinterpret_cast<uint4*>(T + r * RS + (SPARSE ? 128 : 0) + 16 * c) = make_uint4(0, 0, 0, 0);
+    }
+  };
+  // PV of one tile: O^T += V^T P^T over 32 d-tiles.
+  auto pv = [&](const uint8_t* T, const uint32_t (&pop)[2]) {
     const uint8_t* Tv = T + 4 * g4 * RS + 4 * li + (SPARSE ? 128 : 0);
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
@@ -417,7 +414,6 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         w[e] = *reinterpret_cast<const uint32_t*>(Tv + e * RS + 64 * q);
-        if constexpr (decltype(masked)::value) w[e] = ((vmask >> (4 * g4 + e)) & 1u) ? w[e] : 0u;
       }
       uint32_t xr[4];
       transpose4x4_bytes(w, xr);
@@ -430,12 +426,18 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
     }
   };
 
-  auto compute = [&](const uint8_t* T, uint32_t vmask) {
-    float ks[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-    if constexpr (!SPARSE) {  // scales of keys 4 g4 .. 4 g4 + 3
+  // Per-token scales of keys 4 g4 .. 4 g4 + 3 of the tile at T (1 for the sparse format).
+  auto key_scales = [&](const uint8_t* T, float (&ks)[4]) {
+    ks[0] = ks[1] = ks[2] = ks[3] = 1.0f;
+    if constexpr (!SPARSE) {
       const float4 s4 = *reinterpret_cast<const float4*>(T + Geo::SCALES + 16 * g4);
       ks[0] = s4.x, ks[1] = s4.y, ks[2] = s4.z, ks[3] = s4.w;
     }
+  };
+  // The tile's scores in the log2 domain (x[r]: key 4 g4 + r, head li; -inf when masked) and their maximum per head.
+  auto scores = [&](const uint8_t* T, uint32_t vmask, float (&x)[4], float& tmax) {
+    float ks[4];
+    [[clang::always_inline]] key_scales(T, ks);
     // S^T = K Q^T: three accumulators keep three independent MFMA chains in flight
     const uint8_t* Tq = T + li * RS + 16 * g4;
     f32x4_t scp[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
@@ -448,8 +450,10 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
           const uint4 w0 = *reinterpret_cast<const uint4*>(Tq);
           const uint4 w1 = *reinterpret_cast<const uint4*>(Tq + 64);
           const uint32_t a0[4] = {w0.x, w0.y, w0.z, w0.w}, a1[4] = {w1.x, w1.y, w1.z, w1.w};
-          sc = mfma_16x16x32_bf16(a0, qv[0], sc);
-          sc = mfma_16x16x32_bf16(a1, qv[1], sc);
+          const uint4 q0 = sm_q[0][lane], q1 = sm_q[1][lane];
+          const uint32_t b0[4] = {q0.x, q0.y, q0.z, q0.w}, b1[4] = {q1.x, q1.y, q1.z, q1.w};
+          sc = mfma_16x16x32_bf16(a0, b0, sc);
+          sc = mfma_16x16x32_bf16(a1, b1, sc);
           continue;
         }
       }
@@ -459,31 +463,40 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
       fp8x4_to_bf16x4(w.y, op0[2], op0[3]);
       fp8x4_to_bf16x4(w.z, op1[0], op1[1]);
       fp8x4_to_bf16x4(w.w, op1[2], op1[3]);
-      sc = mfma_16x16x32_bf16(op0, qv[2 * k], sc);
-      sc = mfma_16x16x32_bf16(op1, qv[2 * k + 1], sc);
+      const uint4 q0 = sm_q[2 * k][lane], q1 = sm_q[2 * k + 1][lane];
+      const uint32_t b0[4] = {q0.x, q0.y, q0.z, q0.w}, b1[4] = {q1.x, q1.y, q1.z, q1.w};
+      sc = mfma_16x16x32_bf16(op0, b0, sc);
+      sc = mfma_16x16x32_bf16(op1, b1, sc);
     }
     const f32x4_t sc = scp[0] + scp[1] + scp[2];
-    // mask, online softmax with a lazily moved reference maximum
-    float x[4];
-    float tmax = -INFINITY;
+    tmax = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const bool ok = (vmask >> (4 * g4 + r)) & 1u;
-      x[r] = ok ? sc[r] * base_scale * (SPARSE ? 1.0f : ks[r]) : -INFINITY;
+      x[r] = ok ? sc[r] * base_scale * ks[r] : -INFINITY;
       tmax = fmaxf(tmax, x[r]);
     }
     tmax = max_across_groups(tmax);
-    const bool bump = tmax > m_ref + kMlaRescaleSlack;
-    if (__any(bump)) {
-      const float m_new = bump ? tmax : m_ref;
-      const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new);
-      m_ref = m_new;
-      l_run *= alpha;
+  };
+  // Online softmax with a lazily moved reference maximum m_ref: a head moves it only when a tile's maximum passes it
+  // by more than the slack (the probabilities stay below 2^slack), and then the accumulators are rescaled.
+  auto needs_rescale = [&](float tmax) { return __any(tmax > m_ref + kMlaRescaleSlack); };
+  auto rescale = [&](float tmax) {
+    asm volatile("" ::: "memory");  // keeps the branch a branch: the compiler must not run the 128 multiplies always
+    const float m_new = tmax > m_ref + kMlaRescaleSlack ? tmax : m_ref;
+    const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new);
+    m_ref = m_new;
+    l_run *= alpha;
 #pragma unroll
-      for (int q = 0; q < 8; ++q)
+    for (int q = 0; q < 8; ++q)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[q][r] *= alpha;
-    }
+      for (int r = 0; r < 4; ++r) acc[q][r] *= alpha;
+  };
+  // The tile's probabilities against m_ref, folded into the row sum and, through PV, the accumulators.
+  auto accumulate = [&](uint8_t* T, uint32_t vmask, const float (&x)[4]) {
+    if (vmask != 0xffffu) [[clang::always_inline]] sanitize(T, vmask);
+    float ks[4];
+    [[clang::always_inline]] key_scales(T, ks);
     float pw[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -491,43 +504,67 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
       const float p = __builtin_amdgcn_exp2f(x[r] - m_ref);
       l_run += p;
       // V is dequantized through P: p' = p * scale(key); a masked key has p = 0
-      pw[r] = ok ? p * (SPARSE ? 1.0f : ks[r]) : 0.0f;
+      pw[r] = ok ? p * ks[r] : 0.0f;
     }
     const uint32_t pop[2] = {pack_bf16x2(pw[0], pw[1]), pack_bf16x2(pw[2], pw[3])};
-    if (vmask == 0xffffu) pv(T, pop, vmask, std::false_type{});
-    else pv(T, pop, vmask, std::true_type{});
+    [[clang::always_inline]] pv(T, pop);
   };
 
   // ---- the tile loop: wave w takes tiles t_first + w + WAVES i through its ring of DEPTH slots; DEPTH - 1 tiles'
   // loads are in flight while one computes ----
   {
+    // VMEM operations one tile issues: its DMAs, plus the per-token scale DMA of the paged format
+    constexpr int PER_TILE = NDMA + (SPARSE ? 0 : 1);
+    static_assert((DEPTH - 1) * PER_TILE < 64, "vmcnt range");
     const int32_t t0 = t_first + wave;
     const int32_t mine = t0 < t_last ? (t_last - t0 + WAVES - 1) / WAVES : 0;
-    uint8_t* ring = &sm_ring[wave][0][0];
-    lds_u8* ring_lds = (lds_u8*)(&sm_ring[wave][0][0]);
+    const uint32_t ring = lds_address((lds_void*)(lds_u8*)&sm_ring[wave][0][0]);
+    // The compiler's own loads (block table, query, indices) complete here, in a wait it sees (vmcnt(0): encoded
+    // vmcnt 0, expcnt 7, lgkmcnt 15), before any DMA is in flight; otherwise it could wait for them again inside the
+    // loop, and such a wait would drain the DMAs.
+    __builtin_amdgcn_s_waitcnt(0x0f70);
 #pragma unroll
     for (int i = 0; i < DEPTH - 1; ++i)
-      if (i < mine) issue((lds_void*)(ring_lds + i * SLOT), t0 + i * WAVES);
+      if (i < mine) issue(ring + i * SLOT, t0 + i * WAVES);
+    // The rare rescale sits outside the inner loop, so inside it the accumulators are only ever MFMA operands and
+    // keep their registers: a tile whose scores need a rescale leaves the loop before its PV and re-enters after it.
     int slot = 0;
-    for (int32_t i = 0; i < mine; ++i) {
-      // issue tile i + DEPTH - 1, then wait until tile i's loads have landed: those issued after it may stay in flight
-      const int32_t ahead = mine - 1 - i;  // tiles after this one
-      if (ahead >= DEPTH - 1) {
-        const int nslot = slot == 0 ? DEPTH - 1 : slot - 1;  // (slot + DEPTH - 1) % DEPTH
-        issue((lds_void*)(ring_lds + nslot * SLOT), t0 + (i + DEPTH - 1) * WAVES);
-        wait_vmcnt<(DEPTH - 1) * PER_TILE>();
-      } else if (DEPTH > 2 && ahead == DEPTH - 2) {
-        wait_vmcnt<(DEPTH > 2 ? DEPTH - 2 : 0) * PER_TILE>();
-      } else if (DEPTH > 3 && ahead == DEPTH - 3) {
-        wait_vmcnt<(DEPTH > 3 ? DEPTH - 3 : 0) * PER_TILE>();
-      } else {
-        wait_vmcnt<0>();
+    int32_t i = 0;
+    bool pending = false;
+    float x[4], tmax = -INFINITY;
+    uint32_t vm = 0;
+    while (true) {
+      for (; i < mine; ++i) {
+        uint8_t* T = &sm_ring[wave][slot][0];
+        if (!pending) {
+          // issue tile i + DEPTH - 1 into the slot tile i - 1 freed, then wait until tile i's loads have landed:
+          // the loads of the tiles after it may stay in flight
+          const int32_t ahead = mine - 1 - i;
+          if (ahead >= DEPTH - 1) {
+            issue(ring + (slot == 0 ? DEPTH - 1 : slot - 1) * SLOT, t0 + (i + DEPTH - 1) * WAVES);
+            wait_vmcnt<(DEPTH - 1) * PER_TILE>();
+          } else if (DEPTH > 3 && ahead == 2) {
+            wait_vmcnt<2 * PER_TILE>();
+          } else if (ahead == 1) {
+            wait_vmcnt<PER_TILE>();
+          } else {
+            wait_vmcnt<0>();
+          }
+          vm = tile_mask(t0 + i * WAVES);
+          [[clang::always_inline]] scores(T, vm, x, tmax);
+          if (needs_rescale(tmax)) {
+            pending = true;
+            break;
+          }
+        }
+        pending = false;
+        [[clang::always_inline]] accumulate(T, vm, x);
+        slot = slot == DEPTH - 1 ? 0 : slot + 1;
       }
-      const int32_t cur = t0 + i * WAVES;
-      compute(ring + slot * SLOT, tile_mask(cur));
-      slot = slot == DEPTH - 1 ? 0 : slot + 1;
+      if (!pending) break;
+      [[clang::always_inline]] rescale(tmax);
     }
-    wait_vmcnt<0>();
+    wait_vmcnt<0>();  // (the own row's DMA, for a wave without tiles)
   }
 
   // ---- the own row: quantized as the store quantizes it, written into slot 0 as key 0 of a one-key tile ----
@@ -586,7 +623,10 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
         }
       }
     }
-    compute(T, 1u);
+    float xo[4], to;
+    [[clang::always_inline]] scores(T, 1u, xo, to);
+    if (needs_rescale(to)) [[clang::always_inline]] rescale(to);
+    [[clang::always_inline]] accumulate(T, 1u, xo);
   }
 
   // ---- merge: a common maximum per head; wave w sums latent blocks 2 w, 2 w + 1 over the waves and writes them ----
@@ -611,7 +651,7 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const f32x4_t v = acc[q][r] * f;
-      sm_x[((wave * 6 + idx) * 4 + r) * 64 + lane] = make_float4(v[0], v[1], v[2], v[3]);
+      xchg(wave, idx)[r * 64 + lane] = make_float4(v[0], v[1], v[2], v[3]);
     }
   }
   __syncthreads();
@@ -629,7 +669,7 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
       for (int w = 0; w < WAVES; ++w) {
         if (w == wave) continue;
         const int idx = q < 2 * w ? q : q - 2;
-        const float4 t = sm_x[((w * 6 + idx) * 4 + r) * 64 + lane];
+        const float4 t = xchg(w, idx)[r * 64 + lane];
         v[r][0] += t.x;
         v[r][1] += t.y;
         v[r][2] += t.z;

@@ -98,15 +98,30 @@ __device__ __forceinline__ void fp8x4_to_bf16x4(uint32_t w, uint32_t& lo, uint32
   hi = __builtin_bit_cast(uint32_t, b);
 }
 
-// Buffer loads straight into LDS (lane i's bytes land at d + size * i), through a buffer resource: a uniform base and
-// size in SGPRs and a 32-bit offset per lane. Reads past the resource's size return zeros. Kept in helpers: the
-// builtin written inside a kernel template's body has cost the template its host-side launch stub.
+// Loads straight into LDS (lane i's bytes land at LDS address m0 + size * i), written as inline assembly so that the
+// compiler does not see them: it would otherwise drain every load in flight before any LDS read it cannot prove
+// disjoint from them. Callers wait for them with wait_vmcnt, counting every such load they issued after the one they
+// need. The buffer forms read through a buffer resource (a uniform base and size in SGPRs, a 32-bit offset per lane;
+// reads past the size return zeros). The s_nop covers the m0 write -> LDS-DMA hazard.
 typedef __attribute__((address_space(3))) void lds_ptr_t;
-__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t r, lds_ptr_t* d, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, d, 16, voff, 0, 0, 0);
+__device__ __forceinline__ uint32_t lds_address(const lds_ptr_t* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
 }
-__device__ __forceinline__ void buffer_load_lds4(__amdgpu_buffer_rsrc_t r, lds_ptr_t* d, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, d, 4, voff, 0, 0, 0);
+__device__ __forceinline__ void dma_buffer16(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(r)
+               : "memory");
+}
+__device__ __forceinline__ void dma_buffer4(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(r)
+               : "memory");
+}
+__device__ __forceinline__ void dma_global16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 // 4x4 byte transpose with v_perm_b32 (its 8 source bytes are {S1 bytes 0-3, S0 bytes 0-3} for selector values 0-7):

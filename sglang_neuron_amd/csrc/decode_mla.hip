@@ -250,7 +250,9 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
   // (head li). ROWS576: step pair k is chunk 4 k + g4 = dims 16 (4 k + g4) .. + 15 (rope for k = 8). ROWS640: steps
   // 0, 1 are rope chunk 4 s + g4 (dims 8 (4 s + g4) .. + 7); step pair k > 0 is latent chunk m = 4 (k - 1) + g4,
   // whose byte 2 i + bb holds dim 256 a + 128 bb + p0 + i.
-  for (int e = tid; e < 18 * 64; e += NT) {
+  // The paged format DMAs it in the tile loop's prologue, behind the first tiles' loads; the sparse format interleaves
+  // pairs and fills it here.
+  for (int e = tid; SPARSE && e < 18 * 64; e += NT) {
     const int s = e >> 6, ln = e & 63, eg4 = ln >> 4;
     const int32_t h = min(16 * hg + (ln & 15), a.H - 1);  // absent heads read a real head; their results are dropped
     const uint16_t* qlp = a.ql + ((int64_t)b * a.H + h) * kLatent;
@@ -320,8 +322,6 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
 
   // Each lane's source chunk for every DMA of a tile: LDS chunk o = 64 j + lane is chunk o % STRIDE of row
   // o / STRIDE (the pad chunk repeats the row's last chunk; rows past the tile only occur on switched-off lanes).
-  if constexpr (!SPARSE) __syncthreads();  // sm_q complete (the sparse row ids' barrier covers it there)
-
   // Offsets are 32-bit against a uniform base, so the DMAs take the scalar-base + vector-offset address form.
   uint32_t dma_src[NDMA];
 #pragma unroll
@@ -523,9 +523,27 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
     // vmcnt 0, expcnt 7, lgkmcnt 15), before any DMA is in flight; otherwise it could wait for them again inside the
     // loop, and such a wait would drain the DMAs.
     __builtin_amdgcn_s_waitcnt(0x0f70);
+    if constexpr (!SPARSE) {
+      // the query operand, step s by wave s % WAVES: sm_q[s][lane] = dims 16 (4 (s / 2) + g4) + 8 (s % 2) .. + 7
+      const int32_t h = min(16 * hg + li, a.H - 1);
+      const uint16_t* qlp = a.ql + ((int64_t)b * a.H + h) * kLatent;
+      const uint16_t* qpp = a.qpe + ((int64_t)b * a.H + h) * kRope;
+      for (int s = wave; s < 18; s += WAVES) {
+        const int d = 16 * (4 * (s >> 1) + g4) + 8 * (s & 1);
+        dma_global16(d < kLatent ? qlp + d : qpp + (d - kLatent), lds_address((lds_void*)(lds_u8*)&sm_q[s][0]));
+      }
+    }
 #pragma unroll
     for (int i = 0; i < DEPTH - 1; ++i)
       if (i < mine) issue(ring + i * SLOT, t0 + i * WAVES);
+    if constexpr (!SPARSE) {
+      // every wave's query DMAs have landed (the tiles' may stay in flight), then the operand is complete
+      static_assert(DEPTH == 3, "the waits below count two tiles");
+      if (mine >= 2) wait_vmcnt<2 * PER_TILE>();
+      else if (mine == 1) wait_vmcnt<PER_TILE>();
+      else wait_vmcnt<0>();
+      __syncthreads();
+    }
     // The rare rescale sits outside the inner loop, so inside it the accumulators are only ever MFMA operands and
     // keep their registers: a tile whose scores need a rescale leaves the loop before its PV and re-enters after it.
     int slot = 0;

@@ -38,6 +38,7 @@ METRIC = "decode-attn µs/step + achieved HBM GB/s (% of peak), FP8 KV, 1 MI355X
 PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0
 COLD_BYTES = 1 << 30  # rotate pool copies until the rotation spans this much (4x the Infinity Cache)
+COPY_CALIBRATION_BYTES = 1 << 30
 
 
 def log(msg: str) -> None:
@@ -363,6 +364,8 @@ def main() -> int:
     ap.add_argument("--all", action="store_true", help="one line per workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work for the baseline sample")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run one plain device copy of 1 GiB (the reference dispatch for HBM counter scaling)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -376,6 +379,13 @@ def main() -> int:
         return 2
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        src = torch.empty(COPY_CALIBRATION_BYTES, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        log(f"copy calibration: one copy of {COPY_CALIBRATION_BYTES} bytes (read) into as many (written)")
     keys = ["1", "2", "3", "4", "4swa", "5"] if args.all else [args.config]
     for k in keys:
         line = run_one(k, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)

@@ -33,10 +33,11 @@ HIP_FLAGS = [
 ]
 
 
-# Per-source additions. decode_mla.hip: MFMA accumulators in VGPRs. Its split-K kernel holds 128 fp32 accumulators per
-# lane and rescales them in the online softmax; with the accumulators in AGPRs the compiler copies the whole set
-# between register files around that (rare) rescale branch on every tile.
-EXTRA_FLAGS = {"decode_mla.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Per-source additions: MFMA accumulators in VGPRs for the split-K decode kernels. They rescale their accumulators in
+# the online softmax; with the accumulators in AGPRs the compiler copies them between the register files around that
+# (rare) rescale branch on every tile.
+_MFMA_VGPR = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+EXTRA_FLAGS = {"decode_mla.hip": _MFMA_VGPR, "decode_gqa.hip": _MFMA_VGPR}
 
 
 def hipcc() -> str:

@@ -1,0 +1,232 @@
+"""The attention backend: per-forward metadata from SGLang's ForwardBatch, and the decode forward on the HIP path.
+
+Mirrors sglang_neuron/attention/backend.py: ``NeuronForwardMetadata`` (:29-38) and ``NeuronAttnBackend`` (:41-148)
+with the same constructor, hooks and ``build_metadata`` / ``_block_table`` semantics. The reference leaves
+``forward_decode`` to its compiled graphs and raises (:147-148); here it runs: the step's new K/V (or MLA row) is
+stored at ``out_cache_loc`` when ``save_kv_cache`` is set and attended in-band, then the paged split-K decode runs
+over the pool, all on torch's current stream.
+
+Metadata conventions (attention/backend.py:5-8, :114-130): ``block_table[b, j] = req_to_token[row_b, j * page] //
+page`` (int32), -1 where ``j * page >= seq_len_b`` when the batch has more than one row; ``seq_lens`` count the new
+token; an idle batch gets a (0, 1) table. Padded rows use seq_len 1 (``get_cuda_graph_seq_len_fill_value``).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+import torch
+from torch import Tensor
+
+from .. import _lib, ops
+from ..mem_cache.memory_pool import NeuronDSATokenToKVPool, NeuronMHATokenToKVPool, NeuronMLATokenToKVPool
+
+
+@dataclass
+class NeuronForwardMetadata:
+    is_prefill: bool
+    batch_size: int  # real number of requests
+    num_tokens: int  # real number of tokens in this forward
+    block_table: Tensor  # [bs, max_blocks] int32 (CPU), -1 padded
+    slot_mapping: Tensor  # [num_tokens] int64 (CPU)
+    seq_lens: Tensor  # [bs] int64 (CPU) total lens (prefix + new)
+    positions: Tensor  # [num_tokens] int64 (CPU)
+    cached_seq_len: int = 0
+
+
+@dataclass
+class _DecodeState:
+    """The device copies and split-K plans of one decode forward, shared by its layers."""
+    meta: NeuronForwardMetadata
+    table: Tensor  # [bs, max_blocks] int32, device
+    seq_lens: Tensor  # [bs] int32, device
+    slots: Tensor  # [bs] int64, device
+    positions: Tensor  # [bs] int32, device
+    plans: dict
+
+
+class NeuronAttnBackend:
+    """The attention backend of the HIP decode path. ``model_runner`` provides ``req_to_token_pool`` (with
+    ``req_to_token`` [rows, context] int32 on the host), ``token_to_kv_pool`` (one of this package's pools) and
+    ``page_size``."""
+
+    def __init__(self, model_runner):
+        self.model_runner = model_runner
+        self.req_to_token_pool = model_runner.req_to_token_pool
+        self.token_to_kv_pool = model_runner.token_to_kv_pool
+        self.page_size = int(model_runner.page_size)
+        self._r2t_view = None
+
+    # SGLang's hooks: the metadata's consumers build it themselves (attention/backend.py:56-76)
+    def init_forward_metadata(self, forward_batch):
+        return None
+
+    def init_forward_metadata_out_graph(self, forward_batch, in_capture: bool = False):
+        return None
+
+    def init_forward_metadata_in_graph(self, forward_batch):
+        return None
+
+    def init_cuda_graph_state(self, max_bs: int, max_num_tokens: int):
+        return None
+
+    def get_cpu_graph_seq_len_fill_value(self) -> int:
+        return self.get_cuda_graph_seq_len_fill_value()
+
+    def get_cuda_graph_seq_len_fill_value(self) -> int:
+        # padded (idle) rows: seq_len 1, so req_to_token[0, 0] (the reserved page) is read
+        return 1
+
+    def build_metadata(self, fb) -> NeuronForwardMetadata:
+        """Exact (unpadded) metadata from a ForwardBatch (attention/backend.py:78-112)."""
+        mode = fb.forward_mode
+        bs = getattr(fb, "_original_batch_size", None)
+        bs = int(bs) if bs is not None else int(fb.batch_size)
+        n_tok = getattr(fb, "_original_num_tokens", None)
+        n_tok = int(n_tok) if n_tok is not None else int(fb.out_cache_loc.shape[0])
+        req_pool_indices = fb.req_pool_indices.to("cpu", torch.long)[:bs]
+        seq_lens = (fb.seq_lens_cpu if getattr(fb, "seq_lens_cpu", None) is not None else fb.seq_lens).to(
+            "cpu", torch.long)[:bs]
+        out_cache_loc = fb.out_cache_loc.to("cpu", torch.long)[:n_tok]
+        positions = fb.positions.to("cpu", torch.long)[:n_tok]
+        is_prefill = mode.is_extend() if not mode.is_idle() else False
+        if mode.is_idle() or bs == 0:
+            return NeuronForwardMetadata(
+                is_prefill=False, batch_size=0, num_tokens=0, block_table=torch.full((0, 1), -1, dtype=torch.int32),
+                slot_mapping=torch.zeros((0,), dtype=torch.long), seq_lens=torch.zeros((0,), dtype=torch.long),
+                positions=positions[:0])
+        cached = int(fb.extend_prefix_lens[:bs].max()) if is_prefill else 0
+        return NeuronForwardMetadata(
+            is_prefill=is_prefill, batch_size=bs, num_tokens=int(out_cache_loc.shape[0]),
+            block_table=self._block_table(req_pool_indices, seq_lens, bs), slot_mapping=out_cache_loc,
+            seq_lens=seq_lens, positions=positions, cached_seq_len=cached)
+
+    def _block_table(self, req_pool_indices: Tensor, seq_lens: Tensor, bs: int) -> Tensor:
+        """[bs, max_blocks] int32: each row's page representatives over the page size, -1 past its pages
+        (attention/backend.py:114-130)."""
+        page = self.page_size
+        rows = req_pool_indices.numpy()
+        lens = seq_lens.numpy()
+        max_blocks = (int(lens.max()) + page - 1) // page
+        table = (self._req_to_token_np()[rows, : max_blocks * page : page] // page).astype(np.int32, copy=False)
+        if bs != 1:
+            live = np.arange(0, max_blocks * page, page) < lens[:, None]
+            table = np.where(live, table, np.int32(-1))
+        return torch.from_numpy(np.ascontiguousarray(table))
+
+    def _req_to_token_np(self) -> np.ndarray:
+        r2t = self.req_to_token_pool.req_to_token
+        view = self._r2t_view
+        if view is None or view[0] is not r2t or view[1] != r2t.data_ptr():
+            view = self._r2t_view = (r2t, r2t.data_ptr(), r2t.numpy())
+        return view[2]
+
+    # ---- decode ----
+    def _decode_state(self, fb, device: torch.device) -> _DecodeState:
+        st = getattr(fb, "_sna_decode_state", None)
+        if st is not None and st.table.device == device:
+            return st
+        meta = self.build_metadata(fb)
+        if meta.is_prefill:
+            raise NotImplementedError("forward_decode got an extend batch: this build runs the decode path only")
+        if meta.num_tokens != meta.batch_size:
+            raise ValueError(f"a decode batch has one new token per row ({meta.num_tokens} tokens, {meta.batch_size} "
+                             "rows)")
+        st = _DecodeState(meta=meta, table=meta.block_table.to(device), seq_lens=meta.seq_lens.to(device, torch.int32),
+                          slots=meta.slot_mapping.to(device), positions=meta.positions.to(device, torch.int32),
+                          plans={})
+        try:
+            fb._sna_decode_state = st
+        except AttributeError:
+            pass
+        return st
+
+    def forward_extend(self, q, k, v, layer, forward_batch, save_kv_cache=True, **kwargs):
+        raise NotImplementedError("this build runs the paged decode path only (prefill is out of its scope)")
+
+    def forward_decode(self, q: Tensor, k: Optional[Tensor], v: Optional[Tensor], layer, forward_batch,
+                       save_kv_cache: bool = True, **kwargs) -> Tensor:
+        """One decode step of ``layer``: the new K/V of every row stored at ``out_cache_loc`` (when ``save_kv_cache``)
+        and attended in-band, the history read from the pool through the block table.
+
+        GQA (MHA pool): q [bs, H * d] or [bs, H, d], k / v [bs, G * d] or [bs, G, d]; ``layer`` gives ``layer_id``,
+        ``tp_q_head_num``, ``tp_k_head_num``, ``head_dim``, ``scaling`` and optionally ``sliding_window_size`` (> 0:
+        a window of that many keys, the new one included) and ``sinks`` [H] (or the ``sinks`` keyword). Returns
+        [bs, H * d] bf16.
+
+        MLA (MLA pool): q [bs, H, 576] absorbed ([q_nope W_uk 512 | q_pe 64]), k the new compact rows [bs, 576]
+        ([latent | rope]); v is unused. Returns [bs, H * 512] bf16.
+
+        DSA (DSA pool): as MLA with k the new rows in [k_pe | latent] order and the ``topk_indices`` keyword [bs, K]
+        int32 (global positions, -1 empty). Returns [bs, H * 512] bf16; the LSE [bs, H] is kept in
+        ``self.last_lse``."""
+        if q.device.type != "cuda":
+            raise RuntimeError("forward_decode runs on the GPU (there is no CPU path)")
+        pool = self.token_to_kv_pool
+        st = self._decode_state(forward_batch, q.device)
+        bs = st.meta.batch_size
+        layer_id = int(layer.layer_id)
+        if isinstance(pool, NeuronMHATokenToKVPool):
+            return self._decode_gqa(q, k, v, layer, layer_id, st, bs, save_kv_cache, kwargs.get("sinks"))
+        if isinstance(pool, NeuronMLATokenToKVPool):
+            return self._decode_mla(q, k, layer, layer_id, st, bs, save_kv_cache)
+        if isinstance(pool, NeuronDSATokenToKVPool):
+            return self._decode_dsa(q, k, layer, layer_id, st, bs, save_kv_cache, kwargs.get("topk_indices"))
+        raise TypeError(f"unsupported KV pool {type(pool).__name__}")
+
+    def _decode_gqa(self, q, k, v, layer, layer_id, st, bs, save, sinks):
+        pool: NeuronMHATokenToKVPool = self.token_to_kv_pool
+        H, G = int(layer.tp_q_head_num), int(layer.tp_k_head_num)
+        d = int(getattr(layer, "head_dim", pool.head_dim))
+        if G != pool.head_num or d != pool.head_dim:
+            raise ValueError(f"layer {layer_id} has {G} KV heads of {d}, the pool {pool.head_num} of {pool.head_dim}")
+        window = getattr(layer, "sliding_window_size", None)
+        window = int(window) if window is not None and int(window) > 0 else 0
+        if sinks is None:
+            sinks = getattr(layer, "sinks", None)
+        key = ("gqa", window, G)
+        if key not in st.plans:
+            st.plans[key] = ops.plan_decode(_lib.KIND_GQA, bs, host_seq_lens=st.meta.seq_lens, window=window,
+                                            ctas_per_item=G, num_cus=ops._num_cus(q.device))
+        k_cache, v_cache = pool.get_kv_buffer(layer_id)
+        k_scale, v_scale = pool.get_kv_scales(layer_id)
+        fp8 = pool.store_dtype == ops.FP8
+        out = ops.paged_decode_gqa(
+            q.reshape(bs, H, d), k_cache, v_cache, st.table, st.seq_lens, k.reshape(bs, G, d), v.reshape(bs, G, d),
+            sm_scale=float(layer.scaling), k_scale=k_scale if fp8 else None, v_scale=v_scale if fp8 else None,
+            sinks=sinks, window=window, new_slots=st.slots if save else None, plan=st.plans[key])
+        return out.reshape(bs, H * d)
+
+    def _decode_mla(self, q, k, layer, layer_id, st, bs, save):
+        pool: NeuronMLATokenToKVPool = self.token_to_kv_pool
+        H = int(layer.tp_q_head_num)
+        q = q.reshape(bs, H, 576)
+        key = ("mla", H)
+        if key not in st.plans:
+            st.plans[key] = ops.plan_decode(_lib.KIND_MLA, bs, host_seq_lens=st.meta.seq_lens,
+                                            ctas_per_item=(H + 15) // 16, num_cus=ops._num_cus(q.device))
+        out = ops.mla_decode(
+            q[..., :512], q[..., 512:], pool.get_key_buffer(layer_id), pool.get_row_scale(layer_id), st.table,
+            st.seq_lens, k.reshape(bs, 576), sm_scale=float(layer.scaling), page_size=pool.page_size,
+            new_slots=st.slots if save else None, plan=st.plans[key])
+        return out.reshape(bs, H * 512)
+
+    def _decode_dsa(self, q, k, layer, layer_id, st, bs, save, topk_indices):
+        pool: NeuronDSATokenToKVPool = self.token_to_kv_pool
+        if topk_indices is None:
+            raise ValueError("a DSA decode needs topk_indices [bs, K]")
+        H = int(layer.tp_q_head_num)
+        q = q.reshape(bs, H, 576)
+        idx = topk_indices.reshape(bs, -1)
+        key = ("dsa", H, idx.shape[1])
+        if key not in st.plans:
+            st.plans[key] = ops.plan_decode(_lib.KIND_DSA, bs, n_keys_per_row=idx.shape[1],
+                                            ctas_per_item=(H + 15) // 16, num_cus=ops._num_cus(q.device))
+        ctx, lse = ops.mla_decode_sparse(
+            q[..., :512], q[..., 512:], pool.get_key_buffer(layer_id), pool.get_kv_scale(layer_id), idx, st.table,
+            st.positions, k.reshape(bs, 576), sm_scale=float(layer.scaling), page_size=pool.page_size,
+            new_slots=st.slots if save else None, plan=st.plans[key])
+        self.last_lse = lse
+        return ctx.reshape(bs, H * 512)

@@ -1,0 +1,150 @@
+"""The decode step through the reference-shaped interface (pool set_kv_buffer + backend forward_decode) against the
+CPU oracle: outputs within the attention bar, pools bit-exact after the step."""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from conftest import announce
+from _harness import assert_close_attn, dsa_oracle, gqa_oracle, mla_oracle
+from sglang_neuron_amd import workloads
+from sglang_neuron_amd.attention import NeuronAttnBackend
+from sglang_neuron_amd.mem_cache import NeuronDSATokenToKVPool, NeuronMHATokenToKVPool, NeuronMLATokenToKVPool
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+class _Decode:
+    def is_extend(self):
+        return False
+
+    def is_idle(self):
+        return False
+
+
+def _req_to_token(table: torch.Tensor, lens, page: int) -> torch.Tensor:
+    """req_to_token [B, context] of the case's pages: slot of (b, pos) = table[b, pos // page] * page + pos % page."""
+    B = table.shape[0]
+    ctx = table.shape[1] * page
+    pos = torch.arange(ctx)
+    r2t = table.to(torch.int64).clamp(min=0)[:, pos // page] * page + pos % page
+    return r2t.to(torch.int32).reshape(B, ctx)
+
+
+def _backend(pool, table, lens, page):
+    runner = SimpleNamespace(req_to_token_pool=SimpleNamespace(req_to_token=_req_to_token(table, lens, page)),
+                             token_to_kv_pool=pool, page_size=page)
+    return NeuronAttnBackend(runner)
+
+
+def _batch(lens, new_slots, positions=None):
+    lens = lens.to(torch.int64)
+    B = lens.numel()
+    return SimpleNamespace(forward_mode=_Decode(), batch_size=B, req_pool_indices=torch.arange(B), seq_lens=lens.to(DEV),
+                           seq_lens_cpu=lens, out_cache_loc=new_slots.to(DEV),
+                           positions=(lens - 1 if positions is None else positions).to(DEV), extend_prefix_lens=None)
+
+
+GQA = [("cfg1", 1, {}), ("cfg2-small", 2, {"B": 4, "lens": (100, 700)}),
+       ("cfg4-sinks", 4, {"B": 6, "lens": (30, 600)}), ("cfg4-swa", 4, {"B": 5, "lens": (10, 500), "window": 128})]
+
+
+@pytest.mark.parametrize("name,cfg,over", GQA, ids=[g[0] for g in GQA])
+def test_backend_gqa_decode(name, cfg, over):
+    case = workloads.gqa_case(cfg, overrides=over)
+    want, kc_o, vc_o, ks_o, vs_o = gqa_oracle(case)
+    announce(f"backend gqa {name}: B={case.B} H={case.H} G={case.G} d={case.d} fp8={case.fp8}")
+    dtype = torch.float8_e4m3fn if case.fp8 else torch.bfloat16
+    pool = NeuronMHATokenToKVPool(size=(case.num_blocks - 1) * case.P, page_size=case.P, dtype=dtype,
+                                  head_num=case.G, head_dim=case.d, layer_num=2, device=DEV)
+    layer = SimpleNamespace(layer_id=1, tp_q_head_num=case.H, tp_k_head_num=case.G, head_dim=case.d,
+                            scaling=case.sm_scale, sliding_window_size=case.window if case.window else -1,
+                            sinks=None if case.sinks is None else case.sinks.to(DEV))
+    if case.fp8:
+        pool.calibrate_kv_scales(1, torch.cat([case.k_prior, case.k_new]).to(DEV),
+                                 torch.cat([case.v_prior, case.v_new]).to(DEV))
+    pool.set_kv_buffer(layer, case.prior_slots.to(DEV), case.k_prior.to(DEV), case.v_prior.to(DEV))
+    backend = _backend(pool, case.block_table, case.seq_lens, case.P)
+    fb = _batch(case.seq_lens, case.new_slots)
+    out = backend.forward_decode(case.q.reshape(case.B, -1).to(DEV), case.k_new.to(DEV), case.v_new.to(DEV), layer, fb)
+    torch.cuda.synchronize()
+    assert out.shape == (case.B, case.H * case.d)
+    assert_close_attn(out.reshape(case.B, case.H, case.d), want, name)
+    k, v = pool.get_kv_buffer(1)
+    assert torch.equal(k.cpu().view(torch.uint8), kc_o.view(torch.uint8)), "K pool differs"
+    assert torch.equal(v.cpu().view(torch.uint8), vc_o.view(torch.uint8)), "V pool differs"
+    if case.fp8:
+        ks, vs = pool.get_kv_scales(1)
+        assert torch.equal(ks.cpu(), ks_o) and torch.equal(vs.cpu(), vs_o), "scales differ"
+
+
+def test_backend_gqa_decode_without_save_leaves_pool():
+    case = workloads.gqa_case(2, overrides={"B": 3, "lens": (50, 200)})
+    want, *_ = gqa_oracle(case)
+    announce("backend gqa no-save")
+    pool = NeuronMHATokenToKVPool((case.num_blocks - 1) * case.P, case.P, torch.float8_e4m3fn, case.G, case.d, 1, DEV)
+    layer = SimpleNamespace(layer_id=0, tp_q_head_num=case.H, tp_k_head_num=case.G, head_dim=case.d,
+                            scaling=case.sm_scale)
+    pool.calibrate_kv_scales(0, torch.cat([case.k_prior, case.k_new]).to(DEV),
+                             torch.cat([case.v_prior, case.v_new]).to(DEV))
+    pool.set_kv_buffer(layer, case.prior_slots.to(DEV), case.k_prior.to(DEV), case.v_prior.to(DEV))
+    before = pool.get_key_buffer(0).clone()
+    backend = _backend(pool, case.block_table, case.seq_lens, case.P)
+    out = backend.forward_decode(case.q.to(DEV), case.k_new.to(DEV), case.v_new.to(DEV), layer,
+                                 _batch(case.seq_lens, case.new_slots), save_kv_cache=False)
+    torch.cuda.synchronize()
+    assert_close_attn(out.reshape(case.B, case.H, case.d), want, "no-save")
+    assert torch.equal(pool.get_key_buffer(0).view(torch.uint8), before.view(torch.uint8))
+
+
+def test_backend_mla_decode():
+    case = workloads.mla_case(overrides={"B": 4, "lens": (1, 3000)})
+    want, cache_o, scale_o = mla_oracle(case)
+    announce(f"backend mla: B={case.B} lens={case.seq_lens.tolist()}")
+    pool = NeuronMLATokenToKVPool((case.num_blocks - 1) * case.P, case.P, torch.float8_e4m3fn, 512, 64, 1, DEV)
+    layer = SimpleNamespace(layer_id=0, tp_q_head_num=case.H, scaling=case.sm_scale)
+    T = case.prior_slots.numel()
+    pool.set_kv_buffer(layer, case.prior_slots.to(DEV), case.prior_rows.reshape(T, 1, 576).to(DEV))
+    backend = _backend(pool, case.block_table, case.seq_lens, case.P)
+    q = torch.cat([case.ql_nope, case.q_pe], dim=-1).to(DEV)
+    out = backend.forward_decode(q, case.compact_new.to(DEV), None, layer, _batch(case.seq_lens, case.new_slots))
+    torch.cuda.synchronize()
+    assert_close_attn(out.reshape(case.B, case.H, 512), want, "mla")
+    assert torch.equal(pool.kv_buffer[0].cpu().reshape(-1, 576), cache_o), "row pool differs"
+    written = torch.cat([case.prior_slots, case.new_slots])
+    assert torch.equal(pool.row_scale[0].cpu()[written], scale_o[written]), "row scales differ"
+
+
+def test_backend_mla_set_mla_kv_buffer_matches_full_rows():
+    case = workloads.mla_case(overrides={"B": 2, "lens": (40, 90)})
+    announce("backend mla set_mla_kv_buffer")
+    T = case.prior_slots.numel()
+    a = NeuronMLATokenToKVPool((case.num_blocks - 1) * case.P, case.P, torch.float8_e4m3fn, 512, 64, 1, DEV)
+    b = NeuronMLATokenToKVPool((case.num_blocks - 1) * case.P, case.P, torch.float8_e4m3fn, 512, 64, 1, DEV)
+    rows = case.prior_rows.to(DEV)
+    a.set_kv_buffer(0, case.prior_slots.to(DEV), rows.reshape(T, 1, 576))
+    b.set_mla_kv_buffer(0, case.prior_slots.to(DEV), rows[:, :512].reshape(T, 1, 512), rows[:, 512:].reshape(T, 1, 64))
+    torch.cuda.synchronize()
+    assert torch.equal(a.kv_buffer[0], b.kv_buffer[0]) and torch.equal(a.row_scale[0], b.row_scale[0])
+
+
+def test_backend_dsa_decode():
+    case = workloads.dsa_case(overrides={"B": 3, "pool_positions": 2048, "n_indices": 256, "recent": 32,
+                                         "short_rows": (200,)})
+    want_ctx, want_lse, cache_o = dsa_oracle(case)
+    announce(f"backend dsa: B={case.B} K={case.indices.shape[1]}")
+    pool = NeuronDSATokenToKVPool((case.num_blocks - 1) * case.P, case.P, 1, DEV, kv_scale=case.kv_scale)
+    case.fill_rows(lambda v, s: pool.set_kv_buffer(0, s.to(DEV), v.to(DEV)))
+    layer = SimpleNamespace(layer_id=0, tp_q_head_num=case.H, scaling=case.sm_scale)
+    backend = _backend(pool, case.block_table, case.positions.to(torch.int64) + 1, case.P)
+    q = torch.cat([case.q_absorbed, case.q_pe], dim=-1).to(DEV)
+    fb = _batch(case.positions.to(torch.int64) + 1, case.new_slots, positions=case.positions.to(torch.int64))
+    out = backend.forward_decode(q, case.own_rows.to(DEV), None, layer, fb, topk_indices=case.indices.to(DEV))
+    torch.cuda.synchronize()
+    assert_close_attn(out.reshape(case.B, case.H, 512), want_ctx, "dsa")
+    assert torch.allclose(backend.last_lse.cpu(), want_lse, atol=2e-3, rtol=1e-4)
+    assert torch.equal(pool.get_key_buffer(0).cpu().reshape(-1, 640), cache_o), "row pool differs"

@@ -1,0 +1,151 @@
+"""The C ABI on the CPU: the library loads and exports every function include/sglang_neuron_amd.h declares, with the
+ctypes declarations matching; the split-K planner's host logic; host-side argument checks. No kernel is launched."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from sglang_neuron_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sglang_neuron_amd.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        from sglang_neuron_amd import build
+
+        build.build(verbose=False)
+    return _lib.load()
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sna_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declarations_are_exported_and_bound(lib):
+    names = _declared()
+    assert len(names) >= 14, names
+    for n in names:
+        assert hasattr(lib, n), f"{n} is declared but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes declaration"
+    assert set(_lib.SIGNATURES) == set(names), set(_lib.SIGNATURES) ^ set(names)
+
+
+def test_header_parameter_counts_match_ctypes():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    for m in re.finditer(r"\b(sna_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text):
+        name, params = m.group(1), m.group(2).strip()
+        n = 0 if params in ("", "void") else params.count(",") + 1
+        assert len(_lib.SIGNATURES[name][1]) == n, (name, n, len(_lib.SIGNATURES[name][1]))
+
+
+def test_version_and_error_string(lib):
+    assert lib.sna_version() == 100
+    assert isinstance(lib.sna_last_error(), bytes)
+
+
+def _plan(lib, kind, lens=None, B=None, max_len=-1, window=0, keys=0, ctas=1, cus=256, depth=0):
+    p = _lib.SplitPlan()
+    p.depth = depth
+    B = len(lens) if lens is not None else B
+    arr = (ctypes.c_int32 * B)(*lens) if lens is not None else None
+    rc = lib.sna_plan_decode(kind, arr, B, max_len, window, keys, ctas, cus, ctypes.byref(p))
+    return rc, p
+
+
+def _splits(L, window, tile, split):
+    if L <= 1:
+        return 0
+    hi, lo = L - 1, (L - window if window > 0 and L - window > 0 else 0)
+    if hi <= lo:
+        return 0
+    t0, t1 = lo // tile, (hi + tile - 1) // tile
+    return (t1 - t0 + split - 1) // split
+
+
+@pytest.mark.parametrize("kind,lens,window,ctas", [
+    (_lib.KIND_GQA, [4096] * 64, 0, 8),
+    (_lib.KIND_GQA, [2048 + 37 * i for i in range(128)], 0, 1),
+    (_lib.KIND_GQA, [2048 + 37 * i for i in range(128)], 128, 1),
+    (_lib.KIND_GQA, [1, 2, 17, 33, 1000], 0, 8),
+    (_lib.KIND_MLA, [1024 + 467 * i for i in range(32)], 0, 1),
+    (_lib.KIND_MLA, [1, 5, 70000], 0, 2),
+])
+def test_plan_invariants(lib, kind, lens, window, ctas):
+    rc, p = _plan(lib, kind, lens, window=window, ctas=ctas)
+    assert rc == 0, lib.sna_last_error()
+    tile = 32 if kind == _lib.KIND_GQA else 16
+    assert p.tile == tile and p.batch == len(lens)
+    n = [_splits(L, window, tile, p.split_tiles) for L in lens]
+    assert p.n_work == sum(n) and p.max_splits == max(n) <= 64
+    assert p.empty_rows == sum(1 for x in n if x == 0)
+    if kind == _lib.KIND_MLA:
+        assert p.split_tiles * 16 <= 2048 and p.depth == 0
+    else:
+        assert p.depth in (2, 4)
+    if kind == _lib.KIND_MLA or p.depth == 4:  # one-round plans fit the resident target unless splits are capped
+        assert p.n_work * ctas <= p.target_ctas or p.split_tiles == (2048 // 16 if kind else max(
+            (max(lens) - 1 + tile - 1) // tile, 4))
+    ws = lib.sna_decode_workspace_bytes(ctypes.byref(p), 16, 512)
+    assert ws == (0 if p.max_splits <= 1 else p.batch * p.max_splits * 16 * (512 + 2) * 4)
+
+
+def test_plan_from_a_bound_marks_empty_rows_unknown(lib):
+    rc, p = _plan(lib, _lib.KIND_GQA, B=4, max_len=900)
+    assert rc == 0 and p.empty_rows == -1
+
+
+def test_plan_dsa_every_row_alike(lib):
+    rc, p = _plan(lib, _lib.KIND_DSA, B=16, keys=2048, ctas=1)
+    assert rc == 0
+    per = _splits(2049, 0, 16, p.split_tiles)
+    assert p.n_work == 16 * per and p.max_splits == per
+
+
+def test_plan_rejects_bad_arguments(lib):
+    assert _plan(lib, 7, [10])[0] == _lib.SNA_ERR_INVALID_ARGUMENT
+    assert _plan(lib, _lib.KIND_GQA, [10], ctas=0)[0] == _lib.SNA_ERR_INVALID_ARGUMENT
+    assert _plan(lib, _lib.KIND_GQA, None, B=2, max_len=-1)[0] == _lib.SNA_ERR_INVALID_ARGUMENT
+    rc = lib.sna_plan_decode(0, None, 1, 10, 0, 0, 1, 256, None)
+    assert rc == _lib.SNA_ERR_INVALID_ARGUMENT and b"null plan" in lib.sna_last_error()
+
+
+def test_decode_entry_checks_arguments_before_touching_the_gpu(lib):
+    rc, p = _plan(lib, _lib.KIND_GQA, [100, 200], ctas=2)
+    null = None
+    # 5 query heads over 2 KV heads
+    rc = lib.sna_paged_decode_gqa(null, null, null, null, null, null, 0, 0, null, null, null, null, null, 0, 0.1, null,
+                                  2, 5, 2, 128, 16, 10, 1, ctypes.byref(p), null, 0, null)
+    assert rc == _lib.SNA_ERR_INVALID_ARGUMENT and b"head counts" in lib.sna_last_error()
+    # head_dim 96 is not built
+    rc = lib.sna_paged_decode_gqa(null, null, null, null, null, null, 0, 0, null, null, null, null, null, 0, 0.1, null,
+                                  2, 4, 2, 96, 16, 10, 1, ctypes.byref(p), null, 0, null)
+    assert rc == _lib.SNA_ERR_UNSUPPORTED
+    # null tensors with a valid shape
+    rc = lib.sna_paged_decode_gqa(null, null, null, null, null, null, 8, 8, null, null, null, null, null, 0, 0.1, null,
+                                  2, 4, 2, 128, 16, 10, 1, ctypes.byref(p), null, 0, null)
+    assert rc == _lib.SNA_ERR_INVALID_ARGUMENT and b"null pointer" in lib.sna_last_error()
+    # a plan made for another batch
+    rc = lib.sna_paged_decode_gqa(null, null, null, null, null, null, 8, 8, null, null, null, null, null, 0, 0.1, null,
+                                  3, 4, 2, 128, 16, 10, 1, ctypes.byref(p), null, 0, null)
+    assert rc == _lib.SNA_ERR_INVALID_ARGUMENT and b"plan" in lib.sna_last_error()
+    # an empty batch is a no-op
+    rc0, p0 = _plan(lib, _lib.KIND_GQA, B=0, max_len=0)
+    assert rc0 == 0
+    assert lib.sna_paged_decode_gqa(null, null, null, null, null, null, 0, 0, null, null, null, null, null, 0, 0.1,
+                                    null, 0, 4, 2, 128, 16, 10, 1, ctypes.byref(p0), null, 0, null) == 0
+
+
+def test_store_entries_check_arguments(lib):
+    assert lib.sna_kv_store_mha(None, None, None, 4, None, None, None, None, 10, 2, 16, 100, 1, None) < 0
+    assert lib.sna_kv_store_mla(None, None, 4, 576, None, None, 100, 1, None) < 0
+    assert lib.sna_kv_store_dsa(None, None, 4, 0.5, None, 100, None) < 0
+    assert lib.sna_kv_store_mha(None, None, None, 0, None, None, None, None, 10, 2, 16, 128, 0, None) == 0

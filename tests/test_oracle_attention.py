@@ -1,0 +1,276 @@
+"""Pins of the oracle's decode attention (oracle/attention.py) and metadata (oracle/metadata.py): float64 brute force
+with explicit loops over keys on tiny inputs, closed forms, invariances, and block tables built by hand."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oatt
+from oracle import fp8 as ofp8
+from oracle import metadata as omd
+from oracle import store as ost
+
+
+def _bf16(shape, g, scale=1.0):
+    return (torch.randn(shape, generator=g) * scale).to(torch.bfloat16)
+
+
+def _softmax_attend(q, keys, vals, scale, sink=None):
+    """float64 softmax attention of one query over key/value lists, by explicit loops."""
+    s = [sum(float(q[i]) * float(k[i]) for i in range(len(q))) * scale for k in keys]
+    m = max(s + ([sink] if sink is not None else []))
+    e = [math.exp(x - m) for x in s]
+    den = sum(e) + (math.exp(sink - m) if sink is not None else 0.0)
+    return [sum(e[j] * float(vals[j][i]) for j in range(len(keys))) / den for i in range(len(vals[0]))]
+
+
+def _gqa_case(seed, B=3, H=4, G=2, d=8, P=4, fp8=False, window=0, sinks=False):
+    g = torch.Generator().manual_seed(seed)
+    lens = [1, 6, 11][:B]
+    pages = [(L + P - 1) // P for L in lens]
+    nb = sum(pages) + 2
+    perm = (torch.randperm(nb - 1, generator=g) + 1).tolist()
+    W = max(pages)
+    table = torch.full((B, W), -1, dtype=torch.int32)
+    o = 0
+    for b, n in enumerate(pages):
+        table[b, :n] = torch.tensor(perm[o:o + n], dtype=torch.int32)
+        o += n
+    dt = torch.uint8 if fp8 else torch.bfloat16
+    kc = torch.zeros(nb, G, P, d, dtype=dt)
+    vc = torch.zeros(nb, G, P, d, dtype=dt)
+    kp, vp, slots = [], [], []
+    for b, L in enumerate(lens):
+        for p in range(L - 1):
+            slots.append(int(table[b, p // P]) * P + p % P)
+    T = len(slots)
+    kp, vp = _bf16((T, G, d), g), _bf16((T, G, d), g)
+    ks = torch.rand(G, generator=g) * 0.01 + 0.004 if fp8 else None
+    vs = torch.rand(G, generator=g) * 0.01 + 0.004 if fp8 else None
+    ost.kv_store_mha(kp, vp, torch.tensor(slots), kc, vc, ks, vs)
+    q, kn, vn = _bf16((B, H, d), g), _bf16((B, G, d), g), _bf16((B, G, d), g)
+    sk = torch.randn(H, generator=g) if sinks else None
+    return dict(q=q, kc=kc, vc=vc, table=table, lens=torch.tensor(lens), kn=kn, vn=vn, ks=ks, vs=vs, sinks=sk,
+                P=P, G=G, window=window, slots=slots)
+
+
+def _brute_gqa(c, scale):
+    """Loops: row b, head h -> KV head h // (H / G); prior keys at positions p < L - 1 (and >= L - W) read from
+    page table[b, p // P] at offset p % P; then the new token."""
+    q, P, G = c["q"], c["P"], c["G"]
+    B, H, d = q.shape
+    out = torch.empty(B, H, d, dtype=torch.float64)
+    for b in range(B):
+        L = int(c["lens"][b])
+        for h in range(H):
+            g = h // (H // G)
+            keys, vals = [], []
+            for p in range(L - 1):
+                if c["window"] and p < L - c["window"]:
+                    continue
+                page = int(c["table"][b, p // P])
+                kb, vb = c["kc"][page, g, p % P], c["vc"][page, g, p % P]
+                if c["ks"] is not None:
+                    kb = ofp8.dequantize(kb, float(c["ks"][g]))
+                    vb = ofp8.dequantize(vb, float(c["vs"][g]))
+                keys.append(kb.double())
+                vals.append(vb.double())
+            kn, vn = c["kn"][b, g], c["vn"][b, g]
+            if c["ks"] is not None:
+                kn = ofp8.dequantize(ofp8.quantize(kn, float(c["ks"][g])), float(c["ks"][g]))
+                vn = ofp8.dequantize(ofp8.quantize(vn, float(c["vs"][g])), float(c["vs"][g]))
+            keys.append(kn.double())
+            vals.append(vn.double())
+            sink = None if c["sinks"] is None else float(c["sinks"][h])
+            out[b, h] = torch.tensor(_softmax_attend(q[b, h].double(), keys, vals, scale, sink))
+    return out
+
+
+def _oracle_gqa(c, scale):
+    return oatt.paged_decode_gqa(c["q"], c["kc"], c["vc"], c["table"], c["lens"], c["kn"], c["vn"], sm_scale=scale,
+                                 k_scale=c["ks"], v_scale=c["vs"], sinks=c["sinks"], window=c["window"])
+
+
+@pytest.mark.parametrize("fp8,window,sinks", [(False, 0, False), (True, 0, False), (True, 0, True), (False, 3, False),
+                                              (True, 4, True)])
+def test_gqa_matches_float64_brute_force(fp8, window, sinks):
+    c = _gqa_case(11, fp8=fp8, window=window, sinks=sinks)
+    scale = 1 / math.sqrt(8)
+    got = _oracle_gqa(c, scale).double()
+    want = _brute_gqa(c, scale)
+    # the oracle rounds its output to bf16 once: half an ulp of bf16 at these magnitudes
+    assert torch.allclose(got, want, atol=1e-2, rtol=8e-3), (got - want).abs().max()
+
+
+def test_gqa_single_key_returns_its_value():
+    c = _gqa_case(12)
+    c["lens"] = torch.tensor([1, 1, 1])  # no prior: only the new token
+    out = _oracle_gqa(c, 0.3)
+    want = c["vn"].repeat_interleave(2, dim=1)  # head h reads KV head h // 2
+    assert torch.equal(out, want)
+
+
+def test_gqa_equal_keys_give_the_mean_of_values():
+    c = _gqa_case(13)
+    b, L = 2, int(c["lens"][2])
+    key = c["kn"][b]
+    for p in range(L - 1):  # every prior key of row 2 equal to the new key
+        page = int(c["table"][b, p // c["P"]])
+        c["kc"][page, :, p % c["P"]] = key
+    out = _oracle_gqa(c, 0.5)[b].float()
+    vals = [c["vc"][int(c["table"][b, p // c["P"]]), :, p % c["P"]].float() for p in range(L - 1)]
+    vals.append(c["vn"][b].float())
+    mean = torch.stack(vals).mean(0).repeat_interleave(2, dim=0)
+    assert torch.allclose(out, mean, atol=8e-3, rtol=8e-3)
+
+
+def test_gqa_minus_inf_sink_is_no_sink_and_wide_window_is_full():
+    c = _gqa_case(14, sinks=True)
+    base = _oracle_gqa(dict(c, sinks=None), 0.4)
+    assert torch.equal(_oracle_gqa(dict(c, sinks=torch.full((4,), float("-inf"))), 0.4), base)
+    assert torch.equal(_oracle_gqa(dict(c, sinks=None, window=100), 0.4), base)
+    # a finite sink only shrinks the weights: the output moves toward 0
+    with_sink = _oracle_gqa(dict(c, sinks=torch.full((4,), 3.0)), 0.4).float()
+    assert bool((with_sink.abs() <= base.float().abs() + 1e-2).all())
+
+
+def test_gqa_fp8_scale_one_on_representable_values_is_the_bf16_result():
+    c = _gqa_case(15)
+    vals = torch.tensor(ofp8.e4m3fn_values(), dtype=torch.float32)
+    vals = vals[vals.abs() <= 4]
+    g = torch.Generator().manual_seed(9)
+    for key in ("kc", "vc"):
+        pick = vals[torch.randint(0, vals.numel(), c[key].shape, generator=g)]
+        c[key] = pick.to(torch.bfloat16)
+    for key in ("kn", "vn"):
+        c[key] = vals[torch.randint(0, vals.numel(), c[key].shape, generator=g)].to(torch.bfloat16)
+    bf = _oracle_gqa(c, 0.35)
+    f8 = dict(c, kc=ofp8.quantize(c["kc"], 1.0), vc=ofp8.quantize(c["vc"], 1.0), ks=torch.ones(2), vs=torch.ones(2))
+    assert torch.equal(_oracle_gqa(f8, 0.35), bf)
+
+
+def test_gqa_page_permutation_invariance():
+    c = _gqa_case(16, fp8=True)
+    nb = c["kc"].shape[0]
+    g = torch.Generator().manual_seed(17)
+    perm = torch.cat([torch.zeros(1, dtype=torch.long), torch.randperm(nb - 1, generator=g) + 1])  # new id of page i
+    kc2, vc2 = torch.empty_like(c["kc"]), torch.empty_like(c["vc"])
+    kc2[perm], vc2[perm] = c["kc"], c["vc"]
+    table2 = torch.where(c["table"] >= 0, perm[c["table"].clamp(min=0).long()].to(torch.int32), c["table"])
+    assert torch.equal(_oracle_gqa(dict(c, kc=kc2, vc=vc2, table=table2), 0.3), _oracle_gqa(c, 0.3))
+
+
+def test_lse_merge_of_splits_is_the_whole():
+    g = torch.Generator().manual_seed(18)
+    q, keys, vals = torch.randn(8, generator=g), torch.randn(20, 8, generator=g), torch.randn(20, 5, generator=g)
+    s = keys @ q
+    full = torch.softmax(s, 0) @ vals
+    parts, lses = [], []
+    for lo, hi in ((0, 7), (7, 13), (13, 20)):
+        ss = s[lo:hi]
+        parts.append((torch.softmax(ss, 0) @ vals[lo:hi])[None])
+        lses.append(torch.logsumexp(ss, 0).reshape(1))
+    out, lse = oatt.lse_merge(torch.stack(parts), torch.stack(lses))
+    assert torch.allclose(out.float().reshape(-1), full, atol=1e-2)
+    assert torch.allclose(lse.reshape(-1), torch.logsumexp(s, 0).reshape(-1), atol=1e-5)
+
+
+def _mla_case(seed, B=2, H=3, P=4):
+    g = torch.Generator().manual_seed(seed)
+    lens = [3, 9][:B]
+    pages = [(L + P - 1) // P for L in lens]
+    nb = sum(pages) + 1
+    table = torch.full((B, max(pages)), -1, dtype=torch.int32)
+    perm = (torch.randperm(nb - 1, generator=g) + 1).tolist()
+    o = 0
+    for b, n in enumerate(pages):
+        table[b, :n] = torch.tensor(perm[o:o + n], dtype=torch.int32)
+        o += n
+    cache = torch.zeros(nb * P, 576, dtype=torch.uint8)
+    scale = torch.zeros(nb * P)
+    slots = [int(table[b, p // P]) * P + p % P for b, L in enumerate(lens) for p in range(L - 1)]
+    rows = _bf16((len(slots), 576), g)
+    ost.kv_store_mla(rows, torch.tensor(slots), cache, scale)
+    return dict(ql=_bf16((B, H, 512), g), qpe=_bf16((B, H, 64), g), cache=cache, scale=scale, table=table,
+                lens=torch.tensor(lens), new=_bf16((B, 576), g), P=P)
+
+
+def test_mla_matches_float64_brute_force():
+    c = _mla_case(21)
+    sm = 1 / math.sqrt(192)
+    got = oatt.mla_decode(c["ql"], c["qpe"], c["cache"], c["scale"], c["table"], c["lens"], c["new"], sm_scale=sm,
+                          page_size=c["P"]).double()
+    B, H, _ = c["ql"].shape
+    for b in range(B):
+        L = int(c["lens"][b])
+        keys = []
+        for p in range(L - 1):
+            s = int(c["table"][b, p // c["P"]]) * c["P"] + p % c["P"]
+            keys.append(ofp8.dequantize(c["cache"][s], float(c["scale"][s])).double())
+        ns = float(ofp8.absmax_scale(c["new"][b], dims=-1))
+        keys.append(ofp8.dequantize(ofp8.quantize(c["new"][b], ns), ns).double())
+        for h in range(H):
+            q = torch.cat([c["ql"][b, h], c["qpe"][b, h]]).double()
+            want = _softmax_attend(q, keys, [k[:512] for k in keys], sm)
+            assert torch.allclose(got[b, h], torch.tensor(want, dtype=torch.float64), atol=1e-2, rtol=8e-3)
+
+
+def test_dsa_all_prior_indices_match_a_dense_brute_force():
+    g = torch.Generator().manual_seed(31)
+    B, H, P, per = 2, 2, 4, 12
+    W = per // P
+    table = torch.tensor([[3, 1, 5], [2, 6, 4]], dtype=torch.int32)
+    cache = torch.zeros(7 * P, 640, dtype=torch.uint8)
+    kv = 0.5
+    for b in range(B):
+        slots = torch.tensor([int(table[b, p // P]) * P + p % P for p in range(per)])
+        ost.kv_store_dsa(_bf16((per, 576), g), slots, cache, kv)
+    positions = torch.tensor([7, 11], dtype=torch.int32)
+    idx = torch.full((B, per), -1, dtype=torch.int32)
+    for b in range(B):
+        idx[b, :int(positions[b])] = torch.arange(int(positions[b]))  # every prior position
+    own = _bf16((B, 576), g)
+    new_slots = torch.tensor([int(table[b, int(positions[b]) // P]) * P + int(positions[b]) % P for b in range(B)])
+    qa, qpe = _bf16((B, H, 512), g), _bf16((B, H, 64), g)
+    ctx, lse, cache2 = oatt.mla_decode_sparse(qa, qpe, cache, kv, idx, table, positions, own, new_slots,
+                                              sm_scale=0.0625, page_size=P)
+    for b in range(B):
+        keys = []
+        for p in range(int(positions[b]) + 1):  # the prior positions, then the own row (stored at its position)
+            s = int(table[b, p // P]) * P + p % P
+            row = ost.unpack_kv_row(cache2[s][None], kv)[0].double()  # [k_pe | latent]
+            keys.append(row)
+        for h in range(H):
+            q = torch.cat([qpe[b, h], qa[b, h]]).double()
+            want = _softmax_attend(q, keys, [k[64:] for k in keys], 0.0625)
+            assert torch.allclose(ctx[b, h].double(), torch.tensor(want, dtype=torch.float64), atol=1e-2, rtol=8e-3)
+            s = [float((q * k).sum()) * 0.0625 for k in keys]
+            assert float(lse[b, h]) == pytest.approx(float(torch.logsumexp(torch.tensor(s), 0)), abs=1e-4)
+
+
+def test_block_table_by_hand():
+    page = 4
+    r2t = np.arange(6 * 40, dtype=np.int64).reshape(6, 40) * 3 % 997
+    rows, lens = np.array([4, 1, 2]), np.array([9, 1, 16])
+    got = omd.block_table(r2t, rows, lens, page).numpy()
+    want = np.full((3, 4), -1)
+    for i, (r, L) in enumerate(zip(rows, lens)):
+        for j in range(4):
+            if j * page < L:
+                want[i, j] = r2t[r, j * page] // page
+    assert np.array_equal(got, want)
+    one = omd.block_table(r2t, np.array([5]), np.array([3]), page).numpy()  # one row: no -1
+    assert np.array_equal(one, [[r2t[5, 0] // page]])
+
+
+def test_swa_trimmed_table_by_hand():
+    table = torch.arange(1, 11, dtype=torch.int32).reshape(1, 10)
+    trimmed, off = omd.swa_trimmed_table(table, torch.tensor([37]), window=8, page=4, width=3)
+    # ctx 36 -> column 9 is the last; start = 9 - 3 + 1 = 7
+    assert trimmed.tolist() == [[8, 9, 10]] and off.tolist() == [28]
+    trimmed, off = omd.swa_trimmed_table(table, torch.tensor([5]), window=8, page=4, width=3)
+    assert trimmed.tolist() == [[1, 2, 3]] and off.tolist() == [0]

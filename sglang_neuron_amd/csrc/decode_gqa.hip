@@ -367,48 +367,53 @@ void gqa_decode_kernel(GqaArgs a) {
   }
 }
 
-// Merge of a row's splits per (row, KV head): out = sum_s e_s o_s / (sum_s e_s l_s + e_sink), with
-// e_s = exp2(m_s - M). The (m, l) pairs of the group's heads load into LDS in one round and each head's weights are
-// formed once. Every thread then sums its outputs over the splits with independent loads.
+// Merge of a row's splits, one wave per (row, query head): out = sum_s e_s o_s / (sum_s e_s l_s + e_sink), with
+// e_s = exp2(m_s - M) and M the maximum over the splits and the sink. Lane s holds split s's weight; lane i holds the
+// head dims D / 64 * i .. + D / 64. The partials of the first splits load before the weights are known.
 template <int D>
-__global__ __launch_bounds__(256) void gqa_combine_kernel(GqaArgs a) {
-  const int b = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+__global__ __launch_bounds__(64) void gqa_combine_kernel(GqaArgs a) {
+  constexpr int V = D / 64;
+  const int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
   const int32_t S = a.max_splits;
   const int32_t n = min(splits_of<32>(ld_const(a.seq_lens + b), a.window, a.split_tiles), S);
-  __shared__ float sm_w[16][kMaxSplits + 1];
-  __shared__ float sm_l[16][kMaxSplits + 1];
-  __shared__ float sm_inv[16];
-  const int64_t base = (int64_t)b * S * a.H + (int64_t)g * a.group;  // row of (b, split 0, head g * group)
-  for (int e = tid; e < a.group * n; e += blockDim.x) {
-    const int j = e / n, s = e % n;
-    const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + (base + (int64_t)s * a.H + j) * 2);
-    sm_w[j][s] = ml.x;
-    sm_l[j][s] = ml.y;
+  if (n == 0) return;  // a row with no prior key: the lone-token kernel writes it
+  const int64_t row0 = (int64_t)b * S * a.H + h;
+  const float* ob = a.ws_o + row0 * D + V * lane;
+  const int64_t sstride = (int64_t)a.H * D;
+  constexpr int PRE = 8;
+  float pre[PRE][V];
+#pragma unroll
+  for (int s = 0; s < PRE; ++s)
+#pragma unroll
+    for (int v = 0; v < V; ++v) pre[s][v] = s < n ? ob[s * sstride + v] : 0.0f;
+  float m = -INFINITY, l = 0.0f;
+  if (lane < n) {
+    const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + (row0 + (int64_t)lane * a.H) * 2);
+    m = ml.x;
+    l = ml.y;
   }
-  __syncthreads();
-  if (tid < a.group) {
-    const int j = tid;
-    const int32_t h = g * a.group + j;
-    const float sink = a.sinks ? a.sinks[h] * kLog2e : -INFINITY;
-    float M = sink;
-    for (int32_t s = 0; s < n; ++s) M = fmaxf(M, sm_w[j][s]);
-    float den = a.sinks ? __builtin_amdgcn_exp2f(sink - M) : 0.0f;
-    for (int32_t s = 0; s < n; ++s) {
-      const float w = __builtin_amdgcn_exp2f(sm_w[j][s] - M);
-      sm_w[j][s] = w;
-      den += w * sm_l[j][s];
-    }
-    sm_inv[j] = 1.0f / den;
+  const float sink = a.sinks ? a.sinks[h] * kLog2e : -INFINITY;
+  const float M = fmaxf(wave_max(m), sink);
+  const float e = lane < n ? __builtin_amdgcn_exp2f(m - M) : 0.0f;
+  const float den = wave_sum(e * l) + (a.sinks ? __builtin_amdgcn_exp2f(sink - M) : 0.0f);
+  float o[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) o[v] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < PRE; ++s) {
+    const float es = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), s));
+#pragma unroll
+    for (int v = 0; v < V; ++v) o[v] += es * pre[s][v];
   }
-  __syncthreads();
-  for (int idx = tid; idx < a.group * D; idx += blockDim.x) {
-    const int j = idx / D, d = idx % D;
-    const float* op = a.ws_o + (base + j) * D + d;
-    float num = 0.0f;
-#pragma unroll 8
-    for (int32_t s = 0; s < n; ++s) num += sm_w[j][s] * op[(int64_t)s * a.H * D];
-    a.out[((int64_t)b * a.H + g * a.group + j) * D + d] = (uint16_t)f32_to_bf16_bits(num * sm_inv[j]);
+  for (int32_t s = PRE; s < n; ++s) {
+    const float es = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), s));
+#pragma unroll
+    for (int v = 0; v < V; ++v) o[v] += es * ob[s * sstride + v];
   }
+  const float inv = 1.0f / den;
+  uint16_t* dst = a.out + ((int64_t)b * a.H + h) * D + V * lane;
+#pragma unroll
+  for (int v = 0; v < V; ++v) dst[v] = (uint16_t)f32_to_bf16_bits(o[v] * inv);
 }
 
 // Rows with no split at all (seq_len 1) get their output from this pass: only the own token (and the sink).
@@ -484,7 +489,7 @@ static void launch_gqa(const GqaArgs& a, int depth, bool any_lone, hipStream_t s
   }
   if (a.max_splits > 1) {
     timing_events(1, &t0, &t1);
-    hipExtLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.B, a.G), dim3(256), 0, s, t0, t1, 0, a);
+    hipExtLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.B, a.H), dim3(64), 0, s, t0, t1, 0, a);
   }
   if (any_lone) hipLaunchKernelGGL((gqa_lone_token_kernel<D, FP8>), dim3(a.B, a.G), dim3(128), 0, s, a);
   timing_end_call();
@@ -533,7 +538,7 @@ extern "C" int sna_paged_decode_gqa(const void* q, const void* k_cache, const vo
   if (workspace_bytes < need)
     return fail(SNA_ERR_WORKSPACE, "paged_decode_gqa: workspace of %lld bytes, the plan needs %lld",
                 (long long)workspace_bytes, (long long)need);
-  if (num_kv_heads > 65535) return fail(SNA_ERR_INVALID_ARGUMENT, "paged_decode_gqa: grid too large");
+  if (num_q_heads > 65535) return fail(SNA_ERR_INVALID_ARGUMENT, "paged_decode_gqa: grid too large");
 
   GqaArgs a;
   a.q = (const uint16_t*)q;

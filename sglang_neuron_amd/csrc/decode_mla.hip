@@ -160,17 +160,6 @@ struct TileGeo {
 // Dword 3 of a raw buffer resource on gfx9-family chips (no format conversion, no swizzle).
 constexpr int kBufferFlags = 0x00020000;
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
 // Two query dwords of a ROWS640 latent step: bytes 2i + bb of the step hold dim (bb ? y : x)[i], i < 4, from the
 // bf16 pairs x = x0 | x1 << 16 and y = y0 | y1 << 16.
 __device__ __forceinline__ void interleave_pairs(uint32_t x, uint32_t y, uint32_t& d0, uint32_t& d1) {

@@ -178,7 +178,7 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
       int64_t n = 0;
       for (int32_t b = 0; b < B; ++b) n += host_splits(len_of(b), win, tile, split_tiles);
       if (n * ctas_per_item <= target) break;
-      split_tiles = std::min(split_tiles + (kind != 0 ? waves : 1), cap);
+      split_tiles = std::min(split_tiles + 1, cap);
     }
   }
   // the combine passes hold at most kMaxSplits weights per row: grow the split until every row fits

@@ -8,9 +8,10 @@
 //
 // Lane roles in a wave (lane = 16 * g4 + li):
 //   QK   S^T[key, head] = K[key, :] . Q[head, :]   with v_mfma_f32_16x16x32_bf16, M = 16 keys, N = 16 heads (the
-//        group's heads, zero-padded), K = head_dim in steps of 32. Lane (g4, li) feeds key li's elements
-//        [D/4 * g4, D/4 * (g4 + 1)) and head li's query elements over the same range. A and B use one K-index map,
-//        so the contraction pairs them however the instruction orders K internally.
+//        group's heads, zero-padded), K = head_dim in steps of 32. Lane (g4, li) feeds key li's 16-byte chunks
+//        4 c + g4 (so one load instruction reads 64 contiguous bytes of each of 16 keys) and head li's query
+//        elements of the same dims. A and B use one K-index map, so the contraction pairs them however the
+//        instruction orders K internally.
 //   out  lane (g4, j) holds S^T[4 g4 + r, j], r = 0..3, for each half-tile: 8 keys of head j.
 //   PV   O^T[d, head] = V^T[d, keys] . P^T[keys, head]   with v_mfma_f32_16x16x32_bf16, K = the tile's 32 keys,
 //        ordered so that lane (g4, *) supplies keys {4 g4 .. 4 g4 + 3} of both half-tiles: exactly the probabilities
@@ -94,7 +95,6 @@ void gqa_decode_kernel(GqaArgs a) {
   using Tile = GqaTile<D, FP8>;
   constexpr int ESZ = Tile::ESZ;
   constexpr int STEPS = D / 32;  // QK MFMA steps
-  constexpr int KE = D / 4;      // K elements per lane per key
   constexpr int KB = Tile::KB;
   constexpr int VE = D / 16;     // V elements per lane per key (= PV d-tiles)
   constexpr int VB = Tile::VB;
@@ -119,15 +119,18 @@ void gqa_decode_kernel(GqaArgs a) {
   const int32_t t_first = kr.lo / 32 + split * a.split_tiles;
   const int32_t t_last = min(t_first + a.split_tiles, (kr.hi + 31) / 32);
 
-  // Query operand: lane (g4, li) holds head li's elements [KE * g4, KE * g4 + KE) as packed bf16.
+  // Query operand: in step s lane (g4, li) holds head li's 8 elements from dim CE (4 c + g4) + w, with CE the
+  // elements of a 16-byte cache chunk and 8 s = CE c + w: the dims of the key bytes it feeds in that step.
+  constexpr int CE = 16 / ESZ;
   uint32_t qv[STEPS][4];
   {
     const bool live = li < a.group;
     const int32_t h = g * a.group + (live ? li : 0);
-    const uint16_t* qp = a.q + ((int64_t)b * a.H + h) * D + KE * g4;
+    const uint16_t* qp = a.q + ((int64_t)b * a.H + h) * D;
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
-      const uint4 w = live ? ld16(qp + 8 * s) : make_uint4(0, 0, 0, 0);
+      const int dim = CE * (4 * (8 * s / CE) + g4) + (8 * s) % CE;
+      const uint4 w = live ? ld16(qp + dim) : make_uint4(0, 0, 0, 0);
       qv[s][0] = w.x;
       qv[s][1] = w.y;
       qv[s][2] = w.z;
@@ -151,7 +154,9 @@ void gqa_decode_kernel(GqaArgs a) {
       T.pvalid[hf] = e >= 0 && (int64_t)e < a.num_blocks;
       const int32_t pg = T.pvalid[hf] ? e : 0;
       const int64_t blk = ((int64_t)pg * a.G + g) * head_stride + (int64_t)((T.T0 + 16 * hf) % a.P) * D * ESZ;
-      load_bytes<KB>(a.k_cache + blk + (int64_t)li * D * ESZ + KB * g4, T.k[hf]);
+      const uint8_t* kp = a.k_cache + blk + (int64_t)li * D * ESZ + 16 * g4;
+#pragma unroll
+      for (int c = 0; c < KB / 16; ++c) load_bytes<16>(kp + 64 * c, *reinterpret_cast<uint32_t(*)[4]>(&T.k[hf][4 * c]));
 #pragma unroll
       for (int e4 = 0; e4 < 4; ++e4)
         load_bytes<VB>(a.v_cache + blk + (int64_t)(4 * g4 + e4) * D * ESZ + VB * li, T.v[4 * hf + e4]);

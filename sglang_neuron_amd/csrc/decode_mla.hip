@@ -15,15 +15,16 @@
 // workgroup first resolves every index of its split to a row id in LDS (index -> block -> row). The own row is
 // quantized as the store quantizes it and attended as a one-key tile by one wave of the row's first split.
 //
-// Lane roles (lane = 16 * g4 + li), 16-key tiles:
-//   QK   S^T[key, head] = K[key, :] . Q[head, :]   v_mfma_f32_16x16x32_bf16, 18 steps over the 576 dims. In step pair
-//        k lane (g4, li) feeds the 16 bytes of chunk 4 k + g4 of key li's row (ROWS640: the rope chunks 4 s + g4
-//        first, then the latent chunks 8 + 4 (k - 1) + g4), and head li's query elements of the same dims, held in
-//        registers for the whole split.
-//   PV   O^T[latent byte, head] = V^T[byte, keys] . P^T[keys, head]   v_mfma_f32_16x16x16_bf16, K = the 16 keys,
-//        lane (g4, *) supplying keys 4 g4 .. 4 g4 + 3, the S^T rows it holds. For d-tile (q, r), lane (g4, i) reads
-//        dword (64 q + 4 i) of rows 4 g4 .. 4 g4 + 3, transposes the 4x4 bytes and feeds byte r of each.
-//   acc  lane (g4, j) accumulates head j at latent bytes 64 q + 16 g4 + 4 r' + r  (q < 8, r < 4, r' < 4).
+// Lane roles (lane = 16 * g4 + li), 16-key tiles; slot i of a tile (a row of S^T, a K index of PV) holds key
+// key_of(i): the even keys in slots 0 .. 7, the odd ones in 8 .. 15.
+//   QK   S^T[slot, head] = K[key, :] . Q[head, :]   v_mfma_f32_16x16x32_bf16, 18 steps over the 576 dims. In step
+//        pair k lane (g4, li) feeds the 16 bytes of chunk 4 k + g4 of key key_of(li)'s row (ROWS640: the rope chunks
+//        4 s + g4 first, then the latent chunks 8 + 4 (k - 1) + g4), and head li's query elements of the same dims
+//        (from LDS).
+//   PV   O^T[latent byte, head] = V^T[byte, slots] . P^T[slots, head]   v_mfma_f32_16x16x16_bf16, K = the 16 slots,
+//        lane (g4, *) supplying slots 4 g4 .. 4 g4 + 3, the S^T rows it holds. One ds_read_b64_tr_b8 per 32 latent
+//        bytes hands lane (g4, j) bytes 32 s + j and 32 s + 16 + j of those 4 slots' keys: d-tiles 2 s and 2 s + 1.
+//   acc  lane (g4, j) accumulates head j at latent bytes 64 q + 16 r + 4 g4 + r'  (acc[q][r][r'], q < 8, r, r' < 4).
 #include "sna_device.h"
 #include "sna_host.h"
 
@@ -54,11 +55,15 @@ struct MlaArgs {
   int64_t num_blocks;
   float sm_scale;
   int32_t split_tiles, n_work, max_splits;
-  float* ws_o;   // [B, max_splits, H, 512]  unnormalized partials, latent-byte order
+  float* ws_o;   // [B, max_splits, H, 512]  unnormalized partials, latent-dim order
   float* ws_ml;  // [B, max_splits, H, 2]
   uint16_t* out;
   float* lse_out;
 };
+
+// The key in slot i of a tile. In a PV read, lanes 0 .. 31 then touch the 8 even rows and lanes 32 .. 63 the 8 odd
+// ones; with the row strides below, 8 even rows fall in 8 distinct 8-bank blocks.
+__device__ __forceinline__ int key_of(int i) { return 2 * (i & 7) + (i >> 3); }
 
 // latent byte (relative to the latent field) -> latent dim, for ROWS640
 __device__ __forceinline__ int32_t latent_dim_of_byte(int32_t beta) {
@@ -367,11 +372,11 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
       for (int j = 0; j < NDMA; ++j)
         if (j < NDMA - 1 || lane < Geo::TAIL)
           dma_buffer16(rk, d + 1024 * j, dma_src[j]);
-      // the tile's 16 per-token scales, consecutive like its rows
+      // the tile's 16 per-token scales (consecutive like its rows), in slot order
       const __amdgpu_buffer_rsrc_t rs =
           __builtin_amdgcn_make_buffer_rsrc((void*)(a.row_scale + row0), (short)0, 64, kBufferFlags);
       if (lane < 16)
-        dma_buffer4(rs, d + Geo::SCALES, 4u * (uint32_t)lane);
+        dma_buffer4(rs, d + Geo::SCALES, 4u * (uint32_t)key_of(lane));
     }
   };
 
@@ -394,28 +399,23 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
         *reinterpret_cast<uint4*>(T + r * RS + (SPARSE ? 128 : 0) + 16 * c) = make_uint4(0, 0, 0, 0);
     }
   };
-  // PV of one tile: O^T += V^T P^T over 32 d-tiles.
+  // PV of one tile: O^T += V^T P^T over 32 d-tiles. Lane (g4, j) points the transposing read at slot
+  // 4 g4 + (j / 2) % 4, bytes 16 (j / 8) + 8 (j % 2) of each 32-byte step, so that rows 0 .. 3 of its group's 8x16
+  // byte matrix are slots 4 g4 .. 4 g4 + 3 at bytes 32 s .. 32 s + 15 and rows 4 .. 7 the same slots 16 bytes on.
   auto pv = [&](const uint8_t* T, const uint32_t (&pop)[2]) {
-    const uint8_t* Tv = T + 4 * g4 * RS + 4 * li + (SPARSE ? 128 : 0);
+    const uint8_t* Tv = T + key_of(4 * g4 + ((li >> 1) & 3)) * RS + (SPARSE ? 128 : 0) + 16 * (li >> 3) + 8 * (li & 1);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      uint32_t w[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        w[e] = *reinterpret_cast<const uint32_t*>(Tv + e * RS + 64 * q);
-      }
-      uint32_t xr[4];
-      transpose4x4_bytes(w, xr);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        uint32_t op[2];
-        fp8x4_to_bf16x4(xr[r], op[0], op[1]);
-        acc[q][r] = mfma_16x16x16_bf16(op, pop, acc[q][r]);
-      }
+    for (int s = 0; s < 16; ++s) {
+      const uint2 t = lds_read_tr8(Tv + 32 * s);
+      uint32_t op[2];
+      fp8x4_to_bf16x4(t.x, op[0], op[1]);
+      acc[s >> 1][2 * (s & 1)] = mfma_16x16x16_bf16(op, pop, acc[s >> 1][2 * (s & 1)]);
+      fp8x4_to_bf16x4(t.y, op[0], op[1]);
+      acc[s >> 1][2 * (s & 1) + 1] = mfma_16x16x16_bf16(op, pop, acc[s >> 1][2 * (s & 1) + 1]);
     }
   };
 
-  // Per-token scales of keys 4 g4 .. 4 g4 + 3 of the tile at T (1 for the sparse format).
+  // Per-token scales of slots 4 g4 .. 4 g4 + 3 of the tile at T (1 for the sparse format).
   auto key_scales = [&](const uint8_t* T, float (&ks)[4]) {
     ks[0] = ks[1] = ks[2] = ks[3] = 1.0f;
     if constexpr (!SPARSE) {
@@ -423,12 +423,12 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
       ks[0] = s4.x, ks[1] = s4.y, ks[2] = s4.z, ks[3] = s4.w;
     }
   };
-  // The tile's scores in the log2 domain (x[r]: key 4 g4 + r, head li; -inf when masked) and their maximum per head.
+  // The tile's scores in the log2 domain (x[r]: slot 4 g4 + r, head li; -inf when masked) and their maximum per head.
   auto scores = [&](const uint8_t* T, uint32_t vmask, float (&x)[4], float& tmax) {
     float ks[4];
     [[clang::always_inline]] key_scales(T, ks);
     // S^T = K Q^T: three accumulators keep three independent MFMA chains in flight
-    const uint8_t* Tq = T + li * RS + 16 * g4;
+    const uint8_t* Tq = T + key_of(li) * RS + 16 * g4;
     f32x4_t scp[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int k = 0; k < 9; ++k) {
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
     tmax = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const bool ok = (vmask >> (4 * g4 + r)) & 1u;
+      const bool ok = (vmask >> key_of(4 * g4 + r)) & 1u;
       x[r] = ok ? sc[r] * base_scale * ks[r] : -INFINITY;
       tmax = fmaxf(tmax, x[r]);
     }
@@ -489,7 +489,7 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
     float pw[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const bool ok = (vmask >> (4 * g4 + r)) & 1u;
+      const bool ok = (vmask >> key_of(4 * g4 + r)) & 1u;
       const float p = __builtin_amdgcn_exp2f(x[r] - m_ref);
       l_run += p;
       // V is dequantized through P: p' = p * scale(key); a masked key has p = 0
@@ -684,40 +684,39 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
       }
     }
     if (li >= nh) continue;
-    // o[t]: latent byte 64 q + 16 g4 + t, t = 4 r' + r
-    float o[16];
+    // v[r][r']: latent byte beta + r' with beta = 64 q + 16 r + 4 g4; ROWS640 bytes beta, beta + 2 are dims d0, d0 + 1
+    // and bytes beta + 1, beta + 3 dims d0 + 128, d0 + 129
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) o[4 * rr + r] = v[r][rr] * oscale;
-    const int beta0 = 64 * q + 16 * g4;
-    // the 16 bytes' dims: ROWS576 beta0 + t; ROWS640 two runs of 8, base + i (t = 2 i) and base + 128 + i (t = 2 i + 1)
-    const int dim0 = SPARSE ? 256 * (beta0 >> 8) + ((beta0 & 255) >> 1) : beta0;
-    float run[2][8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      run[0][i] = SPARSE ? o[2 * i] : o[i];
-      run[1][i] = SPARSE ? o[2 * i + 1] : o[8 + i];
-    }
-    const int run_off = SPARSE ? 128 : 8;
+    for (int r = 0; r < 4; ++r) v[r] *= oscale;
     if constexpr (FINAL) {
       const float inv = 1.0f / L;
-      uint16_t* dst = a.out + ((int64_t)b * a.H + h) * kLatent + dim0;
+      uint16_t* dst = a.out + ((int64_t)b * a.H + h) * kLatent;
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        uint32_t pk[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pk[i] = pack_bf16x2(run[u][2 * i] * inv, run[u][2 * i + 1] * inv);
-        *reinterpret_cast<uint4*>(dst + u * run_off) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+      for (int r = 0; r < 4; ++r) {
+        const int beta = 64 * q + 16 * r + 4 * g4;
+        if constexpr (!SPARSE) {
+          *reinterpret_cast<uint2*>(dst + beta) =
+              make_uint2(pack_bf16x2(v[r][0] * inv, v[r][1] * inv), pack_bf16x2(v[r][2] * inv, v[r][3] * inv));
+        } else {
+          const int d0 = latent_dim_of_byte(beta);
+          *reinterpret_cast<uint32_t*>(dst + d0) = pack_bf16x2(v[r][0] * inv, v[r][2] * inv);
+          *reinterpret_cast<uint32_t*>(dst + d0 + 128) = pack_bf16x2(v[r][1] * inv, v[r][3] * inv);
+        }
       }
       if (a.lse_out && q == 0 && g4 == 0) a.lse_out[(int64_t)b * a.H + h] = (M + __log2f(L)) * 0.6931471805599453f;
     } else {
       const int64_t row = ((int64_t)b * S + split) * a.H + h;
-      float* dst = a.ws_o + row * kLatent + dim0;
+      float* dst = a.ws_o + row * kLatent;
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        *reinterpret_cast<float4*>(dst + u * run_off) = make_float4(run[u][0], run[u][1], run[u][2], run[u][3]);
-        *reinterpret_cast<float4*>(dst + u * run_off + 4) = make_float4(run[u][4], run[u][5], run[u][6], run[u][7]);
+      for (int r = 0; r < 4; ++r) {
+        const int beta = 64 * q + 16 * r + 4 * g4;
+        if constexpr (!SPARSE) {
+          *reinterpret_cast<float4*>(dst + beta) = make_float4(v[r][0], v[r][1], v[r][2], v[r][3]);
+        } else {
+          const int d0 = latent_dim_of_byte(beta);
+          *reinterpret_cast<float2*>(dst + d0) = make_float2(v[r][0], v[r][2]);
+          *reinterpret_cast<float2*>(dst + d0 + 128) = make_float2(v[r][1], v[r][3]);
+        }
       }
       if (q == 0 && g4 == 0) *reinterpret_cast<float2*>(a.ws_ml + row * 2) = make_float2(M, L);
     }

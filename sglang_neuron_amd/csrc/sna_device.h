@@ -62,6 +62,22 @@ __device__ __forceinline__ float e4m3fn_to_f32(uint32_t b) {
   return __uint_as_float(sign | ((e + 120u) << 23) | (m << 20));
 }
 
+// An element v with |v| < 256 and at most 8 significant bits (a bf16 value times a power of two) as v = hi + lo / 16
+// with hi its top 4 significant bits (truncated) and lo the next 4 times 16: both are e4m3fn values, exactly (but for
+// elements below the e4m3fn normal range, which the conversion rounds).
+__device__ __forceinline__ void split_q(float v, float& hi, float& lo) {
+  hi = __uint_as_float(__float_as_uint(v) & 0xfff00000u);
+  lo = (v - hi) * 16.0f;
+}
+// Four floats in the e4m3fn range to e4m3fn bytes 0..3 (round to nearest even; an exactly representable value is
+// unchanged).
+__device__ __forceinline__ uint32_t pack_e4m3fn_x4(float a, float b, float c, float d) {
+  typedef short s16x2_t __attribute__((ext_vector_type(2)));
+  s16x2_t w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32((s16x2_t){0, 0}, a, b, 1.0f, false);
+  w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, c, d, 1.0f, true);
+  return (uint32_t)(uint16_t)w[0] | ((uint32_t)(uint16_t)w[1] << 16);
+}
+
 // NaN-preserving clamp to the e4m3fn range: comparisons with NaN are false, so NaN passes through.
 __device__ __forceinline__ float clamp_fp8(float x) {
   return x > kFp8Max ? kFp8Max : (x < -kFp8Max ? -kFp8Max : x);
@@ -98,25 +114,37 @@ __device__ __forceinline__ void fp8x4_to_bf16x4(uint32_t w, uint32_t& lo, uint32
   hi = __builtin_bit_cast(uint32_t, b);
 }
 
+// ds_read_b64_tr_b8: in each 16-lane group the lanes' 8-byte chunks (8-byte aligned) form 8 rows of 16 bytes, row k
+// being the chunks of lanes 2 k and 2 k + 1; lane j receives column j, so byte k of its result is byte j of row k.
+__device__ __forceinline__ uint2 lds_read_tr8(const uint8_t* p) {
+  typedef int32_t i32x2_t __attribute__((ext_vector_type(2)));
+  const i32x2_t r = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) i32x2_t*)(uint8_t*)p);
+  return make_uint2((uint32_t)r.x, (uint32_t)r.y);
+}
+
 // Loads straight into LDS (lane i's bytes land at LDS address m0 + size * i), written as inline assembly so that the
 // compiler does not see them: it would otherwise drain every load in flight before any LDS read it cannot prove
 // disjoint from them. Callers wait for them with wait_vmcnt, counting every such load they issued after the one they
 // need. The buffer forms read through a buffer resource (a uniform base and size in SGPRs, a 32-bit offset per lane;
-// reads past the size return zeros). The s_nop covers the m0 write -> LDS-DMA hazard.
+// reads past the size return zeros). The LDS address is wave-uniform (readfirstlane keeps it in an SGPR for m0); the
+// s_nop covers the m0 write -> LDS-DMA hazard.
 typedef __attribute__((address_space(3))) void lds_ptr_t;
 __device__ __forceinline__ uint32_t lds_address(const lds_ptr_t* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
 }
 __device__ __forceinline__ void dma_buffer16(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(r)
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(r)
                : "memory");
 }
 __device__ __forceinline__ void dma_buffer4(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(r)
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(r)
                : "memory");
 }
 __device__ __forceinline__ void dma_global16(const void* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory");
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src) : "memory");
 }
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -151,6 +179,16 @@ __device__ __forceinline__ f32x4_t mfma_16x16x32_bf16(const uint32_t (&a)[4], co
                                                   c, 0, 0, 0);
 }
 
+// FP8 (e4m3fn) A and B, K = 128; lane (g4, i) supplies row i of A and column i of B at the same 32 K positions, and the
+// block scale 2^(scale_b - 127) of its B block (A's scale is 1).
+typedef int32_t i32x8_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x4_t mfma_16x16x128_fp8(const uint32_t (&a)[8], const uint32_t (&b)[8], f32x4_t c,
+                                                     int32_t scale_b) {
+  i32x8_t av, bv;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) av[i] = (int32_t)a[i], bv[i] = (int32_t)b[i];
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 0, 0, 0, 127, 0, scale_b);
+}
 __device__ __forceinline__ f32x4_t mfma_16x16x16_bf16(const uint32_t (&a)[2], const uint32_t (&b)[2], f32x4_t c) {
   typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
   u32x2_t av = {a[0], a[1]};
@@ -173,10 +211,17 @@ __device__ __forceinline__ uint2 ld8(const void* p) { return *reinterpret_cast<c
 __device__ __forceinline__ uint32_t ld4(const void* p) { return *reinterpret_cast<const uint32_t*>(p); }
 
 // Wave64 reductions across the four 16-lane groups (lanes l, l^16, l^32, l^48 hold the same MFMA column).
+// Reductions over the 4 lanes li, li + 16, li + 32, li + 48 of a wave, through the permlane swaps (no LDS round
+// trip): permlane32_swap of v with itself leaves lane l holding v[l] and v[l ^ 32] in its two results, and
+// permlane16_swap v[l] and v[l ^ 16].
+__device__ __forceinline__ float xor32_partner_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 __device__ __forceinline__ float max_across_groups(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  v = fmaxf(v, __shfl_xor(v, 32, 64));
-  return v;
+  v = xor32_partner_max(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -189,9 +234,10 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 __device__ __forceinline__ float sum_across_groups(float v) {
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(t[0]) + __uint_as_float(t[1]);
 }
 
 // ---- split-K work decomposition ----

@@ -143,17 +143,40 @@ void gqa_decode_kernel(GqaArgs a) {
   const float qk_scale = a.sm_scale * kscale * kLog2e;
   const int64_t head_stride = (int64_t)a.P * D * ESZ;  // bytes of one (page, head) block
   const int32_t* trow = a.table + (int64_t)b * a.table_stride;
+  // Table columns and in-page slots: shifts when the page size is a power of two (uniform).
+  const bool p_pow2 = (a.P & (a.P - 1)) == 0;
+  const int p_shift = __builtin_ctz((uint32_t)a.P);
+  auto column = [&](int32_t key) -> int32_t { return p_pow2 ? key >> p_shift : key / a.P; };
+  auto in_page = [&](int32_t key) -> int32_t { return p_pow2 ? key & (a.P - 1) : key % a.P; };
+  // The split's block-table entries, when they fit in 256: column col0 + 64 r + lane in pg[r], -1 past the table
+  // (then a tile's page is a readlane instead of a scalar load and its wait).
+  const int32_t col0 = column(t_first * 32);
+  const bool pre = column(t_last * 32 - 1) - col0 < 256;
+  int32_t pg[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int32_t c = col0 + 64 * r + lane;
+    pg[r] = (pre && c < a.table_width) ? trow[c] : -1;
+  }
+  auto table_entry = [&](int32_t col) -> int32_t {
+    if (pre) {
+      const int32_t c = col - col0;
+      const int32_t v = c < 64 ? pg[0] : (c < 128 ? pg[1] : (c < 192 ? pg[2] : pg[3]));
+      return __builtin_amdgcn_readlane(v, c & 63);
+    }
+    return col < a.table_width ? ld_const(trow + col) : -1;
+  };
 
   auto load_tile = [&](Tile& T, int32_t tile) {
-    T.T0 = __builtin_amdgcn_readfirstlane(tile * 32);  // uniform: the page lookups below are scalar loads
+    T.T0 = __builtin_amdgcn_readfirstlane(tile * 32);  // uniform: the page lookups below are scalar
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       // page of the half-tile (uniform); an entry outside the table or the pool reads page 0 and is masked
-      const int32_t col = (T.T0 + 16 * hf) / a.P;
-      const int32_t e = col < a.table_width ? ld_const(trow + col) : -1;
+      const int32_t col = column(T.T0 + 16 * hf);
+      const int32_t e = table_entry(col);
       T.pvalid[hf] = e >= 0 && (int64_t)e < a.num_blocks;
-      const int32_t pg = T.pvalid[hf] ? e : 0;
-      const int64_t blk = ((int64_t)pg * a.G + g) * head_stride + (int64_t)((T.T0 + 16 * hf) % a.P) * D * ESZ;
+      const int32_t pgid = T.pvalid[hf] ? e : 0;
+      const int64_t blk = ((int64_t)pgid * a.G + g) * head_stride + (int64_t)in_page(T.T0 + 16 * hf) * D * ESZ;
       const uint8_t* kp = a.k_cache + blk + (int64_t)li * D * ESZ + 16 * g4;
 #pragma unroll
       for (int c = 0; c < KB / 16; ++c) load_bytes<16>(kp + 64 * c, *reinterpret_cast<uint32_t(*)[4]>(&T.k[hf][4 * c]));
@@ -374,10 +397,12 @@ void gqa_decode_kernel(GqaArgs a) {
 
 // Merge of a row's splits, one wave per (row, query head): out = sum_s e_s o_s / (sum_s e_s l_s + e_sink), with
 // e_s = exp2(m_s - M) and M the maximum over the splits and the sink. Lane s holds split s's weight; lane i holds the
-// head dims D / 64 * i .. + D / 64. The partials of the first splits load before the weights are known.
+// head dims D / 64 * i .. + D / 64. The partials stream in chunks of 16 splits, each chunk's loads all in flight
+// together (the first before the weights are known).
 template <int D>
 __global__ __launch_bounds__(64) void gqa_combine_kernel(GqaArgs a) {
   constexpr int V = D / 64;
+  constexpr int CH = 16;
   const int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
   const int32_t S = a.max_splits;
   const int32_t n = min(splits_of<32>(ld_const(a.seq_lens + b), a.window, a.split_tiles), S);
@@ -385,12 +410,11 @@ __global__ __launch_bounds__(64) void gqa_combine_kernel(GqaArgs a) {
   const int64_t row0 = (int64_t)b * S * a.H + h;
   const float* ob = a.ws_o + row0 * D + V * lane;
   const int64_t sstride = (int64_t)a.H * D;
-  constexpr int PRE = 8;
-  float pre[PRE][V];
+  float x[CH][V];
 #pragma unroll
-  for (int s = 0; s < PRE; ++s)
+  for (int k = 0; k < CH; ++k)
 #pragma unroll
-    for (int v = 0; v < V; ++v) pre[s][v] = s < n ? ob[s * sstride + v] : 0.0f;
+    for (int v = 0; v < V; ++v) x[k][v] = k < n ? ob[k * sstride + v] : 0.0f;
   float m = -INFINITY, l = 0.0f;
   if (lane < n) {
     const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + (row0 + (int64_t)lane * a.H) * 2);
@@ -404,16 +428,21 @@ __global__ __launch_bounds__(64) void gqa_combine_kernel(GqaArgs a) {
   float o[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) o[v] = 0.0f;
+  for (int32_t base = 0; base < n; base += CH) {
+    if (base > 0) {
 #pragma unroll
-  for (int s = 0; s < PRE; ++s) {
-    const float es = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), s));
+      for (int k = 0; k < CH; ++k)
 #pragma unroll
-    for (int v = 0; v < V; ++v) o[v] += es * pre[s][v];
-  }
-  for (int32_t s = PRE; s < n; ++s) {
-    const float es = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), s));
+        for (int v = 0; v < V; ++v) x[k][v] = base + k < n ? ob[(base + k) * sstride + v] : 0.0f;
+    }
 #pragma unroll
-    for (int v = 0; v < V; ++v) o[v] += es * ob[s * sstride + v];
+    for (int k = 0; k < CH; ++k) {
+      if (base + k < n) {
+        const float es = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), base + k));
+#pragma unroll
+        for (int v = 0; v < V; ++v) o[v] += es * x[k][v];
+      }
+    }
   }
   const float inv = 1.0f / den;
   uint16_t* dst = a.out + ((int64_t)b * a.H + h) * D + V * lane;

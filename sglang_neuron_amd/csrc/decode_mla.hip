@@ -723,28 +723,26 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
   }
 }
 
-// Merge of a row's splits, one wave per (row, head): out = sum_s e_s o_s / sum_s e_s l_s, lse = M + log(sum), with
-// e_s = exp2(m_s - M); lane s holds split s's weight and lane i the latent dims 8 i .. 8 i + 7.
+// Merge of a row's splits, two waves per (row, head): out = sum_s e_s o_s / sum_s e_s l_s, lse = M + log(sum), with
+// e_s = exp2(m_s - M). Lane s holds split s's weight; wave w, lane i the latent dims 256 w + 4 i .. + 3. The
+// partials stream in chunks of 16 splits, each chunk's loads all in flight together (the first before the weights
+// are known).
 template <int FMT>
-__global__ __launch_bounds__(64) void mla_combine_kernel(MlaArgs a) {
+__global__ __launch_bounds__(128) void mla_combine_kernel(MlaArgs a) {
   constexpr bool SPARSE = FMT == ROWS640;
-  const int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+  constexpr int CH = 16;
+  const int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int32_t n = min(SPARSE ? splits_of<16>(a.n_indices + 1, 0, a.split_tiles)
                                : splits_of<16>(ld_const(a.seq_lens + b), 0, a.split_tiles),
                         a.max_splits);
   if (n == 0) return;  // a row with no prior key: the lone-row kernel writes it
   const int64_t row0 = (int64_t)b * a.max_splits * a.H + h;
-  const float* ob = a.ws_o + row0 * kLatent + 8 * lane;
+  const float* ob = a.ws_o + row0 * kLatent + 256 * w + 4 * lane;
   const int64_t sstride = (int64_t)a.H * kLatent;
-  constexpr int PRE = 8;  // splits whose partials load before the weights are known
-  float4 pre[PRE][2];
+  float4 x[CH];
 #pragma unroll
-  for (int s = 0; s < PRE; ++s) {
-    if (s < n) {
-      pre[s][0] = *reinterpret_cast<const float4*>(ob + s * sstride);
-      pre[s][1] = *reinterpret_cast<const float4*>(ob + s * sstride + 4);
-    }
-  }
+  for (int k = 0; k < CH; ++k)
+    if (k < n) x[k] = *reinterpret_cast<const float4*>(ob + k * sstride);
   float m = -INFINITY, l = 0.0f;
   if (lane < n) {
     const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + (row0 + (int64_t)lane * a.H) * 2);
@@ -754,28 +752,25 @@ __global__ __launch_bounds__(64) void mla_combine_kernel(MlaArgs a) {
   const float M = wave_max(m);
   const float e = lane < n ? __builtin_amdgcn_exp2f(m - M) : 0.0f;
   const float den = wave_sum(e * l);
-  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int32_t base = 0; base < n; base += CH) {
+    if (base > 0) {
 #pragma unroll
-  for (int s = 0; s < PRE; ++s) {
-    if (s < n) {
-      const float es = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), s));
-      o[0] += es * pre[s][0].x, o[1] += es * pre[s][0].y, o[2] += es * pre[s][0].z, o[3] += es * pre[s][0].w;
-      o[4] += es * pre[s][1].x, o[5] += es * pre[s][1].y, o[6] += es * pre[s][1].z, o[7] += es * pre[s][1].w;
+      for (int k = 0; k < CH; ++k)
+        if (base + k < n) x[k] = *reinterpret_cast<const float4*>(ob + (base + k) * sstride);
+    }
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      if (base + k < n) {
+        const float es = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), base + k));
+        o.x += es * x[k].x, o.y += es * x[k].y, o.z += es * x[k].z, o.w += es * x[k].w;
+      }
     }
   }
-  for (int32_t s = PRE; s < n; ++s) {
-    const float es = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), s));
-    const float4 x0 = *reinterpret_cast<const float4*>(ob + s * sstride);
-    const float4 x1 = *reinterpret_cast<const float4*>(ob + s * sstride + 4);
-    o[0] += es * x0.x, o[1] += es * x0.y, o[2] += es * x0.z, o[3] += es * x0.w;
-    o[4] += es * x1.x, o[5] += es * x1.y, o[6] += es * x1.z, o[7] += es * x1.w;
-  }
   const float inv = 1.0f / den;
-  uint32_t pk[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) pk[i] = pack_bf16x2(o[2 * i] * inv, o[2 * i + 1] * inv);
-  *reinterpret_cast<uint4*>(a.out + ((int64_t)b * a.H + h) * kLatent + 8 * lane) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-  if (a.lse_out && lane == 0) a.lse_out[(int64_t)b * a.H + h] = (M + __log2f(den)) * 0.6931471805599453f;
+  *reinterpret_cast<uint2*>(a.out + ((int64_t)b * a.H + h) * kLatent + 256 * w + 4 * lane) =
+      make_uint2(pack_bf16x2(o.x * inv, o.y * inv), pack_bf16x2(o.z * inv, o.w * inv));
+  if (a.lse_out && w == 0 && lane == 0) a.lse_out[(int64_t)b * a.H + h] = (M + __log2f(den)) * 0.6931471805599453f;
 }
 
 // A row with no prior key (paged seq_len 1, or an empty index list): the output is its own row's latent.
@@ -819,7 +814,7 @@ static void launch_mla(const MlaArgs& a, int32_t groups, int32_t grid_x, bool an
   }
   if (a.max_splits > 1) {
     timing_events(1, &t0, &t1);
-    hipExtLaunchKernelGGL((mla_combine_kernel<FMT>), dim3(a.B, a.H), dim3(64), 0, s, t0, t1, 0, a);
+    hipExtLaunchKernelGGL((mla_combine_kernel<FMT>), dim3(a.B, a.H), dim3(128), 0, s, t0, t1, 0, a);
   }
   if (any_lone) hipLaunchKernelGGL((mla_lone_row_kernel<FMT>), dim3(a.B, groups), dim3(256), 0, s, a);
   timing_end_call();

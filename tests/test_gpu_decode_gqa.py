@@ -20,6 +20,8 @@ CASES = [
     ("bf16-d64-g1", 1, {"B": 3, "H": 4, "G": 4, "d": 64, "lens": (2, 300)}),
     ("fp8-g16", 2, {"B": 2, "H": 32, "G": 2, "lens": (33, 900)}),
     ("fp8-page64", 2, {"B": 3, "P": 64, "lens": (50, 1500)}),
+    ("cfg2-32-splits", 2, {"B": 2, "lens": (8192, 8192)}),                # the combine's second chunk of 16 splits
+    ("cfg4-64-splits", 4, {"B": 2, "lens": (8000, 8192)}),                # 4 chunks, sinks
 ]
 
 

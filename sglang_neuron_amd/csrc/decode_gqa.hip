@@ -62,19 +62,19 @@ __device__ __forceinline__ void load_bytes(const uint8_t* p, uint32_t (&dst)[NB 
   if constexpr (NB % 16 == 0) {
 #pragma unroll
     for (int i = 0; i < NB / 16; ++i) {
-      const uint4 w = ld16(p + 16 * i);
+      const uint4 w = ld16_stream(p + 16 * i);
       dst[4 * i] = w.x;
       dst[4 * i + 1] = w.y;
       dst[4 * i + 2] = w.z;
       dst[4 * i + 3] = w.w;
     }
   } else if constexpr (NB == 8) {
-    const uint2 w = ld8(p);
+    const uint2 w = ld8_stream(p);
     dst[0] = w.x;
     dst[1] = w.y;
   } else {
     static_assert(NB == 4, "4, 8 or a multiple of 16 bytes");
-    dst[0] = ld4(p);
+    dst[0] = ld4_stream(p);
   }
 }
 

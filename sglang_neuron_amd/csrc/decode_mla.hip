@@ -202,7 +202,10 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
   __shared__ int32_t sm_rowid[SPARSE ? kMlaMaxSplitKeys : 1];
   __shared__ float sm_m[WAVES][16];
   __shared__ float sm_l[WAVES][16];
-  __shared__ __attribute__((aligned(16))) uint16_t sm_own[576];  // the own row (bf16), DMA'd during the prologue
+  // The own row in the pool's row format (its bytes stand for all 16 keys of a tile with row stride 0), then its
+  // scale repeated 16 times at kOwnScales.
+  constexpr int kOwnScales = 640;
+  __shared__ __attribute__((aligned(16))) uint8_t sm_own[kOwnScales + 64];
   __shared__ uint4 sm_q[18][64];
   // The merge exchange: block idx < 6 of sender w, 256 float4.
   static_assert(sizeof(float4) * WAVES * 6 * 256 <= sizeof(sm_ring), "the merge exchange lives in the ring");
@@ -271,15 +274,20 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
     }
     sm_q[s][ln] = w;
   }
-  // The own row is attended by one wave of the row's first split, after its tiles: the wave with the fewest.
+  // The own row is attended by one wave of the row's first split (the wave with the fewest tiles) before its tiles,
+  // while their first loads are in flight. Its bf16 elements 8 lane .. + 7 and 8 (lane + 64) .. + 7 (lane < 8) and
+  // its pool slot load here, with the compiler's other prologue loads.
   const int32_t ntiles = t_last - t_first;
   const bool own_wave = split == 0 && wave == ((ntiles % WAVES) == 0 ? WAVES - 1 : ntiles % WAVES);
-  // Its bytes land in LDS while the tiles stream: issued first, they are complete once the first tile's are.
+  uint4 own0 = make_uint4(0, 0, 0, 0), own1 = make_uint4(0, 0, 0, 0);
+  int64_t own_slot = -1;
+  uint32_t own_q[4] = {0, 0, 0, 0};  // ROWS576: the quantized bytes of those elements, for the deferred pool store
+  float own_s = 1.0f;
   if (own_wave) {
-    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.own + (int64_t)b * 576);
-    const uint32_t dst = lds_address((lds_void*)(lds_u8*)&sm_own[0]);
-    dma_global16(src + 16u * (uint32_t)lane, dst);
-    if (lane < 8) dma_global16(src + 1024u + 16u * (uint32_t)lane, dst + 1024);
+    const uint16_t* src = a.own + (int64_t)b * 576;
+    own0 = ld16(src + 8 * lane);
+    if (lane < 8) own1 = ld16(src + 8 * (lane + 64));
+    if (!SPARSE && hg == 0 && a.new_slots) own_slot = redirect_slot(a.new_slots[b], a.num_blocks * a.P);
   }
 
   // Sparse: every index of the split to a row id (-1: skipped), all loads of a stage in flight together.
@@ -402,8 +410,9 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
   // PV of one tile: O^T += V^T P^T over 32 d-tiles. Lane (g4, j) points the transposing read at slot
   // 4 g4 + (j / 2) % 4, bytes 16 (j / 8) + 8 (j % 2) of each 32-byte step, so that rows 0 .. 3 of its group's 8x16
   // byte matrix are slots 4 g4 .. 4 g4 + 3 at bytes 32 s .. 32 s + 15 and rows 4 .. 7 the same slots 16 bytes on.
-  auto pv = [&](const uint8_t* T, const uint32_t (&pop)[2]) {
-    const uint8_t* Tv = T + key_of(4 * g4 + ((li >> 1) & 3)) * RS + (SPARSE ? 128 : 0) + 16 * (li >> 3) + 8 * (li & 1);
+  // (rs: the tile's LDS row stride; 0 for the own row standing for all 16 keys.)
+  auto pv = [&](const uint8_t* T, const uint32_t (&pop)[2], int rs) {
+    const uint8_t* Tv = T + key_of(4 * g4 + ((li >> 1) & 3)) * rs + (SPARSE ? 128 : 0) + 16 * (li >> 3) + 8 * (li & 1);
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
       const uint2 t = lds_read_tr8(Tv + 32 * s);
@@ -415,20 +424,20 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
     }
   };
 
-  // Per-token scales of slots 4 g4 .. 4 g4 + 3 of the tile at T (1 for the sparse format).
-  auto key_scales = [&](const uint8_t* T, float (&ks)[4]) {
+  // Per-token scales of slots 4 g4 .. 4 g4 + 3 from the tile's 16 scales at S (1 for the sparse format).
+  auto key_scales = [&](const uint8_t* S, float (&ks)[4]) {
     ks[0] = ks[1] = ks[2] = ks[3] = 1.0f;
     if constexpr (!SPARSE) {
-      const float4 s4 = *reinterpret_cast<const float4*>(T + Geo::SCALES + 16 * g4);
+      const float4 s4 = *reinterpret_cast<const float4*>(S + 16 * g4);
       ks[0] = s4.x, ks[1] = s4.y, ks[2] = s4.z, ks[3] = s4.w;
     }
   };
   // The tile's scores in the log2 domain (x[r]: slot 4 g4 + r, head li; -inf when masked) and their maximum per head.
-  auto scores = [&](const uint8_t* T, uint32_t vmask, float (&x)[4], float& tmax) {
+  auto scores = [&](const uint8_t* T, uint32_t vmask, float (&x)[4], float& tmax, int rs, const uint8_t* S) {
     float ks[4];
-    [[clang::always_inline]] key_scales(T, ks);
+    [[clang::always_inline]] key_scales(S, ks);
     // S^T = K Q^T: three accumulators keep three independent MFMA chains in flight
-    const uint8_t* Tq = T + key_of(li) * RS + 16 * g4;
+    const uint8_t* Tq = T + key_of(li) * rs + 16 * g4;
     f32x4_t scp[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int k = 0; k < 9; ++k) {
@@ -482,10 +491,10 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
       for (int r = 0; r < 4; ++r) acc[q][r] *= alpha;
   };
   // The tile's probabilities against m_ref, folded into the row sum and, through PV, the accumulators.
-  auto accumulate = [&](uint8_t* T, uint32_t vmask, const float (&x)[4]) {
-    if (vmask != 0xffffu) [[clang::always_inline]] sanitize(T, vmask);
+  auto accumulate = [&](uint8_t* T, uint32_t vmask, const float (&x)[4], int rs, const uint8_t* S) {
+    if (rs != 0 && vmask != 0xffffu) [[clang::always_inline]] sanitize(T, vmask);
     float ks[4];
-    [[clang::always_inline]] key_scales(T, ks);
+    [[clang::always_inline]] key_scales(S, ks);
     float pw[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -496,7 +505,7 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
       pw[r] = ok ? p * ks[r] : 0.0f;
     }
     const uint32_t pop[2] = {pack_bf16x2(pw[0], pw[1]), pack_bf16x2(pw[2], pw[3])};
-    [[clang::always_inline]] pv(T, pop);
+    [[clang::always_inline]] pv(T, pop, rs);
   };
 
   // ---- the tile loop: wave w takes tiles t_first + w + WAVES i through its ring of DEPTH slots; DEPTH - 1 tiles'
@@ -525,6 +534,57 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
 #pragma unroll
     for (int i = 0; i < DEPTH - 1; ++i)
       if (i < mine) issue(ring + i * SLOT, t0 + i * WAVES);
+    // The own row, quantized as the store quantizes it, into sm_own in the pool's row format (LDS and registers only:
+    // nothing here may add to the VMEM count the waits below rely on).
+    if (own_wave) {
+      const uint32_t w[8] = {own0.x, own0.y, own0.z, own0.w, own1.x, own1.y, own1.z, own1.w};
+      if constexpr (FMT == ROWS576) {
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          m = fmaxf(m, fabsf(bf16_bits_to_f32(w[j] & 0xffffu)));
+          m = fmaxf(m, fabsf(bf16_bits_to_f32(w[j] >> 16)));
+        }
+        own_s = scale_from_absmax(wave_max(m));
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+          if (part == 1 && lane >= 8) continue;
+          uint32_t o[2] = {0, 0};
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const uint32_t bits = (w[part * 4 + (i >> 1)] >> ((i & 1) * 16)) & 0xffffu;
+            o[i >> 2] |= quantize_e4m3fn(bits, own_s) << ((i & 3) * 8);
+          }
+          own_q[2 * part] = o[0];
+          own_q[2 * part + 1] = o[1];
+          *reinterpret_cast<uint2*>(&sm_own[8 * (lane + 64 * part)]) = make_uint2(o[0], o[1]);
+        }
+        if (lane < 16) reinterpret_cast<float*>(&sm_own[kOwnScales])[lane] = own_s;
+      } else {
+        // [rope 64 | latent 512] bf16 -> [bf16(rope / kv_scale) | e4m3fn(latent / kv_scale), permuted]
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+          if (part == 1 && lane >= 8) continue;
+          const int ch = lane + 64 * part;  // 8-element chunk of the own row
+          if (ch < 8) {
+            uint32_t o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const uint32_t lo = f32_to_bf16_bits(bf16_bits_to_f32(w[part * 4 + i] & 0xffffu) / a.kv_scale);
+              const uint32_t hi = f32_to_bf16_bits(bf16_bits_to_f32(w[part * 4 + i] >> 16) / a.kv_scale);
+              o[i] = lo | (hi << 16);
+            }
+            *reinterpret_cast<uint4*>(&sm_own[16 * ch]) = make_uint4(o[0], o[1], o[2], o[3]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const uint32_t bits = (w[part * 4 + (i >> 1)] >> ((i & 1) * 16)) & 0xffffu;
+              sm_own[128 + latent_byte_of_dim(8 * (ch - 8) + i)] = (uint8_t)quantize_e4m3fn(bits, a.kv_scale);
+            }
+          }
+        }
+      }
+    }
     if constexpr (!SPARSE) {
       // every wave's query DMAs have landed (the tiles' may stay in flight), then the operand is complete
       static_assert(DEPTH == 3, "the waits below count two tiles");
@@ -532,6 +592,13 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
       else if (mine == 1) wait_vmcnt<PER_TILE>();
       else wait_vmcnt<0>();
       __syncthreads();
+    }
+    // The own row as key 0 of a one-key tile whose 16 rows all read sm_own (row stride 0; the other keys masked).
+    if (own_wave) {
+      float xo[4], to;
+      [[clang::always_inline]] scores(&sm_own[0], 1u, xo, to, 0, &sm_own[kOwnScales]);
+      if (needs_rescale(to)) [[clang::always_inline]] rescale(to);
+      [[clang::always_inline]] accumulate(&sm_own[0], 1u, xo, 0, &sm_own[kOwnScales]);
     }
     // The rare rescale sits outside the inner loop, so inside it the accumulators are only ever MFMA operands and
     // keep their registers: a tile whose scores need a rescale leaves the loop before its PV and re-enters after it.
@@ -558,82 +625,31 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
             wait_vmcnt<0>();
           }
           vm = tile_mask(t0 + i * WAVES);
-          [[clang::always_inline]] scores(T, vm, x, tmax);
+          [[clang::always_inline]] scores(T, vm, x, tmax, RS, T + Geo::SCALES);
           if (needs_rescale(tmax)) {
             pending = true;
             break;
           }
         }
         pending = false;
-        [[clang::always_inline]] accumulate(T, vm, x);
+        [[clang::always_inline]] accumulate(T, vm, x, RS, T + Geo::SCALES);
         slot = slot == DEPTH - 1 ? 0 : slot + 1;
       }
       if (!pending) break;
       [[clang::always_inline]] rescale(tmax);
     }
-    wait_vmcnt<0>();  // (the own row's DMA, for a wave without tiles)
+    wait_vmcnt<0>();
   }
 
-  // ---- the own row: quantized as the store quantizes it, written into slot 0 as key 0 of a one-key tile ----
-  if (own_wave) {
-    uint8_t* T = &sm_ring[wave][0][0];
-    // 8-element chunks lane and lane + 64 of the own row
-    const uint4 own0 = *reinterpret_cast<const uint4*>(&sm_own[8 * lane]);
-    const uint4 own1 = lane < 8 ? *reinterpret_cast<const uint4*>(&sm_own[8 * (lane + 64)]) : make_uint4(0, 0, 0, 0);
-    const uint32_t w[8] = {own0.x, own0.y, own0.z, own0.w, own1.x, own1.y, own1.z, own1.w};
-    if constexpr (FMT == ROWS576) {
-      float m = 0.0f;
+  // ---- the own row's pool store (ROWS576), deferred to here so that no store sits among the DMAs in flight ----
+  if (own_wave && own_slot >= 0) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        m = fmaxf(m, fabsf(bf16_bits_to_f32(w[j] & 0xffffu)));
-        m = fmaxf(m, fabsf(bf16_bits_to_f32(w[j] >> 16)));
-      }
-      const float s = scale_from_absmax(wave_max(m));
-      int64_t slot = -1;
-      if (hg == 0 && a.new_slots) slot = redirect_slot(a.new_slots[b], a.num_blocks * a.P);
-#pragma unroll
-      for (int part = 0; part < 2; ++part) {
-        if (part == 1 && lane >= 8) continue;
-        uint32_t o[2] = {0, 0};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint32_t bits = (w[part * 4 + (i >> 1)] >> ((i & 1) * 16)) & 0xffffu;
-          o[i >> 2] |= quantize_e4m3fn(bits, s) << ((i & 3) * 8);
-        }
-        const int byte = 8 * (lane + 64 * part);
-        *reinterpret_cast<uint2*>(T + byte) = make_uint2(o[0], o[1]);
-        if (slot >= 0) *reinterpret_cast<uint2*>(a.cache + slot * 576 + byte) = make_uint2(o[0], o[1]);
-      }
-      if (slot >= 0 && lane == 0) a.row_scale[slot] = s;
-      if (lane < 16) reinterpret_cast<float*>(T + Geo::SCALES)[lane] = s;
-    } else {
-      // [rope 64 | latent 512] bf16 -> [bf16(rope / kv_scale) | e4m3fn(latent / kv_scale), permuted]
-#pragma unroll
-      for (int part = 0; part < 2; ++part) {
-        if (part == 1 && lane >= 8) continue;
-        const int ch = lane + 64 * part;  // 8-element chunk of the own row
-        if (ch < 8) {
-          uint32_t o[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint32_t lo = f32_to_bf16_bits(bf16_bits_to_f32(w[part * 4 + i] & 0xffffu) / a.kv_scale);
-            const uint32_t hi = f32_to_bf16_bits(bf16_bits_to_f32(w[part * 4 + i] >> 16) / a.kv_scale);
-            o[i] = lo | (hi << 16);
-          }
-          *reinterpret_cast<uint4*>(T + 16 * ch) = make_uint4(o[0], o[1], o[2], o[3]);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const uint32_t bits = (w[part * 4 + (i >> 1)] >> ((i & 1) * 16)) & 0xffffu;
-            T[128 + latent_byte_of_dim(8 * (ch - 8) + i)] = (uint8_t)quantize_e4m3fn(bits, a.kv_scale);
-          }
-        }
-      }
+    for (int part = 0; part < 2; ++part) {
+      if (part == 1 && lane >= 8) continue;
+      *reinterpret_cast<uint2*>(a.cache + own_slot * 576 + 8 * (lane + 64 * part)) =
+          make_uint2(own_q[2 * part], own_q[2 * part + 1]);
     }
-    float xo[4], to;
-    [[clang::always_inline]] scores(T, 1u, xo, to);
-    if (needs_rescale(to)) [[clang::always_inline]] rescale(to);
-    [[clang::always_inline]] accumulate(T, 1u, xo);
+    if (lane == 0) a.row_scale[own_slot] = own_s;
   }
 
   // ---- merge: a common maximum per head; wave w sums latent blocks 2 w, 2 w + 1 over the waves and writes them ----

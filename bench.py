@@ -15,8 +15,9 @@ One JSON line on stdout:
   cpu_baseline  the CPU oracle (a torch restatement of the reference's torch path) on a bounded sample of the same
                 workload, timed on this host's cores.
 
-Options: --config {1,2,3,4,4swa,5} picks another workload (the default line is cfg2); --all prints one line per
-workload; --gpus above 1 is refused, because this build measures one GPU.
+Options: --config {1,2,3,4,4swa,5} picks another workload (the default line is cfg2); --config meta times the
+device-side decode metadata (block table, window trim) instead; --all prints one line per decode workload; --gpus
+above 1 is refused, because this build measures one GPU.
 """
 
 from __future__ import annotations
@@ -258,6 +259,102 @@ def _time_rows(run, B: int, budget_s: float):
 
 # ---------------------------------------------------------------------------------------------------------------
 
+META_METRIC = "decode metadata build µs/step (block table from req_to_token + window trim), 1 MI355X"
+
+
+def run_meta(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> dict:
+    """The device-side metadata of one decode forward (ops.block_table, then ops.window_table for a 128-key window)
+    for a serving batch: 256 rows of U[1, 8192] tokens, page 16, req_to_token [1024, 8192] int32, rotated over copies
+    past the Infinity Cache. The roofline figure is the block-table kernel's algorithmic bytes (4 B read + 4 B
+    written per entry, 16 B per row) over its time; its req_to_token reads are strided (one 4-byte entry per page),
+    so HBM moves a whole sector for each."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from sglang_neuron_amd import _lib, ops
+
+    B, P, ctx, nrows, window = 256, 16, 8192, 1024, 128
+    g = np.random.default_rng(7)
+    r2t_host = g.integers(0, 1 << 22, size=(nrows, ctx), dtype=np.int32)
+    rows = g.permutation(nrows)[:B].astype(np.int64)
+    lens = g.integers(1, ctx + 1, size=B).astype(np.int64)
+    width = -(-int(lens.max()) // P)
+    nb = ops.window_blocks(window, P, width)
+    copies = _copies(B * width * 64, r2t_host.nbytes, 16)
+    r2ts = [torch.from_numpy(r2t_host).to(dev) for _ in range(copies)]
+    rows_d, lens_d = torch.from_numpy(rows).to(dev), torch.from_numpy(lens).to(dev)
+    lens32 = torch.empty(B, dtype=torch.int32, device=dev)
+    tables = [ops.block_table(r, rows_d, lens_d, P, width, seq_lens_i32=lens32) for r in r2ts]
+    log(f"meta: B={B} page={P} width={width} window={window} ({nb} blocks), req_to_token {nrows}x{ctx} x {copies}")
+
+    lib = _lib.load()
+
+    def device_us(fn):
+        """Average device time of fn's one kernel, from the library's diagnostics timer: the launch's own dispatch
+        packet stamps a HIP event pair on the launch stream (torch's current stream), so host time between launches
+        is not counted."""
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        lib.sna_diag_kernel_timing(1)
+        for i in range(steps_n):
+            fn(i)
+        ms, unused, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
+        _lib.check(lib.sna_diag_kernel_timing_read(ctypes.byref(ms), ctypes.byref(unused), ctypes.byref(n)),
+                   "kernel_timing_read")
+        lib.sna_diag_kernel_timing(0)
+        return ms.value / max(n.value, 1) * 1e3
+
+    def both(i):
+        ops.window_table(ops.block_table(r2ts[i % copies], rows_d, lens_d, P, width, seq_lens_i32=lens32), lens_d, P,
+                         nb)
+
+    bt_us = device_us(lambda i: ops.block_table(r2ts[i % copies], rows_d, lens_d, P, width, seq_lens_i32=lens32))
+    wt_us = device_us(lambda i: ops.window_table(tables[i % copies], lens_d, P, nb))
+    step_us = bt_us + wt_us  # the two kernels back to back (an event pair around both would count host gaps)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for i in range(steps_n):
+        both(i)
+    torch.cuda.synchronize()
+    host_us = (time.perf_counter() - t) / steps_n * 1e6
+    bt_bytes = B * width * 8 + B * 16
+    achieved = bt_bytes / (bt_us * 1e-6) / 1e9
+    log(f"block_table {bt_us:.2f} us ({achieved:.0f} GB/s algorithmic), window_table {wt_us:.2f} us, both {step_us:.2f} "
+        f"us on the device; {host_us:.2f} us per build by the host clock (Python + launches)")
+    line = {
+        "metric": META_METRIC, "value": round(step_us, 3), "unit": "us/step", "n_gpus": 1, "steps": steps_n,
+        "warmup": warmup, "ms_per_step": round(step_us * 1e-3, 6), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int32", "data": "synthetic: random slots (numpy seed 7), U[1, 8192] lengths",
+        "config": {"workload": "meta: decode metadata of a 256-row batch", "batch": B, "page_size": P,
+                   "table_width": width, "window": window, "window_blocks": nb, "req_to_token": [nrows, ctx],
+                   "copies": copies},
+        "block_table_us": round(bt_us, 3), "window_table_us": round(wt_us, 3), "host_clock_us_per_build": round(host_us, 3),
+        "roofline": {"bound": "hbm", "kernel": "block_table_kernel", "achieved": round(achieved, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": _traffic("meta"), "alg_bytes_per_launch": bt_bytes, "avg_launch_us": round(bt_us, 3)},
+        "cpu_baseline": None,
+    }
+    if cpu:
+        from oracle import metadata as omd
+
+        lens_t = torch.from_numpy(lens)
+        times = []
+        for _ in range(3):
+            t = time.perf_counter()
+            tb = omd.block_table(r2t_host, rows, lens, P)
+            omd.swa_trimmed_table(tb, lens_t, window, P, nb)
+            times.append(time.perf_counter() - t)
+        line["cpu_baseline"] = {"value": statistics.median(times) * 1e6, "unit": "us/step",
+                                "cores": torch.get_num_threads(), "kind": "port",
+                                "sample": "the whole batch (median of 3 runs): numpy block table + torch window trim, "
+                                          "as the reference's host builders", "cpu": cpu_model()}
+        log(f"CPU baseline: {line['cpu_baseline']['value']:.0f} us/step")
+    return line
+
+
 def run_one(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> dict:
     import ctypes
 
@@ -360,7 +457,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="2", help="1, 2, 3, 4, 4swa or 5 (default 2, the metric's workload)")
+    ap.add_argument("--config", default="2",
+                    help="1, 2, 3, 4, 4swa or 5 (default 2, the metric's workload); meta: the device-side metadata")
     ap.add_argument("--all", action="store_true", help="one line per workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work for the baseline sample")
@@ -388,7 +486,10 @@ def main() -> int:
         log(f"copy calibration: one copy of {COPY_CALIBRATION_BYTES} bytes (read) into as many (written)")
     keys = ["1", "2", "3", "4", "4swa", "5"] if args.all else [args.config]
     for k in keys:
-        line = run_one(k, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
+        if k == "meta":
+            line = run_meta(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
+        else:
+            line = run_one(k, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
         print(json.dumps(line), flush=True)
         torch.cuda.empty_cache()
     return 0

@@ -226,13 +226,42 @@ int sna_mla_decode_sparse(const void *q_absorbed, const void *q_pe, const void *
 int sna_lse_combine(const float *o_parts, const float *lse_parts, int32_t n_parts, int64_t n_rows, int32_t dim,
                     void *out, float *lse_out, void *stream);
 
+/* =====================================================================================================
+ * Decode metadata on the device
+ * ===================================================================================================== */
+
+/* The decode block table from SGLang's req_to_token map, built on the device (no host view, no upload):
+ *   req_to_token      [r2t_rows, r2t_width] int32 token slots, row stride r2t_stride elements.
+ *   req_pool_indices  [B] int64 rows of req_to_token; seq_lens [B] int64 (prefix + new token).
+ *   table             [B, width] int32 out, contiguous: table[b, j] = floor(req_to_token[row_b, j * page_size] /
+ *                     page_size) while j * page_size < seq_len_b, else -1. A row index outside [0, r2t_rows), or a
+ *                     column whose first token lies past req_to_token's width, gives -1.
+ *   seq_lens_i32      [B] int32 out (seq_lens narrowed for the decode entry points), or NULL.
+ * With width = ceil(max seq_len / page_size) the table is the reference's, entry for entry.
+ * Replaces: NeuronAttnBackend._block_table (attention/backend.py:114-130), which builds it on the host from a numpy
+ * view of req_to_token every step. */
+int sna_block_table(const int32_t *req_to_token, int64_t r2t_rows, int64_t r2t_width, int64_t r2t_stride,
+                    const int64_t *req_pool_indices, const int64_t *seq_lens, int32_t B, int32_t page_size,
+                    int32_t width, int32_t *table, int32_t *seq_lens_i32, void *stream);
+
+/* A sliding-window layer's trimmed block table, built on the device:
+ *   table      [B, table_width] int32, row stride table_stride elements; seq_lens [B] int64.
+ *   trimmed    [B, n_blocks] int32 out, contiguous: trimmed[b, i] = table[b, start_b + i], -1 past table_width, with
+ *              start_b = max(floor((seq_len_b - 1) / page_size) - n_blocks + 1, 0).
+ *   pos_offset [B] int32 out: start_b * page_size, the position of the trimmed table's first key.
+ * Replaces: the decode window trim of model_executor/graph_runner.py:1121-1133 (host torch ops, then an upload). */
+int sna_window_table(const int32_t *table, int64_t table_stride, int32_t table_width, const int64_t *seq_lens,
+                     int32_t B, int32_t page_size, int32_t n_blocks, int32_t *trimmed, int32_t *pos_offset,
+                     void *stream);
+
 /* ---- diagnostics ---- */
 
 /* Per-kernel timing of the decode entry points, for the benchmark's roofline figure. With timing on, each decode call
  * launches its split-K kernel and its combine kernel through hipExtLaunchKernel with a start/stop event pair, so the
  * kernels' own dispatch packets stamp the times and no marker packet runs between them (up to 4096 calls after the
- * switch). sna_diag_kernel_timing_read waits for the events and returns the summed milliseconds of each kernel and
- * the number of split-K launches timed. The events are the library's only state besides the error string. The timer
+ * switch); sna_block_table and sna_window_table time their one kernel as the split-K slot. sna_diag_kernel_timing_read
+ * waits for the events and returns the summed milliseconds of each kernel and the number of split-K-slot launches
+ * timed. The events are the library's only state besides the error string. The timer
  * is not thread-safe and is off by default. */
 int sna_diag_kernel_timing(int enable);
 int sna_diag_kernel_timing_read(double *split_ms, double *combine_ms, int64_t *launches);

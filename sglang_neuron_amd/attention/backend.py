@@ -45,12 +45,19 @@ class _DecodeState:
     slots: Tensor  # [bs] int64, device
     positions: Tensor  # [bs] int32, device
     plans: dict
+    host_lens: Optional[Tensor] = None  # [bs] host seq_lens when known (exact split plans), else None
+    max_len: int = -1  # a bound on seq_lens (plans when host_lens is None)
 
 
 class NeuronAttnBackend:
     """The attention backend of the HIP decode path. ``model_runner`` provides ``req_to_token_pool`` (with
-    ``req_to_token`` [rows, context] int32 on the host), ``token_to_kv_pool`` (one of this package's pools) and
-    ``page_size``."""
+    ``req_to_token`` [rows, context] int32), ``token_to_kv_pool`` (one of this package's pools) and ``page_size``.
+
+    With req_to_token on the host (the reference's arrangement) a decode forward's metadata is built as the
+    reference builds it (``build_metadata``) and uploaded once per forward. With req_to_token on the GPU (SGLang's
+    own arrangement there) it is built on the device (``build_device_metadata``): the block table by a gather
+    kernel, nothing read back; only the batch's longest length is taken from ``seq_lens_cpu`` when the batch carries
+    it, to size the table and plan the splits exactly."""
 
     def __init__(self, model_runner):
         self.model_runner = model_runner
@@ -123,20 +130,58 @@ class NeuronAttnBackend:
             view = self._r2t_view = (r2t, r2t.data_ptr(), r2t.numpy())
         return view[2]
 
+    def build_device_metadata(self, fb, device: torch.device) -> NeuronForwardMetadata:
+        """A decode batch's metadata with req_to_token on the GPU, built there: ``block_table`` [bs, width] int32 by
+        ``ops.block_table`` (the reference's _block_table, attention/backend.py:114-130, entry for entry when width
+        is the longest row's page count), ``slot_mapping`` / ``seq_lens`` / ``positions`` as device views of the
+        batch's own tensors. ``width`` is ceil(max seq_len / page) from ``seq_lens_cpu`` when the batch has it, else
+        req_to_token's context width in pages (a bound)."""
+        mode = fb.forward_mode
+        bs = getattr(fb, "_original_batch_size", None)
+        bs = int(bs) if bs is not None else int(fb.batch_size)
+        n_tok = getattr(fb, "_original_num_tokens", None)
+        n_tok = int(n_tok) if n_tok is not None else int(fb.out_cache_loc.shape[0])
+        r2t = self.req_to_token_pool.req_to_token
+        page = self.page_size
+        if mode.is_idle() or bs == 0:
+            empty = torch.zeros((0,), dtype=torch.long, device=device)
+            return NeuronForwardMetadata(
+                is_prefill=False, batch_size=0, num_tokens=0,
+                block_table=torch.full((0, 1), -1, dtype=torch.int32, device=device), slot_mapping=empty,
+                seq_lens=empty, positions=empty)
+        lens_cpu = getattr(fb, "seq_lens_cpu", None)
+        if lens_cpu is not None:
+            width = max(1, -(-int(lens_cpu[:bs].max()) // page))
+        else:
+            width = max(1, -(-int(r2t.shape[1]) // page))
+        seq_lens = fb.seq_lens[:bs].to(device, torch.long)
+        table = ops.block_table(r2t, fb.req_pool_indices[:bs].to(device, torch.long), seq_lens, page, width)
+        return NeuronForwardMetadata(
+            is_prefill=mode.is_extend(), batch_size=bs, num_tokens=n_tok, block_table=table,
+            slot_mapping=fb.out_cache_loc[:n_tok].to(device, torch.long), seq_lens=seq_lens,
+            positions=fb.positions[:n_tok].to(device, torch.long))
+
     # ---- decode ----
     def _decode_state(self, fb, device: torch.device) -> _DecodeState:
         st = getattr(fb, "_sna_decode_state", None)
         if st is not None and st.table.device == device:
             return st
-        meta = self.build_metadata(fb)
+        on_device = self.req_to_token_pool.req_to_token.is_cuda
+        meta = self.build_device_metadata(fb, device) if on_device else self.build_metadata(fb)
         if meta.is_prefill:
             raise NotImplementedError("forward_decode got an extend batch: this build runs the decode path only")
         if meta.num_tokens != meta.batch_size:
             raise ValueError(f"a decode batch has one new token per row ({meta.num_tokens} tokens, {meta.batch_size} "
                              "rows)")
+        if on_device:
+            lens_cpu = getattr(fb, "seq_lens_cpu", None)
+            host_lens = lens_cpu[:meta.batch_size].to(torch.long) if lens_cpu is not None else None
+            max_len = meta.block_table.shape[1] * self.page_size
+        else:
+            host_lens, max_len = meta.seq_lens, -1
         st = _DecodeState(meta=meta, table=meta.block_table.to(device), seq_lens=meta.seq_lens.to(device, torch.int32),
                           slots=meta.slot_mapping.to(device), positions=meta.positions.to(device, torch.int32),
-                          plans={})
+                          plans={}, host_lens=host_lens, max_len=max_len)
         try:
             fb._sna_decode_state = st
         except AttributeError:
@@ -188,8 +233,8 @@ class NeuronAttnBackend:
             sinks = getattr(layer, "sinks", None)
         key = ("gqa", window, G)
         if key not in st.plans:
-            st.plans[key] = ops.plan_decode(_lib.KIND_GQA, bs, host_seq_lens=st.meta.seq_lens, window=window,
-                                            ctas_per_item=G, num_cus=ops._num_cus(q.device))
+            st.plans[key] = ops.plan_decode(_lib.KIND_GQA, bs, host_seq_lens=st.host_lens, max_seq_len=st.max_len,
+                                            window=window, ctas_per_item=G, num_cus=ops._num_cus(q.device))
         k_cache, v_cache = pool.get_kv_buffer(layer_id)
         k_scale, v_scale = pool.get_kv_scales(layer_id)
         fp8 = pool.store_dtype == ops.FP8
@@ -205,7 +250,7 @@ class NeuronAttnBackend:
         q = q.reshape(bs, H, 576)
         key = ("mla", H)
         if key not in st.plans:
-            st.plans[key] = ops.plan_decode(_lib.KIND_MLA, bs, host_seq_lens=st.meta.seq_lens,
+            st.plans[key] = ops.plan_decode(_lib.KIND_MLA, bs, host_seq_lens=st.host_lens, max_seq_len=st.max_len,
                                             ctas_per_item=(H + 15) // 16, num_cus=ops._num_cus(q.device))
         out = ops.mla_decode(
             q[..., :512], q[..., 512:], pool.get_key_buffer(layer_id), pool.get_row_scale(layer_id), st.table,

@@ -94,7 +94,7 @@ using namespace sna;
 
 extern "C" {
 
-int sna_version(void) { return 100; }
+int sna_version(void) { return 101; }
 
 const char* sna_last_error(void) { return error_buffer(); }
 
@@ -144,15 +144,23 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
   const int32_t tile = kind == 0 ? 32 : 16;
   const int32_t waves = 4;
   const int32_t cus = num_cus > 0 ? num_cus : 256;
-  auto len_of = [&](int32_t b) -> int32_t {
-    if (kind == 2) return n_keys_per_row + 1;  // the index list as "prior keys" + the own row
-    return host_seq_lens ? host_seq_lens[b] : max_seq_len;
-  };
   const int32_t win = kind == 2 ? 0 : window;
+  // A plan from a bound holds every length up to it. With a window, the tiles a row spans depend on where its window
+  // starts inside a tile (periodic in the length, period `tile`), so the bound takes the most tiles of any length in
+  // its last two periods; below the window the count only grows with the length.
+  int32_t bound_tiles = 0;
+  if (kind != 2 && !host_seq_lens)
+    for (int32_t L = std::max(1, max_seq_len - 2 * tile); L <= max_seq_len; ++L)
+      bound_tiles = std::max(bound_tiles, host_tiles(L, win, tile));
+  auto tiles_of = [&](int32_t b) -> int32_t {
+    if (kind == 2) return host_tiles(n_keys_per_row + 1, 0, tile);  // the index list as "prior keys" + the own row
+    return host_seq_lens ? host_tiles(host_seq_lens[b], win, tile) : bound_tiles;
+  };
+  auto splits_of_row = [&](int32_t b, int32_t st) -> int32_t { return (tiles_of(b) + st - 1) / st; };
   int64_t total_tiles = 0;
   int32_t max_tiles = 0;
   for (int32_t b = 0; b < B; ++b) {
-    int32_t t = host_tiles(len_of(b), win, tile);
+    int32_t t = tiles_of(b);
     total_tiles += t;
     max_tiles = std::max(max_tiles, t);
   }
@@ -176,7 +184,7 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
     // grow the split until the item count fits the resident target, so no workgroup waits for a second round
     while (split_tiles < cap) {
       int64_t n = 0;
-      for (int32_t b = 0; b < B; ++b) n += host_splits(len_of(b), win, tile, split_tiles);
+      for (int32_t b = 0; b < B; ++b) n += splits_of_row(b, split_tiles);
       if (n * ctas_per_item <= target) break;
       split_tiles = std::min(split_tiles + 1, cap);
     }
@@ -184,7 +192,7 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
   // the combine passes hold at most kMaxSplits weights per row: grow the split until every row fits
   while (true) {
     int32_t worst = 0;
-    for (int32_t b = 0; b < B; ++b) worst = std::max(worst, host_splits(len_of(b), win, tile, split_tiles));
+    for (int32_t b = 0; b < B; ++b) worst = std::max(worst, splits_of_row(b, split_tiles));
     if (worst <= kMaxSplits) break;
     split_tiles = std::max(split_tiles + 1, (max_tiles + kMaxSplits - 1) / kMaxSplits);
   }
@@ -194,7 +202,7 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
   int64_t n_work = 0;
   int32_t max_splits = 0, empty = 0;
   for (int32_t b = 0; b < B; ++b) {
-    const int32_t n = host_splits(len_of(b), win, tile, split_tiles);
+    const int32_t n = splits_of_row(b, split_tiles);
     n_work += n;
     max_splits = std::max(max_splits, n);
     empty += n == 0;

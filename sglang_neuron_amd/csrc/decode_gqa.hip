@@ -112,7 +112,9 @@ void gqa_decode_kernel(GqaArgs a) {
   locate_work<32>(a.seq_lens, a.B, a.window, a.split_tiles, (int32_t)blockIdx.x, b, split);
   b = __builtin_amdgcn_readfirstlane(b);
   split = __builtin_amdgcn_readfirstlane(split);
-  if (b < 0) return;  // uniform across the workgroup
+  // uniform across the workgroup; a split past the plan's count (a length beyond the plan's bound) is dropped, so no
+  // write leaves the workspace
+  if (b < 0 || split >= max(a.max_splits, 1)) return;
 
   const int32_t L = ld_const(a.seq_lens + b);
   const KeyRange kr = key_range(L, a.window);

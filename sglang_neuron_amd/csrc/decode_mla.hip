@@ -226,7 +226,7 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
   }
   b = __builtin_amdgcn_readfirstlane(b);
   split = __builtin_amdgcn_readfirstlane(split);
-  if (b < 0) return;
+  if (b < 0 || split >= max(a.max_splits, 1)) return;  // (past the plan's count: dropped, no write out of bounds)
 
   const int32_t khi = SPARSE ? a.n_indices : ld_const(a.seq_lens + b) - 1;
   const int32_t t_first = split * a.split_tiles;

@@ -390,6 +390,66 @@ def lse_combine(o_parts: Tensor, lse_parts: Tensor) -> tuple[Tensor, Tensor]:
     return out, lse
 
 
+# ------------------------------------------------------------------------------------------------------------------
+# decode metadata on the device
+# ------------------------------------------------------------------------------------------------------------------
+
+def block_table(req_to_token: Tensor, req_pool_indices: Tensor, seq_lens: Tensor, page_size: int, width: int, *,
+                seq_lens_i32: Optional[Tensor] = None) -> Tensor:
+    """[B, width] int32 block table from req_to_token [rows, context] int32 (device), req_pool_indices [B] and
+    seq_lens [B] (int64, device): floor(req_to_token[row_b, j * page] / page) while j * page < seq_len_b, else -1.
+    ``seq_lens_i32`` [B] int32, when given, receives seq_lens narrowed (what the decode entry points take).
+    With width = ceil(max seq_len / page) this is NeuronAttnBackend._block_table (attention/backend.py:114-130)."""
+    dev = _on_gpu(req_to_token, req_pool_indices, seq_lens, seq_lens_i32)
+    _need(req_to_token.dim() == 2 and req_to_token.dtype == torch.int32 and req_to_token.stride(1) == 1,
+          "req_to_token must be [rows, context] int32 with unit column stride")
+    B = req_pool_indices.shape[0]
+    _need(seq_lens.shape == (B,), f"seq_lens must be [{B}]")
+    _need(width >= 1 and page_size >= 1, f"width {width} and page_size {page_size} must be positive")
+    rows = _contig(req_pool_indices, "req_pool_indices", torch.int64)
+    lens = _contig(seq_lens, "seq_lens", torch.int64)
+    if seq_lens_i32 is not None:
+        _need(seq_lens_i32.shape == (B,) and seq_lens_i32.dtype == torch.int32 and seq_lens_i32.is_contiguous(),
+              f"seq_lens_i32 must be a contiguous [{B}] int32 tensor")
+    table = torch.empty(B, width, dtype=torch.int32, device=dev)
+    rc = _lib.load().sna_block_table(_ptr(req_to_token), req_to_token.shape[0], req_to_token.shape[1],
+                                     req_to_token.stride(0), _ptr(rows), _ptr(lens), B, page_size, width, _ptr(table),
+                                     _ptr(seq_lens_i32), _stream(dev))
+    _lib.check(rc, "block_table")
+    return table
+
+
+def window_blocks(window: int, page_size: int, table_width: int, align_blocks: int = 1) -> int:
+    """Table columns a decode row's sliding window of ``window`` keys spans: its window - 1 prior keys and the new
+    token's page, rounded up to ``align_blocks``, at most the table's width (model_executor/graph_runner.py:871-882;
+    the reference aligns to its Trainium kernel's shard size, which this path does not need: align 1)."""
+    _need(window >= 1 and page_size >= 1 and align_blocks >= 1, "window, page_size and align_blocks must be >= 1")
+    n = -(-(window - 1) // page_size) + 1
+    n = -(-n // align_blocks) * align_blocks
+    return min(n, table_width)
+
+
+def window_table(block_table: Tensor, seq_lens: Tensor, page_size: int, n_blocks: int) -> tuple[Tensor, Tensor]:
+    """A sliding-window layer's (trimmed table [B, n_blocks] int32, position offset [B] int32) from the full
+    ``block_table`` [B, width] int32 and ``seq_lens`` [B] int64: columns from start_b = max((seq_len_b - 1) // page
+    - n_blocks + 1, 0), -1 past the table; offset_b = start_b * page (model_executor/graph_runner.py:1121-1133)."""
+    dev = _on_gpu(block_table, seq_lens)
+    _need(block_table.dim() == 2 and block_table.dtype == torch.int32 and block_table.stride(1) == 1,
+          "block_table must be [B, width] int32 with unit column stride")
+    B, width = block_table.shape
+    _need(seq_lens.shape == (B,), f"seq_lens must be [{B}]")
+    _need(n_blocks >= 1, "n_blocks must be >= 1")
+    lens = _contig(seq_lens, "seq_lens", torch.int64)
+    trimmed = torch.empty(B, n_blocks, dtype=torch.int32, device=dev)
+    offset = torch.empty(B, dtype=torch.int32, device=dev)
+    if B == 0:
+        return trimmed, offset
+    rc = _lib.load().sna_window_table(_ptr(block_table), block_table.stride(0), width, _ptr(lens), B, page_size,
+                                      n_blocks, _ptr(trimmed), _ptr(offset), _stream(dev))
+    _lib.check(rc, "window_table")
+    return trimmed, offset
+
+
 def diag_fp8_to_bf16(x: Tensor) -> Tensor:
     """The gathered-page conversion instruction applied to bytes x (uint8): bf16 bits as int16 view."""
     dev = _on_gpu(x)

@@ -48,7 +48,7 @@ def test_header_parameter_counts_match_ctypes():
 
 
 def test_version_and_error_string(lib):
-    assert lib.sna_version() == 100
+    assert lib.sna_version() == 101
     assert isinstance(lib.sna_last_error(), bytes)
 
 
@@ -101,6 +101,18 @@ def test_plan_invariants(lib, kind, lens, window, ctas):
 def test_plan_from_a_bound_marks_empty_rows_unknown(lib):
     rc, p = _plan(lib, _lib.KIND_GQA, B=4, max_len=900)
     assert rc == 0 and p.empty_rows == -1
+
+
+@pytest.mark.parametrize("kind,window,max_len,B", [
+    (_lib.KIND_GQA, 128, 600, 5), (_lib.KIND_GQA, 128, 129, 3), (_lib.KIND_GQA, 100, 5000, 7),
+    (_lib.KIND_GQA, 1, 300, 2), (_lib.KIND_GQA, 0, 4000, 9), (_lib.KIND_MLA, 0, 3000, 4)])
+def test_plan_from_a_bound_holds_every_length_up_to_it(lib, kind, window, max_len, B):
+    """Every length L <= max_len: its split count fits the plan (max_splits, and n_work for B such rows), whatever
+    tile offset a window starts at."""
+    rc, p = _plan(lib, kind, B=B, max_len=max_len, window=window, ctas=8 if kind == _lib.KIND_GQA else 1)
+    assert rc == 0, lib.sna_last_error()
+    worst = max(_splits(L, window, p.tile, p.split_tiles) for L in range(1, max_len + 1))
+    assert worst <= p.max_splits and B * worst <= p.n_work, (worst, p)
 
 
 def test_plan_dsa_every_row_alike(lib):

@@ -35,17 +35,18 @@ def _req_to_token(table: torch.Tensor, lens, page: int) -> torch.Tensor:
     return r2t.to(torch.int32).reshape(B, ctx)
 
 
-def _backend(pool, table, lens, page):
-    runner = SimpleNamespace(req_to_token_pool=SimpleNamespace(req_to_token=_req_to_token(table, lens, page)),
+def _backend(pool, table, lens, page, device_r2t=False):
+    r2t = _req_to_token(table, lens, page)
+    runner = SimpleNamespace(req_to_token_pool=SimpleNamespace(req_to_token=r2t.to(DEV) if device_r2t else r2t),
                              token_to_kv_pool=pool, page_size=page)
     return NeuronAttnBackend(runner)
 
 
-def _batch(lens, new_slots, positions=None):
+def _batch(lens, new_slots, positions=None, host_lens=True):
     lens = lens.to(torch.int64)
     B = lens.numel()
     return SimpleNamespace(forward_mode=_Decode(), batch_size=B, req_pool_indices=torch.arange(B), seq_lens=lens.to(DEV),
-                           seq_lens_cpu=lens, out_cache_loc=new_slots.to(DEV),
+                           seq_lens_cpu=lens if host_lens else None, out_cache_loc=new_slots.to(DEV),
                            positions=(lens - 1 if positions is None else positions).to(DEV), extend_prefix_lens=None)
 
 
@@ -148,3 +149,57 @@ def test_backend_dsa_decode():
     assert_close_attn(out.reshape(case.B, case.H, 512), want_ctx, "dsa")
     assert torch.allclose(backend.last_lse.cpu(), want_lse, atol=2e-3, rtol=1e-4)
     assert torch.equal(pool.get_key_buffer(0).cpu().reshape(-1, 640), cache_o), "row pool differs"
+
+
+DEVICE_META = [("cfg2-small", 2, {"B": 4, "lens": (100, 700)}), ("cfg4-swa", 4, {"B": 5, "lens": (10, 500), "window": 128})]
+
+
+@pytest.mark.parametrize("host_lens", [True, False], ids=["seq_lens_cpu", "bound"])
+@pytest.mark.parametrize("name,cfg,over", DEVICE_META, ids=[g[0] for g in DEVICE_META])
+def test_backend_gqa_device_metadata(name, cfg, over, host_lens):
+    """req_to_token on the GPU: the block table is built there (ops.block_table). With seq_lens_cpu the step is the
+    host-metadata step bit for bit; without it (a plan from req_to_token's width) it stays within the bar."""
+    case = workloads.gqa_case(cfg, overrides=over)
+    want, kc_o, *_ = gqa_oracle(case)
+    announce(f"backend gqa device metadata {name} host_lens={host_lens}")
+    pool = NeuronMHATokenToKVPool((case.num_blocks - 1) * case.P, case.P, torch.float8_e4m3fn, case.G, case.d, 1, DEV)
+    layer = SimpleNamespace(layer_id=0, tp_q_head_num=case.H, tp_k_head_num=case.G, head_dim=case.d,
+                            scaling=case.sm_scale, sliding_window_size=case.window if case.window else -1,
+                            sinks=None if case.sinks is None else case.sinks.to(DEV))
+    pool.calibrate_kv_scales(0, torch.cat([case.k_prior, case.k_new]).to(DEV),
+                             torch.cat([case.v_prior, case.v_new]).to(DEV))
+    pool.set_kv_buffer(layer, case.prior_slots.to(DEV), case.k_prior.to(DEV), case.v_prior.to(DEV))
+    args = (case.q.reshape(case.B, -1).to(DEV), case.k_new.to(DEV), case.v_new.to(DEV), layer)
+    host = _backend(pool, case.block_table, case.seq_lens, case.P).forward_decode(*args, _batch(case.seq_lens,
+                                                                                                 case.new_slots))
+    dev = _backend(pool, case.block_table, case.seq_lens, case.P, device_r2t=True)
+    fb = _batch(case.seq_lens, case.new_slots, host_lens=host_lens)
+    out = dev.forward_decode(*args, fb)
+    torch.cuda.synchronize()
+    assert fb._sna_decode_state.table.is_cuda
+    if host_lens:
+        assert torch.equal(out, host)
+    assert_close_attn(out.reshape(case.B, case.H, case.d), want, name)
+    assert torch.equal(pool.get_key_buffer(0).cpu().view(torch.uint8), kc_o.view(torch.uint8)), "K pool differs"
+
+
+@pytest.mark.parametrize("host_lens", [True, False], ids=["seq_lens_cpu", "bound"])
+def test_backend_mla_device_metadata(host_lens):
+    case = workloads.mla_case(overrides={"B": 4, "lens": (1, 3000)})
+    want, cache_o, _ = mla_oracle(case)
+    announce(f"backend mla device metadata host_lens={host_lens}")
+    pool = NeuronMLATokenToKVPool((case.num_blocks - 1) * case.P, case.P, torch.float8_e4m3fn, 512, 64, 1, DEV)
+    layer = SimpleNamespace(layer_id=0, tp_q_head_num=case.H, scaling=case.sm_scale)
+    T = case.prior_slots.numel()
+    pool.set_kv_buffer(layer, case.prior_slots.to(DEV), case.prior_rows.reshape(T, 1, 576).to(DEV))
+    q = torch.cat([case.ql_nope, case.q_pe], dim=-1).to(DEV)
+    host = _backend(pool, case.block_table, case.seq_lens, case.P).forward_decode(
+        q, case.compact_new.to(DEV), None, layer, _batch(case.seq_lens, case.new_slots))
+    dev = _backend(pool, case.block_table, case.seq_lens, case.P, device_r2t=True)
+    out = dev.forward_decode(q, case.compact_new.to(DEV), None, layer,
+                             _batch(case.seq_lens, case.new_slots, host_lens=host_lens))
+    torch.cuda.synchronize()
+    if host_lens:
+        assert torch.equal(out, host)
+    assert_close_attn(out.reshape(case.B, case.H, 512), want, "mla device metadata")
+    assert torch.equal(pool.kv_buffer[0].cpu().reshape(-1, 576), cache_o), "row pool differs"

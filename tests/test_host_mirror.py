@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 import torch
 
+from sglang_neuron_amd import ops
 from sglang_neuron_amd.attention import NeuronAttnBackend
 from sglang_neuron_amd.mem_cache import NeuronDSATokenToKVPool, NeuronMHATokenToKVPool, NeuronMLATokenToKVPool
 
@@ -161,3 +162,29 @@ def test_no_cpu_compute_path():
     layer = SimpleNamespace(layer_id=0, tp_q_head_num=4, tp_k_head_num=2, head_dim=64, scaling=0.125)
     with pytest.raises(RuntimeError):
         backend.forward_decode(torch.zeros(1, 4 * 64, dtype=torch.bfloat16), k[:1], k[:1], layer, _batch([0], [5]))
+
+
+@pytest.mark.parametrize("page", [1, 4, 16, 64])
+@pytest.mark.parametrize("window", [1, 2, 15, 16, 17, 128, 1000])
+def test_window_blocks_cover_every_window_and_no_more(window, page):
+    """ops.window_blocks (graph_runner.py:871-882 without the Trainium alignment): the window's keys [L - W, L - 1]
+    of any row fall in the trimmed table's columns (start = (L - 1) // page - nb + 1), and some row needs all nb of
+    them; by brute force over L."""
+    nb = ops.window_blocks(window, page, 10**6)
+    need = 0
+    for L in range(1, 3 * window + 4 * page):
+        first, last = max(L - window, 0) // page, (L - 1) // page
+        start = max((L - 1) // page - nb + 1, 0)
+        assert start <= first and last <= start + nb - 1, (L, first, last, start, nb)
+        need = max(need, last - first + 1)
+    assert need == nb
+    assert ops.window_blocks(window, page, 3) == min(nb, 3)
+    assert ops.window_blocks(window, page, 10**6, align_blocks=4) == -(-nb // 4) * 4
+
+
+def test_device_metadata_refuses_cpu_tensors():
+    r2t = torch.zeros(4, 64, dtype=torch.int32)
+    with pytest.raises(ValueError):
+        ops.block_table(r2t, torch.arange(2), torch.tensor([3, 5]), 16, 4)
+    with pytest.raises(ValueError):
+        ops.window_table(torch.zeros(2, 4, dtype=torch.int32), torch.tensor([3, 5]), 16, 2)

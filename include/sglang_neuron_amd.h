@@ -227,6 +227,34 @@ int sna_lse_combine(const float *o_parts, const float *lse_parts, int32_t n_part
                     void *out, float *lse_out, void *stream);
 
 /* =====================================================================================================
+ * Prefill attention over the pool
+ * ===================================================================================================== */
+
+/* Segmented prefill attention: a chunk's queries attend to their request's prior and, causally, to the chunk
+ * itself, every key read from the pool (store the chunk's K/V first, e.g. with sna_kv_store_mha).
+ *   q            [T, num_q_heads, head_dim] bf16, contiguous, 16-byte aligned; request r owns rows
+ *                q_start[r] .. q_start[r + 1] - 1, its query i at position prior_lens[r] + i.
+ *   k_cache, v_cache  one layer's FP8 e4m3fn pool [num_blocks, num_kv_heads, page_size, head_dim] with per-KV-head
+ *                dequantization scales k_scale / v_scale [num_kv_heads] (kv_dtype SNA_DTYPE_FP8_E4M3FN; bf16 pools
+ *                return SNA_ERR_UNSUPPORTED).
+ *   block_table  [R, table_width] int32 (row stride table_stride), -1 past a row's pages; keys on a -1 page are not
+ *                attended.
+ *   q_start      [R + 1] int32, prior_lens [R] int32 (device); max_q_len >= every request's chunk length.
+ *   sinks        [num_q_heads] fp32 logits joining the softmax denominator, or NULL. window > 0: the query at
+ *                position p sees keys (p - window, p].
+ *   out          [T, num_q_heads, head_dim] bf16.
+ * head_dim 64 or 128, page_size a multiple of 16, num_q_heads / num_kv_heads <= 128.
+ * Replaces: segmented_attention (ops/attention/attention_segmented_cte.py:21-47, its torch path :50-75) and the
+ * attention of the fused sliding-window prefill (ops/attention/swa_fused.py:78-120), which reads the chunk's own
+ * K/V unquantized where this reads them back from the pool. */
+int sna_prefill_attention(const void *q, const void *k_cache, const void *v_cache, const float *k_scale,
+                          const float *v_scale, const int32_t *block_table, int64_t table_stride, int32_t table_width,
+                          const int32_t *q_start, const int32_t *prior_lens, int32_t R, int32_t max_q_len,
+                          const float *sinks, float sm_scale, int32_t window, void *out, int32_t num_q_heads,
+                          int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int64_t num_blocks,
+                          int32_t kv_dtype, void *stream);
+
+/* =====================================================================================================
  * Decode metadata on the device
  * ===================================================================================================== */
 
@@ -259,7 +287,7 @@ int sna_window_table(const int32_t *table, int64_t table_stride, int32_t table_w
 /* Per-kernel timing of the decode entry points, for the benchmark's roofline figure. With timing on, each decode call
  * launches its split-K kernel and its combine kernel through hipExtLaunchKernel with a start/stop event pair, so the
  * kernels' own dispatch packets stamp the times and no marker packet runs between them (up to 4096 calls after the
- * switch); sna_block_table and sna_window_table time their one kernel as the split-K slot. sna_diag_kernel_timing_read
+ * switch); sna_block_table, sna_window_table and sna_prefill_attention time their one kernel as the split-K slot. sna_diag_kernel_timing_read
  * waits for the events and returns the summed milliseconds of each kernel and the number of split-K-slot launches
  * timed. The events are the library's only state besides the error string. The timer
  * is not thread-safe and is off by default. */

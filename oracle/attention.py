@@ -80,6 +80,53 @@ def paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: T
     return out
 
 
+def segmented_prefill(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: Tensor, q_start, prior_lens, *,
+                      sm_scale: float, k_scale=None, v_scale=None, sinks: Optional[Tensor] = None,
+                      window: int = 0) -> Tensor:
+    """[T, H, d] bf16 prefill attention of a chunk's queries q [T, H, d] over caches [blocks, G, page, d] (bf16, or
+    uint8 FP8 bytes with per-KV-head scales [G]) into which the chunk's own K/V were stored first. Request r owns rows
+    q_start[r] .. q_start[r + 1] of q, at positions prior_lens[r] + i, and table row r.
+
+    Follows _torch_segmented_attention (ops/attention/attention_segmented_cte.py:50-75): keys are gathered through the
+    row's whole block table, -1 entries read as page 0 (:57-60); key k is visible to the query at position p iff
+    k < prior + S and k <= p, and, with a window W, k > p - W (:62-66); scores are fp32 (:68); a sink per head joins
+    the softmax as an extra column that is dropped (:70-73); PV is fp32 and the output cast once (:74). GQA maps q
+    head h to KV head h // group (:56-57). The reference folds FP8 scales into ``scale`` (the caller's); here K and V
+    are dequantized, the same arithmetic."""
+    T, H, d = q.shape
+    nb, G, P, _ = k_cache.shape
+    group = H // G
+    out = torch.empty(T, H, d, dtype=torch.bfloat16)
+    qs = [int(x) for x in torch.as_tensor(q_start).tolist()]
+    pl = [int(x) for x in torch.as_tensor(prior_lens).tolist()]
+    for r in range(len(pl)):
+        a, b_, prior = qs[r], qs[r + 1], pl[r]
+        S = b_ - a
+        if S == 0:
+            continue
+        span = prior + S
+        n_pages = -(-span // P)
+        pages = block_table[r, :n_pages].to(torch.int64).clamp(min=0)
+        keys = _dequant_cache(k_cache[pages], k_scale, G).permute(1, 0, 2, 3).reshape(G, n_pages * P, d)[:, :span]
+        vals = _dequant_cache(v_cache[pages], v_scale, G).permute(1, 0, 2, 3).reshape(G, n_pages * P, d)[:, :span]
+        q_pos = torch.arange(S).unsqueeze(1) + prior
+        k_pos = torch.arange(span).unsqueeze(0)
+        allowed = (k_pos < prior + S) & (k_pos <= q_pos)
+        if window > 0:
+            allowed &= k_pos > q_pos - window
+        qr = q[a:b_].float().reshape(S, G, group, d).permute(1, 2, 0, 3)  # [G, group, S, d]
+        scores = torch.einsum("gjsd,gkd->gjsk", qr, keys) * sm_scale
+        scores = scores.masked_fill(~allowed[None, None], float("-inf"))
+        if sinks is not None:
+            sk = sinks.float().reshape(G, group, 1, 1).expand(G, group, S, 1)
+            probs = torch.softmax(torch.cat([scores, sk], dim=-1), dim=-1)[..., :-1]
+        else:
+            probs = torch.softmax(scores, dim=-1)
+        o = torch.einsum("gjsk,gkd->gjsd", probs, vals)  # [G, group, S, d]
+        out[a:b_] = o.permute(2, 0, 1, 3).reshape(S, H, d).to(torch.bfloat16)
+    return out
+
+
 def token_slots(block_table: Tensor, page: int, width: int) -> Tensor:
     """[rows, width] token slots of each row's first ``width`` positions, -1 past its pages (ops/attention/mla.py:
     16-21)."""

@@ -1,0 +1,355 @@
+// Segmented prefill attention over the paged pool (GQA, FP8 K/V with per-KV-head scales): a chunk's queries attend
+// to their request's prior and, causally, to the chunk itself, all read from the pool (the chunk's K/V are stored
+// before the attention runs), optionally inside a sliding window and with a sink logit per head.
+//   reference: segmented_attention / _torch_segmented_attention (ops/attention/attention_segmented_cte.py:21-75)
+//
+// Work: one workgroup of 4 waves per (request, block of query tokens, KV head). Its 128 query rows are (token, head)
+// pairs, token-major (row = t * group + j for the group's query head j); wave w owns rows 32 w .. 32 w + 31 as two
+// 16-row MFMA N tiles. Keys run in tiles of 32 positions (aligned to multiples of 32) from the window's first key
+// to the block's last query. A tile's K and V rows (32 x d bytes each) are DMA'd into a 3-slot LDS ring shared by
+// the 4 waves (each wave issues a share of the tile's DMAs); two tiles are in flight while one computes. The block
+// table entries of the key range are staged in LDS first.
+//
+// Lane roles (lane = 16 g4 + i), all MFMAs v_mfma_f32_16x16x32_bf16:
+//   QK  S^T[key, row] = K[key, :] . Q[row, :] over d / 32 steps, per 16-key half a of the tile: lane (g4, i) feeds
+//       key 8 (i / 4) + 4 a + i % 4 (its bytes 32 s + 8 g4 .. + 7, converted to bf16) and row i's query elements
+//       32 s + 8 g4 .. + 7 (registers, loaded once). The result hands lane (g4, i) keys 8 g4 + 4 a + r (r < 4) of
+//       row i: over both halves the 8 consecutive keys 8 g4 .. 8 g4 + 7.
+//   PV  O^T[dim, row] += V^T[dim, key] . P^T[key, row] per 16-dim tile c, K = the tile's 32 keys: lane (g4, i)
+//       supplies P^T for keys 8 g4 .. + 7 of row i (its own probabilities) and, by one ds_read_b64_tr_b8, the V bytes
+//       of those keys at dim 16 c + i.
+//   acc lane (g4, i) holds row i at dims 16 c + 4 g4 + r.
+// Online softmax in the log2 domain with a lazily moved reference maximum (as the decode kernels). Keys that no row
+// of the block may see (past the chunk, or on an invalid page) have their V bytes zeroed in registers, so stale
+// pool bytes cannot reach the output through p = 0.
+
+#include "sna_device.h"
+#include "sna_host.h"
+
+namespace sna {
+
+struct PrefillArgs {
+  const uint16_t* q;       // [T, H, D] bf16
+  const uint8_t* k_cache;  // [num_blocks, G, P, D] e4m3fn
+  const uint8_t* v_cache;
+  const float* k_scale;  // [G] dequantization scales
+  const float* v_scale;
+  const int32_t* table;  // [R, table_width] (row stride table_stride)
+  int64_t table_stride;
+  int32_t table_width;
+  const int32_t* q_start;  // [R + 1] the requests' first rows in q
+  const int32_t* prior;    // [R] prior tokens of each request
+  const float* sinks;      // [H] natural-log sink logits, or null
+  uint16_t* out;           // [T, H, D] bf16
+  int32_t R, H, G, P, group, bq;  // bq: query tokens per workgroup (128 / group)
+  int64_t num_blocks;
+  float sm_scale;
+  int32_t window;
+};
+
+template <int D>
+struct PrefillGeo {
+  static constexpr int CH = D / 16;                          // 16-byte chunks of a K or V row
+  static constexpr int STRIDE = CH + 1;                      // plus a pad chunk
+  static constexpr int RS = 16 * STRIDE;                     // LDS row stride, bytes
+  static constexpr int HALF = 32 * RS;                       // the K (or V) rows of a tile
+  static constexpr int SLOT = 2 * HALF;                      // one ring slot: K then V
+  static constexpr int NDMA = (32 * STRIDE + 63) / 64;       // wave-wide DMAs of one of K, V
+  static constexpr int TAIL = 32 * STRIDE - 64 * (NDMA - 1);  // active lanes of the last one
+  static constexpr int NI = 2 * NDMA;                        // DMAs of a tile, dealt round-robin to the 4 waves
+  static constexpr int CNT_HI = (NI + 3) / 4, CNT_LO = NI / 4;  // a wave's DMAs per tile (waves < NI % 4: CNT_HI)
+  static constexpr int DEPTH = 3;
+  static constexpr int PAGES = 2048;  // block-table entries staged in LDS at a time
+};
+
+constexpr float kPrefillRescaleSlack = 8.0f;
+
+template <int D>
+__global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
+  using Geo = PrefillGeo<D>;
+  constexpr int CH = Geo::CH, STRIDE = Geo::STRIDE, RS = Geo::RS, HALF = Geo::HALF, SLOT = Geo::SLOT;
+  constexpr int NDMA = Geo::NDMA, NI = Geo::NI, DEPTH = Geo::DEPTH;
+  constexpr int NS = D / 32;  // QK steps
+  constexpr int NC = D / 16;  // PV dim tiles
+  typedef __attribute__((address_space(3))) void lds_void;
+  typedef __attribute__((address_space(3))) uint8_t lds_u8;
+  __shared__ __attribute__((aligned(16))) uint8_t sm_ring[DEPTH * SLOT];
+  __shared__ int32_t sm_pages[Geo::PAGES];
+
+  const int tid = threadIdx.x, lane = tid & 63, g4 = lane >> 4, li = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int32_t r = blockIdx.y, g = blockIdx.z;
+  const int32_t qa = a.q_start[r];
+  const int32_t S = a.q_start[r + 1] - qa;
+  const int32_t nqb = (S + a.bq - 1) / a.bq;
+  if ((int32_t)blockIdx.x >= nqb) return;
+  const int32_t q0 = (nqb - 1 - (int32_t)blockIdx.x) * a.bq;  // the blocks with the most keys start first
+  const int32_t nq = min(a.bq, S - q0);
+  const int32_t pos0 = a.prior[r] + q0;  // position of the block's first query
+  const int32_t hi = pos0 + nq;          // the block reads keys [lo, hi)
+  const int32_t lo = a.window > 0 ? max(0, pos0 - a.window + 1) : 0;
+
+  // ---- this lane's two rows (N tiles n = 0, 1): token, head, position, and the query operand ----
+  int32_t tok[2], head[2], qpos[2];
+  bool row_ok[2];
+  uint32_t qf[2][NS][4];
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const int32_t row = 32 * wave + 16 * n + li;
+    int32_t t = row / a.group;
+    row_ok[n] = t < nq;
+    t = min(t, nq - 1);  // a row past the block computes as its last token and is not written
+    tok[n] = qa + q0 + t;
+    head[n] = g * a.group + row % a.group;
+    qpos[n] = pos0 + t;
+    const uint16_t* qp = a.q + ((int64_t)tok[n] * a.H + head[n]) * D + 8 * g4;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const uint4 w = ld16(qp + 32 * s);
+      qf[n][s][0] = w.x, qf[n][s][1] = w.y, qf[n][s][2] = w.z, qf[n][s][3] = w.w;
+    }
+  }
+  const float qk_scale = a.sm_scale * kLog2e * a.k_scale[g];
+  const float v_scale = a.v_scale[g];
+
+  float m_ref[2] = {kNegBig, kNegBig}, l_run[2] = {0.0f, 0.0f};
+  f32x4_t acc[2][NC];
+#pragma unroll
+  for (int n = 0; n < 2; ++n)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[n][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // Each lane's LDS chunk o = 64 jj + lane of DMA jj (of K or V): chunk o % STRIDE of tile row o / STRIDE (the pad
+  // chunk repeats the row's last chunk; lanes past the tile only occur in the last DMA, which switches them off).
+  const uint32_t ring = lds_address((lds_void*)(lds_u8*)&sm_ring[0]);
+  const int64_t head_stride = (int64_t)a.P * D;  // bytes between KV heads of one page
+
+  int32_t p0 = 0;  // first page index staged in sm_pages
+  auto page_of = [&](int32_t key) -> int32_t { return sm_pages[key / a.P - p0]; };  // -1: invalid
+  auto issue = [&](int32_t t, int slot) {
+    const int32_t k0 = 32 * t;
+    const int32_t pa = page_of(k0), pb = page_of(k0 + 16);
+    const int64_t ba = ((int64_t)max(pa, 0) * a.G + g) * head_stride + (int64_t)(k0 % a.P) * D;
+    const int64_t bb = ((int64_t)max(pb, 0) * a.G + g) * head_stride + (int64_t)((k0 + 16) % a.P) * D;
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      if (j % 4 != wave) continue;
+      const int jj = j < NDMA ? j : j - NDMA;
+      if (jj == NDMA - 1 && lane >= Geo::TAIL) continue;
+      const int o = 64 * jj + lane;
+      const int row = o / STRIDE, c = min(o % STRIDE, CH - 1);
+      const int64_t off = (row < 16 ? ba : bb) + (int64_t)(row & 15) * D + 16 * c;
+      const uint8_t* src = (j < NDMA ? a.k_cache : a.v_cache) + off;
+      dma_global16(src, ring + slot * SLOT + (j < NDMA ? 0 : HALF) + 1024 * jj);
+    }
+  };
+
+  auto compute = [&](int32_t t, int slot) {
+    const uint8_t* K = &sm_ring[slot * SLOT];
+    const uint8_t* V = K + HALF;
+    const int32_t k0 = 32 * t;
+    const int32_t pa = page_of(k0), pb = page_of(k0 + 16);
+    // a full tile: every key valid and visible to every row of the block
+    const bool full = pa >= 0 && pb >= 0 && k0 + 31 <= pos0 && (a.window == 0 || k0 > hi - 1 - a.window);
+    // S^T for both 16-key halves and both N tiles
+    f32x4_t st[2][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int n = 0; n < 2; ++n) st[h][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint2 kw = *reinterpret_cast<const uint2*>(K + (8 * (li >> 2) + 4 * h + (li & 3)) * RS + 32 * s + 8 * g4);
+        uint32_t kop[4];
+        fp8x4_to_bf16x4(kw.x, kop[0], kop[1]);
+        fp8x4_to_bf16x4(kw.y, kop[2], kop[3]);
+#pragma unroll
+        for (int n = 0; n < 2; ++n) st[h][n] = mfma_16x16x32_bf16(kop, qf[n][s], st[h][n]);
+      }
+    }
+    // scores (log2 domain) of keys k0 + 8 g4 + j, j = 4 h + r
+    float x[2][8], tmax[2];
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      tmax[n] = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float v = st[j >> 2][n][j & 3] * qk_scale;
+        if (!full) {
+          const int32_t key = k0 + 8 * g4 + j;
+          const bool page_ok = (8 * g4 + j < 16 ? pa : pb) >= 0;
+          const bool vis = page_ok && key <= qpos[n] && (a.window == 0 || key > qpos[n] - a.window);
+          v = vis ? v : -INFINITY;
+        }
+        x[n][j] = v;
+        tmax[n] = fmaxf(tmax[n], v);
+      }
+      tmax[n] = max_across_groups(tmax[n]);
+    }
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      if (__any(tmax[n] > m_ref[n] + kPrefillRescaleSlack)) {
+        const float m_new = tmax[n] > m_ref[n] + kPrefillRescaleSlack ? tmax[n] : m_ref[n];
+        const float alpha = __builtin_amdgcn_exp2f(m_ref[n] - m_new);
+        m_ref[n] = m_new;
+        l_run[n] *= alpha;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[n][c] *= alpha;
+      }
+    }
+    uint32_t pop[2][4];
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      float p[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        p[j] = __builtin_amdgcn_exp2f(x[n][j] - m_ref[n]);
+        l_run[n] += p[j];
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) pop[n][k] = pack_bf16x2(p[2 * k], p[2 * k + 1]);
+    }
+    // V bytes of keys no row may see (past the chunk or on an invalid page) are zeroed: a stale NaN would survive p = 0
+    uint32_t vm0 = 0xffffffffu, vm1 = 0xffffffffu;
+    if (!full) {
+      vm0 = vm1 = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int32_t key = k0 + 8 * g4 + j;
+        const bool ok = key < hi && (8 * g4 + j < 16 ? pa : pb) >= 0;
+        if (ok) (j < 4 ? vm0 : vm1) |= 0xffu << (8 * (j & 3));
+      }
+    }
+    const uint8_t* Vt = V + (8 * g4 + (li >> 1)) * RS + 8 * (li & 1);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const uint2 vw = lds_read_tr8(Vt + 16 * c);
+      uint32_t vop[4];
+      fp8x4_to_bf16x4(vw.x & vm0, vop[0], vop[1]);
+      fp8x4_to_bf16x4(vw.y & vm1, vop[2], vop[3]);
+#pragma unroll
+      for (int n = 0; n < 2; ++n) acc[n][c] = mfma_16x16x32_bf16(vop, pop[n], acc[n][c]);
+    }
+  };
+
+  // The compiler's own loads (the query operand) complete here, in a wait it sees, before any DMA is in flight.
+  __builtin_amdgcn_s_waitcnt(0x0f70);
+
+  const int32_t t_first = lo / 32, t_end = (hi + 31) / 32;
+  const int32_t chunk_tiles = (Geo::PAGES - 1) * a.P / 32;  // (a chunk may start mid-page: PAGES - 1 whole pages)
+  for (int32_t c0 = t_first; c0 < t_end; c0 += chunk_tiles) {
+    const int32_t c1 = min(c0 + chunk_tiles, t_end);
+    // stage the table entries of pages [p0, p1) (ring and pages are free: the previous chunk drained)
+    __syncthreads();
+    p0 = 32 * c0 / a.P;
+    const int32_t p1 = (32 * c1 - 1) / a.P + 1;
+    const int32_t* trow = a.table + (int64_t)r * a.table_stride;
+    for (int32_t i = tid; i < p1 - p0; i += 256) {
+      const int32_t col = p0 + i;
+      const int32_t e = col < a.table_width ? trow[col] : -1;
+      sm_pages[i] = (e >= 0 && (int64_t)e < a.num_blocks) ? e : -1;
+    }
+    __syncthreads();
+    const int32_t n = c1 - c0;
+#pragma unroll
+    for (int i = 0; i < DEPTH - 1; ++i)
+      if (i < n) issue(c0 + i, i);
+    for (int32_t i = 0; i < n; ++i) {
+      // this wave's DMAs of tile i have landed once at most the next tile's remain in flight
+      if (i + 1 < n) {
+        if (wave < NI % 4 || NI % 4 == 0)
+          wait_vmcnt<Geo::CNT_HI>();
+        else
+          wait_vmcnt<Geo::CNT_LO>();
+      } else {
+        wait_vmcnt<0>();
+      }
+      __syncthreads();  // every wave's DMAs of tile i have landed, and every wave is done with tile i - 1's slot
+      if (i + DEPTH - 1 < n) issue(c0 + i + DEPTH - 1, (i + DEPTH - 1) % DEPTH);
+      compute(c0 + i, i % DEPTH);
+    }
+  }
+
+  // ---- epilogue: normalize (sinks join the denominator), scale by v_scale, write the valid rows ----
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    float L = sum_across_groups(l_run[n]);
+    if (a.sinks) L += __builtin_amdgcn_exp2f(a.sinks[head[n]] * kLog2e - m_ref[n]);
+    const float inv = v_scale / L;
+    if (!row_ok[n]) continue;
+    uint16_t* dst = a.out + ((int64_t)tok[n] * a.H + head[n]) * D + 4 * g4;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      *reinterpret_cast<uint2*>(dst + 16 * c) = make_uint2(pack_bf16x2(acc[n][c][0] * inv, acc[n][c][1] * inv),
+                                                           pack_bf16x2(acc[n][c][2] * inv, acc[n][c][3] * inv));
+  }
+}
+
+}  // namespace sna
+
+using namespace sna;
+
+extern "C" int sna_prefill_attention(const void* q, const void* k_cache, const void* v_cache, const float* k_scale,
+                                     const float* v_scale, const int32_t* block_table, int64_t table_stride,
+                                     int32_t table_width, const int32_t* q_start, const int32_t* prior_lens,
+                                     int32_t R, int32_t max_q_len, const float* sinks, float sm_scale, int32_t window,
+                                     void* out, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                     int32_t page_size, int64_t num_blocks, int32_t kv_dtype, void* stream) {
+  ApiGuard guard;
+  if (R < 0 || max_q_len < 0 || num_q_heads < 1 || num_kv_heads < 1 || num_q_heads % num_kv_heads != 0 ||
+      window < 0 || num_blocks < 1 || table_width < 1 || table_stride < table_width)
+    return fail(SNA_ERR_INVALID_ARGUMENT,
+                "prefill_attention: bad sizes (R %d, max_q_len %d, heads %d / %d, window %d, blocks %lld, table %d "
+                "wide, stride %lld)",
+                R, max_q_len, num_q_heads, num_kv_heads, window, (long long)num_blocks, table_width,
+                (long long)table_stride);
+  const int32_t group = num_q_heads / num_kv_heads;
+  if (group > 128) return fail(SNA_ERR_UNSUPPORTED, "prefill_attention: %d query heads per KV head (at most 128)", group);
+  if (head_dim != 64 && head_dim != 128)
+    return fail(SNA_ERR_UNSUPPORTED, "prefill_attention: head_dim %d (64 or 128)", head_dim);
+  if (page_size < 16 || page_size % 16 != 0)
+    return fail(SNA_ERR_UNSUPPORTED, "prefill_attention: page_size %d (a multiple of 16)", page_size);
+  if (kv_dtype != SNA_DTYPE_FP8_E4M3FN)
+    return fail(SNA_ERR_UNSUPPORTED, "prefill_attention: the KV pool must be FP8 e4m3fn (dtype %d)", kv_dtype);
+  if (R == 0 || max_q_len == 0) return SNA_OK;
+  if (!q || !k_cache || !v_cache || !k_scale || !v_scale || !block_table || !q_start || !prior_lens || !out)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "prefill_attention: null pointer");
+  if (!aligned(q, 16) || !aligned(out, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
+    return fail(SNA_ERR_INVALID_ARGUMENT, "prefill_attention: q, out and the caches must be 16-byte aligned");
+  if (R > 65535 || num_kv_heads > 65535)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "prefill_attention: %d requests x %d KV heads exceed the grid", R,
+                num_kv_heads);
+  PrefillArgs a;
+  a.q = (const uint16_t*)q;
+  a.k_cache = (const uint8_t*)k_cache;
+  a.v_cache = (const uint8_t*)v_cache;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
+  a.table = block_table;
+  a.table_stride = table_stride;
+  a.table_width = table_width;
+  a.q_start = q_start;
+  a.prior = prior_lens;
+  a.sinks = sinks;
+  a.out = (uint16_t*)out;
+  a.R = R;
+  a.H = num_q_heads;
+  a.G = num_kv_heads;
+  a.P = page_size;
+  a.group = group;
+  a.bq = 128 / group;
+  a.num_blocks = num_blocks;
+  a.sm_scale = sm_scale;
+  a.window = window;
+  const dim3 grid((unsigned)((max_q_len + a.bq - 1) / a.bq), (unsigned)R, (unsigned)num_kv_heads);
+  hipEvent_t t0, t1;
+  timing_events(0, &t0, &t1);
+  if (head_dim == 128)
+    hipExtLaunchKernelGGL((prefill_gqa_kernel<128>), grid, dim3(256), 0, (hipStream_t)stream, t0, t1, 0, a);
+  else
+    hipExtLaunchKernelGGL((prefill_gqa_kernel<64>), grid, dim3(256), 0, (hipStream_t)stream, t0, t1, 0, a);
+  timing_end_call();
+  return check_launch("prefill_attention");
+}

@@ -391,6 +391,72 @@ def lse_combine(o_parts: Tensor, lse_parts: Tensor) -> tuple[Tensor, Tensor]:
 
 
 # ------------------------------------------------------------------------------------------------------------------
+# prefill attention over the pool
+# ------------------------------------------------------------------------------------------------------------------
+
+def prefill_attention(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: Tensor, q_start: Tensor,
+                      prior_lens: Tensor, *, max_q_len: int, sm_scale: float, k_scale: Tensor, v_scale: Tensor,
+                      sinks: Optional[Tensor] = None, window: int = 0, out: Optional[Tensor] = None) -> Tensor:
+    """Prefill attention of a batch of chunks: q [T, H, d] bf16 (request r's rows q_start[r] .. q_start[r + 1], at
+    positions prior_lens[r] + i), every key read from one layer's FP8 caches [blocks, G, page, d] through
+    ``block_table`` [R, width] (store the chunk's K/V first, with kv_store_mha). Causal, optionally windowed (keys
+    (p - window, p]) and with sinks [H]. ``max_q_len`` bounds the chunk lengths (a host int). Returns [T, H, d] bf16.
+
+    Stands in for segmented_attention (ops/attention/attention_segmented_cte.py:21-75) over a batch."""
+    dev = _on_gpu(q, k_cache, v_cache, block_table, q_start, prior_lens, k_scale, v_scale, sinks, out)
+    T, H, d = q.shape
+    nb, G, P, dk = k_cache.shape
+    _need(dk == d and tuple(v_cache.shape) == tuple(k_cache.shape), "q, k_cache and v_cache disagree on shape")
+    _need(H % G == 0, f"{H} query heads over {G} KV heads")
+    R = prior_lens.shape[0]
+    _need(q_start.shape == (R + 1,), f"q_start must be [{R + 1}]")
+    _need(block_table.dim() == 2 and block_table.shape[0] >= R and block_table.stride(1) == 1,
+          "block_table must be [R, width] with unit column stride")
+    q = _contig(q, "q", torch.bfloat16)
+    qs = _contig(q_start, "q_start", torch.int32)
+    pl = _contig(prior_lens, "prior_lens", torch.int32)
+    table = _contig(block_table, "block_table", torch.int32) if block_table.dtype != torch.int32 else block_table
+    ks = _contig(k_scale.reshape(-1).float(), "k_scale")
+    vs = _contig(v_scale.reshape(-1).float(), "v_scale")
+    _need(ks.numel() == G and vs.numel() == G, f"k_scale and v_scale must have {G} entries")
+    sk = None if sinks is None else _contig(sinks.reshape(-1).float(), "sinks")
+    if sk is not None:
+        _need(sk.numel() == H, f"sinks must have {H} entries")
+    if out is None:
+        out = torch.empty(T, H, d, dtype=torch.bfloat16, device=dev)
+    _need(out.shape == (T, H, d) and out.dtype == torch.bfloat16 and out.is_contiguous(), "out must be [T, H, d] bf16")
+    if T == 0 or R == 0:
+        return out
+    rc = _lib.load().sna_prefill_attention(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(ks), _ptr(vs), _ptr(table), table.stride(0), table.shape[1],
+        _ptr(qs), _ptr(pl), R, int(max_q_len), _ptr(sk), float(sm_scale), int(window), _ptr(out), H, G, d, P, nb,
+        cache_dtype_code(k_cache.dtype), _stream(dev))
+    _lib.check(rc, "prefill_attention")
+    return out
+
+
+def segmented_attention(q: Tensor, *, k_cache: Tensor, v_cache: Tensor, block_tables: Tensor, prior_tokens,
+                        block_size: int, kv_segment_size: int, scale: float, sliding_window: Optional[int],
+                        sink: Optional[Tensor], k_scale: Tensor, v_scale: Tensor) -> Tensor:
+    """The reference's signature (ops/attention/attention_segmented_cte.py:21-47) for one request: q [heads, S, d],
+    caches [pages, kv_heads, page, d] (FP8, unpacked K), block_tables [1, blocks], prior_tokens (an int or a 1-element
+    tensor), sink [heads, 1] or None; returns [heads, S, d]. The per-KV-head scales k_scale / v_scale are this pool's
+    (the reference folds its per-tensor scale into ``scale``); ``kv_segment_size`` is the Trainium kernel's tiling and
+    has no role here."""
+    del kv_segment_size
+    heads, S, d = q.shape
+    _need(block_size == k_cache.shape[2], f"block_size {block_size} differs from the cache's page {k_cache.shape[2]}")
+    dev = q.device
+    prior = int(torch.as_tensor(prior_tokens).reshape(-1)[0])
+    out = prefill_attention(
+        q.transpose(0, 1).contiguous(), k_cache, v_cache, block_tables[:1].to(dev), torch.tensor([0, S], dtype=torch.int32,
+                                                                                                  device=dev),
+        torch.tensor([prior], dtype=torch.int32, device=dev), max_q_len=S, sm_scale=scale, k_scale=k_scale,
+        v_scale=v_scale, sinks=None if sink is None else sink.reshape(-1), window=int(sliding_window or 0))
+    return out.transpose(0, 1).contiguous()
+
+
+# ------------------------------------------------------------------------------------------------------------------
 # decode metadata on the device
 # ------------------------------------------------------------------------------------------------------------------
 

@@ -274,3 +274,90 @@ def test_swa_trimmed_table_by_hand():
     assert trimmed.tolist() == [[8, 9, 10]] and off.tolist() == [28]
     trimmed, off = omd.swa_trimmed_table(table, torch.tensor([5]), window=8, page=4, width=3)
     assert trimmed.tolist() == [[1, 2, 3]] and off.tolist() == [0]
+
+
+def _prefill_case(seed, H=4, G=2, d=8, P=4, priors=(7, 0, 3), lens=(5, 3, 6), nb=40, fp8=False):
+    g = torch.Generator().manual_seed(seed)
+    R = len(priors)
+    width = max(-(-(p + s) // P) for p, s in zip(priors, lens)) + 1
+    perm = torch.randperm(nb - 1, generator=g) + 1
+    table = torch.full((R, width), -1, dtype=torch.int32)
+    used = 0
+    for r, (p, s) in enumerate(zip(priors, lens)):
+        n = -(-(p + s) // P)
+        table[r, :n] = perm[used:used + n].to(torch.int32)
+        used += n
+    kf = torch.randn(nb, G, P, d, generator=g)
+    vf = torch.randn(nb, G, P, d, generator=g)
+    if fp8:
+        ks, vs = torch.rand(G, generator=g) * 0.02 + 0.005, torch.rand(G, generator=g) * 0.02 + 0.005
+        kc = ofp8.quantize(kf, ks.reshape(1, G, 1, 1))
+        vc = ofp8.quantize(vf, vs.reshape(1, G, 1, 1))
+    else:
+        ks = vs = None
+        kc, vc = kf.to(torch.bfloat16), vf.to(torch.bfloat16)
+    T = sum(lens)
+    q = torch.randn(T, H, d, generator=g).to(torch.bfloat16)
+    q_start = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+    return q, kc, vc, table, q_start, torch.tensor(priors, dtype=torch.int32), ks, vs
+
+
+@pytest.mark.parametrize("window", [0, 3])
+@pytest.mark.parametrize("sinks", [False, True])
+def test_segmented_prefill_brute_force(window, sinks):
+    """Explicit float64 loops over (request, query, head, key) on a tiny case."""
+    q, kc, vc, table, q_start, priors, _, _ = _prefill_case(11)
+    H, d, P, G = q.shape[1], q.shape[2], kc.shape[2], kc.shape[1]
+    sk = torch.randn(H) if sinks else None
+    got = oatt.segmented_prefill(q, kc, vc, table, q_start, priors, sm_scale=0.3, sinks=sk, window=window)
+    for r in range(len(priors)):
+        for i in range(int(q_start[r + 1] - q_start[r])):
+            row, pos = int(q_start[r]) + i, int(priors[r]) + i
+            for h in range(H):
+                kvh = h // (H // G)
+                logits, vals = [], []
+                for k in range(pos + 1):
+                    if window and k <= pos - window:
+                        continue
+                    page = int(table[r, k // P])
+                    kk = kc[page, kvh, k % P].double()
+                    logits.append(float((q[row, h].double() * kk).sum()) * 0.3)
+                    vals.append(vc[page, kvh, k % P].double())
+                m = max(logits + ([float(sk[h])] if sinks else []))
+                w = [math.exp(x - m) for x in logits]
+                den = sum(w) + (math.exp(float(sk[h]) - m) if sinks else 0.0)
+                want = sum(wi * v for wi, v in zip(w, vals)) / den
+                assert torch.allclose(got[row, h].double(), want, atol=1e-2, rtol=8e-3), (r, i, h)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_segmented_prefill_last_query_is_the_decode_of_its_position(fp8):
+    """The chunk's last query sees exactly what a decode of that position sees (its own token as the new key):
+    oracle/attention.segmented_prefill against oracle/attention.paged_decode_gqa, itself pinned above."""
+    q, kc, vc, table, q_start, priors, ks, vs = _prefill_case(5, priors=(9, 0, 14), lens=(4, 6, 2), fp8=fp8)
+    G, P = kc.shape[1], kc.shape[2]
+    sk = torch.randn(q.shape[1])
+    for window in (0, 5):
+        got = oatt.segmented_prefill(q, kc, vc, table, q_start, priors, sm_scale=0.25, k_scale=ks, v_scale=vs,
+                                     sinks=sk, window=window)
+        for r in range(len(priors)):
+            last, L = int(q_start[r + 1]) - 1, int(priors[r] + q_start[r + 1] - q_start[r])
+            page, off = int(table[r, (L - 1) // P]), (L - 1) % P
+            deq = (lambda c, s: ofp8.dequantize(c[page, :, off], s.reshape(G, 1))) if fp8 else \
+                (lambda c, s: c[page, :, off].float())
+            # the new token's K/V as the decode receives them: the pool's values (exact under quantize for FP8)
+            kn, vn = deq(kc, ks), deq(vc, vs)
+            want = oatt.paged_decode_gqa(q[last:last + 1], kc, vc, table[r:r + 1], torch.tensor([L]),
+                                         kn.unsqueeze(0).to(torch.bfloat16) if not fp8 else kn.unsqueeze(0),
+                                         vn.unsqueeze(0).to(torch.bfloat16) if not fp8 else vn.unsqueeze(0),
+                                         sm_scale=0.25, k_scale=ks, v_scale=vs, sinks=sk, window=window)
+            assert torch.allclose(got[last].float(), want[0].float(), atol=1e-2, rtol=1e-2), (r, window)
+
+
+def test_segmented_prefill_is_chunking_invariant():
+    """One chunk of 9 tokens == chunks of 4 and 5 (the second at prior + 4) over the same pool."""
+    q, kc, vc, table, _, _, _, _ = _prefill_case(8, priors=(6,), lens=(9,))
+    whole = oatt.segmented_prefill(q, kc, vc, table, torch.tensor([0, 9]), torch.tensor([6]), sm_scale=0.5, window=4)
+    two = oatt.segmented_prefill(q, kc, vc, table.repeat(2, 1), torch.tensor([0, 4, 9]), torch.tensor([6, 10]),
+                                 sm_scale=0.5, window=4)
+    assert torch.equal(whole, two)

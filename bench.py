@@ -16,7 +16,7 @@ One JSON line on stdout:
                 workload, timed on this host's cores.
 
 Options: --config {1,2,3,4,4swa,5} picks another workload (the default line is cfg2); --config meta times the
-device-side decode metadata (block table, window trim) instead; --all prints one line per decode workload; --gpus
+device-side decode metadata (block table, window trim) instead, --config prefill the segmented prefill attention; --all prints one line per decode workload; --gpus
 above 1 is refused, because this build measures one GPU.
 """
 
@@ -355,6 +355,115 @@ def run_meta(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> di
     return line
 
 
+PREFILL_METRIC = "prefill attention TFLOP/s over the FP8 pool (segmented, causal), 1 MI355X"
+
+
+def run_prefill(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> dict:
+    """Segmented prefill attention (ops.prefill_attention) on Qwen3-8B's shape: 4 requests, each a 2048-token chunk
+    after a 2048-token prior, H 32 / G 8 / d 128, FP8 pool (page 16) written by the store kernel. The algorithmic work
+    is 4 d flops per (query, head, visible key) (QK and PV); MFMA-bound, so the roofline is TFLOP/s against the bf16
+    dense peak."""
+    import ctypes
+
+    import torch
+
+    from sglang_neuron_amd import _lib, ops
+
+    R, S, prior, H, G, d, P = 4, 2048, 2048, 32, 8, 128, 16
+    g = torch.Generator(device="cpu").manual_seed(1100)
+    span = prior + S
+    pages = span // P
+    nb = R * pages + 1
+    table = (torch.randperm(nb - 1, generator=g) + 1).to(torch.int32).reshape(R, pages)
+    kc = torch.empty(nb, G, P, d, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.empty_like(kc)
+    ks = torch.full((G,), 4.0 / 448, device=dev)
+    vs = torch.full((G,), 4.0 / 448, device=dev)
+    for r in range(R):
+        k = torch.randn(span, G, d, generator=g).to(torch.bfloat16).to(dev)
+        v = torch.randn(span, G, d, generator=g).to(torch.bfloat16).to(dev)
+        slots = table[r, torch.arange(span) // P].to(torch.int64) * P + torch.arange(span) % P
+        ops.kv_store_mha(k, v, slots.to(dev), kc, vc, ks, vs)
+    q = torch.randn(R * S, H, d, generator=g).to(torch.bfloat16).to(dev)
+    q_start = torch.arange(0, R * S + 1, S, dtype=torch.int32, device=dev)
+    priors = torch.full((R,), prior, dtype=torch.int32, device=dev)
+    table_d = table.to(dev)
+    out = torch.empty_like(q)
+    scale = d ** -0.5
+    flops = 4 * d * H * R * sum(prior + i + 1 for i in range(S))
+    log(f"prefill: R={R} chunk={S} prior={prior} H={H} G={G} d={d} page={P}, {flops / 1e12:.2f} TFLOP per step")
+
+    def step():
+        ops.prefill_attention(q, kc, vc, table_d, q_start, priors, max_q_len=S, sm_scale=scale, k_scale=ks,
+                              v_scale=vs, out=out)
+
+    lib = _lib.load()
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    lib.sna_diag_kernel_timing(1)
+    for _ in range(steps_n):
+        step()
+    ms, unused, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
+    _lib.check(lib.sna_diag_kernel_timing_read(ctypes.byref(ms), ctypes.byref(unused), ctypes.byref(n)),
+               "kernel_timing_read")
+    lib.sna_diag_kernel_timing(0)
+    kernel_ms = ms.value / max(n.value, 1)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps_n):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    step_ms = e0.elapsed_time(e1) / steps_n
+    tflops = flops / (kernel_ms * 1e-3) / 1e12
+    log(f"prefill_gqa_kernel {kernel_ms * 1e3:.1f} us ({tflops:.0f} TFLOP/s), step {step_ms * 1e3:.1f} us")
+    line = {
+        "metric": PREFILL_METRIC, "value": round(flops / (step_ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": steps_n, "warmup": warmup, "ms_per_step": round(step_ms, 6), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16 MFMA over fp8_e4m3fn K/V",
+        "data": "synthetic: seeded N(0,1) K/V/Q (torch.Generator seed 1100), random page permutation",
+        "config": {"workload": "prefill: qwen3-8b-gqa-fp8, 4 x (2048-token chunk after a 2048-token prior)",
+                   "requests": R, "chunk": S, "prior": prior, "q_heads": H, "kv_heads": G, "head_dim": d,
+                   "page_size": P, "kv_dtype": "fp8_e4m3fn per-KV-head scale"},
+        "roofline": {"bound": "mfma", "kernel": "prefill_gqa_kernel", "achieved": round(tflops, 1),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": _traffic("prefill"), "alg_flops_per_launch": flops,
+                     "avg_launch_us": round(kernel_ms * 1e3, 3)},
+        "cpu_baseline": None,
+    }
+    if cpu:
+        from oracle import attention as oatt
+
+        kc8, vc8 = kc.cpu().view(torch.uint8), vc.cpu().view(torch.uint8)
+        qs, tb = q.cpu(), table.cpu()
+        ksc, vsc = ks.cpu(), vs.cpu()
+
+        def run(nq):  # the first nq queries of request 0
+            oatt.segmented_prefill(qs[:nq], kc8, vc8, tb[:1], torch.tensor([0, nq]), torch.tensor([prior]),
+                                   sm_scale=scale, k_scale=ksc, v_scale=vsc)
+
+        t = time.perf_counter()
+        run(16)
+        t16 = time.perf_counter() - t
+        nq = max(16, min(S, int(16 * cpu_budget / 3 / max(t16, 1e-6))))
+        times = []
+        for _ in range(3):
+            t = time.perf_counter()
+            run(nq)
+            times.append(time.perf_counter() - t)
+        sample_flops = 4 * d * H * sum(prior + i + 1 for i in range(nq))
+        med = statistics.median(times)
+        line["cpu_baseline"] = {"value": round(sample_flops / med / 1e12, 4), "unit": "TFLOP/s",
+                                "cores": torch.get_num_threads(), "kind": "port",
+                                "sample": f"the first {nq} queries of request 0 (median of 3 runs, {sample_flops / 1e9:.0f}"
+                                          f" GFLOP)", "cpu": cpu_model(),
+                                "us_per_step_scaled": round(med * flops / sample_flops * 1e6, 1)}
+        log(f"CPU baseline: {line['cpu_baseline']['value']} TFLOP/s")
+    return line
+
+
 def run_one(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> dict:
     import ctypes
 
@@ -458,7 +567,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="2",
-                    help="1, 2, 3, 4, 4swa or 5 (default 2, the metric's workload); meta: the device-side metadata")
+                    help="1, 2, 3, 4, 4swa or 5 (default 2, the metric's workload); meta: the device-side metadata; "
+                         "prefill: the segmented prefill attention")
     ap.add_argument("--all", action="store_true", help="one line per workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work for the baseline sample")
@@ -488,6 +598,8 @@ def main() -> int:
     for k in keys:
         if k == "meta":
             line = run_meta(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
+        elif k == "prefill":
+            line = run_prefill(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
         else:
             line = run_one(k, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
         print(json.dumps(line), flush=True)

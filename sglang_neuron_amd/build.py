@@ -37,7 +37,7 @@ HIP_FLAGS = [
 # the online softmax; with the accumulators in AGPRs the compiler copies them between the register files around that
 # (rare) rescale branch on every tile.
 _MFMA_VGPR = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
-EXTRA_FLAGS = {"decode_mla.hip": _MFMA_VGPR, "decode_gqa.hip": _MFMA_VGPR}
+EXTRA_FLAGS = {"decode_mla.hip": _MFMA_VGPR, "decode_gqa.hip": _MFMA_VGPR, "prefill_gqa.hip": _MFMA_VGPR}
 
 
 def hipcc() -> str:

@@ -49,13 +49,15 @@ struct PrefillArgs {
 
 template <int D>
 struct PrefillGeo {
+  static constexpr int TK = 64;                              // keys per tile: NSUB sub-tiles of 32
+  static constexpr int NSUB = TK / 32;
   static constexpr int CH = D / 16;                          // 16-byte chunks of a K or V row
   static constexpr int STRIDE = CH + 1;                      // plus a pad chunk
   static constexpr int RS = 16 * STRIDE;                     // LDS row stride, bytes
-  static constexpr int HALF = 32 * RS;                       // the K (or V) rows of a tile
+  static constexpr int HALF = TK * RS;                       // the K (or V) rows of a tile
   static constexpr int SLOT = 2 * HALF;                      // one ring slot: K then V
-  static constexpr int NDMA = (32 * STRIDE + 63) / 64;       // wave-wide DMAs of one of K, V
-  static constexpr int TAIL = 32 * STRIDE - 64 * (NDMA - 1);  // active lanes of the last one
+  static constexpr int NDMA = (TK * STRIDE + 63) / 64;       // wave-wide DMAs of one of K, V
+  static constexpr int TAIL = TK * STRIDE - 64 * (NDMA - 1);  // active lanes of the last one
   static constexpr int NI = 2 * NDMA;                        // DMAs of a tile, dealt round-robin to the 4 waves
   static constexpr int CNT_HI = (NI + 3) / 4, CNT_LO = NI / 4;  // a wave's DMAs per tile (waves < NI % 4: CNT_HI)
   static constexpr int DEPTH = 3;
@@ -68,7 +70,7 @@ template <int D>
 __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
   using Geo = PrefillGeo<D>;
   constexpr int CH = Geo::CH, STRIDE = Geo::STRIDE, RS = Geo::RS, HALF = Geo::HALF, SLOT = Geo::SLOT;
-  constexpr int NDMA = Geo::NDMA, NI = Geo::NI, DEPTH = Geo::DEPTH;
+  constexpr int NDMA = Geo::NDMA, NI = Geo::NI, DEPTH = Geo::DEPTH, TK = Geo::TK, NSUB = Geo::NSUB;
   constexpr int NS = D / 32;  // QK steps
   constexpr int NC = D / 16;  // PV dim tiles
   typedef __attribute__((address_space(3))) void lds_void;
@@ -127,10 +129,11 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
   int32_t p0 = 0;  // first page index staged in sm_pages
   auto page_of = [&](int32_t key) -> int32_t { return sm_pages[key / a.P - p0]; };  // -1: invalid
   auto issue = [&](int32_t t, int slot) {
-    const int32_t k0 = 32 * t;
-    const int32_t pa = page_of(k0), pb = page_of(k0 + 16);
-    const int64_t ba = ((int64_t)max(pa, 0) * a.G + g) * head_stride + (int64_t)(k0 % a.P) * D;
-    const int64_t bb = ((int64_t)max(pb, 0) * a.G + g) * head_stride + (int64_t)((k0 + 16) % a.P) * D;
+    const int32_t k0 = TK * t;
+    int64_t base[TK / 16];  // byte offset of each 16-key group's first row (a group lies in one page)
+#pragma unroll
+    for (int u = 0; u < TK / 16; ++u)
+      base[u] = ((int64_t)max(page_of(k0 + 16 * u), 0) * a.G + g) * head_stride + (int64_t)((k0 + 16 * u) % a.P) * D;
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
       if (j % 4 != wave) continue;
@@ -138,7 +141,10 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
       if (jj == NDMA - 1 && lane >= Geo::TAIL) continue;
       const int o = 64 * jj + lane;
       const int row = o / STRIDE, c = min(o % STRIDE, CH - 1);
-      const int64_t off = (row < 16 ? ba : bb) + (int64_t)(row & 15) * D + 16 * c;
+      int64_t b16 = base[0];
+#pragma unroll
+      for (int u = 1; u < TK / 16; ++u) b16 = row >= 16 * u ? base[u] : b16;
+      const int64_t off = b16 + (int64_t)(row & 15) * D + 16 * c;
       const uint8_t* src = (j < NDMA ? a.k_cache : a.v_cache) + off;
       dma_global16(src, ring + slot * SLOT + (j < NDMA ? 0 : HALF) + 1024 * jj);
     }
@@ -147,45 +153,59 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
   auto compute = [&](int32_t t, int slot) {
     const uint8_t* K = &sm_ring[slot * SLOT];
     const uint8_t* V = K + HALF;
-    const int32_t k0 = 32 * t;
-    const int32_t pa = page_of(k0), pb = page_of(k0 + 16);
+    const int32_t k0 = TK * t;
+    int32_t pg[TK / 16];
+    bool pages_ok = true;
+#pragma unroll
+    for (int u = 0; u < TK / 16; ++u) {
+      pg[u] = page_of(k0 + 16 * u);
+      pages_ok = pages_ok && pg[u] >= 0;
+    }
     // a full tile: every key valid and visible to every row of the block
-    const bool full = pa >= 0 && pb >= 0 && k0 + 31 <= pos0 && (a.window == 0 || k0 > hi - 1 - a.window);
-    // S^T for both 16-key halves and both N tiles
-    f32x4_t st[2][2];
+    const bool full = pages_ok && k0 + TK - 1 <= pos0 && (a.window == 0 || k0 > hi - 1 - a.window);
+    // S^T for each sub-tile of 32 keys (both 16-key halves) and both N tiles
+    f32x4_t st[NSUB][2][2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int u = 0; u < NSUB; ++u)
 #pragma unroll
-      for (int n = 0; n < 2; ++n) st[h][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int n = 0; n < 2; ++n) st[u][h][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint2 kw = *reinterpret_cast<const uint2*>(K + (8 * (li >> 2) + 4 * h + (li & 3)) * RS + 32 * s + 8 * g4);
-        uint32_t kop[4];
-        fp8x4_to_bf16x4(kw.x, kop[0], kop[1]);
-        fp8x4_to_bf16x4(kw.y, kop[2], kop[3]);
+      for (int u = 0; u < NSUB; ++u) {
 #pragma unroll
-        for (int n = 0; n < 2; ++n) st[h][n] = mfma_16x16x32_bf16(kop, qf[n][s], st[h][n]);
+        for (int h = 0; h < 2; ++h) {
+          const uint2 kw = *reinterpret_cast<const uint2*>(K + (32 * u + 8 * (li >> 2) + 4 * h + (li & 3)) * RS +
+                                                           32 * s + 8 * g4);
+          uint32_t kop[4];
+          fp8x4_to_bf16x4(kw.x, kop[0], kop[1]);
+          fp8x4_to_bf16x4(kw.y, kop[2], kop[3]);
+#pragma unroll
+          for (int n = 0; n < 2; ++n) st[u][h][n] = mfma_16x16x32_bf16(kop, qf[n][s], st[u][h][n]);
+        }
       }
     }
-    // scores (log2 domain) of keys k0 + 8 g4 + j, j = 4 h + r
-    float x[2][8], tmax[2];
+    // scores (log2 domain) of keys k0 + 32 u + 8 g4 + j, j = 4 h + r
+    float x[NSUB][2][8], tmax[2];
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
       tmax[n] = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float v = st[j >> 2][n][j & 3] * qk_scale;
-        if (!full) {
-          const int32_t key = k0 + 8 * g4 + j;
-          const bool page_ok = (8 * g4 + j < 16 ? pa : pb) >= 0;
-          const bool vis = page_ok && key <= qpos[n] && (a.window == 0 || key > qpos[n] - a.window);
-          v = vis ? v : -INFINITY;
+      for (int u = 0; u < NSUB; ++u)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float v = st[u][j >> 2][n][j & 3] * qk_scale;
+          if (!full) {
+            const int32_t kk = 32 * u + 8 * g4 + j;  // key within the tile
+            const int32_t key = k0 + kk;
+            const bool vis = pg[kk >> 4] >= 0 && key <= qpos[n] && (a.window == 0 || key > qpos[n] - a.window);
+            v = vis ? v : -INFINITY;
+          }
+          x[u][n][j] = v;
+          tmax[n] = fmaxf(tmax[n], v);
         }
-        x[n][j] = v;
-        tmax[n] = fmaxf(tmax[n], v);
-      }
       tmax[n] = max_across_groups(tmax[n]);
     }
 #pragma unroll
@@ -199,52 +219,56 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
         for (int c = 0; c < NC; ++c) acc[n][c] *= alpha;
       }
     }
-    uint32_t pop[2][4];
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {
-      float p[8];
+    for (int u = 0; u < NSUB; ++u) {
+      uint32_t pop[2][4];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        p[j] = __builtin_amdgcn_exp2f(x[n][j] - m_ref[n]);
-        l_run[n] += p[j];
+      for (int n = 0; n < 2; ++n) {
+        float p[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          p[j] = __builtin_amdgcn_exp2f(x[u][n][j] - m_ref[n]);
+          l_run[n] += p[j];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) pop[n][k] = pack_bf16x2(p[2 * k], p[2 * k + 1]);
       }
+      // V bytes of keys no row may see (past the chunk or on an invalid page) are zeroed: a stale NaN would survive
+      // p = 0
+      uint32_t vm0 = 0xffffffffu, vm1 = 0xffffffffu;
+      if (!full) {
+        vm0 = vm1 = 0;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) pop[n][k] = pack_bf16x2(p[2 * k], p[2 * k + 1]);
-    }
-    // V bytes of keys no row may see (past the chunk or on an invalid page) are zeroed: a stale NaN would survive p = 0
-    uint32_t vm0 = 0xffffffffu, vm1 = 0xffffffffu;
-    if (!full) {
-      vm0 = vm1 = 0;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int32_t key = k0 + 8 * g4 + j;
-        const bool ok = key < hi && (8 * g4 + j < 16 ? pa : pb) >= 0;
-        if (ok) (j < 4 ? vm0 : vm1) |= 0xffu << (8 * (j & 3));
+        for (int j = 0; j < 8; ++j) {
+          const int32_t kk = 32 * u + 8 * g4 + j;
+          const bool ok = k0 + kk < hi && pg[kk >> 4] >= 0;
+          if (ok) (j < 4 ? vm0 : vm1) |= 0xffu << (8 * (j & 3));
+        }
       }
-    }
-    const uint8_t* Vt = V + (8 * g4 + (li >> 1)) * RS + 8 * (li & 1);
+      const uint8_t* Vt = V + (32 * u + 8 * g4 + (li >> 1)) * RS + 8 * (li & 1);
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const uint2 vw = lds_read_tr8(Vt + 16 * c);
-      uint32_t vop[4];
-      fp8x4_to_bf16x4(vw.x & vm0, vop[0], vop[1]);
-      fp8x4_to_bf16x4(vw.y & vm1, vop[2], vop[3]);
+      for (int c = 0; c < NC; ++c) {
+        const uint2 vw = lds_read_tr8(Vt + 16 * c);
+        uint32_t vop[4];
+        fp8x4_to_bf16x4(vw.x & vm0, vop[0], vop[1]);
+        fp8x4_to_bf16x4(vw.y & vm1, vop[2], vop[3]);
 #pragma unroll
-      for (int n = 0; n < 2; ++n) acc[n][c] = mfma_16x16x32_bf16(vop, pop[n], acc[n][c]);
+        for (int n = 0; n < 2; ++n) acc[n][c] = mfma_16x16x32_bf16(vop, pop[n], acc[n][c]);
+      }
     }
   };
 
   // The compiler's own loads (the query operand) complete here, in a wait it sees, before any DMA is in flight.
   __builtin_amdgcn_s_waitcnt(0x0f70);
 
-  const int32_t t_first = lo / 32, t_end = (hi + 31) / 32;
-  const int32_t chunk_tiles = (Geo::PAGES - 1) * a.P / 32;  // (a chunk may start mid-page: PAGES - 1 whole pages)
+  const int32_t t_first = lo / TK, t_end = (hi + TK - 1) / TK;
+  const int32_t chunk_tiles = (Geo::PAGES - 1) * a.P / TK;  // (a chunk may start mid-page: PAGES - 1 whole pages)
   for (int32_t c0 = t_first; c0 < t_end; c0 += chunk_tiles) {
     const int32_t c1 = min(c0 + chunk_tiles, t_end);
     // stage the table entries of pages [p0, p1) (ring and pages are free: the previous chunk drained)
     __syncthreads();
-    p0 = 32 * c0 / a.P;
-    const int32_t p1 = (32 * c1 - 1) / a.P + 1;
+    p0 = TK * c0 / a.P;
+    const int32_t p1 = (TK * c1 - 1) / a.P + 1;
     const int32_t* trow = a.table + (int64_t)r * a.table_stride;
     for (int32_t i = tid; i < p1 - p0; i += 256) {
       const int32_t col = p0 + i;

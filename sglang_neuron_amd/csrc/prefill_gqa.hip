@@ -65,8 +65,11 @@ struct PrefillGeo {
 };
 
 constexpr float kPrefillRescaleSlack = 8.0f;
+constexpr int kPrefillBufferFlags = 0x00020000;  // dword 3 of a raw buffer resource (gfx9 family)
 
-template <int D>
+// BUF: each cache is under 4 GiB, so its tiles load through a buffer resource (the page base a uniform SGPR offset);
+// otherwise through 64-bit addresses.
+template <int D, bool BUF>
 __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
   using Geo = PrefillGeo<D>;
   constexpr int CH = Geo::CH, STRIDE = Geo::STRIDE, RS = Geo::RS, HALF = Geo::HALF, SLOT = Geo::SLOT;
@@ -128,25 +131,54 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
 
   int32_t p0 = 0;  // first page index staged in sm_pages
   auto page_of = [&](int32_t key) -> int32_t { return sm_pages[key / a.P - p0]; };  // -1: invalid
+  // This wave's DMAs of a tile: the m-th is DMA j = wave + 4 m of the tile (K for j < NDMA, then V), whose 64 lanes
+  // fill LDS chunks 64 jj .. 64 jj + 63 of the K or V rows. Its rows span at most two 16-key groups (glo and glo + 1;
+  // a group lies in one page): per lane, the byte offset inside the group and whether the lane's row is in glo + 1.
+  static_assert(Geo::TAIL == 64, "every lane of every DMA lands inside the tile");
+  constexpr int MW = Geo::CNT_HI;
+  const int cnt = (wave < NI % 4 || NI % 4 == 0) ? Geo::CNT_HI : Geo::CNT_LO;
+  uint32_t dma_pk[MW];   // offset in the group | (lane's row in group glo + 1) << 31
+  int32_t dma_glo[MW];   // uniform
+  uint32_t dma_lds[MW];  // uniform LDS offset in the slot
+#pragma unroll
+  for (int m = 0; m < MW; ++m) {
+    const int j = min(wave + 4 * m, NI - 1);
+    const int jj = j < NDMA ? j : j - NDMA;
+    const int o = 64 * jj + lane;
+    const int row = o / STRIDE, c = min(o % STRIDE, CH - 1);
+    const int glo = (64 * jj / STRIDE) >> 4;
+    dma_glo[m] = glo;
+    dma_pk[m] = (uint32_t)((row & 15) * D + 16 * c) | ((uint32_t)((row >> 4) > glo) << 31);
+    dma_lds[m] = (j < NDMA ? 0 : HALF) + 1024 * jj;
+  }
+  const int64_t cache_bytes = a.num_blocks * a.G * head_stride;
+  const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.k_cache, (short)0, BUF ? (int)(uint32_t)cache_bytes : 0, kPrefillBufferFlags);
+  const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.v_cache, (short)0, BUF ? (int)(uint32_t)cache_bytes : 0, kPrefillBufferFlags);
   auto issue = [&](int32_t t, int slot) {
     const int32_t k0 = TK * t;
-    int64_t base[TK / 16];  // byte offset of each 16-key group's first row (a group lies in one page)
+    int64_t base[TK / 16 + 1];  // byte offset of each 16-key group's first row (one page), and a spare
 #pragma unroll
     for (int u = 0; u < TK / 16; ++u)
       base[u] = ((int64_t)max(page_of(k0 + 16 * u), 0) * a.G + g) * head_stride + (int64_t)((k0 + 16 * u) % a.P) * D;
+    base[TK / 16] = base[TK / 16 - 1];
 #pragma unroll
-    for (int j = 0; j < NI; ++j) {
-      if (j % 4 != wave) continue;
-      const int jj = j < NDMA ? j : j - NDMA;
-      if (jj == NDMA - 1 && lane >= Geo::TAIL) continue;
-      const int o = 64 * jj + lane;
-      const int row = o / STRIDE, c = min(o % STRIDE, CH - 1);
-      int64_t b16 = base[0];
+    for (int m = 0; m < MW; ++m) {
+      if (m >= cnt) break;
+      const int j = wave + 4 * m;
+      int64_t blo = base[0], bhi = base[1];
 #pragma unroll
-      for (int u = 1; u < TK / 16; ++u) b16 = row >= 16 * u ? base[u] : b16;
-      const int64_t off = b16 + (int64_t)(row & 15) * D + 16 * c;
-      const uint8_t* src = (j < NDMA ? a.k_cache : a.v_cache) + off;
-      dma_global16(src, ring + slot * SLOT + (j < NDMA ? 0 : HALF) + 1024 * jj);
+      for (int u = 1; u < TK / 16; ++u)
+        if (dma_glo[m] == u) blo = base[u], bhi = base[u + 1];
+      const uint32_t lds = ring + slot * SLOT + dma_lds[m];
+      if constexpr (BUF) {
+        const uint32_t voff = (uint32_t)((dma_pk[m] >> 31) ? bhi : blo) + (dma_pk[m] & 0x7fffffffu);  // < 4 GiB
+        dma_buffer16(j < NDMA ? k_rsrc : v_rsrc, lds, voff);
+      } else {
+        const int64_t off = ((dma_pk[m] >> 31) ? bhi : blo) + (int64_t)(dma_pk[m] & 0x7fffffffu);
+        dma_global16((j < NDMA ? a.k_cache : a.v_cache) + off, lds);
+      }
     }
   };
 
@@ -154,15 +186,12 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
     const uint8_t* K = &sm_ring[slot * SLOT];
     const uint8_t* V = K + HALF;
     const int32_t k0 = TK * t;
-    int32_t pg[TK / 16];
-    bool pages_ok = true;
+    uint32_t pg_ok = 0;  // bit u: the page of keys k0 + 16 u .. + 15 is valid (uniform)
 #pragma unroll
-    for (int u = 0; u < TK / 16; ++u) {
-      pg[u] = page_of(k0 + 16 * u);
-      pages_ok = pages_ok && pg[u] >= 0;
-    }
+    for (int u = 0; u < TK / 16; ++u) pg_ok |= (uint32_t)(page_of(k0 + 16 * u) >= 0) << u;
     // a full tile: every key valid and visible to every row of the block
-    const bool full = pages_ok && k0 + TK - 1 <= pos0 && (a.window == 0 || k0 > hi - 1 - a.window);
+    const bool full = pg_ok == (1u << (TK / 16)) - 1 && k0 + TK - 1 <= pos0 &&
+                      (a.window == 0 || k0 > hi - 1 - a.window);
     // S^T for each sub-tile of 32 keys (both 16-key halves) and both N tiles
     f32x4_t st[NSUB][2][2];
 #pragma unroll
@@ -187,26 +216,40 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
         }
       }
     }
-    // scores (log2 domain) of keys k0 + 32 u + 8 g4 + j, j = 4 h + r
+    // scores (log2 domain) of keys k0 + 32 u + 8 g4 + j, j = 4 h + r; a tile that is not full masks them in one block
     float x[NSUB][2][8], tmax[2];
 #pragma unroll
+    for (int u = 0; u < NSUB; ++u)
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[u][n][j] = st[u][j >> 2][n][j & 3];  // raw: qk_scale (> 0) joins later
+    if (!full) {
+#pragma unroll
+      for (int u = 0; u < NSUB; ++u) {
+        // the lane's keys k0 + 32 u + 8 g4 + j all lie in 16-key group 2 u + g4 / 2
+        const bool page_ok = (pg_ok >> (2 * u + (g4 >> 1))) & 1u;
+        const int32_t key0 = k0 + 32 * u + 8 * g4;
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+          const int32_t lo_n = a.window > 0 ? qpos[n] - a.window + 1 : INT32_MIN;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int32_t key = key0 + j;
+            const bool vis = page_ok & (key <= qpos[n]) & (key >= lo_n);
+            x[u][n][j] = vis ? x[u][n][j] : -INFINITY;
+          }
+        }
+      }
+    }
+#pragma unroll
     for (int n = 0; n < 2; ++n) {
-      tmax[n] = -INFINITY;
+      float m = x[0][n][0];
 #pragma unroll
       for (int u = 0; u < NSUB; ++u)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          float v = st[u][j >> 2][n][j & 3] * qk_scale;
-          if (!full) {
-            const int32_t kk = 32 * u + 8 * g4 + j;  // key within the tile
-            const int32_t key = k0 + kk;
-            const bool vis = pg[kk >> 4] >= 0 && key <= qpos[n] && (a.window == 0 || key > qpos[n] - a.window);
-            v = vis ? v : -INFINITY;
-          }
-          x[u][n][j] = v;
-          tmax[n] = fmaxf(tmax[n], v);
-        }
-      tmax[n] = max_across_groups(tmax[n]);
+        for (int j = 0; j < 8; ++j) m = fmaxf(m, x[u][n][j]);
+      tmax[n] = max_across_groups(m) * qk_scale;
     }
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
@@ -226,24 +269,23 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
       for (int n = 0; n < 2; ++n) {
         float p[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          p[j] = __builtin_amdgcn_exp2f(x[u][n][j] - m_ref[n]);
-          l_run[n] += p[j];
-        }
+        for (int j = 0; j < 8; ++j) p[j] = __builtin_amdgcn_exp2f(fmaf(x[u][n][j], qk_scale, -m_ref[n]));
 #pragma unroll
-        for (int k = 0; k < 4; ++k) pop[n][k] = pack_bf16x2(p[2 * k], p[2 * k + 1]);
+        for (int k = 0; k < 4; ++k) {
+          pop[n][k] = pack_bf16x2(p[2 * k], p[2 * k + 1]);
+          // the row sum adds the bf16 probabilities the numerator weighs (v_dot2 with a pair of ones)
+          l_run[n] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pop[n][k]),
+                                                     __builtin_bit_cast(bf16x2_t, 0x3f803f80u), l_run[n], false);
+        }
       }
       // V bytes of keys no row may see (past the chunk or on an invalid page) are zeroed: a stale NaN would survive
       // p = 0
       uint32_t vm0 = 0xffffffffu, vm1 = 0xffffffffu;
       if (!full) {
-        vm0 = vm1 = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int32_t kk = 32 * u + 8 * g4 + j;
-          const bool ok = k0 + kk < hi && pg[kk >> 4] >= 0;
-          if (ok) (j < 4 ? vm0 : vm1) |= 0xffu << (8 * (j & 3));
-        }
+        const bool page_ok = (pg_ok >> (2 * u + (g4 >> 1))) & 1u;
+        const int32_t nvalid = page_ok ? min(max(hi - (k0 + 32 * u + 8 * g4), 0), 8) : 0;  // keys below hi
+        vm0 = nvalid >= 4 ? 0xffffffffu : (1u << (8 * nvalid)) - 1u;
+        vm1 = nvalid >= 8 ? 0xffffffffu : nvalid <= 4 ? 0u : (1u << (8 * (nvalid - 4))) - 1u;
       }
       const uint8_t* Vt = V + (32 * u + 8 * g4 + (li >> 1)) * RS + 8 * (li & 1);
 #pragma unroll
@@ -370,10 +412,15 @@ extern "C" int sna_prefill_attention(const void* q, const void* k_cache, const v
   const dim3 grid((unsigned)((max_q_len + a.bq - 1) / a.bq), (unsigned)R, (unsigned)num_kv_heads);
   hipEvent_t t0, t1;
   timing_events(0, &t0, &t1);
-  if (head_dim == 128)
-    hipExtLaunchKernelGGL((prefill_gqa_kernel<128>), grid, dim3(256), 0, (hipStream_t)stream, t0, t1, 0, a);
+  const bool buf = num_blocks * num_kv_heads * (int64_t)page_size * head_dim < ((int64_t)1 << 32);
+  if (head_dim == 128 && buf)
+    hipExtLaunchKernelGGL((prefill_gqa_kernel<128, true>), grid, dim3(256), 0, (hipStream_t)stream, t0, t1, 0, a);
+  else if (head_dim == 128)
+    hipExtLaunchKernelGGL((prefill_gqa_kernel<128, false>), grid, dim3(256), 0, (hipStream_t)stream, t0, t1, 0, a);
+  else if (buf)
+    hipExtLaunchKernelGGL((prefill_gqa_kernel<64, true>), grid, dim3(256), 0, (hipStream_t)stream, t0, t1, 0, a);
   else
-    hipExtLaunchKernelGGL((prefill_gqa_kernel<64>), grid, dim3(256), 0, (hipStream_t)stream, t0, t1, 0, a);
+    hipExtLaunchKernelGGL((prefill_gqa_kernel<64, false>), grid, dim3(256), 0, (hipStream_t)stream, t0, t1, 0, a);
   timing_end_call();
   return check_launch("prefill_attention");
 }

@@ -97,7 +97,12 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
   // ---- this lane's two rows (N tiles n = 0, 1): token, head, position, and the query operand ----
   int32_t tok[2], head[2], qpos[2];
   bool row_ok[2];
-  uint32_t qf[2][NS][4];
+  // The query operand of the FP8 QK: lane (g4, i) supplies dims 32 g4 .. 32 g4 + 31 of row i (zeros past d), the bf16
+  // values scaled by a power of two sc (the row's absolute maximum into [128, 256)) and split exactly into two e4m3fn
+  // parts, hi + lo / 16 (hi keeps the top 4 significant bits, lo the next 4). The MFMA's per-lane E8M0 B scales
+  // undo sc (and the 1/16 of lo), so K . Q is the exact bf16 dot product accumulated in fp32.
+  uint32_t qhi[2][8], qlo[2][8];
+  int32_t qsc_hi[2], qsc_lo[2];
 #pragma unroll
   for (int n = 0; n < 2; ++n) {
     const int32_t row = 32 * wave + 16 * n + li;
@@ -107,11 +112,37 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
     tok[n] = qa + q0 + t;
     head[n] = g * a.group + row % a.group;
     qpos[n] = pos0 + t;
-    const uint16_t* qp = a.q + ((int64_t)tok[n] * a.H + head[n]) * D + 8 * g4;
+    float v[32];
+    const bool mine = 32 * g4 < D;
+    const uint16_t* qp = a.q + ((int64_t)tok[n] * a.H + head[n]) * D + (mine ? 32 * g4 : 0);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const uint4 w = ld16(qp + 32 * s);
-      qf[n][s][0] = w.x, qf[n][s][1] = w.y, qf[n][s][2] = w.z, qf[n][s][3] = w.w;
+    for (int c = 0; c < 4; ++c) {
+      const uint4 w = mine ? ld16(qp + 8 * c) : make_uint4(0, 0, 0, 0);
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[8 * c + 2 * e] = bf16_bits_to_f32(ww[e] & 0xffffu);
+        v[8 * c + 2 * e + 1] = bf16_bits_to_f32(ww[e] >> 16);
+      }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(v[e]));
+    amax = max_across_groups(amax);
+    // sc = 2^(7 - floor(log2 amax)): amax * sc in [128, 256); E8M0 scale of hi = 127 - log2 sc, of lo 4 less
+    // (the exponent is held to [-116, 127], where sc and both E8M0 scales are representable; a row that small only
+    // loses bits far below the tolerance)
+    const int32_t ex = amax > 0.0f ? max((int32_t)((__float_as_uint(amax) >> 23) & 0xff) - 127, -116) : -7;
+    const float sc = __uint_as_float((uint32_t)(127 + 7 - ex) << 23);
+    qsc_hi[n] = 127 + ex - 7;
+    qsc_lo[n] = 127 + ex - 7 - 4;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      float h4[4], l4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) split_q(v[4 * k + e] * sc, h4[e], l4[e]);
+      qhi[n][k] = pack_e4m3fn_x4(h4[0], h4[1], h4[2], h4[3]);
+      qlo[n][k] = pack_e4m3fn_x4(l4[0], l4[1], l4[2], l4[3]);
     }
   }
   const float qk_scale = a.sm_scale * kLog2e * a.k_scale[g];
@@ -201,18 +232,21 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
 #pragma unroll
         for (int n = 0; n < 2; ++n) st[u][h][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
+    for (int u = 0; u < NSUB; ++u) {
 #pragma unroll
-      for (int u = 0; u < NSUB; ++u) {
+      for (int h = 0; h < 2; ++h) {
+        // the K bytes of the lane's key, dims 32 g4 .. + 31, straight from LDS (e4m3fn, no conversion)
+        uint32_t kop[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (32 * g4 < D) {
+          const uint8_t* kr = K + (32 * u + 8 * (li >> 2) + 4 * h + (li & 3)) * RS + 32 * g4;
+          const uint4 w0 = *reinterpret_cast<const uint4*>(kr), w1 = *reinterpret_cast<const uint4*>(kr + 16);
+          kop[0] = w0.x, kop[1] = w0.y, kop[2] = w0.z, kop[3] = w0.w;
+          kop[4] = w1.x, kop[5] = w1.y, kop[6] = w1.z, kop[7] = w1.w;
+        }
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const uint2 kw = *reinterpret_cast<const uint2*>(K + (32 * u + 8 * (li >> 2) + 4 * h + (li & 3)) * RS +
-                                                           32 * s + 8 * g4);
-          uint32_t kop[4];
-          fp8x4_to_bf16x4(kw.x, kop[0], kop[1]);
-          fp8x4_to_bf16x4(kw.y, kop[2], kop[3]);
-#pragma unroll
-          for (int n = 0; n < 2; ++n) st[u][h][n] = mfma_16x16x32_bf16(kop, qf[n][s], st[u][h][n]);
+        for (int n = 0; n < 2; ++n) {
+          st[u][h][n] = mfma_16x16x128_fp8(kop, qhi[n], st[u][h][n], qsc_hi[n]);
+          st[u][h][n] = mfma_16x16x128_fp8(kop, qlo[n], st[u][h][n], qsc_lo[n]);
         }
       }
     }

@@ -60,7 +60,8 @@ struct PrefillGeo {
   static constexpr int TAIL = TK * STRIDE - 64 * (NDMA - 1);  // active lanes of the last one
   static constexpr int NI = 2 * NDMA;                        // DMAs of a tile, dealt round-robin to the 4 waves
   static constexpr int CNT_HI = (NI + 3) / 4, CNT_LO = NI / 4;  // a wave's DMAs per tile (waves < NI % 4: CNT_HI)
-  static constexpr int DEPTH = 3;
+  static constexpr int DEPTH = 2;                            // the FP8 ring: one tile loads while one computes
+  static constexpr int VT_RS = 2 * TK + 16;                  // bf16 V^T: a dim's TK keys, padded
   static constexpr int PAGES = 2048;  // block-table entries staged in LDS at a time
 };
 
@@ -80,6 +81,8 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
   typedef __attribute__((address_space(3))) uint8_t lds_u8;
   __shared__ __attribute__((aligned(16))) uint8_t sm_ring[DEPTH * SLOT];
   __shared__ int32_t sm_pages[Geo::PAGES];
+  // The current tile's V, transposed and converted once (each wave a quarter): row d holds the TK keys' bf16 values.
+  __shared__ __attribute__((aligned(16))) uint8_t sm_vt[D * Geo::VT_RS];
 
   const int tid = threadIdx.x, lane = tid & 63, g4 = lane >> 4, li = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -215,7 +218,6 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
 
   auto compute = [&](int32_t t, int slot) {
     const uint8_t* K = &sm_ring[slot * SLOT];
-    const uint8_t* V = K + HALF;
     const int32_t k0 = TK * t;
     uint32_t pg_ok = 0;  // bit u: the page of keys k0 + 16 u .. + 15 is valid (uniform)
 #pragma unroll
@@ -296,6 +298,7 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
         for (int c = 0; c < NC; ++c) acc[n][c] *= alpha;
       }
     }
+    __syncthreads();  // sm_vt holds this tile's V^T (every wave's quarter)
 #pragma unroll
     for (int u = 0; u < NSUB; ++u) {
       uint32_t pop[2][4];
@@ -312,25 +315,45 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
                                                      __builtin_bit_cast(bf16x2_t, 0x3f803f80u), l_run[n], false);
         }
       }
-      // V bytes of keys no row may see (past the chunk or on an invalid page) are zeroed: a stale NaN would survive
-      // p = 0
+      const uint8_t* Vr = &sm_vt[li * Geo::VT_RS + (32 * u + 8 * g4) * 2];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const uint4 w = *reinterpret_cast<const uint4*>(Vr + 16 * c * Geo::VT_RS);
+        const uint32_t vop[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int n = 0; n < 2; ++n) acc[n][c] = mfma_16x16x32_bf16(vop, pop[n], acc[n][c]);
+      }
+    }
+  };
+
+  // Tile t's V (ring slot `slot`) into sm_vt as bf16 V^T: pair e = (sub-tile u, dim tile c) of the tile's NSUB x NC
+  // goes to wave e % 4, whose lane (g4, i) reads keys 32 u + 8 g4 .. + 7 at dim 16 c + i (one ds_read_b64_tr_b8),
+  // converts them and stores the 16 bytes at row 16 c + i. Keys no row may see (past the chunk or on an invalid
+  // page) are zeroed, since a stale NaN would survive p = 0.
+  auto convert_v = [&](int32_t t, int slot) {
+    const uint8_t* V = &sm_ring[slot * SLOT] + HALF;
+    const int32_t k0 = TK * t;
+    uint32_t pg_ok = 0;
+#pragma unroll
+    for (int u = 0; u < TK / 16; ++u) pg_ok |= (uint32_t)(page_of(k0 + 16 * u) >= 0) << u;
+    const bool clean = pg_ok == (1u << (TK / 16)) - 1 && k0 + TK <= hi;
+#pragma unroll
+    for (int q = 0; q < NSUB * NC / 4; ++q) {
+      const int e = wave + 4 * q;
+      const int u = e / NC, c = e % NC;
       uint32_t vm0 = 0xffffffffu, vm1 = 0xffffffffu;
-      if (!full) {
+      if (!clean) {
         const bool page_ok = (pg_ok >> (2 * u + (g4 >> 1))) & 1u;
         const int32_t nvalid = page_ok ? min(max(hi - (k0 + 32 * u + 8 * g4), 0), 8) : 0;  // keys below hi
         vm0 = nvalid >= 4 ? 0xffffffffu : (1u << (8 * nvalid)) - 1u;
         vm1 = nvalid >= 8 ? 0xffffffffu : nvalid <= 4 ? 0u : (1u << (8 * (nvalid - 4))) - 1u;
       }
-      const uint8_t* Vt = V + (32 * u + 8 * g4 + (li >> 1)) * RS + 8 * (li & 1);
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const uint2 vw = lds_read_tr8(Vt + 16 * c);
-        uint32_t vop[4];
-        fp8x4_to_bf16x4(vw.x & vm0, vop[0], vop[1]);
-        fp8x4_to_bf16x4(vw.y & vm1, vop[2], vop[3]);
-#pragma unroll
-        for (int n = 0; n < 2; ++n) acc[n][c] = mfma_16x16x32_bf16(vop, pop[n], acc[n][c]);
-      }
+      const uint2 vw = lds_read_tr8(V + (32 * u + 8 * g4 + (li >> 1)) * RS + 8 * (li & 1) + 16 * c);
+      uint32_t o[4];
+      fp8x4_to_bf16x4(vw.x & vm0, o[0], o[1]);
+      fp8x4_to_bf16x4(vw.y & vm1, o[2], o[3]);
+      *reinterpret_cast<uint4*>(&sm_vt[(16 * c + li) * Geo::VT_RS + (32 * u + 8 * g4) * 2]) = make_uint4(o[0], o[1], o[2],
+                                                                                                       o[3]);
     }
   };
 
@@ -353,21 +376,14 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
     }
     __syncthreads();
     const int32_t n = c1 - c0;
-#pragma unroll
-    for (int i = 0; i < DEPTH - 1; ++i)
-      if (i < n) issue(c0 + i, i);
+    static_assert(DEPTH == 2, "tile i + 1 loads while tile i computes");
+    issue(c0, 0);
     for (int32_t i = 0; i < n; ++i) {
-      // this wave's DMAs of tile i have landed once at most the next tile's remain in flight
-      if (i + 1 < n) {
-        if (wave < NI % 4 || NI % 4 == 0)
-          wait_vmcnt<Geo::CNT_HI>();
-        else
-          wait_vmcnt<Geo::CNT_LO>();
-      } else {
-        wait_vmcnt<0>();
-      }
-      __syncthreads();  // every wave's DMAs of tile i have landed, and every wave is done with tile i - 1's slot
-      if (i + DEPTH - 1 < n) issue(c0 + i + DEPTH - 1, (i + DEPTH - 1) % DEPTH);
+      wait_vmcnt<0>();  // this wave's DMAs of tile i have landed (tile i + 1 is not issued yet)
+      // every wave's DMAs of tile i have landed; every wave is done with tile i - 1 (its slot and sm_vt are free)
+      __syncthreads();
+      if (i + 1 < n) issue(c0 + i + 1, (i + 1) % DEPTH);
+      convert_v(c0 + i, i % DEPTH);
       compute(c0 + i, i % DEPTH);
     }
   }

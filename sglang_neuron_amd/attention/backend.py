@@ -2,9 +2,10 @@
 
 Mirrors sglang_neuron/attention/backend.py: ``NeuronForwardMetadata`` (:29-38) and ``NeuronAttnBackend`` (:41-148)
 with the same constructor, hooks and ``build_metadata`` / ``_block_table`` semantics. The reference leaves
-``forward_decode`` to its compiled graphs and raises (:147-148); here it runs: the step's new K/V (or MLA row) is
-stored at ``out_cache_loc`` when ``save_kv_cache`` is set and attended in-band, then the paged split-K decode runs
-over the pool, all on torch's current stream.
+``forward_decode`` (and ``forward_extend``) to its compiled graphs and raises (:143-148); here they run: the step's
+new K/V (or MLA row) is stored at ``out_cache_loc`` when ``save_kv_cache`` is set, then the paged split-K decode (or,
+for an extend batch on the MHA pool, the segmented prefill attention) runs over the pool, all on torch's current
+stream.
 
 Metadata conventions (attention/backend.py:5-8, :114-130): ``block_table[b, j] = req_to_token[row_b, j * page] //
 page`` (int32), -1 where ``j * page >= seq_len_b`` when the batch has more than one row; ``seq_lens`` count the new
@@ -47,6 +48,17 @@ class _DecodeState:
     plans: dict
     host_lens: Optional[Tensor] = None  # [bs] host seq_lens when known (exact split plans), else None
     max_len: int = -1  # a bound on seq_lens (plans when host_lens is None)
+
+
+@dataclass
+class _ExtendState:
+    """The device copies of one extend forward, shared by its layers."""
+    meta: NeuronForwardMetadata
+    table: Tensor  # [bs, max_blocks] int32, device
+    slots: Tensor  # [T] int64, device
+    q_start: Tensor  # [bs + 1] int32, device
+    prior: Tensor  # [bs] int32, device (extend_prefix_lens)
+    max_q_len: int
 
 
 class NeuronAttnBackend:
@@ -188,8 +200,63 @@ class NeuronAttnBackend:
             pass
         return st
 
-    def forward_extend(self, q, k, v, layer, forward_batch, save_kv_cache=True, **kwargs):
-        raise NotImplementedError("this build runs the paged decode path only (prefill is out of its scope)")
+    def _extend_state(self, fb, device: torch.device) -> _ExtendState:
+        st = getattr(fb, "_sna_extend_state", None)
+        if st is not None and st.table.device == device:
+            return st
+        on_device = self.req_to_token_pool.req_to_token.is_cuda
+        meta = self.build_device_metadata(fb, device) if on_device else self.build_metadata(fb)
+        if not meta.is_prefill:
+            raise ValueError("forward_extend got a batch that is not an extend batch")
+        bs = meta.batch_size
+        ext_cpu = getattr(fb, "extend_seq_lens_cpu", None)
+        ext = torch.as_tensor(ext_cpu if ext_cpu is not None else fb.extend_seq_lens.cpu(), dtype=torch.long)[:bs]
+        prefix = torch.as_tensor(fb.extend_prefix_lens, device=device).to(torch.int32)[:bs]
+        if int(ext.sum()) != meta.num_tokens:
+            raise ValueError(f"extend lengths sum to {int(ext.sum())}, the batch has {meta.num_tokens} tokens")
+        q_start = torch.zeros(bs + 1, dtype=torch.int32)
+        q_start[1:] = torch.cumsum(ext, 0)
+        st = _ExtendState(meta=meta, table=meta.block_table.to(device), slots=meta.slot_mapping.to(device),
+                          q_start=q_start.to(device), prior=prefix, max_q_len=int(ext.max()) if bs else 0)
+        try:
+            fb._sna_extend_state = st
+        except AttributeError:
+            pass
+        return st
+
+    def forward_extend(self, q: Tensor, k: Optional[Tensor], v: Optional[Tensor], layer, forward_batch,
+                       save_kv_cache: bool = True, **kwargs) -> Tensor:
+        """An extend (prefill) step of ``layer`` on the MHA pool: the chunk's K/V [T, G * d] stored at
+        ``out_cache_loc`` (when ``save_kv_cache``), then segmented prefill attention (ops.prefill_attention): request
+        r's ``extend_seq_lens[r]`` new tokens, at positions ``extend_prefix_lens[r] + i``, attend to its prior and
+        causally to themselves, every key read from the pool. q [T, H * d] or [T, H, d]; ``layer`` as in
+        forward_decode (window, sinks). Returns [T, H * d] bf16. The reference leaves extend to its compiled graphs
+        and raises (attention/backend.py:143-145); the FP8 pool is required (the prefill kernel reads e4m3fn)."""
+        if q.device.type != "cuda":
+            raise RuntimeError("forward_extend runs on the GPU (there is no CPU path)")
+        pool = self.token_to_kv_pool
+        if not isinstance(pool, NeuronMHATokenToKVPool):
+            raise NotImplementedError(f"forward_extend runs on the MHA pool, not {type(pool).__name__}")
+        st = self._extend_state(forward_batch, q.device)
+        T = st.meta.num_tokens
+        layer_id = int(layer.layer_id)
+        H, G = int(layer.tp_q_head_num), int(layer.tp_k_head_num)
+        d = int(getattr(layer, "head_dim", pool.head_dim))
+        if G != pool.head_num or d != pool.head_dim:
+            raise ValueError(f"layer {layer_id} has {G} KV heads of {d}, the pool {pool.head_num} of {pool.head_dim}")
+        window = getattr(layer, "sliding_window_size", None)
+        window = int(window) if window is not None and int(window) > 0 else 0
+        sinks = kwargs.get("sinks")
+        if sinks is None:
+            sinks = getattr(layer, "sinks", None)
+        if save_kv_cache:
+            pool.set_kv_buffer(layer, st.slots, k.reshape(T, G, d), v.reshape(T, G, d))
+        k_cache, v_cache = pool.get_kv_buffer(layer_id)
+        k_scale, v_scale = pool.get_kv_scales(layer_id)
+        out = ops.prefill_attention(q.reshape(T, H, d), k_cache, v_cache, st.table, st.q_start, st.prior,
+                                    max_q_len=st.max_q_len, sm_scale=float(layer.scaling), k_scale=k_scale,
+                                    v_scale=v_scale, sinks=sinks, window=window)
+        return out.reshape(T, H * d)
 
     def forward_decode(self, q: Tensor, k: Optional[Tensor], v: Optional[Tensor], layer, forward_batch,
                        save_kv_cache: bool = True, **kwargs) -> Tensor:

@@ -10,6 +10,8 @@ import torch
 
 from conftest import announce
 from _harness import assert_close_attn, dsa_oracle, gqa_oracle, mla_oracle
+from oracle import attention as oatt
+from oracle import store as ost
 from sglang_neuron_amd import workloads
 from sglang_neuron_amd.attention import NeuronAttnBackend
 from sglang_neuron_amd.mem_cache import NeuronDSATokenToKVPool, NeuronMHATokenToKVPool, NeuronMLATokenToKVPool
@@ -203,3 +205,90 @@ def test_backend_mla_device_metadata(host_lens):
         assert torch.equal(out, host)
     assert_close_attn(out.reshape(case.B, case.H, 512), want, "mla device metadata")
     assert torch.equal(pool.kv_buffer[0].cpu().reshape(-1, 576), cache_o), "row pool differs"
+
+
+class _Extend:
+    def is_extend(self):
+        return True
+
+    def is_idle(self):
+        return False
+
+
+EXTEND = [("qwen3-8b-shape", 21, dict(H=32, G=8, d=128, P=16), (50, 0, 300), (40, 70, 5), 0, False),
+          ("gpt-oss-share-swa-sinks", 22, dict(H=8, G=1, d=64, P=16), (200, 17), (150, 33), 128, True)]
+
+
+@pytest.mark.parametrize("device_r2t", [False, True], ids=["host-r2t", "device-r2t"])
+@pytest.mark.parametrize("name,seed,shape,priors,ext,window,sinks", EXTEND, ids=[e[0] for e in EXTEND])
+def test_backend_extend_then_decode(name, seed, shape, priors, ext, window, sinks, device_r2t):
+    """An extend batch through forward_extend (its K/V stored, then segmented prefill attention over the pool), then
+    one decode step through forward_decode over the pool the extend wrote: attention within the bar against the
+    oracle's segmented prefill and decode on the pool's bytes, the pool bit-exact against the oracle's store."""
+    H, G, d, P = shape["H"], shape["G"], shape["d"], shape["P"]
+    R = len(priors)
+    announce(f"backend extend+decode {name} device_r2t={device_r2t}")
+    g = torch.Generator().manual_seed(seed)
+    totals = [p + e + 1 for p, e in zip(priors, ext)]  # prior, the extend chunk, one decoded token
+    pages = [-(-x // P) for x in totals]
+    nb = sum(pages) + 3
+    perm = torch.randperm(nb - 1, generator=g) + 1
+    table = torch.full((R, max(pages)), -1, dtype=torch.int32)
+    used = 0
+    for r, n in enumerate(pages):
+        table[r, :n] = perm[used:used + n].to(torch.int32)
+        used += n
+    slot_of = lambda r, pos: int(table[r, pos // P]) * P + pos % P  # noqa: E731
+    ks_tok = [torch.randn(x, G, d, generator=g).to(torch.bfloat16) for x in totals]
+    vs_tok = [torch.randn(x, G, d, generator=g).to(torch.bfloat16) for x in totals]
+    pool = NeuronMHATokenToKVPool((nb - 1) * P, P, torch.float8_e4m3fn, G, d, 1, DEV)
+    kscale, vscale = pool.calibrate_kv_scales(0, torch.cat(ks_tok).to(DEV), torch.cat(vs_tok).to(DEV))
+    sk = torch.randn(H, generator=g) if sinks else None
+    layer = SimpleNamespace(layer_id=0, tp_q_head_num=H, tp_k_head_num=G, head_dim=d, scaling=d ** -0.5,
+                            sliding_window_size=window if window else -1, sinks=None if sk is None else sk.to(DEV))
+    prior_slots = torch.tensor([slot_of(r, i) for r in range(R) for i in range(priors[r])], dtype=torch.int64)
+    if prior_slots.numel():
+        pool.set_kv_buffer(layer, prior_slots.to(DEV), torch.cat([ks_tok[r][:priors[r]] for r in range(R)]).to(DEV),
+                           torch.cat([vs_tok[r][:priors[r]] for r in range(R)]).to(DEV))
+    backend = _backend(pool, table, torch.tensor(totals), P, device_r2t=device_r2t)
+
+    # extend
+    ext_slots = torch.tensor([slot_of(r, priors[r] + i) for r in range(R) for i in range(ext[r])], dtype=torch.int64)
+    k_ext = torch.cat([ks_tok[r][priors[r]:priors[r] + ext[r]] for r in range(R)])
+    v_ext = torch.cat([vs_tok[r][priors[r]:priors[r] + ext[r]] for r in range(R)])
+    T = sum(ext)
+    q_ext = torch.randn(T, H, d, generator=g).to(torch.bfloat16)
+    seq_ext = torch.tensor([p + e for p, e in zip(priors, ext)], dtype=torch.int64)
+    fb = SimpleNamespace(forward_mode=_Extend(), batch_size=R, req_pool_indices=torch.arange(R),
+                         seq_lens=seq_ext.to(DEV), seq_lens_cpu=seq_ext, extend_seq_lens=torch.tensor(ext).to(DEV),
+                         extend_seq_lens_cpu=list(ext), extend_prefix_lens=torch.tensor(priors).to(DEV),
+                         out_cache_loc=ext_slots.to(DEV),
+                         positions=torch.cat([torch.arange(p, p + e) for p, e in zip(priors, ext)]).to(DEV))
+    out = backend.forward_extend(q_ext.reshape(T, H * d).to(DEV), k_ext.reshape(T, G * d).to(DEV),
+                                 v_ext.reshape(T, G * d).to(DEV), layer, fb)
+    torch.cuda.synchronize()
+    kc_o = torch.zeros(nb, G, P, d, dtype=torch.uint8)
+    vc_o = torch.zeros_like(kc_o)
+    all_slots = torch.cat([prior_slots, ext_slots])
+    ost.kv_store_mha(torch.cat([torch.cat([ks_tok[r][:priors[r]] for r in range(R)]), k_ext]),
+                     torch.cat([torch.cat([vs_tok[r][:priors[r]] for r in range(R)]), v_ext]), all_slots, kc_o, vc_o,
+                     kscale.cpu(), vscale.cpu())
+    k_pool, v_pool = (t.cpu().view(torch.uint8) for t in pool.get_kv_buffer(0))
+    assert torch.equal(k_pool, kc_o) and torch.equal(v_pool, vc_o), "pool after extend differs"
+    q_start = torch.tensor([0] + torch.tensor(ext).cumsum(0).tolist(), dtype=torch.int32)
+    want = oatt.segmented_prefill(q_ext, k_pool, v_pool, table, q_start, torch.tensor(priors), sm_scale=d ** -0.5,
+                                  k_scale=kscale.cpu(), v_scale=vscale.cpu(), sinks=sk, window=window)
+    assert_close_attn(out.reshape(T, H, d).cpu(), want, f"{name} extend")
+
+    # one decode step over the pool the extend wrote
+    L = torch.tensor(totals, dtype=torch.int64)
+    new_slots = torch.tensor([slot_of(r, totals[r] - 1) for r in range(R)], dtype=torch.int64)
+    k_new = torch.stack([ks_tok[r][-1] for r in range(R)])
+    v_new = torch.stack([vs_tok[r][-1] for r in range(R)])
+    q_dec = torch.randn(R, H, d, generator=g).to(torch.bfloat16)
+    out_d = backend.forward_decode(q_dec.reshape(R, H * d).to(DEV), k_new.reshape(R, G * d).to(DEV),
+                                   v_new.reshape(R, G * d).to(DEV), layer, _batch(L, new_slots))
+    torch.cuda.synchronize()
+    want_d = oatt.paged_decode_gqa(q_dec, k_pool, v_pool, table, L, k_new, v_new, sm_scale=d ** -0.5,
+                                   k_scale=kscale.cpu(), v_scale=vscale.cpu(), sinks=sk, window=window)
+    assert_close_attn(out_d.reshape(R, H, d).cpu(), want_d, f"{name} decode after extend")

@@ -231,7 +231,7 @@ class NeuronAttnBackend:
         r's ``extend_seq_lens[r]`` new tokens, at positions ``extend_prefix_lens[r] + i``, attend to its prior and
         causally to themselves, every key read from the pool. q [T, H * d] or [T, H, d]; ``layer`` as in
         forward_decode (window, sinks). Returns [T, H * d] bf16. The reference leaves extend to its compiled graphs
-        and raises (attention/backend.py:143-145); the FP8 pool is required (the prefill kernel reads e4m3fn)."""
+        and raises (attention/backend.py:143-145). FP8 and bf16 pools."""
         if q.device.type != "cuda":
             raise RuntimeError("forward_extend runs on the GPU (there is no CPU path)")
         pool = self.token_to_kv_pool

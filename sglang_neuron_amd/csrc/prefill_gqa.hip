@@ -47,11 +47,12 @@ struct PrefillArgs {
   int32_t window;
 };
 
-template <int D>
+template <int D, int ESZ>  // ESZ: bytes per K/V element (1: e4m3fn, 2: bf16)
 struct PrefillGeo {
-  static constexpr int TK = 64;                              // keys per tile: NSUB sub-tiles of 32
+  static constexpr int TK = ESZ == 1 ? 64 : 32;              // keys per tile: NSUB sub-tiles of 32
   static constexpr int NSUB = TK / 32;
-  static constexpr int CH = D / 16;                          // 16-byte chunks of a K or V row
+  static constexpr int ROWB = D * ESZ;                       // bytes of a K or V row
+  static constexpr int CH = ROWB / 16;                       // 16-byte chunks of a K or V row
   static constexpr int STRIDE = CH + 1;                      // plus a pad chunk
   static constexpr int RS = 16 * STRIDE;                     // LDS row stride, bytes
   static constexpr int HALF = TK * RS;                       // the K (or V) rows of a tile
@@ -60,7 +61,7 @@ struct PrefillGeo {
   static constexpr int TAIL = TK * STRIDE - 64 * (NDMA - 1);  // active lanes of the last one
   static constexpr int NI = 2 * NDMA;                        // DMAs of a tile, dealt round-robin to the 4 waves
   static constexpr int CNT_HI = (NI + 3) / 4, CNT_LO = NI / 4;  // a wave's DMAs per tile (waves < NI % 4: CNT_HI)
-  static constexpr int DEPTH = 2;                            // the FP8 ring: one tile loads while one computes
+  static constexpr int DEPTH = 2;                            // the ring: one tile loads while one computes
   static constexpr int VT_RS = 2 * TK + 16;                  // bf16 V^T: a dim's TK keys, padded
   static constexpr int PAGES = 2048;  // block-table entries staged in LDS at a time
 };
@@ -70,9 +71,10 @@ constexpr int kPrefillBufferFlags = 0x00020000;  // dword 3 of a raw buffer reso
 
 // BUF: each cache is under 4 GiB, so its tiles load through a buffer resource (the page base a uniform SGPR offset);
 // otherwise through 64-bit addresses.
-template <int D, bool BUF>
+template <int D, bool BUF, int ESZ>
 __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
-  using Geo = PrefillGeo<D>;
+  using Geo = PrefillGeo<D, ESZ>;
+  constexpr int ROWB = Geo::ROWB;
   constexpr int CH = Geo::CH, STRIDE = Geo::STRIDE, RS = Geo::RS, HALF = Geo::HALF, SLOT = Geo::SLOT;
   constexpr int NDMA = Geo::NDMA, NI = Geo::NI, DEPTH = Geo::DEPTH, TK = Geo::TK, NSUB = Geo::NSUB;
   constexpr int NS = D / 32;  // QK steps
@@ -104,8 +106,10 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
   // values scaled by a power of two sc (the row's absolute maximum into [128, 256)) and split exactly into two e4m3fn
   // parts, hi + lo / 16 (hi keeps the top 4 significant bits, lo the next 4). The MFMA's per-lane E8M0 B scales
   // undo sc (and the 1/16 of lo), so K . Q is the exact bf16 dot product accumulated in fp32.
+  // A bf16 pool instead takes the bf16 query elements 32 s + 8 g4 .. + 7 for v_mfma_f32_16x16x32_bf16 (qf).
   uint32_t qhi[2][8], qlo[2][8];
   int32_t qsc_hi[2], qsc_lo[2];
+  uint32_t qf[2][ESZ == 2 ? NS : 1][4];
 #pragma unroll
   for (int n = 0; n < 2; ++n) {
     const int32_t row = 32 * wave + 16 * n + li;
@@ -115,6 +119,15 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
     tok[n] = qa + q0 + t;
     head[n] = g * a.group + row % a.group;
     qpos[n] = pos0 + t;
+    if constexpr (ESZ == 2) {
+      const uint16_t* qb = a.q + ((int64_t)tok[n] * a.H + head[n]) * D + 8 * g4;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const uint4 w = ld16(qb + 32 * s);
+        qf[n][s][0] = w.x, qf[n][s][1] = w.y, qf[n][s][2] = w.z, qf[n][s][3] = w.w;
+      }
+      continue;
+    }
     float v[32];
     const bool mine = 32 * g4 < D;
     const uint16_t* qp = a.q + ((int64_t)tok[n] * a.H + head[n]) * D + (mine ? 32 * g4 : 0);
@@ -148,8 +161,8 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
       qlo[n][k] = pack_e4m3fn_x4(l4[0], l4[1], l4[2], l4[3]);
     }
   }
-  const float qk_scale = a.sm_scale * kLog2e * a.k_scale[g];
-  const float v_scale = a.v_scale[g];
+  const float qk_scale = a.sm_scale * kLog2e * (ESZ == 1 ? a.k_scale[g] : 1.0f);
+  const float v_scale = ESZ == 1 ? a.v_scale[g] : 1.0f;
 
   float m_ref[2] = {kNegBig, kNegBig}, l_run[2] = {0.0f, 0.0f};
   f32x4_t acc[2][NC];
@@ -161,17 +174,17 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
   // Each lane's LDS chunk o = 64 jj + lane of DMA jj (of K or V): chunk o % STRIDE of tile row o / STRIDE (the pad
   // chunk repeats the row's last chunk; lanes past the tile only occur in the last DMA, which switches them off).
   const uint32_t ring = lds_address((lds_void*)(lds_u8*)&sm_ring[0]);
-  const int64_t head_stride = (int64_t)a.P * D;  // bytes between KV heads of one page
+  const int64_t head_stride = (int64_t)a.P * ROWB;  // bytes between KV heads of one page
 
   int32_t p0 = 0;  // first page index staged in sm_pages
   auto page_of = [&](int32_t key) -> int32_t { return sm_pages[key / a.P - p0]; };  // -1: invalid
   // This wave's DMAs of a tile: the m-th is DMA j = wave + 4 m of the tile (K for j < NDMA, then V), whose 64 lanes
   // fill LDS chunks 64 jj .. 64 jj + 63 of the K or V rows. Its rows span at most two 16-key groups (glo and glo + 1;
   // a group lies in one page): per lane, the byte offset inside the group and whether the lane's row is in glo + 1.
-  static_assert(Geo::TAIL == 64, "every lane of every DMA lands inside the tile");
+  // (lanes past the tile, only in a tile's last DMA when TAIL < 64, are switched off: bit 30 of dma_pk)
   constexpr int MW = Geo::CNT_HI;
   const int cnt = (wave < NI % 4 || NI % 4 == 0) ? Geo::CNT_HI : Geo::CNT_LO;
-  uint32_t dma_pk[MW];   // offset in the group | (lane's row in group glo + 1) << 31
+  uint32_t dma_pk[MW];   // offset in the group | (lane off) << 30 | (lane's row in group glo + 1) << 31
   int32_t dma_glo[MW];   // uniform
   uint32_t dma_lds[MW];  // uniform LDS offset in the slot
 #pragma unroll
@@ -182,7 +195,8 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
     const int row = o / STRIDE, c = min(o % STRIDE, CH - 1);
     const int glo = (64 * jj / STRIDE) >> 4;
     dma_glo[m] = glo;
-    dma_pk[m] = (uint32_t)((row & 15) * D + 16 * c) | ((uint32_t)((row >> 4) > glo) << 31);
+    const bool off = jj == NDMA - 1 && lane >= Geo::TAIL;
+    dma_pk[m] = (uint32_t)((row & 15) * ROWB + 16 * c) | ((uint32_t)off << 30) | ((uint32_t)((row >> 4) > glo) << 31);
     dma_lds[m] = (j < NDMA ? 0 : HALF) + 1024 * jj;
   }
   const int64_t cache_bytes = a.num_blocks * a.G * head_stride;
@@ -195,7 +209,8 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
     int64_t base[TK / 16 + 1];  // byte offset of each 16-key group's first row (one page), and a spare
 #pragma unroll
     for (int u = 0; u < TK / 16; ++u)
-      base[u] = ((int64_t)max(page_of(k0 + 16 * u), 0) * a.G + g) * head_stride + (int64_t)((k0 + 16 * u) % a.P) * D;
+      base[u] =
+          ((int64_t)max(page_of(k0 + 16 * u), 0) * a.G + g) * head_stride + (int64_t)((k0 + 16 * u) % a.P) * ROWB;
     base[TK / 16] = base[TK / 16 - 1];
 #pragma unroll
     for (int m = 0; m < MW; ++m) {
@@ -206,11 +221,12 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
       for (int u = 1; u < TK / 16; ++u)
         if (dma_glo[m] == u) blo = base[u], bhi = base[u + 1];
       const uint32_t lds = ring + slot * SLOT + dma_lds[m];
+      if (Geo::TAIL < 64 && (dma_pk[m] >> 30 & 1u)) continue;
       if constexpr (BUF) {
-        const uint32_t voff = (uint32_t)((dma_pk[m] >> 31) ? bhi : blo) + (dma_pk[m] & 0x7fffffffu);  // < 4 GiB
+        const uint32_t voff = (uint32_t)((dma_pk[m] >> 31) ? bhi : blo) + (dma_pk[m] & 0x3fffffffu);  // < 4 GiB
         dma_buffer16(j < NDMA ? k_rsrc : v_rsrc, lds, voff);
       } else {
-        const int64_t off = ((dma_pk[m] >> 31) ? bhi : blo) + (int64_t)(dma_pk[m] & 0x7fffffffu);
+        const int64_t off = ((dma_pk[m] >> 31) ? bhi : blo) + (int64_t)(dma_pk[m] & 0x3fffffffu);
         dma_global16((j < NDMA ? a.k_cache : a.v_cache) + off, lds);
       }
     }
@@ -237,6 +253,18 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
     for (int u = 0; u < NSUB; ++u) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
+        if constexpr (ESZ == 2) {
+          // bf16 K: elements 32 s + 8 g4 .. + 7 of the lane's key, one 16-byte LDS read per step
+          const uint8_t* kr = K + (32 * u + 8 * (li >> 2) + 4 * h + (li & 3)) * RS + 16 * g4;
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            const uint4 w = *reinterpret_cast<const uint4*>(kr + 64 * s);
+            const uint32_t kop[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int n = 0; n < 2; ++n) st[u][h][n] = mfma_16x16x32_bf16(kop, qf[n][s], st[u][h][n]);
+          }
+          continue;
+        }
         // the K bytes of the lane's key, dims 32 g4 .. + 31, straight from LDS (e4m3fn, no conversion)
         uint32_t kop[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         if (32 * g4 < D) {
@@ -348,10 +376,24 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
         vm0 = nvalid >= 4 ? 0xffffffffu : (1u << (8 * nvalid)) - 1u;
         vm1 = nvalid >= 8 ? 0xffffffffu : nvalid <= 4 ? 0u : (1u << (8 * (nvalid - 4))) - 1u;
       }
-      const uint2 vw = lds_read_tr8(V + (32 * u + 8 * g4 + (li >> 1)) * RS + 8 * (li & 1) + 16 * c);
       uint32_t o[4];
-      fp8x4_to_bf16x4(vw.x & vm0, o[0], o[1]);
-      fp8x4_to_bf16x4(vw.y & vm1, o[2], o[3]);
+      if constexpr (ESZ == 2) {
+        // bf16 V: the 8 keys' elements at dim 16 c + i, one 2-byte LDS read each (the byte masks select whole values)
+        const uint8_t* vr = V + (32 * u + 8 * g4) * RS + 2 * (16 * c + li);
+        uint32_t e[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) e[k] = *reinterpret_cast<const uint16_t*>(vr + k * RS);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[k] = e[2 * k] | (e[2 * k + 1] << 16);
+        o[0] &= (vm0 & 0xffu ? 0xffffu : 0u) | (vm0 & 0xff00u ? 0xffff0000u : 0u);
+        o[1] &= (vm0 & 0xff0000u ? 0xffffu : 0u) | (vm0 & 0xff000000u ? 0xffff0000u : 0u);
+        o[2] &= (vm1 & 0xffu ? 0xffffu : 0u) | (vm1 & 0xff00u ? 0xffff0000u : 0u);
+        o[3] &= (vm1 & 0xff0000u ? 0xffffu : 0u) | (vm1 & 0xff000000u ? 0xffff0000u : 0u);
+      } else {
+        const uint2 vw = lds_read_tr8(V + (32 * u + 8 * g4 + (li >> 1)) * RS + 8 * (li & 1) + 16 * c);
+        fp8x4_to_bf16x4(vw.x & vm0, o[0], o[1]);
+        fp8x4_to_bf16x4(vw.y & vm1, o[2], o[3]);
+      }
       *reinterpret_cast<uint4*>(&sm_vt[(16 * c + li) * Geo::VT_RS + (32 * u + 8 * g4) * 2]) = make_uint4(o[0], o[1], o[2],
                                                                                                        o[3]);
     }
@@ -427,10 +469,11 @@ extern "C" int sna_prefill_attention(const void* q, const void* k_cache, const v
     return fail(SNA_ERR_UNSUPPORTED, "prefill_attention: head_dim %d (64 or 128)", head_dim);
   if (page_size < 16 || page_size % 16 != 0)
     return fail(SNA_ERR_UNSUPPORTED, "prefill_attention: page_size %d (a multiple of 16)", page_size);
-  if (kv_dtype != SNA_DTYPE_FP8_E4M3FN)
-    return fail(SNA_ERR_UNSUPPORTED, "prefill_attention: the KV pool must be FP8 e4m3fn (dtype %d)", kv_dtype);
+  if (kv_dtype != SNA_DTYPE_FP8_E4M3FN && kv_dtype != SNA_DTYPE_BF16)
+    return fail(SNA_ERR_UNSUPPORTED, "prefill_attention: KV dtype %d (FP8 e4m3fn or bf16)", kv_dtype);
   if (R == 0 || max_q_len == 0) return SNA_OK;
-  if (!q || !k_cache || !v_cache || !k_scale || !v_scale || !block_table || !q_start || !prior_lens || !out)
+  if (!q || !k_cache || !v_cache || (kv_dtype == SNA_DTYPE_FP8_E4M3FN && (!k_scale || !v_scale)) || !block_table ||
+      !q_start || !prior_lens || !out)
     return fail(SNA_ERR_INVALID_ARGUMENT, "prefill_attention: null pointer");
   if (!aligned(q, 16) || !aligned(out, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
     return fail(SNA_ERR_INVALID_ARGUMENT, "prefill_attention: q, out and the caches must be 16-byte aligned");
@@ -462,15 +505,25 @@ extern "C" int sna_prefill_attention(const void* q, const void* k_cache, const v
   const dim3 grid((unsigned)((max_q_len + a.bq - 1) / a.bq), (unsigned)R, (unsigned)num_kv_heads);
   hipEvent_t t0, t1;
   timing_events(0, &t0, &t1);
-  const bool buf = num_blocks * num_kv_heads * (int64_t)page_size * head_dim < ((int64_t)1 << 32);
-  if (head_dim == 128 && buf)
-    hipExtLaunchKernelGGL((prefill_gqa_kernel<128, true>), grid, dim3(256), 0, (hipStream_t)stream, t0, t1, 0, a);
-  else if (head_dim == 128)
-    hipExtLaunchKernelGGL((prefill_gqa_kernel<128, false>), grid, dim3(256), 0, (hipStream_t)stream, t0, t1, 0, a);
-  else if (buf)
-    hipExtLaunchKernelGGL((prefill_gqa_kernel<64, true>), grid, dim3(256), 0, (hipStream_t)stream, t0, t1, 0, a);
-  else
-    hipExtLaunchKernelGGL((prefill_gqa_kernel<64, false>), grid, dim3(256), 0, (hipStream_t)stream, t0, t1, 0, a);
+  const int esz = kv_dtype == SNA_DTYPE_BF16 ? 2 : 1;
+  const bool buf = num_blocks * num_kv_heads * (int64_t)page_size * head_dim * esz < ((int64_t)1 << 32);
+  const hipStream_t s = (hipStream_t)stream;
+#define SNA_PREFILL_LAUNCH(D_, BUF_, ESZ_) \
+  hipExtLaunchKernelGGL((prefill_gqa_kernel<D_, BUF_, ESZ_>), grid, dim3(256), 0, s, t0, t1, 0, a)
+  if (esz == 1) {
+    if (head_dim == 128) {
+      if (buf) SNA_PREFILL_LAUNCH(128, true, 1); else SNA_PREFILL_LAUNCH(128, false, 1);
+    } else {
+      if (buf) SNA_PREFILL_LAUNCH(64, true, 1); else SNA_PREFILL_LAUNCH(64, false, 1);
+    }
+  } else {
+    if (head_dim == 128) {
+      if (buf) SNA_PREFILL_LAUNCH(128, true, 2); else SNA_PREFILL_LAUNCH(128, false, 2);
+    } else {
+      if (buf) SNA_PREFILL_LAUNCH(64, true, 2); else SNA_PREFILL_LAUNCH(64, false, 2);
+    }
+  }
+#undef SNA_PREFILL_LAUNCH
   timing_end_call();
   return check_launch("prefill_attention");
 }

@@ -395,11 +395,13 @@ def lse_combine(o_parts: Tensor, lse_parts: Tensor) -> tuple[Tensor, Tensor]:
 # ------------------------------------------------------------------------------------------------------------------
 
 def prefill_attention(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: Tensor, q_start: Tensor,
-                      prior_lens: Tensor, *, max_q_len: int, sm_scale: float, k_scale: Tensor, v_scale: Tensor,
-                      sinks: Optional[Tensor] = None, window: int = 0, out: Optional[Tensor] = None) -> Tensor:
+                      prior_lens: Tensor, *, max_q_len: int, sm_scale: float, k_scale: Optional[Tensor] = None,
+                      v_scale: Optional[Tensor] = None, sinks: Optional[Tensor] = None, window: int = 0,
+                      out: Optional[Tensor] = None) -> Tensor:
     """Prefill attention of a batch of chunks: q [T, H, d] bf16 (request r's rows q_start[r] .. q_start[r + 1], at
-    positions prior_lens[r] + i), every key read from one layer's FP8 caches [blocks, G, page, d] through
-    ``block_table`` [R, width] (store the chunk's K/V first, with kv_store_mha). Causal, optionally windowed (keys
+    positions prior_lens[r] + i), every key read from one layer's caches [blocks, G, page, d] (FP8 with per-KV-head
+    scales k_scale / v_scale [G], or bf16) through ``block_table`` [R, width] (store the chunk's K/V first, with
+    kv_store_mha). Causal, optionally windowed (keys
     (p - window, p]) and with sinks [H]. ``max_q_len`` bounds the chunk lengths (a host int). Returns [T, H, d] bf16.
 
     Stands in for segmented_attention (ops/attention/attention_segmented_cte.py:21-75) over a batch."""
@@ -416,9 +418,13 @@ def prefill_attention(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: 
     qs = _contig(q_start, "q_start", torch.int32)
     pl = _contig(prior_lens, "prior_lens", torch.int32)
     table = _contig(block_table, "block_table", torch.int32) if block_table.dtype != torch.int32 else block_table
-    ks = _contig(k_scale.reshape(-1).float(), "k_scale")
-    vs = _contig(v_scale.reshape(-1).float(), "v_scale")
-    _need(ks.numel() == G and vs.numel() == G, f"k_scale and v_scale must have {G} entries")
+    code = cache_dtype_code(k_cache.dtype)
+    ks = vs = None
+    if code == _lib.DTYPE_FP8_E4M3FN:
+        _need(k_scale is not None and v_scale is not None, "an FP8 pool needs k_scale and v_scale")
+        ks = _contig(k_scale.reshape(-1).float(), "k_scale")
+        vs = _contig(v_scale.reshape(-1).float(), "v_scale")
+        _need(ks.numel() == G and vs.numel() == G, f"k_scale and v_scale must have {G} entries")
     sk = None if sinks is None else _contig(sinks.reshape(-1).float(), "sinks")
     if sk is not None:
         _need(sk.numel() == H, f"sinks must have {H} entries")
@@ -430,16 +436,17 @@ def prefill_attention(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: 
     rc = _lib.load().sna_prefill_attention(
         _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(ks), _ptr(vs), _ptr(table), table.stride(0), table.shape[1],
         _ptr(qs), _ptr(pl), R, int(max_q_len), _ptr(sk), float(sm_scale), int(window), _ptr(out), H, G, d, P, nb,
-        cache_dtype_code(k_cache.dtype), _stream(dev))
+        code, _stream(dev))
     _lib.check(rc, "prefill_attention")
     return out
 
 
 def segmented_attention(q: Tensor, *, k_cache: Tensor, v_cache: Tensor, block_tables: Tensor, prior_tokens,
                         block_size: int, kv_segment_size: int, scale: float, sliding_window: Optional[int],
-                        sink: Optional[Tensor], k_scale: Tensor, v_scale: Tensor) -> Tensor:
+                        sink: Optional[Tensor], k_scale: Optional[Tensor] = None,
+                        v_scale: Optional[Tensor] = None) -> Tensor:
     """The reference's signature (ops/attention/attention_segmented_cte.py:21-47) for one request: q [heads, S, d],
-    caches [pages, kv_heads, page, d] (FP8, unpacked K), block_tables [1, blocks], prior_tokens (an int or a 1-element
+    caches [pages, kv_heads, page, d] (FP8, unpacked K, or bf16), block_tables [1, blocks], prior_tokens (an int or a 1-element
     tensor), sink [heads, 1] or None; returns [heads, S, d]. The per-KV-head scales k_scale / v_scale are this pool's
     (the reference folds its per-tensor scale into ``scale``); ``kv_segment_size`` is the Trainium kernel's tiling and
     has no role here."""

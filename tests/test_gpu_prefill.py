@@ -1,4 +1,4 @@
-"""Segmented prefill attention over the FP8 pool (ops.prefill_attention, the reference's segmented_attention) against
+"""Segmented prefill attention over the FP8 or bf16 pool (ops.prefill_attention, the reference's segmented_attention) against
 the CPU oracle (oracle/attention.segmented_prefill) on the same pool bytes: within the attention bar."""
 
 from __future__ import annotations
@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def _case(seed, H, G, d, P, priors, lens, spare_pages=5):
+def _case(seed, H, G, d, P, priors, lens, spare_pages=5, bf16=False):
     """A pool holding every request's prior and chunk (stored by ops.kv_store_mha with per-head absmax scales), its
     table, the chunk queries and their row offsets."""
     g = torch.Generator().manual_seed(seed)
@@ -37,9 +37,13 @@ def _case(seed, H, G, d, P, priors, lens, spare_pages=5):
     vs = (v_all.float().abs().amax(dim=(0, 2)) / 448.0).clamp(min=1e-6)
     slots = torch.cat([table[r, torch.arange(x) // P].to(torch.int64) * P + torch.arange(x) % P
                        for r, x in enumerate(spans)])
-    kc = torch.zeros(nb, G, P, d, dtype=torch.float8_e4m3fn, device=DEV)
+    kc = torch.zeros(nb, G, P, d, dtype=torch.bfloat16 if bf16 else torch.float8_e4m3fn, device=DEV)
     vc = torch.zeros_like(kc)
-    ops.kv_store_mha(k_all.to(DEV), v_all.to(DEV), slots.to(DEV), kc, vc, ks.to(DEV), vs.to(DEV))
+    if bf16:
+        ks = vs = None
+        ops.kv_store_mha(k_all.to(DEV), v_all.to(DEV), slots.to(DEV), kc, vc)
+    else:
+        ops.kv_store_mha(k_all.to(DEV), v_all.to(DEV), slots.to(DEV), kc, vc, ks.to(DEV), vs.to(DEV))
     T = sum(lens)
     q = torch.randn(T, H, d, generator=g).to(torch.bfloat16)
     q_start = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32)
@@ -54,6 +58,9 @@ CASES = [
     ("window-1000-page32", 5, dict(H=16, G=4, d=128, P=32, priors=(5000,), lens=(300,)), 1000, False),
     ("mha-d128", 6, dict(H=4, G=4, d=128, P=16, priors=(17, 250), lens=(140, 3)), 0, False),
     ("empty-request", 7, dict(H=8, G=2, d=64, P=16, priors=(40, 9, 0), lens=(20, 0, 33)), 0, False),
+    ("bf16-qwen3-0.6b", 8, dict(H=16, G=8, d=128, P=16, priors=(0, 300, 77), lens=(128, 45, 200), bf16=True), 0, False),
+    ("bf16-swa-sinks-d64", 10, dict(H=8, G=2, d=64, P=32, priors=(500, 3), lens=(70, 130), bf16=True), 96, True),
+    ("bf16-long-prior", 11, dict(H=4, G=1, d=128, P=16, priors=(34000,), lens=(20,), bf16=True), 0, False),
 ]
 
 
@@ -64,12 +71,15 @@ def test_prefill_attention_matches_oracle(name, seed, cfg, window, sinks):
     H, d = cfg["H"], cfg["d"]
     sk = torch.randn(H, generator=torch.Generator().manual_seed(seed + 50)) if sinks else None
     scale = d ** -0.5
+    bf16 = cfg.get("bf16", False)
     out = ops.prefill_attention(q.to(DEV), kc, vc, table.to(DEV), q_start.to(DEV), priors.to(DEV),
-                                max_q_len=max(cfg["lens"]) + 7, sm_scale=scale, k_scale=ks.to(DEV), v_scale=vs.to(DEV),
+                                max_q_len=max(cfg["lens"]) + 7, sm_scale=scale,
+                                k_scale=None if bf16 else ks.to(DEV), v_scale=None if bf16 else vs.to(DEV),
                                 sinks=None if sk is None else sk.to(DEV), window=window)
     torch.cuda.synchronize()
-    want = oatt.segmented_prefill(q, kc.cpu().view(torch.uint8), vc.cpu().view(torch.uint8), table, q_start, priors,
-                                  sm_scale=scale, k_scale=ks, v_scale=vs, sinks=sk, window=window)
+    kh, vh = (kc.cpu(), vc.cpu()) if bf16 else (kc.cpu().view(torch.uint8), vc.cpu().view(torch.uint8))
+    want = oatt.segmented_prefill(q, kh, vh, table, q_start, priors, sm_scale=scale, k_scale=ks, v_scale=vs, sinks=sk,
+                                  window=window)
     assert_close_attn(out.cpu(), want, name)
 
 
@@ -89,15 +99,15 @@ def test_segmented_attention_reference_signature():
     assert_close_attn(out.transpose(0, 1).cpu(), want, "segmented_attention")
 
 
-def test_prefill_rejects_a_bf16_pool_and_bad_pages():
+def test_prefill_rejects_bad_pages_and_missing_scales():
     q = torch.zeros(4, 8, 64, dtype=torch.bfloat16, device=DEV)
-    kc = torch.zeros(3, 2, 16, 64, dtype=torch.bfloat16, device=DEV)
+    kc = torch.zeros(3, 2, 16, 64, dtype=torch.float8_e4m3fn, device=DEV)
     args = (q, kc, kc, torch.zeros(1, 2, dtype=torch.int32, device=DEV), torch.tensor([0, 4], dtype=torch.int32,
                                                                                       device=DEV),
             torch.tensor([0], dtype=torch.int32, device=DEV))
     one = torch.ones(2, device=DEV)
     with pytest.raises(ValueError):
-        ops.prefill_attention(*args, max_q_len=4, sm_scale=1.0, k_scale=one, v_scale=one)
+        ops.prefill_attention(*args, max_q_len=4, sm_scale=1.0)  # an FP8 pool without its scales
     kc8 = torch.zeros(3, 2, 8, 64, dtype=torch.float8_e4m3fn, device=DEV)
     with pytest.raises(ValueError):
         ops.prefill_attention(q, kc8, kc8, *args[3:], max_q_len=4, sm_scale=1.0, k_scale=one, v_scale=one)

@@ -234,9 +234,9 @@ int sna_lse_combine(const float *o_parts, const float *lse_parts, int32_t n_part
  * itself, every key read from the pool (store the chunk's K/V first, e.g. with sna_kv_store_mha).
  *   q            [T, num_q_heads, head_dim] bf16, contiguous, 16-byte aligned; request r owns rows
  *                q_start[r] .. q_start[r + 1] - 1, its query i at position prior_lens[r] + i.
- *   k_cache, v_cache  one layer's FP8 e4m3fn pool [num_blocks, num_kv_heads, page_size, head_dim] with per-KV-head
- *                dequantization scales k_scale / v_scale [num_kv_heads] (kv_dtype SNA_DTYPE_FP8_E4M3FN; bf16 pools
- *                return SNA_ERR_UNSUPPORTED).
+ *   k_cache, v_cache  one layer's pool [num_blocks, num_kv_heads, page_size, head_dim]: FP8 e4m3fn
+ *                (kv_dtype SNA_DTYPE_FP8_E4M3FN) with per-KV-head dequantization scales k_scale / v_scale
+ *                [num_kv_heads], or bf16 (SNA_DTYPE_BF16; the scales are not read and may be NULL).
  *   block_table  [R, table_width] int32 (row stride table_stride), -1 past a row's pages; keys on a -1 page are not
  *                attended.
  *   q_start      [R + 1] int32, prior_lens [R] int32 (device); max_q_len >= every request's chunk length.

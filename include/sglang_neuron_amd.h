@@ -255,6 +255,38 @@ int sna_prefill_attention(const void *q, const void *k_cache, const void *v_cach
                           int32_t kv_dtype, void *stream);
 
 /* =====================================================================================================
+ * DSA indexer (the step that picks the sparse decode's positions)
+ * ===================================================================================================== */
+
+/* Store index-key rows keys [n_tokens, head_dim] bf16 (16-byte aligned) into an index-key cache [n_slots, head_dim]
+ * of e4m3fn bytes as e4m3fn(clamp(key, +-448)) (no scale); slots < 0 or >= n_slots are skipped.
+ * Replaces: pack_indexer_keys_fp8 and the cache append of indexer_kv_score_torch_ref
+ * (models/glm52/kernels/decode/attention/indexer/indexer_torch.py:44-53, :228-234). */
+int sna_index_key_store(const void *keys, const int64_t *slots, int64_t n_tokens, int32_t head_dim, uint8_t *cache,
+                        int64_t n_slots, void *stream);
+
+/* Index scores of every cached key: out[b, e] (bf16, row stride out_stride, e < width) =
+ *   bf16(min(sum_h w[b, h] * relu(q[b, h, :] . key_e * head_dim^-0.5), live ? 1e30 : -1e30)),
+ * key e of row b read at page block_table[b, e / page_size], offset e % page_size of keys [num_blocks, page_size,
+ * head_dim] (e4m3fn bytes); live: e < limits[b] (positions before the query's own) and the page valid.
+ *   q [B, num_heads, 128] bf16 (the rotated index queries, 16-byte aligned), w [B, num_heads] fp32 (the head weights,
+ *   already scaled by num_heads^-0.5); num_heads 16, 32, 64 or 128; head_dim 128.
+ * Replaces: the score of indexer_kv_score_torch_ref (indexer_torch.py:254-268), after the model's projections. */
+int sna_indexer_scores(const void *q, const float *w, const uint8_t *keys, const int32_t *block_table,
+                       int64_t table_stride, int32_t table_width, const int32_t *limits, int32_t B, int32_t num_heads,
+                       int32_t head_dim, int32_t page_size, int64_t num_blocks, int32_t width, void *out,
+                       int64_t out_stride, void *stream);
+
+/* The k largest of each row of bf16 scores [B, width] (row stride score_stride): out[b, 0 .. k) int32 (row stride
+ * out_stride) = their positions e, those above the k-th largest value first, then its ties (the lowest positions),
+ * each group in position order; a selected score <= -1e30 / 2 (a dead key) is written as -1. Exact: the selected
+ * values are the k largest.
+ * Replaces: indexer_topk_local_torch_ref's selection (indexer_torch.py:296-309); its slot order is a Trainium
+ * layout, the set is the same. */
+int sna_topk_positions(const void *scores, int64_t score_stride, int32_t B, int32_t width, int32_t k, int32_t *out,
+                       int64_t out_stride, void *stream);
+
+/* =====================================================================================================
  * Decode metadata on the device
  * ===================================================================================================== */
 
@@ -287,7 +319,8 @@ int sna_window_table(const int32_t *table, int64_t table_stride, int32_t table_w
 /* Per-kernel timing of the decode entry points, for the benchmark's roofline figure. With timing on, each decode call
  * launches its split-K kernel and its combine kernel through hipExtLaunchKernel with a start/stop event pair, so the
  * kernels' own dispatch packets stamp the times and no marker packet runs between them (up to 4096 calls after the
- * switch); sna_block_table, sna_window_table and sna_prefill_attention time their one kernel as the split-K slot. sna_diag_kernel_timing_read
+ * switch); sna_block_table, sna_window_table, sna_prefill_attention, sna_indexer_scores and sna_topk_positions
+ * time their one kernel as the split-K slot. sna_diag_kernel_timing_read
  * waits for the events and returns the summed milliseconds of each kernel and the number of split-K-slot launches
  * timed. The events are the library's only state besides the error string. The timer
  * is not thread-safe and is off by default. */

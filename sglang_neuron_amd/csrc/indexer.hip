@@ -1,0 +1,323 @@
+// The DeepSeek-sparse-attention indexer's decode step on the GPU, after the model's projections: the fp8 index-key
+// store, the head-weighted ReLU score of every cached key, and the exact top-k selection of the positions the sparse
+// MLA decode then gathers.
+//   reference: models/glm52/kernels/decode/attention/indexer/indexer_torch.py (pack_indexer_keys_fp8 :44-53, the
+//   score of indexer_kv_score_torch_ref :254-268, indexer_topk_local_torch_ref :296-309)
+//
+// Score: one workgroup of 4 waves per (row, 256 keys); each wave takes 16-key tiles. S[head, key] = Q . K^T on
+// v_mfma_scale_f32_16x16x128_f8f6f4 (one instruction covers d = 128): lane (g4, i) feeds row i of the head tile (the
+// query split exactly into two e4m3fn parts, hi + lo / 16, of a power-of-two-scaled row, whose E8M0 A scales undo
+// the scaling) and column i, the 32 key bytes 32 g4 .. + 31 of key i, loaded straight from HBM into registers. The
+// result hands lane (g4, i) heads 4 g4 + r of key i: the head-weighted ReLU sum is 16 terms in the lane, then a sum
+// over the four lane groups. Bytes per key: 128 (the fp8 row) + 2 (the bf16 score written).
+//
+// Top-k: one workgroup per row. The bf16 scores map to order-preserving 16-bit keys; two 256-bin histograms (high
+// byte, then the low byte inside the threshold bin) find the k-th largest key T; a third pass writes every position
+// above T and the first (k - count above) positions equal to T, in position order (block-wide scans). Deterministic.
+
+#include "sna_device.h"
+#include "sna_host.h"
+
+namespace sna {
+
+constexpr float kIndexMaskBound = 1.0e30f;
+
+struct IndexerArgs {
+  const uint16_t* q;     // [B, H, 128] bf16, rotated
+  const float* w;        // [B, H] fp32 head weights (already scaled)
+  const uint8_t* keys;   // [num_blocks, P, 128] e4m3fn
+  const int32_t* table;  // [B, table_width] (row stride table_stride)
+  int64_t table_stride;
+  int32_t table_width;
+  const int32_t* limits;  // [B] keys e < limits[b] are resident
+  uint16_t* out;          // [B, width] bf16 (row stride out_stride)
+  int64_t out_stride;
+  int32_t B, H, width, P;
+  int64_t num_blocks;
+  float scale;  // d^-0.5
+};
+
+__device__ __forceinline__ f32x4_t mfma_16x16x128_fp8_sa(const uint32_t (&a)[8], const uint32_t (&b)[8], f32x4_t c,
+                                                        int32_t scale_a) {
+  i32x8_t av, bv;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) av[i] = (int32_t)a[i], bv[i] = (int32_t)b[i];
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 0, 0, 0, scale_a, 0, 127);
+}
+
+template <int HT>  // head tiles of 16
+__global__ __launch_bounds__(256) void indexer_score_kernel(IndexerArgs a) {
+  constexpr int D = 128;
+  const int tid = threadIdx.x, lane = tid & 63, g4 = lane >> 4, li = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int32_t b = blockIdx.y;
+  const int32_t e_blk = (int32_t)blockIdx.x * 256;
+  if (e_blk >= a.width) return;
+  const int32_t limit = a.limits[b];
+
+  // The query operand of head tile ht: lane (g4, i) supplies head 16 ht + i, dims 32 g4 .. + 31, as two exact
+  // e4m3fn parts of the row scaled by sc = 2^(7 - floor(log2 amax)) (amax over the head's 128 dims); the E8M0 A
+  // scales are 127 - log2 sc for hi and 4 less for lo.
+  uint32_t qhi[HT][8], qlo[HT][8];
+  int32_t sc_hi[HT], sc_lo[HT];
+  float wl[HT][4];  // weights of heads 16 ht + 4 g4 + r (the rows this lane's results hold)
+#pragma unroll
+  for (int ht = 0; ht < HT; ++ht) {
+    const int32_t h = 16 * ht + li;
+    const uint16_t* qp = a.q + ((int64_t)b * a.H + h) * D + 32 * g4;
+    float v[32];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint4 x = ld16(qp + 8 * c);
+      const uint32_t xx[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[8 * c + 2 * e] = bf16_bits_to_f32(xx[e] & 0xffffu);
+        v[8 * c + 2 * e + 1] = bf16_bits_to_f32(xx[e] >> 16);
+      }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(v[e]));
+    amax = max_across_groups(amax);
+    const int32_t ex = amax > 0.0f ? max((int32_t)((__float_as_uint(amax) >> 23) & 0xff) - 127, -116) : -7;
+    const float sc = __uint_as_float((uint32_t)(127 + 7 - ex) << 23);
+    sc_hi[ht] = 127 + ex - 7;
+    sc_lo[ht] = 127 + ex - 7 - 4;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      float h4[4], l4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) split_q(v[4 * k + e] * sc, h4[e], l4[e]);
+      qhi[ht][k] = pack_e4m3fn_x4(h4[0], h4[1], h4[2], h4[3]);
+      qlo[ht][k] = pack_e4m3fn_x4(l4[0], l4[1], l4[2], l4[3]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wl[ht][r] = a.w[(int64_t)b * a.H + 16 * ht + 4 * g4 + r];
+  }
+
+  const int32_t* trow = a.table + (int64_t)b * a.table_stride;
+#pragma unroll 1
+  for (int kt = 0; kt < 4; ++kt) {
+    const int32_t e = e_blk + 64 * wave + 16 * kt + li;  // this lane's key
+    if (e_blk + 64 * wave + 16 * kt >= a.width) break;   // (uniform)
+    const int32_t col = e / a.P;
+    int32_t page = (e < a.width && col < a.table_width) ? trow[col] : -1;
+    const bool live = e < limit && page >= 0 && (int64_t)page < a.num_blocks;
+    uint32_t kb[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (live) {
+      const uint8_t* kp = a.keys + ((int64_t)page * a.P + e % a.P) * D + 32 * g4;
+      const uint4 x0 = ld16_stream(kp), x1 = ld16_stream(kp + 16);
+      kb[0] = x0.x, kb[1] = x0.y, kb[2] = x0.z, kb[3] = x0.w, kb[4] = x1.x, kb[5] = x1.y, kb[6] = x1.z, kb[7] = x1.w;
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) {
+      f32x4_t s = {0.f, 0.f, 0.f, 0.f};
+      s = mfma_16x16x128_fp8_sa(qhi[ht], kb, s, sc_hi[ht]);
+      s = mfma_16x16x128_fp8_sa(qlo[ht], kb, s, sc_lo[ht]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sum = fmaf(wl[ht][r], fmaxf(s[r] * a.scale, 0.0f), sum);
+    }
+    sum = sum_across_groups(sum);
+    if (g4 == 0 && e < a.width) {
+      const float v = fminf(sum, live ? kIndexMaskBound : -kIndexMaskBound);
+      a.out[(int64_t)b * a.out_stride + e] = (uint16_t)f32_to_bf16_bits(v);
+    }
+  }
+}
+
+// bf16 bits -> a 16-bit key whose unsigned order is the value order (NaN aside).
+__device__ __forceinline__ uint32_t order_key(uint32_t bits) { return (bits & 0x8000u) ? (~bits & 0xffffu) : (bits | 0x8000u); }
+
+// Top-k of one row per workgroup of 1024 threads: out[b, 0 .. k) = the positions of the k largest scores, those
+// above the threshold first, then the threshold's ties, each group in position order; a dead key (<= -1e30 / 2)
+// selected anyway is written as -1.
+__global__ __launch_bounds__(1024) void topk_kernel(const uint16_t* __restrict__ scores, int64_t score_stride,
+                                                    int32_t width, int32_t k, int32_t* __restrict__ out,
+                                                    int64_t out_stride) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t scan[2][1024];
+  __shared__ uint32_t sel[4];  // [threshold key, count above it, ties needed]
+  const int tid = threadIdx.x;
+  const int32_t b = blockIdx.x;
+  const uint16_t* row = scores + (int64_t)b * score_stride;
+  int32_t* orow = out + (int64_t)b * out_stride;
+  const int32_t per = (width + 1023) / 1024;
+  const int32_t e0 = min(tid * per, width), e1 = min(e0 + per, width);
+
+  // pass 1: histogram of the key's high byte; the bin holding the k-th largest
+  if (tid < 256) hist[tid] = 0;
+  __syncthreads();
+  for (int32_t e = tid; e < width; e += 1024) atomicAdd(&hist[order_key(row[e]) >> 8], 1u);
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t above = 0;
+    int bin = 255;
+    for (; bin > 0; --bin) {
+      if (above + hist[bin] >= (uint32_t)k) break;
+      above += hist[bin];
+    }
+    sel[0] = (uint32_t)bin;
+    sel[1] = above;
+  }
+  __syncthreads();
+  const uint32_t hi_bin = sel[0], above1 = sel[1];
+  // pass 2: histogram of the low byte inside that bin; the threshold key T
+  if (tid < 256) hist[tid] = 0;
+  __syncthreads();
+  for (int32_t e = tid; e < width; e += 1024) {
+    const uint32_t kk = order_key(row[e]);
+    if ((kk >> 8) == hi_bin) atomicAdd(&hist[kk & 0xffu], 1u);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t above = above1;
+    int bin = 255;
+    for (; bin > 0; --bin) {
+      if (above + hist[bin] >= (uint32_t)k) break;
+      above += hist[bin];
+    }
+    sel[0] = (hi_bin << 8) | (uint32_t)bin;
+    sel[1] = above;
+    sel[2] = (uint32_t)k - above;
+  }
+  __syncthreads();
+  const uint32_t T = sel[0], n_above = sel[1], n_ties = sel[2];
+  // pass 3: this thread's run [e0, e1): counts, block-wide exclusive scans, then the writes in position order
+  uint32_t c_gt = 0, c_eq = 0;
+  for (int32_t e = e0; e < e1; ++e) {
+    const uint32_t kk = order_key(row[e]);
+    c_gt += kk > T;
+    c_eq += kk == T;
+  }
+  scan[0][tid] = c_gt;
+  scan[1][tid] = c_eq;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {  // Hillis-Steele inclusive scan of both counts
+    const uint32_t x0 = tid >= off ? scan[0][tid - off] : 0u, x1 = tid >= off ? scan[1][tid - off] : 0u;
+    __syncthreads();
+    scan[0][tid] += x0;
+    scan[1][tid] += x1;
+    __syncthreads();
+  }
+  uint32_t o_gt = scan[0][tid] - c_gt, o_eq = scan[1][tid] - c_eq;
+  for (int32_t e = e0; e < e1; ++e) {
+    const uint32_t bits = row[e], kk = order_key(bits);
+    const int32_t label = bf16_bits_to_f32(bits) > -0.5f * kIndexMaskBound ? e : -1;  // a dead key: -1
+    if (kk > T) {
+      orow[o_gt++] = label;
+    } else if (kk == T) {
+      if (o_eq < n_ties) orow[n_above + o_eq] = label;
+      ++o_eq;
+    }
+  }
+}
+
+// e4m3fn(clamp(key, +-448)) rows into an index-key cache; one thread per 8 elements, out-of-cache slots skipped.
+__global__ __launch_bounds__(256) void index_key_store_kernel(const uint16_t* __restrict__ keys, const int64_t* slots,
+                                                              int64_t n, int32_t d, uint8_t* cache, int64_t n_slots) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int32_t per_row = d / 8;
+  if (i >= n * per_row) return;
+  const int64_t t = i / per_row;
+  const int32_t c = (int32_t)(i % per_row);
+  const int64_t s = slots[t];
+  if (s < 0 || s >= n_slots) return;
+  const uint4 x = ld16(keys + t * d + 8 * c);
+  const uint32_t xx[4] = {x.x, x.y, x.z, x.w};
+  uint32_t o[2] = {0, 0};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j >> 2] |= quantize_e4m3fn((xx[j >> 1] >> (16 * (j & 1))) & 0xffffu, 1.0f) << (8 * (j & 3));
+  *reinterpret_cast<uint2*>(cache + s * d + 8 * c) = make_uint2(o[0], o[1]);
+}
+
+}  // namespace sna
+
+using namespace sna;
+
+extern "C" {
+
+int sna_indexer_scores(const void* q, const float* w, const uint8_t* keys, const int32_t* block_table,
+                       int64_t table_stride, int32_t table_width, const int32_t* limits, int32_t B, int32_t num_heads,
+                       int32_t head_dim, int32_t page_size, int64_t num_blocks, int32_t width, void* out,
+                       int64_t out_stride, void* stream) {
+  ApiGuard guard;
+  if (B < 0 || width < 0 || num_heads < 16 || num_heads % 16 != 0 || num_heads > 128 || page_size < 1 ||
+      num_blocks < 1 || table_width < 1 || table_stride < table_width || out_stride < width)
+    return fail(SNA_ERR_INVALID_ARGUMENT,
+                "indexer_scores: bad sizes (B %d, heads %d (a multiple of 16, at most 128), page %d, blocks %lld, "
+                "table %d wide, width %d, out stride %lld)",
+                B, num_heads, page_size, (long long)num_blocks, table_width, width, (long long)out_stride);
+  if (head_dim != 128) return fail(SNA_ERR_UNSUPPORTED, "indexer_scores: head_dim %d (128)", head_dim);
+  if (B == 0 || width == 0) return SNA_OK;
+  if (!q || !w || !keys || !block_table || !limits || !out)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "indexer_scores: null pointer");
+  if (!aligned(q, 16) || !aligned(keys, 16)) return fail(SNA_ERR_INVALID_ARGUMENT, "indexer_scores: q and keys 16-B aligned");
+  if (B > 65535) return fail(SNA_ERR_INVALID_ARGUMENT, "indexer_scores: %d rows exceed the grid", B);
+  IndexerArgs a;
+  a.q = (const uint16_t*)q;
+  a.w = w;
+  a.keys = keys;
+  a.table = block_table;
+  a.table_stride = table_stride;
+  a.table_width = table_width;
+  a.limits = limits;
+  a.out = (uint16_t*)out;
+  a.out_stride = out_stride;
+  a.B = B;
+  a.H = num_heads;
+  a.width = width;
+  a.P = page_size;
+  a.num_blocks = num_blocks;
+  a.scale = 1.0f / sqrtf((float)head_dim);
+  const dim3 grid((unsigned)((width + 255) / 256), (unsigned)B);
+  hipEvent_t t0, t1;
+  timing_events(0, &t0, &t1);
+  const hipStream_t s = (hipStream_t)stream;
+  switch (num_heads / 16) {
+    case 1: hipExtLaunchKernelGGL((indexer_score_kernel<1>), grid, dim3(256), 0, s, t0, t1, 0, a); break;
+    case 2: hipExtLaunchKernelGGL((indexer_score_kernel<2>), grid, dim3(256), 0, s, t0, t1, 0, a); break;
+    case 4: hipExtLaunchKernelGGL((indexer_score_kernel<4>), grid, dim3(256), 0, s, t0, t1, 0, a); break;
+    case 8: hipExtLaunchKernelGGL((indexer_score_kernel<8>), grid, dim3(256), 0, s, t0, t1, 0, a); break;
+    default:
+      timing_end_call();
+      return fail(SNA_ERR_UNSUPPORTED, "indexer_scores: %d heads (16, 32, 64 or 128)", num_heads);
+  }
+  timing_end_call();
+  return check_launch("indexer_scores");
+}
+
+int sna_topk_positions(const void* scores, int64_t score_stride, int32_t B, int32_t width, int32_t k, int32_t* out,
+                       int64_t out_stride, void* stream) {
+  ApiGuard guard;
+  if (B < 0 || width < 0 || k < 1 || k > width || score_stride < width || out_stride < k)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "topk_positions: bad sizes (B %d, width %d, k %d, strides %lld / %lld)", B,
+                width, k, (long long)score_stride, (long long)out_stride);
+  if (B == 0) return SNA_OK;
+  if (!scores || !out) return fail(SNA_ERR_INVALID_ARGUMENT, "topk_positions: null pointer");
+  hipEvent_t t0, t1;
+  timing_events(0, &t0, &t1);
+  hipExtLaunchKernelGGL(topk_kernel, dim3((unsigned)B), dim3(1024), 0, (hipStream_t)stream, t0, t1, 0,
+                        (const uint16_t*)scores, score_stride, width, k, out, out_stride);
+  timing_end_call();
+  return check_launch("topk_positions");
+}
+
+int sna_index_key_store(const void* keys, const int64_t* slots, int64_t n_tokens, int32_t head_dim, uint8_t* cache,
+                        int64_t n_slots, void* stream) {
+  ApiGuard guard;
+  if (n_tokens < 0 || head_dim < 8 || head_dim % 8 != 0 || n_slots < 0)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "index_key_store: bad sizes (tokens %lld, head_dim %d, slots %lld)",
+                (long long)n_tokens, head_dim, (long long)n_slots);
+  if (n_tokens == 0) return SNA_OK;
+  if (!keys || !slots || !cache) return fail(SNA_ERR_INVALID_ARGUMENT, "index_key_store: null pointer");
+  if (!aligned(keys, 16) || !aligned(cache, 8))
+    return fail(SNA_ERR_INVALID_ARGUMENT, "index_key_store: keys 16-B and cache 8-B aligned");
+  const int64_t n = n_tokens * (head_dim / 8);
+  hipLaunchKernelGGL(index_key_store_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)keys, slots, n_tokens, head_dim, cache, n_slots);
+  return check_launch("index_key_store");
+}
+
+}  // extern "C"

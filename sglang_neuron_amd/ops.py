@@ -464,6 +464,68 @@ def segmented_attention(q: Tensor, *, k_cache: Tensor, v_cache: Tensor, block_ta
 
 
 # ------------------------------------------------------------------------------------------------------------------
+# DSA indexer
+# ------------------------------------------------------------------------------------------------------------------
+
+def index_key_store(keys: Tensor, slots: Tensor, cache: Tensor) -> None:
+    """Write index-key rows keys [T, d] (bf16) at ``slots`` [T] (int64) of an index-key cache [blocks, page, d]
+    (uint8 or float8_e4m3fn) as e4m3fn(clamp(key, +-448)); out-of-cache slots are skipped
+    (indexer_torch.py:44-53, :228-234)."""
+    dev = _on_gpu(keys, slots, cache)
+    d = cache.shape[-1]
+    keys = _contig(keys.reshape(-1, d), "keys", torch.bfloat16)
+    slots = _contig(slots.reshape(-1), "slots", torch.int64)
+    _need(slots.numel() == keys.shape[0], "one slot per key row")
+    _need(cache.dtype in (torch.uint8, FP8) and cache.is_contiguous(), "the index-key cache is contiguous e4m3fn bytes")
+    rc = _lib.load().sna_index_key_store(_ptr(keys), _ptr(slots), keys.shape[0], d, _ptr(cache), cache.numel() // d,
+                                         _stream(dev))
+    _lib.check(rc, "index_key_store")
+
+
+def indexer_scores(q: Tensor, w: Tensor, keys: Tensor, block_table: Tensor, limits: Tensor, width: int, *,
+                   out: Optional[Tensor] = None) -> Tensor:
+    """[B, width] bf16 index scores of every cached key: sum over heads of w[b, h] * relu(q[b, h] . key * d^-0.5),
+    clamped to -1e30 for keys at or past ``limits[b]`` (the positions before the query's own) or on invalid pages.
+    q [B, H, 128] bf16 (rotated), w [B, H] fp32 (scaled by H^-0.5), keys [blocks, page, 128] e4m3fn bytes read through
+    ``block_table`` [B, W]. The score of indexer_kv_score_torch_ref (indexer_torch.py:254-268)."""
+    dev = _on_gpu(q, w, keys, block_table, limits, out)
+    B, H, d = q.shape
+    nb, P, dk = keys.shape
+    _need(dk == d, "q and the keys disagree on head_dim")
+    _need(w.shape == (B, H) and limits.shape == (B,), f"w must be [{B}, {H}] and limits [{B}]")
+    _need(block_table.dim() == 2 and block_table.shape[0] >= B and block_table.stride(1) == 1,
+          "block_table must be [B, W] with unit column stride")
+    q = _contig(q, "q", torch.bfloat16)
+    w = _contig(w.float(), "w")
+    lim = _contig(limits, "limits", torch.int32)
+    table = block_table if block_table.dtype == torch.int32 else _contig(block_table, "block_table", torch.int32)
+    _need(keys.dtype in (torch.uint8, FP8) and keys.is_contiguous(), "keys must be contiguous e4m3fn bytes")
+    if out is None:
+        out = torch.empty(B, width, dtype=torch.bfloat16, device=dev)
+    _need(out.shape[0] == B and out.shape[1] >= width and out.dtype == torch.bfloat16 and out.stride(1) == 1,
+          f"out must be [{B}, >= {width}] bf16")
+    rc = _lib.load().sna_indexer_scores(_ptr(q), _ptr(w), _ptr(keys), _ptr(table), table.stride(0), table.shape[1],
+                                        _ptr(lim), B, H, d, P, nb, int(width), _ptr(out), out.stride(0), _stream(dev))
+    _lib.check(rc, "indexer_scores")
+    return out
+
+
+def topk_positions(scores: Tensor, k: int) -> Tensor:
+    """[B, k] int32 positions of the k largest bf16 scores [B, N] per row: those above the k-th largest value, then
+    its ties (lowest positions), each in position order; -1 for a selected dead key (score <= -1e30 / 2). The
+    selection of indexer_topk_local_torch_ref (indexer_torch.py:296-309)."""
+    dev = _on_gpu(scores)
+    _need(scores.dim() == 2 and scores.dtype == torch.bfloat16 and scores.stride(1) == 1, "scores must be [B, N] bf16")
+    B, N = scores.shape
+    _need(1 <= k <= N, f"k {k} must be in [1, {N}]")
+    out = torch.empty(B, k, dtype=torch.int32, device=dev)
+    rc = _lib.load().sna_topk_positions(_ptr(scores), scores.stride(0), B, N, int(k), _ptr(out), out.stride(0),
+                                        _stream(dev))
+    _lib.check(rc, "topk_positions")
+    return out
+
+
+# ------------------------------------------------------------------------------------------------------------------
 # decode metadata on the device
 # ------------------------------------------------------------------------------------------------------------------
 

@@ -16,7 +16,7 @@ One JSON line on stdout:
                 workload, timed on this host's cores.
 
 Options: --config {1,2,3,4,4swa,5} picks another workload (the default line is cfg2); --config meta times the
-device-side decode metadata (block table, window trim) instead, --config prefill the segmented prefill attention; --all prints one line per decode workload; --gpus
+device-side decode metadata (block table, window trim) instead, --config prefill the segmented prefill attention, --config indexer the DSA indexer; --all prints one line per decode workload; --gpus
 above 1 is refused, because this build measures one GPU.
 """
 
@@ -355,6 +355,113 @@ def run_meta(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> di
     return line
 
 
+INDEXER_METRIC = "DSA indexer µs/step (scores of every cached key + top-k), FP8 index keys, 1 MI355X"
+
+
+def run_indexer(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> dict:
+    """The DSA indexer's decode step at cfg5's scale: 16 rows, each scoring 131072 cached fp8 index keys (page 64,
+    128 dims) with 64 index heads, then the top-2048 positions. The roofline figure is the score kernel's algorithmic
+    bytes (128 per key read + 2 per score written) over its time; it is HBM-bound."""
+    import ctypes
+
+    import torch
+
+    from sglang_neuron_amd import _lib, ops
+
+    B, N, H, P, k = 16, 131072, 64, 64, 2048
+    g = torch.Generator(device="cpu").manual_seed(1200)
+    pages = N // P
+    nb = B * pages + 1
+    copies = 2
+    caches, tables = [], []
+    for c in range(copies):
+        perm = (torch.randperm(nb - 1, generator=g) + 1).to(torch.int32)
+        tables.append(perm.reshape(B, pages).to(dev))
+        cache = torch.empty(nb * P, 128, dtype=torch.uint8, device=dev)
+        rows = torch.randn(nb * P, 128, generator=g).to(torch.bfloat16).to(dev)
+        ops.index_key_store(rows, torch.arange(nb * P, dtype=torch.int64, device=dev), cache)
+        caches.append(cache.reshape(nb, P, 128))
+        del rows
+    q = torch.randn(B, H, 128, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.rand(B, H, generator=g) * H ** -0.5).to(dev)
+    limits = torch.full((B,), N, dtype=torch.int32, device=dev)
+    scores = torch.empty(B, N, dtype=torch.bfloat16, device=dev)
+    log(f"indexer: B={B} keys={N} heads={H} page={P} k={k}, {copies} key caches of {caches[0].numel() / 1e6:.0f} MB")
+
+    def step(i):
+        ops.indexer_scores(q, w, caches[i % copies], tables[i % copies], limits, N, out=scores)
+        return ops.topk_positions(scores, k)
+
+    lib = _lib.load()
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps_n):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    step_us = e0.elapsed_time(e1) / steps_n * 1e3
+    times = {}
+    for name, fn in (("score", lambda i: ops.indexer_scores(q, w, caches[i % copies], tables[i % copies], limits, N,
+                                                             out=scores)),
+                     ("topk", lambda i: ops.topk_positions(scores, k))):
+        lib.sna_diag_kernel_timing(1)
+        for i in range(steps_n):
+            fn(i)
+        ms, unused, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
+        _lib.check(lib.sna_diag_kernel_timing_read(ctypes.byref(ms), ctypes.byref(unused), ctypes.byref(n)),
+                   "kernel_timing_read")
+        lib.sna_diag_kernel_timing(0)
+        times[name] = ms.value / max(n.value, 1) * 1e3
+    score_bytes = B * N * (128 + 2)
+    achieved = score_bytes / (times["score"] * 1e-6) / 1e9
+    log(f"indexer_score_kernel {times['score']:.1f} us ({achieved:.0f} GB/s), topk {times['topk']:.1f} us, "
+        f"step {step_us:.1f} us")
+    line = {
+        "metric": INDEXER_METRIC, "value": round(step_us, 3), "unit": "us/step", "n_gpus": 1, "steps": steps_n,
+        "warmup": warmup, "ms_per_step": round(step_us * 1e-3, 6), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp8_e4m3fn keys, bf16 scores",
+        "data": "synthetic: seeded N(0,1) keys and queries (torch.Generator seed 1200), random page permutation",
+        "config": {"workload": "indexer: cfg5-scale DSA indexer, 16 rows x 131072 keys, 64 heads, top-2048",
+                   "batch": B, "keys_per_row": N, "index_heads": H, "head_dim": 128, "page_size": P, "topk": k,
+                   "key_copies": copies},
+        "score_us": round(times["score"], 3), "topk_us": round(times["topk"], 3),
+        "roofline": {"bound": "hbm", "kernel": "indexer_score_kernel", "achieved": round(achieved, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": _traffic("indexer"), "alg_bytes_per_launch": score_bytes,
+                     "avg_launch_us": round(times["score"], 3)},
+        "cpu_baseline": None,
+    }
+    if cpu:
+        from oracle import indexer as oix
+
+        c0, t0 = caches[0].cpu(), tables[0].cpu()
+        qc, wc = q.cpu(), w.cpu()
+
+        def run(n_keys):  # one row, its first n_keys keys, then its top-k
+            sc = oix.indexer_scores(qc[:1], wc[:1], c0, t0[:1], torch.tensor([n_keys]), n_keys)
+            oix.topk_positions(sc, min(k, n_keys))
+
+        t = time.perf_counter()
+        run(4096)
+        t1 = time.perf_counter() - t
+        n_keys = max(4096, min(N, int(4096 * cpu_budget / 3 / max(t1, 1e-6))))
+        ts = []
+        for _ in range(3):
+            t = time.perf_counter()
+            run(n_keys)
+            ts.append(time.perf_counter() - t)
+        med = statistics.median(ts)
+        line["cpu_baseline"] = {"value": round(med * (B * N / n_keys) * 1e6, 1), "unit": "us/step",
+                                "cores": torch.get_num_threads(), "kind": "port",
+                                "sample": f"row 0's first {n_keys} keys (median of 3 runs, scaled x{B * N / n_keys:.1f}"
+                                          " to the step)", "cpu": cpu_model()}
+        log(f"CPU baseline: {line['cpu_baseline']['value']:.0f} us/step")
+    return line
+
+
 PREFILL_METRIC = "prefill attention TFLOP/s over the FP8 pool (segmented, causal), 1 MI355X"
 
 
@@ -568,7 +675,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="2",
                     help="1, 2, 3, 4, 4swa or 5 (default 2, the metric's workload); meta: the device-side metadata; "
-                         "prefill: the segmented prefill attention")
+                         "prefill: the segmented prefill attention; indexer: the DSA indexer")
     ap.add_argument("--all", action="store_true", help="one line per workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work for the baseline sample")
@@ -600,6 +707,8 @@ def main() -> int:
             line = run_meta(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
         elif k == "prefill":
             line = run_prefill(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
+        elif k == "indexer":
+            line = run_indexer(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
         else:
             line = run_one(k, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
         print(json.dumps(line), flush=True)

@@ -280,11 +280,14 @@ int sna_indexer_scores(const void *q, const float *w, const uint8_t *keys, const
 /* The k largest of each row of bf16 scores [B, width] (row stride score_stride): out[b, 0 .. k) int32 (row stride
  * out_stride) = their positions e, those above the k-th largest value first, then its ties (the lowest positions),
  * each group in position order; a selected score <= -1e30 / 2 (a dead key) is written as -1. Exact: the selected
- * values are the k largest.
+ * values are the k largest. B <= 65535. workspace: device memory of at least sna_topk_workspace_bytes(B, width)
+ * bytes, 4-byte aligned, any contents (every word is written before it is read); calls that share a workspace on
+ * different streams race.
  * Replaces: indexer_topk_local_torch_ref's selection (indexer_torch.py:296-309); its slot order is a Trainium
  * layout, the set is the same. */
+int64_t sna_topk_workspace_bytes(int32_t B, int32_t width);
 int sna_topk_positions(const void *scores, int64_t score_stride, int32_t B, int32_t width, int32_t k, int32_t *out,
-                       int64_t out_stride, void *stream);
+                       int64_t out_stride, void *workspace, int64_t workspace_bytes, void *stream);
 
 /* =====================================================================================================
  * Decode metadata on the device

@@ -69,7 +69,8 @@ SIGNATURES = {
                                      _I32, _I32, _I32, _I32, _I64, _I32, _P]),
     "sna_index_key_store": (_I32, [_P, _P, _I64, _I32, _P, _I64, _P]),
     "sna_indexer_scores": (_I32, [_P, _P, _P, _P, _I64, _I32, _P, _I32, _I32, _I32, _I32, _I64, _I32, _P, _I64, _P]),
-    "sna_topk_positions": (_I32, [_P, _I64, _I32, _I32, _I32, _P, _I64, _P]),
+    "sna_topk_workspace_bytes": (_I64, [_I32, _I32]),
+    "sna_topk_positions": (_I32, [_P, _I64, _I32, _I32, _I32, _P, _I64, _P, _I64, _P]),
     "sna_block_table": (_I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _I32, _I32, _P, _P, _P]),
     "sna_window_table": (_I32, [_P, _I64, _I32, _P, _I32, _I32, _I32, _P, _P, _P]),
     "sna_diag_fp8_to_bf16": (_I32, [_P, _P, _I64, _P]),

@@ -129,85 +129,230 @@ __global__ __launch_bounds__(256) void indexer_score_kernel(IndexerArgs a) {
 
 // bf16 bits -> a 16-bit key whose unsigned order is the value order (NaN aside).
 __device__ __forceinline__ uint32_t order_key(uint32_t bits) { return (bits & 0x8000u) ? (~bits & 0xffffu) : (bits | 0x8000u); }
+__device__ __forceinline__ uint32_t key_bits(uint32_t key) { return (key & 0x8000u) ? (key & 0x7fffu) : (~key & 0xffffu); }
 
-// Top-k of one row per workgroup of 1024 threads: out[b, 0 .. k) = the positions of the k largest scores, those
-// above the threshold first, then the threshold's ties, each group in position order; a dead key (<= -1e30 / 2)
-// selected anyway is written as -1.
-__global__ __launch_bounds__(1024) void topk_kernel(const uint16_t* __restrict__ scores, int64_t score_stride,
-                                                    int32_t width, int32_t k, int32_t* __restrict__ out,
-                                                    int64_t out_stride) {
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t scan[2][1024];
-  __shared__ uint32_t sel[4];  // [threshold key, count above it, ties needed]
-  const int tid = threadIdx.x;
-  const int32_t b = blockIdx.x;
-  const uint16_t* row = scores + (int64_t)b * score_stride;
-  int32_t* orow = out + (int64_t)b * out_stride;
-  const int32_t per = (width + 1023) / 1024;
-  const int32_t e0 = min(tid * per, width), e1 = min(e0 + per, width);
+// ---- top-k: a two-byte radix select over the rows' segments ----
+// A row of bf16 scores is cut into segments of kTopkSeg scores, one workgroup of 1024 lanes (8 scores each, one
+// 16-byte load) per (segment, row). Scores compare through order_key, a 16-bit key that sorts as the value does. Four
+// launches, each workgroup reading only what earlier launches published in the workspace (no zeroing, no global
+// atomics):
+//   topk_hist_hi:  the segment's histogram of the key's high byte          -> hist_hi[b][s][256]
+//   topk_hist_lo:  the row's bin H holding the k-th largest key (summing hist_hi over the segments);
+//                  the segment's histogram of the low byte of keys in H    -> hist_lo[b][s][256]
+//   topk_count:    the threshold key T (the k-th largest) and the count above it; the segment's counts of keys
+//                  above and equal to T                                    -> counts[b][s], and sel[b] from s = 0
+//   topk_write:    positions in order: keys above T at the running count of those before them, then T's ties at
+//                  n_above + their running count, while that is below k.
+// Workspace per row: (2 * 256 + 1) * S + 4 u32, S = ceil(width / kTopkSeg).
+constexpr int kTopkSeg = 8192, kTopkCopies = 32;
 
-  // pass 1: histogram of the key's high byte; the bin holding the k-th largest
-  if (tid < 256) hist[tid] = 0;
-  __syncthreads();
-  for (int32_t e = tid; e < width; e += 1024) atomicAdd(&hist[order_key(row[e]) >> 8], 1u);
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t above = 0;
-    int bin = 255;
-    for (; bin > 0; --bin) {
-      if (above + hist[bin] >= (uint32_t)k) break;
-      above += hist[bin];
+struct TopkRow {
+  const uint16_t* row;  // this row's scores
+  uint32_t* hist_hi;    // [S][256]
+  uint32_t* hist_lo;    // [S][256]
+  uint32_t* counts;     // [S]: (ties << 16) | above
+  uint32_t* sel;        // [4]: T, n_above
+};
+
+__device__ __forceinline__ TopkRow topk_row(const uint16_t* scores, int64_t score_stride, uint32_t* ws, int32_t S) {
+  const int32_t b = blockIdx.y;
+  uint32_t* base = ws + (int64_t)b * ((2 * 256 + 1) * (int64_t)S + 4);
+  return {scores + (int64_t)b * score_stride, base, base + 256 * S, base + 512 * S, base + 513 * S};
+}
+
+// this lane's 8 keys of segment blockIdx.x (past the row: key 0, never counted); in[j] says whether key j is inside
+__device__ __forceinline__ void topk_keys(const uint16_t* row, bool vec, int32_t width, uint32_t (&key)[8]) {
+  const int32_t e = blockIdx.x * kTopkSeg + 8 * threadIdx.x;
+  if (vec && e + 8 <= width) {
+    const uint4 v = *reinterpret_cast<const uint4*>(row + e);
+    const uint32_t x[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) key[j] = order_key((x[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) key[j] = e + j < width ? order_key(row[e + j]) : 0u;
+  }
+}
+
+__device__ __forceinline__ bool topk_vec(const uint16_t* scores, int64_t score_stride) {
+  return (score_stride % 8) == 0 && ((uintptr_t)scores & 15) == 0;  // rows 16-byte aligned: 8 scores per load
+}
+
+// LDS histogram helpers: 256 bins x kTopkCopies copies, bin-major; lane l adds into copy l mod 32, so the lanes of
+// one atomic instruction never share a bank
+__device__ __forceinline__ void topk_clear(uint32_t* hist) {
+  for (int i = threadIdx.x; i < 256 * kTopkCopies; i += blockDim.x) hist[i] = 0;
+}
+__device__ __forceinline__ void topk_publish(const uint32_t* hist, uint32_t* dst) {
+  const int t = threadIdx.x;
+  if (t < 256) {
+    uint32_t c = 0;
+#pragma unroll 8
+    for (int i = 0; i < kTopkCopies; ++i) c += hist[t * kTopkCopies + ((i + t) & (kTopkCopies - 1))];
+    dst[t] = c;
+  }
+}
+
+// The bin (from the top) where the running count of the row's keys, over the S published histograms hist[S][256],
+// reaches `need`, and the count in the bins above it plus base_above; every lane gets both. Threads 0..255 take
+// bin 255 - t. wtot: 4 u32 of LDS, out: 2 u32 of LDS.
+__device__ __forceinline__ void topk_pick(const uint32_t* hist, int32_t S, uint32_t need, uint32_t base_above,
+                                          uint32_t* wtot, uint32_t* out, uint32_t& bin, uint32_t& above) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  uint32_t cnt = 0, incl = 0;
+  if (t < 256) {
+    for (int32_t s = 0; s < S; ++s) cnt += hist[(int64_t)s * 256 + 255 - t];
+    incl = cnt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t v = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += v;
     }
-    sel[0] = (uint32_t)bin;
-    sel[1] = above;
+    if (lane == 63) wtot[wave] = incl;
   }
   __syncthreads();
-  const uint32_t hi_bin = sel[0], above1 = sel[1];
-  // pass 2: histogram of the low byte inside that bin; the threshold key T
-  if (tid < 256) hist[tid] = 0;
-  __syncthreads();
-  for (int32_t e = tid; e < width; e += 1024) {
-    const uint32_t kk = order_key(row[e]);
-    if ((kk >> 8) == hi_bin) atomicAdd(&hist[kk & 0xffu], 1u);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t above = above1;
-    int bin = 255;
-    for (; bin > 0; --bin) {
-      if (above + hist[bin] >= (uint32_t)k) break;
-      above += hist[bin];
+  if (t < 256) {
+    for (int w = 0; w < wave; ++w) incl += wtot[w];
+    incl += base_above;
+    const uint32_t before = incl - cnt;
+    // the first bin from the top whose running count reaches need (bin 0 takes whatever is left)
+    if ((before < need && incl >= need) || (t == 255 && before < need)) {
+      out[0] = 255u - (uint32_t)t;
+      out[1] = before;
     }
-    sel[0] = (hi_bin << 8) | (uint32_t)bin;
-    sel[1] = above;
-    sel[2] = (uint32_t)k - above;
   }
   __syncthreads();
-  const uint32_t T = sel[0], n_above = sel[1], n_ties = sel[2];
-  // pass 3: this thread's run [e0, e1): counts, block-wide exclusive scans, then the writes in position order
-  uint32_t c_gt = 0, c_eq = 0;
-  for (int32_t e = e0; e < e1; ++e) {
-    const uint32_t kk = order_key(row[e]);
-    c_gt += kk > T;
-    c_eq += kk == T;
-  }
-  scan[0][tid] = c_gt;
-  scan[1][tid] = c_eq;
+  bin = out[0];
+  above = out[1];
+}
+
+__global__ __launch_bounds__(1024) void topk_hist_hi_kernel(const uint16_t* __restrict__ scores,
+                                                            int64_t score_stride, int32_t width, int32_t S,
+                                                            uint32_t* __restrict__ ws) {
+  __shared__ uint32_t hist[256 * kTopkCopies];
+  const TopkRow r = topk_row(scores, score_stride, ws, S);
+  uint32_t key[8];
+  topk_keys(r.row, topk_vec(scores, score_stride), width, key);
+  topk_clear(hist);
   __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {  // Hillis-Steele inclusive scan of both counts
-    const uint32_t x0 = tid >= off ? scan[0][tid - off] : 0u, x1 = tid >= off ? scan[1][tid - off] : 0u;
-    __syncthreads();
-    scan[0][tid] += x0;
-    scan[1][tid] += x1;
-    __syncthreads();
+  uint32_t* mine = hist + (threadIdx.x & (kTopkCopies - 1));
+  const int32_t e = blockIdx.x * kTopkSeg + 8 * threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (e + j < width) atomicAdd(&mine[(key[j] >> 8) * kTopkCopies], 1u);
+  __syncthreads();
+  topk_publish(hist, r.hist_hi + (int64_t)blockIdx.x * 256);
+}
+
+__global__ __launch_bounds__(1024) void topk_hist_lo_kernel(const uint16_t* __restrict__ scores,
+                                                            int64_t score_stride, int32_t width, int32_t S, int32_t k,
+                                                            uint32_t* __restrict__ ws) {
+  __shared__ uint32_t hist[256 * kTopkCopies];
+  __shared__ uint32_t wtot[4], pick[2];
+  const TopkRow r = topk_row(scores, score_stride, ws, S);
+  uint32_t key[8];
+  topk_keys(r.row, topk_vec(scores, score_stride), width, key);
+  topk_clear(hist);
+  uint32_t hi, above;
+  topk_pick(r.hist_hi, S, (uint32_t)k, 0, wtot, pick, hi, above);  // its barriers also cover the clear
+  uint32_t* mine = hist + (threadIdx.x & (kTopkCopies - 1));
+  const int32_t e = blockIdx.x * kTopkSeg + 8 * threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (e + j < width && (key[j] >> 8) == hi) atomicAdd(&mine[(key[j] & 0xffu) * kTopkCopies], 1u);
+  __syncthreads();
+  topk_publish(hist, r.hist_lo + (int64_t)blockIdx.x * 256);
+}
+
+// the threshold key T and the count above it, from the two published histograms
+__device__ __forceinline__ void topk_threshold(const TopkRow& r, int32_t S, int32_t k, uint32_t* wtot, uint32_t* pick,
+                                               uint32_t& T, uint32_t& n_above) {
+  uint32_t hi, above1, lo;
+  topk_pick(r.hist_hi, S, (uint32_t)k, 0, wtot, pick, hi, above1);
+  __syncthreads();  // pick[] is rewritten
+  topk_pick(r.hist_lo, S, (uint32_t)k, above1, wtot, pick, lo, n_above);
+  T = (hi << 8) | lo;
+}
+
+__global__ __launch_bounds__(1024) void topk_count_kernel(const uint16_t* __restrict__ scores, int64_t score_stride,
+                                                          int32_t width, int32_t S, int32_t k,
+                                                          uint32_t* __restrict__ ws) {
+  __shared__ uint32_t wtot[16], pick[2];
+  const TopkRow r = topk_row(scores, score_stride, ws, S);
+  uint32_t key[8];
+  topk_keys(r.row, topk_vec(scores, score_stride), width, key);
+  uint32_t T, n_above;
+  topk_threshold(r, S, k, wtot, pick, T, n_above);
+  const int32_t e = blockIdx.x * kTopkSeg + 8 * threadIdx.x;
+  uint32_t cnt = 0;  // (ties << 16) | above, each at most 8 per lane and kTopkSeg per segment
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const bool in = e + j < width;
+    cnt += (in && key[j] > T) ? 1u : 0u;
+    cnt += (in && key[j] == T) ? 0x10000u : 0u;
   }
-  uint32_t o_gt = scan[0][tid] - c_gt, o_eq = scan[1][tid] - c_eq;
-  for (int32_t e = e0; e < e1; ++e) {
-    const uint32_t bits = row[e], kk = order_key(bits);
-    const int32_t label = bf16_bits_to_f32(bits) > -0.5f * kIndexMaskBound ? e : -1;  // a dead key: -1
-    if (kk > T) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+  __syncthreads();  // wtot was read by the picks
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) wtot[wave] = cnt;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t total = 0;
+    for (int w = 0; w < 16; ++w) total += wtot[w];
+    r.counts[blockIdx.x] = total;
+    if (blockIdx.x == 0) {
+      r.sel[0] = T;
+      r.sel[1] = n_above;
+    }
+  }
+}
+
+__global__ __launch_bounds__(1024) void topk_write_kernel(const uint16_t* __restrict__ scores, int64_t score_stride,
+                                                          int32_t width, int32_t S, int32_t k,
+                                                          uint32_t* __restrict__ ws, int32_t* __restrict__ out,
+                                                          int64_t out_stride) {
+  __shared__ uint32_t wtot[16];
+  const TopkRow r = topk_row(scores, score_stride, ws, S);
+  uint32_t key[8];
+  topk_keys(r.row, topk_vec(scores, score_stride), width, key);
+  const uint32_t T = r.sel[0], n_above = r.sel[1], n_ties = (uint32_t)k - n_above;
+  uint32_t run_gt = 0, run_eq = 0;  // the counts of the segments before this one (ties may pass 16 bits here)
+  for (int32_t s = 0; s < (int32_t)blockIdx.x; ++s) {
+    const uint32_t c = r.counts[s];
+    run_gt += c & 0xffffu;
+    run_eq += c >> 16;
+  }
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int32_t e = blockIdx.x * kTopkSeg + 8 * tid;
+  uint32_t cnt = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const bool in = e + j < width;
+    cnt += (in && key[j] > T) ? 1u : 0u;
+    cnt += (in && key[j] == T) ? 0x10000u : 0u;
+  }
+  uint32_t incl = cnt;  // inclusive scan over the wave
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t v = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += v;
+  }
+  if (lane == 63) wtot[wave] = incl;
+  __syncthreads();
+  uint32_t before = 0;  // packed: inside one segment each count is at most kTopkSeg
+#pragma unroll
+  for (int w = 0; w < 16; ++w) before += w < wave ? wtot[w] : 0u;
+  const uint32_t excl = before + incl - cnt;
+  uint32_t o_gt = run_gt + (excl & 0xffffu), o_eq = run_eq + (excl >> 16);
+  int32_t* orow = out + (int64_t)blockIdx.y * out_stride;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (e + j >= width) continue;
+    const int32_t label = bf16_bits_to_f32(key_bits(key[j])) > -0.5f * kIndexMaskBound ? e + j : -1;  // dead: -1
+    if (key[j] > T) {
       orow[o_gt++] = label;
-    } else if (kk == T) {
+    } else if (key[j] == T) {
       if (o_eq < n_ties) orow[n_above + o_eq] = label;
       ++o_eq;
     }
@@ -288,18 +433,38 @@ int sna_indexer_scores(const void* q, const float* w, const uint8_t* keys, const
   return check_launch("indexer_scores");
 }
 
+int64_t sna_topk_workspace_bytes(int32_t B, int32_t width) {
+  if (B <= 0 || width <= 0) return 0;
+  const int64_t S = ((int64_t)width + kTopkSeg - 1) / kTopkSeg;
+  return (int64_t)B * ((2 * 256 + 1) * S + 4) * (int64_t)sizeof(uint32_t);
+}
+
 int sna_topk_positions(const void* scores, int64_t score_stride, int32_t B, int32_t width, int32_t k, int32_t* out,
-                       int64_t out_stride, void* stream) {
+                       int64_t out_stride, void* workspace, int64_t workspace_bytes, void* stream) {
   ApiGuard guard;
-  if (B < 0 || width < 0 || k < 1 || k > width || score_stride < width || out_stride < k)
+  if (B < 0 || width < 0 || k < 1 || k > width || score_stride < width || out_stride < k || B > 65535)
     return fail(SNA_ERR_INVALID_ARGUMENT, "topk_positions: bad sizes (B %d, width %d, k %d, strides %lld / %lld)", B,
                 width, k, (long long)score_stride, (long long)out_stride);
   if (B == 0) return SNA_OK;
-  if (!scores || !out) return fail(SNA_ERR_INVALID_ARGUMENT, "topk_positions: null pointer");
+  if (!scores || !out || !workspace) return fail(SNA_ERR_INVALID_ARGUMENT, "topk_positions: null pointer");
+  const int64_t need = sna_topk_workspace_bytes(B, width);
+  if (workspace_bytes < need)
+    return fail(SNA_ERR_WORKSPACE, "topk_positions: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
+                (long long)need);
+  if (((uintptr_t)workspace & 3) != 0) return fail(SNA_ERR_INVALID_ARGUMENT, "topk_positions: unaligned workspace");
+  const int32_t S = (int32_t)(((int64_t)width + kTopkSeg - 1) / kTopkSeg);
+  const dim3 grid((unsigned)S, (unsigned)B), block(1024);
+  const uint16_t* sc = (const uint16_t*)scores;
+  uint32_t* ws = (uint32_t*)workspace;
   hipEvent_t t0, t1;
-  timing_events(0, &t0, &t1);
-  hipExtLaunchKernelGGL(topk_kernel, dim3((unsigned)B), dim3(1024), 0, (hipStream_t)stream, t0, t1, 0,
-                        (const uint16_t*)scores, score_stride, width, k, out, out_stride);
+  timing_events(0, &t0, &t1);  // the first launch's start to the last launch's end
+  hipStream_t st = (hipStream_t)stream;
+  hipExtLaunchKernelGGL(topk_hist_hi_kernel, grid, block, 0, st, t0, nullptr, 0, sc, score_stride, width, S, ws);
+  hipExtLaunchKernelGGL(topk_hist_lo_kernel, grid, block, 0, st, nullptr, nullptr, 0, sc, score_stride, width, S, k,
+                        ws);
+  hipExtLaunchKernelGGL(topk_count_kernel, grid, block, 0, st, nullptr, nullptr, 0, sc, score_stride, width, S, k, ws);
+  hipExtLaunchKernelGGL(topk_write_kernel, grid, block, 0, st, nullptr, t1, 0, sc, score_stride, width, S, k, ws, out,
+                        out_stride);
   timing_end_call();
   return check_launch("topk_positions");
 }

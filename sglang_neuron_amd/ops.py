@@ -519,8 +519,10 @@ def topk_positions(scores: Tensor, k: int) -> Tensor:
     B, N = scores.shape
     _need(1 <= k <= N, f"k {k} must be in [1, {N}]")
     out = torch.empty(B, k, dtype=torch.int32, device=dev)
-    rc = _lib.load().sna_topk_positions(_ptr(scores), scores.stride(0), B, N, int(k), _ptr(out), out.stride(0),
-                                        _stream(dev))
+    lib = _lib.load()
+    ws = torch.empty(max(int(lib.sna_topk_workspace_bytes(B, N)), 4), dtype=torch.uint8, device=dev)
+    rc = lib.sna_topk_positions(_ptr(scores), scores.stride(0), B, N, int(k), _ptr(out), out.stride(0), _ptr(ws),
+                                ws.numel(), _stream(dev))
     _lib.check(rc, "topk_positions")
     return out
 

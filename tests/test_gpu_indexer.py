@@ -70,13 +70,14 @@ def test_indexer_scores_match_oracle(name, seed, H, P, limits, width):
 
 def _deterministic_topk(row: torch.Tensor, k: int) -> set:
     """The selection with ties taken at the lowest positions (sort by value desc, then position), dead keys as -1."""
-    r = row.float()
-    order = sorted(range(r.numel()), key=lambda e: (-float(r[e]), e))[:k]
-    return {e if float(r[e]) > -5e29 else -1 for e in order}
+    r = row.float().tolist()
+    order = sorted(range(len(r)), key=lambda e: (-r[e], e))[:k]
+    return {e if r[e] > -5e29 else -1 for e in order}
 
 
 TOPK = [("ties", 6, 3, 3000, 300), ("k2048-of-8192", 7, 2, 8192, 2048), ("k-all", 8, 2, 700, 700),
-        ("dead-tail", 9, 2, 1500, 1200)]
+        ("dead-tail", 9, 2, 1500, 1200), ("multi-chunk", 12, 2, 20000, 2048), ("odd-width", 13, 2, 9001, 1000),
+        ("row-in-registers-max", 14, 1, 131072, 2048), ("streamed-row", 15, 1, 140001, 2048)]
 
 
 @pytest.mark.parametrize("name,seed,B,N,k", TOPK, ids=[t[0] for t in TOPK])

@@ -45,30 +45,83 @@ __device__ __forceinline__ f32x4_t mfma_16x16x128_fp8_sa(const uint32_t (&a)[8],
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 0, 0, 0, scale_a, 0, 127);
 }
 
+constexpr int kScoreKeys = 2048;  // keys per workgroup (a multiple of 64): 32 tiles of 16 keys per wave
+
 template <int HT>  // head tiles of 16
 __global__ __launch_bounds__(256) void indexer_score_kernel(IndexerArgs a) {
-  constexpr int D = 128;
+  // PD: key tiles each wave has in flight ahead of the one it scores (fewer with 128 heads, whose query operands
+  // take 128 VGPRs)
+  constexpr int D = 128, TILES = kScoreKeys / 64, PD = HT >= 8 ? 2 : 4;
+  static_assert(kScoreKeys % 64 == 0 && kScoreKeys / 64 <= 32, "a 32-bit mask of live tiles");
+  __shared__ uint32_t sm_q[HT][2][8][64];  // [head tile][hi, lo][dword][lane]: the MFMA A operand of each lane
+  __shared__ int32_t sm_ex[HT][64];         // floor(log2 amax) of the head lane (li) feeds, per head tile
+  __shared__ __align__(16) uint16_t sm_out[kScoreKeys];  // the workgroup's bf16 scores
   const int tid = threadIdx.x, lane = tid & 63, g4 = lane >> 4, li = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int32_t b = blockIdx.y;
-  const int32_t e_blk = (int32_t)blockIdx.x * 256;
+  const int32_t e_blk = (int32_t)blockIdx.x * kScoreKeys;
   if (e_blk >= a.width) return;
   const int32_t limit = a.limits[b];
+  const int32_t* trow = a.table + (int64_t)b * a.table_stride;
+
+  // the raw query rows this wave splits (head tiles wave, wave + 4, ...), loaded before anything they wait on
+  constexpr int QT = (HT + 3) / 4;
+  uint4 qraw[QT][4];
+#pragma unroll
+  for (int j = 0; j < QT; ++j) {
+    const int ht = wave + 4 * j;
+    if (ht < HT) {
+      const uint16_t* qp = a.q + ((int64_t)b * a.H + 16 * ht + li) * D + 32 * g4;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) qraw[j][c] = ld16(qp + 8 * c);
+    }
+  }
+
+  // This lane's key of tile t is e_blk + 64 t + 16 wave + li (the four waves cover 64 consecutive keys per step);
+  // its page is looked up first, all tiles at once. Bit t of live_bits: the key is resident, its page valid.
+  // (col, off) = divmod(e, P), stepped by 64 keys per tile: one division for the first tile, then
+  // (col, off) += divmod(64, P) with at most one carry.
+  int32_t kofs[TILES];  // the key row's byte offset in the cache / 16 (the cache is under 2^35 bytes), if live
+  uint32_t live_bits = 0;
+  {
+    const int32_t e0 = e_blk + 16 * wave + li, step_col = 64 / a.P, step_off = 64 % a.P;
+    int32_t col = e0 / a.P, off = e0 - col * a.P;
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+      const int32_t e = e0 + 64 * t;
+      const int32_t page = (e < a.width && col < a.table_width) ? trow[col] : -1;
+      const bool live = e < limit && page >= 0 && (int64_t)page < a.num_blocks;
+      live_bits |= live ? (1u << t) : 0u;
+      kofs[t] = live ? (int32_t)((((int64_t)page * a.P + off) * D) >> 4) : 0;
+      col += step_col;
+      off += step_off;
+      if (off >= a.P) off -= a.P, ++col;
+    }
+  }
+
+  // key tiles in flight: tile t's 32 bytes of this lane land in ring[t % PD]. Every lane loads (a dead key reads
+  // row 0 of the cache, in bounds, and its score is replaced), so no branch or store sits between a load and its
+  // use and the waits count only the ring's own loads.
+  uint32_t ring[PD][8];
+  auto fetch = [&](int t, uint32_t (&kb)[8]) {
+    const uint8_t* kp = a.keys + ((int64_t)kofs[t] << 4) + 32 * g4;
+    const uint4 x0 = ld16_stream(kp), x1 = ld16_stream(kp + 16);
+    kb[0] = x0.x, kb[1] = x0.y, kb[2] = x0.z, kb[3] = x0.w, kb[4] = x1.x, kb[5] = x1.y, kb[6] = x1.z, kb[7] = x1.w;
+  };
+#pragma unroll
+  for (int u = 0; u < PD; ++u) fetch(u, ring[u]);
 
   // The query operand of head tile ht: lane (g4, i) supplies head 16 ht + i, dims 32 g4 .. + 31, as two exact
   // e4m3fn parts of the row scaled by sc = 2^(7 - floor(log2 amax)) (amax over the head's 128 dims); the E8M0 A
-  // scales are 127 - log2 sc for hi and 4 less for lo.
-  uint32_t qhi[HT][8], qlo[HT][8];
-  int32_t sc_hi[HT], sc_lo[HT];
-  float wl[HT][4];  // weights of heads 16 ht + 4 g4 + r (the rows this lane's results hold)
+  // scales are 127 - log2 sc for hi and 4 less for lo. Wave w splits head tiles w, w + 4, ... into LDS.
 #pragma unroll
-  for (int ht = 0; ht < HT; ++ht) {
-    const int32_t h = 16 * ht + li;
-    const uint16_t* qp = a.q + ((int64_t)b * a.H + h) * D + 32 * g4;
+  for (int j = 0; j < QT; ++j) {
+    const int ht = wave + 4 * j;
+    if (ht >= HT) break;  // (uniform)
     float v[32];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const uint4 x = ld16(qp + 8 * c);
+      const uint4 x = qraw[j][c];
       const uint32_t xx[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -82,48 +135,62 @@ __global__ __launch_bounds__(256) void indexer_score_kernel(IndexerArgs a) {
     amax = max_across_groups(amax);
     const int32_t ex = amax > 0.0f ? max((int32_t)((__float_as_uint(amax) >> 23) & 0xff) - 127, -116) : -7;
     const float sc = __uint_as_float((uint32_t)(127 + 7 - ex) << 23);
-    sc_hi[ht] = 127 + ex - 7;
-    sc_lo[ht] = 127 + ex - 7 - 4;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       float h4[4], l4[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) split_q(v[4 * k + e] * sc, h4[e], l4[e]);
-      qhi[ht][k] = pack_e4m3fn_x4(h4[0], h4[1], h4[2], h4[3]);
-      qlo[ht][k] = pack_e4m3fn_x4(l4[0], l4[1], l4[2], l4[3]);
+      sm_q[ht][0][k][lane] = pack_e4m3fn_x4(h4[0], h4[1], h4[2], h4[3]);
+      sm_q[ht][1][k][lane] = pack_e4m3fn_x4(l4[0], l4[1], l4[2], l4[3]);
     }
+    sm_ex[ht][lane] = ex;
+  }
+  // weights of heads 16 ht + 4 g4 + r (the rows this lane's results hold), times d^-0.5: w relu(s d^-0.5) =
+  // (w d^-0.5) relu(s) as d^-0.5 > 0
+  float wl[HT][4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) wl[ht][r] = a.w[(int64_t)b * a.H + 16 * ht + 4 * g4 + r];
+  for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wl[ht][r] = a.w[(int64_t)b * a.H + 16 * ht + 4 * g4 + r] * a.scale;
+
+  __syncthreads();
+  uint32_t qhi[HT][8], qlo[HT][8];
+  int32_t sc_hi[HT], sc_lo[HT];
+#pragma unroll
+  for (int ht = 0; ht < HT; ++ht) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) qhi[ht][k] = sm_q[ht][0][k][lane], qlo[ht][k] = sm_q[ht][1][k][lane];
+    const int32_t ex = sm_ex[ht][lane];
+    sc_hi[ht] = 127 + ex - 7;
+    sc_lo[ht] = 127 + ex - 7 - 4;
   }
 
-  const int32_t* trow = a.table + (int64_t)b * a.table_stride;
-#pragma unroll 1
-  for (int kt = 0; kt < 4; ++kt) {
-    const int32_t e = e_blk + 64 * wave + 16 * kt + li;  // this lane's key
-    if (e_blk + 64 * wave + 16 * kt >= a.width) break;   // (uniform)
-    const int32_t col = e / a.P;
-    int32_t page = (e < a.width && col < a.table_width) ? trow[col] : -1;
-    const bool live = e < limit && page >= 0 && (int64_t)page < a.num_blocks;
-    uint32_t kb[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (live) {
-      const uint8_t* kp = a.keys + ((int64_t)page * a.P + e % a.P) * D + 32 * g4;
-      const uint4 x0 = ld16_stream(kp), x1 = ld16_stream(kp + 16);
-      kb[0] = x0.x, kb[1] = x0.y, kb[2] = x0.z, kb[3] = x0.w, kb[4] = x1.x, kb[5] = x1.y, kb[6] = x1.z, kb[7] = x1.w;
-    }
+  // scores of the workgroup's keys, written out coalesced at the end
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) {
     float sum = 0.0f;
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht) {
       f32x4_t s = {0.f, 0.f, 0.f, 0.f};
-      s = mfma_16x16x128_fp8_sa(qhi[ht], kb, s, sc_hi[ht]);
-      s = mfma_16x16x128_fp8_sa(qlo[ht], kb, s, sc_lo[ht]);
+      s = mfma_16x16x128_fp8_sa(qhi[ht], ring[t % PD], s, sc_hi[ht]);
+      s = mfma_16x16x128_fp8_sa(qlo[ht], ring[t % PD], s, sc_lo[ht]);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sum = fmaf(wl[ht][r], fmaxf(s[r] * a.scale, 0.0f), sum);
+      for (int r = 0; r < 4; ++r)  // relu as an integer max: a negative float's bits are a negative integer
+        sum = fmaf(wl[ht][r], __int_as_float(max(__float_as_int(s[r]), 0)), sum);
     }
-    sum = sum_across_groups(sum);
-    if (g4 == 0 && e < a.width) {
-      const float v = fminf(sum, live ? kIndexMaskBound : -kIndexMaskBound);
-      a.out[(int64_t)b * a.out_stride + e] = (uint16_t)f32_to_bf16_bits(v);
-    }
+    if (t + PD < TILES) fetch(t + PD, ring[t % PD]);
+    sum = sum_across_groups(sum);  // every lane of key li holds the key's sum
+    const bool live = (live_bits >> t) & 1u;
+    sm_out[64 * t + 16 * wave + li] = (uint16_t)f32_to_bf16_bits(live ? fminf(sum, kIndexMaskBound) : -kIndexMaskBound);
+  }
+  __syncthreads();
+  uint16_t* orow = a.out + (int64_t)b * a.out_stride + e_blk;
+  const int32_t n = min(kScoreKeys, a.width - e_blk);
+  if (n == kScoreKeys && ((uintptr_t)orow & 7) == 0) {
+    for (int32_t i = 4 * tid; i < kScoreKeys; i += 4 * 256)
+      *reinterpret_cast<uint2*>(orow + i) = *reinterpret_cast<const uint2*>(&sm_out[i]);
+  } else {
+    for (int32_t i = tid; i < n; i += 256) orow[i] = sm_out[i];
   }
 }
 
@@ -400,6 +467,8 @@ int sna_indexer_scores(const void* q, const float* w, const uint8_t* keys, const
     return fail(SNA_ERR_INVALID_ARGUMENT, "indexer_scores: null pointer");
   if (!aligned(q, 16) || !aligned(keys, 16)) return fail(SNA_ERR_INVALID_ARGUMENT, "indexer_scores: q and keys 16-B aligned");
   if (B > 65535) return fail(SNA_ERR_INVALID_ARGUMENT, "indexer_scores: %d rows exceed the grid", B);
+  if (num_blocks * (int64_t)page_size * head_dim >= ((int64_t)1 << 35))
+    return fail(SNA_ERR_UNSUPPORTED, "indexer_scores: a key cache of 32 GiB or more");
   IndexerArgs a;
   a.q = (const uint16_t*)q;
   a.w = w;
@@ -416,7 +485,7 @@ int sna_indexer_scores(const void* q, const float* w, const uint8_t* keys, const
   a.P = page_size;
   a.num_blocks = num_blocks;
   a.scale = 1.0f / sqrtf((float)head_dim);
-  const dim3 grid((unsigned)((width + 255) / 256), (unsigned)B);
+  const dim3 grid((unsigned)((width + kScoreKeys - 1) / kScoreKeys), (unsigned)B);
   hipEvent_t t0, t1;
   timing_events(0, &t0, &t1);
   const hipStream_t s = (hipStream_t)stream;

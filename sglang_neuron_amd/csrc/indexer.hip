@@ -4,16 +4,15 @@
 //   reference: models/glm52/kernels/decode/attention/indexer/indexer_torch.py (pack_indexer_keys_fp8 :44-53, the
 //   score of indexer_kv_score_torch_ref :254-268, indexer_topk_local_torch_ref :296-309)
 //
-// Score: one workgroup of 4 waves per (row, 256 keys); each wave takes 16-key tiles. S[head, key] = Q . K^T on
+// Score: one workgroup of 4 waves per (row, 2048 keys); each wave takes 16-key tiles. S[head, key] = Q . K^T on
 // v_mfma_scale_f32_16x16x128_f8f6f4 (one instruction covers d = 128): lane (g4, i) feeds row i of the head tile (the
 // query split exactly into two e4m3fn parts, hi + lo / 16, of a power-of-two-scaled row, whose E8M0 A scales undo
-// the scaling) and column i, the 32 key bytes 32 g4 .. + 31 of key i, loaded straight from HBM into registers. The
-// result hands lane (g4, i) heads 4 g4 + r of key i: the head-weighted ReLU sum is 16 terms in the lane, then a sum
-// over the four lane groups. Bytes per key: 128 (the fp8 row) + 2 (the bf16 score written).
+// the scaling) and column i, the 32 key bytes 32 g4 .. + 31 of key i, loaded straight from HBM into a register ring.
+// The result hands lane (g4, i) heads 4 g4 + r of key i: the head-weighted ReLU sum is 16 terms in the lane, then a
+// sum over the four lane groups. Bytes per key: 128 (the fp8 row) + 2 (the bf16 score written).
 //
-// Top-k: one workgroup per row. The bf16 scores map to order-preserving 16-bit keys; two 256-bin histograms (high
-// byte, then the low byte inside the threshold bin) find the k-th largest key T; a third pass writes every position
-// above T and the first (k - count above) positions equal to T, in position order (block-wide scans). Deterministic.
+// Top-k: a two-byte radix select over order-preserving 16-bit keys of the scores, the row cut into segments of 8192
+// scores, in four launches that publish per-segment histograms and counts to a workspace (described below).
 
 #include "sna_device.h"
 #include "sna_host.h"

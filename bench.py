@@ -462,6 +462,116 @@ def run_indexer(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) ->
     return line
 
 
+WIRE_METRIC = "PD page-item transfer GB/s (one request's KV pages moved pool to pool), Qwen3-8B FP8 pool, 1 MI355X"
+
+
+def run_wire(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> dict:
+    """One request's KV pages moved between two pools, the transfer's WRITE list on one GPU (ops.copy_page_items over
+    get_contiguous_buf_infos): Qwen3-8B's FP8 pool (36 layers x K and V = 72 regions, items of 8 heads x 16 tokens x
+    128 dims = 16 KB), a 4096-token request (256 pages, 302 MB). Four page sets rotate over pools of 2048 pages, so
+    each step moves pages no earlier step touched. Pack (into a wire buffer) and unpack (out of it) are timed beside
+    it. HBM-bound: every byte moved is read once and written once."""
+    import ctypes
+
+    import torch
+
+    from sglang_neuron_amd import _lib, ops
+    from sglang_neuron_amd.mem_cache.memory_pool import NeuronMHATokenToKVPool
+
+    layers, G, d, P, n_pages, pool_pages, sets = 36, 8, 128, 16, 256, 2048, 4
+    pools = [NeuronMHATokenToKVPool(pool_pages * P, P, torch.float8_e4m3fn, G, d, layers, dev) for _ in range(2)]
+    g = torch.Generator(device=dev).manual_seed(1300)
+    for pool in pools:
+        for t in pool.k_buffer + pool.v_buffer:
+            t.view(torch.uint8).random_(0, 256, generator=g)  # in place: no copy dispatch beside the calibration's
+    src_inf, dst_inf = pools[0].get_contiguous_buf_infos(), pools[1].get_contiguous_buf_infos()
+    gc = torch.Generator().manual_seed(1301)
+    src_sets = [(torch.randperm(pool_pages, generator=gc)[:n_pages] + 1).to(torch.int32).to(dev) for _ in range(sets)]
+    dst_sets = [(torch.randperm(pool_pages, generator=gc)[:n_pages] + 1).to(torch.int32).to(dev) for _ in range(sets)]
+    moved = ops.page_items_wire_bytes(src_inf, n_pages)
+    wire = torch.empty(moved, dtype=torch.uint8, device=dev)
+    log(f"wire: {len(src_inf[0])} regions, items of {src_inf[2][0]} B, {n_pages} pages per step: {moved / 1e6:.0f} MB")
+
+    def step(i):
+        ops.copy_page_items(src_inf, dst_inf, src_sets[i % sets], dst_sets[i % sets])
+
+    lib = _lib.load()
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps_n):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    step_us = e0.elapsed_time(e1) / steps_n * 1e3
+    times = {}
+    for name, fn in (("copy", step), ("pack", lambda i: ops.pack_page_items(src_inf, src_sets[i % sets], wire)),
+                     ("unpack", lambda i: ops.unpack_page_items(wire, dst_inf, dst_sets[i % sets]))):
+        lib.sna_diag_kernel_timing(1)
+        for i in range(steps_n):
+            fn(i)
+        ms, unused, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
+        _lib.check(lib.sna_diag_kernel_timing_read(ctypes.byref(ms), ctypes.byref(unused), ctypes.byref(n)),
+                   "kernel_timing_read")
+        lib.sna_diag_kernel_timing(0)
+        times[name] = ms.value / max(n.value, 1) * 1e3
+    # a plain device copy of as many bytes, for the practical ceiling
+    flat = torch.empty(moved, dtype=torch.uint8, device=dev)
+    for _ in range(3):
+        flat.copy_(wire)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(20):
+        flat.copy_(wire)
+    e1.record()
+    torch.cuda.synchronize()
+    dcopy_us = e0.elapsed_time(e1) / 20 * 1e3
+    del flat
+    hbm = 2 * moved
+    achieved = hbm / (times["copy"] * 1e-6) / 1e9
+    log(f"page_items_kernel copy {times['copy']:.1f} us ({achieved:.0f} GB/s of HBM traffic), pack "
+        f"{times['pack']:.1f} us, unpack {times['unpack']:.1f} us; step {step_us:.1f} us; a contiguous device copy "
+        f"of as many bytes (torch copy_) {dcopy_us:.1f} us ({hbm / (dcopy_us * 1e-6) / 1e9:.0f} GB/s)")
+    line = {
+        "metric": WIRE_METRIC, "value": round(moved / (step_us * 1e-6) / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": steps_n, "warmup": warmup, "ms_per_step": round(step_us * 1e-3, 6), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "u8 (fp8_e4m3fn pages)",
+        "data": "synthetic: seeded random pool bytes (torch.Generator seed 1300), random page sets (seed 1301)",
+        "config": {"workload": "wire: one 4096-token request of a Qwen3-8B FP8 pool (36 layers, K and V) moved "
+                               "between two pools", "regions": len(src_inf[0]), "item_bytes": src_inf[2][0],
+                   "pages": n_pages, "pool_pages": pool_pages, "page_sets": sets},
+        "copy_us": round(times["copy"], 3), "pack_us": round(times["pack"], 3), "unpack_us": round(times["unpack"], 3),
+        "device_copy_us": round(dcopy_us, 3),
+        "roofline": {"bound": "hbm", "kernel": "page_items_kernel", "achieved": round(achieved, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": _traffic("wire"), "alg_bytes_per_launch": hbm,
+                     "avg_launch_us": round(times["copy"], 3)},
+        "cpu_baseline": None,
+    }
+    if cpu:
+        from oracle import page_items as opi
+
+        n_reg = 8  # a sample: 4 layers' K and V, every page of the request
+        il = src_inf[2][0]
+        src_host = [pools[0].k_buffer[j // 2].view(torch.uint8).reshape(-1).cpu() if j % 2 == 0 else
+                    pools[0].v_buffer[j // 2].view(torch.uint8).reshape(-1).cpu() for j in range(n_reg)]
+        dst_host = [torch.empty_like(t) for t in src_host]
+        sp, dp = src_sets[0].tolist(), dst_sets[0].tolist()
+        ts = []
+        for _ in range(3):
+            t = time.perf_counter()
+            opi.copy(src_host, dst_host, [il] * n_reg, sp, dp)
+            ts.append(time.perf_counter() - t)
+        med = statistics.median(ts)
+        line["cpu_baseline"] = {"value": round(n_reg * n_pages * il / med / 1e9, 2), "unit": "GB/s", "cores": 1,
+                                "kind": "port", "sample": f"{n_reg} of the {len(src_inf[0])} regions, every page of "
+                                                          "the request (median of 3 runs)", "cpu": cpu_model()}
+        log(f"CPU baseline: {line['cpu_baseline']['value']:.2f} GB/s")
+    return line
+
+
 PREFILL_METRIC = "prefill attention TFLOP/s over the FP8 pool (segmented, causal), 1 MI355X"
 
 
@@ -675,7 +785,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="2",
                     help="1, 2, 3, 4, 4swa or 5 (default 2, the metric's workload); meta: the device-side metadata; "
-                         "prefill: the segmented prefill attention; indexer: the DSA indexer")
+                         "prefill: the segmented prefill attention; indexer: the DSA indexer; wire: the PD page-item "
+                         "transfer")
     ap.add_argument("--all", action="store_true", help="one line per workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work for the baseline sample")
@@ -701,7 +812,7 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
         log(f"copy calibration: one copy of {COPY_CALIBRATION_BYTES} bytes (read) into as many (written)")
-    keys = ["1", "2", "3", "4", "4swa", "5"] if args.all else [args.config]
+    keys = ["1", "2", "3", "4", "4swa", "5", "meta", "prefill", "indexer", "wire"] if args.all else [args.config]
     for k in keys:
         if k == "meta":
             line = run_meta(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
@@ -709,6 +820,8 @@ def main() -> int:
             line = run_prefill(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
         elif k == "indexer":
             line = run_indexer(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
+        elif k == "wire":
+            line = run_wire(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
         else:
             line = run_one(k, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
         print(json.dumps(line), flush=True)

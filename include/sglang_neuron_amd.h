@@ -317,13 +317,50 @@ int sna_window_table(const int32_t *table, int64_t table_stride, int32_t table_w
                      int32_t B, int32_t page_size, int32_t n_blocks, int32_t *trimmed, int32_t *pos_offset,
                      void *stream);
 
+/* =====================================================================================================
+ * Page items: what a prefill-decode transfer moves
+ * ===================================================================================================== */
+
+/* A pool's regions as its get_contiguous_buf_infos gives them (host arrays of n_regions): region r is region_lens[r]
+ * bytes at device address region_ptrs[r], page p its item_lens[r] bytes at region_ptrs[r] + p * item_lens[r]
+ * (addresses and item sizes multiples of 16, items under 2 GiB, under 2^31 items a region). pages: device int32
+ * [n_pages]. Every call moves whole items, one workgroup per (page, region), in launches of up to 96 regions on
+ * `stream`.
+ * Replaces: the page-item addressing of NeuronMHATokenToKVPool.get_contiguous_buf_infos (mem_cache/memory_pool.py:
+ * 193-202) and the transfer's per-item WRITE (disaggregation/state_transfer.py:9-10), on one GPU. */
+
+/* The wire bytes of n_pages pages over the regions: n_pages * sum(item_lens); -1 for bad arguments. */
+int64_t sna_page_items_wire_bytes(const int64_t *item_lens, int32_t n_regions, int64_t n_pages);
+
+/* Gathers the items (r, pages[i]) into `wire`, region-major: region r's items start at n_pages * (sum of item_lens
+ * before r), item i at + i * item_lens[r]. A page outside region r (negative or >= region_lens[r] / item_lens[r])
+ * writes zeros in its place. wire: device, 16-B aligned, at least sna_page_items_wire_bytes bytes. */
+int sna_page_items_pack(const uint64_t *region_ptrs, const int64_t *region_lens, const int64_t *item_lens,
+                        int32_t n_regions, const int32_t *pages, int64_t n_pages, void *wire, int64_t wire_bytes,
+                        void *stream);
+
+/* Scatters a wire buffer of sna_page_items_pack's layout into the items (r, pages[i]); a page outside region r is
+ * skipped. pages must be distinct (two writes of one item race). */
+int sna_page_items_unpack(const void *wire, int64_t wire_bytes, const uint64_t *region_ptrs,
+                          const int64_t *region_lens, const int64_t *item_lens, int32_t n_regions,
+                          const int32_t *pages, int64_t n_pages, void *stream);
+
+/* Copies item (r, src_pages[i]) of the source regions to item (r, dst_pages[i]) of the destination regions, both
+ * with items of item_lens[r] bytes (a destination block of a larger page is addressed in units of the source item,
+ * as a stripe into a replicated page is); an item whose source or destination page is outside its region is skipped.
+ * dst_pages must be distinct. */
+int sna_page_items_copy(const uint64_t *src_ptrs, const int64_t *src_lens, const uint64_t *dst_ptrs,
+                        const int64_t *dst_lens, const int64_t *item_lens, int32_t n_regions,
+                        const int32_t *src_pages, const int32_t *dst_pages, int64_t n_pages, void *stream);
+
 /* ---- diagnostics ---- */
 
 /* Per-kernel timing of the decode entry points, for the benchmark's roofline figure. With timing on, each decode call
  * launches its split-K kernel and its combine kernel through hipExtLaunchKernel with a start/stop event pair, so the
  * kernels' own dispatch packets stamp the times and no marker packet runs between them (up to 4096 calls after the
- * switch); sna_block_table, sna_window_table, sna_prefill_attention, sna_indexer_scores and sna_topk_positions
- * time their one kernel as the split-K slot. sna_diag_kernel_timing_read
+ * switch); sna_block_table, sna_window_table, sna_prefill_attention, sna_indexer_scores, sna_topk_positions and the
+ * sna_page_items_* calls time their kernels (first launch's start to last launch's end) as the split-K slot.
+ * sna_diag_kernel_timing_read
  * waits for the events and returns the summed milliseconds of each kernel and the number of split-K-slot launches
  * timed. The events are the library's only state besides the error string. The timer
  * is not thread-safe and is off by default. */

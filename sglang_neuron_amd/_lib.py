@@ -69,6 +69,10 @@ SIGNATURES = {
                                      _I32, _I32, _I32, _I32, _I64, _I32, _P]),
     "sna_index_key_store": (_I32, [_P, _P, _I64, _I32, _P, _I64, _P]),
     "sna_indexer_scores": (_I32, [_P, _P, _P, _P, _I64, _I32, _P, _I32, _I32, _I32, _I32, _I64, _I32, _P, _I64, _P]),
+    "sna_page_items_wire_bytes": (_I64, [_P, _I32, _I64]),
+    "sna_page_items_pack": (_I32, [_P, _P, _P, _I32, _P, _I64, _P, _I64, _P]),
+    "sna_page_items_unpack": (_I32, [_P, _I64, _P, _P, _P, _I32, _P, _I64, _P]),
+    "sna_page_items_copy": (_I32, [_P, _P, _P, _P, _P, _I32, _P, _P, _I64, _P]),
     "sna_topk_workspace_bytes": (_I64, [_I32, _I32]),
     "sna_topk_positions": (_I32, [_P, _I64, _I32, _I32, _I32, _P, _I64, _P, _I64, _P]),
     "sna_block_table": (_I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _I32, _I32, _P, _P, _P]),

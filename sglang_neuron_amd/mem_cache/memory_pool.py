@@ -312,6 +312,14 @@ class NeuronMLATokenToKVPool:
         lens = [t.numel() * t.element_size() for t in self.kv_buffer]
         return ptrs, lens, [t[0].numel() * t.element_size() * self.page_size for t in self.kv_buffer]
 
+    def get_scale_buf_infos(self):
+        """(ptrs, lens, item_lens) of each layer's per-slot fp32 row scales, paged like the rows (page p is page_size *
+        4 bytes at ptr + p * item_len). The reference's MLA pool has no such scales; a transfer of this pool moves
+        these items beside the rows of get_contiguous_buf_infos."""
+        ptrs = [t.data_ptr() for t in self.row_scale]
+        lens = [t.numel() * t.element_size() for t in self.row_scale]
+        return ptrs, lens, [self.page_size * 4] * len(self.row_scale)
+
     def get_cpu_copy(self, *args, **kwargs):
         raise NotImplementedError("KV host offload is not part of this build")
 

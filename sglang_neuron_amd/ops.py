@@ -8,6 +8,7 @@ Reference interfaces each function stands in for are cited per function (paths u
 
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Optional, Sequence, Union
 
@@ -599,3 +600,74 @@ def diag_fp8_to_bf16(x: Tensor) -> Tensor:
 
 def default_sm_scale(head_dim: int) -> float:
     return 1.0 / math.sqrt(head_dim)
+
+
+# ------------------------------------------------------------------------------------------------------------------
+# page items: what a prefill-decode transfer moves
+# ------------------------------------------------------------------------------------------------------------------
+
+def _regions(infos, what: str):
+    """Host arrays (ptrs u64, lens i64, item_lens i64) of a pool's get_contiguous_buf_infos() triple."""
+    ptrs, lens, items = (list(x) for x in infos)
+    _need(len(ptrs) == len(lens) == len(items), f"{what}: ptrs, lens and item_lens differ in length")
+    n = len(ptrs)
+    return ((ctypes.c_uint64 * n)(*[int(x) for x in ptrs]), (ctypes.c_int64 * n)(*[int(x) for x in lens]),
+            (ctypes.c_int64 * n)(*[int(x) for x in items]), n)
+
+
+def _pages(pages: Tensor, what: str) -> Tensor:
+    _need(pages.dim() == 1, f"{what}: pages must be 1-D")
+    return pages.to(torch.int32).contiguous()
+
+
+def page_items_wire_bytes(infos, n_pages: int) -> int:
+    """Bytes of the wire buffer holding n_pages pages of every region of ``infos`` (a pool's
+    get_contiguous_buf_infos(): (ptrs, lens, item_lens), mem_cache/memory_pool.py:193-202)."""
+    _, _, items, n = _regions(infos, "page_items_wire_bytes")
+    return int(_lib.load().sna_page_items_wire_bytes(items, n, int(n_pages)))
+
+
+def pack_page_items(infos, pages: Tensor, wire: Optional[Tensor] = None) -> Tensor:
+    """The items (region r, pages[i]) of ``infos``'s regions gathered into one uint8 wire buffer, region-major (region
+    r's items at n_pages * (item bytes of the regions before r), item i at + i * item_lens[r]); a page outside a
+    region packs as zeros. ``pages``: device int tensor [n]."""
+    dev = _on_gpu(pages)
+    p = _pages(pages, "pack_page_items")
+    ptrs, lens, items, n = _regions(infos, "pack_page_items")
+    lib = _lib.load()
+    need = int(lib.sna_page_items_wire_bytes(items, n, p.numel()))
+    if wire is None:
+        wire = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    _on_gpu(pages, wire)
+    _need(wire.dtype == torch.uint8 and wire.is_contiguous(), "wire must be contiguous uint8")
+    rc = lib.sna_page_items_pack(ptrs, lens, items, n, _ptr(p), p.numel(), _ptr(wire), wire.numel(), _stream(dev))
+    _lib.check(rc, "page_items_pack")
+    return wire[:need]
+
+
+def unpack_page_items(wire: Tensor, infos, pages: Tensor) -> None:
+    """Scatters a wire buffer of pack_page_items' layout into the items (region r, pages[i]) of ``infos``'s regions; a
+    page outside a region is skipped. ``pages`` must be distinct."""
+    dev = _on_gpu(wire, pages)
+    p = _pages(pages, "unpack_page_items")
+    _need(wire.dtype == torch.uint8 and wire.is_contiguous(), "wire must be contiguous uint8")
+    ptrs, lens, items, n = _regions(infos, "unpack_page_items")
+    rc = _lib.load().sna_page_items_unpack(_ptr(wire), wire.numel(), ptrs, lens, items, n, _ptr(p), p.numel(),
+                                           _stream(dev))
+    _lib.check(rc, "page_items_unpack")
+
+
+def copy_page_items(src_infos, dst_infos, src_pages: Tensor, dst_pages: Tensor) -> None:
+    """The transfer's WRITE list on one GPU: item (r, src_pages[i]) of the source pool's regions to item (r,
+    dst_pages[i]) of the destination's (disaggregation/state_transfer.py:9-10), items of the source's item_lens[r]
+    bytes (a destination page holding several source items is addressed in source-item units). A page outside its
+    region is skipped; ``dst_pages`` must be distinct."""
+    dev = _on_gpu(src_pages, dst_pages)
+    sp, dp = _pages(src_pages, "copy_page_items"), _pages(dst_pages, "copy_page_items")
+    _need(sp.numel() == dp.numel(), "copy_page_items: src_pages and dst_pages differ in length")
+    s_ptrs, s_lens, items, n = _regions(src_infos, "copy_page_items")
+    d_ptrs, d_lens, _, n_dst = _regions((dst_infos[0], dst_infos[1], src_infos[2]), "copy_page_items")
+    _need(n == n_dst, f"copy_page_items: {n} source regions, {n_dst} destination regions")
+    rc = _lib.load().sna_page_items_copy(s_ptrs, s_lens, d_ptrs, d_lens, items, n, _ptr(sp), _ptr(dp), sp.numel(),
+                                         _stream(dev))
+    _lib.check(rc, "page_items_copy")

@@ -19,5 +19,9 @@ How each function is pinned (tests/test_oracle_*.py):
            every prior position -> dense MLA, FP8 with scale 1 on representable values -> the bf16 result); page
            permutation invariance; split + LSE merge == unsplit.
   metadata brute-force construction of the block table from req_to_token.
+  indexer  the key cast against the e4m3fn definition and a known answer; the score by explicit float64 loops;
+           the top-k against a full sort.
+  page_items the item address against the pools' tensor indexing; pack by byte loops; unpack(pack) and
+           copy == unpack(pack) invariants.
 Nothing here is "parity unpinned"; see the tests for the pin of each function.
 """

@@ -267,7 +267,14 @@ __device__ __forceinline__ void topk_pick(const uint32_t* hist, int32_t S, uint3
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   uint32_t cnt = 0, incl = 0;
   if (t < 256) {
-    for (int32_t s = 0; s < S; ++s) cnt += hist[(int64_t)s * 256 + 255 - t];
+    // S published histograms, written by other workgroups (other XCDs): 16 independent loads in flight at a time
+    for (int32_t s0 = 0; s0 < S; s0 += 16) {
+      uint32_t v[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = s0 + j < S ? hist[(int64_t)(s0 + j) * 256 + 255 - t] : 0u;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) cnt += v[j];
+    }
     incl = cnt;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -384,10 +391,12 @@ __global__ __launch_bounds__(1024) void topk_write_kernel(const uint16_t* __rest
   topk_keys(r.row, topk_vec(scores, score_stride), width, key);
   const uint32_t T = r.sel[0], n_above = r.sel[1], n_ties = (uint32_t)k - n_above;
   uint32_t run_gt = 0, run_eq = 0;  // the counts of the segments before this one (ties may pass 16 bits here)
-  for (int32_t s = 0; s < (int32_t)blockIdx.x; ++s) {
-    const uint32_t c = r.counts[s];
-    run_gt += c & 0xffffu;
-    run_eq += c >> 16;
+  for (int32_t s0 = 0; s0 < (int32_t)blockIdx.x; s0 += 16) {
+    uint32_t c[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) c[j] = s0 + j < (int32_t)blockIdx.x ? r.counts[s0 + j] : 0u;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) run_gt += c[j] & 0xffffu, run_eq += c[j] >> 16;
   }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int32_t e = blockIdx.x * kTopkSeg + 8 * tid;

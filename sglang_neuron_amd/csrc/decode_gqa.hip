@@ -1,5 +1,5 @@
 // GQA paged decode: split-K online softmax over the block table with MFMA for QK^T and PV. The workgroup of a
-// row's first split also attends the step's own token in-band and stores it into the pool. A row with one split
+// row's last split also attends the step's own token in-band and stores it into the pool. A row with one split
 // writes its final output; otherwise a combine pass merges the splits and adds the sink.
 //
 // Work: one workgroup of 4 waves per (sequence, split, KV head). A wave takes 32-key tiles round-robin, loading the
@@ -305,9 +305,11 @@ void gqa_decode_kernel(GqaArgs a) {
     }
   }
 
-  // ---- the step's own token, attended in-band by the row's first split (and stored) ----
+  // ---- the step's own token, attended in-band by the row's last split (and stored) ----
+  // The last split is the row's shortest: the own token's dependent loads and its store then delay a workgroup that
+  // finishes early rather than one of the row's full-length splits.
   __shared__ float sm_kn[D], sm_vn[D], sm_sn[16];
-  const bool own = split == 0;  // uniform
+  const bool own = split == splits_of<32>(L, a.window, a.split_tiles) - 1;  // uniform
   if (own) {
     if (tid < D) {
       const int64_t src = ((int64_t)b * a.G + g) * D + tid;

@@ -1,7 +1,7 @@
 // Absorbed-MLA decode (paged, per-token FP8 scale) and DSA sparse decode (index lists over 640-byte packed rows):
 // split-K online softmax with all 16 heads of a head group in one wave, MFMA for QK^T and PV. The workgroup of a
-// row's first split also attends the row's own new token in-band (and, paged, stores it). A row with one split
-// writes its final output; otherwise a combine pass merges the splits.
+// row's last split (paged; sparse: its first) also attends the row's own new token in-band (and, paged, stores it).
+// A row with one split writes its final output; otherwise a combine pass merges the splits.
 //
 // Row formats:
 //   ROWS576  [latent 512 | k_pe 64] e4m3fn, one fp32 dequantization scale per token slot (row_scale).
@@ -13,7 +13,8 @@
 // registers. Paged: a tile is 16 consecutive slots of one page (the page size is a multiple of 16), one contiguous
 // 9 KB run of HBM; the split's block-table entries sit in two VGPRs and a tile's page is a readlane. Sparse: the
 // workgroup first resolves every index of its split to a row id in LDS (index -> block -> row). The own row is
-// quantized as the store quantizes it and attended as a one-key tile by one wave of the row's first split.
+// quantized as the store quantizes it and attended as a one-key tile by one wave of the row's last split (paged) or
+// first split (sparse).
 //
 // Lane roles (lane = 16 * g4 + li), 16-key tiles; slot i of a tile (a row of S^T, a K index of PV) holds key
 // key_of(i): the even keys in slots 0 .. 7, the odd ones in 8 .. 15.
@@ -274,11 +275,14 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
     }
     sm_q[s][ln] = w;
   }
-  // The own row is attended by one wave of the row's first split (the wave with the fewest tiles) before its tiles,
-  // while their first loads are in flight. Its bf16 elements 8 lane .. + 7 and 8 (lane + 64) .. + 7 (lane < 8) and
-  // its pool slot load here, with the compiler's other prologue loads.
+  // The own row is attended by one wave (the one with the fewest tiles) before its tiles, while their first loads are
+  // in flight. Paged, that is a wave of the row's last split: the row's shortest, so the own row's quantization (a
+  // few microseconds of one wave that its workgroup waits for) lands on a workgroup that finishes early. Sparse rows
+  // split evenly, and split 0 takes it (measured faster there). Its bf16 elements 8 lane .. + 7 and
+  // 8 (lane + 64) .. + 7 (lane < 8) and its pool slot load here, with the compiler's other prologue loads.
   const int32_t ntiles = t_last - t_first;
-  const bool own_wave = split == 0 && wave == ((ntiles % WAVES) == 0 ? WAVES - 1 : ntiles % WAVES);
+  const int32_t own_split = (!SPARSE && khi > 0) ? ((khi + 15) / 16 - 1) / a.split_tiles : 0;
+  const bool own_wave = split == own_split && wave == ((ntiles % WAVES) == 0 ? WAVES - 1 : ntiles % WAVES);
   uint4 own0 = make_uint4(0, 0, 0, 0), own1 = make_uint4(0, 0, 0, 0);
   int64_t own_slot = -1;
   uint32_t own_q[4] = {0, 0, 0, 0};  // ROWS576: the quantized bytes of those elements, for the deferred pool store

@@ -281,6 +281,34 @@ void gqa_decode_kernel(GqaArgs a) {
     }
   };
 
+  // The step's own token is attended in-band by the row's last split (and stored). The last split is the row's
+  // shortest, so the own token's work delays a workgroup that finishes early rather than one of the row's
+  // full-length splits. Its operands (k, v, the slot and the query elements the score needs) load here, with the
+  // prologue's loads, so that nothing after the tile loop waits for memory.
+  const bool own = split == splits_of<32>(L, a.window, a.split_tiles) - 1;  // uniform
+  constexpr int OWN_J = (16 + WAVES - 1) / WAVES;  // query heads per wave in the own token's score
+  uint32_t own_kb = 0, own_vb = 0;
+  int64_t own_dst = -1;
+  float own_q[OWN_J][D / 64];
+  if (own) {
+    if (tid < D) {
+      const int64_t src = ((int64_t)b * a.G + g) * D + tid;
+      own_kb = a.k_new[src];
+      own_vb = a.v_new[src];
+      if (a.new_slots) {
+        const int64_t slot = redirect_slot(a.new_slots[b], a.num_blocks * a.P);
+        own_dst = (((slot / a.P) * a.G + g) * a.P + slot % a.P) * D + tid;
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < OWN_J; ++jj) {
+      const int j = wave + WAVES * jj;
+      const uint16_t* qp = a.q + ((int64_t)b * a.H + g * a.group + min(j, a.group - 1)) * D;
+#pragma unroll
+      for (int v = 0; v < D / 64; ++v) own_q[jj][v] = bf16_bits_to_f32(qp[lane + 64 * v]);
+    }
+  }
+
   // ---- the tile loop: a ring of DEPTH register tiles, DEPTH - 1 of them in flight ahead of the one computed ----
   {
     Tile ring[DEPTH];
@@ -305,21 +333,13 @@ void gqa_decode_kernel(GqaArgs a) {
     }
   }
 
-  // ---- the step's own token, attended in-band by the row's last split (and stored) ----
-  // The last split is the row's shortest: the own token's dependent loads and its store then delay a workgroup that
-  // finishes early rather than one of the row's full-length splits.
+  // ---- the step's own token (operands loaded before the tile loop) ----
   __shared__ float sm_kn[D], sm_vn[D], sm_sn[16];
-  const bool own = split == splits_of<32>(L, a.window, a.split_tiles) - 1;  // uniform
   if (own) {
     if (tid < D) {
-      const int64_t src = ((int64_t)b * a.G + g) * D + tid;
-      const uint32_t kb = a.k_new[src], vb = a.v_new[src];
+      const uint32_t kb = own_kb, vb = own_vb;
+      const int64_t dst = own_dst;
       float kd, vd;
-      int64_t dst = -1;
-      if (a.new_slots) {
-        const int64_t slot = redirect_slot(a.new_slots[b], a.num_blocks * a.P);
-        dst = (((slot / a.P) * a.G + g) * a.P + slot % a.P) * D + tid;
-      }
       if constexpr (FP8) {
         const uint32_t kq = quantize_e4m3fn(kb, kscale), vq = quantize_e4m3fn(vb, vscale);
         kd = e4m3fn_to_f32(kq) * kscale;
@@ -340,11 +360,13 @@ void gqa_decode_kernel(GqaArgs a) {
       sm_vn[tid] = vd;
     }
     __syncthreads();
-    for (int j = wave; j < a.group; j += WAVES) {
-      const uint16_t* qp = a.q + ((int64_t)b * a.H + g * a.group + j) * D;
+#pragma unroll
+    for (int jj = 0; jj < OWN_J; ++jj) {
+      const int j = wave + WAVES * jj;  // uniform
+      if (j >= a.group) break;
       float s = 0.0f;
 #pragma unroll
-      for (int d = lane; d < D; d += 64) s += bf16_bits_to_f32(qp[d]) * sm_kn[d];
+      for (int v = 0; v < D / 64; ++v) s += own_q[jj][v] * sm_kn[lane + 64 * v];
 #pragma unroll
       for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
       if (lane == 0) sm_sn[j] = s * a.sm_scale * kLog2e;

@@ -111,6 +111,8 @@ int sna_kv_store_dsa(const void *rows, const int64_t *slots, int64_t n_tokens, f
  * (sequence, split) items the split-K kernel runs. Partials are kept per (row, split): the workspace holds
  * batch * max_splits of them. A plan whose rows all fit one split (max_splits <= 1) needs no workspace, because its
  * split-K kernel writes the final output and no combine pass runs. */
+#define SNA_MAX_WORK_MAP 512
+
 typedef struct {
   int32_t split_tiles;
   int32_t n_work;
@@ -121,6 +123,10 @@ typedef struct {
   int32_t empty_rows;   /* rows with no prior key (seq_len 1), or -1 when planned from a bound */
   int32_t depth;        /* GQA: tiles each wave keeps in its register ring (2: two waves per SIMD; 4: one wave per
                            SIMD with three tiles in flight). The planner picks it; splits were sized for it. */
+  int32_t work_n;       /* entries in work[] (0: the kernels locate their items from the device's seq_lens) */
+  uint32_t work[SNA_MAX_WORK_MAP]; /* a plan from host seq_lens with n_work <= SNA_MAX_WORK_MAP: item i is row
+                           work[i] >> 6, split work[i] & 63, in launch order. The decode kernels read it from their
+                           arguments and skip the device-side search over seq_lens. */
 } sna_split_plan;
 
 /* Plan a decode from host copies of seq_lens (exact) or, with host_seq_lens == NULL, from an upper bound

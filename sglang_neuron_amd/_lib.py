@@ -34,7 +34,8 @@ class SplitPlan(ctypes.Structure):
 
     _fields_ = [("split_tiles", ctypes.c_int32), ("n_work", ctypes.c_int32), ("tile", ctypes.c_int32),
                 ("target_ctas", ctypes.c_int32), ("max_splits", ctypes.c_int32), ("batch", ctypes.c_int32),
-                ("empty_rows", ctypes.c_int32), ("depth", ctypes.c_int32)]
+                ("empty_rows", ctypes.c_int32), ("depth", ctypes.c_int32), ("work_n", ctypes.c_int32),
+                ("work", ctypes.c_uint32 * 512)]
 
     def __repr__(self) -> str:
         return (f"SplitPlan(split_tiles={self.split_tiles}, n_work={self.n_work}, tile={self.tile}, "

@@ -51,6 +51,8 @@ struct GqaArgs {
   int32_t split_tiles;
   int32_t n_work;
   int32_t max_splits;
+  int32_t work_n;                       // entries of work (0: locate items from seq_lens)
+  uint32_t work[SNA_MAX_WORK_MAP];      // item -> row << 6 | split, from the plan
   float* ws_o;   // [B, max_splits, H, D]  unnormalized partials (V dequantized)
   float* ws_ml;  // [B, max_splits, H, 2]  reference max (log2 domain) and softmax sum
   uint16_t* out;
@@ -109,7 +111,13 @@ void gqa_decode_kernel(GqaArgs a) {
   const int g = blockIdx.y;
 
   int32_t b, split;
-  locate_work<32>(a.seq_lens, a.B, a.window, a.split_tiles, (int32_t)blockIdx.x, b, split);
+  if ((int32_t)blockIdx.x < a.work_n) {  // the plan's map, from the kernel arguments
+    const uint32_t e = a.work[blockIdx.x];
+    b = (int32_t)(e >> 6);
+    split = (int32_t)(e & 63u);
+  } else {
+    locate_work<32>(a.seq_lens, a.B, a.window, a.split_tiles, (int32_t)blockIdx.x, b, split);
+  }
   b = __builtin_amdgcn_readfirstlane(b);
   split = __builtin_amdgcn_readfirstlane(split);
   // uniform across the workgroup; a split past the plan's count (a length beyond the plan's bound) is dropped, so no
@@ -625,6 +633,8 @@ extern "C" int sna_paged_decode_gqa(const void* q, const void* k_cache, const vo
   a.split_tiles = plan->split_tiles;
   a.n_work = plan->n_work;
   a.max_splits = plan->max_splits;
+  a.work_n = plan->work_n;
+  for (int32_t i = 0; i < plan->work_n; ++i) a.work[i] = plan->work[i];
   float* ws = (float*)workspace;
   a.ws_o = need > 0 ? ws : nullptr;
   a.ws_ml = need > 0 ? ws + (int64_t)B * plan->max_splits * num_q_heads * head_dim : nullptr;

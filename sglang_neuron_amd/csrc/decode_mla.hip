@@ -56,6 +56,8 @@ struct MlaArgs {
   int64_t num_blocks;
   float sm_scale;
   int32_t split_tiles, n_work, max_splits;
+  int32_t work_n;                   // entries of work (0: locate items from seq_lens)
+  uint32_t work[SNA_MAX_WORK_MAP];  // item -> row << 6 | split, from the plan
   float* ws_o;   // [B, max_splits, H, 512]  unnormalized partials, latent-dim order
   float* ws_ml;  // [B, max_splits, H, 2]
   uint16_t* out;
@@ -223,7 +225,13 @@ __global__ __launch_bounds__(64 * WAVES) void mla_decode_kernel(MlaArgs a) {
       split = w % per;
     }
   } else {
+    if ((int32_t)blockIdx.x < a.work_n) {  // the plan's map, from the kernel arguments
+    const uint32_t e = a.work[blockIdx.x];
+    b = (int32_t)(e >> 6);
+    split = (int32_t)(e & 63u);
+  } else {
     locate_work<16>(a.seq_lens, a.B, 0, a.split_tiles, (int32_t)blockIdx.x, b, split);
+  }
   }
   b = __builtin_amdgcn_readfirstlane(b);
   split = __builtin_amdgcn_readfirstlane(split);
@@ -903,6 +911,8 @@ extern "C" int sna_mla_decode(const void* ql_nope, const void* q_pe, const void*
   a.split_tiles = plan->split_tiles;
   a.n_work = plan->n_work;
   a.max_splits = plan->max_splits;
+  a.work_n = plan->work_n;
+  for (int32_t i = 0; i < plan->work_n; ++i) a.work[i] = plan->work[i];
   a.ws_o = need > 0 ? ws : nullptr;
   a.ws_ml = need > 0 ? ws + (int64_t)B * plan->max_splits * num_heads * kLatent : nullptr;
   a.out = (uint16_t*)out;
@@ -964,6 +974,8 @@ extern "C" int sna_mla_decode_sparse(const void* q_absorbed, const void* q_pe, c
   a.split_tiles = plan->split_tiles;
   a.n_work = plan->n_work;
   a.max_splits = plan->max_splits;
+  a.work_n = plan->work_n;
+  for (int32_t i = 0; i < plan->work_n; ++i) a.work[i] = plan->work[i];
   a.ws_o = need > 0 ? ws : nullptr;
   a.ws_ml = need > 0 ? ws + (int64_t)B * plan->max_splits * num_heads * kLatent : nullptr;
   a.out = (uint16_t*)ctx_out;

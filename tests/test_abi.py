@@ -94,13 +94,19 @@ def test_plan_invariants(lib, kind, lens, window, ctas):
     if kind == _lib.KIND_MLA or p.depth == 4:  # one-round plans fit the resident target unless splits are capped
         assert p.n_work * ctas <= p.target_ctas or p.split_tiles == (2048 // 16 if kind else max(
             (max(lens) - 1 + tile - 1) // tile, 4))
+    # the item map the kernels read instead of searching seq_lens: (row, split) in launch order
+    want = [(b << 6) | sp for b, nb in enumerate(n) for sp in range(nb)]
+    if len(want) <= 512:
+        assert p.work_n == len(want) and list(p.work[:p.work_n]) == want
+    else:
+        assert p.work_n == 0
     ws = lib.sna_decode_workspace_bytes(ctypes.byref(p), 16, 512)
     assert ws == (0 if p.max_splits <= 1 else p.batch * p.max_splits * 16 * (512 + 2) * 4)
 
 
 def test_plan_from_a_bound_marks_empty_rows_unknown(lib):
     rc, p = _plan(lib, _lib.KIND_GQA, B=4, max_len=900)
-    assert rc == 0 and p.empty_rows == -1
+    assert rc == 0 and p.empty_rows == -1 and p.work_n == 0  # no map: the kernels search the device's seq_lens
 
 
 @pytest.mark.parametrize("kind,window,max_len,B", [

@@ -22,6 +22,10 @@ CASES = [
     ("fp8-page64", 2, {"B": 3, "P": 64, "lens": (50, 1500)}),
     ("cfg2-32-splits", 2, {"B": 2, "lens": (8192, 8192)}),                # the combine's second chunk of 16 splits
     ("cfg4-64-splits", 4, {"B": 2, "lens": (8000, 8192)}),                # 4 chunks, sinks
+    # the bench workloads at their full sizes (the metric's cfg2 included): same seeds, same split plans
+    ("cfg2-full", 2, {}),
+    ("cfg4-full-size", 4, {}),
+    ("cfg4-swa-full-size", 4, {"window": workloads.SWA_WINDOW}),
 ]
 
 

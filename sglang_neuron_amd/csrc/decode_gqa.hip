@@ -439,8 +439,9 @@ __global__ __launch_bounds__(64) void gqa_combine_kernel(GqaArgs a) {
   constexpr int CH = 16;
   const int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
   const int32_t S = a.max_splits;
-  const int32_t n = min(splits_of<32>(ld_const(a.seq_lens + b), a.window, a.split_tiles), S);
-  if (n == 0) return;  // a row with no prior key: the lone-token kernel writes it
+  // The first chunk of partials and every split's (m, l) load before the row's split count is known: they are
+  // bounded by the workspace's S splits per row, not by the count, so they do not wait for the seq_lens load. Entries
+  // past the count are dropped by selects.
   const int64_t row0 = (int64_t)b * S * a.H + h;
   const float* ob = a.ws_o + row0 * D + V * lane;
   const int64_t sstride = (int64_t)a.H * D;
@@ -448,13 +449,12 @@ __global__ __launch_bounds__(64) void gqa_combine_kernel(GqaArgs a) {
 #pragma unroll
   for (int k = 0; k < CH; ++k)
 #pragma unroll
-    for (int v = 0; v < V; ++v) x[k][v] = k < n ? ob[k * sstride + v] : 0.0f;
-  float m = -INFINITY, l = 0.0f;
-  if (lane < n) {
-    const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + (row0 + (int64_t)lane * a.H) * 2);
-    m = ml.x;
-    l = ml.y;
-  }
+    for (int v = 0; v < V; ++v) x[k][v] = k < S ? ob[k * sstride + v] : 0.0f;
+  float2 ml = make_float2(-INFINITY, 0.0f);
+  if (lane < S) ml = *reinterpret_cast<const float2*>(a.ws_ml + (row0 + (int64_t)lane * a.H) * 2);
+  const int32_t n = min(splits_of<32>(ld_const(a.seq_lens + b), a.window, a.split_tiles), S);
+  if (n == 0) return;  // a row with no prior key: the lone-token kernel writes it
+  const float m = lane < n ? ml.x : -INFINITY, l = lane < n ? ml.y : 0.0f;
   const float sink = a.sinks ? a.sinks[h] * kLog2e : -INFINITY;
   const float M = fmaxf(wave_max(m), sink);
   const float e = lane < n ? __builtin_amdgcn_exp2f(m - M) : 0.0f;

@@ -760,23 +760,24 @@ __global__ __launch_bounds__(128) void mla_combine_kernel(MlaArgs a) {
   constexpr bool SPARSE = FMT == ROWS640;
   constexpr int CH = 16;
   const int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int32_t n = min(SPARSE ? splits_of<16>(a.n_indices + 1, 0, a.split_tiles)
-                               : splits_of<16>(ld_const(a.seq_lens + b), 0, a.split_tiles),
-                        a.max_splits);
-  if (n == 0) return;  // a row with no prior key: the lone-row kernel writes it
-  const int64_t row0 = (int64_t)b * a.max_splits * a.H + h;
+  const int32_t S = a.max_splits;
+  // The first chunk of partials and every split's (m, l) load before the row's split count is known: they are
+  // bounded by the workspace's S splits per row, not by the count, so they do not wait for the seq_lens load. Entries
+  // past the count are dropped by selects.
+  const int64_t row0 = (int64_t)b * S * a.H + h;
   const float* ob = a.ws_o + row0 * kLatent + 256 * w + 4 * lane;
   const int64_t sstride = (int64_t)a.H * kLatent;
   float4 x[CH];
 #pragma unroll
   for (int k = 0; k < CH; ++k)
-    if (k < n) x[k] = *reinterpret_cast<const float4*>(ob + k * sstride);
-  float m = -INFINITY, l = 0.0f;
-  if (lane < n) {
-    const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + (row0 + (int64_t)lane * a.H) * 2);
-    m = ml.x;
-    l = ml.y;
-  }
+    if (k < S) x[k] = *reinterpret_cast<const float4*>(ob + k * sstride);
+  float2 ml = make_float2(-INFINITY, 0.0f);
+  if (lane < S) ml = *reinterpret_cast<const float2*>(a.ws_ml + (row0 + (int64_t)lane * a.H) * 2);
+  const int32_t n = min(SPARSE ? splits_of<16>(a.n_indices + 1, 0, a.split_tiles)
+                               : splits_of<16>(ld_const(a.seq_lens + b), 0, a.split_tiles),
+                        S);
+  if (n == 0) return;  // a row with no prior key: the lone-row kernel writes it
+  const float m = lane < n ? ml.x : -INFINITY, l = lane < n ? ml.y : 0.0f;
   const float M = wave_max(m);
   const float e = lane < n ? __builtin_amdgcn_exp2f(m - M) : 0.0f;
   const float den = wave_sum(e * l);

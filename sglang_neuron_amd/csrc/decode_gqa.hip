@@ -595,6 +595,7 @@ extern "C" int sna_paged_decode_gqa(const void* q, const void* k_cache, const vo
       plan->batch != B)
     return fail(SNA_ERR_INVALID_ARGUMENT, "paged_decode_gqa: missing or foreign split plan (made for %d rows)",
                 plan ? plan->batch : -1);
+  if (const int rc = check_work_map(plan, B, "paged_decode_gqa")) return rc;
   if (B == 0) return SNA_OK;
   const bool fp8 = cache_dtype == SNA_DTYPE_FP8_E4M3FN;
   const int64_t need = sna_decode_workspace_bytes(plan, num_q_heads, head_dim);

@@ -857,7 +857,7 @@ static int check_plan(const sna_split_plan* plan, int32_t B, const char* what) {
   if (plan->split_tiles * 16 > kMlaMaxSplitKeys)
     return fail(SNA_ERR_INVALID_ARGUMENT, "%s: a split of %d keys exceeds the kernel's %d", what,
                 plan->split_tiles * 16, kMlaMaxSplitKeys);
-  return SNA_OK;
+  return check_work_map(plan, B, what);
 }
 
 }  // namespace sna

@@ -36,6 +36,22 @@ inline int check_launch(const char* what) {
 
 inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
+// A plan's item map, checked before a kernel reads it from its arguments: at most SNA_MAX_WORK_MAP entries, no more
+// than the plan's items, every row below B and every split below the plan's count (a kernel indexes seq_lens, the
+// block table and the workspace with them).
+inline int check_work_map(const sna_split_plan* plan, int32_t B, const char* what) {
+  if (plan->work_n < 0 || plan->work_n > SNA_MAX_WORK_MAP || plan->work_n > plan->n_work)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "%s: plan item map of %d entries (n_work %d, at most %d)", what,
+                plan->work_n, plan->n_work, SNA_MAX_WORK_MAP);
+  for (int32_t i = 0; i < plan->work_n; ++i) {
+    const uint32_t e = plan->work[i];
+    if ((int64_t)(e >> 6) >= B || (int32_t)(e & 63u) >= (plan->max_splits > 1 ? plan->max_splits : 1))
+      return fail(SNA_ERR_INVALID_ARGUMENT, "%s: plan item %d names row %u split %u (B %d, max_splits %d)", what, i,
+                  e >> 6, e & 63u, B, plan->max_splits);
+  }
+  return SNA_OK;
+}
+
 // Diagnostics timer (capi.hip). When sna_diag_kernel_timing(1) has switched it on, timing_events hands a decode
 // launcher the start/stop events of its split-K kernel (phase 0) or its combine kernel (phase 1), and the launcher
 // passes them to hipExtLaunchKernelGGL, so the dispatch packet itself stamps them: no marker packet sits between

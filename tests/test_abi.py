@@ -155,6 +155,20 @@ def test_decode_entry_checks_arguments_before_touching_the_gpu(lib):
     rc = lib.sna_paged_decode_gqa(null, null, null, null, null, null, 8, 8, null, null, null, null, null, 0, 0.1, null,
                                   3, 4, 2, 128, 16, 10, 1, ctypes.byref(p), null, 0, null)
     assert rc == _lib.SNA_ERR_INVALID_ARGUMENT and b"plan" in lib.sna_last_error()
+    # a plan whose item map names a row past the batch, or more entries than the map holds
+    assert p.work_n == p.n_work > 0
+    bad = _lib.SplitPlan.from_buffer_copy(p)
+    bad.work[0] = (2 << 6) | 0
+    rc = lib.sna_paged_decode_gqa(null, null, null, null, null, null, 8, 8, null, null, null, null, null, 0, 0.1, null,
+                                  2, 4, 2, 128, 16, 10, 1, ctypes.byref(bad), null, 0, null)
+    assert rc == _lib.SNA_ERR_INVALID_ARGUMENT and b"item" in lib.sna_last_error()
+    rcm, pm = _plan(lib, _lib.KIND_MLA, [100, 200])
+    assert rcm == 0 and pm.work_n == pm.n_work
+    bad = _lib.SplitPlan.from_buffer_copy(pm)
+    bad.work_n = 513
+    rc = lib.sna_mla_decode(null, null, null, null, null, 0, 0, null, null, null, 0.1, null, 2, 16, 64, 10, 1,
+                            ctypes.byref(bad), null, 0, null)
+    assert rc == _lib.SNA_ERR_INVALID_ARGUMENT and b"item map" in lib.sna_last_error()
     # an empty batch is a no-op
     rc0, p0 = _plan(lib, _lib.KIND_GQA, B=0, max_len=0)
     assert rc0 == 0

@@ -70,6 +70,30 @@ int sna_kv_store_mha(const void *k, const void *v, const int64_t *slots, int64_t
                      const float *v_scale, void *k_cache, void *v_cache, int64_t num_blocks, int32_t num_kv_heads,
                      int32_t page_size, int32_t head_dim, int32_t cache_dtype, void *stream);
 
+/* The QKV writer after the projection: optional per-head RMSNorm of Q and K, rotate-half RoPE of Q and K, Q written
+ * out, K and V stored into the MHA pool layer as sna_kv_store_mha stores them.
+ *   qkv          [n_tokens, qkv_stride] bf16: the projection's output (bias included), heads [Q Hq | K Hkv | V Hkv]
+ *                of head_dim each (head_dim even, <= 128).
+ *   q_norm, k_norm
+ *                [head_dim] bf16 RMSNorm gammas, both or neither (NULL: no QK norm); eps as the model's.
+ *   cos, sin     [n_tokens, rope_stride] bf16, head_dim columns each (qkv_paged.py's [1, T, d] over contiguous
+ *                halves; qkv.py's caches repeat the first half, and the two forms then agree).
+ *   slots        [n_tokens] int64; out-of-pool or negative slots go to slot 0, as for sna_kv_store_mha.
+ *   q_out        [n_tokens, num_q_heads, head_dim] bf16.
+ *   k_cache, v_cache, k_scale, v_scale, num_blocks, page_size, cache_dtype
+ *                as for sna_kv_store_mha (per-KV-head scales; one per-tensor scale is all heads alike).
+ * Every rounding of the reference's torch path is kept (bf16 norm output, bf16 gamma product, bf16 RoPE products and
+ * sum); without QK norm the result is bit-exact with it. With QK norm the fp32 sum of squares runs in another order,
+ * so a value may land one bf16 step away where that moves the sum's last bit.
+ * Replaces: the torch writer of _torch_qkv_paged after its projection (ops/attention/qkv_paged.py:45-68: _rms, rope,
+ * the cache writes) and of _torch_qkv (ops/attention/qkv.py:57-85: rope, the FP8 divide-and-clamp, the writes); the
+ * projection itself (`hidden @ weights + bias`) is a plain GEMM left to the caller. */
+int sna_qkv_norm_rope_store(const void *qkv, int64_t qkv_stride, int64_t n_tokens, int32_t num_q_heads,
+                            int32_t num_kv_heads, int32_t head_dim, const void *q_norm, const void *k_norm, float eps,
+                            const void *cos, const void *sin, int64_t rope_stride, const int64_t *slots, void *q_out,
+                            void *k_cache, void *v_cache, const float *k_scale, const float *v_scale,
+                            int64_t num_blocks, int32_t page_size, int32_t cache_dtype, void *stream);
+
 /* Per-head absmax scales, s[h] = max |x[:, h, :]| / 448, or 1 for an all-zero head.
  *   x         [n_tokens, num_heads, head_dim] bf16.
  *   scale_out [num_heads] fp32.

@@ -23,5 +23,8 @@ How each function is pinned (tests/test_oracle_*.py):
            the top-k against a full sort.
   page_items the item address against the pools' tensor indexing; pack by byte loops; unpack(pack) and
            copy == unpack(pack) invariants.
+  qkv      RoPE at angle 0 is the identity and at a quarter turn the exact rotate-half; RoPE against complex
+           multiplication in float64 within its three bf16 roundings; RMSNorm of a constant-magnitude head against
+           its closed form; the writes against the pinned MHA store.
 Nothing here is "parity unpinned"; see the tests for the pin of each function.
 """

@@ -53,6 +53,8 @@ SIGNATURES = {
     "sna_version": (_I32, []),
     "sna_last_error": (ctypes.c_char_p, []),
     "sna_kv_store_mha": (_I32, [_P, _P, _P, _I64, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P]),
+    "sna_qkv_norm_rope_store": (_I32, [_P, _I64, _I64, _I32, _I32, _I32, _P, _P, ctypes.c_float, _P, _P, _I64, _P, _P,
+                                        _P, _P, _P, _P, _I64, _I32, _I32, _P]),
     "sna_absmax_workspace_bytes": (_I64, [_I64, _I32]),
     "sna_kv_absmax_scale": (_I32, [_P, _I64, _I32, _I32, _P, _P, _I64, _P]),
     "sna_kv_store_mla": (_I32, [_P, _P, _I64, _I32, _P, _P, _I64, _I32, _P]),

@@ -97,6 +97,57 @@ def kv_store_mha(k: Tensor, v: Tensor, slots: Tensor, k_cache: Tensor, v_cache: 
     _lib.check(rc, "kv_store_mha")
 
 
+def qkv_norm_rope_store(qkv: Tensor, *, cos: Tensor, sin: Tensor, num_q_heads: int, num_kv_heads: int, d_head: int,
+                        k_cache: Tensor, v_cache: Tensor, slot_mapping: Tensor, q_norm: Optional[Tensor] = None,
+                        k_norm: Optional[Tensor] = None, norm_eps: float = 1e-6, k_scale: Optional[Tensor] = None,
+                        v_scale: Optional[Tensor] = None, q_out: Optional[Tensor] = None) -> Tensor:
+    """The writer after the QKV projection: ``qkv`` [T, (q + 2 kv) * d] bf16 (the projection with its bias), per-head
+    RMSNorm of Q and K when ``q_norm`` / ``k_norm`` [d] are given, rotate-half RoPE by ``cos`` / ``sin`` [T, d] (or
+    [1, T, d]), K and V stored at ``slot_mapping`` [T] into the layer's caches [blocks, kv, page, d] (bf16, or FP8 with
+    per-KV-head ``k_scale`` / ``v_scale``). Returns Q [T, q, d] bf16; the caches are written in place.
+
+    Stands in for _torch_qkv_paged after its projection (ops/attention/qkv_paged.py:45-68) and for _torch_qkv's rope
+    and FP8 write (ops/attention/qkv.py:57-85)."""
+    dev = _on_gpu(qkv, cos, sin, k_cache, v_cache, slot_mapping, q_norm, k_norm, k_scale, v_scale, q_out)
+    nb, G, P, d = k_cache.shape
+    _need(G == num_kv_heads and d == d_head, f"caches {tuple(k_cache.shape)} for {num_kv_heads} heads of {d_head}")
+    _need(v_cache.shape == k_cache.shape and v_cache.dtype == k_cache.dtype, "K and V caches differ")
+    _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
+    width = (num_q_heads + 2 * num_kv_heads) * d_head
+    qkv = qkv.reshape(-1, qkv.shape[-1])
+    _need(qkv.dtype == torch.bfloat16 and qkv.shape[-1] == width and qkv.stride(-1) == 1,
+          f"qkv must be bf16 [T, {width}] with unit column stride")
+    T = qkv.shape[0]
+    cos = _contig(cos.reshape(-1, d_head), "cos", torch.bfloat16)
+    sin = _contig(sin.reshape(-1, d_head), "sin", torch.bfloat16)
+    _need(cos.shape[0] == T and sin.shape[0] == T, f"cos/sin need {T} rows")
+    slots = _contig(slot_mapping.reshape(-1).to(torch.int64), "slot_mapping")
+    _need(slots.numel() == T, f"{slots.numel()} slots for {T} tokens")
+    _need((q_norm is None) == (k_norm is None), "give both QK-norm gammas or neither")
+    if q_norm is not None:
+        q_norm = _contig(q_norm.reshape(-1), "q_norm", torch.bfloat16)
+        k_norm = _contig(k_norm.reshape(-1), "k_norm", torch.bfloat16)
+        _need(q_norm.numel() == d_head and k_norm.numel() == d_head, f"QK-norm gammas need {d_head} entries")
+    code = cache_dtype_code(k_cache.dtype)
+    if code == _lib.DTYPE_FP8_E4M3FN:
+        _need(k_scale is not None and v_scale is not None, "an FP8 cache needs k_scale and v_scale")
+        k_scale = _contig(k_scale.reshape(-1).float().expand(G) if k_scale.numel() == 1 else k_scale.reshape(-1).float(),
+                          "k_scale")
+        v_scale = _contig(v_scale.reshape(-1).float().expand(G) if v_scale.numel() == 1 else v_scale.reshape(-1).float(),
+                          "v_scale")
+        _need(k_scale.numel() == G and v_scale.numel() == G, f"scales need 1 or {G} entries")
+    if q_out is None:
+        q_out = torch.empty(T, num_q_heads, d_head, dtype=torch.bfloat16, device=dev)
+    _need(q_out.shape == (T, num_q_heads, d_head) and q_out.dtype == torch.bfloat16 and q_out.is_contiguous(),
+          "bad q_out tensor")
+    rc = _lib.load().sna_qkv_norm_rope_store(
+        _ptr(qkv), qkv.stride(0), T, num_q_heads, num_kv_heads, d_head, _ptr(q_norm), _ptr(k_norm), float(norm_eps),
+        _ptr(cos), _ptr(sin), cos.stride(0), _ptr(slots), _ptr(q_out), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale),
+        _ptr(v_scale), nb, P, code, _stream(dev))
+    _lib.check(rc, "qkv_norm_rope_store")
+    return q_out
+
+
 def kv_absmax_scale(x: Tensor) -> Tensor:
     """Per-head dequantization scales [H] fp32 of x [T, H, d] bf16: absmax / 448, or 1 for an all-zero head."""
     dev = _on_gpu(x)

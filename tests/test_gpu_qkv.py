@@ -1,0 +1,105 @@
+"""QKV writer parity: the HIP norm + RoPE + store kernel against the oracle (oracle/qkv.py). Without QK norm every
+byte matches; with it the fp32 sum of squares runs in another order, so a value may sit one bf16 step away (and a K
+byte one e4m3fn step away), rarely."""
+
+import math
+
+import pytest
+import torch
+
+from oracle import qkv as oqkv
+from sglang_neuron_amd import ops
+from tests.conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # name, T, Hq, Hkv, d, P, fp8, norm
+    ("qwen3-8b-fp8-norm", 300, 32, 8, 128, 16, True, True),
+    ("qwen3-8b-fp8", 300, 32, 8, 128, 16, True, False),
+    ("qwen3-0.6b-bf16-norm", 257, 16, 8, 128, 16, False, True),
+    ("gpt-oss-share-bf16", 129, 8, 1, 64, 16, False, False),
+    ("gpt-oss-share-fp8-page64", 200, 8, 1, 64, 64, True, False),
+]
+
+
+def _inputs(T, Hq, Hkv, d, P, fp8, norm, seed):
+    g = torch.Generator().manual_seed(seed)
+    qkv = (torch.randn(T, (Hq + 2 * Hkv) * d, generator=g) * 2.0).to(torch.bfloat16)
+    pos = torch.arange(T, dtype=torch.float64)[:, None] + 1000.0
+    inv = 1.0 / (1.0e6 ** (torch.arange(d // 2, dtype=torch.float64) * 2 / d))
+    ang = torch.cat([pos * inv, pos * inv], dim=-1)
+    cos, sin = ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
+    nb = (T + P - 1) // P + 2
+    slots = torch.randperm((nb - 1) * P, generator=g)[:T] + P  # distinct slots past the reserved page
+    slots[T // 3] = -1                                          # out of pool: slot 0
+    qn = (1.0 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16) if norm else None
+    kn = (1.0 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16) if norm else None
+    ks = (0.5 + torch.rand(Hkv, generator=g)) * 0.02 if fp8 else None
+    vs = (0.5 + torch.rand(Hkv, generator=g)) * 0.02 if fp8 else None
+    return qkv, cos, sin, slots, qn, kn, ks, vs, nb
+
+
+@pytest.mark.parametrize("name,T,Hq,Hkv,d,P,fp8,norm", CASES, ids=[c[0] for c in CASES])
+def test_qkv_writer_matches_oracle(name, T, Hq, Hkv, d, P, fp8, norm):
+    announce(f"qkv {name}: T={T} Hq={Hq} Hkv={Hkv} d={d} P={P} fp8={fp8} norm={norm}")
+    qkv, cos, sin, slots, qn, kn, ks, vs, nb = _inputs(T, Hq, Hkv, d, P, fp8, norm, 7)
+    dt = torch.uint8 if fp8 else torch.bfloat16
+    kc_o, vc_o = torch.zeros(nb, Hkv, P, d, dtype=dt), torch.zeros(nb, Hkv, P, d, dtype=dt)
+    q_o = oqkv.qkv_norm_rope_store(qkv, cos, sin, Hq, Hkv, d, kc_o, vc_o, slots, qn, kn, 1e-6, ks, vs)
+    dev = "cuda"
+    gdt = torch.float8_e4m3fn if fp8 else torch.bfloat16
+    kc = torch.zeros(nb, Hkv, P, d, dtype=gdt, device=dev)
+    vc = torch.zeros(nb, Hkv, P, d, dtype=gdt, device=dev)
+    q = ops.qkv_norm_rope_store(qkv.to(dev), cos=cos.to(dev), sin=sin.to(dev), num_q_heads=Hq, num_kv_heads=Hkv,
+                                d_head=d, k_cache=kc, v_cache=vc, slot_mapping=slots.to(dev),
+                                q_norm=None if qn is None else qn.to(dev), k_norm=None if kn is None else kn.to(dev),
+                                norm_eps=1e-6, k_scale=None if ks is None else ks.to(dev),
+                                v_scale=None if vs is None else vs.to(dev))
+    torch.cuda.synchronize()
+    kb = kc.cpu().view(torch.uint8) if fp8 else kc.cpu()
+    vb = vc.cpu().view(torch.uint8) if fp8 else vc.cpu()
+    assert torch.equal(vb, vc_o), "V pool differs"  # V has no norm and no rotation: always bit-exact
+    if not norm:
+        assert torch.equal(q.cpu(), q_o), "Q differs"
+        assert torch.equal(kb, kc_o), "K pool differs"
+        return
+    # with QK norm: a normed element one bf16 step away moves both rotated elements of its pair by about that step
+    # times the pair's magnitude (which the rotation keeps), on a small share of the values
+    def pair_mag(x):
+        m = (x[..., :d // 2] ** 2 + x[..., d // 2:] ** 2).sqrt()
+        return torch.cat([m, m], dim=-1)
+
+    qc, qo = q.cpu().float(), q_o.float()
+    diff = (qc - qo).abs()
+    assert bool((diff <= 2.0 ** -6 * pair_mag(qo) + 1e-30).all()), float(diff.max())
+    assert float((diff > 0).float().mean()) < 0.01
+    if fp8:
+        from oracle import fp8 as ofp8
+        kd = ofp8.dequantize(kb, ks.reshape(1, Hkv, 1, 1))
+        ko = ofp8.dequantize(kc_o, ks.reshape(1, Hkv, 1, 1))
+        # one e4m3fn step of the larger neighbour, or the rotation's one-bf16-step move rounded onto that grid
+        step = ks.reshape(1, Hkv, 1, 1) * torch.clamp(pair_mag(ko) / ks.reshape(1, Hkv, 1, 1), min=2.0 ** -6) * 2.0 ** -3
+        assert bool(((kd - ko).abs() <= step + 1e-12).all())
+        assert float((kb != kc_o).float().mean()) < 0.01
+    else:
+        kd, ko = kb.float(), kc_o.float()
+        assert bool(((kd - ko).abs() <= 2.0 ** -6 * pair_mag(ko) + 1e-30).all())
+        assert float((kb != kc_o).float().mean()) < 0.01
+
+
+def test_qkv_writer_rejects_bad_arguments():
+    dev = "cuda"
+    kc = torch.zeros(4, 2, 16, 64, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    qkv = torch.zeros(3, 8 * 64, dtype=torch.bfloat16, device=dev)
+    cs = torch.zeros(3, 64, dtype=torch.bfloat16, device=dev)
+    slots = torch.zeros(3, dtype=torch.int64, device=dev)
+    with pytest.raises(ValueError):  # one gamma without the other
+        ops.qkv_norm_rope_store(qkv, cos=cs, sin=cs, num_q_heads=4, num_kv_heads=2, d_head=64, k_cache=kc,
+                                v_cache=vc, slot_mapping=slots, q_norm=torch.ones(64, dtype=torch.bfloat16,
+                                                                                   device=dev))
+    with pytest.raises(ValueError):  # an FP8 cache without scales
+        kf = torch.zeros(4, 2, 16, 64, dtype=torch.float8_e4m3fn, device=dev)
+        ops.qkv_norm_rope_store(qkv, cos=cs, sin=cs, num_q_heads=4, num_kv_heads=2, d_head=64, k_cache=kf,
+                                v_cache=torch.zeros_like(kf), slot_mapping=slots)

@@ -16,7 +16,7 @@ One JSON line on stdout:
                 workload, timed on this host's cores.
 
 Options: --config {1,2,3,4,4swa,5} picks another workload (the default line is cfg2); --config meta times the
-device-side decode metadata (block table, window trim) instead, --config prefill the segmented prefill attention, --config indexer the DSA indexer; --all prints one line per decode workload; --gpus
+device-side decode metadata (block table, window trim) instead, --config prefill the segmented prefill attention, --config indexer the DSA indexer, --config qkv the QKV writer; --all prints one line per decode workload; --gpus
 above 1 is refused, because this build measures one GPU.
 """
 
@@ -356,6 +356,89 @@ def run_meta(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> di
 
 
 INDEXER_METRIC = "DSA indexer µs/step (scores of every cached key + top-k), FP8 index keys, 1 MI355X"
+
+
+QKV_METRIC = "QKV writer µs/step (QK RMSNorm + RoPE + FP8 K/V store of a prefill chunk), 1 MI355X"
+
+
+def run_qkv(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> dict:
+    """The writer after the QKV projection for a Qwen3-8B-shaped prefill chunk: 8192 tokens (4 x 2048), 32 query and
+    8 KV heads of 128, QK RMSNorm, RoPE, K/V stored into an FP8 pool (page 16, per-KV-head scales) at permuted slots.
+    The projection output is rotated over copies past the Infinity Cache. The roofline figure is the kernel's
+    algorithmic bytes (qkv, cos/sin, slots and gammas read; Q and the FP8 K/V written) over its time; it is HBM-bound.
+    Its time comes from torch events on the stream the kernel launches on (torch's current stream)."""
+    import torch
+
+    from sglang_neuron_amd import ops
+
+    T, Hq, Hkv, d, P = 8192, 32, 8, 128, 16
+    g = torch.Generator().manual_seed(1400)
+    width = (Hq + 2 * Hkv) * d
+    qkv_host = (torch.randn(T, width, generator=g) * 2.0).to(torch.bfloat16)
+    pos = torch.arange(T, dtype=torch.float64)[:, None] % 2048
+    inv = 1.0 / (1.0e6 ** (torch.arange(d // 2, dtype=torch.float64) * 2 / d))
+    ang = torch.cat([pos * inv, pos * inv], dim=-1)
+    cos, sin = ang.cos().to(torch.bfloat16).to(dev), ang.sin().to(torch.bfloat16).to(dev)
+    nb = T // P + 1
+    slots = (torch.randperm(T, generator=g) + P).to(dev)
+    qn = (1.0 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(dev)
+    kn = (1.0 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(dev)
+    ks = ((0.5 + torch.rand(Hkv, generator=g)) * 0.02).to(dev)
+    vs = ((0.5 + torch.rand(Hkv, generator=g)) * 0.02).to(dev)
+    kc = torch.zeros(nb, Hkv, P, d, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.zeros_like(kc)
+    q_out = torch.empty(T, Hq, d, dtype=torch.bfloat16, device=dev)
+    alg = T * width * 2 + 2 * T * d * 2 + T * 8 + 2 * d * 2 + T * Hq * d * 2 + 2 * T * Hkv * d
+    n = _copies(alg, qkv_host.numel() * 2, 16)
+    inputs = [qkv_host.to(dev) for _ in range(n)]
+    log(f"qkv: T={T} Hq={Hq} Hkv={Hkv} d={d} FP8 pool page {P}, {alg / 1e6:.1f} MB per step, {n} input copies")
+
+    def step(i):
+        ops.qkv_norm_rope_store(inputs[i % n], cos=cos, sin=sin, num_q_heads=Hq, num_kv_heads=Hkv, d_head=d,
+                                k_cache=kc, v_cache=vc, slot_mapping=slots, q_norm=qn, k_norm=kn, norm_eps=1e-6,
+                                k_scale=ks, v_scale=vs, q_out=q_out)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps_n):
+        step(i)
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) / steps_n * 1e3
+    achieved = alg / (us * 1e-6) / 1e9
+    log(f"qkv_norm_rope_store: {us:.2f} us/step ({achieved:.0f} GB/s)")
+    line = {
+        "metric": QKV_METRIC, "value": round(us, 3), "unit": "us/step", "n_gpus": 1, "steps": steps_n,
+        "warmup": warmup, "ms_per_step": round(us / 1e3, 6), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 in, fp8_e4m3fn K/V out",
+        "data": "synthetic: seeded N(0,1) projection output (torch.Generator seed 1400), permuted slots",
+        "config": {"workload": "qkv: qwen3-8b prefill chunk writer", "tokens": T, "q_heads": Hq, "kv_heads": Hkv,
+                   "head_dim": d, "page_size": P, "qk_norm": True, "kv_dtype": "fp8_e4m3fn per-KV-head scale",
+                   "input_copies": n},
+        "roofline": {"bound": "hbm", "kernel": "qkv_norm_rope_store_kernel", "achieved": round(achieved, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": _traffic("qkv"), "alg_bytes_per_launch": alg, "avg_launch_us": round(us, 3)},
+        "cpu_baseline": None,
+    }
+    if cpu:
+        from oracle import qkv as oqkv
+
+        log("CPU baseline (oracle on the host cores)")
+        qkv_c, cos_c, sin_c, slots_c = qkv_host, cos.cpu(), sin.cpu(), slots.cpu()
+        qn_c, kn_c, ks_c, vs_c = qn.cpu(), kn.cpu(), ks.cpu(), vs.cpu()
+        kc_c = torch.zeros(nb, Hkv, P, d, dtype=torch.uint8)
+        vc_c = torch.zeros_like(kc_c)
+
+        def run(rows):
+            oqkv.qkv_norm_rope_store(qkv_c[:rows], cos_c[:rows], sin_c[:rows], Hq, Hkv, d, kc_c, vc_c, slots_c[:rows],
+                                     qn_c, kn_c, 1e-6, ks_c, vs_c)
+
+        line["cpu_baseline"] = _time_rows(run, T, cpu_budget)
+        log(f"CPU baseline: {line['cpu_baseline']['value']:.0f} us/step")
+    return line
 
 
 def run_indexer(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> dict:
@@ -812,7 +895,7 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
         log(f"copy calibration: one copy of {COPY_CALIBRATION_BYTES} bytes (read) into as many (written)")
-    keys = ["1", "2", "3", "4", "4swa", "5", "meta", "prefill", "indexer", "wire"] if args.all else [args.config]
+    keys = ["1", "2", "3", "4", "4swa", "5", "meta", "prefill", "indexer", "wire", "qkv"] if args.all else [args.config]
     for k in keys:
         if k == "meta":
             line = run_meta(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
@@ -822,6 +905,8 @@ def main() -> int:
             line = run_indexer(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
         elif k == "wire":
             line = run_wire(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
+        elif k == "qkv":
+            line = run_qkv(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
         else:
             line = run_one(k, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
         print(json.dumps(line), flush=True)

@@ -36,12 +36,23 @@ __global__ __launch_bounds__(256) void kv_store_mha_kernel(const uint16_t* __res
     const uint32_t kw[4] = {kin.x, kin.y, kin.z, kin.w};
     const uint32_t vw[4] = {vin.x, vin.y, vin.z, vin.w};
     uint32_t ko[2] = {0, 0}, vo[2] = {0, 0};
+    if (rcp_scale_ok(ks) && rcp_scale_ok(vs)) {
+      const float rks = 1.0f / ks, rvs = 1.0f / vs;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t kb = (kw[i >> 1] >> ((i & 1) * 16)) & 0xffffu;
-      const uint32_t vb = (vw[i >> 1] >> ((i & 1) * 16)) & 0xffffu;
-      ko[i >> 2] |= quantize_e4m3fn(kb, ks) << ((i & 3) * 8);
-      vo[i >> 2] |= quantize_e4m3fn(vb, vs) << ((i & 3) * 8);
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t kb = (kw[i >> 1] >> ((i & 1) * 16)) & 0xffffu;
+        const uint32_t vb = (vw[i >> 1] >> ((i & 1) * 16)) & 0xffffu;
+        ko[i >> 2] |= quantize_e4m3fn_rcp(kb, ks, rks) << ((i & 3) * 8);
+        vo[i >> 2] |= quantize_e4m3fn_rcp(vb, vs, rvs) << ((i & 3) * 8);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t kb = (kw[i >> 1] >> ((i & 1) * 16)) & 0xffffu;
+        const uint32_t vb = (vw[i >> 1] >> ((i & 1) * 16)) & 0xffffu;
+        ko[i >> 2] |= quantize_e4m3fn(kb, ks) << ((i & 3) * 8);
+        vo[i >> 2] |= quantize_e4m3fn(vb, vs) << ((i & 3) * 8);
+      }
     }
     *reinterpret_cast<uint2*>(kc + dst_elem) = make_uint2(ko[0], ko[1]);
     *reinterpret_cast<uint2*>(vc + dst_elem) = make_uint2(vo[0], vo[1]);

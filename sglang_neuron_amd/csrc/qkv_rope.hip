@@ -2,10 +2,8 @@
 // Q and K, Q written out and K / V stored into the paged MHA pool (bf16, or e4m3fn with per-KV-head scales), in one
 // pass over the projection's output.
 //
-// Work: one wave per (token, head) unit, heads ordered [Q 0 .. Hq) [K 0 .. Hkv) [V 0 .. Hkv) as the fused projection
-// lays them out. Lane l < d / 2 holds the rotate-half pair (l, l + d / 2), so RoPE needs no exchange and the norm's
-// sum of squares is one wave reduction. Every rounding step of the reference's torch path is kept: the norm rounds
-// x * rsqrt(mean + eps) to bf16 and multiplies by the bf16 gamma with a bf16 result; RoPE rounds each product and the
+// Heads are ordered [Q 0 .. Hq) [K 0 .. Hkv) [V 0 .. Hkv) as the fused projection lays them out. Every rounding step
+// of the reference's torch path is kept: the norm rounds x * rsqrt(mean + eps) to bf16 and multiplies by the bf16 gamma with a bf16 result; RoPE rounds each product and the
 // sum to bf16. The sum of squares is fp32 in a wave-reduction order, so with the norm on a value can differ from the
 // reference's by one bf16 step where that order changes the sum's last bit; without the norm the path is bit-exact.
 #include "sna_device.h"
@@ -13,71 +11,125 @@
 
 namespace sna {
 
-__device__ __forceinline__ float bf16_round(float x) { return bf16_bits_to_f32(f32_to_bf16_bits(x)); }
+// x rounded to bf16 (nearest even) and back, by the hardware conversion (v_cvt_pk_bf16_f32). It equals
+// f32_to_bf16_bits for every non-NaN input; a NaN stays a NaN, and the final conversion of each output writes the
+// canonical NaN, as torch does.
+__device__ __forceinline__ float bf16_round(float x) { return (float)(__bf16)x; }
 
-template <bool FP8>
+// Lane layout: a head row of D bf16 is D / 8 lanes of 16 bytes (LPH lanes per head, 64 / LPH heads per wave), so
+// every load and store is a 16-byte vector access. Lane j of a head holds elements 8 j .. 8 j + 7; its rotate-half
+// partner (the lane LPH / 2 away) holds the elements D / 2 further on, fetched by one xor shuffle per dword. A unit is
+// (token, a wave's worth of consecutive heads); a head's type (Q, K, V) is fixed per LPH-lane group.
+template <bool FP8, int D>
 __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
-    const uint16_t* __restrict__ qkv, int64_t qkv_stride, int64_t n_tokens, int32_t Hq, int32_t Hkv, int32_t D,
+    const uint16_t* __restrict__ qkv, int64_t qkv_stride, int64_t n_tokens, int32_t Hq, int32_t Hkv,
     const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm, float eps,
     const uint16_t* __restrict__ cosv, const uint16_t* __restrict__ sinv, int64_t rope_stride,
     const int64_t* __restrict__ slots, uint16_t* __restrict__ q_out, uint8_t* __restrict__ kc,
     uint8_t* __restrict__ vc, const float* __restrict__ k_scale, const float* __restrict__ v_scale,
     int64_t num_slots, int32_t P) {
-  const int lane = threadIdx.x & 63;
+  constexpr int LPH = D / 8, HPW = 64 / LPH, HALF = LPH / 2;
+  const int lane = threadIdx.x & 63, sub = lane % LPH;
   const int32_t heads = Hq + 2 * Hkv;
-  const int64_t units = n_tokens * heads;
-  const int32_t half = D / 2;
-  const bool live = lane < half;
-  for (int64_t u = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); u < units; u += (int64_t)gridDim.x * 4) {
-    const int64_t t = u / heads;
-    const int32_t head = (int32_t)(u % heads);  // uniform per wave
-    const uint16_t* src = qkv + t * qkv_stride + (int64_t)head * D;
-    float x0 = live ? bf16_bits_to_f32(src[lane]) : 0.0f;
-    float x1 = live ? bf16_bits_to_f32(src[lane + half]) : 0.0f;
-    if (head < Hq + Hkv) {
-      const bool is_q = head < Hq;
-      const uint16_t* gamma = is_q ? q_norm : k_norm;
-      if (gamma) {
-        // _rms: gamma * (x32 * rsqrt(mean(x32^2) + eps)).to(bf16), rsqrt as 1 / sqrt (both correctly rounded)
-        const float ss = wave_sum(x0 * x0 + x1 * x1);
-        const float inv = 1.0f / __fsqrt_rn(ss / (float)D + eps);
-        if (live) {
-          x0 = bf16_round(bf16_bits_to_f32(gamma[lane]) * bf16_round(x0 * inv));
-          x1 = bf16_round(bf16_bits_to_f32(gamma[lane + half]) * bf16_round(x1 * inv));
-        }
-      }
-      if (!live) continue;
-      // rope(t) = t * c + cat(-t[half:], t[:half]) * s, every product and the sum rounded to bf16
-      const uint16_t* cr = cosv + t * rope_stride;
-      const uint16_t* sr = sinv + t * rope_stride;
-      const float c0 = bf16_bits_to_f32(cr[lane]), c1 = bf16_bits_to_f32(cr[lane + half]);
-      const float s0 = bf16_bits_to_f32(sr[lane]), s1 = bf16_bits_to_f32(sr[lane + half]);
-      const float y0 = bf16_round(bf16_round(x0 * c0) + bf16_round(-x1 * s0));
-      const float y1 = bf16_round(bf16_round(x1 * c1) + bf16_round(x0 * s1));
-      if (is_q) {
-        uint16_t* dst = q_out + (t * Hq + head) * D;
-        dst[lane] = (uint16_t)f32_to_bf16_bits(y0);
-        dst[lane + half] = (uint16_t)f32_to_bf16_bits(y1);
-        continue;
-      }
-      x0 = y0;
-      x1 = y1;
+  const int32_t groups = (heads + HPW - 1) / HPW;
+  const int64_t units = n_tokens * groups;
+  const bool first = sub < HALF;
+  // U units per wave per pass: the loads of all U are issued before any is computed
+  constexpr int U = 1;
+  auto process = [&](int64_t u, const uint4& w, const uint4& cw, const uint4& sw) {
+    const int64_t t = u / groups;
+    const int32_t head = (int32_t)(u % groups) * HPW + lane / LPH;
+    const bool live = u < units && head < heads;
+    const bool is_q = head < Hq, is_k = !is_q && head < Hq + Hkv;
+    float x[8];
+    {
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = bf16_bits_to_f32((ww[e >> 1] >> (16 * (e & 1))) & 0xffffu);
     }
-    if (!live) continue;
+    if (q_norm) {  // uniform: both gammas or neither
+      // _rms: gamma * (x32 * rsqrt(mean(x32^2) + eps)).to(bf16), rsqrt as 1 / sqrt (both correctly rounded); the
+      // sum of squares over the head's LPH lanes (every lane takes part in the shuffles)
+      float ss = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+#pragma unroll
+      for (int off = HALF; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+      if (live && (is_q || is_k)) {
+        const float inv = 1.0f / __fsqrt_rn(ss / (float)D + eps);
+        const uint4 gw = ld16((is_q ? q_norm : k_norm) + 8 * sub);
+        const uint32_t gg[4] = {gw.x, gw.y, gw.z, gw.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          x[e] = bf16_round(bf16_bits_to_f32((gg[e >> 1] >> (16 * (e & 1))) & 0xffffu) * bf16_round(x[e] * inv));
+      }
+    }
+    // the partner's elements (every lane takes part in the shuffles)
+    uint32_t pw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      pw[e] = (uint32_t)__shfl_xor((int)(f32_to_bf16_bits(x[2 * e]) | (f32_to_bf16_bits(x[2 * e + 1]) << 16)), HALF,
+                                   64);
+    if (!live) return;
+    if (is_q || is_k) {
+      // rope(t) = t * c + cat(-t[D/2:], t[:D/2]) * s, every product and the sum rounded to bf16
+      const uint32_t cc[4] = {cw.x, cw.y, cw.z, cw.w}, sc[4] = {sw.x, sw.y, sw.z, sw.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float c = bf16_bits_to_f32((cc[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+        const float sn = bf16_bits_to_f32((sc[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+        const float p = bf16_bits_to_f32((pw[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+        x[e] = bf16_round(bf16_round(x[e] * c) + bf16_round((first ? -p : p) * sn));
+      }
+    }
+    uint32_t ob[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ob[e] = f32_to_bf16_bits(x[2 * e]) | (f32_to_bf16_bits(x[2 * e + 1]) << 16);
+    if (is_q) {
+      *reinterpret_cast<uint4*>(q_out + (t * Hq + head) * D + 8 * sub) = make_uint4(ob[0], ob[1], ob[2], ob[3]);
+      return;
+    }
     // K (rotated) or V into the pool at the token's slot, as the MHA store writes it
-    const bool is_k = head < Hq + Hkv;
     const int32_t h = head - Hq - (is_k ? 0 : Hkv);
     const int64_t slot = redirect_slot(slots[t], num_slots);
-    const int64_t dst = (((slot / P) * Hkv + h) * P + slot % P) * D + lane;
+    const int64_t dst = (((slot / P) * Hkv + h) * P + slot % P) * D + 8 * sub;
     uint8_t* cache = is_k ? kc : vc;
     if constexpr (FP8) {
-      const float s = is_k ? k_scale[h] : v_scale[h];
-      cache[dst] = (uint8_t)quantize_e4m3fn(f32_to_bf16_bits(x0), s);
-      cache[dst + half] = (uint8_t)quantize_e4m3fn(f32_to_bf16_bits(x1), s);
+      const float scl = is_k ? k_scale[h] : v_scale[h];
+      uint32_t q8[2] = {0, 0};
+      if (rcp_scale_ok(scl)) {
+        const float rs = 1.0f / scl;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          q8[e >> 2] |= quantize_e4m3fn_rcp((ob[e >> 1] >> (16 * (e & 1))) & 0xffffu, scl, rs) << (8 * (e & 3));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          q8[e >> 2] |= quantize_e4m3fn((ob[e >> 1] >> (16 * (e & 1))) & 0xffffu, scl) << (8 * (e & 3));
+      }
+      *reinterpret_cast<uint2*>(cache + dst) = make_uint2(q8[0], q8[1]);
     } else {
-      reinterpret_cast<uint16_t*>(cache)[dst] = (uint16_t)f32_to_bf16_bits(x0);
-      reinterpret_cast<uint16_t*>(cache)[dst + half] = (uint16_t)f32_to_bf16_bits(x1);
+      *reinterpret_cast<uint4*>(cache + 2 * dst) = make_uint4(ob[0], ob[1], ob[2], ob[3]);
     }
+  };
+  const int64_t stride = (int64_t)gridDim.x * 4 * U;
+  for (int64_t base = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * U; base < units; base += stride) {
+    uint4 w[U], cw[U], sw[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int64_t u = base + k;
+      const int64_t t = u / groups;
+      const int32_t head = (int32_t)(u % groups) * HPW + lane / LPH;
+      const bool live = u < units && head < heads;
+      w[k] = live ? ld16(qkv + t * qkv_stride + (int64_t)head * D + 8 * sub) : make_uint4(0, 0, 0, 0);
+      cw[k] = sw[k] = make_uint4(0, 0, 0, 0);
+      if (live && head < Hq + Hkv) {
+        cw[k] = ld16(cosv + t * rope_stride + 8 * sub);
+        sw[k] = ld16(sinv + t * rope_stride + 8 * sub);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) process(base + k, w[k], cw[k], sw[k]);
   }
 }
 
@@ -92,12 +144,12 @@ extern "C" int sna_qkv_norm_rope_store(const void* qkv, int64_t qkv_stride, int6
                                        void* v_cache, const float* k_scale, const float* v_scale, int64_t num_blocks,
                                        int32_t page_size, int32_t cache_dtype, void* stream) {
   ApiGuard guard;
-  if (n_tokens < 0 || num_q_heads < 1 || num_kv_heads < 1 || head_dim < 2 || head_dim > 128 || head_dim % 2 ||
-      page_size < 1 || num_blocks < 1)
+  if (n_tokens < 0 || num_q_heads < 1 || num_kv_heads < 1 || page_size < 1 || num_blocks < 1)
     return fail(SNA_ERR_INVALID_ARGUMENT,
-                "qkv_norm_rope_store: bad sizes (tokens %lld, heads %d/%d, head_dim %d (even, <= 128), page %d, "
-                "blocks %lld)",
+                "qkv_norm_rope_store: bad sizes (tokens %lld, heads %d/%d, head_dim %d, page %d, blocks %lld)",
                 (long long)n_tokens, num_q_heads, num_kv_heads, head_dim, page_size, (long long)num_blocks);
+  if (head_dim != 64 && head_dim != 128)
+    return fail(SNA_ERR_UNSUPPORTED, "qkv_norm_rope_store: head_dim %d (64 or 128 are built)", head_dim);
   if (qkv_stride < (int64_t)(num_q_heads + 2 * num_kv_heads) * head_dim || rope_stride < head_dim)
     return fail(SNA_ERR_INVALID_ARGUMENT, "qkv_norm_rope_store: row strides %lld / %lld are shorter than a row",
                 (long long)qkv_stride, (long long)rope_stride);
@@ -110,21 +162,24 @@ extern "C" int sna_qkv_norm_rope_store(const void* qkv, int64_t qkv_stride, int6
   if (!qkv || !cos || !sin || !slots || !q_out || !k_cache || !v_cache || (fp8 && (!k_scale || !v_scale)))
     return fail(SNA_ERR_INVALID_ARGUMENT, "qkv_norm_rope_store: null pointer");
   if (!(eps >= 0.0f)) return fail(SNA_ERR_INVALID_ARGUMENT, "qkv_norm_rope_store: eps %g", (double)eps);
-  const int64_t units = n_tokens * (num_q_heads + 2 * num_kv_heads);
-  const unsigned grid = (unsigned)std::min<int64_t>((units + 3) / 4, 65536);
+  if (!aligned(qkv, 16) || qkv_stride % 8 || !aligned(cos, 16) || !aligned(sin, 16) || rope_stride % 8 ||
+      !aligned(q_out, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || (q_norm && (!aligned(q_norm, 16) ||
+      !aligned(k_norm, 16))))
+    return fail(SNA_ERR_INVALID_ARGUMENT, "qkv_norm_rope_store: tensors and row strides must be 16-byte aligned");
+  const int32_t hpw = 64 / (head_dim / 8);
+  const int64_t units = n_tokens * ((num_q_heads + 2 * num_kv_heads + hpw - 1) / hpw);
+  const unsigned grid = (unsigned)std::min<int64_t>((units + 4 * 1 - 1) / (4 * 1), (int64_t)1 << 22);  // 4 waves x U
   const int64_t num_slots = num_blocks * page_size;
   hipStream_t s = (hipStream_t)stream;
-  if (fp8)
-    hipLaunchKernelGGL(qkv_norm_rope_store_kernel<true>, dim3(grid), dim3(256), 0, s, (const uint16_t*)qkv,
-                       qkv_stride, n_tokens, num_q_heads, num_kv_heads, head_dim, (const uint16_t*)q_norm,
-                       (const uint16_t*)k_norm, eps, (const uint16_t*)cos, (const uint16_t*)sin, rope_stride, slots,
-                       (uint16_t*)q_out, (uint8_t*)k_cache, (uint8_t*)v_cache, k_scale, v_scale, num_slots,
-                       page_size);
-  else
-    hipLaunchKernelGGL(qkv_norm_rope_store_kernel<false>, dim3(grid), dim3(256), 0, s, (const uint16_t*)qkv,
-                       qkv_stride, n_tokens, num_q_heads, num_kv_heads, head_dim, (const uint16_t*)q_norm,
-                       (const uint16_t*)k_norm, eps, (const uint16_t*)cos, (const uint16_t*)sin, rope_stride, slots,
-                       (uint16_t*)q_out, (uint8_t*)k_cache, (uint8_t*)v_cache, k_scale, v_scale, num_slots,
-                       page_size);
+#define SNA_QKV_LAUNCH(F, DD)                                                                                   \
+  hipLaunchKernelGGL((qkv_norm_rope_store_kernel<F, DD>), dim3(grid), dim3(256), 0, s, (const uint16_t*)qkv,     \
+                     qkv_stride, n_tokens, num_q_heads, num_kv_heads, (const uint16_t*)q_norm,                   \
+                     (const uint16_t*)k_norm, eps, (const uint16_t*)cos, (const uint16_t*)sin, rope_stride, slots, \
+                     (uint16_t*)q_out, (uint8_t*)k_cache, (uint8_t*)v_cache, k_scale, v_scale, num_slots, page_size)
+  if (fp8 && head_dim == 128) SNA_QKV_LAUNCH(true, 128);
+  else if (fp8) SNA_QKV_LAUNCH(true, 64);
+  else if (head_dim == 128) SNA_QKV_LAUNCH(false, 128);
+  else SNA_QKV_LAUNCH(false, 64);
+#undef SNA_QKV_LAUNCH
   return check_launch("qkv_norm_rope_store");
 }

@@ -88,6 +88,31 @@ __device__ __forceinline__ uint32_t quantize_e4m3fn(uint32_t bf16_bits, float s)
   return f32_to_e4m3fn(clamp_fp8(bf16_bits_to_f32(bf16_bits) / s));
 }
 
+// The same quantizer without a division per element or branches, for a scale s whose correctly rounded reciprocal rs
+// = 1 / s the caller computes once (s positive and normal; otherwise use quantize_e4m3fn). |x| / s is q0 = |x| * rs,
+// within an ulp, corrected once by its exact FMA residual (Markstein's sequence, which yields the correctly rounded
+// quotient from a correctly rounded reciprocal); an overflowing q0 (|x| infinite or the quotient past the float range)
+// stands for itself, since the clamp maps it to 448 like the exact quotient. The sign goes on last, so -0 stays -0.
+// Both e4m3fn encodings (subnormal, normal) are computed and one is selected.
+__device__ __forceinline__ uint32_t quantize_e4m3fn_rcp(uint32_t bf16_bits, float s, float rs) {
+  const float x = bf16_bits_to_f32(bf16_bits);
+  const float a = fabsf(x);
+  const float q0 = a * rs;
+  const float q1 = q0 == __builtin_inff() ? q0 : fmaf(fmaf(-q0, s, a), rs, q0);
+  const float y = clamp_fp8(copysignf(q1, x));
+  const uint32_t u = __float_as_uint(y);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t m = u & 0x7fffffffu;
+  const uint32_t sub = (uint32_t)__builtin_rintf(__uint_as_float(m) * 512.0f);
+  const uint32_t nrm = ((m + 0x7ffffu + ((m >> 20) & 1u)) >> 20) - 960u;
+  uint32_t r = m < 0x3c800000u ? sub : nrm;
+  r = (m > 0x7f800000u || r > 0x7eu) ? 0x7fu : r;
+  return sign | r;
+}
+
+// Whether quantize_e4m3fn_rcp serves the scale s (a positive normal float).
+__device__ __forceinline__ bool rcp_scale_ok(float s) { return s >= 1.17549435e-38f && s <= 3.40282347e+38f; }
+
 // The scale rule for per-head and per-token scales: absmax / 448, or 1 for an all-zero operand (whose bytes are then
 // all zero), so no division by zero can happen.
 __device__ __forceinline__ float scale_from_absmax(float amax) { return amax > 0.0f ? amax / kFp8Max : 1.0f; }

@@ -23,7 +23,8 @@ def test_fp8_conversion_instruction_exact():
     assert bool(torch.isnan(got[~finite]).all())
 
 
-@pytest.mark.parametrize("scales", [(1.0, 1.0, 1.0, 1.0), (2 ** -6, 0.5, 1 / 448, 0.0123)])
+@pytest.mark.parametrize("scales", [(1.0, 1.0, 1.0, 1.0), (2 ** -6, 0.5, 1 / 448, 0.0123),
+                                    (0.0173, 3.3e-3, 0.771, 1.7e-4), (0.02931, 5.5, 1 / 3, 6.1e-5)])
 def test_mha_store_every_bf16_pattern(scales):
     announce(f"kv_store_mha all bf16 patterns scales={scales}")
     G, d, P = 4, 128, 16

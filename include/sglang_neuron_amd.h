@@ -73,7 +73,7 @@ int sna_kv_store_mha(const void *k, const void *v, const int64_t *slots, int64_t
 /* The QKV writer after the projection: optional per-head RMSNorm of Q and K, rotate-half RoPE of Q and K, Q written
  * out, K and V stored into the MHA pool layer as sna_kv_store_mha stores them.
  *   qkv          [n_tokens, qkv_stride] bf16: the projection's output (bias included), heads [Q Hq | K Hkv | V Hkv]
- *                of head_dim each (head_dim even, <= 128).
+ *                of head_dim each (64 or 128). Tensors and row strides 16-byte aligned.
  *   q_norm, k_norm
  *                [head_dim] bf16 RMSNorm gammas, both or neither (NULL: no QK norm); eps as the model's.
  *   cos, sin     [n_tokens, rope_stride] bf16, head_dim columns each (qkv_paged.py's [1, T, d] over contiguous

@@ -16,6 +16,21 @@ namespace sna {
 // canonical NaN, as torch does.
 __device__ __forceinline__ float bf16_round(float x) { return (float)(__bf16)x; }
 
+// Two floats that are already bf16 values, packed (lo in the low half) by one byte permute.
+__device__ __forceinline__ uint32_t pack_exact(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// Two floats rounded to bf16 (nearest even) and packed by one conversion, each NaN written as the canonical 0x7FC0
+// (f32_to_bf16_bits' and torch's NaN).
+__device__ __forceinline__ uint32_t round_pack(float lo, float hi) {
+  const bf16x2_t v = __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t);
+  uint32_t r = __builtin_bit_cast(uint32_t, v);
+  if (lo != lo) r = (r & 0xffff0000u) | 0x7fc0u;
+  if (hi != hi) r = (r & 0x0000ffffu) | 0x7fc00000u;
+  return r;
+}
+
 // Lane layout: a head row of D bf16 is D / 8 lanes of 16 bytes (LPH lanes per head, 64 / LPH heads per wave), so
 // every load and store is a 16-byte vector access. Lane j of a head holds elements 8 j .. 8 j + 7; its rotate-half
 // partner (the lane LPH / 2 away) holds the elements D / 2 further on, fetched by one xor shuffle per dword. A unit is
@@ -68,23 +83,30 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
     uint32_t pw[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      pw[e] = (uint32_t)__shfl_xor((int)(f32_to_bf16_bits(x[2 * e]) | (f32_to_bf16_bits(x[2 * e + 1]) << 16)), HALF,
-                                   64);
+      pw[e] = (uint32_t)__shfl_xor((int)pack_exact(x[2 * e], x[2 * e + 1]), HALF, 64);
     if (!live) return;
+    uint32_t ob[4];
     if (is_q || is_k) {
-      // rope(t) = t * c + cat(-t[D/2:], t[:D/2]) * s, every product and the sum rounded to bf16
+      // rope(t) = t * c + cat(-t[D/2:], t[:D/2]) * s, every product and the sum rounded to bf16 (the sums by the
+      // packing conversion)
       const uint32_t cc[4] = {cw.x, cw.y, cw.z, cw.w}, sc[4] = {sw.x, sw.y, sw.z, sw.w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float c = bf16_bits_to_f32((cc[e >> 1] >> (16 * (e & 1))) & 0xffffu);
-        const float sn = bf16_bits_to_f32((sc[e >> 1] >> (16 * (e & 1))) & 0xffffu);
-        const float p = bf16_bits_to_f32((pw[e >> 1] >> (16 * (e & 1))) & 0xffffu);
-        x[e] = bf16_round(bf16_round(x[e] * c) + bf16_round((first ? -p : p) * sn));
-      }
-    }
-    uint32_t ob[4];
+      for (int e2 = 0; e2 < 4; ++e2) {
+        float y[2];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) ob[e] = f32_to_bf16_bits(x[2 * e]) | (f32_to_bf16_bits(x[2 * e + 1]) << 16);
+        for (int i = 0; i < 2; ++i) {
+          const int e = 2 * e2 + i;
+          const float c = bf16_bits_to_f32((cc[e2] >> (16 * i)) & 0xffffu);
+          const float sn = bf16_bits_to_f32((sc[e2] >> (16 * i)) & 0xffffu);
+          const float p = bf16_bits_to_f32((pw[e2] >> (16 * i)) & 0xffffu);
+          y[i] = bf16_round(x[e] * c) + bf16_round((first ? -p : p) * sn);
+        }
+        ob[e2] = round_pack(y[0], y[1]);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ob[e] = pack_exact(x[2 * e], x[2 * e + 1]);
+    }
     if (is_q) {
       *reinterpret_cast<uint4*>(q_out + (t * Hq + head) * D + 8 * sub) = make_uint4(ob[0], ob[1], ob[2], ob[3]);
       return;

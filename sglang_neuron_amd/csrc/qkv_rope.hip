@@ -21,6 +21,30 @@ __device__ __forceinline__ uint32_t pack_exact(float lo, float hi) {
   return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
+// The value of the lane `half` lanes away inside the head's lane group (lane ^ half). A 16-lane group (D = 128) is one
+// DPP row, where a rotation by 8 is that exchange; other widths go through the LDS crossbar.
+template <int HALF>
+__device__ __forceinline__ uint32_t partner(uint32_t v) {
+  if constexpr (HALF == 8) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, false);  // row_ror:8
+  else return (uint32_t)__shfl_xor((int)v, HALF, 64);
+}
+
+// The sum over the head's lane group, in every lane of it: DPP row rotations for a 16-lane group, xor shuffles else.
+template <int HALF>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (HALF == 8) {
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false));  // row_ror:8
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xf, 0xf, false));  // row_ror:4
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x122, 0xf, 0xf, false));  // row_ror:2
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x121, 0xf, 0xf, false));  // row_ror:1
+    return v;
+  } else {
+#pragma unroll
+    for (int off = HALF; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+  }
+}
+
 // Two floats rounded to bf16 (nearest even) and packed by one conversion, each NaN written as the canonical 0x7FC0
 // (f32_to_bf16_bits' and torch's NaN).
 __device__ __forceinline__ uint32_t round_pack(float lo, float hi) {
@@ -68,8 +92,7 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
       float ss = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
-#pragma unroll
-      for (int off = HALF; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+      ss = group_sum<HALF>(ss);
       if (live && (is_q || is_k)) {
         const float inv = 1.0f / __fsqrt_rn(ss / (float)D + eps);
         const uint4 gw = ld16((is_q ? q_norm : k_norm) + 8 * sub);
@@ -83,7 +106,7 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
     uint32_t pw[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      pw[e] = (uint32_t)__shfl_xor((int)pack_exact(x[2 * e], x[2 * e + 1]), HALF, 64);
+      pw[e] = partner<HALF>(pack_exact(x[2 * e], x[2 * e + 1]));
     if (!live) return;
     uint32_t ob[4];
     if (is_q || is_k) {

@@ -879,7 +879,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: this build runs no collectives (asked for {max(args.gpus, world)} GPUs). "
-              "The single-GPU number is the per-GPU share; see DESIGN.md for how the path shards.", file=sys.stderr)
+              "The single-GPU number is the per-GPU share (GQA would shard by KV head, MLA and DSA by context).", file=sys.stderr)
         return 2
     import torch
 

@@ -163,6 +163,21 @@ typedef struct {
 int sna_plan_decode(int32_t kind, const int32_t *host_seq_lens, int32_t B, int32_t max_seq_len, int32_t window,
                     int32_t n_keys_per_row, int32_t ctas_per_item, int32_t num_cus, sna_split_plan *plan);
 
+/* Host check of one decode batch's operands, before any launch (host copies of every array):
+ *   seq_lens     [B] int64, prefix plus the new token: each in [1, INT32_MAX] (positions are int32 in the kernels).
+ *   block_table  [B, table_stride] int32, table_width valid columns: a row's ceil(seq_len / page_size) pages must fit
+ *                the table and name pages inside the pool [0, num_blocks) (a -1 inside a row would drop its keys).
+ *   new_slots    [B] int64 or NULL: a live row's slot (one off the reserved page 0 and inside the pool; the others are
+ *                padding writes, redirected to slot 0) sits at the row's position in its page, slot % page ==
+ *                (seq_len - 1) % page, on the row's last page, and no two live rows share one.
+ * Returns SNA_ERR_INVALID_ARGUMENT naming the first offending row. The decode entry points themselves check shapes
+ * only (their operands are device memory).
+ * Replaces: the refusals of decode_operands (attention/mla_operands.py:64-97: an int32 position bound, a slot that
+ * disagrees with its position, a table too narrow for the row, two live rows sharing a write slot). */
+int sna_check_decode_operands(const int64_t *seq_lens, const int32_t *block_table, int64_t table_stride,
+                              int32_t table_width, const int64_t *new_slots, int32_t B, int32_t page_size,
+                              int64_t num_blocks);
+
 /* Workspace bytes a decode with this plan needs: batch * max_splits * heads * (head_dim_v + 2) * 4, or 0 when
  * max_splits <= 1. */
 int64_t sna_decode_workspace_bytes(const sna_split_plan *plan, int32_t num_q_heads, int32_t head_dim_v);

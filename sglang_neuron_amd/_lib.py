@@ -61,6 +61,7 @@ SIGNATURES = {
     "sna_kv_store_dsa": (_I32, [_P, _P, _I64, _F32, _P, _I64, _P]),
     "sna_plan_decode": (_I32, [_I32, _P, _I32, _I32, _I32, _I32, _I32, _I32, ctypes.POINTER(SplitPlan)]),
     "sna_decode_workspace_bytes": (_I64, [ctypes.POINTER(SplitPlan), _I32, _I32]),
+    "sna_check_decode_operands": (_I32, [_P, _P, _I64, _I32, _P, _I32, _I32, _I64]),
     "sna_paged_decode_gqa": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _I32, _F32, _P, _I32,
                                     _I32, _I32, _I32, _I32, _I64, _I32, ctypes.POINTER(SplitPlan), _P, _I64, _P]),
     "sna_mla_decode": (_I32, [_P, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _F32, _P, _I32, _I32, _I32, _I64, _I32,

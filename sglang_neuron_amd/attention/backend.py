@@ -17,7 +17,6 @@ from __future__ import annotations
 from dataclasses import dataclass
 from typing import Optional
 
-import numpy as np
 import torch
 from torch import Tensor
 
@@ -61,6 +60,54 @@ class _ExtendState:
     max_q_len: int
 
 
+def _real_sizes(fb) -> tuple:
+    """(requests, tokens) of a ForwardBatch without the padding SGLang's DP attention adds on the eager path, which
+    keeps the real sizes in ``_original_batch_size`` / ``_original_num_tokens`` (attention/backend.py:86-93)."""
+    n_req = getattr(fb, "_original_batch_size", None)
+    n_tok = getattr(fb, "_original_num_tokens", None)
+    return (int(fb.batch_size) if n_req is None else int(n_req),
+            int(fb.out_cache_loc.shape[0]) if n_tok is None else int(n_tok))
+
+
+def _seq_lens_source(fb) -> Tensor:
+    """The batch's seq_lens, from its host copy when it carries one."""
+    host = getattr(fb, "seq_lens_cpu", None)
+    return fb.seq_lens if host is None else host
+
+
+def _first(t: Tensor, n: int, device) -> Tensor:
+    """The first n entries of a batch tensor as int64 on ``device``."""
+    return t[:n].to(device=device, dtype=torch.int64)
+
+
+def _idle_metadata(positions: Tensor, device) -> NeuronForwardMetadata:
+    """The metadata of an idle (or empty) batch: no rows, a (0, 1) block table of -1."""
+    none = torch.zeros((0,), dtype=torch.long, device=device)
+    return NeuronForwardMetadata(is_prefill=False, batch_size=0, num_tokens=0,
+                                 block_table=torch.full((0, 1), -1, dtype=torch.int32, device=device),
+                                 slot_mapping=none, seq_lens=none.clone(), positions=positions)
+
+
+def _need_positions_fit(seq_lens: Tensor) -> None:
+    """A decode row's length must be in [1, 2^31 - 1]: positions are int32 in the kernels (attention/mla_operands.py:
+    73)."""
+    lo, hi = int(seq_lens.min()), int(seq_lens.max())
+    if lo < 1 or hi > 2 ** 31 - 1:
+        raise ValueError(f"decode seq_lens must lie in [1, 2^31 - 1], got [{lo}, {hi}]")
+
+
+def host_block_table(req_to_token: Tensor, rows: Tensor, seq_lens: Tensor, page_size: int) -> Tensor:
+    """The decode block table on the host: [n, ceil(max seq_len / page)] int32 whose column j of row i is the page of
+    the row's token j * page (``req_to_token[rows[i], j * page] // page``) while that token lies inside the row
+    (j * page < seq_lens[i]), else -1. The reference's NeuronAttnBackend._block_table (attention/backend.py:114-130)
+    gives the same entries; ``req_to_token`` is SGLang's [rows, context] int32 map on the CPU."""
+    first_token = torch.arange(0, -(-int(seq_lens.max()) // page_size) * page_size, page_size, dtype=torch.int64)
+    slots = req_to_token.index_select(0, rows.to(torch.int64)).index_select(1, first_token)
+    table = torch.div(slots, page_size, rounding_mode="floor").to(torch.int32)
+    table.masked_fill_(first_token.unsqueeze(0) >= seq_lens.to(torch.int64).unsqueeze(1), -1)
+    return table.contiguous()
+
+
 class NeuronAttnBackend:
     """The attention backend of the HIP decode path. ``model_runner`` provides ``req_to_token_pool`` (with
     ``req_to_token`` [rows, context] int32), ``token_to_kv_pool`` (one of this package's pools) and ``page_size``.
@@ -76,7 +123,6 @@ class NeuronAttnBackend:
         self.req_to_token_pool = model_runner.req_to_token_pool
         self.token_to_kv_pool = model_runner.token_to_kv_pool
         self.page_size = int(model_runner.page_size)
-        self._r2t_view = None
 
     # SGLang's hooks: the metadata's consumers build it themselves (attention/backend.py:56-76)
     def init_forward_metadata(self, forward_batch):
@@ -99,79 +145,43 @@ class NeuronAttnBackend:
         return 1
 
     def build_metadata(self, fb) -> NeuronForwardMetadata:
-        """Exact (unpadded) metadata from a ForwardBatch (attention/backend.py:78-112)."""
-        mode = fb.forward_mode
-        bs = getattr(fb, "_original_batch_size", None)
-        bs = int(bs) if bs is not None else int(fb.batch_size)
-        n_tok = getattr(fb, "_original_num_tokens", None)
-        n_tok = int(n_tok) if n_tok is not None else int(fb.out_cache_loc.shape[0])
-        req_pool_indices = fb.req_pool_indices.to("cpu", torch.long)[:bs]
-        seq_lens = (fb.seq_lens_cpu if getattr(fb, "seq_lens_cpu", None) is not None else fb.seq_lens).to(
-            "cpu", torch.long)[:bs]
-        out_cache_loc = fb.out_cache_loc.to("cpu", torch.long)[:n_tok]
-        positions = fb.positions.to("cpu", torch.long)[:n_tok]
-        is_prefill = mode.is_extend() if not mode.is_idle() else False
-        if mode.is_idle() or bs == 0:
-            return NeuronForwardMetadata(
-                is_prefill=False, batch_size=0, num_tokens=0, block_table=torch.full((0, 1), -1, dtype=torch.int32),
-                slot_mapping=torch.zeros((0,), dtype=torch.long), seq_lens=torch.zeros((0,), dtype=torch.long),
-                positions=positions[:0])
-        cached = int(fb.extend_prefix_lens[:bs].max()) if is_prefill else 0
+        """Exact (unpadded) host metadata of a ForwardBatch, the reference's NeuronForwardMetadata semantics
+        (attention/backend.py:29-40, 78-112): the batch's real requests and tokens only, CPU int64 seq_lens /
+        slot_mapping / positions, and the block table of ``host_block_table``. An idle batch gets a (0, 1) table."""
+        n_req, n_tok = _real_sizes(fb)
+        positions = _first(fb.positions, n_tok, "cpu")
+        if fb.forward_mode.is_idle() or n_req == 0:
+            return _idle_metadata(positions[:0], torch.device("cpu"))
+        lens = _first(_seq_lens_source(fb), n_req, "cpu")
+        extend = bool(fb.forward_mode.is_extend())
+        slots = _first(fb.out_cache_loc, n_tok, "cpu")
+        table = host_block_table(self.req_to_token_pool.req_to_token, _first(fb.req_pool_indices, n_req, "cpu"), lens,
+                                 self.page_size)
         return NeuronForwardMetadata(
-            is_prefill=is_prefill, batch_size=bs, num_tokens=int(out_cache_loc.shape[0]),
-            block_table=self._block_table(req_pool_indices, seq_lens, bs), slot_mapping=out_cache_loc,
-            seq_lens=seq_lens, positions=positions, cached_seq_len=cached)
-
-    def _block_table(self, req_pool_indices: Tensor, seq_lens: Tensor, bs: int) -> Tensor:
-        """[bs, max_blocks] int32: each row's page representatives over the page size, -1 past its pages
-        (attention/backend.py:114-130)."""
-        page = self.page_size
-        rows = req_pool_indices.numpy()
-        lens = seq_lens.numpy()
-        max_blocks = (int(lens.max()) + page - 1) // page
-        table = (self._req_to_token_np()[rows, : max_blocks * page : page] // page).astype(np.int32, copy=False)
-        if bs != 1:
-            live = np.arange(0, max_blocks * page, page) < lens[:, None]
-            table = np.where(live, table, np.int32(-1))
-        return torch.from_numpy(np.ascontiguousarray(table))
-
-    def _req_to_token_np(self) -> np.ndarray:
-        r2t = self.req_to_token_pool.req_to_token
-        view = self._r2t_view
-        if view is None or view[0] is not r2t or view[1] != r2t.data_ptr():
-            view = self._r2t_view = (r2t, r2t.data_ptr(), r2t.numpy())
-        return view[2]
+            is_prefill=extend, batch_size=n_req, num_tokens=int(slots.numel()), block_table=table, slot_mapping=slots,
+            seq_lens=lens, positions=positions,
+            cached_seq_len=int(fb.extend_prefix_lens[:n_req].max()) if extend else 0)
 
     def build_device_metadata(self, fb, device: torch.device) -> NeuronForwardMetadata:
-        """A decode batch's metadata with req_to_token on the GPU, built there: ``block_table`` [bs, width] int32 by
+        """A batch's metadata with req_to_token on the GPU, built there: ``block_table`` [bs, width] int32 by
         ``ops.block_table`` (the reference's _block_table, attention/backend.py:114-130, entry for entry when width
         is the longest row's page count), ``slot_mapping`` / ``seq_lens`` / ``positions`` as device views of the
         batch's own tensors. ``width`` is ceil(max seq_len / page) from ``seq_lens_cpu`` when the batch has it, else
         req_to_token's context width in pages (a bound)."""
-        mode = fb.forward_mode
-        bs = getattr(fb, "_original_batch_size", None)
-        bs = int(bs) if bs is not None else int(fb.batch_size)
-        n_tok = getattr(fb, "_original_num_tokens", None)
-        n_tok = int(n_tok) if n_tok is not None else int(fb.out_cache_loc.shape[0])
+        n_req, n_tok = _real_sizes(fb)
+        if fb.forward_mode.is_idle() or n_req == 0:
+            return _idle_metadata(torch.zeros((0,), dtype=torch.long, device=device), device)
         r2t = self.req_to_token_pool.req_to_token
         page = self.page_size
-        if mode.is_idle() or bs == 0:
-            empty = torch.zeros((0,), dtype=torch.long, device=device)
-            return NeuronForwardMetadata(
-                is_prefill=False, batch_size=0, num_tokens=0,
-                block_table=torch.full((0, 1), -1, dtype=torch.int32, device=device), slot_mapping=empty,
-                seq_lens=empty, positions=empty)
         lens_cpu = getattr(fb, "seq_lens_cpu", None)
-        if lens_cpu is not None:
-            width = max(1, -(-int(lens_cpu[:bs].max()) // page))
-        else:
-            width = max(1, -(-int(r2t.shape[1]) // page))
-        seq_lens = fb.seq_lens[:bs].to(device, torch.long)
-        table = ops.block_table(r2t, fb.req_pool_indices[:bs].to(device, torch.long), seq_lens, page, width)
+        longest = int(lens_cpu[:n_req].max()) if lens_cpu is not None else int(r2t.shape[1])
+        lens = _first(fb.seq_lens, n_req, device)
+        table = ops.block_table(r2t, _first(fb.req_pool_indices, n_req, device), lens, page,
+                                max(1, -(-longest // page)))
         return NeuronForwardMetadata(
-            is_prefill=mode.is_extend(), batch_size=bs, num_tokens=n_tok, block_table=table,
-            slot_mapping=fb.out_cache_loc[:n_tok].to(device, torch.long), seq_lens=seq_lens,
-            positions=fb.positions[:n_tok].to(device, torch.long))
+            is_prefill=bool(fb.forward_mode.is_extend()), batch_size=n_req, num_tokens=n_tok, block_table=table,
+            slot_mapping=_first(fb.out_cache_loc, n_tok, device), seq_lens=lens,
+            positions=_first(fb.positions, n_tok, device))
 
     # ---- decode ----
     def _decode_state(self, fb, device: torch.device) -> _DecodeState:
@@ -186,11 +196,17 @@ class NeuronAttnBackend:
             raise ValueError(f"a decode batch has one new token per row ({meta.num_tokens} tokens, {meta.batch_size} "
                              "rows)")
         if on_device:
+            # the operands live on the device: only the host lengths (when the batch carries them) are checked
             lens_cpu = getattr(fb, "seq_lens_cpu", None)
             host_lens = lens_cpu[:meta.batch_size].to(torch.long) if lens_cpu is not None else None
             max_len = meta.block_table.shape[1] * self.page_size
+            if host_lens is not None and meta.batch_size:
+                _need_positions_fit(host_lens)
         else:
             host_lens, max_len = meta.seq_lens, -1
+            if meta.batch_size:
+                ops.check_decode_operands(meta.seq_lens, meta.block_table, meta.slot_mapping, self.page_size,
+                                          int(self.token_to_kv_pool.num_blocks))
         st = _DecodeState(meta=meta, table=meta.block_table.to(device), seq_lens=meta.seq_lens.to(device, torch.int32),
                           slots=meta.slot_mapping.to(device), positions=meta.positions.to(device, torch.int32),
                           plans={}, host_lens=host_lens, max_len=max_len)

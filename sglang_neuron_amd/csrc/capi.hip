@@ -1,6 +1,7 @@
 // C ABI plumbing: version, error state, split-K planning and the LSE merge of partial results.
 #include <algorithm>
 #include <cmath>
+#include <vector>
 
 #include "sna_device.h"
 #include "sna_host.h"
@@ -225,6 +226,58 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
     for (int32_t b = 0; b < B; ++b)
       for (int32_t s = 0, n = splits_of_row(b, split_tiles); s < n; ++s) plan->work[i++] = ((uint32_t)b << 6) | s;
     plan->work_n = i;
+  }
+  return SNA_OK;
+}
+
+int sna_check_decode_operands(const int64_t* seq_lens, const int32_t* block_table, int64_t table_stride,
+                              int32_t table_width, const int64_t* new_slots, int32_t B, int32_t page_size,
+                              int64_t num_blocks) {
+  ApiGuard guard;
+  if (B < 0 || page_size < 1 || num_blocks < 1 || table_width < 0 || table_stride < table_width)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "check_decode_operands: bad sizes (B %d, page %d, blocks %lld, table %d/%lld)",
+                B, page_size, (long long)num_blocks, table_width, (long long)table_stride);
+  if (B == 0) return SNA_OK;
+  if (!seq_lens || (table_width > 0 && !block_table))
+    return fail(SNA_ERR_INVALID_ARGUMENT, "check_decode_operands: null pointer");
+  const int64_t pool_slots = num_blocks * page_size;
+  for (int32_t b = 0; b < B; ++b) {
+    const int64_t L = seq_lens[b];
+    if (L < 1) return fail(SNA_ERR_INVALID_ARGUMENT, "row %d: seq_len %lld (a decode row holds at least its new token)",
+                           b, (long long)L);
+    if (L > INT32_MAX)
+      return fail(SNA_ERR_INVALID_ARGUMENT, "row %d: position %lld exceeds the kernels' int32 positions", b,
+                  (long long)(L - 1));
+    const int64_t pages = (L + page_size - 1) / page_size;
+    if (pages > table_width)
+      return fail(SNA_ERR_INVALID_ARGUMENT, "row %d: %lld tokens span %lld pages, the block table holds %d", b,
+                  (long long)L, (long long)pages, table_width);
+    const int32_t* row = block_table + (int64_t)b * table_stride;
+    for (int64_t j = 0; j < pages; ++j)
+      if (row[j] < 0 || row[j] >= num_blocks)
+        return fail(SNA_ERR_INVALID_ARGUMENT, "row %d: table column %lld holds page %d, outside the pool's %lld pages "
+                    "(the row's pages must cover its %lld tokens)", b, (long long)j, row[j], (long long)num_blocks,
+                    (long long)L);
+    if (!new_slots) continue;
+    const int64_t slot = new_slots[b];
+    // a slot on the reserved page 0 or outside the pool is a padding row's write (redirected to slot 0)
+    if (slot < page_size || slot >= pool_slots) continue;
+    if (slot % page_size != (L - 1) % page_size)
+      return fail(SNA_ERR_INVALID_ARGUMENT, "row %d: new slot %lld disagrees with position %lld (page %d)", b,
+                  (long long)slot, (long long)(L - 1), page_size);
+    if (slot / page_size != row[(L - 1) / page_size])
+      return fail(SNA_ERR_INVALID_ARGUMENT, "row %d: new slot %lld is on page %lld, the row's last page is %d", b,
+                  (long long)slot, (long long)(slot / page_size), row[(L - 1) / page_size]);
+  }
+  if (new_slots) {
+    std::vector<int64_t> live;
+    live.reserve(B);
+    for (int32_t b = 0; b < B; ++b)
+      if (new_slots[b] >= page_size && new_slots[b] < pool_slots) live.push_back(new_slots[b]);
+    std::sort(live.begin(), live.end());
+    for (size_t i = 1; i < live.size(); ++i)
+      if (live[i] == live[i - 1])
+        return fail(SNA_ERR_INVALID_ARGUMENT, "two live decode rows write slot %lld", (long long)live[i]);
   }
   return SNA_OK;
 }

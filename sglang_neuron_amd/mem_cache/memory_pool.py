@@ -34,30 +34,27 @@ logger = logging.getLogger(__name__)
 GB = 1024 ** 3
 FP8 = torch.float8_e4m3fn
 
-# MHATokenToKVPool keyword arguments whose features the pool does not have, with the value that means "off"
-# (memory_pool.py:260-261)
-_POOL_OPTIONS_OFF = {"post_capture_active": False, "quant_method": None, "kv_cache_layout": None,
-                     "enable_kv_cache_copy": False}
-# MLATokenToKVPool keyword arguments likewise (memory_pool.py:432)
-_MLA_POOL_OPTIONS_OFF = {"use_dsa": False, "override_kv_cache_dim": None, "dcp_replicated": False}
+# SGLang pool keyword arguments naming features these pools do not build. A pool accepts such an argument only when it
+# leaves the feature off (absent, None or False); any other value is a ValueError, as the reference pools refuse them
+# (mem_cache/memory_pool.py:260-282 for the MHA pool, :432 for the MLA pool). The head-dim arguments must repeat the
+# pool's own head dim: K and V pages share it on every layer.
+_FEATURES_NOT_BUILT = {
+    "mha": ("post_capture_active", "quant_method", "kv_cache_layout", "enable_kv_cache_copy"),
+    "mla": ("use_dsa", "override_kv_cache_dim", "dcp_replicated"),
+}
+_SAME_HEAD_DIM = ("v_head_dim", "swa_head_dim", "swa_v_head_dim")
 
 
-def _refuse_other_head_dims(head_dim: int, kwargs: dict) -> None:
-    """A V or sliding-window head dim other than ``head_dim`` is refused: K and V pages share one head dim
-    (memory_pool.py:264-271)."""
-    other = {k: kwargs[k] for k in ("v_head_dim", "swa_head_dim", "swa_v_head_dim")
-             if kwargs.get(k) not in (None, head_dim)}
-    if other:
-        raise ValueError(f"the KV pool holds K and V of one head dim ({head_dim}) on every layer, not "
-                         f"{', '.join(f'{k}={v}' for k, v in other.items())}")
-
-
-def _refuse_unsupported_pool_options(kwargs: dict, options_off=None) -> None:
-    """A pool option the pool does not implement is refused (memory_pool.py:274-282)."""
-    options_off = _POOL_OPTIONS_OFF if options_off is None else options_off
-    on = sorted(k for k, off in options_off.items() if k in kwargs and kwargs[k] not in (off, None, False))
-    if on:
-        raise ValueError(f"the KV pool does not support {', '.join(f'{k}={kwargs[k]!r}' for k in on)}")
+def _check_pool_kwargs(kind: str, kwargs: dict, head_dim: Optional[int] = None) -> None:
+    """Raise ValueError naming every keyword argument of ``kwargs`` that asks ``kind``'s pool for something it does not
+    build: a feature switched on, or (with ``head_dim``) a second head dim."""
+    asked = [f"{name}={kwargs[name]!r}" for name in _FEATURES_NOT_BUILT[kind]
+             if kwargs.get(name) not in (None, False)]
+    if head_dim is not None:
+        asked += [f"{name}={kwargs[name]!r}" for name in _SAME_HEAD_DIM if kwargs.get(name) not in (None, head_dim)]
+    if asked:
+        raise ValueError(f"the {kind.upper()} KV pool (one head dim, FP8 or bf16 pages) does not support "
+                         f"{', '.join(sorted(asked))}")
 
 
 def _layer_id(layer) -> int:
@@ -86,8 +83,7 @@ class NeuronMHATokenToKVPool:
     def __init__(self, size: int, page_size: int, dtype: torch.dtype, head_num: int, head_dim: int, layer_num: int,
                  device: Union[str, torch.device], enable_memory_saver: bool = False,
                  start_layer: Optional[int] = None, end_layer: Optional[int] = None, **kwargs):
-        _refuse_unsupported_pool_options(kwargs)
-        _refuse_other_head_dims(head_dim, kwargs)
+        _check_pool_kwargs("mha", kwargs, head_dim)
         if enable_memory_saver:
             raise ValueError("the KV pool does not support enable_memory_saver")
         if size % page_size:
@@ -223,7 +219,7 @@ class NeuronMLATokenToKVPool:
     def __init__(self, size: int, page_size: int, dtype: torch.dtype, kv_lora_rank: int, qk_rope_head_dim: int,
                  layer_num: int, device: Union[str, torch.device], enable_memory_saver: bool = False,
                  start_layer: Optional[int] = None, end_layer: Optional[int] = None, **kwargs):
-        _refuse_unsupported_pool_options(kwargs, _MLA_POOL_OPTIONS_OFF)
+        _check_pool_kwargs("mla", kwargs)
         if enable_memory_saver:
             raise ValueError("the MLA pool does not support enable_memory_saver")
         if dtype not in (FP8, torch.uint8):

@@ -220,6 +220,28 @@ def plan_decode(kind: int, B: int, *, host_seq_lens: Union[Tensor, Sequence[int]
     return plan
 
 
+def check_decode_operands(seq_lens: Tensor, block_table: Tensor, new_slots: Optional[Tensor], page_size: int,
+                          num_blocks: int) -> None:
+    """Refuse a decode batch whose host operands the kernels cannot serve (sna_check_decode_operands): a seq_len
+    outside [1, 2^31 - 1], a block table too narrow for a row or naming a page outside the pool inside a row's pages,
+    a live row's new slot that is not at its position on its last page, two live rows writing one slot. Host (CPU)
+    tensors: seq_lens [B] int, block_table [B, W] int32, new_slots [B] int or None. Raises ValueError naming the row.
+
+    The refusals of the reference's decode_operands (attention/mla_operands.py:64-97)."""
+    for t in (seq_lens, block_table, new_slots):
+        _need(t is None or not t.is_cuda, "check_decode_operands takes host copies of the operands")
+    lens = seq_lens.reshape(-1).to(torch.int64).contiguous()
+    B = lens.numel()
+    _need(block_table.dim() == 2 and block_table.shape[0] == B, f"block_table must be [{B}, width]")
+    table = block_table.to(torch.int32).contiguous()
+    slots = None if new_slots is None else new_slots.reshape(-1).to(torch.int64).contiguous()
+    _need(slots is None or slots.numel() == B, f"new_slots must have {B} entries")
+    rc = _lib.load().sna_check_decode_operands(lens.data_ptr(), table.data_ptr(), table.stride(0), table.shape[1],
+                                               None if slots is None else slots.data_ptr(), B, int(page_size),
+                                               int(num_blocks))
+    _lib.check(rc, "check_decode_operands")
+
+
 def workspace_bytes(plan: _lib.SplitPlan, heads: int, dim_v: int) -> int:
     return int(_lib.load().sna_decode_workspace_bytes(plan, heads, dim_v))
 

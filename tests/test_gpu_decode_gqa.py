@@ -20,6 +20,10 @@ CASES = [
     ("bf16-d64-g1", 1, {"B": 3, "H": 4, "G": 4, "d": 64, "lens": (2, 300)}),
     ("fp8-g16", 2, {"B": 2, "H": 32, "G": 2, "lens": (33, 900)}),
     ("fp8-page64", 2, {"B": 3, "P": 64, "lens": (50, 1500)}),
+    # page 128: the page the reference serves Qwen3 with (docs/model-recipes/qwen3.md:126)
+    ("cfg2-page128", 2, {"B": 8, "P": 128, "lens": (2000, 4096)}),
+    ("bf16-page128", 1, {"B": 5, "P": 128, "lens": (100, 3000)}),
+    ("cfg4-page128-sinks", 4, {"B": 6, "P": 128, "lens": (1000, 5000)}),
     ("cfg2-32-splits", 2, {"B": 2, "lens": (8192, 8192)}),                # the combine's second chunk of 16 splits
     ("cfg4-64-splits", 4, {"B": 2, "lens": (8000, 8192)}),                # 4 chunks, sinks
     # the bench workloads at their full sizes (the metric's cfg2 included): same seeds, same split plans

@@ -221,6 +221,23 @@ int sna_paged_decode_gqa(const void *q, const void *k_cache, const void *v_cache
                          int64_t num_blocks, int32_t cache_dtype, const sna_split_plan *plan, void *workspace,
                          int64_t workspace_bytes, void *stream);
 
+/* sna_paged_decode_gqa for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). It has no counterpart in the reference. Same arguments and results as
+ * sna_paged_decode_gqa without the workspace: the split partials go to a scratch array of
+ * SNA_NOALLOC_SCRATCH_BYTES (16 MiB) that the library holds on each GPU it runs on until the process ends (its device
+ * address is looked up on the first call on a device). A plan whose partials need more is refused with
+ * SNA_ERR_WORKSPACE. Nothing is allocated, freed or cleared per call: every partial a combine pass reads was written
+ * by the same call. Calls that overlap on one GPU (other streams, other threads) share the array and race; serialize
+ * them. */
+#define SNA_NOALLOC_SCRATCH_BYTES (16ll << 20)
+int sna_paged_decode_gqa_noalloc(const void *q, const void *k_cache, const void *v_cache, const float *k_scale,
+                                 const float *v_scale, const int32_t *block_table, int64_t table_stride,
+                                 int32_t table_width, const int32_t *seq_lens, const void *k_new, const void *v_new,
+                                 const int64_t *new_slots, const float *sinks, int32_t window, float sm_scale,
+                                 void *out, int32_t B, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                 int32_t page_size, int64_t num_blocks, int32_t cache_dtype,
+                                 const sna_split_plan *plan, void *stream);
+
 /* Absorbed-MLA paged decode over an MLA pool layer of compact rows [latent(512) | k_pe(64)].
  *   ql_nope      [B, num_heads, 512] bf16 (W_UK folded in); q_pe [B, num_heads, 64] bf16 (RoPE'd).
  *   cache        [num_blocks * page_size, 576] of cache_dtype; row_scale [num_blocks * page_size] fp32 (FP8).

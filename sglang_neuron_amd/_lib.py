@@ -21,6 +21,8 @@ SNA_ERR_WORKSPACE = -2
 SNA_ERR_LAUNCH = -3
 SNA_ERR_UNSUPPORTED = -4
 
+NOALLOC_SCRATCH_BYTES = 16 << 20  # SNA_NOALLOC_SCRATCH_BYTES
+
 DTYPE_BF16 = 0
 DTYPE_FP8_E4M3FN = 1
 
@@ -64,6 +66,8 @@ SIGNATURES = {
     "sna_check_decode_operands": (_I32, [_P, _P, _I64, _I32, _P, _I32, _I32, _I64]),
     "sna_paged_decode_gqa": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _I32, _F32, _P, _I32,
                                     _I32, _I32, _I32, _I32, _I64, _I32, ctypes.POINTER(SplitPlan), _P, _I64, _P]),
+    "sna_paged_decode_gqa_noalloc": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _I32, _F32, _P,
+                                            _I32, _I32, _I32, _I32, _I32, _I64, _I32, ctypes.POINTER(SplitPlan), _P]),
     "sna_mla_decode": (_I32, [_P, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _F32, _P, _I32, _I32, _I32, _I64, _I32,
                               ctypes.POINTER(SplitPlan), _P, _I64, _P]),
     "sna_mla_decode_sparse": (_I32, [_P, _P, _P, _F32, _P, _I32, _P, _I64, _I32, _P, _P, _F32, _P, _P, _I32, _I32,

@@ -23,6 +23,8 @@
 // Softmax state per head is (m, l, acc) in the log2 domain. m moves only when a tile's maximum passes it by more than
 // 8 (a factor of 256), so the accumulators are rescaled rarely. Probabilities stay <= 256, which bf16 and fp32
 // hold without loss of relative precision.
+#include <mutex>
+
 #include "sna_device.h"
 #include "sna_host.h"
 
@@ -567,47 +569,52 @@ static void launch_gqa(const GqaArgs& a, int depth, bool any_lone, hipStream_t s
 
 using namespace sna;
 
-extern "C" int sna_paged_decode_gqa(const void* q, const void* k_cache, const void* v_cache, const float* k_scale,
-                                    const float* v_scale, const int32_t* block_table, int64_t table_stride,
-                                    int32_t table_width, const int32_t* seq_lens, const void* k_new,
-                                    const void* v_new, const int64_t* new_slots, const float* sinks, int32_t window,
-                                    float sm_scale, void* out, int32_t B, int32_t num_q_heads, int32_t num_kv_heads,
-                                    int32_t head_dim, int32_t page_size, int64_t num_blocks, int32_t cache_dtype,
-                                    const sna_split_plan* plan, void* workspace, int64_t workspace_bytes,
-                                    void* stream) {
-  ApiGuard guard;
+// The library's own split-K workspace for callers that cannot allocate: one array per GPU, resident for the process.
+// Host code never passes `scratch` itself to a kernel (its name is a host-side stand-in for the symbol); it passes the
+// device address hipGetSymbolAddress gives on each device, looked up once per device with that device current.
+static __device__ __align__(256) uint8_t scratch[SNA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+// The checks and launches of one GQA decode, with the split partials in `workspace` (the caller's device memory, or
+// the library's scratch array for sna_paged_decode_gqa_noalloc). `what` names the entry point in error messages.
+int decode_gqa(const char* what, const void* q, const void* k_cache, const void* v_cache, const float* k_scale,
+               const float* v_scale, const int32_t* block_table, int64_t table_stride, int32_t table_width,
+               const int32_t* seq_lens, const void* k_new, const void* v_new, const int64_t* new_slots,
+               const float* sinks, int32_t window, float sm_scale, void* out, int32_t B, int32_t num_q_heads,
+               int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int64_t num_blocks, int32_t cache_dtype,
+               const sna_split_plan* plan, void* workspace, int64_t workspace_bytes, void* stream) {
   if (B < 0 || num_q_heads < 1 || num_kv_heads < 1 || num_q_heads % num_kv_heads)
-    return fail(SNA_ERR_INVALID_ARGUMENT, "paged_decode_gqa: bad head counts (q %d, kv %d)", num_q_heads,
-                num_kv_heads);
+    return fail(SNA_ERR_INVALID_ARGUMENT, "%s: bad head counts (q %d, kv %d)", what, num_q_heads, num_kv_heads);
   const int32_t group = num_q_heads / num_kv_heads;
   if (group > 16)
-    return fail(SNA_ERR_UNSUPPORTED, "paged_decode_gqa: GQA group %d > 16 (a workgroup covers 16 query heads)", group);
+    return fail(SNA_ERR_UNSUPPORTED, "%s: GQA group %d > 16 (a workgroup covers 16 query heads)", what, group);
   if (head_dim != 64 && head_dim != 128)
-    return fail(SNA_ERR_UNSUPPORTED, "paged_decode_gqa: head_dim %d (64 or 128 are built)", head_dim);
+    return fail(SNA_ERR_UNSUPPORTED, "%s: head_dim %d (64 or 128 are built)", what, head_dim);
   if (page_size < 16 || page_size % 16)
-    return fail(SNA_ERR_UNSUPPORTED, "paged_decode_gqa: page_size %d (a multiple of 16 is required)", page_size);
+    return fail(SNA_ERR_UNSUPPORTED, "%s: page_size %d (a multiple of 16 is required)", what, page_size);
   if (cache_dtype != SNA_DTYPE_BF16 && cache_dtype != SNA_DTYPE_FP8_E4M3FN)
-    return fail(SNA_ERR_INVALID_ARGUMENT, "paged_decode_gqa: unknown cache dtype %d", cache_dtype);
+    return fail(SNA_ERR_INVALID_ARGUMENT, "%s: unknown cache dtype %d", what, cache_dtype);
   if (window < 0 || table_width < 0 || table_stride < table_width || num_blocks < 1 || !(sm_scale > 0.0f))
-    return fail(SNA_ERR_INVALID_ARGUMENT, "paged_decode_gqa: bad window %d, table %d/%lld, blocks %lld or scale %g",
-                window, table_width, (long long)table_stride, (long long)num_blocks, (double)sm_scale);
+    return fail(SNA_ERR_INVALID_ARGUMENT, "%s: bad window %d, table %d/%lld, blocks %lld or scale %g", what, window,
+                table_width, (long long)table_stride, (long long)num_blocks, (double)sm_scale);
   if (!plan || plan->tile != 32 || plan->split_tiles < 1 || plan->n_work < 0 || plan->max_splits < 0 ||
       plan->batch != B)
-    return fail(SNA_ERR_INVALID_ARGUMENT, "paged_decode_gqa: missing or foreign split plan (made for %d rows)",
+    return fail(SNA_ERR_INVALID_ARGUMENT, "%s: missing or foreign split plan (made for %d rows)", what,
                 plan ? plan->batch : -1);
-  if (const int rc = check_work_map(plan, B, "paged_decode_gqa")) return rc;
+  if (const int rc = check_work_map(plan, B, what)) return rc;
   if (B == 0) return SNA_OK;
   const bool fp8 = cache_dtype == SNA_DTYPE_FP8_E4M3FN;
   const int64_t need = sna_decode_workspace_bytes(plan, num_q_heads, head_dim);
   if (!q || !k_cache || !v_cache || !block_table || !seq_lens || !k_new || !v_new || !out ||
       (fp8 && (!k_scale || !v_scale)) || (need > 0 && !workspace))
-    return fail(SNA_ERR_INVALID_ARGUMENT, "paged_decode_gqa: null pointer");
+    return fail(SNA_ERR_INVALID_ARGUMENT, "%s: null pointer", what);
   if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
-    return fail(SNA_ERR_INVALID_ARGUMENT, "paged_decode_gqa: q and caches must be 16-byte aligned");
+    return fail(SNA_ERR_INVALID_ARGUMENT, "%s: q and caches must be 16-byte aligned", what);
   if (workspace_bytes < need)
-    return fail(SNA_ERR_WORKSPACE, "paged_decode_gqa: workspace of %lld bytes, the plan needs %lld",
+    return fail(SNA_ERR_WORKSPACE, "%s: workspace of %lld bytes, the plan needs %lld", what,
                 (long long)workspace_bytes, (long long)need);
-  if (num_q_heads > 65535) return fail(SNA_ERR_INVALID_ARGUMENT, "paged_decode_gqa: grid too large");
+  if (num_q_heads > 65535) return fail(SNA_ERR_INVALID_ARGUMENT, "%s: grid too large", what);
 
   GqaArgs a;
   a.q = (const uint16_t*)q;
@@ -651,5 +658,69 @@ extern "C" int sna_paged_decode_gqa(const void* q, const void* k_cache, const vo
     if (fp8) launch_gqa<64, true>(a, plan->depth, any_lone, s);
     else launch_gqa<64, false>(a, plan->depth, any_lone, s);
   }
-  return check_launch("paged_decode_gqa");
+  return check_launch(what);
+}
+
+constexpr int64_t kScratchBytes = SNA_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address, looked up on its first use (SNA_OK), or an error status.
+int scratch_address(const char* what, void** ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(SNA_ERR_LAUNCH, "%s: no current device (or device %d past %d)", what, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(SNA_ERR_LAUNCH, "%s: the scratch array of device %d has no address: %s", what, dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return SNA_OK;
+}
+
+}  // namespace
+
+extern "C" int sna_paged_decode_gqa(const void* q, const void* k_cache, const void* v_cache, const float* k_scale,
+                                    const float* v_scale, const int32_t* block_table, int64_t table_stride,
+                                    int32_t table_width, const int32_t* seq_lens, const void* k_new,
+                                    const void* v_new, const int64_t* new_slots, const float* sinks, int32_t window,
+                                    float sm_scale, void* out, int32_t B, int32_t num_q_heads, int32_t num_kv_heads,
+                                    int32_t head_dim, int32_t page_size, int64_t num_blocks, int32_t cache_dtype,
+                                    const sna_split_plan* plan, void* workspace, int64_t workspace_bytes,
+                                    void* stream) {
+  ApiGuard guard;
+  return decode_gqa("paged_decode_gqa", q, k_cache, v_cache, k_scale, v_scale, block_table, table_stride,
+                    table_width, seq_lens, k_new, v_new, new_slots, sinks, window, sm_scale, out, B, num_q_heads,
+                    num_kv_heads, head_dim, page_size, num_blocks, cache_dtype, plan, workspace, workspace_bytes,
+                    stream);
+}
+
+extern "C" int sna_paged_decode_gqa_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                            const float* k_scale, const float* v_scale, const int32_t* block_table,
+                                            int64_t table_stride, int32_t table_width, const int32_t* seq_lens,
+                                            const void* k_new, const void* v_new, const int64_t* new_slots,
+                                            const float* sinks, int32_t window, float sm_scale, void* out, int32_t B,
+                                            int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                            int32_t page_size, int64_t num_blocks, int32_t cache_dtype,
+                                            const sna_split_plan* plan, void* stream) {
+  ApiGuard guard;
+  const char* what = "paged_decode_gqa_noalloc";
+  if (plan && num_q_heads > 0 && head_dim > 0) {
+    const int64_t need = sna_decode_workspace_bytes(plan, num_q_heads, head_dim);
+    if (need > kScratchBytes)
+      return fail(SNA_ERR_WORKSPACE, "%s: the plan's split partials need %lld bytes, past the library's %lld-byte "
+                  "scratch (use sna_paged_decode_gqa with a workspace)", what, (long long)need,
+                  (long long)kScratchBytes);
+  }
+  void* ws = nullptr;
+  if (const int rc = scratch_address(what, &ws)) return rc;
+  return decode_gqa(what, q, k_cache, v_cache, k_scale, v_scale, block_table, table_stride, table_width, seq_lens,
+                    k_new, v_new, new_slots, sinks, window, sm_scale, out, B, num_q_heads, num_kv_heads, head_dim,
+                    page_size, num_blocks, cache_dtype, plan, ws, kScratchBytes, stream);
 }

@@ -281,8 +281,11 @@ def prepare_paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_
                              k_new: Tensor, v_new: Tensor, *, sm_scale: float, k_scale: Optional[Tensor] = None,
                              v_scale: Optional[Tensor] = None, sinks: Optional[Tensor] = None, window: int = 0,
                              new_slots: Optional[Tensor] = None, out: Optional[Tensor] = None,
-                             host_seq_lens=None, plan: Optional[_lib.SplitPlan] = None) -> Prepared:
-    """paged_decode_gqa's checks and argument binding, launched by calling the result."""
+                             host_seq_lens=None, plan: Optional[_lib.SplitPlan] = None,
+                             library_scratch: bool = False) -> Prepared:
+    """paged_decode_gqa's checks and argument binding, launched by calling the result. With ``library_scratch`` the
+    call is sna_paged_decode_gqa_noalloc: no workspace tensor is allocated, the split partials go to the library's
+    per-GPU scratch array (at most NOALLOC_SCRATCH_BYTES; calls that overlap on one GPU race)."""
     dev = _on_gpu(q, k_cache, v_cache, block_table, seq_lens, k_new, v_new, k_scale, v_scale, sinks, new_slots, out)
     _need(q.dim() == 3, f"q must be [B, H, d], got {tuple(q.shape)}")
     B, H, d = q.shape
@@ -318,13 +321,17 @@ def prepare_paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_
         hl = _host_lens(seq_lens, host_seq_lens)
         plan = plan_decode(_lib.KIND_GQA, B, host_seq_lens=hl, max_seq_len=table.shape[1] * P, window=window,
                            ctas_per_item=G, num_cus=_num_cus(dev))
-    ws = torch.empty(max(workspace_bytes(plan, H, d), 16), dtype=torch.uint8, device=dev)
     lib = _lib.load()
     args = (_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), _ptr(table), table.stride(0),
             table.shape[1], _ptr(lens), _ptr(k_new), _ptr(v_new), _ptr(new_slots), _ptr(sinks), int(window),
-            float(sm_scale), _ptr(out), B, H, G, d, P, nb, code, plan, _ptr(ws), ws.numel(), _stream(dev))
-    keep = (q, k_cache, v_cache, k_scale, v_scale, table, lens, k_new, v_new, new_slots, sinks, out, ws, plan)
-    return Prepared([(lib.sna_paged_decode_gqa, args)], keep, out, "paged_decode_gqa")
+            float(sm_scale), _ptr(out), B, H, G, d, P, nb, code, plan)
+    keep = (q, k_cache, v_cache, k_scale, v_scale, table, lens, k_new, v_new, new_slots, sinks, out, plan)
+    if library_scratch:
+        return Prepared([(lib.sna_paged_decode_gqa_noalloc, args + (_stream(dev),))], keep, out,
+                        "paged_decode_gqa_noalloc")
+    ws = torch.empty(max(workspace_bytes(plan, H, d), 16), dtype=torch.uint8, device=dev)
+    return Prepared([(lib.sna_paged_decode_gqa, args + (_ptr(ws), ws.numel(), _stream(dev)))], keep + (ws,), out,
+                    "paged_decode_gqa")
 
 
 def paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: Tensor, seq_lens: Tensor,

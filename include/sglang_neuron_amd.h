@@ -131,37 +131,64 @@ int sna_kv_store_dsa(const void *rows, const int64_t *slots, int64_t n_tokens, f
  * Split-K planning (host side; no device access)
  * ===================================================================================================== */
 
-/* The split plan of a decode launch. `split_tiles` is how many key tiles each split covers. `n_work` is the number of
- * (sequence, split) items the split-K kernel runs. Partials are kept per (row, split): the workspace holds
- * batch * max_splits of them. A plan whose rows all fit one split (max_splits <= 1) needs no workspace, because its
- * split-K kernel writes the final output and no combine pass runs. */
+/* The split plan of a decode launch.
+ *
+ * GQA (kind 0): `split_tiles` is how many key tiles each split covers and `n_work` is the number of (sequence, split)
+ * items the split-K kernel runs. Partials are kept per (row, split): the workspace holds batch * max_splits of them.
+ * A plan whose rows all fit one split (max_splits <= 1) needs no workspace: its split-K kernel writes the final output
+ * and no combine pass runs.
+ *
+ * MLA and DSA (kinds 1, 2): a stream split. Row b's keys (paged: the seq_len - 1 prior positions; sparse: the index
+ * list) form ceil(keys / 16) tiles (at least 1), the rows' tiles are laid end to end, and workgroup w takes tiles
+ * [cta_start[w], cta_start[w + 1]) of that sequence: n_ctas workgroups (one per CU) of equal tile counts, each
+ * starting in row cta_row[w] at tile cta_off[w] of that row. A workgroup whose range holds a whole row writes its
+ * output; a row split over several workgroups is merged inside the same launch (its workgroups publish partials and
+ * the last to arrive, with those still waiting for it, merges them), so one launch is the whole decode. row_keys[b] is
+ * row b's key count: an MLA or DSA launch uses these host lengths, not the device's seq_lens. */
 #define SNA_MAX_WORK_MAP 512
+#define SNA_MAX_CTAS 256      /* workgroups of an MLA / DSA stream split */
+#define SNA_MAX_PLAN_ROWS 256 /* rows of an MLA / DSA plan */
 
 typedef struct {
   int32_t split_tiles;
   int32_t n_work;
   int32_t tile;         /* keys per tile of the kernel family: 32 (GQA) or 16 (MLA, DSA) */
   int32_t target_ctas;  /* the workgroup count the plan aimed for */
-  int32_t max_splits;   /* the most splits any row has */
+  int32_t max_splits;   /* GQA: the most splits any row has; MLA / DSA: the most workgroups any row spans */
   int32_t batch;        /* rows the plan was made for */
   int32_t empty_rows;   /* rows with no prior key (seq_len 1), or -1 when planned from a bound */
   int32_t depth;        /* GQA: tiles each wave keeps in its register ring (2: two waves per SIMD; 4: one wave per
                            SIMD with three tiles in flight). The planner picks it; splits were sized for it. */
-  int32_t work_n;       /* entries in work[] (0: the kernels locate their items from the device's seq_lens) */
-  uint32_t work[SNA_MAX_WORK_MAP]; /* a plan from host seq_lens with n_work <= SNA_MAX_WORK_MAP: item i is row
+  int32_t work_n;       /* GQA: entries in work[] (0: the kernels locate their items from the device's seq_lens) */
+  uint32_t work[SNA_MAX_WORK_MAP]; /* GQA, a plan from host seq_lens with n_work <= SNA_MAX_WORK_MAP: item i is row
                            work[i] >> 6, split work[i] & 63, in launch order. The decode kernels read it from their
                            arguments and skip the device-side search over seq_lens. */
+  int32_t n_ctas;       /* MLA / DSA: workgroups of the stream split (per 16-head group) */
+  int32_t total_tiles;  /* MLA / DSA: tiles of all rows */
+  int32_t wait_polls;   /* MLA / DSA: how many times a workgroup that published a partial polls for its row's last
+                           partial before it leaves the merge to the others (0: the last to arrive merges alone) */
+  uint32_t cta_start[SNA_MAX_CTAS + 1];
+  uint16_t cta_row[SNA_MAX_CTAS];
+  uint16_t cta_off[SNA_MAX_CTAS];
+  int32_t row_keys[SNA_MAX_PLAN_ROWS];
 } sna_split_plan;
 
 /* Plan a decode from host copies of seq_lens (exact) or, with host_seq_lens == NULL, from an upper bound
- * max_seq_len for every row (then n_work bounds the device's count and the workspace is sized for it).
+ * max_seq_len for every row (then n_work bounds the device's count and the workspace is sized for it; GQA only).
  * `kind`: 0 GQA, 1 MLA, 2 DSA. For DSA, seq_lens are ignored: `n_keys_per_row` (the index-list length) is the
  * row's key count. `window` is the sliding window (0 = full). `ctas_per_item` is the number of workgroups that
  * one (sequence, split) item launches: num_kv_heads for GQA, and 1 for MLA and DSA. `num_cus` is the device's CU
- * count (0 = 256). Returns SNA_OK and fills *plan. Host and device seq_lens must agree: a device length past the
- * host's leaves its extra splits unread, though all reads stay inside the workspace. */
+ * count (0 = 256). Returns SNA_OK and fills *plan. MLA and DSA plans hold at most SNA_MAX_PLAN_ROWS rows of at most
+ * 65535 tiles each. GQA: host and device seq_lens must agree: a device length past the host's leaves its extra splits
+ * unread, though all reads stay inside the workspace. */
 int sna_plan_decode(int32_t kind, const int32_t *host_seq_lens, int32_t B, int32_t max_seq_len, int32_t window,
                     int32_t n_keys_per_row, int32_t ctas_per_item, int32_t num_cus, sna_split_plan *plan);
+
+/* Workspace bytes a decode with this plan needs. GQA: batch * max_splits * heads * (head_dim_v + 2) * 4, or 0 when
+ * max_splits <= 1. MLA / DSA: a 256 KiB block of counters, then 2 * n_ctas partials of heads * (head_dim_v + 2) fp32.
+ * The counters must be zero before the first call on a workspace (allocate it zeroed); every completed call leaves
+ * them zero. Calls that share a workspace must be ordered (one stream). */
+int64_t sna_decode_workspace_bytes(const sna_split_plan *plan, int32_t num_q_heads, int32_t head_dim_v);
 
 /* Host check of one decode batch's operands, before any launch (host copies of every array):
  *   seq_lens     [B] int64, prefix plus the new token: each in [1, INT32_MAX] (positions are int32 in the kernels).
@@ -177,10 +204,6 @@ int sna_plan_decode(int32_t kind, const int32_t *host_seq_lens, int32_t B, int32
 int sna_check_decode_operands(const int64_t *seq_lens, const int32_t *block_table, int64_t table_stride,
                               int32_t table_width, const int64_t *new_slots, int32_t B, int32_t page_size,
                               int64_t num_blocks);
-
-/* Workspace bytes a decode with this plan needs: batch * max_splits * heads * (head_dim_v + 2) * 4, or 0 when
- * max_splits <= 1. */
-int64_t sna_decode_workspace_bytes(const sna_split_plan *plan, int32_t num_q_heads, int32_t head_dim_v);
 
 /* =====================================================================================================
  * Decode attention

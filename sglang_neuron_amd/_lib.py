@@ -26,6 +26,9 @@ NOALLOC_SCRATCH_BYTES = 16 << 20  # SNA_NOALLOC_SCRATCH_BYTES
 DTYPE_BF16 = 0
 DTYPE_FP8_E4M3FN = 1
 
+MAX_CTAS = 256       # SNA_MAX_CTAS
+MAX_PLAN_ROWS = 256  # SNA_MAX_PLAN_ROWS
+
 KIND_GQA = 0
 KIND_MLA = 1
 KIND_DSA = 2
@@ -37,12 +40,15 @@ class SplitPlan(ctypes.Structure):
     _fields_ = [("split_tiles", ctypes.c_int32), ("n_work", ctypes.c_int32), ("tile", ctypes.c_int32),
                 ("target_ctas", ctypes.c_int32), ("max_splits", ctypes.c_int32), ("batch", ctypes.c_int32),
                 ("empty_rows", ctypes.c_int32), ("depth", ctypes.c_int32), ("work_n", ctypes.c_int32),
-                ("work", ctypes.c_uint32 * 512)]
+                ("work", ctypes.c_uint32 * 512), ("n_ctas", ctypes.c_int32), ("total_tiles", ctypes.c_int32),
+                ("wait_polls", ctypes.c_int32), ("cta_start", ctypes.c_uint32 * (MAX_CTAS + 1)),
+                ("cta_row", ctypes.c_uint16 * MAX_CTAS), ("cta_off", ctypes.c_uint16 * MAX_CTAS),
+                ("row_keys", ctypes.c_int32 * MAX_PLAN_ROWS)]
 
     def __repr__(self) -> str:
         return (f"SplitPlan(split_tiles={self.split_tiles}, n_work={self.n_work}, tile={self.tile}, "
                 f"target_ctas={self.target_ctas}, max_splits={self.max_splits}, batch={self.batch}, "
-                f"empty_rows={self.empty_rows}, depth={self.depth})")
+                f"empty_rows={self.empty_rows}, depth={self.depth}, n_ctas={self.n_ctas})")
 
 
 _P = ctypes.c_void_p

@@ -333,12 +333,15 @@ class NeuronAttnBackend:
         q = q.reshape(bs, H, 576)
         key = ("mla", H)
         if key not in st.plans:
-            st.plans[key] = ops.plan_decode(_lib.KIND_MLA, bs, host_seq_lens=st.host_lens, max_seq_len=st.max_len,
-                                            ctas_per_item=(H + 15) // 16, num_cus=ops._num_cus(q.device))
+            # the MLA launch runs on host lengths: without a host copy the device's are read once per forward
+            lens = st.host_lens if st.host_lens is not None else st.seq_lens.cpu()
+            st.plans[key] = ops.plan_decode(_lib.KIND_MLA, bs, host_seq_lens=lens, ctas_per_item=(H + 15) // 16,
+                                            num_cus=ops._num_cus(q.device))
+            st.plans[key + ("ws",)] = ops.stream_workspace(st.plans[key], H, q.device)
         out = ops.mla_decode(
             q[..., :512], q[..., 512:], pool.get_key_buffer(layer_id), pool.get_row_scale(layer_id), st.table,
             st.seq_lens, k.reshape(bs, 576), sm_scale=float(layer.scaling), page_size=pool.page_size,
-            new_slots=st.slots if save else None, plan=st.plans[key])
+            new_slots=st.slots if save else None, plan=st.plans[key], workspace=st.plans[key + ("ws",)])
         return out.reshape(bs, H * 512)
 
     def _decode_dsa(self, q, k, layer, layer_id, st, bs, save, topk_indices):
@@ -352,9 +355,10 @@ class NeuronAttnBackend:
         if key not in st.plans:
             st.plans[key] = ops.plan_decode(_lib.KIND_DSA, bs, n_keys_per_row=idx.shape[1],
                                             ctas_per_item=(H + 15) // 16, num_cus=ops._num_cus(q.device))
+            st.plans[key + ("ws",)] = ops.stream_workspace(st.plans[key], H, q.device)
         ctx, lse = ops.mla_decode_sparse(
             q[..., :512], q[..., 512:], pool.get_key_buffer(layer_id), pool.get_kv_scale(layer_id), idx, st.table,
             st.positions, k.reshape(bs, 576), sm_scale=float(layer.scaling), page_size=pool.page_size,
-            new_slots=st.slots if save else None, plan=st.plans[key])
+            new_slots=st.slots if save else None, plan=st.plans[key], workspace=st.plans[key + ("ws",)])
         self.last_lse = lse
         return ctx.reshape(bs, H * 512)

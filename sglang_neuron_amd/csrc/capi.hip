@@ -1,6 +1,7 @@
 // C ABI plumbing: version, error state, split-K planning and the LSE merge of partial results.
 #include <algorithm>
 #include <cmath>
+#include <queue>
 #include <vector>
 
 #include "sna_device.h"
@@ -25,6 +26,116 @@ int32_t host_splits(int32_t seq_len, int32_t window, int32_t tile, int32_t split
 }
 
 int32_t host_tiles(int32_t seq_len, int32_t window, int32_t tile) { return host_splits(seq_len, window, tile, 1); }
+
+// The MLA / DSA stream split: every row's key tiles (at least one, so a row with no prior key still has a workgroup
+// to attend its own row) laid end to end, cut into n_ctas ranges of equal tile counts. A workgroup runs per CU (the
+// kernel's LDS holds one), so n_ctas is the CU count over the head groups, fewer when there are fewer tiles; a sparse workgroup resolves at
+// most kMlaMaxSplitKeys indices in LDS, and sparse rows are latency-bound gathers, so a sparse plan aims for 16 tiles
+// per workgroup.
+int plan_stream(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32_t n_keys_per_row, int32_t groups,
+                int32_t num_cus, sna_split_plan* plan) {
+  if (kind == 1 && !host_seq_lens)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "plan_decode: an MLA plan needs host seq_lens (its launch uses them)");
+  if (B > SNA_MAX_PLAN_ROWS)
+    return fail(SNA_ERR_UNSUPPORTED, "plan_decode: an MLA / DSA plan holds at most %d rows, not %d",
+                SNA_MAX_PLAN_ROWS, B);
+  int64_t total = 0;
+  int32_t empty = 0, max_tiles = 0;
+  for (int32_t b = 0; b < B; ++b) {
+    const int32_t keys = kind == 2 ? n_keys_per_row : std::max(host_seq_lens[b] - 1, 0);
+    if (kind == 1 && host_seq_lens[b] < 1)
+      return fail(SNA_ERR_INVALID_ARGUMENT, "plan_decode: row %d has seq_len %d (at least its new token)", b,
+                  host_seq_lens[b]);
+    const int32_t tiles = std::max((keys + 15) / 16, 1);
+    if (tiles > 65535)
+      return fail(SNA_ERR_UNSUPPORTED, "plan_decode: row %d has %d keys, past the stream split's 65535 tiles", b,
+                  keys);
+    plan->row_keys[b] = keys;
+    total += tiles;
+    empty += keys == 0;
+    max_tiles = std::max(max_tiles, tiles);
+  }
+  // one round: every 16-head group's workgroups are resident together
+  const int32_t cus = std::max(1, std::min((num_cus > 0 ? num_cus : 256) / groups, SNA_MAX_CTAS));
+  int64_t n = 0;
+  if (total > 0) {
+    constexpr int32_t kSparseCap = kMlaMaxSplitKeys / 16;
+    n = kind == 1 ? std::min<int64_t>(cus, total) : std::min<int64_t>(cus, std::max<int64_t>((total + 15) / 16, 1));
+    if (kind == 2) n = std::max<int64_t>(n, (total + kSparseCap - 1) / kSparseCap);
+    if (n > SNA_MAX_CTAS)
+      return fail(SNA_ERR_UNSUPPORTED, "plan_decode: %lld index tiles need more than %d workgroups of %d tiles",
+                  (long long)total, SNA_MAX_CTAS, kSparseCap);
+  }
+  // row r's first tile in the global sequence, for the ranges' starting rows
+  std::vector<int64_t> first(B + 1, 0);
+  for (int32_t b = 0; b < B; ++b) first[b + 1] = first[b] + std::max((plan->row_keys[b] + 15) / 16, 1);
+  // The ranges. With a workgroup for every row, rows are apportioned whole: each gets n_b workgroups (at least one),
+  // the next one going to the row whose pieces are longest, and its tiles are cut into n_b equal pieces, so no range
+  // spans two rows (a second row would restart the tile ring and publish a second partial) and the longest piece is
+  // as short as whole pieces allow. With more rows than workgroups the sequence is cut into equal ranges.
+  if (n > 0 && B <= n) {
+    std::vector<int32_t> pieces(B, 1);
+    std::priority_queue<std::pair<double, int32_t>> longest;
+    for (int32_t b = 0; b < B; ++b) longest.push({(double)(first[b + 1] - first[b]), b});
+    for (int64_t left = n - B; left > 0 && !longest.empty(); --left) {
+      const int32_t b = longest.top().second;
+      longest.pop();
+      const int64_t tiles = first[b + 1] - first[b];
+      if (pieces[b] >= tiles) {  // a row never gets more pieces than tiles
+        ++left;
+        continue;
+      }
+      ++pieces[b];
+      longest.push({(double)tiles / pieces[b], b});
+    }
+    int64_t w = 0;
+    for (int32_t b = 0; b < B; ++b) {
+      const int64_t tiles = first[b + 1] - first[b];
+      for (int32_t i = 0; i < pieces[b]; ++i, ++w) {
+        plan->cta_start[w] = (uint32_t)(first[b] + i * tiles / pieces[b]);
+        plan->cta_row[w] = (uint16_t)b;
+        plan->cta_off[w] = (uint16_t)(i * tiles / pieces[b]);
+      }
+    }
+    n = w;
+    plan->cta_start[n] = (uint32_t)total;
+  } else {
+    int32_t row = 0;
+    for (int64_t w = 0; w <= n; ++w) {
+      const int64_t g = w * total / std::max<int64_t>(n, 1);
+      plan->cta_start[w] = (uint32_t)g;
+      if (w == n) break;
+      while (row + 1 < B && first[row + 1] <= g) ++row;
+      plan->cta_row[w] = (uint16_t)row;
+      plan->cta_off[w] = (uint16_t)(g - first[row]);
+    }
+  }
+  int32_t widest = 0;
+  // the most workgroups one row spans (the merge's partial count)
+  for (int32_t b = 0, w = 0; b < B && n > 0; ++b) {
+    while (w + 1 < n && (int64_t)plan->cta_start[w + 1] <= first[b]) ++w;
+    int32_t w_end = w;
+    while (w_end + 1 < n && (int64_t)plan->cta_start[w_end + 1] < first[b + 1]) ++w_end;
+    widest = std::max(widest, w_end - w + 1);
+  }
+  int64_t longest_range = 0;
+  for (int64_t w = 0; w < n; ++w)
+    longest_range = std::max<int64_t>(longest_range, (int64_t)plan->cta_start[w + 1] - plan->cta_start[w]);
+  plan->split_tiles = (int32_t)longest_range;
+  plan->n_work = (int32_t)n;
+  plan->tile = 16;
+  plan->target_ctas = cus;
+  plan->max_splits = widest;
+  plan->batch = B;
+  plan->empty_rows = empty;
+  plan->depth = 0;
+  plan->work_n = 0;
+  plan->n_ctas = (int32_t)n;
+  plan->total_tiles = (int32_t)total;
+  plan->wait_polls = kStreamWaitPolls;
+  (void)max_tiles;
+  return SNA_OK;
+}
 
 }  // namespace
 
@@ -142,6 +253,7 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
     return fail(SNA_ERR_INVALID_ARGUMENT, "plan_decode: negative index count %d", n_keys_per_row);
   if (kind != 2 && !host_seq_lens && max_seq_len < 0)
     return fail(SNA_ERR_INVALID_ARGUMENT, "plan_decode: need host seq_lens or max_seq_len >= 0");
+  if (kind != 0) return plan_stream(kind, host_seq_lens, B, n_keys_per_row, ctas_per_item, num_cus, plan);
   const int32_t tile = kind == 0 ? 32 : 16;
   const int32_t waves = 4;
   const int32_t cus = num_cus > 0 ? num_cus : 256;
@@ -283,7 +395,13 @@ int sna_check_decode_operands(const int64_t* seq_lens, const int32_t* block_tabl
 }
 
 int64_t sna_decode_workspace_bytes(const sna_split_plan* plan, int32_t num_q_heads, int32_t head_dim_v) {
-  if (!plan || num_q_heads < 1 || head_dim_v < 1 || plan->max_splits <= 1) return 0;
+  if (!plan || num_q_heads < 1 || head_dim_v < 1) return 0;
+  if (plan->tile == 16) {  // MLA / DSA stream split: counters, then two partial slots per workgroup
+    if (plan->n_ctas < 1) return 0;
+    return kStreamCounterBytes +
+           2ll * plan->n_ctas * num_q_heads * ((int64_t)head_dim_v + 2) * (int64_t)sizeof(float);
+  }
+  if (plan->max_splits <= 1) return 0;
   return (int64_t)plan->batch * plan->max_splits * num_q_heads * ((int64_t)head_dim_v + 2) * (int64_t)sizeof(float);
 }
 

@@ -19,8 +19,17 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegBig = -1.0e30f;
 // The most splits a row may have (the combine passes hold one weight per split in LDS); the planner keeps to it.
 constexpr int kMaxSplits = 64;
-// The most keys one MLA / DSA split may cover (the split's row ids live in the kernel's LDS); the planner keeps to it.
+// The most keys one sparse (DSA) workgroup may resolve (their row ids live in the kernel's LDS); the planner keeps to it.
 constexpr int kMlaMaxSplitKeys = 2048;
+// The MLA / DSA stream split's counter block at the start of its workspace: per (row, head group) an arrival counter
+// and a mask of merged latent blocks, then one count of finished workgroups, each in a 64-byte line of its own; zero
+// at rest.
+constexpr int kCounterStride = 16;        // int32 words between counters
+constexpr int kStreamMaxCounters = 2047;  // (row, head group) pairs the block holds
+constexpr int64_t kStreamCounterBytes = 256 * 1024;  // (2 * kStreamMaxCounters + 1) lines of 64 bytes, rounded up
+static_assert((2 * kStreamMaxCounters + 1) * kCounterStride * 4 <= kStreamCounterBytes, "the counters fit");
+// Polls of a row's arrival counter by a workgroup that published a partial, before it leaves the merge to others.
+constexpr int kStreamWaitPolls = 96;
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 

@@ -246,6 +246,22 @@ def workspace_bytes(plan: _lib.SplitPlan, heads: int, dim_v: int) -> int:
     return int(_lib.load().sna_decode_workspace_bytes(plan, heads, dim_v))
 
 
+def _stream_workspace_arg(ws: Optional[Tensor], plan: _lib.SplitPlan, heads: int, device) -> Tensor:
+    if ws is None:
+        return stream_workspace(plan, heads, device)
+    _need(ws.dtype == torch.uint8 and ws.is_contiguous() and ws.device == device, "workspace must be contiguous uint8 "
+          "on the decode's device")
+    _need(ws.numel() >= workspace_bytes(plan, heads, 512), f"workspace of {ws.numel()} bytes, the plan needs "
+          f"{workspace_bytes(plan, heads, 512)}")
+    return ws
+
+
+def stream_workspace(plan: _lib.SplitPlan, heads: int, device: torch.device) -> Tensor:
+    """A workspace for an MLA / DSA plan: zeroed, so its counter block starts at zero (each completed launch leaves it
+    zero again, so one workspace serves every later call ordered on one stream)."""
+    return torch.zeros(max(workspace_bytes(plan, heads, 512), 256), dtype=torch.uint8, device=device)
+
+
 def _host_lens(seq_lens: Tensor, host_seq_lens) -> Optional[Tensor]:
     if host_seq_lens is not None:
         return torch.as_tensor(host_seq_lens, dtype=torch.int32).reshape(-1)
@@ -348,8 +364,9 @@ def paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: T
 def prepare_mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: Tensor, block_table: Tensor,
                        seq_lens: Tensor, compact_new: Tensor, *, sm_scale: float, page_size: int,
                        new_slots: Optional[Tensor] = None, out: Optional[Tensor] = None, host_seq_lens=None,
-                       plan: Optional[_lib.SplitPlan] = None) -> Prepared:
-    """mla_decode's checks and argument binding, launched by calling the result."""
+                       plan: Optional[_lib.SplitPlan] = None, workspace: Optional[Tensor] = None) -> Prepared:
+    """mla_decode's checks and argument binding, launched by calling the result. ``workspace``: a uint8 tensor from
+    stream_workspace (zeroed once, reused by calls ordered on one stream), or None for a new one."""
     dev = _on_gpu(ql_nope, q_pe, cache, row_scale, block_table, seq_lens, compact_new, new_slots, out)
     B, H, lat = ql_nope.shape
     _need(lat == 512 and q_pe.shape == (B, H, 64), "ql_nope [B, H, 512] and q_pe [B, H, 64]")
@@ -378,10 +395,11 @@ def prepare_mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: 
         out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
     _need(out.shape == (B, H, 512) and out.dtype == torch.bfloat16 and out.is_contiguous(), "bad out tensor")
     if plan is None:
+        # the launch runs on host lengths: read the device's once when the caller has no host copy
         hl = _host_lens(seq_lens, host_seq_lens)
-        plan = plan_decode(_lib.KIND_MLA, B, host_seq_lens=hl, max_seq_len=table.shape[1] * P,
+        plan = plan_decode(_lib.KIND_MLA, B, host_seq_lens=hl if hl is not None else lens.cpu(),
                            ctas_per_item=(H + 15) // 16, num_cus=_num_cus(dev))
-    ws = torch.empty(max(workspace_bytes(plan, H, 512), 16), dtype=torch.uint8, device=dev)
+    ws = _stream_workspace_arg(workspace, plan, H, dev)
     lib = _lib.load()
     args = (_ptr(ql_nope), _ptr(q_pe), _ptr(cache), _ptr(row_scale), _ptr(table), table.stride(0), table.shape[1],
             _ptr(lens), _ptr(compact_new), _ptr(new_slots), float(sm_scale), _ptr(out), B, H, P, nb, code, plan,
@@ -404,7 +422,7 @@ def mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: Tensor, 
 def prepare_mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, kv_scale: float, indices: Tensor,
                               block_table: Tensor, positions: Tensor, own_rows: Tensor, *, sm_scale: float,
                               page_size: int, new_slots: Optional[Tensor] = None,
-                              plan: Optional[_lib.SplitPlan] = None) -> Prepared:
+                              plan: Optional[_lib.SplitPlan] = None, workspace: Optional[Tensor] = None) -> Prepared:
     """mla_decode_sparse's checks and argument binding (with ``new_slots``, the own rows' store first), launched by
     calling the result."""
     dev = _on_gpu(q_absorbed, q_pe, cache, indices, block_table, positions, own_rows, new_slots)
@@ -425,7 +443,7 @@ def prepare_mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, k
     _need(pos.numel() == B, f"{pos.numel()} positions for {B} rows")
     if plan is None:
         plan = plan_decode(_lib.KIND_DSA, B, n_keys_per_row=K, ctas_per_item=(H + 15) // 16, num_cus=_num_cus(dev))
-    ws = torch.empty(max(workspace_bytes(plan, H, 512), 16), dtype=torch.uint8, device=dev)
+    ws = _stream_workspace_arg(workspace, plan, H, dev)
     ctx = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
     lse = torch.empty(B, H, dtype=torch.float32, device=dev)
     lib = _lib.load()

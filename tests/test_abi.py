@@ -76,24 +76,18 @@ def _splits(L, window, tile, split):
     (_lib.KIND_GQA, [2048 + 37 * i for i in range(128)], 0, 1),
     (_lib.KIND_GQA, [2048 + 37 * i for i in range(128)], 128, 1),
     (_lib.KIND_GQA, [1, 2, 17, 33, 1000], 0, 8),
-    (_lib.KIND_MLA, [1024 + 467 * i for i in range(32)], 0, 1),
-    (_lib.KIND_MLA, [1, 5, 70000], 0, 2),
 ])
 def test_plan_invariants(lib, kind, lens, window, ctas):
     rc, p = _plan(lib, kind, lens, window=window, ctas=ctas)
     assert rc == 0, lib.sna_last_error()
-    tile = 32 if kind == _lib.KIND_GQA else 16
+    tile = 32
     assert p.tile == tile and p.batch == len(lens)
     n = [_splits(L, window, tile, p.split_tiles) for L in lens]
     assert p.n_work == sum(n) and p.max_splits == max(n) <= 64
     assert p.empty_rows == sum(1 for x in n if x == 0)
-    if kind == _lib.KIND_MLA:
-        assert p.split_tiles * 16 <= 2048 and p.depth == 0
-    else:
-        assert p.depth in (2, 4)
-    if kind == _lib.KIND_MLA or p.depth == 4:  # one-round plans fit the resident target unless splits are capped
-        assert p.n_work * ctas <= p.target_ctas or p.split_tiles == (2048 // 16 if kind else max(
-            (max(lens) - 1 + tile - 1) // tile, 4))
+    assert p.depth in (2, 4)
+    if p.depth == 4:  # one-round plans fit the resident target unless splits are capped
+        assert p.n_work * ctas <= p.target_ctas or p.split_tiles == max((max(lens) - 1 + tile - 1) // tile, 4)
     # the item map the kernels read instead of searching seq_lens: (row, split) in launch order
     want = [(b << 6) | sp for b, nb in enumerate(n) for sp in range(nb)]
     if len(want) <= 512:
@@ -111,7 +105,7 @@ def test_plan_from_a_bound_marks_empty_rows_unknown(lib):
 
 @pytest.mark.parametrize("kind,window,max_len,B", [
     (_lib.KIND_GQA, 128, 600, 5), (_lib.KIND_GQA, 128, 129, 3), (_lib.KIND_GQA, 100, 5000, 7),
-    (_lib.KIND_GQA, 1, 300, 2), (_lib.KIND_GQA, 0, 4000, 9), (_lib.KIND_MLA, 0, 3000, 4)])
+    (_lib.KIND_GQA, 1, 300, 2), (_lib.KIND_GQA, 0, 4000, 9)])
 def test_plan_from_a_bound_holds_every_length_up_to_it(lib, kind, window, max_len, B):
     """Every length L <= max_len: its split count fits the plan (max_splits, and n_work for B such rows), whatever
     tile offset a window starts at."""
@@ -121,11 +115,71 @@ def test_plan_from_a_bound_holds_every_length_up_to_it(lib, kind, window, max_le
     assert worst <= p.max_splits and B * worst <= p.n_work, (worst, p)
 
 
-def test_plan_dsa_every_row_alike(lib):
+def _row_tiles(keys):
+    return [max((k + 15) // 16, 1) for k in keys]
+
+
+def _check_stream_plan(p, keys, cus, ctas=1):
+    """The MLA / DSA stream split by brute force: every row's tiles (at least one) end to end, cut into n_ctas ranges
+    that start where cta_row / cta_off say. With a workgroup per row the rows are apportioned whole: no range spans
+    two rows, a row's pieces differ by at most one tile, and no other apportionment of the workgroups has a shorter
+    longest piece. Otherwise the ranges are equal (+-1). max_splits is the most ranges any row meets."""
+    tiles = _row_tiles(keys)
+    first = [0]
+    for t in tiles:
+        first.append(first[-1] + t)
+    total = first[-1]
+    n = p.n_ctas
+    assert p.tile == 16 and p.total_tiles == total and list(p.row_keys[:len(keys)]) == list(keys)
+    assert 1 <= n <= min(cus // ctas, 256, total)
+    starts = list(p.cta_start[:n + 1])
+    assert starts[0] == 0 and starts[-1] == total
+    sizes = [starts[w + 1] - starts[w] for w in range(n)]
+    assert min(sizes) >= 1 and p.split_tiles == max(sizes)
+    for w in range(n):
+        r = p.cta_row[w]
+        assert first[r] <= starts[w] < first[r + 1] and starts[w] - first[r] == p.cta_off[w]
+    meets = [sum(1 for w in range(n) if starts[w] < first[b + 1] and starts[w + 1] > first[b])
+             for b in range(len(keys))]
+    assert p.max_splits == max(meets)
+    if len(keys) <= n:
+        assert all(starts[w + 1] <= first[p.cta_row[w] + 1] for w in range(n)), "a range spans two rows"
+        for b, t in enumerate(tiles):
+            mine = [sizes[w] for w in range(n) if p.cta_row[w] == b]
+            assert sum(mine) == t and max(mine) - min(mine) <= 1
+        # optimality of the longest piece: fewer than n workgroups cannot give every row pieces of <= longest - 1
+        shorter = max(sizes) - 1
+        if shorter >= 1:
+            assert sum(-(-t // shorter) for t in tiles) > n
+    else:
+        assert max(sizes) - min(sizes) <= 1
+    assert p.empty_rows == sum(1 for k in keys if k == 0)
+
+
+@pytest.mark.parametrize("lens,ctas,cus", [([1024 + 467 * i for i in range(32)], 1, 256), ([1, 5, 70000], 2, 256),
+                                          ([1] * 7, 1, 256), ([16385] * 8, 1, 80), ([3000] * 256, 1, 256)])
+def test_mla_stream_plan(lib, lens, ctas, cus):
+    rc, p = _plan(lib, _lib.KIND_MLA, lens, ctas=ctas, cus=cus)
+    assert rc == 0, lib.sna_last_error()
+    _check_stream_plan(p, [L - 1 for L in lens], cus, ctas)
+    ws = lib.sna_decode_workspace_bytes(ctypes.byref(p), 16 * ctas, 512)
+    assert ws == 262144 + 2 * p.n_ctas * 16 * ctas * (512 + 2) * 4
+
+
+def test_dsa_stream_plan(lib):
     rc, p = _plan(lib, _lib.KIND_DSA, B=16, keys=2048, ctas=1)
     assert rc == 0
-    per = _splits(2049, 0, 16, p.split_tiles)
-    assert p.n_work == 16 * per and p.max_splits == per
+    _check_stream_plan(p, [2048] * 16, 256)
+    assert max(p.cta_start[w + 1] - p.cta_start[w] for w in range(p.n_ctas)) <= 2048 // 16
+    rc, p = _plan(lib, _lib.KIND_DSA, B=3, keys=0, ctas=1)  # empty index lists: one tile each for the own rows
+    assert rc == 0 and p.total_tiles == 3 and p.empty_rows == 3
+
+
+def test_stream_plan_refusals(lib):
+    assert _plan(lib, _lib.KIND_MLA, None, B=4, max_len=3000)[0] == _lib.SNA_ERR_INVALID_ARGUMENT  # no host lengths
+    assert _plan(lib, _lib.KIND_MLA, [100] * 257)[0] == _lib.SNA_ERR_UNSUPPORTED  # past SNA_MAX_PLAN_ROWS
+    assert _plan(lib, _lib.KIND_MLA, [16 * 65536])[0] == _lib.SNA_ERR_UNSUPPORTED  # a row past 65535 tiles
+    assert _plan(lib, _lib.KIND_MLA, [0, 5])[0] == _lib.SNA_ERR_INVALID_ARGUMENT  # seq_len 0
 
 
 def test_plan_rejects_bad_arguments(lib):
@@ -163,12 +217,18 @@ def test_decode_entry_checks_arguments_before_touching_the_gpu(lib):
                                   2, 4, 2, 128, 16, 10, 1, ctypes.byref(bad), null, 0, null)
     assert rc == _lib.SNA_ERR_INVALID_ARGUMENT and b"item" in lib.sna_last_error()
     rcm, pm = _plan(lib, _lib.KIND_MLA, [100, 200])
-    assert rcm == 0 and pm.work_n == pm.n_work
-    bad = _lib.SplitPlan.from_buffer_copy(pm)
-    bad.work_n = 513
-    rc = lib.sna_mla_decode(null, null, null, null, null, 0, 0, null, null, null, 0.1, null, 2, 16, 64, 10, 1,
-                            ctypes.byref(bad), null, 0, null)
-    assert rc == _lib.SNA_ERR_INVALID_ARGUMENT and b"item map" in lib.sna_last_error()
+    assert rcm == 0 and pm.n_ctas > 0
+    for field, value in (("total_tiles", 3), ("cta_off", None), ("cta_row", None)):
+        bad = _lib.SplitPlan.from_buffer_copy(pm)
+        if field == "total_tiles":
+            bad.total_tiles = value
+        elif field == "cta_off":
+            bad.cta_off[1] += 1
+        else:
+            bad.cta_row[0] = 5
+        rc = lib.sna_mla_decode(null, null, null, null, null, 0, 0, null, null, null, 0.1, null, 2, 16, 64, 10, 1,
+                                ctypes.byref(bad), null, 0, null)
+        assert rc == _lib.SNA_ERR_INVALID_ARGUMENT and b"plan" in lib.sna_last_error(), field
     # an empty batch is a no-op
     rc0, p0 = _plan(lib, _lib.KIND_GQA, B=0, max_len=0)
     assert rc0 == 0

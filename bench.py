@@ -1,23 +1,28 @@
 #!/usr/bin/env python
 """Benchmark of the paged decode-attention step on one MI355X (the metric of BASELINE.json).
 
-A step is one decode of the whole batch with the default workload cfg2 (Qwen3-8B-shaped GQA, FP8 e4m3fn KV with
-per-KV-head scales, B64 H32 G8 d128, L=4096, page 16). That covers the new token's store, the split-K decode and the
-combine pass. Inputs are already resident in HBM. The pool is rotated over copies whose total exceeds the 256 MB
-Infinity Cache several times, so every step reads cold HBM.
+A step is one decode of the whole batch: the new token's store, the decode kernel(s), and (GQA rows split over
+several workgroups) the combine pass. The default line is cfg2 (Qwen3-8B-shaped GQA, FP8 e4m3fn KV with per-KV-head
+scales, B64 H32 G8 d128, L=4096, page 16), the metric's workload, and carries every other config under "per_config".
+Inputs are resident in HBM; the pool is rotated over copies whose total exceeds the 256 MB Infinity Cache several
+times, so every step reads cold HBM.
 
 One JSON line on stdout:
-  value         algorithmic HBM bytes of the step / step time, GB/s (higher is better); ms_per_step beside it.
-  roofline      the split-K decode kernel alone: its algorithmic bytes per launch / its average launch duration,
-                measured with HIP events on the launch stream (the library's diagnostics timer) over the timed
-                steps, against MI355X's 8 TB/s. traffic = FETCH_SIZE + WRITE_SIZE per launch from the committed
-                rocprofv3 counter summary when one exists for the workload, else null.
+  value         algorithmic HBM bytes of the step / step time, GB/s (higher is better); ms_per_step beside it. The
+                step time is one HIP event pair (torch events on the stream the kernels launch on) around K
+                back-to-back steps, divided by K.
+  roofline      the step's kernels (cfg2: the one split-K decode kernel): their algorithmic bytes per step / the step
+                time, against MI355X's 8 TB/s. traffic = FETCH_SIZE + WRITE_SIZE per step from the committed
+                rocprofv3 counter summary (traffic_source says which), else null.
   cpu_baseline  the CPU oracle (a torch restatement of the reference's torch path) on a bounded sample of the same
-                workload, timed on this host's cores.
+                workload, timed on this host's cores (2 warm-ups, median of 5 runs).
+  per_config    cfg1, cfg3, cfg4 (full and sliding-window layers) and cfg5, each with us_per_step, its roofline and
+                cpu_baseline.
 
-Options: --config {1,2,3,4,4swa,5} picks another workload (the default line is cfg2); --config meta times the
-device-side decode metadata (block table, window trim) instead, --config prefill the segmented prefill attention, --config indexer the DSA indexer, --config qkv the QKV writer; --all prints one line per decode workload; --gpus
-above 1 is refused, because this build measures one GPU.
+Options: --config {1,2,3,4,4swa,5} prints that workload's line alone; --config meta times the device-side decode
+metadata (block table, window trim) instead, --config prefill the segmented prefill attention, --config indexer the
+DSA indexer, --config qkv the QKV writer, --config wire the PD page items; --all prints one line per workload;
+--no-per-config drops the per_config map; --gpus above 1 is refused, because this build measures one GPU.
 """
 
 from __future__ import annotations
@@ -64,13 +69,55 @@ def _copies(touched_bytes: int, pool_bytes: int, cap: int) -> int:
 
 
 def _traffic(workload: str):
-    """FETCH_SIZE + WRITE_SIZE bytes per launch from profiles/traffic_<workload>.json, if measured."""
+    """(FETCH_SIZE + WRITE_SIZE bytes per step, where they come from) from profiles/traffic_<workload>.json, the
+    committed summary of two rocprofv3 counter passes; (None, None) when no such pass was committed."""
     p = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
     if not os.path.exists(p):
-        return None
+        return None, None
     with open(p) as f:
         d = json.load(f)
-    return d.get("bytes_per_launch")
+    b = d.get("bytes_per_step", d.get("bytes_per_launch"))
+    return b, f"committed rocprofv3 counter passes (profiles/traffic_{workload}.json), not this run"
+
+
+def time_us(fn, n_steps: int, warmup: int) -> float:
+    """Microseconds per call of fn(i): warmup calls, then one HIP event pair (torch events, recorded on torch's current
+    stream, the stream every launch here goes to) around n_steps back-to-back calls."""
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(n_steps):
+        fn(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n_steps * 1e3
+
+
+def cpu_threads() -> int:
+    """The CPU baseline's thread count: the host's cores, capped by OMP_NUM_THREADS (a GPU box grants each GPU a share
+    of its cores through it)."""
+    n = os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS")
+    return max(1, min(n, int(cap))) if cap and cap.isdigit() else n
+
+
+def cpu_median_s(run) -> float:
+    """Seconds per call of run(): 2 warm-up calls, then the median of 5 timed calls, on cpu_threads() threads."""
+    import torch
+
+    torch.set_num_threads(cpu_threads())
+    for _ in range(2):
+        run()
+    times = []
+    for _ in range(5):
+        t = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t)
+    return statistics.median(times)
 
 
 # ---------------------------------------------------------------------------------------------------------------
@@ -103,10 +150,6 @@ def setup_gqa(cfg: int, window: int, dev):
     steps = [ops.prepare_paged_decode_gqa(q, k, v, table, lens, kn, vn, sm_scale=case.sm_scale, k_scale=ks,
                                           v_scale=vs, sinks=sinks, window=case.window, new_slots=slots, out=out,
                                           plan=plan) for (k, v) in pools]
-    esz = 1 if case.fp8 else 2
-    keys = sum(min(L - 1, case.window - 1) if case.window else L - 1 for L in case.seq_lens.tolist())
-    pages = sum(-(-(min(L - 1, case.window - 1) if case.window else L - 1) // case.P) for L in case.seq_lens.tolist())
-    split_bytes = keys * case.G * case.d * esz * 2 + case.B * case.H * case.d * 2 + pages * 4
     tiles = 0
     for L in case.seq_lens.tolist():
         hi = L - 1
@@ -142,7 +185,9 @@ def setup_gqa(cfg: int, window: int, dev):
 
         return _time_rows(run, case.B, budget_s)
 
-    return steps, desc, case.kv_bytes_per_step(), split_bytes, mfma_flops, cpu_baseline
+    kernels = ["gqa_decode_kernel"] + (["gqa_combine_kernel"] if plan.max_splits > 1 else []) + \
+        (["gqa_lone_token_kernel"] if bool((case.seq_lens == 1).any()) else [])
+    return steps, desc, case.kv_bytes_per_step(), kernels, mfma_flops, cpu_baseline
 
 
 def setup_mla(dev):
@@ -165,9 +210,6 @@ def setup_mla(dev):
     steps = [ops.prepare_mla_decode(case.ql_nope, case.q_pe, c, s, table, lens, case.compact_new,
                                     sm_scale=case.sm_scale, page_size=case.P, new_slots=case.new_slots.to(dev),
                                     out=out, plan=plan) for (c, s) in pools]
-    keys = int((case.seq_lens - 1).sum())
-    pages = int(((case.seq_lens - 1 + case.P - 1) // case.P).sum())
-    split_bytes = keys * 580 + case.B * case.H * 576 * 2 + pages * 4
     tiles = int(((case.seq_lens - 1 + 15) // 16).sum())
     mfma_flops = tiles * (18 * 16 * 16 * 32 * 2 + 32 * 16 * 16 * 16 * 2)
     desc = {"workload": "cfg3: deepseek-v2-lite absorbed MLA", "batch": case.B, "q_heads": case.H,
@@ -189,7 +231,7 @@ def setup_mla(dev):
 
         return _time_rows(run, case.B, budget_s)
 
-    return steps, desc, case.kv_bytes_per_step(), split_bytes, mfma_flops, cpu_baseline
+    return steps, desc, case.kv_bytes_per_step(), ["mla_decode_kernel"], mfma_flops, cpu_baseline
 
 
 def setup_dsa(dev):
@@ -212,8 +254,6 @@ def setup_dsa(dev):
     steps = [ops.prepare_mla_decode_sparse(case.q_absorbed, case.q_pe, c, case.kv_scale, idx, table, pos,
                                            case.own_rows, sm_scale=case.sm_scale, page_size=case.P,
                                            new_slots=case.new_slots.to(dev), plan=plan) for c in pools]
-    valid = int((case.indices >= 0).sum())
-    split_bytes = valid * (640 + 4 + 4) + int((case.indices < 0).sum()) * 4 + case.B * case.H * 576 * 2
     tiles = case.B * (-(-case.indices.shape[1] // 16))
     mfma_flops = tiles * (18 * 16 * 16 * 32 * 2 + 32 * 16 * 16 * 16 * 2)
     desc = {"workload": "cfg5: glm-5.2-style DSA absorbed MLA", "batch": case.B, "q_heads": case.H,
@@ -235,25 +275,30 @@ def setup_dsa(dev):
 
         return _time_rows(run, case.B, budget_s)
 
-    return steps, desc, case.kv_bytes_per_step(), split_bytes, mfma_flops, cpu_baseline
+    return steps, desc, case.kv_bytes_per_step(), ["kv_store_dsa_kernel", "mla_decode_kernel"], mfma_flops, cpu_baseline
 
 
 def _time_rows(run, B: int, budget_s: float):
-    """Time the CPU oracle on the first n rows (n sized to the budget), median of 3, scaled to the whole batch."""
+    """Time the CPU oracle on the first n rows (n sized to the budget: 2 warm-ups and 5 timed runs in about budget_s),
+    median of the 5 timed runs, scaled to the whole batch."""
     import torch
 
+    torch.set_num_threads(cpu_threads())
     t = time.perf_counter()
     run(1)
     t1 = time.perf_counter() - t
-    nrows = max(1, min(B, int(budget_s / 3 / max(t1, 1e-6))))
+    nrows = max(1, min(B, int(budget_s / 7 / max(t1, 1e-6))))
+    for _ in range(2):
+        run(nrows)
     times = []
-    for _ in range(3):
+    for _ in range(5):
         t = time.perf_counter()
         run(nrows)
         times.append(time.perf_counter() - t)
     med = statistics.median(times)
-    return {"value": med * (B / nrows) * 1e6, "unit": "us/step", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"rows 0..{nrows - 1} of {B} (median of 3 runs, scaled x{B / nrows:.2f} to the batch)",
+    return {"value": round(med * (B / nrows) * 1e6, 1), "unit": "us/step", "cores": torch.get_num_threads(),
+            "host_cpus": os.cpu_count(), "kind": "port",
+            "sample": f"rows 0..{nrows - 1} of {B} (2 warm-ups, median of 5 runs, scaled x{B / nrows:.2f} to the batch)",
             "cpu": cpu_model()}
 
 
@@ -268,12 +313,10 @@ def run_meta(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> di
     past the Infinity Cache. The roofline figure is the block-table kernel's algorithmic bytes (4 B read + 4 B
     written per entry, 16 B per row) over its time; its req_to_token reads are strided (one 4-byte entry per page),
     so HBM moves a whole sector for each."""
-    import ctypes
-
     import numpy as np
     import torch
 
-    from sglang_neuron_amd import _lib, ops
+    from sglang_neuron_amd import ops
 
     B, P, ctx, nrows, window = 256, 16, 8192, 1024, 128
     g = np.random.default_rng(7)
@@ -289,23 +332,9 @@ def run_meta(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> di
     tables = [ops.block_table(r, rows_d, lens_d, P, width, seq_lens_i32=lens32) for r in r2ts]
     log(f"meta: B={B} page={P} width={width} window={window} ({nb} blocks), req_to_token {nrows}x{ctx} x {copies}")
 
-    lib = _lib.load()
-
     def device_us(fn):
-        """Average device time of fn's one kernel, from the library's diagnostics timer: the launch's own dispatch
-        packet stamps a HIP event pair on the launch stream (torch's current stream), so host time between launches
-        is not counted."""
-        for i in range(warmup):
-            fn(i)
-        torch.cuda.synchronize()
-        lib.sna_diag_kernel_timing(1)
-        for i in range(steps_n):
-            fn(i)
-        ms, unused, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
-        _lib.check(lib.sna_diag_kernel_timing_read(ctypes.byref(ms), ctypes.byref(unused), ctypes.byref(n)),
-                   "kernel_timing_read")
-        lib.sna_diag_kernel_timing(0)
-        return ms.value / max(n.value, 1) * 1e3
+        """Device time of fn's one kernel: one event pair around steps_n back-to-back launches."""
+        return time_us(fn, steps_n, warmup)
 
     def both(i):
         ops.window_table(ops.block_table(r2ts[i % copies], rows_d, lens_d, P, width, seq_lens_i32=lens32), lens_d, P,
@@ -313,7 +342,7 @@ def run_meta(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> di
 
     bt_us = device_us(lambda i: ops.block_table(r2ts[i % copies], rows_d, lens_d, P, width, seq_lens_i32=lens32))
     wt_us = device_us(lambda i: ops.window_table(tables[i % copies], lens_d, P, nb))
-    step_us = bt_us + wt_us  # the two kernels back to back (an event pair around both would count host gaps)
+    step_us = device_us(both)
     torch.cuda.synchronize()
     t = time.perf_counter()
     for i in range(steps_n):
@@ -322,8 +351,8 @@ def run_meta(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> di
     host_us = (time.perf_counter() - t) / steps_n * 1e6
     bt_bytes = B * width * 8 + B * 16
     achieved = bt_bytes / (bt_us * 1e-6) / 1e9
-    log(f"block_table {bt_us:.2f} us ({achieved:.0f} GB/s algorithmic), window_table {wt_us:.2f} us, both {step_us:.2f} "
-        f"us on the device; {host_us:.2f} us per build by the host clock (Python + launches)")
+    log(f"block_table {bt_us:.2f} us ({achieved:.0f} GB/s algorithmic), window_table {wt_us:.2f} us, both back to back "
+        f"{step_us:.2f} us; {host_us:.2f} us per build by the host clock (Python + launches)")
     line = {
         "metric": META_METRIC, "value": round(step_us, 3), "unit": "us/step", "n_gpus": 1, "steps": steps_n,
         "warmup": warmup, "ms_per_step": round(step_us * 1e-3, 6), "higher_is_better": False, "scaling": "weak",
@@ -334,22 +363,21 @@ def run_meta(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> di
         "block_table_us": round(bt_us, 3), "window_table_us": round(wt_us, 3), "host_clock_us_per_build": round(host_us, 3),
         "roofline": {"bound": "hbm", "kernel": "block_table_kernel", "achieved": round(achieved, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                     "traffic": _traffic("meta"), "alg_bytes_per_launch": bt_bytes, "avg_launch_us": round(bt_us, 3)},
+                     "traffic": _traffic("meta")[0], "traffic_source": _traffic("meta")[1], "alg_bytes_per_launch": bt_bytes, "avg_launch_us": round(bt_us, 3)},
         "cpu_baseline": None,
     }
     if cpu:
         from oracle import metadata as omd
 
         lens_t = torch.from_numpy(lens)
-        times = []
-        for _ in range(3):
-            t = time.perf_counter()
+
+        def run():
             tb = omd.block_table(r2t_host, rows, lens, P)
             omd.swa_trimmed_table(tb, lens_t, window, P, nb)
-            times.append(time.perf_counter() - t)
-        line["cpu_baseline"] = {"value": statistics.median(times) * 1e6, "unit": "us/step",
+
+        line["cpu_baseline"] = {"value": cpu_median_s(run) * 1e6, "unit": "us/step",
                                 "cores": torch.get_num_threads(), "kind": "port",
-                                "sample": "the whole batch (median of 3 runs): numpy block table + torch window trim, "
+                                "sample": "the whole batch (2 warm-ups, median of 5 runs): numpy block table + torch window trim, "
                                           "as the reference's host builders", "cpu": cpu_model()}
         log(f"CPU baseline: {line['cpu_baseline']['value']:.0f} us/step")
     return line
@@ -398,16 +426,7 @@ def run_qkv(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> dic
                                 k_cache=kc, v_cache=vc, slot_mapping=slots, q_norm=qn, k_norm=kn, norm_eps=1e-6,
                                 k_scale=ks, v_scale=vs, q_out=q_out)
 
-    for i in range(warmup):
-        step(i)
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(steps_n):
-        step(i)
-    end.record()
-    torch.cuda.synchronize()
-    us = start.elapsed_time(end) / steps_n * 1e3
+    us = time_us(step, steps_n, warmup)
     achieved = alg / (us * 1e-6) / 1e9
     log(f"qkv_norm_rope_store: {us:.2f} us/step ({achieved:.0f} GB/s)")
     line = {
@@ -420,7 +439,7 @@ def run_qkv(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> dic
                    "input_copies": n},
         "roofline": {"bound": "hbm", "kernel": "qkv_norm_rope_store_kernel", "achieved": round(achieved, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                     "traffic": _traffic("qkv"), "alg_bytes_per_launch": alg, "avg_launch_us": round(us, 3)},
+                     "traffic": _traffic("qkv")[0], "traffic_source": _traffic("qkv")[1], "alg_bytes_per_launch": alg, "avg_launch_us": round(us, 3)},
         "cpu_baseline": None,
     }
     if cpu:
@@ -445,11 +464,9 @@ def run_indexer(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) ->
     """The DSA indexer's decode step at cfg5's scale: 16 rows, each scoring 131072 cached fp8 index keys (page 64,
     128 dims) with 64 index heads, then the top-2048 positions. The roofline figure is the score kernel's algorithmic
     bytes (128 per key read + 2 per score written) over its time; it is HBM-bound."""
-    import ctypes
-
     import torch
 
-    from sglang_neuron_amd import _lib, ops
+    from sglang_neuron_amd import ops
 
     B, N, H, P, k = 16, 131072, 64, 64, 2048
     g = torch.Generator(device="cpu").manual_seed(1200)
@@ -475,29 +492,10 @@ def run_indexer(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) ->
         ops.indexer_scores(q, w, caches[i % copies], tables[i % copies], limits, N, out=scores)
         return ops.topk_positions(scores, k)
 
-    lib = _lib.load()
-    for i in range(warmup):
-        step(i)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(steps_n):
-        step(i)
-    e1.record()
-    torch.cuda.synchronize()
-    step_us = e0.elapsed_time(e1) / steps_n * 1e3
-    times = {}
-    for name, fn in (("score", lambda i: ops.indexer_scores(q, w, caches[i % copies], tables[i % copies], limits, N,
-                                                             out=scores)),
-                     ("topk", lambda i: ops.topk_positions(scores, k))):
-        lib.sna_diag_kernel_timing(1)
-        for i in range(steps_n):
-            fn(i)
-        ms, unused, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
-        _lib.check(lib.sna_diag_kernel_timing_read(ctypes.byref(ms), ctypes.byref(unused), ctypes.byref(n)),
-                   "kernel_timing_read")
-        lib.sna_diag_kernel_timing(0)
-        times[name] = ms.value / max(n.value, 1) * 1e3
+    step_us = time_us(step, steps_n, warmup)
+    times = {"score": time_us(lambda i: ops.indexer_scores(q, w, caches[i % copies], tables[i % copies], limits, N,
+                                                           out=scores), steps_n, warmup),
+             "topk": time_us(lambda i: ops.topk_positions(scores, k), steps_n, warmup)}
     score_bytes = B * N * (128 + 2)
     achieved = score_bytes / (times["score"] * 1e-6) / 1e9
     log(f"indexer_score_kernel {times['score']:.1f} us ({achieved:.0f} GB/s), topk {times['topk']:.1f} us, "
@@ -513,7 +511,7 @@ def run_indexer(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) ->
         "score_us": round(times["score"], 3), "topk_us": round(times["topk"], 3),
         "roofline": {"bound": "hbm", "kernel": "indexer_score_kernel", "achieved": round(achieved, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                     "traffic": _traffic("indexer"), "alg_bytes_per_launch": score_bytes,
+                     "traffic": _traffic("indexer")[0], "traffic_source": _traffic("indexer")[1], "alg_bytes_per_launch": score_bytes,
                      "avg_launch_us": round(times["score"], 3)},
         "cpu_baseline": None,
     }
@@ -530,16 +528,12 @@ def run_indexer(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) ->
         t = time.perf_counter()
         run(4096)
         t1 = time.perf_counter() - t
-        n_keys = max(4096, min(N, int(4096 * cpu_budget / 3 / max(t1, 1e-6))))
-        ts = []
-        for _ in range(3):
-            t = time.perf_counter()
-            run(n_keys)
-            ts.append(time.perf_counter() - t)
-        med = statistics.median(ts)
+        n_keys = max(4096, min(N, int(4096 * cpu_budget / 7 / max(t1, 1e-6))))
+        med = cpu_median_s(lambda: run(n_keys))
         line["cpu_baseline"] = {"value": round(med * (B * N / n_keys) * 1e6, 1), "unit": "us/step",
                                 "cores": torch.get_num_threads(), "kind": "port",
-                                "sample": f"row 0's first {n_keys} keys (median of 3 runs, scaled x{B * N / n_keys:.1f}"
+                                "sample": f"row 0's first {n_keys} keys (2 warm-ups, median of 5 runs, scaled "
+                                          f"x{B * N / n_keys:.1f}"
                                           " to the step)", "cpu": cpu_model()}
         log(f"CPU baseline: {line['cpu_baseline']['value']:.0f} us/step")
     return line
@@ -554,11 +548,9 @@ def run_wire(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> di
     128 dims = 16 KB), a 4096-token request (256 pages, 302 MB). Four page sets rotate over pools of 2048 pages, so
     each step moves pages no earlier step touched. Pack (into a wire buffer) and unpack (out of it) are timed beside
     it. HBM-bound: every byte moved is read once and written once."""
-    import ctypes
-
     import torch
 
-    from sglang_neuron_amd import _lib, ops
+    from sglang_neuron_amd import ops
     from sglang_neuron_amd.mem_cache.memory_pool import NeuronMHATokenToKVPool
 
     layers, G, d, P, n_pages, pool_pages, sets = 36, 8, 128, 16, 256, 2048, 4
@@ -578,39 +570,13 @@ def run_wire(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> di
     def step(i):
         ops.copy_page_items(src_inf, dst_inf, src_sets[i % sets], dst_sets[i % sets])
 
-    lib = _lib.load()
-    for i in range(warmup):
-        step(i)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(steps_n):
-        step(i)
-    e1.record()
-    torch.cuda.synchronize()
-    step_us = e0.elapsed_time(e1) / steps_n * 1e3
-    times = {}
-    for name, fn in (("copy", step), ("pack", lambda i: ops.pack_page_items(src_inf, src_sets[i % sets], wire)),
-                     ("unpack", lambda i: ops.unpack_page_items(wire, dst_inf, dst_sets[i % sets]))):
-        lib.sna_diag_kernel_timing(1)
-        for i in range(steps_n):
-            fn(i)
-        ms, unused, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
-        _lib.check(lib.sna_diag_kernel_timing_read(ctypes.byref(ms), ctypes.byref(unused), ctypes.byref(n)),
-                   "kernel_timing_read")
-        lib.sna_diag_kernel_timing(0)
-        times[name] = ms.value / max(n.value, 1) * 1e3
+    step_us = time_us(step, steps_n, warmup)
+    times = {"copy": step_us,
+             "pack": time_us(lambda i: ops.pack_page_items(src_inf, src_sets[i % sets], wire), steps_n, warmup),
+             "unpack": time_us(lambda i: ops.unpack_page_items(wire, dst_inf, dst_sets[i % sets]), steps_n, warmup)}
     # a plain device copy of as many bytes, for the practical ceiling
     flat = torch.empty(moved, dtype=torch.uint8, device=dev)
-    for _ in range(3):
-        flat.copy_(wire)
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(20):
-        flat.copy_(wire)
-    e1.record()
-    torch.cuda.synchronize()
-    dcopy_us = e0.elapsed_time(e1) / 20 * 1e3
+    dcopy_us = time_us(lambda i: flat.copy_(wire), 20, 3)
     del flat
     hbm = 2 * moved
     achieved = hbm / (times["copy"] * 1e-6) / 1e9
@@ -629,7 +595,7 @@ def run_wire(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> di
         "device_copy_us": round(dcopy_us, 3),
         "roofline": {"bound": "hbm", "kernel": "page_items_kernel", "achieved": round(achieved, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                     "traffic": _traffic("wire"), "alg_bytes_per_launch": hbm,
+                     "traffic": _traffic("wire")[0], "traffic_source": _traffic("wire")[1], "alg_bytes_per_launch": hbm,
                      "avg_launch_us": round(times["copy"], 3)},
         "cpu_baseline": None,
     }
@@ -642,15 +608,11 @@ def run_wire(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> di
                     pools[0].v_buffer[j // 2].view(torch.uint8).reshape(-1).cpu() for j in range(n_reg)]
         dst_host = [torch.empty_like(t) for t in src_host]
         sp, dp = src_sets[0].tolist(), dst_sets[0].tolist()
-        ts = []
-        for _ in range(3):
-            t = time.perf_counter()
-            opi.copy(src_host, dst_host, [il] * n_reg, sp, dp)
-            ts.append(time.perf_counter() - t)
-        med = statistics.median(ts)
+        med = cpu_median_s(lambda: opi.copy(src_host, dst_host, [il] * n_reg, sp, dp))
         line["cpu_baseline"] = {"value": round(n_reg * n_pages * il / med / 1e9, 2), "unit": "GB/s", "cores": 1,
                                 "kind": "port", "sample": f"{n_reg} of the {len(src_inf[0])} regions, every page of "
-                                                          "the request (median of 3 runs)", "cpu": cpu_model()}
+                                                          "the request (2 warm-ups, median of 5 runs; a scalar loop)",
+                                "cpu": cpu_model()}
         log(f"CPU baseline: {line['cpu_baseline']['value']:.2f} GB/s")
     return line
 
@@ -663,11 +625,9 @@ def run_prefill(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) ->
     after a 2048-token prior, H 32 / G 8 / d 128, FP8 pool (page 16) written by the store kernel. The algorithmic work
     is 4 d flops per (query, head, visible key) (QK and PV); MFMA-bound, so the roofline is TFLOP/s against the bf16
     dense peak."""
-    import ctypes
-
     import torch
 
-    from sglang_neuron_amd import _lib, ops
+    from sglang_neuron_amd import ops
 
     R, S, prior, H, G, d, P = 4, 2048, 2048, 32, 8, 128, 16
     g = torch.Generator(device="cpu").manual_seed(1100)
@@ -697,28 +657,10 @@ def run_prefill(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) ->
         ops.prefill_attention(q, kc, vc, table_d, q_start, priors, max_q_len=S, sm_scale=scale, k_scale=ks,
                               v_scale=vs, out=out)
 
-    lib = _lib.load()
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    lib.sna_diag_kernel_timing(1)
-    for _ in range(steps_n):
-        step()
-    ms, unused, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
-    _lib.check(lib.sna_diag_kernel_timing_read(ctypes.byref(ms), ctypes.byref(unused), ctypes.byref(n)),
-               "kernel_timing_read")
-    lib.sna_diag_kernel_timing(0)
-    kernel_ms = ms.value / max(n.value, 1)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps_n):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    step_ms = e0.elapsed_time(e1) / steps_n
+    step_ms = time_us(lambda i: step(), steps_n, warmup) * 1e-3
+    kernel_ms = step_ms  # the step is the one prefill kernel
     tflops = flops / (kernel_ms * 1e-3) / 1e12
-    log(f"prefill_gqa_kernel {kernel_ms * 1e3:.1f} us ({tflops:.0f} TFLOP/s), step {step_ms * 1e3:.1f} us")
+    log(f"prefill_gqa_kernel {kernel_ms * 1e3:.1f} us/step ({tflops:.0f} TFLOP/s)")
     line = {
         "metric": PREFILL_METRIC, "value": round(flops / (step_ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": steps_n, "warmup": warmup, "ms_per_step": round(step_ms, 6), "higher_is_better": True,
@@ -729,7 +671,7 @@ def run_prefill(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) ->
                    "page_size": P, "kv_dtype": "fp8_e4m3fn per-KV-head scale"},
         "roofline": {"bound": "mfma", "kernel": "prefill_gqa_kernel", "achieved": round(tflops, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": _traffic("prefill"), "alg_flops_per_launch": flops,
+                     "traffic": _traffic("prefill")[0], "traffic_source": _traffic("prefill")[1], "alg_flops_per_launch": flops,
                      "avg_launch_us": round(kernel_ms * 1e3, 3)},
         "cpu_baseline": None,
     }
@@ -747,117 +689,113 @@ def run_prefill(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) ->
         t = time.perf_counter()
         run(16)
         t16 = time.perf_counter() - t
-        nq = max(16, min(S, int(16 * cpu_budget / 3 / max(t16, 1e-6))))
-        times = []
-        for _ in range(3):
-            t = time.perf_counter()
-            run(nq)
-            times.append(time.perf_counter() - t)
+        nq = max(16, min(S, int(16 * cpu_budget / 7 / max(t16, 1e-6))))
+        med = cpu_median_s(lambda: run(nq))
         sample_flops = 4 * d * H * sum(prior + i + 1 for i in range(nq))
-        med = statistics.median(times)
         line["cpu_baseline"] = {"value": round(sample_flops / med / 1e12, 4), "unit": "TFLOP/s",
                                 "cores": torch.get_num_threads(), "kind": "port",
-                                "sample": f"the first {nq} queries of request 0 (median of 3 runs, {sample_flops / 1e9:.0f}"
-                                          f" GFLOP)", "cpu": cpu_model(),
+                                "sample": f"the first {nq} queries of request 0 (2 warm-ups, median of 5 runs, "
+                                          f"{sample_flops / 1e9:.0f} GFLOP)", "cpu": cpu_model(),
                                 "us_per_step_scaled": round(med * flops / sample_flops * 1e6, 1)}
         log(f"CPU baseline: {line['cpu_baseline']['value']} TFLOP/s")
     return line
 
 
-def run_one(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> dict:
-    import ctypes
+DECODE_CONFIGS = ("2", "1", "3", "4", "4swa", "5")
 
-    import torch
 
-    from sglang_neuron_amd import _lib
-
+def setup(key: str, dev):
     if key in ("1", "2", "4"):
-        built = setup_gqa(int(key), 0, dev)
-    elif key == "4swa":
+        return setup_gqa(int(key), 0, dev)
+    if key == "4swa":
         from sglang_neuron_amd import workloads
 
-        built = setup_gqa(4, workloads.SWA_WINDOW, dev)
-    elif key == "3":
-        built = setup_mla(dev)
-    elif key == "5":
-        built = setup_dsa(dev)
-    else:
-        raise SystemExit(f"unknown config {key}")
-    steps, desc, step_bytes, split_bytes, mfma_flops, cpu_fn = built
+        return setup_gqa(4, workloads.SWA_WINDOW, dev)
+    if key == "3":
+        return setup_mla(dev)
+    if key == "5":
+        return setup_dsa(dev)
+    raise SystemExit(f"unknown config {key}")
+
+
+def measure_decode(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> dict:
+    """One decode config: its step time from one event pair around steps_n back-to-back steps, the roofline of the
+    step's kernels, and (cpu) the CPU baseline. The pools are freed before returning."""
+    import torch
+
+    steps, desc, step_bytes, kernels, mfma_flops, cpu_fn = setup(key, dev)
     n = len(steps)
-    lib = _lib.load()
-
-    for i in range(warmup):
-        steps[i % n]()
-    torch.cuda.synchronize()
-    log(f"warmup {warmup} done; timing {steps_n} steps")
-
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     wall = time.perf_counter()
-    start.record()
-    for i in range(steps_n):
-        steps[i % n]()
-    end.record()
-    torch.cuda.synchronize()
+    us = time_us(lambda i: steps[i % n](), steps_n, warmup)
     wall = time.perf_counter() - wall
-    ms = start.elapsed_time(end) / steps_n
-    log(f"timed: {ms * 1e3:.2f} us/step ({wall * 1e6 / steps_n:.2f} us/step by the host clock)")
-
-    # the split-K kernel alone, with the library's HIP-event timer on the launch stream
-    lib.sna_diag_kernel_timing(1)
-    for i in range(steps_n):
-        steps[i % n]()
-    split_ms, comb_ms, launches = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
-    _lib.check(lib.sna_diag_kernel_timing_read(ctypes.byref(split_ms), ctypes.byref(comb_ms), ctypes.byref(launches)),
-               "kernel_timing_read")
-    lib.sna_diag_kernel_timing(0)
-    avg_split_ms = split_ms.value / max(launches.value, 1)
-    avg_comb_ms = comb_ms.value / max(launches.value, 1)
-    achieved = split_bytes / (avg_split_ms * 1e-3) / 1e9 if avg_split_ms > 0 else 0.0
-    log(f"split-K kernel: {avg_split_ms * 1e3:.2f} us/launch ({achieved:.0f} GB/s), combine {avg_comb_ms * 1e3:.2f} us")
-
-    value = step_bytes / (ms * 1e-3) / 1e9
+    gbs = step_bytes / (us * 1e-6) / 1e9
     wl = desc["workload"].split(":")[0]
+    traffic, traffic_source = _traffic(wl)
+    mfma_tflops = mfma_flops / (us * 1e-6) / 1e12
+    log(f"{wl}: {us:.2f} us/step over {steps_n} back-to-back steps ({gbs:.0f} GB/s, {gbs / PEAK_HBM_GBS:.1%} of HBM "
+        f"peak); {wall * 1e6 / (steps_n + warmup):.1f} us/step by the host clock; kernels {kernels}")
+    out = {
+        "config": desc,
+        "us_per_step": round(us, 3),
+        "step_alg_bytes": step_bytes,
+        "roofline": {
+            "bound": "hbm",
+            "kernels": kernels,
+            "scope": "the whole step (its kernels back to back)" if len(kernels) > 1 else "the step's one kernel",
+            "achieved": round(gbs, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4),
+            "traffic": traffic,
+            "traffic_source": traffic_source,
+            "alg_bytes_per_step": step_bytes,
+            "us_per_step": round(us, 3),
+            "timing": f"one HIP event pair (torch events, the launch stream) around {steps_n} back-to-back steps",
+        },
+        "mfma": {"alg_tflops": round(mfma_tflops, 2), "frac_of_bf16_dense_peak": round(mfma_tflops / PEAK_BF16_TFLOPS, 4),
+                 "source": "algorithmic: MFMA instructions the kernel issues (16x16 key tiles x shapes) / step time, "
+                           "not a hardware counter"},
+        "cpu_baseline": None,
+    }
+    if cpu:
+        log(f"{wl}: CPU baseline (oracle on {cpu_threads()} host threads)")
+        cb = cpu_fn(cpu_budget)
+        cb["alg_gbs"] = round(step_bytes / (cb["value"] * 1e-6) / 1e9, 3)
+        out["cpu_baseline"] = cb
+        log(f"{wl}: CPU baseline {cb['value']:.0f} us/step on {cb['cores']} threads")
+    del steps
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
+def run_one(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev, per_config=()) -> dict:
+    m = measure_decode(key, steps_n, warmup, cpu, cpu_budget, dev)
+    us = m["us_per_step"]
+    desc = m.pop("config")
     line = {
         "metric": METRIC,
-        "value": round(value, 1),
+        "value": m["roofline"]["achieved"],
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps_n,
         "warmup": warmup,
-        "ms_per_step": round(ms, 6),
+        "ms_per_step": round(us * 1e-3, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp8_e4m3fn" if "fp8" in desc.get("kv_dtype", "") else "bf16",
         "data": "synthetic: seeded N(0,1) values (torch.Generator seed 1000+cfg), random page permutation",
         "config": desc,
-        "us_per_step": round(ms * 1e3, 3),
-        "step_alg_bytes": step_bytes,
-        "step_hbm_frac": round(value / PEAK_HBM_GBS, 4),
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "split-K decode (gqa_decode_kernel / mla_decode_kernel)",
-            "achieved": round(achieved, 1),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": _traffic(wl),
-            "alg_bytes_per_launch": split_bytes,
-            "avg_launch_us": round(avg_split_ms * 1e3, 3),
-            "combine_avg_launch_us": round(avg_comb_ms * 1e3, 3),
-            "launches_timed": launches.value,
-            "mfma_tflops": round(mfma_flops / (avg_split_ms * 1e-3) / 1e12, 2) if avg_split_ms > 0 else None,
-            "mfma_util_of_bf16_dense_peak": round(mfma_flops / (avg_split_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)
-            if avg_split_ms > 0 else None,
-        },
-        "cpu_baseline": None,
+        **m,
     }
-    if cpu:
-        log("CPU baseline (oracle on the host cores)")
-        line["cpu_baseline"] = cpu_fn(cpu_budget)
-        log(f"CPU baseline: {line['cpu_baseline']['value']:.0f} us/step on {line['cpu_baseline']['cores']} threads")
+    if per_config:
+        line["per_config"] = {}
+        for k in per_config:
+            pm = measure_decode(k, steps_n, warmup, cpu, cpu_budget * 2 / 3, dev)
+            name = "cfg" + k.replace("swa", "-swa128")
+            pm["workload"] = pm.pop("config")["workload"]
+            line["per_config"][name] = pm
     return line
 
 
@@ -871,6 +809,8 @@ def main() -> int:
                          "prefill: the segmented prefill attention; indexer: the DSA indexer; wire: the PD page-item "
                          "transfer")
     ap.add_argument("--all", action="store_true", help="one line per workload")
+    ap.add_argument("--no-per-config", action="store_true",
+                    help="the cfg2 line without the other decode configs under per_config")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work for the baseline sample")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -908,7 +848,8 @@ def main() -> int:
         elif k == "qkv":
             line = run_qkv(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
         else:
-            line = run_one(k, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
+            extra = () if (args.all or args.no_per_config or k != "2") else DECODE_CONFIGS[1:]
+            line = run_one(k, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev, extra)
         print(json.dumps(line), flush=True)
         torch.cuda.empty_cache()
     return 0

@@ -5,8 +5,8 @@
  * function takes raw device pointers, int32/int64 sizes, and a hipStream_t passed as `void *`. Each returns an int
  * status: SNA_OK (0), or a negative code with a message that sna_last_error() gives back on the calling thread.
  * Nothing throws across the ABI, and no function allocates device memory. Kernels are enqueued on the caller's
- * stream in call order, so a store followed by a decode on one stream sees the store. The library keeps no device
- * state between calls. Its only state is the thread-local error string and the diagnostics timer (off by default).
+ * stream in call order, so a store followed by a decode on one stream sees the store. The library's only state is the
+ * thread-local error string and, for sna_paged_decode_gqa_noalloc, each device's scratch array and its address.
  *
  * Conventions (sglang-neuron, reference paths under /root/reference/sglang_neuron):
  *   - A token slot is page * page_size + offset; page = slot / page_size (attention/backend.py:6-7).
@@ -439,18 +439,6 @@ int sna_page_items_copy(const uint64_t *src_ptrs, const int64_t *src_lens, const
                         const int32_t *src_pages, const int32_t *dst_pages, int64_t n_pages, void *stream);
 
 /* ---- diagnostics ---- */
-
-/* Per-kernel timing of the decode entry points, for the benchmark's roofline figure. With timing on, each decode call
- * launches its split-K kernel and its combine kernel through hipExtLaunchKernel with a start/stop event pair, so the
- * kernels' own dispatch packets stamp the times and no marker packet runs between them (up to 4096 calls after the
- * switch); sna_block_table, sna_window_table, sna_prefill_attention, sna_indexer_scores, sna_topk_positions and the
- * sna_page_items_* calls time their kernels (first launch's start to last launch's end) as the split-K slot.
- * sna_diag_kernel_timing_read
- * waits for the events and returns the summed milliseconds of each kernel and the number of split-K-slot launches
- * timed. The events are the library's only state besides the error string. The timer
- * is not thread-safe and is off by default. */
-int sna_diag_kernel_timing(int enable);
-int sna_diag_kernel_timing_read(double *split_ms, double *combine_ms, int64_t *launches);
 
 /* Decode n e4m3fn bytes to bf16 bits with the conversion instruction the decode kernels use for gathered pages. It
  * lets a test compare that instruction with the exact decoding on all 256 byte values. */

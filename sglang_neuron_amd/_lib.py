@@ -92,9 +92,6 @@ SIGNATURES = {
     "sna_block_table": (_I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _I32, _I32, _P, _P, _P]),
     "sna_window_table": (_I32, [_P, _I64, _I32, _P, _I32, _I32, _I32, _P, _P, _P]),
     "sna_diag_fp8_to_bf16": (_I32, [_P, _P, _I64, _P]),
-    "sna_diag_kernel_timing": (_I32, [_I32]),
-    "sna_diag_kernel_timing_read": (_I32, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
-                                           ctypes.POINTER(ctypes.c_int64)]),
 }
 
 _lib = None

@@ -139,39 +139,6 @@ int plan_stream(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32_t n
 
 }  // namespace
 
-// ---- diagnostics timer ----
-namespace {
-constexpr int kMaxTimed = 4096;
-bool g_timing = false;
-int g_timed = 0;
-hipEvent_t g_events[kMaxTimed][2][2];  // [call][split, combine][start, stop]
-bool g_made[kMaxTimed] = {};
-bool g_used[kMaxTimed][2] = {};
-}  // namespace
-
-void timing_events(int phase, hipEvent_t* start, hipEvent_t* stop) {
-  *start = nullptr;
-  *stop = nullptr;
-  if (!g_timing || g_timed >= kMaxTimed || phase < 0 || phase > 1) return;
-  if (!g_made[g_timed]) {
-    for (int p = 0; p < 2; ++p)
-      for (int i = 0; i < 2; ++i)
-        if (hipEventCreate(&g_events[g_timed][p][i]) != hipSuccess) {
-          g_timing = false;
-          return;
-        }
-    g_made[g_timed] = true;
-  }
-  g_used[g_timed][phase] = true;
-  *start = g_events[g_timed][phase][0];
-  *stop = g_events[g_timed][phase][1];
-}
-
-void timing_end_call() {
-  if (!g_timing || g_timed >= kMaxTimed) return;
-  if (g_used[g_timed][0] || g_used[g_timed][1]) ++g_timed;
-}
-
 // ---- LSE merge of partials (decode-context-parallel style) ----
 __global__ __launch_bounds__(256) void lse_combine_kernel(const float* __restrict__ o_parts,
                                                           const float* __restrict__ lse_parts, int32_t n_parts,
@@ -209,36 +176,6 @@ extern "C" {
 int sna_version(void) { return 101; }
 
 const char* sna_last_error(void) { return error_buffer(); }
-
-int sna_diag_kernel_timing(int enable) {
-  ApiGuard guard;
-  g_timing = enable != 0;
-  if (g_timing) {
-    g_timed = 0;
-    for (int i = 0; i < kMaxTimed; ++i) g_used[i][0] = g_used[i][1] = false;
-  }
-  return SNA_OK;
-}
-
-int sna_diag_kernel_timing_read(double* split_ms, double* combine_ms, int64_t* launches) {
-  ApiGuard guard;
-  if (!split_ms || !combine_ms || !launches) return fail(SNA_ERR_INVALID_ARGUMENT, "kernel_timing_read: null pointer");
-  *split_ms = 0.0;
-  *combine_ms = 0.0;
-  *launches = 0;
-  for (int i = 0; i < g_timed; ++i) {
-    for (int p = 0; p < 2; ++p) {
-      if (!g_used[i][p]) continue;
-      float ms = 0.f;
-      if (hipEventSynchronize(g_events[i][p][1]) != hipSuccess ||
-          hipEventElapsedTime(&ms, g_events[i][p][0], g_events[i][p][1]) != hipSuccess)
-        return fail(SNA_ERR_LAUNCH, "kernel_timing_read: elapsed time failed");
-      (p == 0 ? *split_ms : *combine_ms) += ms;
-    }
-    *launches += g_used[i][0];
-  }
-  return SNA_OK;
-}
 
 int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32_t max_seq_len, int32_t window,
                     int32_t n_keys_per_row, int32_t ctas_per_item, int32_t num_cus, sna_split_plan* plan) {

@@ -541,28 +541,18 @@ __global__ __launch_bounds__(128) void gqa_lone_token_kernel(GqaArgs a) {
 
 template <int D, bool FP8>
 static void launch_gqa(const GqaArgs& a, int depth, bool any_lone, hipStream_t s) {
-  hipEvent_t t0, t1;
   if (a.n_work > 0) {
     const dim3 grid(a.n_work, a.G);
-    timing_events(0, &t0, &t1);
     if (depth >= 4) {
-      if (a.max_splits <= 1)
-        hipExtLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, true, 4>), grid, dim3(256), 0, s, t0, t1, 0, a);
-      else
-        hipExtLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, false, 4>), grid, dim3(256), 0, s, t0, t1, 0, a);
+      if (a.max_splits <= 1) hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, true, 4>), grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, false, 4>), grid, dim3(256), 0, s, a);
     } else {
-      if (a.max_splits <= 1)
-        hipExtLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, true, 2>), grid, dim3(256), 0, s, t0, t1, 0, a);
-      else
-        hipExtLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, false, 2>), grid, dim3(256), 0, s, t0, t1, 0, a);
+      if (a.max_splits <= 1) hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, true, 2>), grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, false, 2>), grid, dim3(256), 0, s, a);
     }
   }
-  if (a.max_splits > 1) {
-    timing_events(1, &t0, &t1);
-    hipExtLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.B, a.H), dim3(64), 0, s, t0, t1, 0, a);
-  }
+  if (a.max_splits > 1) hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.B, a.H), dim3(64), 0, s, a);
   if (any_lone) hipLaunchKernelGGL((gqa_lone_token_kernel<D, FP8>), dim3(a.B, a.G), dim3(128), 0, s, a);
-  timing_end_call();
 }
 
 }  // namespace sna

@@ -494,19 +494,15 @@ int sna_indexer_scores(const void* q, const float* w, const uint8_t* keys, const
   a.num_blocks = num_blocks;
   a.scale = 1.0f / sqrtf((float)head_dim);
   const dim3 grid((unsigned)((width + kScoreKeys - 1) / kScoreKeys), (unsigned)B);
-  hipEvent_t t0, t1;
-  timing_events(0, &t0, &t1);
   const hipStream_t s = (hipStream_t)stream;
   switch (num_heads / 16) {
-    case 1: hipExtLaunchKernelGGL((indexer_score_kernel<1>), grid, dim3(256), 0, s, t0, t1, 0, a); break;
-    case 2: hipExtLaunchKernelGGL((indexer_score_kernel<2>), grid, dim3(256), 0, s, t0, t1, 0, a); break;
-    case 4: hipExtLaunchKernelGGL((indexer_score_kernel<4>), grid, dim3(256), 0, s, t0, t1, 0, a); break;
-    case 8: hipExtLaunchKernelGGL((indexer_score_kernel<8>), grid, dim3(256), 0, s, t0, t1, 0, a); break;
+    case 1: hipLaunchKernelGGL((indexer_score_kernel<1>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((indexer_score_kernel<2>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((indexer_score_kernel<4>), grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((indexer_score_kernel<8>), grid, dim3(256), 0, s, a); break;
     default:
-      timing_end_call();
       return fail(SNA_ERR_UNSUPPORTED, "indexer_scores: %d heads (16, 32, 64 or 128)", num_heads);
   }
-  timing_end_call();
   return check_launch("indexer_scores");
 }
 
@@ -533,16 +529,13 @@ int sna_topk_positions(const void* scores, int64_t score_stride, int32_t B, int3
   const dim3 grid((unsigned)S, (unsigned)B), block(1024);
   const uint16_t* sc = (const uint16_t*)scores;
   uint32_t* ws = (uint32_t*)workspace;
-  hipEvent_t t0, t1;
-  timing_events(0, &t0, &t1);  // the first launch's start to the last launch's end
   hipStream_t st = (hipStream_t)stream;
-  hipExtLaunchKernelGGL(topk_hist_hi_kernel, grid, block, 0, st, t0, nullptr, 0, sc, score_stride, width, S, ws);
-  hipExtLaunchKernelGGL(topk_hist_lo_kernel, grid, block, 0, st, nullptr, nullptr, 0, sc, score_stride, width, S, k,
+  hipLaunchKernelGGL(topk_hist_hi_kernel, grid, block, 0, st, sc, score_stride, width, S, ws);
+  hipLaunchKernelGGL(topk_hist_lo_kernel, grid, block, 0, st, sc, score_stride, width, S, k,
                         ws);
-  hipExtLaunchKernelGGL(topk_count_kernel, grid, block, 0, st, nullptr, nullptr, 0, sc, score_stride, width, S, k, ws);
-  hipExtLaunchKernelGGL(topk_write_kernel, grid, block, 0, st, nullptr, t1, 0, sc, score_stride, width, S, k, ws, out,
+  hipLaunchKernelGGL(topk_count_kernel, grid, block, 0, st, sc, score_stride, width, S, k, ws);
+  hipLaunchKernelGGL(topk_write_kernel, grid, block, 0, st, sc, score_stride, width, S, k, ws, out,
                         out_stride);
-  timing_end_call();
   return check_launch("topk_positions");
 }
 

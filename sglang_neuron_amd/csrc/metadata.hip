@@ -66,12 +66,9 @@ int sna_block_table(const int32_t* req_to_token, int64_t r2t_rows, int64_t r2t_w
   if (B == 0) return SNA_OK;
   if (!req_to_token || !req_pool_indices || !seq_lens || !table)
     return fail(SNA_ERR_INVALID_ARGUMENT, "block_table: null pointer");
-  hipEvent_t t0, t1;
-  timing_events(0, &t0, &t1);
-  hipExtLaunchKernelGGL(block_table_kernel, dim3(grid_for((int64_t)B * width)), dim3(256), 0, (hipStream_t)stream, t0,
-                        t1, 0, req_to_token, r2t_rows, r2t_width, r2t_stride, req_pool_indices, seq_lens, B, page_size,
-                        width, table, seq_lens_i32);
-  timing_end_call();
+  hipLaunchKernelGGL(block_table_kernel, dim3(grid_for((int64_t)B * width)), dim3(256), 0, (hipStream_t)stream,
+                     req_to_token, r2t_rows, r2t_width, r2t_stride, req_pool_indices, seq_lens, B, page_size, width, table,
+                     seq_lens_i32);
   return check_launch("block_table");
 }
 
@@ -84,12 +81,8 @@ int sna_window_table(const int32_t* table, int64_t table_stride, int32_t table_w
                 B, table_width, (long long)table_stride, page_size, n_blocks);
   if (B == 0) return SNA_OK;
   if (!table || !seq_lens || !trimmed || !pos_offset) return fail(SNA_ERR_INVALID_ARGUMENT, "window_table: null pointer");
-  hipEvent_t t0, t1;
-  timing_events(0, &t0, &t1);
-  hipExtLaunchKernelGGL(window_table_kernel, dim3(grid_for((int64_t)B * n_blocks)), dim3(256), 0, (hipStream_t)stream,
-                        t0, t1, 0, table, table_stride, table_width, seq_lens, B, page_size, n_blocks, trimmed,
-                        pos_offset);
-  timing_end_call();
+  hipLaunchKernelGGL(window_table_kernel, dim3(grid_for((int64_t)B * n_blocks)), dim3(256), 0, (hipStream_t)stream,
+                     table, table_stride, table_width, seq_lens, B, page_size, n_blocks, trimmed, pos_offset);
   return check_launch("window_table");
 }
 

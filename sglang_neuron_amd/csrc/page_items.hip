@@ -98,8 +98,6 @@ int launch_items(const char* what, int32_t n_regions, int64_t n_pages, const int
                                           (long long)n_pages);
   const int32_t batches = (n_regions + kItemRegions - 1) / kItemRegions;
   const int32_t per = (n_regions + batches - 1) / batches;  // even batches
-  hipEvent_t t0, t1;
-  timing_events(0, &t0, &t1);  // the first launch's start to the last launch's end
   for (int32_t r0 = 0; r0 < n_regions; r0 += per) {
     const int32_t nr = n_regions - r0 < per ? n_regions - r0 : per;
     PageItemsArgs a;
@@ -108,11 +106,8 @@ int launch_items(const char* what, int32_t n_regions, int64_t n_pages, const int
     a.src_pages = src_pages;
     a.dst_pages = dst_pages;
     a.zero_invalid = zero_invalid;
-    const bool first = r0 == 0, last = r0 + nr >= n_regions;
-    hipExtLaunchKernelGGL(page_items_kernel, dim3((unsigned)n_pages, (unsigned)nr), dim3(256), 0, stream,
-                          first ? t0 : nullptr, last ? t1 : nullptr, 0, a);
+    hipLaunchKernelGGL(page_items_kernel, dim3((unsigned)n_pages, (unsigned)nr), dim3(256), 0, stream, a);
   }
-  timing_end_call();
   return check_launch(what);
 }
 

@@ -503,13 +503,11 @@ extern "C" int sna_prefill_attention(const void* q, const void* k_cache, const v
   a.sm_scale = sm_scale;
   a.window = window;
   const dim3 grid((unsigned)((max_q_len + a.bq - 1) / a.bq), (unsigned)R, (unsigned)num_kv_heads);
-  hipEvent_t t0, t1;
-  timing_events(0, &t0, &t1);
   const int esz = kv_dtype == SNA_DTYPE_BF16 ? 2 : 1;
   const bool buf = num_blocks * num_kv_heads * (int64_t)page_size * head_dim * esz < ((int64_t)1 << 32);
   const hipStream_t s = (hipStream_t)stream;
 #define SNA_PREFILL_LAUNCH(D_, BUF_, ESZ_) \
-  hipExtLaunchKernelGGL((prefill_gqa_kernel<D_, BUF_, ESZ_>), grid, dim3(256), 0, s, t0, t1, 0, a)
+  hipLaunchKernelGGL((prefill_gqa_kernel<D_, BUF_, ESZ_>), grid, dim3(256), 0, s, a)
   if (esz == 1) {
     if (head_dim == 128) {
       if (buf) SNA_PREFILL_LAUNCH(128, true, 1); else SNA_PREFILL_LAUNCH(128, false, 1);
@@ -524,6 +522,5 @@ extern "C" int sna_prefill_attention(const void* q, const void* k_cache, const v
     }
   }
 #undef SNA_PREFILL_LAUNCH
-  timing_end_call();
   return check_launch("prefill_attention");
 }

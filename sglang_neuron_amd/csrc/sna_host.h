@@ -1,7 +1,6 @@
 // Host-side helpers of the C ABI: the thread-local error message, argument checks and launch checks.
 #pragma once
 
-#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdint.h>
@@ -51,12 +50,5 @@ inline int check_work_map(const sna_split_plan* plan, int32_t B, const char* wha
   }
   return SNA_OK;
 }
-
-// Diagnostics timer (capi.hip). When sna_diag_kernel_timing(1) has switched it on, timing_events hands a decode
-// launcher the start/stop events of its split-K kernel (phase 0) or its combine kernel (phase 1), and the launcher
-// passes them to hipExtLaunchKernelGGL, so the dispatch packet itself stamps them: no marker packet sits between
-// the kernels. Both events are null when the timer is off. timing_end_call closes the launcher's call.
-void timing_events(int phase, hipEvent_t* start, hipEvent_t* stop);
-void timing_end_call();
 
 }  // namespace sna

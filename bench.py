@@ -275,7 +275,7 @@ def setup_dsa(dev):
 
         return _time_rows(run, case.B, budget_s)
 
-    return steps, desc, case.kv_bytes_per_step(), ["kv_store_dsa_kernel", "mla_decode_kernel"], mfma_flops, cpu_baseline
+    return steps, desc, case.kv_bytes_per_step(), ["mla_decode_kernel"], mfma_flops, cpu_baseline
 
 
 def _time_rows(run, B: int, budget_s: float):

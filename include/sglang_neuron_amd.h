@@ -286,9 +286,12 @@ int sna_mla_decode(const void *ql_nope, const void *q_pe, const void *cache, con
  *   block_table  [B, table_stride] int32 (logical block -> physical block); `table_width` valid columns.
  *   positions    [B] int32, the query token's absolute position.
  *   own_rows     [B, 576] bf16 in [k_pe | latent] order: the step's rows, attended in-band from their packed bytes
- *                (mla_decode_attention_torch.py:181-190). The caller stores them first with sna_kv_store_dsa, so an
- *                index equal to a row's own position reads the stored row, as in the reference (steps 0-1 precede
- *                the gather there).
+ *                (mla_decode_attention_torch.py:181-190).
+ *   new_slots    [B] int64 or NULL: the cache rows the own rows are stored to in this launch, bit-exact with
+ *                sna_kv_store_dsa (a slot < 0 or past the cache is skipped; of rows sharing a slot the last one's
+ *                bytes land). As in the reference, where steps 0-1 store every own row before any gather, an index
+ *                resolving to such a row attends the stored bytes. NULL: the caller has stored them
+ *                (sna_kv_store_dsa) before the launch.
  *   ctx_out      [B, num_heads, 512] bf16; lse_out [B, num_heads] fp32 (natural log), or NULL.
  * Position pos resolves to row table[pos / page_size] * page_size + pos % page_size. It is dropped when pos < 0,
  * its block is outside the table or unallocated, or the row is outside the cache. A resolved key is kept iff
@@ -297,8 +300,9 @@ int sna_mla_decode(const void *ql_nope, const void *q_pe, const void *cache, con
  * On Trainium that is mla_decode_attention (models/glm52/kernels/decode/attention/mla/mla_decode_attention.py:207). */
 int sna_mla_decode_sparse(const void *q_absorbed, const void *q_pe, const void *cache, float kv_scale,
                           const int32_t *indices, int32_t n_indices, const int32_t *block_table, int64_t table_stride,
-                          int32_t table_width, const int32_t *positions, const void *own_rows, float sm_scale,
-                          void *ctx_out, float *lse_out, int32_t B, int32_t num_heads, int32_t page_size,
+                          int32_t table_width, const int32_t *positions, const void *own_rows,
+                          const int64_t *new_slots, float sm_scale, void *ctx_out, float *lse_out, int32_t B,
+                          int32_t num_heads, int32_t page_size,
                           int64_t num_blocks, const sna_split_plan *plan, void *workspace, int64_t workspace_bytes,
                           void *stream);
 

@@ -59,7 +59,7 @@ struct MlaArgs {
   int32_t n_indices;
   const int32_t* positions;  // sparse [B]
   const uint16_t* own;       // [B, 576] bf16: ROWS576 [latent | rope], ROWS640 [rope | latent]
-  const int64_t* new_slots;  // paged: store the own row there (NULL: no store)
+  const int64_t* new_slots;  // store the own rows there (NULL: the caller has stored them)
   int32_t B, H, P, groups;
   int64_t num_blocks;
   float sm_scale;
@@ -133,6 +133,39 @@ constexpr int kCachePolicyDevice = 0x10;
 __device__ __forceinline__ void interleave_pairs(uint32_t x, uint32_t y, uint32_t& d0, uint32_t& d1) {
   d0 = (x & 0xffffu) | (y << 16);
   d1 = (x >> 16) | (y & 0xffff0000u);
+}
+
+// One 640-byte DSA row packed from its bf16 [rope 64 | latent 512] source into LDS at dst, by the 64 lanes of a wave,
+// bit for bit as kv_store_dsa_kernel packs it: lane l quantizes latent bytes 8 l .. 8 l + 7, lanes 0 .. 15 the rope.
+__device__ __forceinline__ void pack_row640(const uint16_t* src, uint8_t* dst, float kv_scale, int lane) {
+  uint32_t o[2] = {0, 0};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int32_t beta = 8 * lane + i, a0 = beta >> 8, rem = beta & 255;
+    o[i >> 2] |= quantize_e4m3fn(src[64 + (a0 << 8) + ((rem & 1) << 7) + (rem >> 1)], kv_scale) << ((i & 3) * 8);
+  }
+  *reinterpret_cast<uint2*>(dst + 128 + 8 * lane) = make_uint2(o[0], o[1]);
+  if (lane < 16) {
+    const uint2 w = ld8(src + 4 * lane);
+    const uint32_t r0 = f32_to_bf16_bits(bf16_bits_to_f32(w.x & 0xffffu) / kv_scale) |
+                        (f32_to_bf16_bits(bf16_bits_to_f32(w.x >> 16) / kv_scale) << 16);
+    const uint32_t r1 = f32_to_bf16_bits(bf16_bits_to_f32(w.y & 0xffffu) / kv_scale) |
+                        (f32_to_bf16_bits(bf16_bits_to_f32(w.y >> 16) / kv_scale) << 16);
+    *reinterpret_cast<uint2*>(dst + 8 * lane) = make_uint2(r0, r1);
+  }
+}
+
+// The rows' new slots in a 512-entry open-addressing table in LDS (key: pool row, value: the highest batch row that
+// stores there, the one whose bytes a gather of that slot sees, since the rows are stored in order): B <= 256 keys, so
+// every probe sequence meets an empty entry.
+constexpr int kSlotHash = 512;
+__device__ __forceinline__ uint32_t slot_hash(int32_t row) { return ((uint32_t)row * 2654435761u) >> 23; }
+__device__ __forceinline__ int32_t slot_lookup(const int32_t* keys, const int32_t* vals, int32_t row) {
+  for (uint32_t h = slot_hash(row);; h = (h + 1) & (kSlotHash - 1)) {
+    const int32_t k = keys[h];
+    if (k == row) return vals[h];
+    if (k == -1) return -1;
+  }
 }
 
 // Partials cross workgroups (and so the chip's per-XCD L2s) inside one launch: they are written and read with device
@@ -379,10 +412,17 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
       const uint16_t* src = a.own + (int64_t)b * 576;
       own0 = ld16(src + 8 * lane);
       if (lane < 8) own1 = ld16(src + 8 * (lane + 64));
-      if (!SPARSE && hg == 0 && a.new_slots) own_slot = redirect_slot(a.new_slots[b], a.num_blocks * a.P);
+      if (hg == 0 && a.new_slots) {
+        // paged: an out-of-range slot goes to the reserved row 0, as kv_store_mla does; sparse: it is skipped, as
+        // kv_store_dsa does
+        const int64_t s0 = a.new_slots[b];
+        own_slot = SPARSE ? ((s0 >= 0 && s0 < a.num_blocks * a.P) ? s0 : -1) : redirect_slot(s0, a.num_blocks * a.P);
+      }
     }
 
-    // Sparse: every index of the segment to a row id (-1: skipped), all loads of a stage in flight together.
+    // Sparse: every index of the segment to a row id (-1: skipped), all loads of a stage in flight together. With
+    // new_slots, a row that some batch row's own row is stored to in this launch becomes -2 - (that batch row): its
+    // bytes are packed from the source row after the tile lands, so no gather depends on when the store lands.
     if constexpr (SPARSE) {
       constexpr int KPT = kMlaMaxSplitKeys / NT;
       const int32_t nkeys = ntiles * 16;
@@ -393,6 +433,27 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
       for (int i = 0; i < KPT; ++i) {
         const int32_t k = tid + i * NT, key = kbase + k;
         pos[i] = (k < nkeys && key < khi) ? a.indices[(int64_t)b * a.n_indices + key] : -1;
+      }
+      // the new-slot table lives in the ring (unused until the tile loop)
+      int32_t* hkey = reinterpret_cast<int32_t*>(&sm_ring[0][0][0]);
+      int32_t* hval = hkey + kSlotHash;
+      if (a.new_slots) {
+        for (int e = tid; e < kSlotHash; e += NT) hkey[e] = hval[e] = -1;
+        __syncthreads();
+        for (int32_t e = tid; e < a.B; e += NT) {
+          const int64_t s0 = a.new_slots[e];
+          if (s0 < 0 || s0 >= n_rows) continue;
+          for (uint32_t h = slot_hash((int32_t)s0);; h = (h + 1) & (kSlotHash - 1)) {
+            const int32_t prev = atomicCAS(&hkey[h], -1, (int32_t)s0);
+            if (prev == -1 || prev == (int32_t)s0) {
+              atomicMax(&hval[h], e);
+              break;
+            }
+          }
+        }
+        __syncthreads();
+        // several rows storing to one slot: the last of them stores (the rows are stored in order)
+        if (own_slot >= 0 && slot_lookup(hkey, hval, (int32_t)own_slot) != b) own_slot = -1;
       }
       int32_t ent[KPT];
 #pragma unroll
@@ -408,6 +469,10 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
         if (ent[i] >= 0 && (int64_t)ent[i] < a.num_blocks) {
           const int64_t r = (int64_t)ent[i] * a.P + pos[i] % a.P;
           if (r < n_rows) row = (int32_t)r;
+        }
+        if (row >= 0 && a.new_slots) {
+          const int32_t src = slot_lookup(hkey, hval, row);
+          if (src >= 0) row = -2 - src;
         }
         sm_rowid[k] = row;
       }
@@ -432,12 +497,25 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     // The valid keys of tile `tile` (bit k: key k), uniform.
     auto tile_mask = [&](int32_t tile) -> uint32_t {
       if constexpr (SPARSE) {
-        return (uint32_t)(__ballot(sm_rowid[tile * 16 - kbase + li] >= 0) & 0xffffull);
+        return (uint32_t)(__ballot(sm_rowid[tile * 16 - kbase + li] != -1) & 0xffffull);
       } else {
         bool ok;
         (void)tile_row0(tile, ok);
         const int32_t nvalid = ok ? max(min(16, khi - tile * 16), 0) : 0;
         return nvalid >= 16 ? 0xffffu : (1u << nvalid) - 1u;
+      }
+    };
+    // Sparse: the keys of tile `tile` whose rows an own row is stored to in this launch (bit k: key k), uniform; their
+    // LDS rows are packed from the source rows once the tile has landed.
+    auto tile_aliases = [&](int32_t tile) -> uint32_t {
+      if constexpr (SPARSE) return (uint32_t)(__ballot(sm_rowid[tile * 16 - kbase + li] <= -2) & 0xffffull);
+      return 0u;
+    };
+    auto patch_aliases = [&](uint8_t* T, int32_t tile, uint32_t al) {
+      for (; al; al &= al - 1) {
+        const int r = __builtin_ctz(al);
+        const int32_t src = -2 - sm_rowid[tile * 16 - kbase + r];
+        pack_row640(a.own + (int64_t)src * 576, T + r * RS, a.kv_scale, lane);
       }
     };
     // Issue the loads of tile `tile` into the ring slot at dst: NDMA DMAs, and the per-token scales (paged).
@@ -707,6 +785,13 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
               wait_vmcnt<0>();
             }
             vm = tile_mask(t0 + i * WAVES);
+            if constexpr (SPARSE) {
+              // rare: the gathers read a slot this launch stores an own row to (the loads drain first)
+              if (const uint32_t al = a.new_slots ? tile_aliases(t0 + i * WAVES) : 0u) {
+                wait_vmcnt<0>();
+                patch_aliases(T, t0 + i * WAVES, al);
+              }
+            }
             [[clang::always_inline]] scores(T, vm, x, tmax, RS, T + Geo::SCALES);
             if (needs_rescale(tmax)) {
               pending = true;
@@ -723,15 +808,22 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
       wait_vmcnt<0>();
     }
 
-    // ---- the own row's pool store (ROWS576), deferred to here so that no store sits among the DMAs in flight ----
+    // ---- the own row's pool store, deferred to here so that no store sits among the DMAs in flight ----
     if (own_wave && own_slot >= 0) {
+      if constexpr (FMT == ROWS576) {
 #pragma unroll
-      for (int part = 0; part < 2; ++part) {
-        if (part == 1 && lane >= 8) continue;
-        *reinterpret_cast<uint2*>(a.cache + own_slot * 576 + 8 * (lane + 64 * part)) =
-            make_uint2(own_q[2 * part], own_q[2 * part + 1]);
+        for (int part = 0; part < 2; ++part) {
+          if (part == 1 && lane >= 8) continue;
+          *reinterpret_cast<uint2*>(a.cache + own_slot * 576 + 8 * (lane + 64 * part)) =
+              make_uint2(own_q[2 * part], own_q[2 * part + 1]);
+        }
+        if (lane == 0) a.row_scale[own_slot] = own_s;
+      } else {
+        // the packed row is sm_own's first 640 bytes
+        uint8_t* dst = a.cache + own_slot * 640;
+        *reinterpret_cast<uint2*>(dst + 8 * lane) = *reinterpret_cast<const uint2*>(&sm_own[8 * lane]);
+        if (lane < 16) *reinterpret_cast<uint2*>(dst + 512 + 8 * lane) = *reinterpret_cast<const uint2*>(&sm_own[512 + 8 * lane]);
       }
-      if (lane == 0) a.row_scale[own_slot] = own_s;
     }
 
     // ---- merge the waves: a common maximum per head; wave w sums latent blocks 2 w, 2 w + 1 over the waves ----
@@ -878,6 +970,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     g = s_hi;
     row_t0 = row_t1;
     if constexpr (!MULTI) break;
+    __syncthreads();  // every wave is done with the ring's merge exchange before the next segment refills the ring
   }
 
   // ---- the launch's last workgroup returns the counters to zero (every other one has finished with them) ----
@@ -1007,7 +1100,8 @@ extern "C" int sna_mla_decode(const void* ql_nope, const void* q_pe, const void*
 extern "C" int sna_mla_decode_sparse(const void* q_absorbed, const void* q_pe, const void* cache, float kv_scale,
                                      const int32_t* indices, int32_t n_indices, const int32_t* block_table,
                                      int64_t table_stride, int32_t table_width, const int32_t* positions,
-                                     const void* own_rows, float sm_scale, void* ctx_out, float* lse_out, int32_t B,
+                                     const void* own_rows, const int64_t* new_slots, float sm_scale, void* ctx_out,
+                                     float* lse_out, int32_t B,
                                      int32_t num_heads, int32_t page_size, int64_t num_blocks,
                                      const sna_split_plan* plan, void* workspace, int64_t workspace_bytes,
                                      void* stream) {
@@ -1052,7 +1146,7 @@ extern "C" int sna_mla_decode_sparse(const void* q_absorbed, const void* q_pe, c
   a.n_indices = n_indices;
   a.positions = positions;
   a.own = (const uint16_t*)own_rows;
-  a.new_slots = nullptr;
+  a.new_slots = new_slots;
   a.B = B;
   a.H = num_heads;
   a.P = page_size;

@@ -423,8 +423,8 @@ def prepare_mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, k
                               block_table: Tensor, positions: Tensor, own_rows: Tensor, *, sm_scale: float,
                               page_size: int, new_slots: Optional[Tensor] = None,
                               plan: Optional[_lib.SplitPlan] = None, workspace: Optional[Tensor] = None) -> Prepared:
-    """mla_decode_sparse's checks and argument binding (with ``new_slots``, the own rows' store first), launched by
-    calling the result."""
+    """mla_decode_sparse's checks and argument binding (with ``new_slots``, the own rows are stored by the same launch),
+    launched by calling the result."""
     dev = _on_gpu(q_absorbed, q_pe, cache, indices, block_table, positions, own_rows, new_slots)
     B, H, lat = q_absorbed.shape
     _need(lat == 512 and q_pe.shape == (B, H, 64), "q_absorbed [B, H, 512] and q_pe [B, H, 64]")
@@ -447,16 +447,13 @@ def prepare_mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, k
     ctx = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
     lse = torch.empty(B, H, dtype=torch.float32, device=dev)
     lib = _lib.load()
-    calls = []
     if new_slots is not None:
         new_slots = _contig(new_slots.reshape(-1).to(torch.int64), "new_slots")
         _need(new_slots.numel() == B, f"{new_slots.numel()} new slots for {B} rows")
-        calls.append((lib.sna_kv_store_dsa, (_ptr(own_rows), _ptr(new_slots), B, float(kv_scale), _ptr(cache),
-                                             n_rows, _stream(dev))))
-    calls.append((lib.sna_mla_decode_sparse, (
+    calls = [(lib.sna_mla_decode_sparse, (
         _ptr(q_absorbed), _ptr(q_pe), _ptr(cache), float(kv_scale), _ptr(idx), K, _ptr(table), table.stride(0),
-        table.shape[1], _ptr(pos), _ptr(own_rows), float(sm_scale), _ptr(ctx), _ptr(lse), B, H, P, n_rows // P, plan,
-        _ptr(ws), ws.numel(), _stream(dev))))
+        table.shape[1], _ptr(pos), _ptr(own_rows), _ptr(new_slots), float(sm_scale), _ptr(ctx), _ptr(lse), B, H, P,
+        n_rows // P, plan, _ptr(ws), ws.numel(), _stream(dev)))]
     keep = (q_absorbed, q_pe, cache, idx, table, pos, own_rows, new_slots, ctx, lse, ws, plan)
     return Prepared(calls, keep, (ctx, lse), "mla_decode_sparse")
 
@@ -465,8 +462,9 @@ def mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, kv_scale:
                       block_table: Tensor, positions: Tensor, own_rows: Tensor, **kw) -> tuple[Tensor, Tensor]:
     """DSA sparse decode: q_absorbed [B, H, 512], q_pe [B, H, 64], the 640-byte row cache, ``indices`` [B, K] int32
     global positions (-1 empty), ``block_table`` [B, W], ``positions`` [B], own rows [B, 576] ([k_pe | latent]).
-    With ``new_slots`` the own rows are stored first (the reference's steps 0-1); without, the caller has stored them.
-    Keyword arguments: sm_scale, page_size, new_slots, plan. Returns (ctx [B, H, 512] bf16, lse [B, H] fp32).
+    With ``new_slots`` the launch also stores the own rows there, and a gather of such a slot attends the stored bytes
+    (the reference stores them first, steps 0-1); without, the caller has stored them. Keyword arguments: sm_scale,
+    page_size, new_slots, plan. Returns (ctx [B, H, 512] bf16, lse [B, H] fp32).
 
     Stands in for mla_decode_attention_torch_ref with one token per sequence and one CP rank
     (models/glm52/kernels/decode/attention/mla/mla_decode_attention_torch.py:38-130)."""

@@ -110,9 +110,13 @@ def dsa_gpu_pool(case: workloads.DsaCase, dev="cuda", gen_device="cpu"):
     return workloads.dsa_pool(case, dev, gen_device)
 
 
-def dsa_gpu_step(case: workloads.DsaCase, cache, dev="cuda"):
-    """The step as the path runs it: store the own rows, then the sparse decode."""
-    ops.kv_store_dsa(case.own_rows.to(dev), case.new_slots.to(dev), cache, case.kv_scale)
+def dsa_gpu_step(case: workloads.DsaCase, cache, dev="cuda", fused=True):
+    """The step as the path runs it: the sparse decode storing the own rows in the same launch (fused), or the store
+    kernel first and then the decode."""
+    slots = case.new_slots.to(dev)
+    if not fused:
+        ops.kv_store_dsa(case.own_rows.to(dev), slots, cache, case.kv_scale)
     return ops.mla_decode_sparse(case.q_absorbed.to(dev), case.q_pe.to(dev), cache, case.kv_scale,
                                  case.indices.to(dev), case.block_table.to(dev), case.positions.to(dev),
-                                 case.own_rows.to(dev), sm_scale=case.sm_scale, page_size=case.P)
+                                 case.own_rows.to(dev), sm_scale=case.sm_scale, page_size=case.P,
+                                 new_slots=slots if fused else None)

@@ -60,6 +60,42 @@ def test_dsa_decode_matches_oracle(name, over):
     assert torch.equal(cache.cpu(), cache_o), "row pool differs"
 
 
+def test_dsa_caller_stored_rows():
+    """Without new_slots the caller stores the own rows first (sna_kv_store_dsa), and the decode only reads."""
+    case = workloads.dsa_case(overrides=DSA_CASES[0][1])
+    want_ctx, want_lse, cache_o = dsa_oracle(case)
+    announce("dsa caller-stored own rows")
+    cache = dsa_gpu_pool(case)
+    ctx, lse = dsa_gpu_step(case, cache, fused=False)
+    assert_close_attn(ctx, want_ctx, "caller-stored")
+    assert torch.allclose(lse.cpu(), want_lse, atol=2e-3, rtol=1e-4)
+    assert torch.equal(cache.cpu(), cache_o), "row pool differs"
+
+
+@pytest.mark.parametrize("name,over", [
+    ("one-workgroup", {"B": 3, "pool_positions": 1024, "n_indices": 64, "recent": 8, "short_rows": ()}),
+    ("split-rows", {"B": 3, "pool_positions": 8192, "n_indices": 2048, "recent": 64, "short_rows": ()}),
+])
+def test_dsa_gathers_of_slots_stored_in_the_launch(name, over):
+    """Gathers of a row that this launch stores an own row to attend the stored bytes, as in the reference, which
+    stores every own row before any gather: a row indexing its own position, a row whose table maps a block onto
+    another row's new slot, and two rows storing to one slot (the later row's bytes land and are gathered)."""
+    case = workloads.dsa_case(overrides=over)
+    P = case.P
+    p0 = int(case.positions[0])
+    case.indices[0, 10] = p0                                   # row 0 attends its own position through an index
+    case.block_table[1, 3] = case.block_table[0, p0 // P]      # row 1's block 3 is row 0's last block
+    case.indices[1, 11] = 3 * P + p0 % P                       # ... and row 1 gathers row 0's new slot
+    case.new_slots[2] = case.new_slots[0]                      # rows 0 and 2 store to one slot: row 2's bytes land
+    want_ctx, want_lse, cache_o = dsa_oracle(case)
+    announce(f"dsa aliased gathers {name}: B={case.B} K={case.indices.shape[1]}")
+    cache = dsa_gpu_pool(case)
+    ctx, lse = dsa_gpu_step(case, cache)
+    assert_close_attn(ctx, want_ctx, name)
+    assert torch.allclose(lse.cpu(), want_lse, atol=2e-3, rtol=1e-4)
+    assert torch.equal(cache.cpu(), cache_o), "row pool differs"
+
+
 def test_dsa_invalid_indices_are_dropped():
     """Indices past the table, into unallocated blocks, or after the query's position are dropped; -1 is empty."""
     case = workloads.dsa_case(overrides={"B": 2, "pool_positions": 1024, "n_indices": 64, "recent": 8,

@@ -16,10 +16,11 @@ One JSON line on stdout:
                 rocprofv3 counter summary (traffic_source says which), else null.
   cpu_baseline  the CPU oracle (a torch restatement of the reference's torch path) on a bounded sample of the same
                 workload, timed on this host's cores (2 warm-ups, median of 5 runs).
-  per_config    cfg1, cfg3, cfg4 (full and sliding-window layers) and cfg5, each with us_per_step, its roofline and
-                cpu_baseline.
+  per_config    cfg1, cfg3, cfg4 (full and sliding-window layers), cfg5 and cfg3 over bf16 rows, each with
+                us_per_step, its roofline and cpu_baseline.
 
-Options: --config {1,2,3,4,4swa,5} prints that workload's line alone; --config meta times the device-side decode
+Options: --config {1,2,3,4,4swa,5,3bf16} prints that workload's line alone (3bf16: cfg3 over bf16 rows, the
+reference's served DeepSeek-V2 pool); --config meta times the device-side decode
 metadata (block table, window trim) instead, --config prefill the segmented prefill attention, --config indexer the
 DSA indexer, --config qkv the QKV writer, --config wire the PD page items; --all prints one line per workload;
 --no-per-config drops the per_config map; --gpus above 1 is refused, because this build measures one GPU.
@@ -190,20 +191,20 @@ def setup_gqa(cfg: int, window: int, dev):
     return steps, desc, case.kv_bytes_per_step(), kernels, mfma_flops, cpu_baseline
 
 
-def setup_mla(dev):
+def setup_mla(dev, bf16: bool = False):
     import torch
 
     from sglang_neuron_amd import ops, workloads
 
     t0 = time.time()
     case = workloads.mla_case(gen_device=dev)
-    cache, scale = workloads.mla_pool(case, dev)
-    pool_bytes = cache.numel() + scale.numel() * 4
-    n = _copies(case.kv_bytes_per_step(), pool_bytes, 64)
-    pools = [(cache, scale)] + [(cache.clone(), scale.clone()) for _ in range(n - 1)]
+    cache, scale = workloads.mla_pool(case, dev, bf16)
+    pool_bytes = cache.numel() * cache.element_size() + (0 if bf16 else scale.numel() * 4)
+    n = _copies(case.kv_bytes_per_step(bf16), pool_bytes, 64)
+    pools = [(cache, scale)] + [(cache.clone(), None if bf16 else scale.clone()) for _ in range(n - 1)]
     torch.cuda.synchronize()
-    log(f"cfg3: B={case.B} H={case.H} P={case.P} tokens={int(case.seq_lens.sum())} pool={pool_bytes / 1e6:.1f} MB x "
-        f"{n} copies, built in {time.time() - t0:.1f}s")
+    log(f"cfg3{'-bf16' if bf16 else ''}: B={case.B} H={case.H} P={case.P} tokens={int(case.seq_lens.sum())} "
+        f"pool={pool_bytes / 1e6:.1f} MB x {n} copies, built in {time.time() - t0:.1f}s")
     table, lens = case.block_table.to(dev), case.seq_lens.to(dev)
     plan = ops.plan_decode(1, case.B, host_seq_lens=case.seq_lens, ctas_per_item=1, num_cus=ops._num_cus(table.device))
     out = torch.empty(case.B, case.H, 512, dtype=torch.bfloat16, device=dev)
@@ -212,8 +213,10 @@ def setup_mla(dev):
                                     out=out, plan=plan) for (c, s) in pools]
     tiles = int(((case.seq_lens - 1 + 15) // 16).sum())
     mfma_flops = tiles * (18 * 16 * 16 * 32 * 2 + 32 * 16 * 16 * 16 * 2)
-    desc = {"workload": "cfg3: deepseek-v2-lite absorbed MLA", "batch": case.B, "q_heads": case.H,
-            "qk_dim": 576, "v_dim": 512, "page_size": case.P, "kv_dtype": "fp8_e4m3fn per-token scale",
+    desc = {"workload": "cfg3-bf16: deepseek-v2-lite absorbed MLA, bf16 rows (the reference's served dtype)" if bf16
+            else "cfg3: deepseek-v2-lite absorbed MLA", "batch": case.B, "q_heads": case.H,
+            "qk_dim": 576, "v_dim": 512, "page_size": case.P,
+            "kv_dtype": "bf16" if bf16 else "fp8_e4m3fn per-token scale",
             "seq_len": "U[1024, 16384]", "pool_copies": n,
             "split_plan": {"split_tiles": plan.split_tiles, "n_work": plan.n_work}}
 
@@ -221,7 +224,7 @@ def setup_mla(dev):
         from oracle import attention as oatt
         from oracle import store as ost
 
-        c0, s0 = pools[0][0].cpu(), pools[0][1].cpu()
+        c0, s0 = pools[0][0].cpu(), None if bf16 else pools[0][1].cpu()
         ql, qp, cn = case.ql_nope.cpu(), case.q_pe.cpu(), case.compact_new.cpu()
 
         def run(nrows):
@@ -231,7 +234,7 @@ def setup_mla(dev):
 
         return _time_rows(run, case.B, budget_s)
 
-    return steps, desc, case.kv_bytes_per_step(), ["mla_decode_kernel"], mfma_flops, cpu_baseline
+    return steps, desc, case.kv_bytes_per_step(bf16), ["mla_decode_kernel"], mfma_flops, cpu_baseline
 
 
 def setup_dsa(dev):
@@ -701,7 +704,7 @@ def run_prefill(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) ->
     return line
 
 
-DECODE_CONFIGS = ("2", "1", "3", "4", "4swa", "5")
+DECODE_CONFIGS = ("2", "1", "3", "4", "4swa", "5", "3bf16")
 
 
 def setup(key: str, dev):
@@ -711,8 +714,8 @@ def setup(key: str, dev):
         from sglang_neuron_amd import workloads
 
         return setup_gqa(4, workloads.SWA_WINDOW, dev)
-    if key == "3":
-        return setup_mla(dev)
+    if key in ("3", "3bf16"):
+        return setup_mla(dev, key == "3bf16")
     if key == "5":
         return setup_dsa(dev)
     raise SystemExit(f"unknown config {key}")
@@ -793,7 +796,7 @@ def run_one(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: float, d
         line["per_config"] = {}
         for k in per_config:
             pm = measure_decode(k, steps_n, warmup, cpu, cpu_budget * 2 / 3, dev)
-            name = "cfg" + k.replace("swa", "-swa128")
+            name = "cfg" + k.replace("swa", "-swa128").replace("bf16", "-bf16")
             pm["workload"] = pm.pop("config")["workload"]
             line["per_config"][name] = pm
     return line
@@ -805,7 +808,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="2",
-                    help="1, 2, 3, 4, 4swa or 5 (default 2, the metric's workload); meta: the device-side metadata; "
+                    help="1, 2, 3, 4, 4swa, 5 or 3bf16 (default 2, the metric's workload); meta: the device-side metadata; "
                          "prefill: the segmented prefill attention; indexer: the DSA indexer; wire: the PD page-item "
                          "transfer")
     ap.add_argument("--all", action="store_true", help="one line per workload")
@@ -835,7 +838,8 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
         log(f"copy calibration: one copy of {COPY_CALIBRATION_BYTES} bytes (read) into as many (written)")
-    keys = ["1", "2", "3", "4", "4swa", "5", "meta", "prefill", "indexer", "wire", "qkv"] if args.all else [args.config]
+    keys = ["1", "2", "3", "4", "4swa", "5", "3bf16", "meta", "prefill", "indexer", "wire", "qkv"] if args.all \
+        else [args.config]
     for k in keys:
         if k == "meta":
             line = run_meta(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)

@@ -3,6 +3,7 @@
 //
 // Row formats:
 //   ROWS576  [latent 512 | k_pe 64] e4m3fn, one fp32 dequantization scale per token slot (row_scale).
+//   ROWS1152 [latent 512 | k_pe 64] bf16, no scale (the reference's DeepSeek-V2 pool).
 //   ROWS640  [k_pe 64 bf16 | latent 512 e4m3fn, permuted], one per-tensor kv_scale. Latent dim c = 256a + 128b + p
 //            sits at latent byte 256a + 2p + b.
 //
@@ -40,7 +41,7 @@
 
 namespace sna {
 
-enum { ROWS576 = 0, ROWS640 = 1 };
+enum { ROWS576 = 0, ROWS640 = 1, ROWS1152 = 2 };
 
 constexpr int kLatent = 512;
 constexpr int kRope = 64;
@@ -96,30 +97,36 @@ struct RowFmt;
 template <>
 struct RowFmt<ROWS576> {
   static constexpr int kRowBytes = 576;
-  static constexpr int kLaneChunks = 9;  // 16-byte chunks per lane per key
+  static constexpr int kLatentBytes = 512;
 };
 template <>
 struct RowFmt<ROWS640> {
   static constexpr int kRowBytes = 640;
-  static constexpr int kLaneChunks = 10;
+  static constexpr int kLatentBytes = 512;
+};
+template <>
+struct RowFmt<ROWS1152> {
+  static constexpr int kRowBytes = 1152;
+  static constexpr int kLatentBytes = 1024;
 };
 
 // Tile geometry in LDS. A tile is 16 key rows; chunk c (16 bytes) of row r sits at LDS chunk r * STRIDE + c, with
-// STRIDE = CHUNKS + 1: the pad chunk puts rows 1 apart 20 (ROWS576) or 36 (ROWS640) banks apart and rows 4 apart 16
-// banks apart, so the QK reads (16 rows, one 16-byte chunk each) and the PV reads (4 rows x 64 bytes per lane group)
+// STRIDE = CHUNKS + 1: the pad chunk puts rows 1 apart 20 (ROWS576) or 36 (ROWS640, ROWS1152) banks apart and rows 4
+// apart 16 banks apart, so the QK reads (16 rows, one 16-byte chunk each) and the PV reads (4 rows x 64 bytes per lane group)
 // are free of bank conflicts, and every LDS address is a per-lane base plus a constant. NDMA wave-wide DMAs fill a
 // slot: lane i of DMA j fills LDS chunk 64 j + i. A pad chunk loads a duplicate of its row's last chunk; the lanes of
 // the last DMA past the tile are switched off. ROWS576 tiles bring their 16 per-token scales along in one more DMA.
 template <int FMT>
 struct TileGeo {
-  static constexpr int CHUNKS = FMT == ROWS576 ? 36 : 40;
+  static constexpr int CHUNKS = RowFmt<FMT>::kRowBytes / 16;
   static constexpr int STRIDE = CHUNKS + 1;
   static constexpr int RS = 16 * STRIDE;                        // LDS row stride, bytes
   static constexpr int NDMA = (16 * STRIDE + 63) / 64;          // 10 or 11
   static constexpr int TAIL = 16 * STRIDE - 64 * (NDMA - 1);    // active lanes of the last DMA
   static constexpr int SCALES = 16 * RS;                        // offset of the 16 per-token scales (ROWS576)
   static constexpr int SLOT = 16 * RS + 64;                     // bytes of one ring slot
-  static constexpr int DEPTH = 3;                               // ring slots per wave
+  // ring slots per wave: a bf16 tile is twice the bytes, so two slots hold as many bytes in flight as three
+  static constexpr int DEPTH = FMT == ROWS1152 ? 2 : (FMT == ROWS576 ? 4 : 3);
 };
 
 // Dword 3 of a raw buffer resource on gfx9-family chips (no format conversion, no swizzle).
@@ -268,14 +275,15 @@ __device__ void merge_chunks(const MlaArgs& a, __amdgpu_buffer_rsrc_t ro, __amdg
   }
 }
 
-// The blocks of `mask` (bit c: latent block c) merged over the row's S partials: one block streams 16 partials at a
-// time, several blocks go together 8 partials at a time (up to 64 loads in flight per thread).
+// The blocks of `mask` (bit c: latent block c) merged over the row's S partials, 8 partials at a time (up to 64 loads
+// in flight per thread). The grouping is the same however many blocks go together, so a block's bits do not depend on
+// which workgroup merges it (a block merged twice gets the same bits twice).
 template <bool SPARSE>
 __device__ void merge_mask(const MlaArgs& a, __amdgpu_buffer_rsrc_t ro, __amdgpu_buffer_rsrc_t rml, int32_t b, int hg,
                            int32_t w0, bool w0_second, int32_t S, uint32_t mask) {
   if (__popc(mask) == 1) {
     const int chunks[1] = {__builtin_ctz(mask)};
-    merge_chunks<SPARSE, 1, 16>(a, ro, rml, b, hg, w0, w0_second, S, chunks);
+    merge_chunks<SPARSE, 1, 8>(a, ro, rml, b, hg, w0, w0_second, S, chunks);
     return;
   }
   int chunks[8];
@@ -298,6 +306,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
   constexpr int DEPTH = Geo::DEPTH;
   constexpr int ROWB = RowFmt<FMT>::kRowBytes;
   constexpr bool SPARSE = FMT == ROWS640;
+  constexpr bool BF16 = FMT == ROWS1152;
   constexpr int NT = 64 * WAVES;
   typedef __attribute__((address_space(3))) void lds_void;
   typedef __attribute__((address_space(3))) uint8_t lds_u8;
@@ -312,16 +321,17 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
   const int32_t w = blockIdx.x;
 
   // LDS: each wave's ring of DEPTH tile slots (after a segment's tile loop: the merge exchange), the sparse row ids,
-  // the waves' softmax statistics, the own row, the query operand, and a broadcast word.
+  // the waves' softmax statistics, the own row, the query operand (bf16 rows: in registers, the ring takes the
+  // space), and a broadcast word.
   __shared__ __attribute__((aligned(16))) uint8_t sm_ring[WAVES][DEPTH][SLOT];
   __shared__ int32_t sm_rowid[SPARSE ? kMlaMaxSplitKeys : 1];
+  __shared__ uint4 sm_q[SPARSE ? 18 : 1][64];
   __shared__ float sm_m[WAVES][16];
   __shared__ float sm_l[WAVES][16];
   // The own row in the pool's row format (its bytes stand for all 16 keys of a tile with row stride 0), then its
-  // scale repeated 16 times at kOwnScales.
-  constexpr int kOwnScales = 640;
+  // scale repeated 16 times at kOwnScales (ROWS576).
+  constexpr int kOwnScales = BF16 ? 1152 : 640;
   __shared__ __attribute__((aligned(16))) uint8_t sm_own[kOwnScales + 64];
-  __shared__ uint4 sm_q[18][64];
   __shared__ int32_t sm_word;
   // The merge exchange: block idx < 6 of sender w, 256 float4.
   static_assert(sizeof(float4) * WAVES * 6 * 256 <= sizeof(sm_ring), "the merge exchange lives in the ring");
@@ -372,12 +382,11 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
       for (int r = 0; r < 4; ++r)
         if (col0 + 64 * r + lane < a.table_width) pg[r] = trow[col0 + 64 * r + lane];
     }
-    // The query operand of every QK step, in lane order: sm_q[s][lane] holds the 8 bf16 lane (g4, li) feeds in step s
-    // (head li). ROWS576: step pair k is chunk 4 k + g4 = dims 16 (4 k + g4) .. + 15 (rope for k = 8). ROWS640: steps
-    // 0, 1 are rope chunk 4 s + g4 (dims 8 (4 s + g4) .. + 7); step pair k > 0 is latent chunk m = 4 (k - 1) + g4,
-    // whose byte 2 i + bb holds dim 256 a + 128 bb + p0 + i.
-    // The paged format DMAs it in the tile loop's prologue, behind the first tiles' loads; the sparse format interleaves
-    // pairs and fills it here.
+    // The query operand of every QK step, the 8 bf16 lane (g4, li) feeds in step s (head li). Paged formats: in
+    // registers, qreg[s] = dims 16 (4 k + g4) + 8 (s % 2) .. + 7 for step pair k = s / 2 (rope for k = 8). ROWS640: in
+    // LDS, sm_q[s][lane]: steps 0, 1 are rope chunk 4 s + g4 (dims 8 (4 s + g4) .. + 7); step pair k > 0 is latent
+    // chunk m = 4 (k - 1) + g4, whose byte 2 i + bb holds dim 256 a + 128 bb + p0 + i (pairs interleaved here; the
+    // workgroup's threads share the loads, which sit on a sparse row's critical path).
     for (int e = tid; SPARSE && e < 18 * 64; e += NT) {
       const int s = e >> 6, ln = e & 63, eg4 = ln >> 4;
       const int32_t h = min(16 * hg + (ln & 15), a.H - 1);  // absent heads read a real head; their results are dropped
@@ -400,6 +409,22 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
       }
       sm_q[s][ln] = wq;
     }
+    uint4 qreg[SPARSE ? 1 : 18];
+    if constexpr (!SPARSE) {
+      const int32_t h = min(16 * hg + li, a.H - 1);
+      const uint16_t* qlp = a.ql + ((int64_t)b * a.H + h) * kLatent;
+      const uint16_t* qpp = a.qpe + ((int64_t)b * a.H + h) * kRope;
+#pragma unroll
+      for (int st = 0; st < 18; ++st) {
+        const int d = 16 * (4 * (st >> 1) + g4) + 8 * (st & 1);
+        qreg[st] = ld16(d < kLatent ? qlp + d : qpp + (d - kLatent));
+      }
+    }
+    // the query operand of QK step st (8 bf16 of head li, as lane (g4, li) feeds them)
+    auto q_op = [&](int st) -> uint4 {
+      if constexpr (SPARSE) return sm_q[st][lane];
+      else return qreg[st];
+    };
     // The own row is attended by one wave (the one with the fewest tiles of the segment) before its tiles, while their
     // first loads are in flight. Its bf16 elements 8 lane .. + 7 and 8 (lane + 64) .. + 7 (lane < 8) and its pool slot
     // load here, with the compiler's other prologue loads.
@@ -543,11 +568,13 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
         for (int j = 0; j < NDMA; ++j)
           if (j < NDMA - 1 || lane < Geo::TAIL)
             dma_buffer16(rk, d + 1024 * j, dma_src[j]);
-        // the tile's 16 per-token scales (consecutive like its rows), in slot order
-        const __amdgpu_buffer_rsrc_t rs =
-            __builtin_amdgcn_make_buffer_rsrc((void*)(a.row_scale + row0), (short)0, 64, kBufferFlags);
-        if (lane < 16)
-          dma_buffer4(rs, d + Geo::SCALES, 4u * (uint32_t)key_of(lane));
+        if constexpr (FMT == ROWS576) {
+          // the tile's 16 per-token scales (consecutive like its rows), in slot order
+          const __amdgpu_buffer_rsrc_t rs =
+              __builtin_amdgcn_make_buffer_rsrc((void*)(a.row_scale + row0), (short)0, 64, kBufferFlags);
+          if (lane < 16)
+            dma_buffer4(rs, d + Geo::SCALES, 4u * (uint32_t)key_of(lane));
+        }
       }
     };
 
@@ -562,9 +589,10 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     // A masked key's latent bytes may be anything, and a stale NaN or Inf would survive p = 0 in PV: a tile with masked
     // keys has their latent bytes zeroed in LDS first (its scores and scales are masked by selects).
     auto sanitize = [&](uint8_t* T, uint32_t vmask) {
+      constexpr int LCH = RowFmt<FMT>::kLatentBytes / 16;  // 16-byte latent chunks per row (32 or 64)
 #pragma unroll
-      for (int it = 0; it < 8; ++it) {
-        const int idx = lane + 64 * it, r = idx >> 5, c = idx & 31;
+      for (int it = 0; it < LCH / 4; ++it) {
+        const int idx = lane + 64 * it, r = idx / LCH, c = idx % LCH;
         if (!((vmask >> r) & 1u))
           *reinterpret_cast<uint4*>(T + r * RS + (SPARSE ? 128 : 0) + 16 * c) = make_uint4(0, 0, 0, 0);
       }
@@ -574,6 +602,21 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     // byte matrix are slots 4 g4 .. 4 g4 + 3 at bytes 32 s .. 32 s + 15 and rows 4 .. 7 the same slots 16 bytes on.
     // (rs: the tile's LDS row stride; 0 for the own row standing for all 16 keys.)
     auto pv = [&](const uint8_t* T, const uint32_t (&pop)[2], int rs) {
+      if constexpr (BF16) {
+        // bf16: lane (g4, j) points the transposing read at slot 4 g4 + j / 4, dims d0 + 4 (j % 4) .. + 3, so that row
+        // k of its group's 4x16 matrix is slot 4 g4 + k at dims d0 .. d0 + 15 and lane (g4, i) receives dim d0 + i of
+        // slots 4 g4 .. 4 g4 + 3: the A operand of d-tile d0 = 64 q + 16 r
+        const uint8_t* Tb = T + key_of(4 * g4 + (li >> 2)) * rs + 8 * (li & 3);
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const uint2 t = lds_read_tr16(Tb + 2 * (64 * q + 16 * r));
+            const uint32_t op[2] = {t.x, t.y};
+            acc[q][r] = mfma_16x16x16_bf16(op, pop, acc[q][r]);
+          }
+        return;
+      }
       const uint8_t* Tv = T + key_of(4 * g4 + ((li >> 1) & 3)) * rs + (SPARSE ? 128 : 0) + 16 * (li >> 3) + 8 * (li & 1);
 #pragma unroll
       for (int s = 0; s < 16; ++s) {
@@ -589,7 +632,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     // Per-token scales of slots 4 g4 .. 4 g4 + 3 from the tile's 16 scales at S (1 for the sparse format).
     auto key_scales = [&](const uint8_t* S, float (&ks)[4]) {
       ks[0] = ks[1] = ks[2] = ks[3] = 1.0f;
-      if constexpr (!SPARSE) {
+      if constexpr (FMT == ROWS576) {
         const float4 s4 = *reinterpret_cast<const float4*>(S + 16 * g4);
         ks[0] = s4.x, ks[1] = s4.y, ks[2] = s4.z, ks[3] = s4.w;
       }
@@ -604,13 +647,24 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
 #pragma unroll
       for (int k = 0; k < 9; ++k) {
         f32x4_t& sc = scp[k % 3];
+        if constexpr (BF16) {
+          // step pair k: dims 16 (4 k + g4) .. + 15 of key key_of(li), bytes 32 (4 k + g4) .. + 31 of its row
+          const uint8_t* Tk = T + key_of(li) * rs + 32 * (4 * k + g4);
+          const uint4 w0 = *reinterpret_cast<const uint4*>(Tk), w1 = *reinterpret_cast<const uint4*>(Tk + 16);
+          const uint32_t a0[4] = {w0.x, w0.y, w0.z, w0.w}, a1[4] = {w1.x, w1.y, w1.z, w1.w};
+          const uint4 q0 = q_op(2 * k), q1 = q_op(2 * k + 1);
+          const uint32_t b0[4] = {q0.x, q0.y, q0.z, q0.w}, b1[4] = {q1.x, q1.y, q1.z, q1.w};
+          sc = mfma_16x16x32_bf16(a0, b0, sc);
+          sc = mfma_16x16x32_bf16(a1, b1, sc);
+          continue;
+        }
         if constexpr (SPARSE) {
           if (k == 0) {
             // steps 0 and 1: the bf16 rope, one chunk each
             const uint4 w0 = *reinterpret_cast<const uint4*>(Tq);
             const uint4 w1 = *reinterpret_cast<const uint4*>(Tq + 64);
             const uint32_t a0[4] = {w0.x, w0.y, w0.z, w0.w}, a1[4] = {w1.x, w1.y, w1.z, w1.w};
-            const uint4 q0 = sm_q[0][lane], q1 = sm_q[1][lane];
+            const uint4 q0 = q_op(0), q1 = q_op(1);
             const uint32_t b0[4] = {q0.x, q0.y, q0.z, q0.w}, b1[4] = {q1.x, q1.y, q1.z, q1.w};
             sc = mfma_16x16x32_bf16(a0, b0, sc);
             sc = mfma_16x16x32_bf16(a1, b1, sc);
@@ -623,7 +677,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
         fp8x4_to_bf16x4(wk.y, op0[2], op0[3]);
         fp8x4_to_bf16x4(wk.z, op1[0], op1[1]);
         fp8x4_to_bf16x4(wk.w, op1[2], op1[3]);
-        const uint4 q0 = sm_q[2 * k][lane], q1 = sm_q[2 * k + 1][lane];
+        const uint4 q0 = q_op(2 * k), q1 = q_op(2 * k + 1);
         const uint32_t b0[4] = {q0.x, q0.y, q0.z, q0.w}, b1[4] = {q1.x, q1.y, q1.z, q1.w};
         sc = mfma_16x16x32_bf16(op0, b0, sc);
         sc = mfma_16x16x32_bf16(op1, b1, sc);
@@ -670,12 +724,108 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
       [[clang::always_inline]] pv(T, pop, rs);
     };
 
-    // ---- the tile loop: wave w takes tiles t_first + w + WAVES i through its ring of DEPTH slots; DEPTH - 1 tiles'
-    // loads are in flight while one computes ----
+    // ROWS576: a tile's operands are staged in registers right after it lands (the QK chunks, the PV transposed reads,
+    // the key scales), so its ring slot is refilled while it computes: all DEPTH slots of a wave are in flight then.
+    // (bf16 rows compute from LDS: twice the operand registers would not fit beside the accumulators; sparse rows'
+    // gathers are latency-bound, and staging measured slower there.)
+    constexpr bool STAGED = FMT == ROWS576;
+    constexpr int KST = SPARSE ? 10 : 9;  // 16-byte QK chunks per lane: ROWS640 has two rope chunks
+    uint4 kst[STAGED ? KST : 1];
+    uint2 vst[STAGED ? 16 : 1];
+    float kss[4];
+    auto stage = [&](const uint8_t* T, const uint8_t* S) {
+      if constexpr (STAGED) {
+        const uint8_t* Tq = T + key_of(li) * RS + 16 * g4;
+        if constexpr (SPARSE) {
+          kst[0] = *reinterpret_cast<const uint4*>(Tq);
+          kst[1] = *reinterpret_cast<const uint4*>(Tq + 64);
+#pragma unroll
+          for (int k = 1; k < 9; ++k) kst[k + 1] = *reinterpret_cast<const uint4*>(Tq + 128 + 64 * (k - 1));
+        } else {
+#pragma unroll
+          for (int k = 0; k < 9; ++k) kst[k] = *reinterpret_cast<const uint4*>(Tq + 64 * k);
+        }
+        const uint8_t* Tv = T + key_of(4 * g4 + ((li >> 1) & 3)) * RS + (SPARSE ? 128 : 0) + 16 * (li >> 3) + 8 * (li & 1);
+#pragma unroll
+        for (int s = 0; s < 16; ++s) vst[s] = lds_read_tr8(Tv + 32 * s);
+        [[clang::always_inline]] key_scales(S, kss);
+      }
+    };
+    // scores and accumulate of the staged tile, as above
+    auto scores_staged = [&](uint32_t vmask, float (&x)[4], float& tmax) {
+      f32x4_t scp[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int k = 0; k < 9; ++k) {
+        f32x4_t& sc = scp[k % 3];
+        if constexpr (STAGED) {
+          if (SPARSE && k == 0) {
+            const uint32_t a0[4] = {kst[0].x, kst[0].y, kst[0].z, kst[0].w};
+            const uint32_t a1[4] = {kst[1].x, kst[1].y, kst[1].z, kst[1].w};
+            const uint4 q0 = q_op(0), q1 = q_op(1);
+            const uint32_t b0[4] = {q0.x, q0.y, q0.z, q0.w}, b1[4] = {q1.x, q1.y, q1.z, q1.w};
+            sc = mfma_16x16x32_bf16(a0, b0, sc);
+            sc = mfma_16x16x32_bf16(a1, b1, sc);
+            continue;
+          }
+          const uint4 wk = kst[SPARSE ? k + 1 : k];
+          uint32_t op0[4], op1[4];
+          fp8x4_to_bf16x4(wk.x, op0[0], op0[1]);
+          fp8x4_to_bf16x4(wk.y, op0[2], op0[3]);
+          fp8x4_to_bf16x4(wk.z, op1[0], op1[1]);
+          fp8x4_to_bf16x4(wk.w, op1[2], op1[3]);
+          const uint4 q0 = q_op(2 * k), q1 = q_op(2 * k + 1);
+          const uint32_t b0[4] = {q0.x, q0.y, q0.z, q0.w}, b1[4] = {q1.x, q1.y, q1.z, q1.w};
+          sc = mfma_16x16x32_bf16(op0, b0, sc);
+          sc = mfma_16x16x32_bf16(op1, b1, sc);
+        }
+      }
+      const f32x4_t sc = scp[0] + scp[1] + scp[2];
+      tmax = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = (vmask >> key_of(4 * g4 + r)) & 1u;
+        x[r] = ok ? sc[r] * base_scale * kss[r] : -INFINITY;
+        tmax = fmaxf(tmax, x[r]);
+      }
+      tmax = max_across_groups(tmax);
+    };
+    auto accumulate_staged = [&](uint32_t vmask, const float (&x)[4]) {
+      float pw[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = (vmask >> key_of(4 * g4 + r)) & 1u;
+        const float p = __builtin_amdgcn_exp2f(x[r] - m_ref);
+        l_run += p;
+        pw[r] = ok ? p * kss[r] : 0.0f;
+      }
+      const uint32_t pop[2] = {pack_bf16x2(pw[0], pw[1]), pack_bf16x2(pw[2], pw[3])};
+      if constexpr (STAGED) {
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+          uint32_t op[2];
+          fp8x4_to_bf16x4(vst[s].x, op[0], op[1]);
+          acc[s >> 1][2 * (s & 1)] = mfma_16x16x16_bf16(op, pop, acc[s >> 1][2 * (s & 1)]);
+          fp8x4_to_bf16x4(vst[s].y, op[0], op[1]);
+          acc[s >> 1][2 * (s & 1) + 1] = mfma_16x16x16_bf16(op, pop, acc[s >> 1][2 * (s & 1) + 1]);
+        }
+      }
+    };
+
+    // ---- the tile loop: wave w takes tiles t_first + w + WAVES i through its ring of DEPTH slots; while one tile
+    // computes, DEPTH (staged) or DEPTH - 1 tiles' loads are in flight ----
     {
       // VMEM operations one tile issues: its DMAs, plus the per-token scale DMA of the paged format
-      constexpr int PER_TILE = NDMA + (SPARSE ? 0 : 1);
-      static_assert((DEPTH - 1) * PER_TILE < 64, "vmcnt range");
+      constexpr int PER_TILE = NDMA + (FMT == ROWS576 ? 1 : 0);
+      constexpr int AHEAD = STAGED ? DEPTH : DEPTH - 1;  // tiles issued before the loop
+      static_assert(AHEAD * PER_TILE < 64, "vmcnt range");
+      static_assert(AHEAD <= 4, "the waits below count at most three tiles");
+      // wait until at most n tiles' loads (n <= 3) are in flight
+      auto wait_tiles = [&](int32_t n) {
+        if (n >= 3) wait_vmcnt<3 * PER_TILE>();
+        else if (n == 2) wait_vmcnt<2 * PER_TILE>();
+        else if (n == 1) wait_vmcnt<PER_TILE>();
+        else wait_vmcnt<0>();
+      };
       const int32_t t0 = t_first + wave;
       const int32_t mine = t0 < t_last ? (t_last - t0 + WAVES - 1) / WAVES : 0;
       const uint32_t ring = lds_address((lds_void*)(lds_u8*)&sm_ring[wave][0][0]);
@@ -683,24 +833,18 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
       // vmcnt 0, expcnt 7, lgkmcnt 15), before any DMA is in flight; otherwise it could wait for them again inside the
       // loop, and such a wait would drain the DMAs.
       __builtin_amdgcn_s_waitcnt(0x0f70);
-      if constexpr (!SPARSE) {
-        // the query operand, step s by wave s % WAVES: sm_q[s][lane] = dims 16 (4 (s / 2) + g4) + 8 (s % 2) .. + 7
-        const int32_t h = min(16 * hg + li, a.H - 1);
-        const uint16_t* qlp = a.ql + ((int64_t)b * a.H + h) * kLatent;
-        const uint16_t* qpp = a.qpe + ((int64_t)b * a.H + h) * kRope;
-        for (int s = wave; s < 18; s += WAVES) {
-          const int d = 16 * (4 * (s >> 1) + g4) + 8 * (s & 1);
-          dma_global16(d < kLatent ? qlp + d : qpp + (d - kLatent), lds_address((lds_void*)(lds_u8*)&sm_q[s][0]));
-        }
-      }
 #pragma unroll
-      for (int i = 0; i < DEPTH - 1; ++i)
+      for (int i = 0; i < AHEAD; ++i)
         if (i < mine) issue(ring + i * SLOT, t0 + i * WAVES);
       // The own row, quantized as the store quantizes it, into sm_own in the pool's row format (LDS and registers only:
       // nothing here may add to the VMEM count the waits below rely on).
       if (own_wave) {
         const uint32_t wv[8] = {own0.x, own0.y, own0.z, own0.w, own1.x, own1.y, own1.z, own1.w};
-        if constexpr (FMT == ROWS576) {
+        if constexpr (BF16) {
+          // the row as it is: 72 16-byte chunks, lane l holding chunks l and 64 + l (l < 8)
+          *reinterpret_cast<uint4*>(&sm_own[16 * lane]) = own0;
+          if (lane < 8) *reinterpret_cast<uint4*>(&sm_own[16 * (lane + 64)]) = own1;
+        } else if constexpr (FMT == ROWS576) {
           float m = 0.0f;
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
@@ -747,14 +891,6 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
           }
         }
       }
-      if constexpr (!SPARSE) {
-        // every wave's query DMAs have landed (the tiles' may stay in flight), then the operand is complete
-        static_assert(DEPTH == 3, "the waits below count two tiles");
-        if (mine >= 2) wait_vmcnt<2 * PER_TILE>();
-        else if (mine == 1) wait_vmcnt<PER_TILE>();
-        else wait_vmcnt<0>();
-        __syncthreads();
-      }
       // The own row as key 0 of a one-key tile whose 16 rows all read sm_own (row stride 0; the other keys masked).
       if (own_wave) {
         float xo[4], to;
@@ -773,16 +909,20 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
         for (; i < mine; ++i) {
           uint8_t* T = &sm_ring[wave][slot][0];
           if (!pending) {
-            // issue tile i + DEPTH - 1 into the slot tile i - 1 freed, then wait until tile i's loads have landed:
-            // the loads of the tiles after it may stay in flight
+            // wait until tile i's loads have landed (the loads of the tiles after it may stay in flight); unstaged,
+            // first issue tile i + DEPTH - 1 into the slot tile i - 1 freed
             const int32_t ahead = mine - 1 - i;
-            if (ahead >= DEPTH - 1) {
-              issue(ring + (slot == 0 ? DEPTH - 1 : slot - 1) * SLOT, t0 + (i + DEPTH - 1) * WAVES);
-              wait_vmcnt<(DEPTH - 1) * PER_TILE>();
-            } else if (ahead == 1) {
-              wait_vmcnt<PER_TILE>();
+            if constexpr (STAGED) {
+              wait_tiles(min(ahead, DEPTH - 1));
             } else {
-              wait_vmcnt<0>();
+              if (ahead >= DEPTH - 1) {
+                issue(ring + (slot == 0 ? DEPTH - 1 : slot - 1) * SLOT, t0 + (i + DEPTH - 1) * WAVES);
+                wait_vmcnt<(DEPTH - 1) * PER_TILE>();
+              } else if (ahead == 1) {
+                wait_vmcnt<PER_TILE>();
+              } else {
+                wait_vmcnt<0>();
+              }
             }
             vm = tile_mask(t0 + i * WAVES);
             if constexpr (SPARSE) {
@@ -792,14 +932,24 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
                 patch_aliases(T, t0 + i * WAVES, al);
               }
             }
-            [[clang::always_inline]] scores(T, vm, x, tmax, RS, T + Geo::SCALES);
+            if constexpr (STAGED) {
+              if (vm != 0xffffu) [[clang::always_inline]] sanitize(T, vm);
+              [[clang::always_inline]] stage(T, T + Geo::SCALES);
+              [[clang::always_inline]] scores_staged(vm, x, tmax);
+              // the staged reads have returned (QK has consumed its chunks): refill the slot with tile i + DEPTH
+              asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+              if (i + DEPTH < mine) issue(ring + slot * SLOT, t0 + (i + DEPTH) * WAVES);
+            } else {
+              [[clang::always_inline]] scores(T, vm, x, tmax, RS, T + Geo::SCALES);
+            }
             if (needs_rescale(tmax)) {
               pending = true;
               break;
             }
           }
           pending = false;
-          [[clang::always_inline]] accumulate(T, vm, x, RS, T + Geo::SCALES);
+          if constexpr (STAGED) [[clang::always_inline]] accumulate_staged(vm, x);
+          else [[clang::always_inline]] accumulate(T, vm, x, RS, T + Geo::SCALES);
           slot = slot == DEPTH - 1 ? 0 : slot + 1;
         }
         if (!pending) break;
@@ -810,7 +960,11 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
 
     // ---- the own row's pool store, deferred to here so that no store sits among the DMAs in flight ----
     if (own_wave && own_slot >= 0) {
-      if constexpr (FMT == ROWS576) {
+      if constexpr (BF16) {
+        uint8_t* dst = a.cache + own_slot * 1152;
+        *reinterpret_cast<uint4*>(dst + 16 * lane) = own0;
+        if (lane < 8) *reinterpret_cast<uint4*>(dst + 16 * (lane + 64)) = own1;
+      } else if constexpr (FMT == ROWS576) {
 #pragma unroll
         for (int part = 0; part < 2; ++part) {
           if (part == 1 && lane >= 8) continue;
@@ -1048,9 +1202,9 @@ extern "C" int sna_mla_decode(const void* ql_nope, const void* q_pe, const void*
                               int64_t num_blocks, int32_t cache_dtype, const sna_split_plan* plan, void* workspace,
                               int64_t workspace_bytes, void* stream) {
   ApiGuard guard;
-  if (cache_dtype != SNA_DTYPE_FP8_E4M3FN)
-    return fail(SNA_ERR_UNSUPPORTED, "mla_decode: only the FP8 per-token-scale row pool is built (dtype %d)",
-                cache_dtype);
+  if (cache_dtype != SNA_DTYPE_FP8_E4M3FN && cache_dtype != SNA_DTYPE_BF16)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode: unknown cache dtype %d", cache_dtype);
+  const bool bf16 = cache_dtype == SNA_DTYPE_BF16;
   if (B < 0 || num_heads < 1 || page_size < 16 || page_size % 16 || num_blocks < 1 || table_width < 0 ||
       table_stride < table_width || !(sm_scale > 0.0f) || num_blocks * page_size > INT32_MAX)
     return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode: bad sizes (B %d, heads %d, page %d (a multiple of 16), blocks "
@@ -1061,11 +1215,11 @@ extern "C" int sna_mla_decode(const void* ql_nope, const void* q_pe, const void*
   if (int rc = check_plan(plan, B, groups, "mla_decode", &multi)) return rc;
   if (B == 0) return SNA_OK;
   const int64_t need = sna_decode_workspace_bytes(plan, num_heads, kLatent);
-  if (!ql_nope || !q_pe || !cache || !row_scale || !block_table || !compact_new || !out || !workspace)
+  if (!ql_nope || !q_pe || !cache || (!bf16 && !row_scale) || !block_table || !compact_new || !out || !workspace)
     return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode: null pointer");
   (void)seq_lens;  // the plan's host lengths drive the launch
-  if (!aligned(ql_nope, 16) || !aligned(q_pe, 16) || !aligned(cache, 16) || !aligned(row_scale, 16) ||
-      !aligned(workspace, 256))
+  if (!aligned(ql_nope, 16) || !aligned(q_pe, 16) || !aligned(cache, 16) || !aligned(compact_new, 16) ||
+      (!bf16 && !aligned(row_scale, 16)) || !aligned(workspace, 256))
     return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode: q, cache and row_scale must be 16-byte aligned, the workspace "
                 "256-byte aligned");
   if (workspace_bytes < need)
@@ -1092,8 +1246,14 @@ extern "C" int sna_mla_decode(const void* ql_nope, const void* q_pe, const void*
   a.lse_out = nullptr;
   fill_stream_args(a, plan, (float*)workspace);
   const dim3 grid(plan->n_ctas, groups);
-  if (multi) hipLaunchKernelGGL((mla_decode_kernel<ROWS576, false, true>), grid, dim3(256), 0, (hipStream_t)stream, a);
-  else hipLaunchKernelGGL((mla_decode_kernel<ROWS576, false, false>), grid, dim3(256), 0, (hipStream_t)stream, a);
+  hipStream_t s = (hipStream_t)stream;
+  if (bf16) {
+    if (multi) hipLaunchKernelGGL((mla_decode_kernel<ROWS1152, false, true>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((mla_decode_kernel<ROWS1152, false, false>), grid, dim3(256), 0, s, a);
+  } else {
+    if (multi) hipLaunchKernelGGL((mla_decode_kernel<ROWS576, false, true>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((mla_decode_kernel<ROWS576, false, false>), grid, dim3(256), 0, s, a);
+  }
   return check_launch("mla_decode");
 }
 

@@ -156,6 +156,16 @@ __device__ __forceinline__ uint2 lds_read_tr8(const uint8_t* p) {
   return make_uint2((uint32_t)r.x, (uint32_t)r.y);
 }
 
+// ds_read_b64_tr_b16: in each 16-lane group the lanes' 8-byte chunks (8-byte aligned) form 4 rows of 16 16-bit
+// elements, row k being the chunks of lanes 4 k .. 4 k + 3; lane j receives column j, so element k of its result
+// (bits 16 k of the pair, low dword first) is element j of row k. (Measured on gfx950 with an in-bounds probe.)
+__device__ __forceinline__ uint2 lds_read_tr16(const uint8_t* p) {
+  typedef short s16x4_t_ __attribute__((ext_vector_type(4)));
+  const s16x4_t_ r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t_*)(uint8_t*)p);
+  return make_uint2((uint32_t)(uint16_t)r.x | ((uint32_t)(uint16_t)r.y << 16),
+                    (uint32_t)(uint16_t)r.z | ((uint32_t)(uint16_t)r.w << 16));
+}
+
 // Loads straight into LDS (lane i's bytes land at LDS address m0 + size * i), written as inline assembly so that the
 // compiler does not see them: it would otherwise drain every load in flight before any LDS read it cannot prove
 // disjoint from them. Callers wait for them with wait_vmcnt, counting every such load they issued after the one they

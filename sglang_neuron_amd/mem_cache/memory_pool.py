@@ -210,9 +210,10 @@ class NeuronMHATokenToKVPool:
 
 class NeuronMLATokenToKVPool:
     """The absorbed-MLA pool: per layer one compact row per token slot, ``kv_buffer[layer]`` [size + page_size, 1,
-    kv_lora_rank + qk_rope_head_dim] in row order [latent | rope] (models/deepseek_v2/model.py:110), FP8 stored as
-    uint8 (memory_pool.py:313-315), with one fp32 dequantization scale per slot in ``row_scale[layer]``. Constructor
-    arguments as SGLang's MLATokenToKVPool."""
+    kv_lora_rank + qk_rope_head_dim] in row order [latent | rope] (models/deepseek_v2/model.py:110). bf16 rows as the
+    reference's DeepSeek-V2 pool holds them (memory_pool.py:306-351, models/catalog.py:230-231), or FP8 stored as
+    uint8 (memory_pool.py:313-315) with one fp32 dequantization scale per slot in ``row_scale[layer]`` (bf16 pools
+    have no row scales). Constructor arguments as SGLang's MLATokenToKVPool."""
 
     publishes_kv_layer_ids = True
 
@@ -222,16 +223,17 @@ class NeuronMLATokenToKVPool:
         _check_pool_kwargs("mla", kwargs)
         if enable_memory_saver:
             raise ValueError("the MLA pool does not support enable_memory_saver")
-        if dtype not in (FP8, torch.uint8):
-            raise ValueError(f"the HIP MLA decode reads FP8 rows with per-token scales, not {dtype}")
+        if dtype not in (FP8, torch.uint8, torch.bfloat16):
+            raise ValueError(f"the HIP MLA decode reads bf16 rows or FP8 rows with per-token scales, not {dtype}")
         if kv_lora_rank + qk_rope_head_dim != 576 or qk_rope_head_dim != 64:
             raise ValueError("the HIP MLA decode reads 576-wide rows (kv_lora_rank 512 + rope 64)")
         if page_size % 16:
             raise ValueError(f"the HIP MLA decode reads pages that are whole 16-slot tiles, not {page_size}")
         self.size = int(size)
         self.page_size = int(page_size)
-        self.dtype = FP8
-        self.store_dtype = torch.uint8
+        self.fp8 = dtype != torch.bfloat16
+        self.dtype = FP8 if self.fp8 else torch.bfloat16
+        self.store_dtype = torch.uint8 if self.fp8 else torch.bfloat16
         self.kv_lora_rank = int(kv_lora_rank)
         self.qk_rope_head_dim = int(qk_rope_head_dim)
         self.kv_cache_dim = self.kv_lora_rank + self.qk_rope_head_dim
@@ -244,7 +246,7 @@ class NeuronMLATokenToKVPool:
             torch.zeros((self.size + self.page_size, 1, self.kv_cache_dim), dtype=self.store_dtype, device=self.device)
             for _ in range(self.layer_num)]
         self.row_scale: List[Tensor] = [torch.ones(self.size + self.page_size, dtype=torch.float32, device=self.device)
-                                        for _ in range(self.layer_num)]
+                                        for _ in range(self.layer_num)] if self.fp8 else []
         self.mem_usage = self.get_kv_size_bytes() / GB
 
     @property
@@ -268,8 +270,10 @@ class NeuronMLATokenToKVPool:
     def get_kv_buffer(self, layer_id: int) -> Tuple[Tensor, Tensor]:
         return self.get_key_buffer(layer_id), self.get_value_buffer(layer_id)
 
-    def get_row_scale(self, layer_id: int) -> Tensor:
-        return self.row_scale[self._idx(layer_id)]
+    def get_row_scale(self, layer_id: int) -> Optional[Tensor]:
+        """The layer's per-slot fp32 scales (FP8 rows), None for bf16 rows."""
+        i = self._idx(layer_id)
+        return self.row_scale[i] if self.fp8 else None
 
     def get_block_buffer(self, layer_id: int) -> Tensor:
         """The layer's rows as blocks [num_blocks, page_size, kv_cache_dim] of the stored bytes, a view
@@ -295,11 +299,11 @@ class NeuronMLATokenToKVPool:
 
     def _store(self, layer_id: int, loc: Tensor, rows: Tensor) -> None:
         i = self._idx(layer_id)
-        ops.kv_store_mla(rows, loc, self.kv_buffer[i], self.row_scale[i])
+        ops.kv_store_mla(rows, loc, self.kv_buffer[i], self.row_scale[i] if self.fp8 else None)
 
     def get_kv_size_bytes(self) -> int:
         rows = (self.size + self.page_size) * self.layer_num
-        return rows * (self.kv_cache_dim * self.store_dtype.itemsize + 4)
+        return rows * (self.kv_cache_dim * self.store_dtype.itemsize + (4 if self.fp8 else 0))
 
     def get_contiguous_buf_infos(self):
         """(ptrs, lens, item_lens) of each layer's rows: page p is item_len bytes at ptr + p * item_len
@@ -311,7 +315,7 @@ class NeuronMLATokenToKVPool:
     def get_scale_buf_infos(self):
         """(ptrs, lens, item_lens) of each layer's per-slot fp32 row scales, paged like the rows (page p is page_size *
         4 bytes at ptr + p * item_len). The reference's MLA pool has no such scales; a transfer of this pool moves
-        these items beside the rows of get_contiguous_buf_infos."""
+        these items beside the rows of get_contiguous_buf_infos. A bf16 pool has none: empty lists."""
         ptrs = [t.data_ptr() for t in self.row_scale]
         lens = [t.numel() * t.element_size() for t in self.row_scale]
         return ptrs, lens, [self.page_size * 4] * len(self.row_scale)

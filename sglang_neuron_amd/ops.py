@@ -361,7 +361,7 @@ def paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: T
     return prepare_paged_decode_gqa(q, k_cache, v_cache, block_table, seq_lens, k_new, v_new, **kw)()
 
 
-def prepare_mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: Tensor, block_table: Tensor,
+def prepare_mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: Optional[Tensor], block_table: Tensor,
                        seq_lens: Tensor, compact_new: Tensor, *, sm_scale: float, page_size: int,
                        new_slots: Optional[Tensor] = None, out: Optional[Tensor] = None, host_seq_lens=None,
                        plan: Optional[_lib.SplitPlan] = None, workspace: Optional[Tensor] = None) -> Prepared:
@@ -374,13 +374,15 @@ def prepare_mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: 
     _need(cache.shape[-1] == 576 and cache.is_contiguous(), f"MLA rows must be contiguous [.., 576], got "
           f"{tuple(cache.shape)}")
     code = cache_dtype_code(cache.dtype)
-    _need(code == _lib.DTYPE_FP8_E4M3FN, "the HIP MLA decode reads the FP8 row pool")
     n_slots = cache.numel() // 576
     P = int(page_size)
     _need(n_slots % P == 0, f"{n_slots} rows are not whole pages of {P}")
     nb = n_slots // P
-    _need(row_scale.numel() == n_slots and row_scale.dtype == torch.float32 and row_scale.is_contiguous(),
-          "row_scale must be contiguous fp32 with one entry per row")
+    if code == _lib.DTYPE_FP8_E4M3FN:
+        _need(row_scale is not None and row_scale.numel() == n_slots and row_scale.dtype == torch.float32 and
+              row_scale.is_contiguous(), "FP8 rows need row_scale: contiguous fp32 with one entry per row")
+    else:
+        row_scale = None  # bf16 rows carry no scale
     ql_nope = _contig(ql_nope, "ql_nope", torch.bfloat16)
     q_pe = _contig(q_pe, "q_pe", torch.bfloat16)
     compact_new = _contig(compact_new.reshape(B, 576), "compact_new", torch.bfloat16)
@@ -410,9 +412,10 @@ def prepare_mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: 
 
 def mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: Tensor, block_table: Tensor,
                seq_lens: Tensor, compact_new: Tensor, **kw) -> Tensor:
-    """Absorbed-MLA decode of ql_nope [B, H, 512] / q_pe [B, H, 64] over a layer's FP8 rows [slots, 576] (uint8 or
-    float8 storage) with per-token scales ``row_scale`` [slots], the history through ``block_table`` and the own row
-    ``compact_new`` [B, 576] in-band (stored at ``new_slots`` when given). Keyword arguments: sm_scale, page_size,
+    """Absorbed-MLA decode of ql_nope [B, H, 512] / q_pe [B, H, 64] over a layer's rows [slots, 576]: FP8 (uint8 or
+    float8 storage) with per-token scales ``row_scale`` [slots], or bf16 (``row_scale`` unused, may be None); the
+    history through ``block_table`` and the own row ``compact_new`` [B, 576] in-band (stored at ``new_slots`` when
+    given). Keyword arguments: sm_scale, page_size,
     new_slots, out, host_seq_lens, plan. Returns [B, H, 512] bf16.
 
     Stands in for mla_decode (ops/attention/mla.py:32-53)."""

@@ -174,10 +174,11 @@ class MlaCase:
             setattr(out, k, getattr(self, k).to(device))
         return out
 
-    def kv_bytes_per_step(self) -> int:
+    def kv_bytes_per_step(self, bf16: bool = False) -> int:
         keys = int((self.seq_lens - 1).sum())
-        b = keys * (576 + 4)                               # fp8 row + per-token scale
-        b += self.B * (576 * 2 + 576 + 4)                  # own row: bf16 in, fp8 row + scale out
+        row = 1152 if bf16 else 576 + 4                    # bf16 row, or fp8 row + per-token scale
+        b = keys * row
+        b += self.B * (576 * 2 + row)                      # own row: bf16 in, row (+ scale) out
         b += self.B * self.H * (512 + 64) * 2 + self.B * self.H * 512 * 2
         pages = int(((self.seq_lens - 1 + self.P - 1) // self.P).sum())
         b += pages * 4 + self.B * 4 * 2
@@ -318,14 +319,14 @@ def gqa_pool(case: GqaCase, device="cuda"):
     return kc, vc, ks, vs
 
 
-def mla_pool(case: MlaCase, device="cuda"):
+def mla_pool(case: MlaCase, device="cuda", bf16: bool = False):
     """(rows [slots, 576] uint8, row_scale [slots]) of one layer on ``device``, the prior rows stored by the HIP
-    per-token FP8 store."""
+    per-token FP8 store; with ``bf16``, (rows [slots, 576] bf16, None) stored as they are."""
     from . import ops
 
     n = case.num_blocks * case.P
-    cache = torch.zeros(n, 576, dtype=torch.uint8, device=device)
-    scale = torch.zeros(n, dtype=torch.float32, device=device)
+    cache = torch.zeros(n, 576, dtype=torch.bfloat16 if bf16 else torch.uint8, device=device)
+    scale = None if bf16 else torch.zeros(n, dtype=torch.float32, device=device)
     if case.prior_slots.numel():
         ops.kv_store_mla(case.prior_rows.to(device), case.prior_slots.to(device), cache, scale)
     return cache, scale

@@ -71,11 +71,12 @@ def cache_bytes(c: torch.Tensor) -> torch.Tensor:
 
 # ---- MLA ----
 
-def mla_oracle(case: workloads.MlaCase):
-    """(out, cache, row_scale) on the CPU: prefill rows, decode, then the own row's store."""
+def mla_oracle(case: workloads.MlaCase, bf16: bool = False):
+    """(out, cache, row_scale) on the CPU: prefill rows, decode, then the own row's store. ``bf16``: a bf16 row pool
+    (row_scale None)."""
     n = case.num_blocks * case.P
-    cache = torch.zeros(n, 576, dtype=torch.uint8)
-    scale = torch.zeros(n, dtype=torch.float32)
+    cache = torch.zeros(n, 576, dtype=torch.bfloat16 if bf16 else torch.uint8)
+    scale = None if bf16 else torch.zeros(n, dtype=torch.float32)
     ost.kv_store_mla(case.prior_rows.cpu(), case.prior_slots.cpu(), cache, scale)
     out = oatt.mla_decode(case.ql_nope.cpu(), case.q_pe.cpu(), cache, scale, case.block_table, case.seq_lens,
                           case.compact_new.cpu(), sm_scale=case.sm_scale, page_size=case.P)
@@ -83,8 +84,8 @@ def mla_oracle(case: workloads.MlaCase):
     return out, cache, scale
 
 
-def mla_gpu_pool(case: workloads.MlaCase, dev="cuda"):
-    return workloads.mla_pool(case, dev)
+def mla_gpu_pool(case: workloads.MlaCase, dev="cuda", bf16: bool = False):
+    return workloads.mla_pool(case, dev, bf16)
 
 
 def mla_gpu_decode(case: workloads.MlaCase, cache, scale, dev="cuda", store_new=True):

@@ -122,6 +122,25 @@ def test_backend_mla_decode():
     assert torch.equal(pool.row_scale[0].cpu()[written], scale_o[written]), "row scales differ"
 
 
+def test_backend_mla_decode_bf16_pool():
+    """The reference's DeepSeek-V2 serving pool: bf16 rows at page 128 (models/catalog.py:230-231)."""
+    case = workloads.mla_case(overrides={"B": 4, "P": 128, "lens": (1, 3000)})
+    want, cache_o, _ = mla_oracle(case, bf16=True)
+    announce(f"backend mla bf16: B={case.B} lens={case.seq_lens.tolist()}")
+    pool = NeuronMLATokenToKVPool((case.num_blocks - 1) * case.P, case.P, torch.bfloat16, 512, 64, 1, DEV)
+    assert pool.get_row_scale(0) is None and pool.get_scale_buf_infos() == ([], [], [])
+    layer = SimpleNamespace(layer_id=0, tp_q_head_num=case.H, scaling=case.sm_scale)
+    T = case.prior_slots.numel()
+    pool.set_kv_buffer(layer, case.prior_slots.to(DEV), case.prior_rows.reshape(T, 1, 576).to(DEV))
+    backend = _backend(pool, case.block_table, case.seq_lens, case.P)
+    q = torch.cat([case.ql_nope, case.q_pe], dim=-1).to(DEV)
+    out = backend.forward_decode(q, case.compact_new.to(DEV), None, layer, _batch(case.seq_lens, case.new_slots))
+    torch.cuda.synchronize()
+    assert_close_attn(out.reshape(case.B, case.H, 512), want, "mla bf16")
+    assert torch.equal(pool.kv_buffer[0].cpu().reshape(-1, 576).view(torch.int16), cache_o.view(torch.int16)), \
+        "row pool differs"
+
+
 def test_backend_mla_set_mla_kv_buffer_matches_full_rows():
     case = workloads.mla_case(overrides={"B": 2, "lens": (40, 90)})
     announce("backend mla set_mla_kv_buffer")

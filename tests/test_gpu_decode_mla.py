@@ -21,6 +21,8 @@ MLA_CASES = [
     # page 128: the page the reference serves DeepSeek-V2 with (docs/model-recipes/deepseek-v2.md:122)
     ("cfg3-page128", {"B": 6, "P": 128, "lens": (1024, 16384)}),
     ("cfg3-full", {}),                                                   # the bench workload at its full size
+    # more rows than workgroups (20 heads: two head groups of 128 workgroups): ranges span several rows
+    ("multi-row-ranges", {"B": 200, "H": 20, "lens": (1, 200)}),
 ]
 
 
@@ -35,6 +37,29 @@ def test_mla_decode_matches_oracle(name, over):
     assert_close_attn(out, want, name)
     assert torch.equal(cache.cpu(), cache_o), "row pool differs"
     assert torch.equal(scale.cpu(), scale_o), "row scales differ"
+
+
+# bf16 rows, the reference's DeepSeek-V2 pool (models/catalog.py:230-231: bf16 KV at page 128)
+MLA_BF16_CASES = [
+    ("bf16-cfg3-page128", {"B": 8, "P": 128, "lens": (1024, 16384)}),
+    ("bf16-cfg3-full", {}),
+    ("bf16-ragged", {"B": 6, "lens": (1, 300)}),
+    ("bf16-heads-20", {"B": 2, "H": 20, "lens": (100, 1000)}),
+    ("bf16-page-16", {"B": 3, "P": 16, "lens": (40, 900)}),
+    ("bf16-multi-row-ranges", {"B": 200, "H": 20, "lens": (1, 200)}),
+]
+
+
+@pytest.mark.parametrize("name,over", MLA_BF16_CASES, ids=[c[0] for c in MLA_BF16_CASES])
+def test_mla_decode_bf16_rows_matches_oracle(name, over):
+    case = workloads.mla_case(overrides=over)
+    want, cache_o, _ = mla_oracle(case, bf16=True)
+    announce(f"mla {name}: B={case.B} H={case.H} P={case.P} lens={case.seq_lens.tolist()[:8]}")
+    cache, scale = mla_gpu_pool(case, bf16=True)
+    out = mla_gpu_decode(case, cache, scale)
+    torch.cuda.synchronize()
+    assert_close_attn(out, want, name)
+    assert torch.equal(cache.cpu().view(torch.int16), cache_o.view(torch.int16)), "row pool differs"
 
 
 DSA_CASES = [

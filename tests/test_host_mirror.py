@@ -136,7 +136,7 @@ def test_mla_pool_shapes_and_views():
     assert tuple(pool.get_row_scale(0).shape) == (320,)
     ptrs, lens, items = pool.get_contiguous_buf_infos()
     assert lens == [320 * 576] * 2 and items == [576 * 64] * 2
-    for bad in ({"dtype": torch.bfloat16}, {"page_size": 8}):
+    for bad in ({"dtype": torch.float16}, {"page_size": 8}):
         args = dict(size=256, page_size=64, dtype=torch.float8_e4m3fn, kv_lora_rank=512, qk_rope_head_dim=64,
                     layer_num=1, device="cpu")
         args.update(bad)
@@ -144,6 +144,16 @@ def test_mla_pool_shapes_and_views():
             NeuronMLATokenToKVPool(**args)
     with pytest.raises(ValueError):
         NeuronMLATokenToKVPool(256, 64, torch.float8_e4m3fn, 512, 64, 1, "cpu", use_dsa=True)
+
+
+def test_mla_pool_bf16_rows():
+    """bf16 rows as the reference's DeepSeek-V2 pool holds them: no row scales, 1152-byte rows."""
+    pool = NeuronMLATokenToKVPool(256, 128, torch.bfloat16, 512, 64, 2, "cpu")
+    assert pool.kv_buffer[0].dtype == torch.bfloat16 and tuple(pool.kv_buffer[0].shape) == (256 + 128, 1, 576)
+    assert pool.get_row_scale(0) is None and pool.get_scale_buf_infos() == ([], [], [])
+    ptrs, lens, items = pool.get_contiguous_buf_infos()
+    assert lens == [384 * 1152] * 2 and items == [1152 * 128] * 2
+    assert pool.get_kv_size_bytes() == 2 * 384 * 1152
 
 
 def test_dsa_pool_shapes():

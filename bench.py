@@ -797,7 +797,7 @@ def run_one(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: float, d
         for k in per_config:
             pm = measure_decode(k, steps_n, warmup, cpu, cpu_budget * 2 / 3, dev)
             name = "cfg" + k.replace("swa", "-swa128").replace("bf16", "-bf16")
-            pm["workload"] = pm.pop("config")["workload"]
+            pm["workload"] = pm["config"]["workload"]
             line["per_config"][name] = pm
     return line
 

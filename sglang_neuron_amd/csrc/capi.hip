@@ -30,8 +30,9 @@ int32_t host_tiles(int32_t seq_len, int32_t window, int32_t tile) { return host_
 // The MLA / DSA stream split: every row's key tiles (at least one, so a row with no prior key still has a workgroup
 // to attend its own row) laid end to end, cut into n_ctas ranges of equal tile counts. A workgroup runs per CU (the
 // kernel's LDS holds one), so n_ctas is the CU count over the head groups, fewer when there are fewer tiles; a sparse workgroup resolves at
-// most kMlaMaxSplitKeys indices in LDS, and sparse rows are latency-bound gathers, so a sparse plan aims for 16 tiles
-// per workgroup.
+// most kMlaMaxSplitKeys indices in LDS, and sparse rows are latency-bound gathers, so a sparse plan aims for 8 tiles
+// per workgroup (two per wave: every tile's gathers go out at once; measured on cfg5, 16 workgroups per 2048-index
+// row beat 8 by ~1.3 us and 4 by ~8 us).
 int plan_stream(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32_t n_keys_per_row, int32_t groups,
                 int32_t num_cus, sna_split_plan* plan) {
   if (kind == 1 && !host_seq_lens)
@@ -60,7 +61,7 @@ int plan_stream(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32_t n
   int64_t n = 0;
   if (total > 0) {
     constexpr int32_t kSparseCap = kMlaMaxSplitKeys / 16;
-    n = kind == 1 ? std::min<int64_t>(cus, total) : std::min<int64_t>(cus, std::max<int64_t>((total + 15) / 16, 1));
+    n = kind == 1 ? std::min<int64_t>(cus, total) : std::min<int64_t>(cus, std::max<int64_t>((total + 7) / 8, 1));
     if (kind == 2) n = std::max<int64_t>(n, (total + kSparseCap - 1) / kSparseCap);
     if (n > SNA_MAX_CTAS)
       return fail(SNA_ERR_UNSUPPORTED, "plan_decode: %lld index tiles need more than %d workgroups of %d tiles",

@@ -160,9 +160,11 @@ typedef struct {
   int32_t depth;        /* GQA: tiles each wave keeps in its register ring (2: two waves per SIMD; 4: one wave per
                            SIMD with three tiles in flight). The planner picks it; splits were sized for it. */
   int32_t work_n;       /* GQA: entries in work[] (0: the kernels locate their items from the device's seq_lens) */
-  uint32_t work[SNA_MAX_WORK_MAP]; /* GQA, a plan from host seq_lens with n_work <= SNA_MAX_WORK_MAP: item i is row
-                           work[i] >> 6, split work[i] & 63, in launch order. The decode kernels read it from their
-                           arguments and skip the device-side search over seq_lens. */
+  uint32_t work[SNA_MAX_WORK_MAP]; /* GQA, a plan from host seq_lens with n_work and B <= SNA_MAX_WORK_MAP: item i
+                           is row (work[i] & 0x7fffffff) >> 6, split work[i] & 63, bit 31 set on a row's last item, in
+                           launch order (a row's items consecutive, splits 0, 1, ...). The decode kernels read it from their arguments and skip the device-side search
+                           over seq_lens; a row's last item attends its own token, and its combine merges exactly the
+                           row's items, even where the device's length needs fewer splits. */
   int32_t n_ctas;       /* MLA / DSA: workgroups of the stream split (per 16-head group) */
   int32_t total_tiles;  /* MLA / DSA: tiles of all rows */
   int32_t wait_polls;   /* MLA / DSA: how many times a workgroup that published a partial polls for its row's last
@@ -179,8 +181,9 @@ typedef struct {
  * row's key count. `window` is the sliding window (0 = full). `ctas_per_item` is the number of workgroups that
  * one (sequence, split) item launches: num_kv_heads for GQA, and 1 for MLA and DSA. `num_cus` is the device's CU
  * count (0 = 256). Returns SNA_OK and fills *plan. MLA and DSA plans hold at most SNA_MAX_PLAN_ROWS rows of at most
- * 65535 tiles each. GQA: host and device seq_lens must agree: a device length past the host's leaves its extra splits
- * unread, though all reads stay inside the workspace. */
+ * 65535 tiles each. GQA: a device length needing more splits than the plan holds leaves those keys unread (all
+ * reads stay inside the workspace; the row's own token is still attended and stored); a shorter one only leaves
+ * splits empty. */
 int sna_plan_decode(int32_t kind, const int32_t *host_seq_lens, int32_t B, int32_t max_seq_len, int32_t window,
                     int32_t n_keys_per_row, int32_t ctas_per_item, int32_t num_cus, sna_split_plan *plan);
 

@@ -271,10 +271,11 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
   plan->depth = kind == 0 ? depth : 0;
   // the item -> (row, split) map, when the lengths are exact and the items fit it (the order locate_work finds)
   plan->work_n = 0;
-  if (kind != 2 && host_seq_lens && n_work <= SNA_MAX_WORK_MAP && B < (1 << 26)) {
+  if (kind != 2 && host_seq_lens && n_work <= SNA_MAX_WORK_MAP && B <= SNA_MAX_WORK_MAP) {
     int32_t i = 0;
     for (int32_t b = 0; b < B; ++b)
-      for (int32_t s = 0, n = splits_of_row(b, split_tiles); s < n; ++s) plan->work[i++] = ((uint32_t)b << 6) | s;
+      for (int32_t s = 0, n = splits_of_row(b, split_tiles); s < n; ++s)
+        plan->work[i++] = ((uint32_t)b << 6) | s | (s == n - 1 ? kWorkLastSplit : 0u);
     plan->work_n = i;
   }
   return SNA_OK;

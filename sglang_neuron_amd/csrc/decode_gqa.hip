@@ -54,11 +54,19 @@ struct GqaArgs {
   int32_t n_work;
   int32_t max_splits;
   int32_t work_n;                       // entries of work (0: locate items from seq_lens)
-  uint32_t work[SNA_MAX_WORK_MAP];      // item -> row << 6 | split, from the plan
+  uint32_t work[SNA_MAX_WORK_MAP];      // item -> row << 6 | split (| kWorkLastSplit on a row's last), from the plan
+  uint8_t row_splits[SNA_MAX_WORK_MAP]; // with a map (B <= SNA_MAX_WORK_MAP): the map's items per row
   float* ws_o;   // [B, max_splits, H, D]  unnormalized partials (V dequantized)
   float* ws_ml;  // [B, max_splits, H, 2]  reference max (log2 domain) and softmax sum
   uint16_t* out;
 };
+
+// The splits this launch runs for row b: its entries in the plan's item map (counted on the host), or (no map: items
+// located from seq_lens) the device length's split count up to the plan's.
+__device__ __forceinline__ int32_t launched_splits(const GqaArgs& a, int32_t b, int32_t seq_len) {
+  if (a.work_n > 0) return a.row_splits[b];
+  return min(splits_of<32>(seq_len, a.window, a.split_tiles), max(a.max_splits, 1));
+}
 
 template <int NB>
 __device__ __forceinline__ void load_bytes(const uint8_t* p, uint32_t (&dst)[NB / 4]) {
@@ -115,7 +123,7 @@ void gqa_decode_kernel(GqaArgs a) {
   int32_t b, split;
   if ((int32_t)blockIdx.x < a.work_n) {  // the plan's map, from the kernel arguments
     const uint32_t e = a.work[blockIdx.x];
-    b = (int32_t)(e >> 6);
+    b = (int32_t)((e & ~kWorkLastSplit) >> 6);
     split = (int32_t)(e & 63u);
   } else {
     locate_work<32>(a.seq_lens, a.B, a.window, a.split_tiles, (int32_t)blockIdx.x, b, split);
@@ -294,8 +302,13 @@ void gqa_decode_kernel(GqaArgs a) {
   // The step's own token is attended in-band by the row's last split (and stored). The last split is the row's
   // shortest, so the own token's work delays a workgroup that finishes early rather than one of the row's
   // full-length splits. Its operands (k, v, the slot and the query elements the score needs) load here, with the
-  // prologue's loads, so that nothing after the tile loop waits for memory.
-  const bool own = split == splits_of<32>(L, a.window, a.split_tiles) - 1;  // uniform
+  // prologue's loads, so that nothing after the tile loop waits for memory. "Last" is the last split this launch
+  // runs for the row: the plan's map counts them (a row's items are consecutive there, splits in order); without a map
+  // the items were located from seq_lens, up to the plan's split count. So the own token is attended and stored even
+  // when the device's length disagrees with the plan's.
+  // (with a map the item's own flag says it, from the entry already loaded)
+  const bool own = (int32_t)blockIdx.x < a.work_n ? (a.work[blockIdx.x] & kWorkLastSplit) != 0
+                                                   : split == launched_splits(a, b, L) - 1;  // uniform
   constexpr int OWN_J = (16 + WAVES - 1) / WAVES;  // query heads per wave in the own token's score
   uint32_t own_kb = 0, own_vb = 0;
   int64_t own_dst = -1;
@@ -454,7 +467,7 @@ __global__ __launch_bounds__(64) void gqa_combine_kernel(GqaArgs a) {
     for (int v = 0; v < V; ++v) x[k][v] = k < S ? ob[k * sstride + v] : 0.0f;
   float2 ml = make_float2(-INFINITY, 0.0f);
   if (lane < S) ml = *reinterpret_cast<const float2*>(a.ws_ml + (row0 + (int64_t)lane * a.H) * 2);
-  const int32_t n = min(splits_of<32>(ld_const(a.seq_lens + b), a.window, a.split_tiles), S);
+  const int32_t n = min(launched_splits(a, b, ld_const(a.seq_lens + b)), S);
   if (n == 0) return;  // a row with no prior key: the lone-token kernel writes it
   const float m = lane < n ? ml.x : -INFINITY, l = lane < n ? ml.y : 0.0f;
   const float sink = a.sinks ? a.sinks[h] * kLog2e : -INFINITY;
@@ -490,7 +503,7 @@ __global__ __launch_bounds__(64) void gqa_combine_kernel(GqaArgs a) {
 template <int D, bool FP8>
 __global__ __launch_bounds__(128) void gqa_lone_token_kernel(GqaArgs a) {
   const int b = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
-  if (splits_of<32>(a.seq_lens[b], a.window, a.split_tiles) > 0) return;
+  if (launched_splits(a, b, a.seq_lens[b]) > 0) return;
   __shared__ float sm_kn[D], sm_vn[D];
   const float kscale = FP8 ? a.k_scale[g] : 1.0f, vscale = FP8 ? a.v_scale[g] : 1.0f;
   if (tid < D) {
@@ -633,6 +646,10 @@ int decode_gqa(const char* what, const void* q, const void* k_cache, const void*
   a.max_splits = plan->max_splits;
   a.work_n = plan->work_n;
   for (int32_t i = 0; i < plan->work_n; ++i) a.work[i] = plan->work[i];
+  if (plan->work_n > 0) {
+    for (int32_t r = 0; r < B; ++r) a.row_splits[r] = 0;
+    for (int32_t i = 0; i < plan->work_n; ++i) ++a.row_splits[(plan->work[i] & ~kWorkLastSplit) >> 6];
+  }
   float* ws = (float*)workspace;
   a.ws_o = need > 0 ? ws : nullptr;
   a.ws_ml = need > 0 ? ws + (int64_t)B * plan->max_splits * num_q_heads * head_dim : nullptr;

@@ -30,6 +30,8 @@ constexpr int64_t kStreamCounterBytes = 256 * 1024;  // (2 * kStreamMaxCounters 
 static_assert((2 * kStreamMaxCounters + 1) * kCounterStride * 4 <= kStreamCounterBytes, "the counters fit");
 // Polls of a row's arrival counter by a workgroup that published a partial, before it leaves the merge to others.
 constexpr int kStreamWaitPolls = 96;
+// A GQA plan's item map entry: row << 6 | split, with this bit set on a row's last item (its own token's split).
+constexpr uint32_t kWorkLastSplit = 1u << 31;
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 

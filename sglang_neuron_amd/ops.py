@@ -220,6 +220,40 @@ def plan_decode(kind: int, B: int, *, host_seq_lens: Union[Tensor, Sequence[int]
     return plan
 
 
+def _row_splits(L: int, window: int, split_tiles: int) -> int:
+    """A GQA row's split count: its key tiles of 32 from its window's first key to its last prior key, over
+    split_tiles (the kernels' splits_of)."""
+    if L <= 1:
+        return 0
+    hi, lo = L - 1, (L - window if window > 0 and L - window > 0 else 0)
+    if hi <= lo:
+        return 0
+    return (-(-hi // 32) - lo // 32 + split_tiles - 1) // split_tiles
+
+
+def check_plan_lengths(plan: _lib.SplitPlan, kind: int, host_seq_lens, window: int = 0) -> None:
+    """Refuse a plan that cannot serve these lengths (host copies): a GQA plan whose item map or split count misses a
+    split some row needs (those keys would be dropped), an MLA plan made for other key counts (its launch is cut by
+    the plan's). Raises ValueError naming the first row."""
+    lens = [int(x) for x in torch.as_tensor(host_seq_lens).reshape(-1).tolist()]
+    _need(len(lens) == plan.batch, f"a plan for {plan.batch} rows, {len(lens)} lengths")
+    if kind == _lib.KIND_GQA:
+        need = [_row_splits(L, window, plan.split_tiles) for L in lens]
+        if plan.work_n > 0:
+            have = [0] * len(lens)
+            for i in range(plan.work_n):
+                have[(plan.work[i] & 0x7FFFFFFF) >> 6] += 1
+        else:
+            have = [max(plan.max_splits, 1)] * len(lens)
+        for b, (n, h) in enumerate(zip(need, have)):
+            _need(n <= h, f"row {b}: seq_len {lens[b]} needs {n} splits, the plan runs {h} (made for other lengths)")
+        _need(sum(need) <= plan.n_work, f"the lengths need {sum(need)} split items, the plan runs {plan.n_work}")
+    elif kind == _lib.KIND_MLA:
+        for b, L in enumerate(lens):
+            _need(plan.row_keys[b] == max(L - 1, 0),
+                  f"row {b}: seq_len {L}, the plan was made for {plan.row_keys[b] + 1} (its launch is cut by them)")
+
+
 def check_decode_operands(seq_lens: Tensor, block_table: Tensor, new_slots: Optional[Tensor], page_size: int,
                           num_blocks: int) -> None:
     """Refuse a decode batch whose host operands the kernels cannot serve (sna_check_decode_operands): a seq_len
@@ -333,10 +367,12 @@ def prepare_paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_
     if out is None:
         out = torch.empty(B, H, d, dtype=torch.bfloat16, device=dev)
     _need(out.shape == (B, H, d) and out.dtype == torch.bfloat16 and out.is_contiguous(), "bad out tensor")
+    hl = _host_lens(seq_lens, host_seq_lens)
     if plan is None:
-        hl = _host_lens(seq_lens, host_seq_lens)
         plan = plan_decode(_lib.KIND_GQA, B, host_seq_lens=hl, max_seq_len=table.shape[1] * P, window=window,
                            ctas_per_item=G, num_cus=_num_cus(dev))
+    elif hl is not None:
+        check_plan_lengths(plan, _lib.KIND_GQA, hl, window)
     lib = _lib.load()
     args = (_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), _ptr(table), table.stride(0),
             table.shape[1], _ptr(lens), _ptr(k_new), _ptr(v_new), _ptr(new_slots), _ptr(sinks), int(window),
@@ -396,11 +432,13 @@ def prepare_mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: 
     if out is None:
         out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
     _need(out.shape == (B, H, 512) and out.dtype == torch.bfloat16 and out.is_contiguous(), "bad out tensor")
+    hl = _host_lens(seq_lens, host_seq_lens)
     if plan is None:
         # the launch runs on host lengths: read the device's once when the caller has no host copy
-        hl = _host_lens(seq_lens, host_seq_lens)
         plan = plan_decode(_lib.KIND_MLA, B, host_seq_lens=hl if hl is not None else lens.cpu(),
                            ctas_per_item=(H + 15) // 16, num_cus=_num_cus(dev))
+    elif hl is not None:
+        check_plan_lengths(plan, _lib.KIND_MLA, hl)
     ws = _stream_workspace_arg(workspace, plan, H, dev)
     lib = _lib.load()
     args = (_ptr(ql_nope), _ptr(q_pe), _ptr(cache), _ptr(row_scale), _ptr(table), table.stride(0), table.shape[1],

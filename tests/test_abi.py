@@ -89,8 +89,8 @@ def test_plan_invariants(lib, kind, lens, window, ctas):
     if p.depth == 4:  # one-round plans fit the resident target unless splits are capped
         assert p.n_work * ctas <= p.target_ctas or p.split_tiles == max((max(lens) - 1 + tile - 1) // tile, 4)
     # the item map the kernels read instead of searching seq_lens: (row, split) in launch order
-    want = [(b << 6) | sp for b, nb in enumerate(n) for sp in range(nb)]
-    if len(want) <= 512:
+    want = [(b << 6) | sp | (1 << 31 if sp == nb - 1 else 0) for b, nb in enumerate(n) for sp in range(nb)]
+    if len(want) <= 512 and len(lens) <= 512:
         assert p.work_n == len(want) and list(p.work[:p.work_n]) == want
     else:
         assert p.work_n == 0
@@ -216,6 +216,19 @@ def test_decode_entry_checks_arguments_before_touching_the_gpu(lib):
     rc = lib.sna_paged_decode_gqa(null, null, null, null, null, null, 8, 8, null, null, null, null, null, 0, 0.1, null,
                                   2, 4, 2, 128, 16, 10, 1, ctypes.byref(bad), null, 0, null)
     assert rc == _lib.SNA_ERR_INVALID_ARGUMENT and b"item" in lib.sna_last_error()
+    # a map whose rows are not consecutive, splits in order (the kernel counts a row's splits from it)
+    rc2, p2 = _plan(lib, _lib.KIND_GQA, [3000, 3000], ctas=2)
+    assert rc2 == 0 and p2.work_n >= 4
+    bad = _lib.SplitPlan.from_buffer_copy(p2)
+    bad.work[0], bad.work[1] = bad.work[1], bad.work[0]
+    rc = lib.sna_paged_decode_gqa(null, null, null, null, null, null, 8, 8, null, null, null, null, null, 0, 0.1, null,
+                                  2, 4, 2, 128, 16, 10, 1, ctypes.byref(bad), null, 0, null)
+    assert rc == _lib.SNA_ERR_INVALID_ARGUMENT and b"out of order" in lib.sna_last_error()
+    bad = _lib.SplitPlan.from_buffer_copy(p2)
+    bad.work[0] |= 1 << 31  # a row's first item flagged as its last
+    rc = lib.sna_paged_decode_gqa(null, null, null, null, null, null, 8, 8, null, null, null, null, null, 0, 0.1, null,
+                                  2, 4, 2, 128, 16, 10, 1, ctypes.byref(bad), null, 0, null)
+    assert rc == _lib.SNA_ERR_INVALID_ARGUMENT and b"mis-flagged" in lib.sna_last_error()
     rcm, pm = _plan(lib, _lib.KIND_MLA, [100, 200])
     assert rcm == 0 and pm.n_ctas > 0
     for field, value in (("total_tiles", 3), ("cta_off", None), ("cta_row", None)):

@@ -141,3 +141,21 @@ def test_pools_accept_options_switched_off():
     NeuronMHATokenToKVPool(64, 16, torch.bfloat16, 2, 64, 1, "cpu", quant_method=None, enable_kv_cache_copy=False,
                            v_head_dim=64, swa_head_dim=None)
     NeuronMLATokenToKVPool(256, 64, torch.float8_e4m3fn, 512, 64, 1, "cpu", use_dsa=False, dcp_replicated=False)
+
+
+def test_plan_made_for_other_lengths_is_refused():
+    """A plan must hold every split the host lengths need (GQA) or be cut by exactly those lengths (MLA); a mismatch
+    with the device's lengths would drop keys (the host copy is what the check can see)."""
+    short = ops.plan_decode(0, 3, host_seq_lens=[100, 200, 300], ctas_per_item=8, num_cus=256)
+    ops.check_plan_lengths(short, 0, [100, 200, 300])
+    ops.check_plan_lengths(short, 0, [50, 1, 300])  # fewer splits than planned: the extra items run empty
+    with pytest.raises(ValueError, match="row 2"):
+        ops.check_plan_lengths(short, 0, [100, 200, 300 + 64 * short.split_tiles])
+    bound = ops.plan_decode(0, 3, max_seq_len=1000, ctas_per_item=8, num_cus=256)
+    ops.check_plan_lengths(bound, 0, [1000, 17, 640])
+    with pytest.raises(ValueError, match="splits"):
+        ops.check_plan_lengths(bound, 0, [1000, 1000, 64000])
+    mla = ops.plan_decode(1, 2, host_seq_lens=[100, 200], ctas_per_item=1, num_cus=256)
+    ops.check_plan_lengths(mla, 1, [100, 200])
+    with pytest.raises(ValueError, match="row 1"):
+        ops.check_plan_lengths(mla, 1, [100, 201])

@@ -55,7 +55,7 @@ class _ExtendState:
     meta: NeuronForwardMetadata
     table: Tensor  # [bs, max_blocks] int32, device
     slots: Tensor  # [T] int64, device
-    q_start: Tensor  # [bs + 1] int32, device
+    q_start: Tensor  # [bs + 1] int32, device (a cumsum of the host's extend lengths: 0 first, T last, steps <= max_q_len)
     prior: Tensor  # [bs] int32, device (extend_prefix_lens)
     max_q_len: int
 

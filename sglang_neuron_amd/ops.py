@@ -535,12 +535,14 @@ def lse_combine(o_parts: Tensor, lse_parts: Tensor) -> tuple[Tensor, Tensor]:
 def prefill_attention(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: Tensor, q_start: Tensor,
                       prior_lens: Tensor, *, max_q_len: int, sm_scale: float, k_scale: Optional[Tensor] = None,
                       v_scale: Optional[Tensor] = None, sinks: Optional[Tensor] = None, window: int = 0,
-                      out: Optional[Tensor] = None) -> Tensor:
+                      out: Optional[Tensor] = None, host_q_start=None) -> Tensor:
     """Prefill attention of a batch of chunks: q [T, H, d] bf16 (request r's rows q_start[r] .. q_start[r + 1], at
     positions prior_lens[r] + i), every key read from one layer's caches [blocks, G, page, d] (FP8 with per-KV-head
     scales k_scale / v_scale [G], or bf16) through ``block_table`` [R, width] (store the chunk's K/V first, with
     kv_store_mha). Causal, optionally windowed (keys
     (p - window, p]) and with sinks [H]. ``max_q_len`` bounds the chunk lengths (a host int). Returns [T, H, d] bf16.
+    ``host_q_start``: a host copy of q_start; with it the offsets are checked (0 first, non-decreasing, T last, no
+    chunk longer than max_q_len: a row past the bound would be left unwritten) before the launch.
 
     Stands in for segmented_attention (ops/attention/attention_segmented_cte.py:21-75) over a batch."""
     dev = _on_gpu(q, k_cache, v_cache, block_table, q_start, prior_lens, k_scale, v_scale, sinks, out)
@@ -553,9 +555,16 @@ def prefill_attention(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: 
     _need(block_table.dim() == 2 and block_table.shape[0] >= R and block_table.stride(1) == 1,
           "block_table must be [R, width] with unit column stride")
     q = _contig(q, "q", torch.bfloat16)
-    qs = _contig(q_start, "q_start", torch.int32)
-    pl = _contig(prior_lens, "prior_lens", torch.int32)
-    table = _contig(block_table, "block_table", torch.int32) if block_table.dtype != torch.int32 else block_table
+    qs = q_start.to(torch.int32).contiguous()
+    pl = prior_lens.to(torch.int32).contiguous()
+    table = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32).contiguous()
+    if host_q_start is not None:
+        hq = [int(x) for x in torch.as_tensor(host_q_start).reshape(-1).tolist()]
+        _need(len(hq) == R + 1 and hq[0] == 0 and hq[-1] == T, f"q_start must run from 0 to T = {T} over {R + 1} "
+              f"entries, got {hq[:4]}{'...' if len(hq) > 4 else ''} ending {hq[-1] if hq else None}")
+        lens = [hq[r + 1] - hq[r] for r in range(R)]
+        _need(min(lens, default=0) >= 0, "q_start must not decrease")
+        _need(max(lens, default=0) <= int(max_q_len), f"a chunk of {max(lens)} queries exceeds max_q_len {max_q_len}")
     code = cache_dtype_code(k_cache.dtype)
     ks = vs = None
     if code == _lib.DTYPE_FP8_E4M3FN:
@@ -594,10 +603,10 @@ def segmented_attention(q: Tensor, *, k_cache: Tensor, v_cache: Tensor, block_ta
     dev = q.device
     prior = int(torch.as_tensor(prior_tokens).reshape(-1)[0])
     out = prefill_attention(
-        q.transpose(0, 1).contiguous(), k_cache, v_cache, block_tables[:1].to(dev), torch.tensor([0, S], dtype=torch.int32,
-                                                                                                  device=dev),
-        torch.tensor([prior], dtype=torch.int32, device=dev), max_q_len=S, sm_scale=scale, k_scale=k_scale,
-        v_scale=v_scale, sinks=None if sink is None else sink.reshape(-1), window=int(sliding_window or 0))
+        q.transpose(0, 1).contiguous(), k_cache, v_cache, block_tables[:1].to(dev),
+        torch.tensor([0, S], dtype=torch.int32, device=dev), torch.tensor([prior], dtype=torch.int32, device=dev),
+        max_q_len=S, sm_scale=scale, k_scale=k_scale, v_scale=v_scale, sinks=None if sink is None else sink.reshape(-1),
+        window=int(sliding_window or 0), host_q_start=[0, S])
     return out.transpose(0, 1).contiguous()
 
 

@@ -111,3 +111,22 @@ def test_prefill_rejects_bad_pages_and_missing_scales():
     kc8 = torch.zeros(3, 2, 8, 64, dtype=torch.float8_e4m3fn, device=DEV)
     with pytest.raises(ValueError):
         ops.prefill_attention(q, kc8, kc8, *args[3:], max_q_len=4, sm_scale=1.0, k_scale=one, v_scale=one)
+
+
+def test_prefill_takes_int64_tables_and_checks_host_offsets():
+    """An int64 block table, q_start and prior_lens are converted (as the decode wrappers do); with a host copy of
+    q_start, offsets that do not run from 0 to T or a chunk past max_q_len are refused before the launch."""
+    announce("prefill int64 operands and host offsets")
+    q, kc, vc, ks, vs, table, q_start, priors = _case(12, H=8, G=2, d=64, P=16, priors=(30, 5), lens=(40, 25))
+    args = dict(max_q_len=40, sm_scale=0.125, k_scale=ks.to(DEV), v_scale=vs.to(DEV))
+    out = ops.prefill_attention(q.to(DEV), kc, vc, table.to(torch.int64).to(DEV), q_start.to(torch.int64).to(DEV),
+                                priors.to(torch.int64).to(DEV), host_q_start=q_start, **args)
+    torch.cuda.synchronize()
+    want = oatt.segmented_prefill(q, kc.cpu().view(torch.uint8), vc.cpu().view(torch.uint8), table, q_start, priors,
+                                  sm_scale=0.125, k_scale=ks, v_scale=vs)
+    assert_close_attn(out.cpu(), want, "int64 operands")
+    dev_args = (q.to(DEV), kc, vc, table.to(DEV), q_start.to(DEV), priors.to(DEV))
+    with pytest.raises(ValueError, match="max_q_len"):
+        ops.prefill_attention(*dev_args, host_q_start=q_start, **{**args, "max_q_len": 39})
+    with pytest.raises(ValueError, match="from 0 to T"):
+        ops.prefill_attention(*dev_args, host_q_start=q_start - 1, **args)

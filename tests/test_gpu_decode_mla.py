@@ -69,6 +69,9 @@ DSA_CASES = [
     ("cfg5-page128", {"B": 4, "P": 128, "pool_positions": 8192, "n_indices": 2048, "recent": 128,
                       "short_rows": (600,)}),
     ("cfg5-full", {}),                                                   # the bench workload: 131072 positions per row
+    # a block table past the prologue's LDS copy (20000 one-slot pages): indices resolve entry by entry
+    ("page-1-wide-table", {"B": 2, "P": 1, "pool_positions": 20000, "n_indices": 256, "recent": 16,
+                           "short_rows": ()}),
 ]
 
 

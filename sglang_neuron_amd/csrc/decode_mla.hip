@@ -459,19 +459,21 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
         const int32_t k = tid + i * NT, key = kbase + k;
         pos[i] = (k < nkeys && key < khi) ? a.indices[(int64_t)b * a.n_indices + key] : -1;
       }
+      // thread e's row's new slot (B <= SNA_MAX_PLAN_ROWS = NT), loaded beside the indices: the barriers below wait
+      // for every load in flight, so a load issued after one costs a round trip of its own
+      static_assert(SNA_MAX_PLAN_ROWS <= NT, "one new slot per thread");
+      const int64_t my_slot = (a.new_slots && tid < a.B) ? a.new_slots[tid] : -1;
       // the new-slot table lives in the ring (unused until the tile loop)
       int32_t* hkey = reinterpret_cast<int32_t*>(&sm_ring[0][0][0]);
       int32_t* hval = hkey + kSlotHash;
       if (a.new_slots) {
         for (int e = tid; e < kSlotHash; e += NT) hkey[e] = hval[e] = -1;
         __syncthreads();
-        for (int32_t e = tid; e < a.B; e += NT) {
-          const int64_t s0 = a.new_slots[e];
-          if (s0 < 0 || s0 >= n_rows) continue;
-          for (uint32_t h = slot_hash((int32_t)s0);; h = (h + 1) & (kSlotHash - 1)) {
-            const int32_t prev = atomicCAS(&hkey[h], -1, (int32_t)s0);
-            if (prev == -1 || prev == (int32_t)s0) {
-              atomicMax(&hval[h], e);
+        if (my_slot >= 0 && my_slot < n_rows) {
+          for (uint32_t h = slot_hash((int32_t)my_slot);; h = (h + 1) & (kSlotHash - 1)) {
+            const int32_t prev = atomicCAS(&hkey[h], -1, (int32_t)my_slot);
+            if (prev == -1 || prev == (int32_t)my_slot) {
+              atomicMax(&hval[h], tid);
               break;
             }
           }

@@ -72,8 +72,7 @@ struct MlaArgs {
   uint16_t* out;
   float* lse_out;
   uint32_t cta_start[SNA_MAX_CTAS + 1];  // the stream split (sna_split_plan)
-  uint16_t cta_row[SNA_MAX_CTAS];
-  uint16_t cta_off[SNA_MAX_CTAS];
+  uint32_t cta_row_off[SNA_MAX_CTAS];    // row << 16 | tile offset in it (32-bit words take scalar loads)
   int32_t row_keys[SNA_MAX_PLAN_ROWS];   // keys per row: paged seq_len - 1, sparse n_indices
 };
 
@@ -356,8 +355,8 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
 
   // ---- the workgroup's range of the stream, one segment (a piece of one row) at a time ----
   const uint32_t g_lo = a.cta_start[w], g_hi = a.cta_start[w + 1];
-  int32_t b = a.cta_row[w];
-  uint32_t row_t0 = g_lo - a.cta_off[w];  // the global index of row b's first tile
+  int32_t b = (int32_t)(a.cta_row_off[w] >> 16);
+  uint32_t row_t0 = g_lo - (a.cta_row_off[w] & 0xffffu);  // the global index of row b's first tile
   for (uint32_t g = g_lo; g < g_hi; ++b) {
     const int32_t khi = a.row_keys[b];  // the row's keys: positions [0, khi) (paged) or index entries (sparse)
     const uint32_t row_t1 = row_t0 + (uint32_t)max((khi + 15) >> 4, 1);
@@ -387,27 +386,30 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     // LDS, sm_q[s][lane]: steps 0, 1 are rope chunk 4 s + g4 (dims 8 (4 s + g4) .. + 7); step pair k > 0 is latent
     // chunk m = 4 (k - 1) + g4, whose byte 2 i + bb holds dim 256 a + 128 bb + p0 + i (pairs interleaved here; the
     // workgroup's threads share the loads, which sit on a sparse row's critical path).
-    for (int e = tid; SPARSE && e < 18 * 64; e += NT) {
-      const int s = e >> 6, ln = e & 63, eg4 = ln >> 4;
-      const int32_t h = min(16 * hg + (ln & 15), a.H - 1);  // absent heads read a real head; their results are dropped
-      const uint16_t* qlp = a.ql + ((int64_t)b * a.H + h) * kLatent;
-      const uint16_t* qpp = a.qpe + ((int64_t)b * a.H + h) * kRope;
-      uint4 wq;
-      if (s < 2) {
-        wq = ld16(qpp + 8 * (4 * s + eg4));
-      } else {
-        const int m = 4 * ((s >> 1) - 1) + eg4;
-        const int a0 = (16 * m) >> 8, p0 = ((16 * m) & 255) >> 1;
-        const uint4 x = ld16(qlp + 256 * a0 + p0), y = ld16(qlp + 256 * a0 + 128 + p0);
-        if (s & 1) {
-          interleave_pairs(x.z, y.z, wq.x, wq.y);
-          interleave_pairs(x.w, y.w, wq.z, wq.w);
-        } else {
-          interleave_pairs(x.x, y.x, wq.x, wq.y);
-          interleave_pairs(x.y, y.y, wq.z, wq.w);
+    // (The loads are issued here, with the other prologue loads; the LDS stores follow the index loads below, so
+    // the query, the own row, the indices and the new slots share one round trip.)
+    constexpr int QIT = SPARSE ? (18 * 64 + NT - 1) / NT : 1;
+    uint4 qx[QIT], qy[QIT];
+    if constexpr (SPARSE) {
+#pragma unroll
+      for (int it = 0; it < QIT; ++it) {
+        const int e = tid + it * NT;
+        const int s = e >> 6, ln = e & 63, eg4 = ln >> 4;
+        const int32_t h = min(16 * hg + (ln & 15), a.H - 1);  // absent heads read a real head; their results are dropped
+        const uint16_t* qlp = a.ql + ((int64_t)b * a.H + h) * kLatent;
+        const uint16_t* qpp = a.qpe + ((int64_t)b * a.H + h) * kRope;
+        qx[it] = qy[it] = make_uint4(0, 0, 0, 0);
+        if (e < 18 * 64) {
+          if (s < 2) {
+            qx[it] = ld16(qpp + 8 * (4 * s + eg4));
+          } else {
+            const int m = 4 * ((s >> 1) - 1) + eg4;
+            const int a0 = (16 * m) >> 8, p0 = ((16 * m) & 255) >> 1;
+            qx[it] = ld16(qlp + 256 * a0 + p0);
+            qy[it] = ld16(qlp + 256 * a0 + 128 + p0);
+          }
         }
       }
-      sm_q[s][ln] = wq;
     }
     uint4 qreg[SPARSE ? 1 : 18];
     if constexpr (!SPARSE) {
@@ -436,7 +438,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     if (own_wave) {
       const uint16_t* src = a.own + (int64_t)b * 576;
       own0 = ld16(src + 8 * lane);
-      if (lane < 8) own1 = ld16(src + 8 * (lane + 64));
+      own1 = ld16(src + 8 * (min(lane, 7) + 64));  // lanes 8 .. 63 repeat lane 7's load (their own1 is unused)
       if (hg == 0 && a.new_slots) {
         // paged: an out-of-range slot goes to the reserved row 0, as kv_store_mla does; sparse: it is skipped, as
         // kv_store_dsa does
@@ -463,6 +465,25 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
       // for every load in flight, so a load issued after one costs a round trip of its own
       static_assert(SNA_MAX_PLAN_ROWS <= NT, "one new slot per thread");
       const int64_t my_slot = (a.new_slots && tid < a.B) ? a.new_slots[tid] : -1;
+      // the query operand's LDS stores (its loads were issued with the prologue's first loads)
+#pragma unroll
+      for (int it = 0; it < QIT; ++it) {
+        const int e = tid + it * NT;
+        if (e >= 18 * 64) continue;
+        const int s = e >> 6, ln = e & 63;
+        const uint4 x = qx[it], y = qy[it];
+        uint4 wq = x;
+        if (s >= 2) {
+          if (s & 1) {
+            interleave_pairs(x.z, y.z, wq.x, wq.y);
+            interleave_pairs(x.w, y.w, wq.z, wq.w);
+          } else {
+            interleave_pairs(x.x, y.x, wq.x, wq.y);
+            interleave_pairs(x.y, y.y, wq.z, wq.w);
+          }
+        }
+        sm_q[s][ln] = wq;
+      }
       // the new-slot table lives in the ring (unused until the tile loop)
       int32_t* hkey = reinterpret_cast<int32_t*>(&sm_ring[0][0][0]);
       int32_t* hval = hkey + kSlotHash;
@@ -1187,8 +1208,7 @@ static void fill_stream_args(MlaArgs& a, const sna_split_plan* plan, float* ws) 
   a.ws_ml = a.ws_o + 2ll * plan->n_ctas * a.H * kLatent;
   for (int32_t w = 0; w <= plan->n_ctas; ++w) a.cta_start[w] = plan->cta_start[w];
   for (int32_t w = 0; w < plan->n_ctas; ++w) {
-    a.cta_row[w] = plan->cta_row[w];
-    a.cta_off[w] = plan->cta_off[w];
+    a.cta_row_off[w] = (uint32_t)plan->cta_row[w] << 16 | plan->cta_off[w];
   }
   for (int32_t b = 0; b < plan->batch; ++b) a.row_keys[b] = plan->row_keys[b];
 }

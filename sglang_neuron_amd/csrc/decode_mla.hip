@@ -18,10 +18,10 @@
 //
 // A segment that is a whole row writes the row's output. A row split over S workgroups is merged in the same launch:
 // each of its workgroups writes its partial (unnormalized context, max and sum per head) through to memory and counts
-// itself in the row's arrival counter. The row's eight 64-dim latent blocks are shared out by arrival order: a
-// workgroup that sees the row complete (the last to arrive, or one still polling the counter when it completes) merges
-// its blocks over the S partials in one pass and marks them in the row's done mask, and the last to arrive merges any
-// block not marked within a bounded wait. The last workgroup of the launch to finish returns every counter to zero.
+// itself in the row's arrival word. The row's eight 64-dim latent blocks are shared out by arrival order: a workgroup
+// that sees the row complete (the last to arrive, or one still polling the word when it completes) merges its blocks
+// over the S partials in one pass; an owner whose bounded polls run out retracts its blocks in the same word, and the
+// last to arrive merges those. The last workgroup of the launch to finish returns every word to zero.
 //
 // Lane roles (lane = 16 * g4 + li), 16-key tiles; slot i of a tile (a row of S^T, a K index of PV) holds key
 // key_of(i): the even keys in slots 0 .. 7, the odd ones in 8 .. 15.
@@ -68,7 +68,7 @@ struct MlaArgs {
   int32_t wait_polls;  // polls of a row's arrival counter by a workgroup that published a partial
   float* ws_o;         // [2 n_ctas, H, 512] partial contexts (unnormalized, natural latent-dim order)
   float* ws_ml;        // [2 n_ctas, H, 2] their (max, sum), log2 domain
-  int32_t* ws_cnt;     // arrivals [kStreamMaxCounters], done masks [kStreamMaxCounters], finished workgroups [1]
+  int32_t* ws_cnt;     // arrival words [kStreamMaxCounters], (unused) [kStreamMaxCounters], finished workgroups [1]
   uint16_t* out;
   float* lse_out;
   uint32_t cta_start[SNA_MAX_CTAS + 1];  // the stream split (sna_split_plan)
@@ -218,51 +218,75 @@ __device__ __forceinline__ int32_t ctas_starting_by(const MlaArgs& a, uint32_t x
 
 // Merge of up to NC latent blocks (chunks[i]: dims 64 c .. 64 c + 63; -1 = none) of row b, head group hg, over its S
 // partials: those of workgroups w0 .. w0 + S - 1 (workgroup w0's is its second slot when its range starts before the
-// row). Thread (j, q) = (tid / 16, tid % 16) takes head 16 hg + j, dims 64 c + 4 q .. + 3 of each block; lane q of a
-// head's 16 lanes loads partial base + q's (max, sum). The partials stream in groups of NK, every load of a group in
-// flight together (NC * NK <= 64 float4 per thread), with an online rescale between groups.
+// row). Thread (j, q) = (tid / 16, tid % 16) takes head 16 hg + j, dims 64 c + 4 q .. + 3 of each block. First the
+// row's max M and sum L: lane q of a head's 16 lanes loads the (max, sum) of partials q, q + 16, ... (four rounds of
+// loads in flight at once, the first NK partials' contexts with them) and keeps them in `lds` ([16][256] float2, its
+// own entries), where each max is then replaced by the partial's weight 2^(m_k - M). Then the contexts are added in
+// partial order with those final weights, NK partials' loads in flight at a time. No running rescale: the sums are
+// the same bits whatever NC and NK, so a block's result does not depend on which workgroup merges it.
 template <bool SPARSE, int NC, int NK>
 __device__ void merge_chunks(const MlaArgs& a, __amdgpu_buffer_rsrc_t ro, __amdgpu_buffer_rsrc_t rml, int32_t b, int hg,
-                             int32_t w0, bool w0_second, int32_t S, const int (&chunks)[NC]) {
-  static_assert(NC * NK <= 64 && NK <= 16, "a group's loads stay in registers");
+                             int32_t w0, bool w0_second, int32_t S, const int (&chunks)[NC], float2* lds) {
+  static_assert(NC * NK <= 64, "a group's loads stay in registers");
+  static_assert(SNA_MAX_CTAS <= 16 * 16, "16 rounds of 16 partials cover a row");
   const int tid = threadIdx.x, j = tid >> 4, q = tid & 15;
   const int32_t h = min(16 * hg + j, a.H - 1);  // absent heads merge a real head's data; their results are dropped
   auto slot_of = [&](int32_t k) -> int32_t { return 2 * (w0 + k) + ((k == 0 && w0_second) ? 1 : 0); };
-  float M = kNegBig, L = 0.0f;
-  float4 o[NC];
-#pragma unroll
-  for (int i = 0; i < NC; ++i) o[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int32_t base = 0; base < S; base += NK) {
-    const int32_t n = min(S - base, NK);
-    float4 x[NC][NK];
+  auto ml_of = [&](int32_t k) -> float2 {
+    return k < S ? load_dev8(rml, (uint32_t)(((int64_t)slot_of(k) * a.H + h) * 8)) : make_float2(kNegBig, 0.0f);
+  };
+  float4 x[NC][NK];
+  auto load_group = [&](int32_t base) {
 #pragma unroll
     for (int k = 0; k < NK; ++k) {
-      if (k >= n) continue;
+      if (base + k >= S) continue;
       const int64_t prow = ((int64_t)slot_of(base + k) * a.H + h) * kLatent + 4 * q;
 #pragma unroll
       for (int i = 0; i < NC; ++i)
         if (chunks[i] >= 0) x[i][k] = load_dev16(ro, (uint32_t)((prow + 64 * chunks[i]) * 4));
     }
-    float2 ml = make_float2(kNegBig, 0.0f);
-    if (q < n) ml = load_dev8(rml, (uint32_t)(((int64_t)slot_of(base + q) * a.H + h) * 8));
-    const float Mn = fmaxf(M, row16_max(ml.x));
-    const float r = __builtin_amdgcn_exp2f(M - Mn);
-    const float e = __builtin_amdgcn_exp2f(ml.x - Mn);
-    L = L * r + row16_sum(e * ml.y);
-    M = Mn;
+  };
+  load_group(0);
+  const int32_t R = (S + 15) >> 4;
+  float m = kNegBig;
+  for (int32_t r0 = 0; r0 < R; r0 += 4) {
+    float2 ml[4];
 #pragma unroll
-    for (int i = 0; i < NC; ++i) o[i].x *= r, o[i].y *= r, o[i].z *= r, o[i].w *= r;
+    for (int i = 0; i < 4; ++i) ml[i] = ml_of(16 * (r0 + i) + q);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (r0 + i >= R) break;
+      lds[(r0 + i) * 256 + tid] = ml[i];
+      m = fmaxf(m, ml[i].x);
+    }
+  }
+  const float M = row16_max(m);
+  float l = 0.0f;
+  for (int32_t r = 0; r < R; ++r) {
+    const float2 ml = lds[r * 256 + tid];
+    const float e = __builtin_amdgcn_exp2f(ml.x - M);
+    l += e * ml.y;
+    lds[r * 256 + tid].x = e;
+  }
+  const float L = row16_sum(l);
+  __syncthreads();  // every lane's weights are in LDS
+  float4 o[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) o[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int32_t base = 0; base < S; base += NK) {
+    if (base > 0) load_group(base);
 #pragma unroll
     for (int k = 0; k < NK; ++k) {
-      if (k >= n) continue;
-      const float ek = __shfl(e, k, 16);
+      const int32_t kk = base + k;
+      if (kk >= S) continue;
+      const float ek = lds[(kk >> 4) * 256 + 16 * j + (kk & 15)].x;
 #pragma unroll
       for (int i = 0; i < NC; ++i)
         if (chunks[i] >= 0) o[i].x += ek * x[i][k].x, o[i].y += ek * x[i][k].y, o[i].z += ek * x[i][k].z,
                             o[i].w += ek * x[i][k].w;
     }
   }
-  if (16 * hg + j >= a.H) return;
+  if (16 * hg + j >= a.H) return;  // (the caller's next barrier ends the weights' use of the LDS)
   const float inv = 1.0f / L;
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
@@ -274,21 +298,20 @@ __device__ void merge_chunks(const MlaArgs& a, __amdgpu_buffer_rsrc_t ro, __amdg
   }
 }
 
-// The blocks of `mask` (bit c: latent block c) merged over the row's S partials, 8 partials at a time (up to 64 loads
-// in flight per thread). The grouping is the same however many blocks go together, so a block's bits do not depend on
-// which workgroup merges it (a block merged twice gets the same bits twice).
+// The blocks of `mask` (bit c: latent block c) merged over the row's S partials: one block with 16 partials' loads in
+// flight, several with 8. lds: 32 KB of LDS for the merge's weights.
 template <bool SPARSE>
 __device__ void merge_mask(const MlaArgs& a, __amdgpu_buffer_rsrc_t ro, __amdgpu_buffer_rsrc_t rml, int32_t b, int hg,
-                           int32_t w0, bool w0_second, int32_t S, uint32_t mask) {
+                           int32_t w0, bool w0_second, int32_t S, uint32_t mask, float2* lds) {
   if (__popc(mask) == 1) {
     const int chunks[1] = {__builtin_ctz(mask)};
-    merge_chunks<SPARSE, 1, 8>(a, ro, rml, b, hg, w0, w0_second, S, chunks);
+    merge_chunks<SPARSE, 1, 16>(a, ro, rml, b, hg, w0, w0_second, S, chunks, lds);
     return;
   }
   int chunks[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) chunks[i] = (mask >> i) & 1u ? i : -1;
-  merge_chunks<SPARSE, 8, 8>(a, ro, rml, b, hg, w0, w0_second, S, chunks);
+  merge_chunks<SPARSE, 8, 8>(a, ro, rml, b, hg, w0, w0_second, S, chunks, lds);
 }
 
 // WIDE: a sparse pool past 4 GiB, whose rows take 64-bit addresses (every other pool is read through 32-bit buffer
@@ -1093,10 +1116,11 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     }
 
     // ---- a row split over workgroups: publish, count, and merge when the row is complete ----
-    // The workgroup that arrives k-th owns latent blocks c = k, k + n, ... (n = min(S, 8)); one that sees the row
-    // complete (the last to arrive at once, the others by polling a bounded number of times) merges its blocks and
-    // marks them done. The last to arrive then waits, again a bounded number of polls, for the other blocks to be
-    // marked and merges any that are not: a block may be merged twice, into the same bits, never zero times.
+    // The row's arrival word counts arrivals (bits 0 .. 15) and holds retracted blocks (bits 16 .. 23). The workgroup
+    // that arrives k-th owns latent blocks c = k, k + n, ... (n = min(S, 8)). An owner polls, a bounded number of
+    // times, until the count reaches S and merges its blocks; one whose polls run out retracts them (an atomic or of
+    // their bits) unless the or finds every arrival counted, in which case it merges them itself. The last to arrive
+    // merges its own blocks and those its add found retracted, and waits for nothing: each block is merged exactly once.
     if (!whole) {
       const int32_t wa = ctas_starting_by(a, row_t0) - 1;      // the row's first workgroup
       const int32_t wb = ctas_starting_by(a, row_t1 - 1) - 1;  // its last
@@ -1104,44 +1128,39 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
       const bool wa_second = a.cta_start[wa] != row_t0;        // the row is not wa's first segment
       const int32_t pair = b * a.groups + hg;
       int32_t* arrive = a.ws_cnt + kCounterStride * pair;
-      int32_t* done = a.ws_cnt + kCounterStride * (kStreamMaxCounters + pair);
       wait_vmcnt<0>();  // this wave's partial stores are complete (written through) before the count
       __syncthreads();
       if (tid == 0) {
-        const int32_t k = __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        int32_t seen = k + 1;
-        for (int32_t p = 0; seen < S && p < a.wait_polls; ++p) {
-          __builtin_amdgcn_s_sleep(1);
-          seen = __hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        sm_word = seen >= S ? k : -1;
-      }
-      __syncthreads();
-      const int32_t k = sm_word;
-      if (k >= 0) {
         const int32_t nown = min(S, 8);
+        const int32_t old = __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int32_t k = old & 0xffff;
         uint32_t mine = 0;
         for (int32_t c = k; k < nown && c < 8; c += nown) mine |= 1u << c;
-        if (mine) {
-          merge_mask<SPARSE>(a, ws_o_rsrc, ws_ml_rsrc, b, hg, wa, wa_second, S, mine);
-          __syncthreads();
-          if (tid == 0) __hip_atomic_fetch_or(done, (int32_t)mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        uint32_t todo = 0;
         if (k == S - 1) {
-          __syncthreads();
-          if (tid == 0) {
-            int32_t d = __hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            for (int32_t p = 0; (d & 0xff) != 0xff && p < a.wait_polls; ++p) {
-              __builtin_amdgcn_s_sleep(1);
-              d = __hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            sm_word = d;
+          todo = mine | (((uint32_t)old >> 16) & 0xffu);
+        } else if (mine) {
+          int32_t seen = k + 1;
+          for (int32_t p = 0; seen < S && p < a.wait_polls; ++p) {
+            __builtin_amdgcn_s_sleep(1);
+            seen = __hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 0xffff;
           }
-          __syncthreads();
-          const uint32_t missing = ~(uint32_t)sm_word & 0xffu;
-          if (missing) merge_mask<SPARSE>(a, ws_o_rsrc, ws_ml_rsrc, b, hg, wa, wa_second, S, missing);
+          if (seen >= S) {
+            todo = mine;
+          } else {
+            const int32_t now = __hip_atomic_fetch_or(arrive, (int32_t)(mine << 16), __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+            if ((now & 0xffff) >= S) todo = mine;  // the last arrived before the or: it left these blocks here
+          }
         }
+        sm_word = (int32_t)todo;
       }
+      __syncthreads();
+      const uint32_t todo = (uint32_t)sm_word;
+      static_assert(sizeof(sm_ring) >= 16 * 256 * sizeof(float2), "the merge's weights fit the ring");
+      if (todo)
+        merge_mask<SPARSE>(a, ws_o_rsrc, ws_ml_rsrc, b, hg, wa, wa_second, S, todo,
+                           reinterpret_cast<float2*>(&sm_ring[0][0][0]));
       __syncthreads();
     }
     g = s_hi;
@@ -1160,11 +1179,8 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
   }
   __syncthreads();
   if (sm_word) {
-    for (int32_t i = tid; i < a.B * a.groups; i += NT) {
+    for (int32_t i = tid; i < a.B * a.groups; i += NT)
       __hip_atomic_store(a.ws_cnt + kCounterStride * i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(a.ws_cnt + kCounterStride * (kStreamMaxCounters + i), 0, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    }
     if (tid == 0)
       __hip_atomic_store(a.ws_cnt + kCounterStride * 2 * kStreamMaxCounters, 0, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);

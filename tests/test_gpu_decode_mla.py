@@ -4,7 +4,7 @@ oracle on seeded cases, with the pools compared bit-exact after the step."""
 import pytest
 import torch
 
-from sglang_neuron_amd import workloads
+from sglang_neuron_amd import ops, workloads
 from tests.conftest import announce
 from tests._harness import (assert_close_attn, dsa_gpu_pool, dsa_gpu_step, dsa_oracle, mla_gpu_decode, mla_gpu_pool,
                             mla_oracle)
@@ -139,3 +139,45 @@ def test_dsa_invalid_indices_are_dropped():
     ctx, lse = dsa_gpu_step(case, cache)
     assert_close_attn(ctx, want_ctx, "invalid indices")
     assert torch.allclose(lse.cpu(), want_lse, atol=2e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize("polls", [0, 1])
+def test_split_merge_when_polls_run_out(polls):
+    """A split row's owners poll a bounded number of times for the row's last partial; with the bound at 0 or 1 they
+    mostly give up and retract their latent blocks, and the last workgroup to arrive merges them. Every block is still
+    merged once, to the same bits as with the planner's bound (the merge's sums do not depend on which workgroup
+    runs them), on two calls in a row. (The bound is forced from the host: every wait still ends.)"""
+    dev = torch.device("cuda", 0)
+    case = workloads.mla_case(overrides={"B": 4, "lens": (1024, 4096)})
+    want, _, _ = mla_oracle(case)
+    cache, scale = mla_gpu_pool(case)
+    args = (case.ql_nope.to(dev), case.q_pe.to(dev), cache, scale, case.block_table.to(dev), case.seq_lens.to(dev),
+            case.compact_new.to(dev))
+    kw = dict(sm_scale=case.sm_scale, page_size=case.P, new_slots=case.new_slots.to(dev), host_seq_lens=case.seq_lens)
+    plan = ops.plan_decode(1, case.B, host_seq_lens=case.seq_lens, ctas_per_item=1, num_cus=ops._num_cus(dev))
+    announce(f"mla merge with {polls} polls: B={case.B} n_ctas={plan.n_ctas} max_splits={plan.max_splits}")
+    assert plan.max_splits > 1
+    base = ops.mla_decode(*args, **kw, plan=plan)
+    plan.wait_polls = polls
+    for _ in range(2):
+        out = ops.mla_decode(*args, **kw, plan=plan)
+        torch.cuda.synchronize()
+        assert torch.equal(out, base), "MLA output differs from the default plan's"
+    assert_close_attn(out, want, f"mla polls={polls}")
+
+    dcase = workloads.dsa_case(overrides=DSA_CASES[0][1])
+    dplan = ops.plan_decode(2, dcase.B, n_keys_per_row=dcase.indices.shape[1], ctas_per_item=1,
+                            num_cus=ops._num_cus(dev))
+    assert dplan.max_splits > 1
+    want_ctx, want_lse, _ = dsa_oracle(dcase)
+    cache = dsa_gpu_pool(dcase)
+    dargs = (dcase.q_absorbed.to(dev), dcase.q_pe.to(dev), cache, dcase.kv_scale, dcase.indices.to(dev),
+             dcase.block_table.to(dev), dcase.positions.to(dev), dcase.own_rows.to(dev))
+    dkw = dict(sm_scale=dcase.sm_scale, page_size=dcase.P, new_slots=dcase.new_slots.to(dev))
+    base_ctx, base_lse = ops.mla_decode_sparse(*dargs, **dkw, plan=dplan)
+    dplan.wait_polls = polls
+    for _ in range(2):
+        ctx, lse = ops.mla_decode_sparse(*dargs, **dkw, plan=dplan)
+        torch.cuda.synchronize()
+        assert torch.equal(ctx, base_ctx) and torch.equal(lse, base_lse), "DSA output differs from the default plan's"
+    assert_close_attn(ctx, want_ctx, f"dsa polls={polls}")

@@ -1121,6 +1121,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     // times, until the count reaches S and merges its blocks; one whose polls run out retracts them (an atomic or of
     // their bits) unless the or finds every arrival counted, in which case it merges them itself. The last to arrive
     // merges its own blocks and those its add found retracted, and waits for nothing: each block is merged exactly once.
+    // (A workgroup whose range goes on into another row retracts at once.)
     if (!whole) {
       const int32_t wa = ctas_starting_by(a, row_t0) - 1;      // the row's first workgroup
       const int32_t wb = ctas_starting_by(a, row_t1 - 1) - 1;  // its last
@@ -1141,7 +1142,10 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
           todo = mine | (((uint32_t)old >> 16) & 0xffu);
         } else if (mine) {
           int32_t seen = k + 1;
-          for (int32_t p = 0; seen < S && p < a.wait_polls; ++p) {
+          // a workgroup with another segment after this one does not wait: the row's other pieces may be segments
+          // that other workgroups reach only after their own merges, so its waits would chain across the launch
+          const int32_t polls = s_hi < g_hi ? 0 : a.wait_polls;
+          for (int32_t p = 0; seen < S && p < polls; ++p) {
             __builtin_amdgcn_s_sleep(1);
             seen = __hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 0xffff;
           }

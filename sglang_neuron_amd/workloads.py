@@ -277,7 +277,8 @@ def dsa_case(*, gen_device="cpu", overrides: Optional[dict] = None) -> DsaCase:
     for i, L in enumerate(spec["short_rows"]):
         if i < B:
             lens[B - 1 - i] = min(L, per)
-    table, nb = _page_layout([per] * B, P, g_cpu)
+    # extra_pages: unused pages mixed into the permutation (a larger pool, e.g. one past 4 GiB)
+    table, nb = _page_layout([per] * B, P, g_cpu, spec.get("extra_pages", 0))
     idx = torch.full((B, K), -1, dtype=torch.int32)
     for b, L in enumerate(lens):
         prior = L - 1

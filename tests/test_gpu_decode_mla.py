@@ -181,3 +181,22 @@ def test_split_merge_when_polls_run_out(polls):
         torch.cuda.synchronize()
         assert torch.equal(ctx, base_ctx) and torch.equal(lse, base_lse), "DSA output differs from the default plan's"
     assert_close_attn(ctx, want_ctx, f"dsa polls={polls}")
+
+
+def test_dsa_pool_past_4gib():
+    """A DSA pool of more than 4 GiB (150,000 unused pages mixed into the permutation): its rows take 64-bit addresses
+    (the kernel's WIDE form) instead of 32-bit offsets against one buffer resource. Parity and the pool bit-exact,
+    as for the smaller pools."""
+    case = workloads.dsa_case(overrides={"B": 2, "pool_positions": 8192, "n_indices": 2048, "recent": 128,
+                                         "short_rows": (), "extra_pages": 150_000})
+    assert case.num_blocks * case.P * 640 > (1 << 32)
+    far = int((case.block_table.to(torch.int64) * case.P * 640 >= (1 << 32)).sum())
+    assert far > 0, "no page of the case lies past 4 GiB"
+    want_ctx, want_lse, cache_o = dsa_oracle(case)
+    announce(f"dsa pool past 4 GiB: {case.num_blocks * case.P * 640 / 2**30:.2f} GiB, {far} pages past 4 GiB")
+    cache = dsa_gpu_pool(case)
+    ctx, lse = dsa_gpu_step(case, cache)
+    torch.cuda.synchronize()
+    assert_close_attn(ctx, want_ctx, "pool past 4 GiB")
+    assert torch.allclose(lse.cpu(), want_lse, atol=2e-3, rtol=1e-4)
+    assert torch.equal(cache.cpu(), cache_o), "row pool differs"

@@ -200,3 +200,27 @@ def test_dsa_pool_past_4gib():
     assert_close_attn(ctx, want_ctx, "pool past 4 GiB")
     assert torch.allclose(lse.cpu(), want_lse, atol=2e-3, rtol=1e-4)
     assert torch.equal(cache.cpu(), cache_o), "row pool differs"
+
+
+@pytest.mark.parametrize("polls", [0, 1])
+def test_multi_segment_merge_with_bounded_polls(polls):
+    """Ranges that span rows (200 rows, 20 heads: two head groups of 128 workgroups): a workgroup whose range goes on
+    into another row publishes its partial without polling, and the merge of every split row still completes, to the
+    same bits with the poll bound forced to 0 or 1 as with the planner's, and within the oracle's tolerance."""
+    dev = torch.device("cuda", 0)
+    case = workloads.mla_case(overrides={"B": 200, "H": 20, "lens": (1, 200)})
+    want, _, _ = mla_oracle(case)
+    cache, scale = mla_gpu_pool(case)
+    args = (case.ql_nope.to(dev), case.q_pe.to(dev), cache, scale, case.block_table.to(dev), case.seq_lens.to(dev),
+            case.compact_new.to(dev))
+    kw = dict(sm_scale=case.sm_scale, page_size=case.P, new_slots=case.new_slots.to(dev), host_seq_lens=case.seq_lens)
+    plan = ops.plan_decode(1, case.B, host_seq_lens=case.seq_lens, ctas_per_item=2, num_cus=ops._num_cus(dev))
+    announce(f"mla multi-segment merge, {polls} polls: B={case.B} n_ctas={plan.n_ctas} max_splits={plan.max_splits}")
+    assert plan.n_ctas < case.B and plan.max_splits > 1
+    base = ops.mla_decode(*args, **kw, plan=plan)
+    plan.wait_polls = polls
+    for _ in range(2):
+        out = ops.mla_decode(*args, **kw, plan=plan)
+        torch.cuda.synchronize()
+        assert torch.equal(out, base), "output differs from the default plan's"
+    assert_close_attn(out, want, f"multi-segment polls={polls}")

@@ -167,8 +167,9 @@ typedef struct {
                            row's items, even where the device's length needs fewer splits. */
   int32_t n_ctas;       /* MLA / DSA: workgroups of the stream split (per 16-head group) */
   int32_t total_tiles;  /* MLA / DSA: tiles of all rows */
-  int32_t wait_polls;   /* MLA / DSA: how many times a workgroup that published a partial polls for its row's last
-                           partial before it leaves the merge to the others (0: the last to arrive merges alone) */
+  int32_t wait_polls;   /* MLA / DSA: how many times a workgroup that owns merge blocks of a split row polls for the
+                           row's last partial before it hands its blocks to the last to arrive (0: the last to
+                           arrive merges alone); a workgroup whose range continues into another row never polls */
   uint32_t cta_start[SNA_MAX_CTAS + 1];
   uint16_t cta_row[SNA_MAX_CTAS];
   uint16_t cta_off[SNA_MAX_CTAS];

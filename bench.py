@@ -81,6 +81,16 @@ def _traffic(workload: str):
     return b, f"committed rocprofv3 counter passes (profiles/traffic_{workload}.json), not this run"
 
 
+def _mfma_counters(workload: str):
+    """The step's MFMA busy share and bf16 MFMA flops from profiles/mfma_<workload>.json, the committed summary of a
+    rocprofv3 pass of the derived counters MfmaUtil and MfmaFlopsBF16; None when no such pass was committed."""
+    p = os.path.join(ROOT, "profiles", f"mfma_{workload}.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f)
+
+
 def time_us(fn, n_steps: int, warmup: int) -> float:
     """Microseconds per call of fn(i): warmup calls, then one HIP event pair (torch events, recorded on torch's current
     stream, the stream every launch here goes to) around n_steps back-to-back calls."""
@@ -760,6 +770,12 @@ def measure_decode(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: f
                            "not a hardware counter"},
         "cpu_baseline": None,
     }
+    mc = _mfma_counters(wl)
+    if mc:
+        out["mfma"]["counter_busy_pct"] = mc["mfma_busy_pct"]
+        out["mfma"]["counter_flops_per_step"] = mc["mfma_flops_per_step"]
+        out["mfma"]["counter_source"] = (f"committed rocprofv3 pass of MfmaUtil and MfmaFlopsBF16 "
+                                         f"(profiles/mfma_{wl}.json), not this run")
     if cpu:
         log(f"{wl}: CPU baseline (oracle on {cpu_threads()} host threads)")
         cb = cpu_fn(cpu_budget)

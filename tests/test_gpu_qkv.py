@@ -2,7 +2,6 @@
 byte matches; with it the fp32 sum of squares runs in another order, so a value may sit one bf16 step away (and a K
 byte one e4m3fn step away), rarely."""
 
-import math
 
 import pytest
 import torch

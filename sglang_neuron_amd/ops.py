@@ -311,7 +311,9 @@ def _host_lens(seq_lens: Tensor, host_seq_lens) -> Optional[Tensor]:
 class Prepared:
     """One or more C-ABI calls with validated, bound arguments, launched again on every call. It keeps its tensors
     (inputs, outputs, workspace) alive and returns its outputs. The bench runs its timed loop through these, so host
-    work stays out of the timing, and every public decode function below is prepare + one launch."""
+    work stays out of the timing, and every public decode function below is prepare + one launch. The launches go to
+    the stream that was current when it was prepared (bound like the pointers): prepare it on the stream it will run
+    on, e.g. inside a graph capture to capture it."""
 
     def __init__(self, calls, keep, outputs, what):
         self._calls = calls        # [(fn, args)]

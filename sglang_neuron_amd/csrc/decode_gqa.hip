@@ -160,6 +160,9 @@ void gqa_decode_kernel(GqaArgs a) {
 
   const float kscale = FP8 ? a.k_scale[g] : 1.0f;
   const float vscale = FP8 ? a.v_scale[g] : 1.0f;
+  // the group's sink logits (final outputs only), loaded with the prologue's loads: read after the tile loop, a load
+  // there would add a memory round trip to the end of every workgroup
+  const float sink_pre = (FINAL && a.sinks && tid < a.group) ? a.sinks[g * a.group + tid] : 0.0f;
   const float qk_scale = a.sm_scale * kscale * kLog2e;
   const int64_t head_stride = (int64_t)a.P * D * ESZ;  // bytes of one (page, head) block
   const int32_t* trow = a.table + (int64_t)b * a.table_stride;
@@ -398,6 +401,8 @@ void gqa_decode_kernel(GqaArgs a) {
 
   // ---- merge the waves (and the own token) in LDS; write the output or this split's partial ----
   __shared__ float sm_o[WAVES][16][D + 1];
+  __shared__ float sm_sink[16];
+  if (FINAL && tid < a.group) sm_sink[tid] = sink_pre;
   __shared__ float sm_m[WAVES][16];
   __shared__ float sm_l[WAVES][16];
   const float l_tot = sum_across_groups(l_run);
@@ -431,7 +436,7 @@ void gqa_decode_kernel(GqaArgs a) {
       l += e;
     }
     if constexpr (FINAL) {
-      if (a.sinks) l += __builtin_amdgcn_exp2f(a.sinks[h] * kLog2e - M);
+      if (a.sinks) l += __builtin_amdgcn_exp2f(sm_sink[j] * kLog2e - M);
       a.out[((int64_t)b * a.H + h) * D + d] = (uint16_t)f32_to_bf16_bits(o / l);
     } else {
       const int64_t row = ((int64_t)b * S + split) * a.H + h;

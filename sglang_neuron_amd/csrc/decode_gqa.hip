@@ -393,8 +393,7 @@ void gqa_decode_kernel(GqaArgs a) {
       float s = 0.0f;
 #pragma unroll
       for (int v = 0; v < D / 64; ++v) s += own_q[jj][v] * sm_kn[lane + 64 * v];
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+      s = wave_sum(s);
       if (lane == 0) sm_sn[j] = s * a.sm_scale * kLog2e;
     }
   }
@@ -543,8 +542,7 @@ __global__ __launch_bounds__(128) void gqa_lone_token_kernel(GqaArgs a) {
     const uint16_t* qp = a.q + ((int64_t)b * a.H + h) * D;
     float s = 0.0f;
     for (int d = lane; d < D; d += 64) s += bf16_bits_to_f32(qp[d]) * sm_kn[d];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    s = wave_sum(s);
     s *= a.sm_scale * kLog2e;
     float M = s, den = 1.0f;
     if (a.sinks) {

@@ -193,18 +193,6 @@ __device__ __forceinline__ float2 load_dev8(__amdgpu_buffer_rsrc_t r, uint32_t o
   return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
 }
 
-// Max and sum over the 16 lanes of a lane's 16-lane row (the lanes of one head in the merge).
-__device__ __forceinline__ float row16_max(float v) {
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 16));
-  return v;
-}
-__device__ __forceinline__ float row16_sum(float v) {
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, 16);
-  return v;
-}
-
 // The number of workgroups (of n) whose range starts at or before global tile x.
 __device__ __forceinline__ int32_t ctas_starting_by(const MlaArgs& a, uint32_t x) {
   const int lane = threadIdx.x & 63;

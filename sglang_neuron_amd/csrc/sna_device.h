@@ -285,22 +285,35 @@ __device__ __forceinline__ float max_across_groups(float v) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
 __device__ __forceinline__ float sum_across_groups(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(t[0]) + __uint_as_float(t[1]);
 }
+// Reductions over the 16 lanes of each 16-lane row, in VALU data-parallel moves (no LDS round trip): quad_perm
+// [1,0,3,2] and [2,3,0,1] pair lanes within quads, row_half_mirror pairs a half-row's two quads, row_mirror the
+// row's two halves. Each step combines two lanes that then hold the same value (the operations commute), so every
+// lane of the row ends with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_move<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_move<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_move<0x141>(v);  // row_half_mirror
+  return v + dpp_move<0x140>(v);  // row_mirror
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_move<0xB1>(v));
+  v = fmaxf(v, dpp_move<0x4E>(v));
+  v = fmaxf(v, dpp_move<0x141>(v));
+  return fmaxf(v, dpp_move<0x140>(v));
+}
+// Whole-wave reductions: across the four row groups, then within the row.
+__device__ __forceinline__ float wave_max(float v) { return row16_max(max_across_groups(v)); }
+__device__ __forceinline__ float wave_sum(float v) { return row16_sum(sum_across_groups(v)); }
 
 // ---- split-K work decomposition ----
 // Sequence b's keys from the pool are positions [lo_b, hi_b): hi_b = seq_len_b - 1 (the step's own token is attended

@@ -66,7 +66,7 @@ struct MlaArgs {
   float sm_scale;
   int32_t n_ctas;      // workgroups per head group
   int32_t wait_polls;  // polls of a row's arrival counter by a workgroup that published a partial
-  float* ws_o;         // [2 n_ctas, H, 512] partial contexts (unnormalized, natural latent-dim order)
+  float* ws_o;         // [2 n_ctas, H, 512] partial contexts (unnormalized; ROWS640 in latent-byte order)
   float* ws_ml;        // [2 n_ctas, H, 2] their (max, sum), log2 domain
   int32_t* ws_cnt;     // arrival words [kStreamMaxCounters], (unused) [kStreamMaxCounters], finished workgroups [1]
   uint16_t* out;
@@ -279,8 +279,17 @@ __device__ void merge_chunks(const MlaArgs& a, __amdgpu_buffer_rsrc_t ro, __amdg
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
     if (chunks[i] < 0) continue;
-    *reinterpret_cast<uint2*>(a.out + ((int64_t)b * a.H + h) * kLatent + 64 * chunks[i] + 4 * q) =
-        make_uint2(pack_bf16x2(o[i].x * inv, o[i].y * inv), pack_bf16x2(o[i].z * inv, o[i].w * inv));
+    uint16_t* dst = a.out + ((int64_t)b * a.H + h) * kLatent;
+    const int beta = 64 * chunks[i] + 4 * q;  // the partials' latent byte of o[i].x
+    if constexpr (!SPARSE) {
+      *reinterpret_cast<uint2*>(dst + beta) =
+          make_uint2(pack_bf16x2(o[i].x * inv, o[i].y * inv), pack_bf16x2(o[i].z * inv, o[i].w * inv));
+    } else {
+      // bytes beta .. beta + 3 of a ROWS640 latent are dims d0, d0 + 128, d0 + 1, d0 + 129
+      const int d0 = latent_dim_of_byte(beta);
+      *reinterpret_cast<uint32_t*>(dst + d0) = pack_bf16x2(o[i].x * inv, o[i].z * inv);
+      *reinterpret_cast<uint32_t*>(dst + d0 + 128) = pack_bf16x2(o[i].y * inv, o[i].w * inv);
+    }
     if (SPARSE && a.lse_out && chunks[i] == 0 && q == 0)
       a.lse_out[(int64_t)b * a.H + h] = (M + __log2f(L)) * 0.6931471805599453f;
   }
@@ -1090,14 +1099,10 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
         const int64_t prow = (int64_t)pslot * a.H + h;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
+          // partials are kept in latent-byte order (ROWS640: byte beta holds dim latent_dim_of_byte(beta)), so
+          // each lane stores 16 bytes and a head's 4 lanes 64 contiguous bytes; the merge maps bytes to dims
           const int beta = 64 * q + 16 * r + 4 * g4;
-          if constexpr (!SPARSE) {
-            store_dev16(ws_o_rsrc, (uint32_t)((prow * kLatent + beta) * 4), make_float4(v[r][0], v[r][1], v[r][2], v[r][3]));
-          } else {
-            const int d0 = latent_dim_of_byte(beta);
-            store_dev8(ws_o_rsrc, (uint32_t)((prow * kLatent + d0) * 4), make_float2(v[r][0], v[r][2]));
-            store_dev8(ws_o_rsrc, (uint32_t)((prow * kLatent + d0 + 128) * 4), make_float2(v[r][1], v[r][3]));
-          }
+          store_dev16(ws_o_rsrc, (uint32_t)((prow * kLatent + beta) * 4), make_float4(v[r][0], v[r][1], v[r][2], v[r][3]));
         }
         if (q == 0 && g4 == 0) store_dev8(ws_ml_rsrc, (uint32_t)(prow * 8), make_float2(M, L));
       }

@@ -193,15 +193,25 @@ __device__ __forceinline__ float2 load_dev8(__amdgpu_buffer_rsrc_t r, uint32_t o
   return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
 }
 
-// The number of workgroups (of n) whose range starts at or before global tile x.
-__device__ __forceinline__ int32_t ctas_starting_by(const MlaArgs& a, uint32_t x) {
+// The numbers of workgroups (of n) whose range starts at or before global tiles x0 and x1: the stream split's
+// starts, one per lane in four independent loads (so one memory round trip), counted by ballots.
+__device__ __forceinline__ void ctas_starting_by(const MlaArgs& a, uint32_t x0, uint32_t x1, int32_t& n0, int32_t& n1) {
+  static_assert(SNA_MAX_CTAS <= 256, "four loads of 64 starts");
   const int lane = threadIdx.x & 63;
-  int32_t n = 0;
-  for (int32_t base = 0; base < a.n_ctas; base += 64) {
-    const bool le = base + lane < a.n_ctas && a.cta_start[base + lane] <= x;
-    n += __popcll(__ballot(le));
+  uint32_t c[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int k = 64 * i + lane;
+    c[i] = k < a.n_ctas ? a.cta_start[k] : 0xffffffffu;
   }
-  return __builtin_amdgcn_readfirstlane(n);
+  int32_t s0 = 0, s1 = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s0 += __popcll(__ballot(c[i] <= x0));
+    s1 += __popcll(__ballot(c[i] <= x1));
+  }
+  n0 = __builtin_amdgcn_readfirstlane(s0);
+  n1 = __builtin_amdgcn_readfirstlane(s1);
 }
 
 // Merge of up to NC latent blocks (chunks[i]: dims 64 c .. 64 c + 63; -1 = none) of row b, head group hg, over its S
@@ -386,6 +396,11 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     const bool whole = g == row_t0 && s_hi == row_t1;   // the segment is the whole row: it writes the output
     const bool has_own = g == row_t0;                    // it holds the row's first tile: it attends the own row
     const bool first_seg = g == g_lo;                    // the partial slot: 2 w for the first segment, 2 w + 1 after
+    // the row's first and last workgroups (for the merge of a split row), found with the prologue's loads
+    int32_t wa, wb;
+    ctas_starting_by(a, row_t0, row_t1 - 1, wa, wb);
+    --wa;
+    --wb;
     const int32_t kbase = t_first * 16;
     const int32_t* trow = a.table + (int64_t)b * a.table_stride;
     const int32_t ntiles = t_last - t_first;
@@ -1116,8 +1131,6 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     // merges its own blocks and those its add found retracted, and waits for nothing: each block is merged exactly once.
     // (A workgroup whose range goes on into another row retracts at once.)
     if (!whole) {
-      const int32_t wa = ctas_starting_by(a, row_t0) - 1;      // the row's first workgroup
-      const int32_t wb = ctas_starting_by(a, row_t1 - 1) - 1;  // its last
       const int32_t S = wb - wa + 1;
       const bool wa_second = a.cta_start[wa] != row_t0;        // the row is not wa's first segment
       const int32_t pair = b * a.groups + hg;

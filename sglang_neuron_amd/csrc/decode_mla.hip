@@ -1179,8 +1179,8 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     __syncthreads();  // every wave is done with the ring's merge exchange before the next segment refills the ring
   }
 
-  // ---- the launch's last workgroup returns the counters to zero (every other one has finished with them) ----
-  wait_vmcnt<0>();
+  // ---- the launch's last workgroup returns the counters to zero (every other one has finished with them: its
+  // atomics on them have returned; its output stores need not have landed, so none is waited for here) ----
   __syncthreads();
   if (tid == 0) {
     const int32_t done = __hip_atomic_fetch_add(a.ws_cnt + kCounterStride * 2 * kStreamMaxCounters, 1,

@@ -124,9 +124,15 @@ struct TileGeo {
   static constexpr int TAIL = 16 * STRIDE - 64 * (NDMA - 1);    // active lanes of the last DMA
   static constexpr int SCALES = 16 * RS;                        // offset of the 16 per-token scales (ROWS576)
   static constexpr int SLOT = 16 * RS + 64;                     // bytes of one ring slot
-  // ring slots per wave: a bf16 tile is twice the bytes, so two slots hold as many bytes in flight as three
-  static constexpr int DEPTH = FMT == ROWS1152 ? 2 : (FMT == ROWS576 ? 4 : 3);
+  // ring slots per wave: two for the paged formats (FP8 rows with staged tiles measured 42.3 µs on the cfg3 batch
+  // against 43.3 with three and 44.7 with four: fewer loads outstanding per wave stream faster), three for the sparse
+  // gathers, whose latency-bound rows need the depth
+  static constexpr int DEPTH = FMT == ROWS640 ? 3 : 2;
 };
+// Slots the ring array holds per wave: its depth, or three FP8 slots' bytes, which the waves' merge exchange (96 KB)
+// reuses after the tile loop.
+template <int FMT>
+constexpr int kRingSlots = FMT == ROWS576 ? 3 : TileGeo<FMT>::DEPTH;
 
 // Dword 3 of a raw buffer resource on gfx9-family chips (no format conversion, no swizzle).
 constexpr int kBufferFlags = 0x00020000;
@@ -352,7 +358,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
   // LDS: each wave's ring of DEPTH tile slots (after a segment's tile loop: the merge exchange), the sparse row ids,
   // the waves' softmax statistics, the own row, the query operand (bf16 rows: in registers, the ring takes the
   // space), and a broadcast word.
-  __shared__ __attribute__((aligned(16))) uint8_t sm_ring[WAVES][DEPTH][SLOT];
+  __shared__ __attribute__((aligned(16))) uint8_t sm_ring[WAVES][kRingSlots<FMT>][SLOT];
   __shared__ int32_t sm_rowid[SPARSE ? kMlaMaxSplitKeys : 1];
   __shared__ uint4 sm_q[SPARSE ? 18 : 1][64];
   __shared__ float sm_m[WAVES][16];

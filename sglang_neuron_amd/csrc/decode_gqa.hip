@@ -102,7 +102,7 @@ struct GqaTile {
 };
 
 template <int D, bool FP8, int WAVES, bool FINAL, int DEPTH>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(DEPTH >= 4 ? 1 : 2)))
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
 void gqa_decode_kernel(GqaArgs a) {
   using Tile = GqaTile<D, FP8>;
   constexpr int ESZ = Tile::ESZ;
@@ -559,9 +559,9 @@ template <int D, bool FP8>
 static void launch_gqa(const GqaArgs& a, int depth, bool any_lone, hipStream_t s) {
   if (a.n_work > 0) {
     const dim3 grid(a.n_work, a.G);
-    if (depth >= 4) {
-      if (a.max_splits <= 1) hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, true, 4>), grid, dim3(256), 0, s, a);
-      else hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, false, 4>), grid, dim3(256), 0, s, a);
+    if (depth >= 3) {
+      if (a.max_splits <= 1) hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, true, 3>), grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, false, 3>), grid, dim3(256), 0, s, a);
     } else {
       if (a.max_splits <= 1) hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, true, 2>), grid, dim3(256), 0, s, a);
       else hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, false, 2>), grid, dim3(256), 0, s, a);

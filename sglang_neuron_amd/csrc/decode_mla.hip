@@ -124,15 +124,15 @@ struct TileGeo {
   static constexpr int TAIL = 16 * STRIDE - 64 * (NDMA - 1);    // active lanes of the last DMA
   static constexpr int SCALES = 16 * RS;                        // offset of the 16 per-token scales (ROWS576)
   static constexpr int SLOT = 16 * RS + 64;                     // bytes of one ring slot
-  // ring slots per wave: two for the paged formats (FP8 rows with staged tiles measured 42.3 µs on the cfg3 batch
-  // against 43.3 with three and 44.7 with four: fewer loads outstanding per wave stream faster), three for the sparse
-  // gathers, whose latency-bound rows need the depth
-  static constexpr int DEPTH = FMT == ROWS640 ? 3 : 2;
+  // ring slots per wave: two (FP8 rows with staged tiles measured 42.3 µs on the cfg3 batch against 43.3 with three
+  // and 44.7 with four, and the sparse gathers of the cfg5 batch 20.0 against 21.1 with three: fewer loads
+  // outstanding per wave stream faster)
+  static constexpr int DEPTH = 2;
 };
-// Slots the ring array holds per wave: its depth, or three FP8 slots' bytes, which the waves' merge exchange (96 KB)
-// reuses after the tile loop.
+// Slots the ring array holds per wave: its depth, or three 16-key FP8 slots' bytes, which the waves' merge exchange
+// (96 KB) reuses after the tile loop.
 template <int FMT>
-constexpr int kRingSlots = FMT == ROWS576 ? 3 : TileGeo<FMT>::DEPTH;
+constexpr int kRingSlots = FMT == ROWS1152 ? TileGeo<FMT>::DEPTH : 3;
 
 // Dword 3 of a raw buffer resource on gfx9-family chips (no format conversion, no swizzle).
 constexpr int kBufferFlags = 0x00020000;

@@ -452,6 +452,13 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
         }
       }
     }
+    // FP8 rows (FP8QK): QK runs on v_mfma_scale_f32_16x16x128_f8f6f4 for the latent dims, K's bytes straight from the
+    // tile. Lane (g4, li) then supplies dims 128 kb + 32 g4 .. + 31 of latent block kb (kb < 4) of head li: its bf16
+    // query values (loaded here as qreg[4 kb .. 4 kb + 3]) scaled by a power of two sc (the head's absolute maximum
+    // into [128, 256)) and split exactly into two e4m3fn parts, hi + lo / 16, whose per-lane E8M0 B scales undo sc
+    // (and lo's 1/16), so K . Q is the bf16 dot product accumulated in fp32. The rope dims stay bf16 (qreg[16],
+    // qreg[17]: dims 16 g4 .. + 7 and 16 g4 + 8 .. + 15 of the rope) for two v_mfma_f32_16x16x32_bf16 steps.
+    constexpr bool FP8QK = FMT == ROWS576;
     uint4 qreg[SPARSE ? 1 : 18];
     if constexpr (!SPARSE) {
       const int32_t h = min(16 * hg + li, a.H - 1);
@@ -459,10 +466,49 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
       const uint16_t* qpp = a.qpe + ((int64_t)b * a.H + h) * kRope;
 #pragma unroll
       for (int st = 0; st < 18; ++st) {
-        const int d = 16 * (4 * (st >> 1) + g4) + 8 * (st & 1);
+        const int d = FP8QK ? (st < 16 ? 128 * (st >> 2) + 32 * g4 + 8 * (st & 3) : kLatent + 16 * g4 + 8 * (st & 1))
+                            : 16 * (4 * (st >> 1) + g4) + 8 * (st & 1);
         qreg[st] = ld16(d < kLatent ? qlp + d : qpp + (d - kLatent));
       }
     }
+    uint32_t qhi[FP8QK ? 4 : 1][8], qlo[FP8QK ? 4 : 1][8];
+    int32_t qs_hi = 127, qs_lo = 127;
+    // the split of the latent query (after the first tiles' loads are issued, so that it runs under their latency)
+    auto split_query = [&]() {
+      if constexpr (FP8QK) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int st = 0; st < 16; ++st) {
+          const uint32_t ww[4] = {qreg[st].x, qreg[st].y, qreg[st].z, qreg[st].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            amax = fmaxf(amax, fmaxf(fabsf(bf16_bits_to_f32(ww[e] & 0xffffu)), fabsf(bf16_bits_to_f32(ww[e] >> 16))));
+        }
+        amax = max_across_groups(amax);
+        // sc = 2^(7 - floor(log2 amax)): amax * sc in [128, 256); E8M0 scale of hi = 127 - log2 sc, of lo 4 less (the
+        // exponent is held to [-116, 127], where sc and both E8M0 scales are representable; a head that small only
+        // loses bits far below the tolerance)
+        const int32_t ex = amax > 0.0f ? max((int32_t)((__float_as_uint(amax) >> 23) & 0xff) - 127, -116) : -7;
+        const float sc = __uint_as_float((uint32_t)(127 + 7 - ex) << 23);
+        qs_hi = 127 + ex - 7;
+        qs_lo = qs_hi - 4;
+#pragma unroll
+        for (int st = 0; st < 16; ++st) {
+          const uint32_t ww[4] = {qreg[st].x, qreg[st].y, qreg[st].z, qreg[st].w};
+#pragma unroll
+          for (int e2 = 0; e2 < 2; ++e2) {
+            float h4[4], l4[4];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              split_q(bf16_bits_to_f32(ww[2 * e2 + e] & 0xffffu) * sc, h4[2 * e], l4[2 * e]);
+              split_q(bf16_bits_to_f32(ww[2 * e2 + e] >> 16) * sc, h4[2 * e + 1], l4[2 * e + 1]);
+            }
+            qhi[st >> 2][2 * (st & 3) + e2] = pack_e4m3fn_x4(h4[0], h4[1], h4[2], h4[3]);
+            qlo[st >> 2][2 * (st & 3) + e2] = pack_e4m3fn_x4(l4[0], l4[1], l4[2], l4[3]);
+          }
+        }
+      }
+    };
     // the query operand of QK step st (8 bf16 of head li, as lane (g4, li) feeds them)
     auto q_op = [&](int st) -> uint4 {
       if constexpr (SPARSE) return sm_q[st][lane];
@@ -702,9 +748,55 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
       }
     };
     // The tile's scores in the log2 domain (x[r]: slot 4 g4 + r, head li; -inf when masked) and their maximum per head.
+    // FP8 rows: S^T of a tile from its 9 chunks of key key_of(li)'s row, kc[2 kb + j] = latent chunk 8 kb + 2 g4 + j
+    // and kc[8] = rope chunk 32 + g4, in three independent MFMA chains
+    auto qk_fp8 = [&](const uint4 (&kc)[9]) -> f32x4_t {
+      f32x4_t sp[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const uint32_t a8[8] = {kc[2 * kb].x, kc[2 * kb].y, kc[2 * kb].z, kc[2 * kb].w,
+                                kc[2 * kb + 1].x, kc[2 * kb + 1].y, kc[2 * kb + 1].z, kc[2 * kb + 1].w};
+        f32x4_t& sc = sp[kb >> 1];
+        sc = mfma_16x16x128_fp8(a8, qhi[kb], sc, qs_hi);
+        sc = mfma_16x16x128_fp8(a8, qlo[kb], sc, qs_lo);
+      }
+      uint32_t op0[4], op1[4];
+      fp8x4_to_bf16x4(kc[8].x, op0[0], op0[1]);
+      fp8x4_to_bf16x4(kc[8].y, op0[2], op0[3]);
+      fp8x4_to_bf16x4(kc[8].z, op1[0], op1[1]);
+      fp8x4_to_bf16x4(kc[8].w, op1[2], op1[3]);
+      const uint32_t b0[4] = {qreg[16].x, qreg[16].y, qreg[16].z, qreg[16].w};
+      const uint32_t b1[4] = {qreg[17].x, qreg[17].y, qreg[17].z, qreg[17].w};
+      sp[2] = mfma_16x16x32_bf16(op0, b0, sp[2]);
+      sp[2] = mfma_16x16x32_bf16(op1, b1, sp[2]);
+      return sp[0] + sp[1] + sp[2];
+    };
+    // the 9 chunks of a tile in LDS at T (row stride rs)
+    auto load_chunks = [&](const uint8_t* T, int rs, uint4 (&kc)[9]) {
+      const uint8_t* Tq = T + key_of(li) * rs;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) kc[2 * kb + j] = *reinterpret_cast<const uint4*>(Tq + 16 * (8 * kb + 2 * g4 + j));
+      kc[8] = *reinterpret_cast<const uint4*>(Tq + 16 * (32 + g4));
+    };
     auto scores = [&](const uint8_t* T, uint32_t vmask, float (&x)[4], float& tmax, int rs, const uint8_t* S) {
       float ks[4];
       [[clang::always_inline]] key_scales(S, ks);
+      if constexpr (FP8QK) {
+        uint4 kc[9];
+        [[clang::always_inline]] load_chunks(T, rs, kc);
+        const f32x4_t sc = qk_fp8(kc);
+        tmax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool ok = (vmask >> key_of(4 * g4 + r)) & 1u;
+          x[r] = ok ? sc[r] * base_scale * ks[r] : -INFINITY;
+          tmax = fmaxf(tmax, x[r]);
+        }
+        tmax = max_across_groups(tmax);
+        return;
+      }
       // S^T = K Q^T: three accumulators keep three independent MFMA chains in flight
       const uint8_t* Tq = T + key_of(li) * rs + 16 * g4;
       f32x4_t scp[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
@@ -806,8 +898,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
 #pragma unroll
           for (int k = 1; k < 9; ++k) kst[k + 1] = *reinterpret_cast<const uint4*>(Tq + 128 + 64 * (k - 1));
         } else {
-#pragma unroll
-          for (int k = 0; k < 9; ++k) kst[k] = *reinterpret_cast<const uint4*>(Tq + 64 * k);
+          [[clang::always_inline]] load_chunks(T, RS, kst);
         }
         const uint8_t* Tv = T + key_of(4 * g4 + ((li >> 1) & 3)) * RS + (SPARSE ? 128 : 0) + 16 * (li >> 3) + 8 * (li & 1);
 #pragma unroll
@@ -817,6 +908,18 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     };
     // scores and accumulate of the staged tile, as above
     auto scores_staged = [&](uint32_t vmask, float (&x)[4], float& tmax) {
+      if constexpr (FP8QK) {
+        const f32x4_t sc = qk_fp8(kst);
+        tmax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool ok = (vmask >> key_of(4 * g4 + r)) & 1u;
+          x[r] = ok ? sc[r] * base_scale * kss[r] : -INFINITY;
+          tmax = fmaxf(tmax, x[r]);
+        }
+        tmax = max_across_groups(tmax);
+        return;
+      }
       f32x4_t scp[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
       for (int k = 0; k < 9; ++k) {
@@ -900,6 +1003,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
 #pragma unroll
       for (int i = 0; i < AHEAD; ++i)
         if (i < mine) issue(ring + i * SLOT, t0 + i * WAVES);
+      [[clang::always_inline]] split_query();
       // The own row, quantized as the store quantizes it, into sm_own in the pool's row format (LDS and registers only:
       // nothing here may add to the VMEM count the waits below rely on).
       if (own_wave) {

@@ -157,9 +157,10 @@ typedef struct {
   int32_t max_splits;   /* GQA: the most splits any row has; MLA / DSA: the most workgroups any row spans */
   int32_t batch;        /* rows the plan was made for */
   int32_t empty_rows;   /* rows with no prior key (seq_len 1), or -1 when planned from a bound */
-  int32_t depth;        /* GQA: tiles each wave keeps in its register ring (2: small launches of several rounds;
-                           3: the deep ring of one round, two tiles in flight per wave). The planner picks it; splits
-                           were sized for it. */
+  int32_t depth;        /* GQA: the plan's shape (3: one round of two 4-wave workgroups per CU, for launches with
+                           enough work to fill the chip with long splits; 2: small launches of several rounds). The
+                           kernels keep two tiles per wave in their register rings either way. The planner picks it;
+                           splits were sized for it. */
   int32_t work_n;       /* GQA: entries in work[] (0: the kernels locate their items from the device's seq_lens) */
   uint32_t work[SNA_MAX_WORK_MAP]; /* GQA, a plan from host seq_lens with n_work and B <= SNA_MAX_WORK_MAP: item i
                            is row (work[i] & 0x7fffffff) >> 6, split work[i] & 63, bit 31 set on a row's last item, in

@@ -181,7 +181,7 @@ const char* sna_last_error(void) { return error_buffer(); }
 int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32_t max_seq_len, int32_t window,
                     int32_t n_keys_per_row, int32_t ctas_per_item, int32_t num_cus, sna_split_plan* plan) {
   ApiGuard guard;
-  const int32_t gqa_depth = plan ? plan->depth : 0;  // a caller may preset the ring depth it wants (2 or 3)
+  const int32_t gqa_depth = plan ? plan->depth : 0;  // a caller may preset the plan shape it wants (2 or 3)
   if (!plan) return fail(SNA_ERR_INVALID_ARGUMENT, "plan_decode: null plan");
   if (kind < 0 || kind > 2) return fail(SNA_ERR_INVALID_ARGUMENT, "plan_decode: unknown kind %d", kind);
   if (B < 0 || ctas_per_item < 1 || window < 0)
@@ -215,9 +215,8 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
     total_tiles += t;
     max_tiles = std::max(max_tiles, t);
   }
-  // GQA register-ring depth: the deep ring (3) when there is enough work to fill the chip with long splits; the
-  // shallow ring (2) keeps small launches short. (A ring of 4 measured 1-2% slower than 3 on the cfg2 and cfg4
-  // batches: fewer loads outstanding per wave stream faster.)
+  // GQA plan shape: one round of two workgroups per CU (3) when there is enough work to fill the chip with long
+  // splits; several rounds of smaller splits (2) keep small launches short.
   const int32_t depth = gqa_depth > 0 ? gqa_depth : (total_tiles * ctas_per_item >= (int64_t)cus * 32 ? 3 : 2);
   // Resident workgroups the launch aims for, and whether it must fit them in one round. GQA with the deep ring holds
   // two 4-wave workgroups per CU and runs one round; the shallow ring holds about three and runs a few rounds. The

@@ -206,7 +206,7 @@ def plan_decode(kind: int, B: int, *, host_seq_lens: Union[Tensor, Sequence[int]
                 max_seq_len: int = -1, window: int = 0, n_keys_per_row: int = 0, ctas_per_item: int = 1,
                 num_cus: int = 0, gqa_depth: int = 0) -> _lib.SplitPlan:
     """The split-K plan of a decode launch (sna_plan_decode): exact from host seq_lens, or a bound from
-    ``max_seq_len``. ``gqa_depth`` (2 or 3) asks for a GQA register-ring depth; 0 lets the planner pick."""
+    ``max_seq_len``. ``gqa_depth`` (2 or 3) asks for a GQA plan shape (see sna_split_plan.depth); 0 lets the planner pick."""
     plan = _lib.SplitPlan()
     plan.depth = int(gqa_depth)
     arr = None

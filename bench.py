@@ -9,8 +9,11 @@ times, so every step reads cold HBM.
 
 One JSON line on stdout:
   value         algorithmic HBM bytes of the step / step time, GB/s (higher is better); ms_per_step beside it. The
-                step time is one HIP event pair (torch events on the stream the kernels launch on) around K
-                back-to-back steps, divided by K.
+                step time: the K steps captured in one HIP graph on the stream the kernels launch on, one untimed
+                replay, then one HIP event pair (torch events) around one replay, divided by K. The same K steps
+                launched one by one from the host (after W warm-up steps, one event pair around them) are reported as
+                us_per_step_launched: for the small steps (cfg1, cfg4's window layer) that number is the host's
+                launch rate.
   roofline      the step's kernels (cfg2: the one split-K decode kernel): their algorithmic bytes per step / the step
                 time, against MI355X's 8 TB/s. traffic = FETCH_SIZE + WRITE_SIZE per step from the committed
                 rocprofv3 counter summary (traffic_source says which), else null.
@@ -44,6 +47,7 @@ if ROOT not in sys.path:
 METRIC = "decode-attn µs/step + achieved HBM GB/s (% of peak), FP8 KV, 1 MI355X"
 PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP8_TFLOPS = 5000.0
 COLD_BYTES = 1 << 30  # rotate pool copies until the rotation spans this much (4x the Infinity Cache)
 COPY_CALIBRATION_BYTES = 1 << 30
 
@@ -106,6 +110,30 @@ def time_us(fn, n_steps: int, warmup: int) -> float:
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / n_steps * 1e3
+
+
+def time_us_graph(fn, n_steps: int) -> float:
+    """Microseconds per call of fn(i) with the n_steps calls captured in one HIP graph (torch.cuda.CUDAGraph, on the
+    current stream, which the calls are bound to): one untimed replay, then one HIP event pair around one replay of
+    all n_steps calls. The GPU's time for the steps, without the host's per-call launch cost (a serving loop replays
+    such a graph)."""
+    import torch
+
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=torch.cuda.current_stream()):
+        for i in range(n_steps):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / n_steps * 1e3
+    del g
+    return us
 
 
 def cpu_threads() -> int:
@@ -222,7 +250,12 @@ def setup_mla(dev, bf16: bool = False):
                                     sm_scale=case.sm_scale, page_size=case.P, new_slots=case.new_slots.to(dev),
                                     out=out, plan=plan) for (c, s) in pools]
     tiles = int(((case.seq_lens - 1 + 15) // 16).sum())
-    mfma_flops = tiles * (18 * 16 * 16 * 32 * 2 + 32 * 16 * 16 * 16 * 2)
+    # bf16 rows: 18 QK steps of 16x16x32 and 32 PV steps of 16x16x16 (bf16); FP8 rows: the latent QK as 8 scaled FP8
+    # 16x16x128 (4 blocks, the query's two parts), the rope as 2 bf16 16x16x32, PV as 32 bf16 16x16x16
+    if bf16:
+        mfma_flops = tiles * (18 * 16 * 16 * 32 * 2 + 32 * 16 * 16 * 16 * 2)
+    else:
+        mfma_flops = {"bf16": tiles * (2 * 16 * 16 * 32 * 2 + 32 * 16 * 16 * 16 * 2), "fp8": tiles * 8 * 16 * 16 * 128 * 2}
     desc = {"workload": "cfg3-bf16: deepseek-v2-lite absorbed MLA, bf16 rows (the reference's served dtype)" if bf16
             else "cfg3: deepseek-v2-lite absorbed MLA", "batch": case.B, "q_heads": case.H,
             "qk_dim": 576, "v_dim": 512, "page_size": case.P,
@@ -732,24 +765,36 @@ def setup(key: str, dev):
 
 
 def measure_decode(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> dict:
-    """One decode config: its step time from one event pair around steps_n back-to-back steps, the roofline of the
-    step's kernels, and (cpu) the CPU baseline. The pools are freed before returning."""
+    """One decode config: its step time, the roofline of the step's kernels, and (cpu) the CPU baseline. The step time
+    is the steps_n steps captured in one HIP graph and replayed (one event pair around the replay); the same steps
+    launched one by one from the host (one event pair around steps_n back-to-back calls, after warmup calls) are
+    reported beside it: for the small steps that number is the host's launch rate, not the GPU's. The pools are freed
+    before returning."""
     import torch
 
-    steps, desc, step_bytes, kernels, mfma_flops, cpu_fn = setup(key, dev)
-    n = len(steps)
-    wall = time.perf_counter()
-    us = time_us(lambda i: steps[i % n](), steps_n, warmup)
-    wall = time.perf_counter() - wall
+    stream = torch.cuda.Stream()  # a side stream: the steps are bound to it, and a graph captures it
+    with torch.cuda.stream(stream):
+        steps, desc, step_bytes, kernels, mfma_flops, cpu_fn = setup(key, dev)
+        n = len(steps)
+        wall = time.perf_counter()
+        us_eager = time_us(lambda i: steps[i % n](), steps_n, warmup)
+        wall = time.perf_counter() - wall
+        us = time_us_graph(lambda i: steps[i % n](), steps_n)
     gbs = step_bytes / (us * 1e-6) / 1e9
     wl = desc["workload"].split(":")[0]
     traffic, traffic_source = _traffic(wl)
-    mfma_tflops = mfma_flops / (us * 1e-6) / 1e12
-    log(f"{wl}: {us:.2f} us/step over {steps_n} back-to-back steps ({gbs:.0f} GB/s, {gbs / PEAK_HBM_GBS:.1%} of HBM "
-        f"peak); {wall * 1e6 / (steps_n + warmup):.1f} us/step by the host clock; kernels {kernels}")
+    # MFMA work the kernels issue, bf16 and FP8 (a dict when both): total TFLOP/s and the fraction of the pipe's dense
+    # peak time they fill (bf16 work over the bf16 peak plus FP8 work over the FP8 peak)
+    mf = mfma_flops if isinstance(mfma_flops, dict) else {"bf16": mfma_flops, "fp8": 0}
+    mfma_tflops = (mf["bf16"] + mf["fp8"]) / (us * 1e-6) / 1e12
+    mfma_frac = (mf["bf16"] / PEAK_BF16_TFLOPS + mf["fp8"] / PEAK_FP8_TFLOPS) / (us * 1e-6) / 1e12
+    log(f"{wl}: {us:.2f} us/step over {steps_n} steps replayed from a HIP graph ({gbs:.0f} GB/s, {gbs / PEAK_HBM_GBS:.1%} "
+        f"of HBM peak); {us_eager:.2f} us/step launched one by one ({wall * 1e6 / (steps_n + warmup):.1f} us/step by "
+        f"the host clock); kernels {kernels}")
     out = {
         "config": desc,
         "us_per_step": round(us, 3),
+        "us_per_step_launched": round(us_eager, 3),
         "step_alg_bytes": step_bytes,
         "roofline": {
             "bound": "hbm",
@@ -763,9 +808,11 @@ def measure_decode(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: f
             "traffic_source": traffic_source,
             "alg_bytes_per_step": step_bytes,
             "us_per_step": round(us, 3),
-            "timing": f"one HIP event pair (torch events, the launch stream) around {steps_n} back-to-back steps",
+            "timing": f"one HIP event pair (torch events, the launch stream) around one replay of a HIP graph of "
+                      f"{steps_n} steps; us_per_step_launched: the same steps launched one by one from the host",
         },
-        "mfma": {"alg_tflops": round(mfma_tflops, 2), "frac_of_bf16_dense_peak": round(mfma_tflops / PEAK_BF16_TFLOPS, 4),
+        "mfma": {"alg_tflops": round(mfma_tflops, 2), "frac_of_dense_peak": round(mfma_frac, 4),
+                 "fp8_share": round(mf["fp8"] / max(mf["bf16"] + mf["fp8"], 1), 4),
                  "source": "algorithmic: MFMA instructions the kernel issues (16x16 key tiles x shapes) / step time, "
                            "not a hardware counter"},
         "cpu_baseline": None,
@@ -774,8 +821,10 @@ def measure_decode(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: f
     if mc:
         out["mfma"]["counter_busy_pct"] = mc["mfma_busy_pct"]
         out["mfma"]["counter_flops_per_step"] = mc["mfma_flops_per_step"]
-        out["mfma"]["counter_source"] = (f"committed rocprofv3 pass of MfmaUtil and MfmaFlopsBF16 "
-                                         f"(profiles/mfma_{wl}.json), not this run")
+        if "mfma_f8_flops_per_step" in mc:
+            out["mfma"]["counter_f8_flops_per_step"] = mc["mfma_f8_flops_per_step"]
+        out["mfma"]["counter_source"] = (f"committed rocprofv3 pass of MfmaUtil, MfmaFlopsBF16 and "
+                                         f"SQ_INSTS_VALU_MFMA_MOPS_F8 (profiles/mfma_{wl}.json), not this run")
     if cpu:
         log(f"{wl}: CPU baseline (oracle on {cpu_threads()} host threads)")
         cb = cpu_fn(cpu_budget)

@@ -361,6 +361,9 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t sm_ring[WAVES][kRingSlots<FMT>][SLOT];
   __shared__ int32_t sm_rowid[SPARSE ? kMlaMaxSplitKeys : 1];
   __shared__ uint4 sm_q[SPARSE ? 18 : 1][64];
+  // FP8 rows: the head group's query as it lies in memory, DMA'd once per workgroup ([16][512] latent, then [16][64]
+  // rope, bf16)
+  __shared__ __attribute__((aligned(16))) uint8_t sm_qraw[FMT == ROWS576 ? 18432 : 16];
   __shared__ float sm_m[WAVES][16];
   __shared__ float sm_l[WAVES][16];
   // The own row in the pool's row format (its bytes stand for all 16 keys of a tile with row stride 0), then its
@@ -460,7 +463,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     // qreg[17]: dims 16 g4 .. + 7 and 16 g4 + 8 .. + 15 of the rope) for two v_mfma_f32_16x16x32_bf16 steps.
     constexpr bool FP8QK = FMT == ROWS576;
     uint4 qreg[SPARSE ? 1 : 18];
-    if constexpr (!SPARSE) {
+    if constexpr (!SPARSE && !FP8QK) {
       const int32_t h = min(16 * hg + li, a.H - 1);
       const uint16_t* qlp = a.ql + ((int64_t)b * a.H + h) * kLatent;
       const uint16_t* qpp = a.qpe + ((int64_t)b * a.H + h) * kRope;
@@ -1000,9 +1003,37 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
       // vmcnt 0, expcnt 7, lgkmcnt 15), before any DMA is in flight; otherwise it could wait for them again inside the
       // loop, and such a wait would drain the DMAs.
       __builtin_amdgcn_s_waitcnt(0x0f70);
+      if constexpr (FP8QK) {
+        // the query's 18 KB by 18 wave-wide DMAs dealt round-robin to the waves (a head past the group reads zeros)
+        const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(a.ql + ((int64_t)b * a.H + 16 * hg) * kLatent), (short)0, nh * kLatent * 2, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(a.qpe + ((int64_t)b * a.H + 16 * hg) * kRope), (short)0, nh * kRope * 2, kBufferFlags);
+        const uint32_t qb = lds_address((lds_void*)(lds_u8*)&sm_qraw[0]);
+        for (int k = wave; k < 18; k += WAVES) {
+          if (k < 16) dma_buffer16(rq, qb + 1024 * k, 1024 * k + 16 * lane);
+          else dma_buffer16(rr, qb + 1024 * k, 1024 * (k - 16) + 16 * lane);
+        }
+      }
 #pragma unroll
       for (int i = 0; i < AHEAD; ++i)
         if (i < mine) issue(ring + i * SLOT, t0 + i * WAVES);
+      if constexpr (FP8QK) {
+        // this wave's query DMAs have landed (only its tiles' DMAs, issued after them, may be in flight), then every
+        // wave's; lane (g4, li) takes its operand elements of head li
+        static_assert(AHEAD == 2, "the waits below count two tiles");
+        const int32_t n_after = min(mine, AHEAD);
+        if (n_after >= 2) wait_vmcnt<2 * PER_TILE>();
+        else if (n_after == 1) wait_vmcnt<PER_TILE>();
+        else wait_vmcnt<0>();
+        __syncthreads();
+#pragma unroll
+        for (int st = 0; st < 18; ++st) {
+          const int off = st < 16 ? 1024 * li + 2 * (128 * (st >> 2) + 32 * g4 + 8 * (st & 3))
+                                  : 16384 + 128 * li + 2 * (16 * g4 + 8 * (st & 1));
+          qreg[st] = *reinterpret_cast<const uint4*>(&sm_qraw[off]);
+        }
+      }
       [[clang::always_inline]] split_query();
       // The own row, quantized as the store quantizes it, into sm_own in the pool's row format (LDS and registers only:
       // nothing here may add to the VMEM count the waits below rely on).

@@ -32,6 +32,7 @@ DSA indexer, --config qkv the QKV writer, --config wire the PD page items; --all
 from __future__ import annotations
 
 import argparse
+import functools
 import json
 import math
 import os
@@ -160,8 +161,10 @@ def cpu_median_s(run) -> float:
 
 
 # ---------------------------------------------------------------------------------------------------------------
-# workloads: each returns (steps [Prepared per pool copy], description dict, alg bytes of the step, alg bytes and
-# MFMA flops of the split-K kernel launch, a CPU-baseline callable)
+# workloads: each returns (steps [Prepared per pool copy], description dict, alg bytes of the step, the step's kernels,
+# the MFMA flops they issue, a CPU-baseline callable, and the step's two halves timed apart: "store" (the standalone
+# store kernel of the step's new tokens) and "decode" (the decode without its fused store), each a callable per pool
+# copy)
 # ---------------------------------------------------------------------------------------------------------------
 
 def setup_gqa(cfg: int, window: int, dev):
@@ -189,6 +192,10 @@ def setup_gqa(cfg: int, window: int, dev):
     steps = [ops.prepare_paged_decode_gqa(q, k, v, table, lens, kn, vn, sm_scale=case.sm_scale, k_scale=ks,
                                           v_scale=vs, sinks=sinks, window=case.window, new_slots=slots, out=out,
                                           plan=plan) for (k, v) in pools]
+    legs = {"store": [functools.partial(ops.kv_store_mha, kn, vn, slots, k, v, ks, vs) for (k, v) in pools],
+            "decode": [ops.prepare_paged_decode_gqa(q, k, v, table, lens, kn, vn, sm_scale=case.sm_scale, k_scale=ks,
+                                                    v_scale=vs, sinks=sinks, window=case.window, out=out, plan=plan)
+                       for (k, v) in pools]}
     tiles = 0
     for L in case.seq_lens.tolist():
         hi = L - 1
@@ -226,7 +233,7 @@ def setup_gqa(cfg: int, window: int, dev):
 
     kernels = ["gqa_decode_kernel"] + (["gqa_combine_kernel"] if plan.max_splits > 1 else []) + \
         (["gqa_lone_token_kernel"] if bool((case.seq_lens == 1).any()) else [])
-    return steps, desc, case.kv_bytes_per_step(), kernels, mfma_flops, cpu_baseline
+    return steps, desc, case.kv_bytes_per_step(), kernels, mfma_flops, cpu_baseline, legs
 
 
 def setup_mla(dev, bf16: bool = False):
@@ -246,9 +253,14 @@ def setup_mla(dev, bf16: bool = False):
     table, lens = case.block_table.to(dev), case.seq_lens.to(dev)
     plan = ops.plan_decode(1, case.B, host_seq_lens=case.seq_lens, ctas_per_item=1, num_cus=ops._num_cus(table.device))
     out = torch.empty(case.B, case.H, 512, dtype=torch.bfloat16, device=dev)
+    new_slots = case.new_slots.to(dev)
     steps = [ops.prepare_mla_decode(case.ql_nope, case.q_pe, c, s, table, lens, case.compact_new,
-                                    sm_scale=case.sm_scale, page_size=case.P, new_slots=case.new_slots.to(dev),
+                                    sm_scale=case.sm_scale, page_size=case.P, new_slots=new_slots,
                                     out=out, plan=plan) for (c, s) in pools]
+    legs = {"store": [functools.partial(ops.kv_store_mla, case.compact_new, new_slots, c, s) for (c, s) in pools],
+            "decode": [ops.prepare_mla_decode(case.ql_nope, case.q_pe, c, s, table, lens, case.compact_new,
+                                              sm_scale=case.sm_scale, page_size=case.P, out=out, plan=plan)
+                       for (c, s) in pools]}
     tiles = int(((case.seq_lens - 1 + 15) // 16).sum())
     # bf16 rows: 18 QK steps of 16x16x32 and 32 PV steps of 16x16x16 (bf16); FP8 rows: the latent QK as 8 scaled FP8
     # 16x16x128 (4 blocks, the query's two parts), the rope as 2 bf16 16x16x32, PV as 32 bf16 16x16x16
@@ -277,7 +289,7 @@ def setup_mla(dev, bf16: bool = False):
 
         return _time_rows(run, case.B, budget_s)
 
-    return steps, desc, case.kv_bytes_per_step(bf16), ["mla_decode_kernel"], mfma_flops, cpu_baseline
+    return steps, desc, case.kv_bytes_per_step(bf16), ["mla_decode_kernel"], mfma_flops, cpu_baseline, legs
 
 
 def setup_dsa(dev):
@@ -297,9 +309,14 @@ def setup_dsa(dev):
     idx, table, pos = case.indices.to(dev), case.block_table.to(dev), case.positions.to(dev)
     plan = ops.plan_decode(2, case.B, n_keys_per_row=case.indices.shape[1], ctas_per_item=1,
                            num_cus=ops._num_cus(idx.device))
+    new_slots = case.new_slots.to(dev)
     steps = [ops.prepare_mla_decode_sparse(case.q_absorbed, case.q_pe, c, case.kv_scale, idx, table, pos,
                                            case.own_rows, sm_scale=case.sm_scale, page_size=case.P,
-                                           new_slots=case.new_slots.to(dev), plan=plan) for c in pools]
+                                           new_slots=new_slots, plan=plan) for c in pools]
+    legs = {"store": [functools.partial(ops.kv_store_dsa, case.own_rows, new_slots, c, case.kv_scale) for c in pools],
+            "decode": [ops.prepare_mla_decode_sparse(case.q_absorbed, case.q_pe, c, case.kv_scale, idx, table, pos,
+                                                     case.own_rows, sm_scale=case.sm_scale, page_size=case.P,
+                                                     plan=plan) for c in pools]}
     tiles = case.B * (-(-case.indices.shape[1] // 16))
     mfma_flops = tiles * (18 * 16 * 16 * 32 * 2 + 32 * 16 * 16 * 16 * 2)
     desc = {"workload": "cfg5: glm-5.2-style DSA absorbed MLA", "batch": case.B, "q_heads": case.H,
@@ -321,7 +338,7 @@ def setup_dsa(dev):
 
         return _time_rows(run, case.B, budget_s)
 
-    return steps, desc, case.kv_bytes_per_step(), ["mla_decode_kernel"], mfma_flops, cpu_baseline
+    return steps, desc, case.kv_bytes_per_step(), ["mla_decode_kernel"], mfma_flops, cpu_baseline, legs
 
 
 def _time_rows(run, B: int, budget_s: float):
@@ -774,12 +791,17 @@ def measure_decode(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: f
 
     stream = torch.cuda.Stream()  # a side stream: the steps are bound to it, and a graph captures it
     with torch.cuda.stream(stream):
-        steps, desc, step_bytes, kernels, mfma_flops, cpu_fn = setup(key, dev)
+        steps, desc, step_bytes, kernels, mfma_flops, cpu_fn, legs = setup(key, dev)
         n = len(steps)
         wall = time.perf_counter()
         us_eager = time_us(lambda i: steps[i % n](), steps_n, warmup)
         wall = time.perf_counter() - wall
         us = time_us_graph(lambda i: steps[i % n](), steps_n)
+        # the step's halves apart, the same way (the decode without its store, and the store kernel alone)
+        apart = {}
+        for leg, fns in legs.items():
+            time_us(lambda i: fns[i % n](), min(warmup, 5), 0)
+            apart[f"{leg}_us"] = round(time_us_graph(lambda i: fns[i % n](), steps_n), 3)
     gbs = step_bytes / (us * 1e-6) / 1e9
     wl = desc["workload"].split(":")[0]
     traffic, traffic_source = _traffic(wl)
@@ -790,11 +812,14 @@ def measure_decode(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: f
     mfma_frac = (mf["bf16"] / PEAK_BF16_TFLOPS + mf["fp8"] / PEAK_FP8_TFLOPS) / (us * 1e-6) / 1e12
     log(f"{wl}: {us:.2f} us/step over {steps_n} steps replayed from a HIP graph ({gbs:.0f} GB/s, {gbs / PEAK_HBM_GBS:.1%} "
         f"of HBM peak); {us_eager:.2f} us/step launched one by one ({wall * 1e6 / (steps_n + warmup):.1f} us/step by "
-        f"the host clock); kernels {kernels}")
+        f"the host clock); kernels {kernels}; apart: store {apart['store_us']:.2f} us, decode without it "
+        f"{apart['decode_us']:.2f} us")
     out = {
         "config": desc,
         "us_per_step": round(us, 3),
         "us_per_step_launched": round(us_eager, 3),
+        "apart": dict(apart, note="the step's store kernel alone and its decode without the fused store, each replayed "
+                                  "from a HIP graph of the same steps; us_per_step is both together (fused)"),
         "step_alg_bytes": step_bytes,
         "roofline": {
             "bound": "hbm",

@@ -1157,28 +1157,6 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
       wait_vmcnt<0>();
     }
 
-    // ---- the own row's pool store, deferred to here so that no store sits among the DMAs in flight ----
-    if (own_wave && own_slot >= 0) {
-      if constexpr (BF16) {
-        uint8_t* dst = a.cache + own_slot * 1152;
-        *reinterpret_cast<uint4*>(dst + 16 * lane) = own0;
-        if (lane < 8) *reinterpret_cast<uint4*>(dst + 16 * (lane + 64)) = own1;
-      } else if constexpr (FMT == ROWS576) {
-#pragma unroll
-        for (int part = 0; part < 2; ++part) {
-          if (part == 1 && lane >= 8) continue;
-          *reinterpret_cast<uint2*>(a.cache + own_slot * 576 + 8 * (lane + 64 * part)) =
-              make_uint2(own_q[2 * part], own_q[2 * part + 1]);
-        }
-        if (lane == 0) a.row_scale[own_slot] = own_s;
-      } else {
-        // the packed row is sm_own's first 640 bytes
-        uint8_t* dst = a.cache + own_slot * 640;
-        *reinterpret_cast<uint2*>(dst + 8 * lane) = *reinterpret_cast<const uint2*>(&sm_own[8 * lane]);
-        if (lane < 16) *reinterpret_cast<uint2*>(dst + 512 + 8 * lane) = *reinterpret_cast<const uint2*>(&sm_own[512 + 8 * lane]);
-      }
-    }
-
     // ---- merge the waves: a common maximum per head; wave w sums latent blocks 2 w, 2 w + 1 over the waves ----
     const float l_w = sum_across_groups(l_run);
     if (g4 == 0) {
@@ -1314,6 +1292,29 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
                            reinterpret_cast<float2*>(&sm_ring[0][0][0]));
       __syncthreads();
     }
+    // ---- the own row's pool store, last: no store sits among the DMAs in flight, and none delays the partial's
+    // publication (nothing in the launch reads the slot: a gather of it takes the packed source row) ----
+    if (own_wave && own_slot >= 0) {
+      if constexpr (BF16) {
+        uint8_t* dst = a.cache + own_slot * 1152;
+        *reinterpret_cast<uint4*>(dst + 16 * lane) = own0;
+        if (lane < 8) *reinterpret_cast<uint4*>(dst + 16 * (lane + 64)) = own1;
+      } else if constexpr (FMT == ROWS576) {
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+          if (part == 1 && lane >= 8) continue;
+          *reinterpret_cast<uint2*>(a.cache + own_slot * 576 + 8 * (lane + 64 * part)) =
+              make_uint2(own_q[2 * part], own_q[2 * part + 1]);
+        }
+        if (lane == 0) a.row_scale[own_slot] = own_s;
+      } else {
+        // the packed row is sm_own's first 640 bytes
+        uint8_t* dst = a.cache + own_slot * 640;
+        *reinterpret_cast<uint2*>(dst + 8 * lane) = *reinterpret_cast<const uint2*>(&sm_own[8 * lane]);
+        if (lane < 16) *reinterpret_cast<uint2*>(dst + 512 + 8 * lane) = *reinterpret_cast<const uint2*>(&sm_own[512 + 8 * lane]);
+      }
+    }
+
     g = s_hi;
     row_t0 = row_t1;
     if constexpr (!MULTI) break;

@@ -1035,8 +1035,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
         }
       }
       [[clang::always_inline]] split_query();
-      // The own row, quantized as the store quantizes it, into sm_own in the pool's row format (LDS and registers only:
-      // nothing here may add to the VMEM count the waits below rely on).
+      // The own row, quantized as the store quantizes it, into sm_own in the pool's row format.
       if (own_wave) {
         const uint32_t wv[8] = {own0.x, own0.y, own0.z, own0.w, own1.x, own1.y, own1.z, own1.w};
         if constexpr (BF16) {
@@ -1088,6 +1087,31 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
               }
             }
           }
+        }
+      }
+      // The own row's pool store, issued as soon as the row is packed. It sits among the DMAs, which only makes the
+      // waits below stricter until it completes: a wait for tile i still needs fewer outstanding operations than the
+      // DMAs issued after tile i, so tile i's have landed. (Issued after the tile loop, its completion fell on the
+      // workgroup's tail: +1.2 µs on cfg3.) Paged formats; the sparse one stores its own row at the segment's end
+      // (measured 0.2 µs better there, its unstaged ring being the more sensitive to a stricter wait).
+      if (!SPARSE && own_wave && own_slot >= 0) {
+        if constexpr (BF16) {
+          uint8_t* dst = a.cache + own_slot * 1152;
+          *reinterpret_cast<uint4*>(dst + 16 * lane) = own0;
+          if (lane < 8) *reinterpret_cast<uint4*>(dst + 16 * (lane + 64)) = own1;
+        } else if constexpr (FMT == ROWS576) {
+  #pragma unroll
+          for (int part = 0; part < 2; ++part) {
+            if (part == 1 && lane >= 8) continue;
+            *reinterpret_cast<uint2*>(a.cache + own_slot * 576 + 8 * (lane + 64 * part)) =
+                make_uint2(own_q[2 * part], own_q[2 * part + 1]);
+          }
+          if (lane == 0) a.row_scale[own_slot] = own_s;
+        } else {
+          // the packed row is sm_own's first 640 bytes
+          uint8_t* dst = a.cache + own_slot * 640;
+          *reinterpret_cast<uint2*>(dst + 8 * lane) = *reinterpret_cast<const uint2*>(&sm_own[8 * lane]);
+          if (lane < 16) *reinterpret_cast<uint2*>(dst + 512 + 8 * lane) = *reinterpret_cast<const uint2*>(&sm_own[512 + 8 * lane]);
         }
       }
       // The own row as key 0 of a one-key tile whose 16 rows all read sm_own (row stride 0; the other keys masked).
@@ -1292,29 +1316,14 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
                            reinterpret_cast<float2*>(&sm_ring[0][0][0]));
       __syncthreads();
     }
-    // ---- the own row's pool store, last: no store sits among the DMAs in flight, and none delays the partial's
-    // publication (nothing in the launch reads the slot: a gather of it takes the packed source row) ----
-    if (own_wave && own_slot >= 0) {
-      if constexpr (BF16) {
-        uint8_t* dst = a.cache + own_slot * 1152;
-        *reinterpret_cast<uint4*>(dst + 16 * lane) = own0;
-        if (lane < 8) *reinterpret_cast<uint4*>(dst + 16 * (lane + 64)) = own1;
-      } else if constexpr (FMT == ROWS576) {
-#pragma unroll
-        for (int part = 0; part < 2; ++part) {
-          if (part == 1 && lane >= 8) continue;
-          *reinterpret_cast<uint2*>(a.cache + own_slot * 576 + 8 * (lane + 64 * part)) =
-              make_uint2(own_q[2 * part], own_q[2 * part + 1]);
-        }
-        if (lane == 0) a.row_scale[own_slot] = own_s;
-      } else {
-        // the packed row is sm_own's first 640 bytes
-        uint8_t* dst = a.cache + own_slot * 640;
-        *reinterpret_cast<uint2*>(dst + 8 * lane) = *reinterpret_cast<const uint2*>(&sm_own[8 * lane]);
-        if (lane < 16) *reinterpret_cast<uint2*>(dst + 512 + 8 * lane) = *reinterpret_cast<const uint2*>(&sm_own[512 + 8 * lane]);
-      }
+    // ---- the sparse format's own row store (the paged formats store theirs before the tile loop); nothing in the
+    // launch reads the slot: a gather of it takes the packed source row ----
+    if (SPARSE && own_wave && own_slot >= 0) {
+      // the packed row is sm_own's first 640 bytes
+      uint8_t* dst = a.cache + own_slot * 640;
+      *reinterpret_cast<uint2*>(dst + 8 * lane) = *reinterpret_cast<const uint2*>(&sm_own[8 * lane]);
+      if (lane < 16) *reinterpret_cast<uint2*>(dst + 512 + 8 * lane) = *reinterpret_cast<const uint2*>(&sm_own[512 + 8 * lane]);
     }
-
     g = s_hi;
     row_t0 = row_t1;
     if constexpr (!MULTI) break;

@@ -8,16 +8,47 @@ quantization as the MHA store."""
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 from torch import Tensor
 
 from . import store
 
 
+def sum_of_squares(x32: Tensor) -> Tensor:
+    """The fp32 sum of x32^2 over the last dim (a multiple of 8) in one fixed order: each square rounded (pow(2)),
+    each run of 8 consecutive squares summed in sequence, then the runs folded in halves (the second half added onto
+    the first) until one is left. The reference's mean leaves this order to its backend (torch's CPU reduction, the
+    Neuron compiler), where a different order can move a normed value by one bf16 step; this is the order the HIP
+    writer's lanes reduce in, so its stores can be compared bit for bit."""
+    sq = x32 * x32
+    runs = sq.reshape(*sq.shape[:-1], -1, 8)
+    acc = runs[..., 0]
+    for e in range(1, 8):
+        acc = acc + runs[..., e]
+    while acc.shape[-1] > 1:
+        h = acc.shape[-1] // 2
+        acc = acc[..., :h] + acc[..., h:]
+    return acc
+
+
+def recip_sqrt(v: Tensor) -> Tensor:
+    """1 / sqrt(v) for float32 v (>= 0), the square root and the reciprocal each rounded to the nearest float32: each
+    is computed in float64 (numpy, the hardware's IEEE sqrt and divide) and rounded once to float32, which gives the
+    correctly rounded float32 result for both operations (53 >= 2 * 24 + 2 bits). torch's float32 CPU sqrt and
+    reciprocal are not correctly rounded on every host (two x86 hosts here disagree by one ulp on a fifth of the
+    values), so the oracle does not use them."""
+    a = v.detach().cpu().contiguous().numpy().astype(np.float64)
+    s = np.sqrt(a).astype(np.float32).astype(np.float64)
+    return torch.from_numpy((1.0 / s).astype(np.float32)).to(v.device)
+
+
 def rms(x: Tensor, gamma: Tensor, eps: float) -> Tensor:
-    """_rms (qkv_paged.py:40-42): gamma * (x32 * rsqrt(mean(x32^2) + eps)).to(x.dtype)."""
+    """_rms (qkv_paged.py:40-42): gamma * (x32 * rsqrt(mean(x32^2) + eps)).to(x.dtype), the mean as the sum of
+    squares (sum_of_squares) over d, rsqrt as 1 / sqrt (recip_sqrt: each correctly rounded)."""
     x32 = x.float()
-    return gamma.reshape(-1) * (x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype)
+    mean = sum_of_squares(x32) / x32.shape[-1]
+    return gamma.reshape(-1) * (x32 * recip_sqrt(mean + eps)).to(x.dtype)
 
 
 def rope(t: Tensor, c: Tensor, s: Tensor) -> Tensor:

@@ -29,7 +29,9 @@ __device__ __forceinline__ uint32_t partner(uint32_t v) {
   else return (uint32_t)__shfl_xor((int)v, HALF, 64);
 }
 
-// The sum over the head's lane group, in every lane of it: DPP row rotations for a 16-lane group, xor shuffles else.
+// The sum over the head's lane group, in every lane of it, folded in halves: lane i adds the lane HALF away, then
+// HALF / 2, ..., 1 (every lane ends with the same bits, addition being commutative). DPP row rotations for a
+// 16-lane group (rotations by 8, 4, 2, 1 pair the same lanes there), xor shuffles else.
 template <int HALF>
 __device__ __forceinline__ float group_sum(float v) {
   if constexpr (HALF == 8) {
@@ -87,14 +89,18 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
       for (int e = 0; e < 8; ++e) x[e] = bf16_bits_to_f32((ww[e >> 1] >> (16 * (e & 1))) & 0xffffu);
     }
     if (q_norm) {  // uniform: both gammas or neither
-      // _rms: gamma * (x32 * rsqrt(mean(x32^2) + eps)).to(bf16), rsqrt as 1 / sqrt (both correctly rounded); the
-      // sum of squares over the head's LPH lanes (every lane takes part in the shuffles)
+      // _rms: gamma * (x32 * rsqrt(mean(x32^2) + eps)).to(bf16), rsqrt as 1 / sqrt (both correctly rounded). The
+      // sum of squares: each square rounded (pow(2)), a lane's 8 summed in sequence, then the head's LPH lane sums
+      // folded in halves (group_sum; every lane takes part in the shuffles)
       float ss = 0.0f;
+      {
+#pragma clang fp contract(off)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+        for (int e = 0; e < 8; ++e) ss = ss + x[e] * x[e];
+      }
       ss = group_sum<HALF>(ss);
       if (live && (is_q || is_k)) {
-        const float inv = 1.0f / __fsqrt_rn(ss / (float)D + eps);
+        const float inv = 1.0f / sqrtf(ss / (float)D + eps);  // sqrtf: correctly rounded (__fsqrt_rn is the native one)
         const uint4 gw = ld16((is_q ? q_norm : k_norm) + 8 * sub);
         const uint32_t gg[4] = {gw.x, gw.y, gw.z, gw.w};
 #pragma unroll

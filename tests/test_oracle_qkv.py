@@ -78,3 +78,49 @@ def test_writer_stores_the_rotated_k_and_the_raw_v():
         assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
         # out-of-pool slots (-1, 5000) went to slot 0, the reserved page
         assert bool((kc[0, :, 0] != 0).any())
+
+
+def test_sum_of_squares_order_is_a_full_sum():
+    """The oracle's fixed-order fp32 sum of squares against a float64 sum of the same squares: within the bound any
+    summation order of d fp32 terms keeps (a dropped, doubled or misindexed term is off by far more); on small
+    integers, where every partial sum is exact in fp32, equal to torch's own reduction."""
+    g = torch.Generator().manual_seed(5)
+    for d in (64, 128):
+        x = torch.randn(7, 3, d, generator=g).to(torch.bfloat16).float()
+        got = oqkv.sum_of_squares(x)[..., 0].double()
+        want = (x.double() ** 2).sum(-1)
+        assert bool(((got - want).abs() <= d * 2.0 ** -23 * want).all()), d
+        ints = torch.randint(-40, 41, (5, 2, d), generator=g).float()
+        assert torch.equal(oqkv.sum_of_squares(ints)[..., 0], ints.pow(2).sum(-1))
+        # a term placed by hand: only element j is non-zero
+        for j in (0, 7, 8, d // 2, d - 1):
+            e = torch.zeros(1, d)
+            e[0, j] = 3.0
+            assert float(oqkv.sum_of_squares(e)) == 9.0, j
+
+
+def test_recip_sqrt_rounds_each_step_to_the_nearest_float32():
+    """recip_sqrt's square root is the float32 nearest the exact root and its reciprocal the float32 nearest the exact
+    1 / root: checked with exact rationals (Fraction) against both float32 neighbours, on random positive values
+    across exponents and on exact squares."""
+    from fractions import Fraction
+
+    import numpy as np
+
+    g = torch.Generator().manual_seed(11)
+    v = torch.exp(torch.randn(400, generator=g) * 4.0)
+    v = torch.cat([v, torch.tensor([1.0, 4.0, 0.25, 2.0 ** -20, 3.0, 1e-6])])
+    got = oqkv.recip_sqrt(v)
+    for vi, ri in zip(v.tolist(), got.tolist()):
+        a = Fraction(vi)
+        r = np.float32(ri)
+        # a candidate root (a float32 near sqrt(a)), shown to be the nearest: a lies on its side of the squared
+        # midpoint towards each float32 neighbour
+        root = np.float32(np.sqrt(np.float64(vi)))
+        for cand in (np.nextafter(root, np.float32(0)), np.nextafter(root, np.float32(np.inf))):
+            mid = (Fraction(float(cand)) + Fraction(float(root))) / 2
+            assert (a - mid * mid) * (Fraction(float(root)) - mid) >= 0, (vi, float(root), float(cand))
+        # r is the float32 nearest 1 / root
+        rr = 1 / Fraction(float(root))
+        for cand in (np.nextafter(r, np.float32(0)), np.nextafter(r, np.float32(np.inf))):
+            assert abs(Fraction(float(r)) - rr) <= abs(Fraction(float(cand)) - rr), (vi, ri)

@@ -189,12 +189,15 @@ def setup_gqa(cfg: int, window: int, dev):
     plan = ops.plan_decode(0, case.B, host_seq_lens=case.seq_lens, window=case.window, ctas_per_item=case.G,
                            num_cus=ops._num_cus(q.device))
     out = torch.empty(case.B, case.H, case.d, dtype=torch.bfloat16, device=dev)
+    mul = case.scales_multiply
     steps = [ops.prepare_paged_decode_gqa(q, k, v, table, lens, kn, vn, sm_scale=case.sm_scale, k_scale=ks,
                                           v_scale=vs, sinks=sinks, window=case.window, new_slots=slots, out=out,
-                                          plan=plan) for (k, v) in pools]
-    legs = {"store": [functools.partial(ops.kv_store_mha, kn, vn, slots, k, v, ks, vs) for (k, v) in pools],
+                                          plan=plan, scales_multiply=mul) for (k, v) in pools]
+    legs = {"store": [functools.partial(ops.kv_store_mha, kn, vn, slots, k, v, ks, vs, scales_multiply=mul)
+                      for (k, v) in pools],
             "decode": [ops.prepare_paged_decode_gqa(q, k, v, table, lens, kn, vn, sm_scale=case.sm_scale, k_scale=ks,
-                                                    v_scale=vs, sinks=sinks, window=case.window, out=out, plan=plan)
+                                                    v_scale=vs, sinks=sinks, window=case.window, out=out, plan=plan,
+                                                    scales_multiply=mul)
                        for (k, v) in pools]}
     tiles = 0
     for L in case.seq_lens.tolist():
@@ -207,7 +210,8 @@ def setup_gqa(cfg: int, window: int, dev):
     name = {1: "qwen3-0.6b-gqa-bf16", 2: "qwen3-8b-gqa-fp8", 4: "gpt-oss-120b-share-fp8"}[cfg]
     desc = {"workload": f"cfg{cfg}{'-swa' + str(window) if window else ''}: {name}", "batch": case.B,
             "q_heads": case.H, "kv_heads": case.G, "head_dim": case.d, "page_size": case.P,
-            "kv_dtype": "fp8_e4m3fn per-KV-head scale" if case.fp8 else "bf16",
+            "kv_dtype": ("fp8_e4m3fn, the GPT-OSS decode write (bf16 product with the inverted bf16 scale)" if mul
+                         else "fp8_e4m3fn per-KV-head scale") if case.fp8 else "bf16",
             "seq_len": "4096" if cfg == 2 else f"U{list(workloads.GQA_CONFIGS[cfg]['lens'])}",
             "window": case.window or None, "sinks": case.sinks is not None, "pool_copies": n,
             "split_plan": {"split_tiles": plan.split_tiles, "n_work": plan.n_work}}
@@ -226,8 +230,8 @@ def setup_gqa(cfg: int, window: int, dev):
         def run(nrows):
             oatt.paged_decode_gqa(qc[:nrows], kcpu, vcpu, case.block_table[:nrows], case.seq_lens[:nrows],
                                   knc[:nrows], vnc[:nrows], sm_scale=case.sm_scale, k_scale=kss, v_scale=vss,
-                                  sinks=sk, window=case.window)
-            ost.kv_store_mha(knc[:nrows], vnc[:nrows], case.new_slots[:nrows], kcpu, vcpu, kss, vss)
+                                  sinks=sk, window=case.window, scales_multiply=mul)
+            ost.kv_store_mha(knc[:nrows], vnc[:nrows], case.new_slots[:nrows], kcpu, vcpu, kss, vss, mul)
 
         return _time_rows(run, case.B, budget_s)
 

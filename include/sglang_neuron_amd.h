@@ -20,7 +20,9 @@
  *     stored unpacked (fp8_packed_k = False; the reference's packed [.., page/2, d, 2] K is a Trainium-kernel
  *     layout, attention_decode.py:207-223).
  *   - FP8 is OCP e4m3fn. A stored value is e4m3fn_RNE(clamp(float(x) / s, -448, 448)), where s is the
- *     dequantization scale (swa_fused.py:73-75, qkv.py:69-70, mla_decode_attention_torch.py:216-220).
+ *     dequantization scale (swa_fused.py:73-75, qkv.py:69-70, mla_decode_attention_torch.py:216-220), or, for an MHA
+ *     cache of dtype SNA_DTYPE_FP8_E4M3FN_MUL, e4m3fn_RNE(clamp(bf16_RNE(x * m), -448, 448)) with the GPT-OSS
+ *     quantization multiplier m (attention_decode.py:259-260).
  */
 #ifndef SGLANG_NEURON_AMD_H_
 #define SGLANG_NEURON_AMD_H_
@@ -38,9 +40,20 @@ extern "C" {
 #define SNA_ERR_LAUNCH (-3)           /* the HIP runtime refused a launch */
 #define SNA_ERR_UNSUPPORTED (-4)      /* a dtype or head layout this build has no kernel for */
 
-/* ---- dtypes of cache storage ---- */
+/* ---- dtypes of cache storage ----
+ * SNA_DTYPE_FP8_E4M3FN and SNA_DTYPE_FP8_E4M3FN_MUL caches hold the same e4m3fn bytes; they differ in what the scale
+ * arrays hold and so in how a store rounds:
+ *   FP8_E4M3FN      scale = s, the dequantization scale: byte = e4m3fn_RNE(clamp(float(x) / s, +-448)) (the divide of
+ *                   qkv.py:69-70 and swa_fused.py:73-75); value = float(byte) * s.
+ *   FP8_E4M3FN_MUL  scale = m, the reference's GPT-OSS k_scale / v_scale: the inverted checkpoint scale as a bf16 value
+ *                   (gpt_oss/mxfp4/common.py:481-485, 1 / bf16(s) rounded to bf16): byte =
+ *                   e4m3fn_RNE(clamp(bf16_RNE(x * m), +-448)) (the decode write of attention_decode.py:259-260, a
+ *                   product of two bf16 tensors); value = float(byte) / m (the dequantization the model folds into the
+ *                   softmax scale and the output projection, gpt_oss/mxfp4/model_decode.py:62-70).
+ * The two give different bytes unless m and 1 / s are powers of two. */
 #define SNA_DTYPE_BF16 0
 #define SNA_DTYPE_FP8_E4M3FN 1
+#define SNA_DTYPE_FP8_E4M3FN_MUL 2
 
 /* Library ABI version (major * 100 + minor). */
 int sna_version(void);
@@ -58,11 +71,14 @@ const char *sna_last_error(void);
  *   slots       [n_tokens] int64 token slots. A slot < 0 or >= num_blocks * page_size is written to slot 0, the
  *               reserved padding page (attention_decode.py:288-291; transformer/model.py:99-102).
  *   k_scale, v_scale
- *               [num_kv_heads] fp32 dequantization scales. Required for an FP8 cache and ignored for bf16.
+ *               [num_kv_heads] fp32: the dequantization scales s (SNA_DTYPE_FP8_E4M3FN) or the quantization
+ *               multipliers m (SNA_DTYPE_FP8_E4M3FN_MUL). Required for an FP8 cache and ignored for bf16.
  *   k_cache, v_cache
  *               [num_blocks, num_kv_heads, page_size, head_dim], of dtype cache_dtype.
- * FP8 cache: byte = e4m3fn_RNE(clamp(float(x) / scale[h], +-448)), bit-exact with the reference's quantize-then-cast
- * (attention_decode.py:259-260, qkv.py:69-79). bf16 cache: a copy (attention_decode_paged.py:174-176).
+ * FP8_E4M3FN: byte = e4m3fn_RNE(clamp(float(x) / s[h], +-448)), bit-exact with the reference's divide-and-clamp
+ * (qkv.py:69-79, swa_fused.py:73-75). FP8_E4M3FN_MUL: byte = e4m3fn_RNE(clamp(bf16_RNE(x * m[h]), +-448)), bit-exact
+ * with the GPT-OSS decode write (attention_decode.py:259-260, 288-300). bf16 cache: a copy
+ * (attention_decode_paged.py:174-176).
  * Replaces: the pool write that the reference's compiled graphs do. The reference pool's own set_kv_buffer refuses
  * (mem_cache/memory_pool.py:178-179); this is upstream SGLang's
  * MHATokenToKVPool.set_kv_buffer(layer, loc, cache_k, cache_v, k_scale, v_scale) for this pool layout. */
@@ -81,10 +97,13 @@ int sna_kv_store_mha(const void *k, const void *v, const int64_t *slots, int64_t
  *   slots        [n_tokens] int64; out-of-pool or negative slots go to slot 0, as for sna_kv_store_mha.
  *   q_out        [n_tokens, num_q_heads, head_dim] bf16.
  *   k_cache, v_cache, k_scale, v_scale, num_blocks, page_size, cache_dtype
- *                as for sna_kv_store_mha (per-KV-head scales; one per-tensor scale is all heads alike).
+ *                as for sna_kv_store_mha (per-KV-head scales; one per-tensor scale is all heads alike), cache_dtype
+ *                SNA_DTYPE_BF16 or SNA_DTYPE_FP8_E4M3FN. The writer divides, as the reference's prefill writers do
+ *                (qkv.py:69-70); a GPT-OSS pool of multipliers m is written by passing SNA_DTYPE_FP8_E4M3FN with the
+ *                scales bf16(1 / m), as its prefill does (gpt_oss/mxfp4/model_prefill.py:41-43).
  * Every rounding of the reference's torch path is kept (bf16 norm output, bf16 gamma product, bf16 RoPE products and
- * sum); without QK norm the result is bit-exact with it. With QK norm the fp32 sum of squares runs in another order,
- * so a value may land one bf16 step away where that moves the sum's last bit.
+ * sum). The norm's fp32 sum of squares (the reference leaves its order to the backend) runs in a stated order: each
+ * square rounded, a lane's 8 in sequence, then the head's lane sums folded in halves; 1 / sqrt is correctly rounded.
  * Replaces: the torch writer of _torch_qkv_paged after its projection (ops/attention/qkv_paged.py:45-68: _rms, rope,
  * the cache writes) and of _torch_qkv (ops/attention/qkv.py:57-85: rope, the FP8 divide-and-clamp, the writes); the
  * projection itself (`hidden @ weights + bias`) is a plain GEMM left to the caller. */
@@ -200,16 +219,19 @@ int64_t sna_decode_workspace_bytes(const sna_split_plan *plan, int32_t num_q_hea
  *   seq_lens     [B] int64, prefix plus the new token: each in [1, INT32_MAX] (positions are int32 in the kernels).
  *   block_table  [B, table_stride] int32, table_width valid columns: a row's ceil(seq_len / page_size) pages must fit
  *                the table and name pages inside the pool [0, num_blocks) (a -1 inside a row would drop its keys).
- *   new_slots    [B] int64 or NULL: a live row's slot (one off the reserved page 0 and inside the pool; the others are
- *                padding writes, redirected to slot 0) sits at the row's position in its page, slot % page ==
- *                (seq_len - 1) % page, on the row's last page, and no two live rows share one.
+ *   new_slots    [B] int64 or NULL: a live row's slot lies inside the pool off the reserved page 0, at the row's
+ *                position in its page, slot % page == (seq_len - 1) % page, on the row's last page, and no two live
+ *                rows share one. A row that is not live is a padding row: its write is redirected to slot 0 and not
+ *                checked.
+ *   active       [B] int32 or NULL: 1 for a live row (the reference's active flags). NULL: a row is live unless it is
+ *                a padding row by its operands, its own token only (seq_len 1) written to page 0 or outside the pool.
  * Returns SNA_ERR_INVALID_ARGUMENT naming the first offending row. The decode entry points themselves check shapes
  * only (their operands are device memory).
- * Replaces: the refusals of decode_operands (attention/mla_operands.py:64-97: an int32 position bound, a slot that
- * disagrees with its position, a table too narrow for the row, two live rows sharing a write slot). */
+ * Replaces: the refusals of decode_operands (attention/mla_operands.py:54-97: an int32 position bound, a live row's
+ * slot that disagrees with its position, a table too narrow for the row, two live rows sharing a write slot). */
 int sna_check_decode_operands(const int64_t *seq_lens, const int32_t *block_table, int64_t table_stride,
-                              int32_t table_width, const int64_t *new_slots, int32_t B, int32_t page_size,
-                              int64_t num_blocks);
+                              int32_t table_width, const int64_t *new_slots, const int32_t *active, int32_t B,
+                              int32_t page_size, int64_t num_blocks);
 
 /* =====================================================================================================
  * Decode attention
@@ -220,14 +242,16 @@ int sna_check_decode_operands(const int64_t *seq_lens, const int32_t *block_tabl
  *   k_cache, v_cache
  *                [num_blocks, num_kv_heads, page_size, head_dim] of cache_dtype.
  *   k_scale, v_scale
- *                [num_kv_heads] fp32 dequantization scales (FP8 only; NULL for bf16).
+ *                [num_kv_heads] fp32, FP8 only (NULL for bf16): dequantization scales s (SNA_DTYPE_FP8_E4M3FN), or the
+ *                GPT-OSS quantization multipliers m (SNA_DTYPE_FP8_E4M3FN_MUL: a cached byte is worth byte / m, and the
+ *                step's token is stored and attended as the decode write of attention_decode.py:259-260 rounds it).
  *   block_table  [B, table_stride] int32, of which `table_width` columns are valid; -1 marks no page.
  *   seq_lens     [B] int32, prefix plus the new token (>= 1).
  *   k_new, v_new [B, num_kv_heads, head_dim] bf16: the step's token. With an FP8 cache it is attended as
  *                dequant(quant(x)), the value the store writes (attention_decode.py:259-269).
- *   new_slots    [B] int64 or NULL. If not NULL, the combine pass also stores k_new / v_new at these slots,
- *                bit-exact with sna_kv_store_mha. Positions < seq_len - 1 are read, so the store never races the
- *                reads.
+ *   new_slots    [B] int64 or NULL. If not NULL, the decode also stores k_new / v_new at these slots, bit-exact
+ *                with sna_kv_store_mha of the same cache_dtype. Positions < seq_len - 1 are read, so the store never
+ *                races the reads.
  *   sinks        [num_q_heads] fp32 or NULL. exp(sink_h - max) joins the softmax denominator
  *                (attention_decode.py:274-275).
  *   window       0 for full attention, or W > 0: keys at positions [seq_len - W, seq_len - 1], the new one
@@ -331,7 +355,9 @@ int sna_lse_combine(const float *o_parts, const float *lse_parts, int32_t n_part
  *                q_start[r] .. q_start[r + 1] - 1, its query i at position prior_lens[r] + i.
  *   k_cache, v_cache  one layer's pool [num_blocks, num_kv_heads, page_size, head_dim]: FP8 e4m3fn
  *                (kv_dtype SNA_DTYPE_FP8_E4M3FN) with per-KV-head dequantization scales k_scale / v_scale
- *                [num_kv_heads], or bf16 (SNA_DTYPE_BF16; the scales are not read and may be NULL).
+ *                [num_kv_heads], FP8 e4m3fn with GPT-OSS multipliers (SNA_DTYPE_FP8_E4M3FN_MUL: a byte is worth
+ *                byte / m, the dequantization model_prefill.py:103-108 folds into the softmax scale and the output),
+ *                or bf16 (SNA_DTYPE_BF16; the scales are not read and may be NULL).
  *   block_table  [R, table_width] int32 (row stride table_stride), -1 past a row's pages; keys on a -1 page are not
  *                attended.
  *   q_start      [R + 1] int32, prior_lens [R] int32 (device); max_q_len >= every request's chunk length.

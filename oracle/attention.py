@@ -19,18 +19,21 @@ from . import fp8
 from . import store as st
 
 
-def _dequant_cache(cache: Tensor, scale: Optional[Tensor], G: int) -> Tensor:
-    """A head-major cache [blocks, G, page, d] as float32 values (uint8 = FP8 bytes, times the per-head scale)."""
+def _dequant_cache(cache: Tensor, scale: Optional[Tensor], G: int, multiply: bool = False) -> Tensor:
+    """A head-major cache [blocks, G, page, d] as float32 values (uint8 = FP8 bytes, times the per-head dequantization
+    scale, or over the per-head GPT-OSS multiplier)."""
     if cache.dtype == torch.uint8:
-        return fp8.dequantize(cache, torch.as_tensor(scale, dtype=torch.float32).reshape(1, G, 1, 1))
+        sc = torch.as_tensor(scale, dtype=torch.float32).reshape(1, G, 1, 1)
+        return fp8.dequantize_mul(cache, sc) if multiply else fp8.dequantize(cache, sc)
     return cache.float()
 
 
 def paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: Tensor, seq_lens: Tensor,
                      k_new: Tensor, v_new: Tensor, *, sm_scale: float, k_scale=None, v_scale=None,
-                     sinks: Optional[Tensor] = None, window: int = 0) -> Tensor:
+                     sinks: Optional[Tensor] = None, window: int = 0, scales_multiply: bool = False) -> Tensor:
     """[B, H, d] bf16 GQA decode of q [B, H, d] over caches [blocks, G, page, d] (bf16, or uint8 FP8 bytes with
-    per-KV-head dequantization scales [G]).
+    per-KV-head dequantization scales [G], or with ``scales_multiply`` the GPT-OSS multipliers [G]: a byte is worth
+    byte / m and the new token is stored as fp8.quantize_mul writes it, attention_decode.py:259-260).
 
     Follows _torch_attention_decode_paged (attention_decode_paged.py:159-173) for the gather, visibility and GQA
     head mapping (q head h reads KV head h // group, :170), and _torch_attention_decode (attention_decode.py:259-276)
@@ -52,16 +55,20 @@ def paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: T
         tb = table[b]
         page_ok = (tb >= 0) & (tb < nb)
         rows = tb.clamp(min=0, max=nb - 1)
-        keys = _dequant_cache(k_cache[rows], k_scale, G).permute(1, 0, 2, 3).reshape(G, Wt * P, d)  # [G, W*P, d]
-        vals = _dequant_cache(v_cache[rows], v_scale, G).permute(1, 0, 2, 3).reshape(G, Wt * P, d)
+        keys = _dequant_cache(k_cache[rows], k_scale, G, scales_multiply).permute(1, 0, 2, 3).reshape(G, Wt * P, d)
+        vals = _dequant_cache(v_cache[rows], v_scale, G, scales_multiply).permute(1, 0, 2, 3).reshape(G, Wt * P, d)
         visible = page_ok.repeat_interleave(P) & (key_pos < L - 1)
         if window > 0:
             visible &= key_pos >= L - window
         if k_cache.dtype == torch.uint8:
             ks = torch.as_tensor(k_scale, dtype=torch.float32).reshape(G, 1)
             vs = torch.as_tensor(v_scale, dtype=torch.float32).reshape(G, 1)
-            kn = fp8.dequantize(fp8.quantize(k_new[b], ks), ks)
-            vn = fp8.dequantize(fp8.quantize(v_new[b], vs), vs)
+            if scales_multiply:
+                kn = fp8.dequantize_mul(fp8.quantize_mul(k_new[b], ks), ks)
+                vn = fp8.dequantize_mul(fp8.quantize_mul(v_new[b], vs), vs)
+            else:
+                kn = fp8.dequantize(fp8.quantize(k_new[b], ks), ks)
+                vn = fp8.dequantize(fp8.quantize(v_new[b], vs), vs)
         else:
             kn, vn = k_new[b].float(), v_new[b].float()
         keys = torch.cat([keys, kn.reshape(G, 1, d)], dim=1)
@@ -82,9 +89,10 @@ def paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: T
 
 def segmented_prefill(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: Tensor, q_start, prior_lens, *,
                       sm_scale: float, k_scale=None, v_scale=None, sinks: Optional[Tensor] = None,
-                      window: int = 0) -> Tensor:
+                      window: int = 0, scales_multiply: bool = False) -> Tensor:
     """[T, H, d] bf16 prefill attention of a chunk's queries q [T, H, d] over caches [blocks, G, page, d] (bf16, or
-    uint8 FP8 bytes with per-KV-head scales [G]) into which the chunk's own K/V were stored first. Request r owns rows
+    uint8 FP8 bytes with per-KV-head scales [G]: dequantization scales, or with ``scales_multiply`` GPT-OSS multipliers
+    m, a byte worth byte / m) into which the chunk's own K/V were stored first. Request r owns rows
     q_start[r] .. q_start[r + 1] of q, at positions prior_lens[r] + i, and table row r.
 
     Follows _torch_segmented_attention (ops/attention/attention_segmented_cte.py:50-75): keys are gathered through the
@@ -107,8 +115,10 @@ def segmented_prefill(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: 
         span = prior + S
         n_pages = -(-span // P)
         pages = block_table[r, :n_pages].to(torch.int64).clamp(min=0)
-        keys = _dequant_cache(k_cache[pages], k_scale, G).permute(1, 0, 2, 3).reshape(G, n_pages * P, d)[:, :span]
-        vals = _dequant_cache(v_cache[pages], v_scale, G).permute(1, 0, 2, 3).reshape(G, n_pages * P, d)[:, :span]
+        keys = _dequant_cache(k_cache[pages], k_scale, G, scales_multiply).permute(1, 0, 2, 3).reshape(
+            G, n_pages * P, d)[:, :span]
+        vals = _dequant_cache(v_cache[pages], v_scale, G, scales_multiply).permute(1, 0, 2, 3).reshape(
+            G, n_pages * P, d)[:, :span]
         q_pos = torch.arange(S).unsqueeze(1) + prior
         k_pos = torch.arange(span).unsqueeze(0)
         allowed = (k_pos < prior + S) & (k_pos <= q_pos)

@@ -22,6 +22,33 @@ def quantize(x: Tensor, scale) -> Tensor:
     return (x.float() / s).clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn).view(torch.uint8)
 
 
+def quantize_mul(x: Tensor, multiplier) -> Tensor:
+    """uint8 e4m3fn bytes of ``x`` stored by the GPT-OSS decode write with quantization multiplier ``multiplier``
+    (broadcastable; each a bf16 value): e4m3fn(clamp(bf16(bf16(x) * bf16(m)), -448, 448)).
+
+    Follows ``(k * k_scale).clamp(-FP8_CLAMP_MAX, FP8_CLAMP_MAX).to(torch.float8_e4m3fn)`` of _torch_attention_decode
+    (ops/attention/attention_decode.py:259-260): k is the bf16 step token and k_scale the bf16 inverted checkpoint scale
+    (models/gpt_oss/mxfp4/common.py:481-485), so the product is a bf16 tensor. A NaN element's byte is not fixed by
+    that formula: torch's bf16 product writes NaN as 0x7FC0 or as 0xFFFF depending on whether the element falls in its
+    vectorized loop, which casts to 0x7F or 0xFF. Here it is 0x7F, bf16's canonical NaN cast (the HIP store's too)."""
+    m = torch.as_tensor(multiplier, dtype=torch.float32).to(torch.bfloat16)
+    xb = x.to(torch.bfloat16)
+    q = (xb * m).clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn).view(torch.uint8)
+    return torch.where(torch.isnan(xb), torch.full_like(q, 0x7F), q)
+
+
+def dequantize_mul(b: Tensor, multiplier) -> Tensor:
+    """float32 values of e4m3fn bytes stored with quantization multiplier m: byte / m (the dequantization the GPT-OSS
+    model folds into its softmax scale and output projection, models/gpt_oss/mxfp4/model_decode.py:62-70)."""
+    return b.view(torch.float8_e4m3fn).float() / torch.as_tensor(multiplier, dtype=torch.float32)
+
+
+def inverted_scale(scale) -> Tensor:
+    """The GPT-OSS multiplier of a dequantization scale, as the reference's loader computes it: ``1.0 /
+    scale.to(bfloat16)``, a bf16 value, here as float32 (models/gpt_oss/mxfp4/common.py:481-485)."""
+    return (1.0 / torch.as_tensor(scale, dtype=torch.float32).to(torch.bfloat16)).float()
+
+
 def dequantize(b: Tensor, scale) -> Tensor:
     """float32 values of e4m3fn bytes times their dequantization scale."""
     return b.view(torch.float8_e4m3fn).float() * torch.as_tensor(scale, dtype=torch.float32)
@@ -79,6 +106,18 @@ def e4m3fn_rne_spec(x: np.ndarray) -> np.ndarray:
     code = np.where(np.isnan(x), 0x7F, code)
     sign = np.signbit(x).astype(np.int64) << 7
     return (code | sign).astype(np.uint8)
+
+
+def bf16_round_spec(x: np.ndarray) -> np.ndarray:
+    """float64 values of float64 ``x`` rounded to bf16's 8 significant bits, ties to even, by the significand (frexp):
+    a restatement independent of the binary32 bit layout. Exact for results in bf16's normal range; a magnitude that
+    rounds past bf16's largest finite value becomes infinite. (Results below 2^-126 keep 8 bits, as bf16 subnormals do
+    not; the e4m3fn cast sends every such value to a signed zero.)"""
+    x = np.asarray(x, dtype=np.float64)
+    mant, exp = np.frexp(x)
+    r = np.ldexp(np.rint(mant * 256.0) / 256.0, exp)
+    big = (2.0 - 2.0 ** -7) * 2.0 ** 127
+    return np.where(np.isfinite(x) & (np.abs(r) > big), np.copysign(np.inf, x), r)
 
 
 def bf16_rne_spec(x: np.ndarray) -> np.ndarray:

@@ -23,12 +23,13 @@ def redirect_slots(slots: Tensor, num_slots: int) -> Tensor:
 
 
 def kv_store_mha(k: Tensor, v: Tensor, slots: Tensor, k_cache: Tensor, v_cache: Tensor, k_scale=None,
-                 v_scale=None) -> None:
+                 v_scale=None, scales_multiply: bool = False) -> None:
     """Write k, v [T, G, d] (bf16) into caches [blocks, G, page, d] at (slot // page, head, slot % page).
 
     bf16 cache: a copy (ops/attention/attention_decode_paged.py:174-176, index_copy_ of the row).
-    uint8 (FP8) cache: quantize with the per-head scales [G], then index_put_ (attention_decode.py:259-260, 288-300;
-    the quantize is qkv.py:69-70's divide-and-clamp)."""
+    uint8 (FP8) cache: quantize with the per-head scales [G], then index_put_ (attention_decode.py:288-300). The
+    quantize is qkv.py:69-70's divide-and-clamp by dequantization scales, or, with ``scales_multiply``, the GPT-OSS
+    decode write by multipliers, e4m3fn(bf16(k * k_scale)) (attention_decode.py:259-260)."""
     nb, G, P, d = k_cache.shape
     T = k.shape[0]
     s = redirect_slots(slots, nb * P)
@@ -36,8 +37,9 @@ def kv_store_mha(k: Tensor, v: Tensor, slots: Tensor, k_cache: Tensor, v_cache: 
     if k_cache.dtype == torch.uint8:
         ks = torch.as_tensor(k_scale, dtype=torch.float32).reshape(1, G, 1)
         vs = torch.as_tensor(v_scale, dtype=torch.float32).reshape(1, G, 1)
-        kq = fp8.quantize(k.reshape(T, G, d), ks)
-        vq = fp8.quantize(v.reshape(T, G, d), vs)
+        quant = fp8.quantize_mul if scales_multiply else fp8.quantize
+        kq = quant(k.reshape(T, G, d), ks)
+        vq = quant(v.reshape(T, G, d), vs)
         k_cache.index_put_(index, kq.reshape(T * G, d))
         v_cache.index_put_(index, vq.reshape(T * G, d))
     else:

@@ -25,9 +25,12 @@ NOALLOC_SCRATCH_BYTES = 16 << 20  # SNA_NOALLOC_SCRATCH_BYTES
 
 DTYPE_BF16 = 0
 DTYPE_FP8_E4M3FN = 1
+DTYPE_FP8_E4M3FN_MUL = 2  # FP8 bytes; the scales are the GPT-OSS quantization multipliers (SNA_DTYPE_FP8_E4M3FN_MUL)
 
 MAX_CTAS = 256       # SNA_MAX_CTAS
 MAX_PLAN_ROWS = 256  # SNA_MAX_PLAN_ROWS
+STREAM_MAX_COUNTERS = 2047  # (row, head group) merge counters of one MLA / DSA launch
+SPARSE_MAX_RANGE_KEYS = 2048  # indices one DSA workgroup resolves
 
 KIND_GQA = 0
 KIND_MLA = 1
@@ -69,7 +72,7 @@ SIGNATURES = {
     "sna_kv_store_dsa": (_I32, [_P, _P, _I64, _F32, _P, _I64, _P]),
     "sna_plan_decode": (_I32, [_I32, _P, _I32, _I32, _I32, _I32, _I32, _I32, ctypes.POINTER(SplitPlan)]),
     "sna_decode_workspace_bytes": (_I64, [ctypes.POINTER(SplitPlan), _I32, _I32]),
-    "sna_check_decode_operands": (_I32, [_P, _P, _I64, _I32, _P, _I32, _I32, _I64]),
+    "sna_check_decode_operands": (_I32, [_P, _P, _I64, _I32, _P, _P, _I32, _I32, _I64]),
     "sna_paged_decode_gqa": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _I32, _F32, _P, _I32,
                                     _I32, _I32, _I32, _I32, _I64, _I32, ctypes.POINTER(SplitPlan), _P, _I64, _P]),
     "sna_paged_decode_gqa_noalloc": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _I32, _F32, _P,

@@ -266,12 +266,13 @@ class NeuronAttnBackend:
         if sinks is None:
             sinks = getattr(layer, "sinks", None)
         if save_kv_cache:
-            pool.set_kv_buffer(layer, st.slots, k.reshape(T, G, d), v.reshape(T, G, d))
+            pool.set_kv_buffer_prefill(layer, st.slots, k.reshape(T, G, d), v.reshape(T, G, d))
         k_cache, v_cache = pool.get_kv_buffer(layer_id)
         k_scale, v_scale = pool.get_kv_scales(layer_id)
         out = ops.prefill_attention(q.reshape(T, H, d), k_cache, v_cache, st.table, st.q_start, st.prior,
                                     max_q_len=st.max_q_len, sm_scale=float(layer.scaling), k_scale=k_scale,
-                                    v_scale=v_scale, sinks=sinks, window=window)
+                                    v_scale=v_scale, sinks=sinks, window=window,
+                                    scales_multiply=pool.kv_scales_inverted(layer_id))
         return out.reshape(T, H * d)
 
     def forward_decode(self, q: Tensor, k: Optional[Tensor], v: Optional[Tensor], layer, forward_batch,
@@ -324,7 +325,8 @@ class NeuronAttnBackend:
         out = ops.paged_decode_gqa(
             q.reshape(bs, H, d), k_cache, v_cache, st.table, st.seq_lens, k.reshape(bs, G, d), v.reshape(bs, G, d),
             sm_scale=float(layer.scaling), k_scale=k_scale if fp8 else None, v_scale=v_scale if fp8 else None,
-            sinks=sinks, window=window, new_slots=st.slots if save else None, plan=st.plans[key])
+            sinks=sinks, window=window, new_slots=st.slots if save else None, plan=st.plans[key],
+            scales_multiply=fp8 and pool.kv_scales_inverted(layer_id))
         return out.reshape(bs, H * d)
 
     def _decode_mla(self, q, k, layer, layer_id, st, bs, save):

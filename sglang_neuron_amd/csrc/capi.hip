@@ -38,9 +38,13 @@ int plan_stream(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32_t n
   if (kind == 1 && !host_seq_lens)
     return fail(SNA_ERR_INVALID_ARGUMENT, "plan_decode: an MLA plan needs host seq_lens (its launch uses them)");
   if (B > SNA_MAX_PLAN_ROWS)
-    return fail(SNA_ERR_UNSUPPORTED, "plan_decode: an MLA / DSA plan holds at most %d rows, not %d",
+    return fail(SNA_ERR_UNSUPPORTED, "plan_decode: an MLA / DSA plan holds at most %d rows, not %d (split the batch)",
                 SNA_MAX_PLAN_ROWS, B);
-  int64_t total = 0;
+  if ((int64_t)B * groups > kStreamMaxCounters)
+    return fail(SNA_ERR_UNSUPPORTED, "plan_decode: %d rows x %d head groups exceed the %d merge counters of a launch "
+                "(split the batch)", B, groups, kStreamMaxCounters);
+  constexpr int32_t kSparseCap = kMlaMaxSplitKeys / 16;  // a sparse range's tiles: its indices resolve in LDS
+  int64_t total = 0, min_pieces = 0;
   int32_t empty = 0, max_tiles = 0;
   for (int32_t b = 0; b < B; ++b) {
     const int32_t keys = kind == 2 ? n_keys_per_row : std::max(host_seq_lens[b] - 1, 0);
@@ -53,6 +57,7 @@ int plan_stream(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32_t n
                   keys);
     plan->row_keys[b] = keys;
     total += tiles;
+    min_pieces += kind == 2 ? (tiles + kSparseCap - 1) / kSparseCap : 1;
     empty += keys == 0;
     max_tiles = std::max(max_tiles, tiles);
   }
@@ -60,12 +65,16 @@ int plan_stream(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32_t n
   const int32_t cus = std::max(1, std::min((num_cus > 0 ? num_cus : 256) / groups, SNA_MAX_CTAS));
   int64_t n = 0;
   if (total > 0) {
-    constexpr int32_t kSparseCap = kMlaMaxSplitKeys / 16;
     n = kind == 1 ? std::min<int64_t>(cus, total) : std::min<int64_t>(cus, std::max<int64_t>((total + 7) / 8, 1));
-    if (kind == 2) n = std::max<int64_t>(n, (total + kSparseCap - 1) / kSparseCap);
+    // a sparse range holds at most kSparseCap tiles: equal ranges need ceil(total / cap) of them, and whole rows
+    // (when every row gets a workgroup) need each row's ceil(tiles / cap) pieces
+    if (kind == 2) {
+      n = std::max<int64_t>(n, (total + kSparseCap - 1) / kSparseCap);
+      if (B <= n) n = std::max<int64_t>(n, min_pieces);
+    }
     if (n > SNA_MAX_CTAS)
-      return fail(SNA_ERR_UNSUPPORTED, "plan_decode: %lld index tiles need more than %d workgroups of %d tiles",
-                  (long long)total, SNA_MAX_CTAS, kSparseCap);
+      return fail(SNA_ERR_UNSUPPORTED, "plan_decode: %lld index tiles of %d rows need more than %d workgroups of at "
+                  "most %d tiles (split the batch)", (long long)total, B, SNA_MAX_CTAS, kSparseCap);
   }
   // row r's first tile in the global sequence, for the ranges' starting rows
   std::vector<int64_t> first(B + 1, 0);
@@ -75,10 +84,17 @@ int plan_stream(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32_t n
   // spans two rows (a second row would restart the tile ring and publish a second partial) and the longest piece is
   // as short as whole pieces allow. With more rows than workgroups the sequence is cut into equal ranges.
   if (n > 0 && B <= n) {
+    // every row starts with its least piece count (1; a sparse row: enough pieces of at most kSparseCap tiles)
     std::vector<int32_t> pieces(B, 1);
+    int64_t given = 0;
     std::priority_queue<std::pair<double, int32_t>> longest;
-    for (int32_t b = 0; b < B; ++b) longest.push({(double)(first[b + 1] - first[b]), b});
-    for (int64_t left = n - B; left > 0 && !longest.empty(); --left) {
+    for (int32_t b = 0; b < B; ++b) {
+      const int64_t tiles = first[b + 1] - first[b];
+      if (kind == 2) pieces[b] = (int32_t)((tiles + kSparseCap - 1) / kSparseCap);
+      given += pieces[b];
+      longest.push({(double)tiles / pieces[b], b});
+    }
+    for (int64_t left = n - given; left > 0 && !longest.empty(); --left) {
       const int32_t b = longest.top().second;
       longest.pop();
       const int64_t tiles = first[b + 1] - first[b];
@@ -282,8 +298,8 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
 }
 
 int sna_check_decode_operands(const int64_t* seq_lens, const int32_t* block_table, int64_t table_stride,
-                              int32_t table_width, const int64_t* new_slots, int32_t B, int32_t page_size,
-                              int64_t num_blocks) {
+                              int32_t table_width, const int64_t* new_slots, const int32_t* active, int32_t B,
+                              int32_t page_size, int64_t num_blocks) {
   ApiGuard guard;
   if (B < 0 || page_size < 1 || num_blocks < 1 || table_width < 0 || table_stride < table_width)
     return fail(SNA_ERR_INVALID_ARGUMENT, "check_decode_operands: bad sizes (B %d, page %d, blocks %lld, table %d/%lld)",
@@ -292,6 +308,10 @@ int sna_check_decode_operands(const int64_t* seq_lens, const int32_t* block_tabl
   if (!seq_lens || (table_width > 0 && !block_table))
     return fail(SNA_ERR_INVALID_ARGUMENT, "check_decode_operands: null pointer");
   const int64_t pool_slots = num_blocks * page_size;
+  // A row is live by its flag; without flags, unless it is a padding row: its own token only (seq_len 1) written to
+  // the reserved page 0 or outside the pool (redirected to slot 0).
+  auto in_pool = [&](int64_t slot) { return slot >= page_size && slot < pool_slots; };
+  auto live = [&](int32_t b) { return active ? active[b] != 0 : (seq_lens[b] > 1 || in_pool(new_slots[b])); };
   for (int32_t b = 0; b < B; ++b) {
     const int64_t L = seq_lens[b];
     if (L < 1) return fail(SNA_ERR_INVALID_ARGUMENT, "row %d: seq_len %lld (a decode row holds at least its new token)",
@@ -309,10 +329,12 @@ int sna_check_decode_operands(const int64_t* seq_lens, const int32_t* block_tabl
         return fail(SNA_ERR_INVALID_ARGUMENT, "row %d: table column %lld holds page %d, outside the pool's %lld pages "
                     "(the row's pages must cover its %lld tokens)", b, (long long)j, row[j], (long long)num_blocks,
                     (long long)L);
-    if (!new_slots) continue;
+    if (!new_slots || !live(b)) continue;
     const int64_t slot = new_slots[b];
-    // a slot on the reserved page 0 or outside the pool is a padding row's write (redirected to slot 0)
-    if (slot < page_size || slot >= pool_slots) continue;
+    if (!in_pool(slot))
+      return fail(SNA_ERR_INVALID_ARGUMENT, "row %d: live row's new slot %lld is %s (the write would go to the reserved "
+                  "slot 0 and the token be lost)", b, (long long)slot,
+                  slot < 0 || slot >= pool_slots ? "outside the pool" : "on the reserved page 0");
     if (slot % page_size != (L - 1) % page_size)
       return fail(SNA_ERR_INVALID_ARGUMENT, "row %d: new slot %lld disagrees with position %lld (page %d)", b,
                   (long long)slot, (long long)(L - 1), page_size);
@@ -321,14 +343,14 @@ int sna_check_decode_operands(const int64_t* seq_lens, const int32_t* block_tabl
                   (long long)slot, (long long)(slot / page_size), row[(L - 1) / page_size]);
   }
   if (new_slots) {
-    std::vector<int64_t> live;
-    live.reserve(B);
+    std::vector<int64_t> written;
+    written.reserve(B);
     for (int32_t b = 0; b < B; ++b)
-      if (new_slots[b] >= page_size && new_slots[b] < pool_slots) live.push_back(new_slots[b]);
-    std::sort(live.begin(), live.end());
-    for (size_t i = 1; i < live.size(); ++i)
-      if (live[i] == live[i - 1])
-        return fail(SNA_ERR_INVALID_ARGUMENT, "two live decode rows write slot %lld", (long long)live[i]);
+      if (live(b)) written.push_back(new_slots[b]);
+    std::sort(written.begin(), written.end());
+    for (size_t i = 1; i < written.size(); ++i)
+      if (written[i] == written[i - 1])
+        return fail(SNA_ERR_INVALID_ARGUMENT, "two live decode rows write slot %lld", (long long)written[i]);
   }
   return SNA_OK;
 }

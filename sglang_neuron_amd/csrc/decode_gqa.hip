@@ -36,8 +36,9 @@ struct GqaArgs {
   const uint16_t* q;
   uint8_t* k_cache;
   uint8_t* v_cache;
-  const float* k_scale;
+  const float* k_scale;  // FP8: dequantization scales s, or (mul_scale) the GPT-OSS quantization multipliers m
   const float* v_scale;
+  bool mul_scale;        // SNA_DTYPE_FP8_E4M3FN_MUL: a cached byte is worth byte / m; the own token stores bf16(x m)
   const int32_t* table;
   int64_t table_stride;
   int32_t table_width;
@@ -158,8 +159,11 @@ void gqa_decode_kernel(GqaArgs a) {
     }
   }
 
-  const float kscale = FP8 ? a.k_scale[g] : 1.0f;
-  const float vscale = FP8 ? a.v_scale[g] : 1.0f;
+  // the stored scales, and the dequantization scales they give (m -> 1 / m for the GPT-OSS multipliers)
+  const float kstored = FP8 ? a.k_scale[g] : 1.0f;
+  const float vstored = FP8 ? a.v_scale[g] : 1.0f;
+  const float kscale = (FP8 && a.mul_scale) ? 1.0f / kstored : kstored;
+  const float vscale = (FP8 && a.mul_scale) ? 1.0f / vstored : vstored;
   // the group's sink logits (final outputs only), loaded with the prologue's loads: read after the tile loop, a load
   // there would add a memory round trip to the end of every workgroup
   const float sink_pre = (FINAL && a.sinks && tid < a.group) ? a.sinks[g * a.group + tid] : 0.0f;
@@ -367,7 +371,8 @@ void gqa_decode_kernel(GqaArgs a) {
       const int64_t dst = own_dst;
       float kd, vd;
       if constexpr (FP8) {
-        const uint32_t kq = quantize_e4m3fn(kb, kscale), vq = quantize_e4m3fn(vb, vscale);
+        const uint32_t kq = a.mul_scale ? quantize_e4m3fn_mul(kb, kstored) : quantize_e4m3fn(kb, kscale);
+        const uint32_t vq = a.mul_scale ? quantize_e4m3fn_mul(vb, vstored) : quantize_e4m3fn(vb, vscale);
         kd = e4m3fn_to_f32(kq) * kscale;
         vd = e4m3fn_to_f32(vq) * vscale;
         if (dst >= 0) {
@@ -509,7 +514,9 @@ __global__ __launch_bounds__(128) void gqa_lone_token_kernel(GqaArgs a) {
   const int b = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
   if (launched_splits(a, b, a.seq_lens[b]) > 0) return;
   __shared__ float sm_kn[D], sm_vn[D];
-  const float kscale = FP8 ? a.k_scale[g] : 1.0f, vscale = FP8 ? a.v_scale[g] : 1.0f;
+  const float kstored = FP8 ? a.k_scale[g] : 1.0f, vstored = FP8 ? a.v_scale[g] : 1.0f;
+  const float kscale = (FP8 && a.mul_scale) ? 1.0f / kstored : kstored;
+  const float vscale = (FP8 && a.mul_scale) ? 1.0f / vstored : vstored;
   if (tid < D) {
     const int64_t src = ((int64_t)b * a.G + g) * D + tid;
     const uint32_t kb = a.k_new[src], vb = a.v_new[src];
@@ -519,7 +526,8 @@ __global__ __launch_bounds__(128) void gqa_lone_token_kernel(GqaArgs a) {
       dst = (((slot / a.P) * a.G + g) * a.P + slot % a.P) * D + tid;
     }
     if constexpr (FP8) {
-      const uint32_t kq = quantize_e4m3fn(kb, kscale), vq = quantize_e4m3fn(vb, vscale);
+      const uint32_t kq = a.mul_scale ? quantize_e4m3fn_mul(kb, kstored) : quantize_e4m3fn(kb, kscale);
+      const uint32_t vq = a.mul_scale ? quantize_e4m3fn_mul(vb, vstored) : quantize_e4m3fn(vb, vscale);
       sm_kn[tid] = e4m3fn_to_f32(kq) * kscale;
       sm_vn[tid] = e4m3fn_to_f32(vq) * vscale;
       if (dst >= 0) {
@@ -596,7 +604,7 @@ int decode_gqa(const char* what, const void* q, const void* k_cache, const void*
     return fail(SNA_ERR_UNSUPPORTED, "%s: head_dim %d (64 or 128 are built)", what, head_dim);
   if (page_size < 16 || page_size % 16)
     return fail(SNA_ERR_UNSUPPORTED, "%s: page_size %d (a multiple of 16 is required)", what, page_size);
-  if (cache_dtype != SNA_DTYPE_BF16 && cache_dtype != SNA_DTYPE_FP8_E4M3FN)
+  if (cache_dtype != SNA_DTYPE_BF16 && cache_dtype != SNA_DTYPE_FP8_E4M3FN && cache_dtype != SNA_DTYPE_FP8_E4M3FN_MUL)
     return fail(SNA_ERR_INVALID_ARGUMENT, "%s: unknown cache dtype %d", what, cache_dtype);
   if (window < 0 || table_width < 0 || table_stride < table_width || num_blocks < 1 || !(sm_scale > 0.0f))
     return fail(SNA_ERR_INVALID_ARGUMENT, "%s: bad window %d, table %d/%lld, blocks %lld or scale %g", what, window,
@@ -607,7 +615,7 @@ int decode_gqa(const char* what, const void* q, const void* k_cache, const void*
                 plan ? plan->batch : -1);
   if (const int rc = check_work_map(plan, B, what)) return rc;
   if (B == 0) return SNA_OK;
-  const bool fp8 = cache_dtype == SNA_DTYPE_FP8_E4M3FN;
+  const bool fp8 = cache_dtype != SNA_DTYPE_BF16;
   const int64_t need = sna_decode_workspace_bytes(plan, num_q_heads, head_dim);
   if (!q || !k_cache || !v_cache || !block_table || !seq_lens || !k_new || !v_new || !out ||
       (fp8 && (!k_scale || !v_scale)) || (need > 0 && !workspace))
@@ -625,6 +633,7 @@ int decode_gqa(const char* what, const void* q, const void* k_cache, const void*
   a.v_cache = (uint8_t*)v_cache;
   a.k_scale = k_scale;
   a.v_scale = v_scale;
+  a.mul_scale = cache_dtype == SNA_DTYPE_FP8_E4M3FN_MUL;
   a.table = block_table;
   a.table_stride = table_stride;
   a.table_width = table_width;

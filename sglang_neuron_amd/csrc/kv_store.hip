@@ -8,9 +8,13 @@
 namespace sna {
 
 // ---------------------------------------------------------------------------------------------------------------
-// MHA store. Thread = 8 consecutive elements of one (token, head) row of K and of V.
+// MHA store. Thread = 8 consecutive elements of one (token, head) row of K and of V. MODE: kStoreBf16 (a copy),
+// kStoreDiv (e4m3fn of x / s, s the dequantization scale) or kStoreMul (e4m3fn of bf16(x * m), m the reference's
+// GPT-OSS quantization multiplier).
 // ---------------------------------------------------------------------------------------------------------------
-template <bool FP8>
+constexpr int kStoreBf16 = 0, kStoreDiv = 1, kStoreMul = 2;
+
+template <int MODE>
 __global__ __launch_bounds__(256) void kv_store_mha_kernel(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                                                            const int64_t* __restrict__ slots, int64_t n_tokens,
                                                            const float* __restrict__ k_scale,
@@ -31,12 +35,20 @@ __global__ __launch_bounds__(256) void kv_store_mha_kernel(const uint16_t* __res
   const int64_t src_elem = th * D + (int64_t)c * 8;
   const uint4 kin = ld16(k + src_elem);
   const uint4 vin = ld16(v + src_elem);
-  if constexpr (FP8) {
+  if constexpr (MODE != kStoreBf16) {
     const float ks = k_scale[h], vs = v_scale[h];
     const uint32_t kw[4] = {kin.x, kin.y, kin.z, kin.w};
     const uint32_t vw[4] = {vin.x, vin.y, vin.z, vin.w};
     uint32_t ko[2] = {0, 0}, vo[2] = {0, 0};
-    if (rcp_scale_ok(ks) && rcp_scale_ok(vs)) {
+    if constexpr (MODE == kStoreMul) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t kb = (kw[i >> 1] >> ((i & 1) * 16)) & 0xffffu;
+        const uint32_t vb = (vw[i >> 1] >> ((i & 1) * 16)) & 0xffffu;
+        ko[i >> 2] |= quantize_e4m3fn_mul(kb, ks) << ((i & 3) * 8);
+        vo[i >> 2] |= quantize_e4m3fn_mul(vb, vs) << ((i & 3) * 8);
+      }
+    } else if (rcp_scale_ok(ks) && rcp_scale_ok(vs)) {
       const float rks = 1.0f / ks, rvs = 1.0f / vs;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -222,12 +234,12 @@ int sna_kv_store_mha(const void* k, const void* v, const int64_t* slots, int64_t
     return fail(SNA_ERR_INVALID_ARGUMENT, "kv_store_mha: bad sizes (n_tokens %lld, blocks %lld, heads %d, page %d, "
                 "head_dim %d; head_dim must be a multiple of 8)", (long long)n_tokens, (long long)num_blocks,
                 num_kv_heads, page_size, head_dim);
-  if (cache_dtype != SNA_DTYPE_BF16 && cache_dtype != SNA_DTYPE_FP8_E4M3FN)
+  if (cache_dtype != SNA_DTYPE_BF16 && cache_dtype != SNA_DTYPE_FP8_E4M3FN && cache_dtype != SNA_DTYPE_FP8_E4M3FN_MUL)
     return fail(SNA_ERR_INVALID_ARGUMENT, "kv_store_mha: unknown cache dtype %d", cache_dtype);
   if (n_tokens == 0) return SNA_OK;
   if (!k || !v || !slots || !k_cache || !v_cache)
     return fail(SNA_ERR_INVALID_ARGUMENT, "kv_store_mha: null pointer");
-  const bool fp8 = cache_dtype == SNA_DTYPE_FP8_E4M3FN;
+  const bool fp8 = cache_dtype != SNA_DTYPE_BF16;
   if (fp8 && (!k_scale || !v_scale)) return fail(SNA_ERR_INVALID_ARGUMENT, "kv_store_mha: FP8 cache needs k/v scales");
   if (!aligned(k, 16) || !aligned(v, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
     return fail(SNA_ERR_INVALID_ARGUMENT, "kv_store_mha: pointers must be 16-byte aligned");
@@ -235,14 +247,11 @@ int sna_kv_store_mha(const void* k, const void* v, const int64_t* slots, int64_t
   const dim3 grid((unsigned)((total + 255) / 256));
   hipStream_t s = (hipStream_t)stream;
   const int64_t num_slots = num_blocks * page_size;
-  if (fp8)
-    hipLaunchKernelGGL(kv_store_mha_kernel<true>, grid, dim3(256), 0, s, (const uint16_t*)k, (const uint16_t*)v, slots,
-                       n_tokens, k_scale, v_scale, (uint8_t*)k_cache, (uint8_t*)v_cache, num_slots, num_kv_heads,
-                       page_size, head_dim);
-  else
-    hipLaunchKernelGGL(kv_store_mha_kernel<false>, grid, dim3(256), 0, s, (const uint16_t*)k, (const uint16_t*)v,
-                       slots, n_tokens, k_scale, v_scale, (uint8_t*)k_cache, (uint8_t*)v_cache, num_slots,
-                       num_kv_heads, page_size, head_dim);
+  auto kernel = cache_dtype == SNA_DTYPE_FP8_E4M3FN_MUL ? kv_store_mha_kernel<kStoreMul>
+                : cache_dtype == SNA_DTYPE_FP8_E4M3FN   ? kv_store_mha_kernel<kStoreDiv>
+                                                        : kv_store_mha_kernel<kStoreBf16>;
+  hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, (const uint16_t*)k, (const uint16_t*)v, slots, n_tokens, k_scale,
+                     v_scale, (uint8_t*)k_cache, (uint8_t*)v_cache, num_slots, num_kv_heads, page_size, head_dim);
   return check_launch("kv_store_mha");
 }
 

@@ -32,8 +32,9 @@ struct PrefillArgs {
   const uint16_t* q;       // [T, H, D] bf16
   const uint8_t* k_cache;  // [num_blocks, G, P, D] e4m3fn
   const uint8_t* v_cache;
-  const float* k_scale;  // [G] dequantization scales
+  const float* k_scale;  // [G] dequantization scales, or (mul_scale) GPT-OSS multipliers m: a byte is worth byte / m
   const float* v_scale;
+  bool mul_scale;
   const int32_t* table;  // [R, table_width] (row stride table_stride)
   int64_t table_stride;
   int32_t table_width;
@@ -161,8 +162,9 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
       qlo[n][k] = pack_e4m3fn_x4(l4[0], l4[1], l4[2], l4[3]);
     }
   }
-  const float qk_scale = a.sm_scale * kLog2e * (ESZ == 1 ? a.k_scale[g] : 1.0f);
-  const float v_scale = ESZ == 1 ? a.v_scale[g] : 1.0f;
+  const float k_deq = ESZ == 1 ? (a.mul_scale ? 1.0f / a.k_scale[g] : a.k_scale[g]) : 1.0f;
+  const float qk_scale = a.sm_scale * kLog2e * k_deq;
+  const float v_scale = ESZ == 1 ? (a.mul_scale ? 1.0f / a.v_scale[g] : a.v_scale[g]) : 1.0f;
 
   float m_ref[2] = {kNegBig, kNegBig}, l_run[2] = {0.0f, 0.0f};
   f32x4_t acc[2][NC];
@@ -469,10 +471,10 @@ extern "C" int sna_prefill_attention(const void* q, const void* k_cache, const v
     return fail(SNA_ERR_UNSUPPORTED, "prefill_attention: head_dim %d (64 or 128)", head_dim);
   if (page_size < 16 || page_size % 16 != 0)
     return fail(SNA_ERR_UNSUPPORTED, "prefill_attention: page_size %d (a multiple of 16)", page_size);
-  if (kv_dtype != SNA_DTYPE_FP8_E4M3FN && kv_dtype != SNA_DTYPE_BF16)
+  if (kv_dtype != SNA_DTYPE_FP8_E4M3FN && kv_dtype != SNA_DTYPE_FP8_E4M3FN_MUL && kv_dtype != SNA_DTYPE_BF16)
     return fail(SNA_ERR_UNSUPPORTED, "prefill_attention: KV dtype %d (FP8 e4m3fn or bf16)", kv_dtype);
   if (R == 0 || max_q_len == 0) return SNA_OK;
-  if (!q || !k_cache || !v_cache || (kv_dtype == SNA_DTYPE_FP8_E4M3FN && (!k_scale || !v_scale)) || !block_table ||
+  if (!q || !k_cache || !v_cache || (kv_dtype != SNA_DTYPE_BF16 && (!k_scale || !v_scale)) || !block_table ||
       !q_start || !prior_lens || !out)
     return fail(SNA_ERR_INVALID_ARGUMENT, "prefill_attention: null pointer");
   if (!aligned(q, 16) || !aligned(out, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
@@ -486,6 +488,7 @@ extern "C" int sna_prefill_attention(const void* q, const void* k_cache, const v
   a.v_cache = (const uint8_t*)v_cache;
   a.k_scale = k_scale;
   a.v_scale = v_scale;
+  a.mul_scale = kv_dtype == SNA_DTYPE_FP8_E4M3FN_MUL;
   a.table = block_table;
   a.table_stride = table_stride;
   a.table_width = table_width;

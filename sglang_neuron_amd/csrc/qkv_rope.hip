@@ -206,6 +206,10 @@ extern "C" int sna_qkv_norm_rope_store(const void* qkv, int64_t qkv_stride, int6
                 (long long)qkv_stride, (long long)rope_stride);
   if ((q_norm == nullptr) != (k_norm == nullptr))
     return fail(SNA_ERR_INVALID_ARGUMENT, "qkv_norm_rope_store: give both QK-norm gammas or neither");
+  if (cache_dtype == SNA_DTYPE_FP8_E4M3FN_MUL)
+    return fail(SNA_ERR_UNSUPPORTED, "qkv_norm_rope_store: the writer divides by dequantization scales; for a pool of "
+                "GPT-OSS multipliers m pass SNA_DTYPE_FP8_E4M3FN with the scales bf16(1 / m), as the reference's "
+                "prefill does (gpt_oss/mxfp4/model_prefill.py:41-43)");
   if (cache_dtype != SNA_DTYPE_BF16 && cache_dtype != SNA_DTYPE_FP8_E4M3FN)
     return fail(SNA_ERR_INVALID_ARGUMENT, "qkv_norm_rope_store: unknown cache dtype %d", cache_dtype);
   const bool fp8 = cache_dtype == SNA_DTYPE_FP8_E4M3FN;

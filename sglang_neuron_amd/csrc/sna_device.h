@@ -121,6 +121,16 @@ __device__ __forceinline__ uint32_t quantize_e4m3fn_rcp(uint32_t bf16_bits, floa
   return sign | r;
 }
 
+// The GPT-OSS decode write (attention_decode.py:259-260): a bf16 element times the bf16 quantization multiplier m
+// (the inverted checkpoint scale, gpt_oss/mxfp4/common.py:481-485), the product rounded to bf16 as a product of two
+// bf16 tensors is, then clamped to +-448 (exact in bf16) and cast. The fp32 product of two bf16 values is exact (two
+// 8-bit significands) outside the subnormal range, so the one rounding is the bf16 one. A NaN product is bf16's
+// canonical NaN (0x7FC0), which casts to 0x7F.
+__device__ __forceinline__ uint32_t quantize_e4m3fn_mul(uint32_t bf16_bits, float m) {
+  const float p = bf16_bits_to_f32(bf16_bits) * m;
+  return f32_to_e4m3fn(clamp_fp8(bf16_bits_to_f32(f32_to_bf16_bits(p))));
+}
+
 // Whether quantize_e4m3fn_rcp serves the scale s (a positive normal float).
 __device__ __forceinline__ bool rcp_scale_ok(float s) { return s >= 1.17549435e-38f && s <= 3.40282347e+38f; }
 

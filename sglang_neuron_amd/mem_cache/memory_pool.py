@@ -12,7 +12,11 @@ Differences from the reference, all on the write path the reference leaves to it
     :178-179, :414-418) with the HIP store kernels: FP8 e4m3fn quantization, bit-exact with the reference's
     ``e4m3fn(clamp(x / s, +-448))``, scattered to token slots, out-of-pool slots redirected to the reserved slot 0.
   * FP8 scales are tensors of the pool: per layer and KV head for MHA (``k_scale[layer]``, ``v_scale[layer]`` [G]
-    fp32), per token slot for MLA (``row_scale[layer]`` [slots] fp32, set by the store from each row's absmax).
+    fp32), per token slot for MLA (``row_scale[layer]`` [slots] fp32, set by the store from each row's absmax). An
+    MHA layer's scales are dequantization scales s (stores divide: e4m3fn(x / s), qkv.py:69-70), or, set with
+    ``inverted=True``, the GPT-OSS model's inverted bf16 scales m (gpt_oss/mxfp4/common.py:481-485), which its decode
+    multiplies by (e4m3fn(bf16(x * m)), attention_decode.py:259-260) and its prefill divides by bf16(1 / m)
+    (gpt_oss/mxfp4/model_prefill.py:41-43).
   * K stays unpacked ``[blocks, kv_heads, page, head_dim]``: ``fp8_packed_k`` is False (the packed
     ``[.., page/2, d, 2]`` K of :133-137 is a Trainium-kernel layout).
 
@@ -107,6 +111,7 @@ class NeuronMHATokenToKVPool:
         self.v_buffer: List[Tensor] = []
         self.k_scale: List[Tensor] = []
         self.v_scale: List[Tensor] = []
+        self.scales_inverted: List[bool] = []  # per layer: the scales are GPT-OSS multipliers m, not divisors s
         self._create_buffers()
         self.mem_usage = self.get_kv_size_bytes() / GB
         logger.info("KV pool: layers=%d blocks=%d page=%d kv_heads=%d head_dim=%d dtype=%s (%.2f GB)", self.layer_num,
@@ -124,6 +129,7 @@ class NeuronMHATokenToKVPool:
             self.v_buffer.append(torch.zeros(shape, dtype=self.store_dtype, device=self.device))
             self.k_scale.append(torch.ones(self.head_num, dtype=torch.float32, device=self.device))
             self.v_scale.append(torch.ones(self.head_num, dtype=torch.float32, device=self.device))
+            self.scales_inverted.append(False)
 
     def _idx(self, layer_id: int) -> int:
         i = layer_id - self.start_layer
@@ -143,28 +149,54 @@ class NeuronMHATokenToKVPool:
         return self.get_key_buffer(layer_id), self.get_value_buffer(layer_id)
 
     def get_kv_scales(self, layer_id: int) -> Tuple[Tensor, Tensor]:
-        """The layer's FP8 dequantization scales [head_num] fp32 (K, V)."""
+        """The layer's FP8 scales [head_num] fp32 (K, V): dequantization scales, or the GPT-OSS multipliers when
+        ``kv_scales_inverted(layer_id)``."""
         i = self._idx(layer_id)
         return self.k_scale[i], self.v_scale[i]
+
+    def kv_scales_inverted(self, layer_id: int) -> bool:
+        """Whether the layer's scales are GPT-OSS multipliers m (a byte is worth byte / m) rather than dequantization
+        scales."""
+        return self.scales_inverted[self._idx(layer_id)]
+
+    def prefill_kv_scales(self, layer_id: int) -> Tuple[Tensor, Tensor]:
+        """The dequantization scales the layer's prefill writers divide by: the layer's scales, or for multipliers m
+        ``1 / m`` rounded to bf16, as the reference's GPT-OSS prefill computes them (model_prefill.py:41-43)."""
+        i = self._idx(layer_id)
+        if not self.scales_inverted[i]:
+            return self.k_scale[i], self.v_scale[i]
+        return (ops.prefill_write_scale(self.k_scale[i]).to(self.device),
+                ops.prefill_write_scale(self.v_scale[i]).to(self.device))
 
     def get_kv_layer_ids(self) -> List[int]:
         layers = list(range(self.start_layer, self.start_layer + self.layer_num))
         return layers + layers
 
     # writes
-    def set_kv_scales(self, layer_id: int, k_scale: Union[float, Tensor], v_scale: Union[float, Tensor]) -> None:
-        """Set the layer's dequantization scales (a float or one per KV head)."""
+    def set_kv_scales(self, layer_id: int, k_scale: Union[float, Tensor], v_scale: Union[float, Tensor], *,
+                      inverted: bool = False) -> None:
+        """Set the layer's scales (a float or one per KV head): dequantization scales, or with ``inverted`` the GPT-OSS
+        model's inverted scales (its ``attn.k_scale`` / ``attn.v_scale``, bf16 values: 1 / bf16(checkpoint scale),
+        gpt_oss/mxfp4/common.py:481-485), which the layer's decode then multiplies by."""
         i = self._idx(layer_id)
+        if inverted:
+            k_scale = torch.as_tensor(k_scale).detach().float().cpu().to(torch.bfloat16).float()
+            v_scale = torch.as_tensor(v_scale).detach().float().cpu().to(torch.bfloat16).float()
         self.k_scale[i] = _scale_tensor(k_scale, self.head_num, self.device)
         self.v_scale[i] = _scale_tensor(v_scale, self.head_num, self.device)
+        self.scales_inverted[i] = bool(inverted)
 
-    def calibrate_kv_scales(self, layer_id: int, cache_k: Tensor, cache_v: Tensor) -> Tuple[Tensor, Tensor]:
+    def calibrate_kv_scales(self, layer_id: int, cache_k: Tensor, cache_v: Tensor,
+                            inverted: bool = False) -> Tuple[Tensor, Tensor]:
         """Per-KV-head absmax / 448 scales of bf16 tokens [T, head_num, head_dim] (the HIP absmax kernel), set as the
-        layer's scales and returned."""
+        layer's scales and returned. With ``inverted`` they stand for a GPT-OSS checkpoint's scales: the layer gets
+        the multipliers the reference's loader makes of them (ops.inverted_kv_scale), which are returned."""
         k = cache_k.reshape(-1, self.head_num, self.head_dim)
         v = cache_v.reshape(-1, self.head_num, self.head_dim)
         ks, vs = ops.kv_absmax_scale(k), ops.kv_absmax_scale(v)
-        self.set_kv_scales(layer_id, ks, vs)
+        if inverted:
+            ks, vs = ops.inverted_kv_scale(ks).to(self.device), ops.inverted_kv_scale(vs).to(self.device)
+        self.set_kv_scales(layer_id, ks, vs, inverted=inverted)
         return ks, vs
 
     def set_kv_buffer(self, layer, loc: Tensor, cache_k: Tensor, cache_v: Tensor,
@@ -172,7 +204,8 @@ class NeuronMHATokenToKVPool:
                       layer_id_override: Optional[int] = None) -> None:
         """Store tokens [T, head_num, head_dim] (bf16) at slots ``loc`` [T] of layer ``layer`` (a layer id or an object
         with ``layer_id``). SGLang's signature; ``k_scale`` / ``v_scale``, when given, are the dequantization scales
-        (the stored value is x / scale) and become the layer's. The reference pool raises here
+        (the stored value is x / scale) and become the layer's. A layer of GPT-OSS multipliers is written as its
+        decode writes (e4m3fn(bf16(x * m)), attention_decode.py:259-260). The reference pool raises here
         (memory_pool.py:178-179)."""
         layer_id = layer_id_override if layer_id_override is not None else _layer_id(layer)
         i = self._idx(layer_id)
@@ -181,7 +214,19 @@ class NeuronMHATokenToKVPool:
         fp8 = self.store_dtype == FP8
         ops.kv_store_mha(cache_k.reshape(-1, self.head_num, self.head_dim),
                          cache_v.reshape(-1, self.head_num, self.head_dim), loc, self.k_buffer[i], self.v_buffer[i],
-                         self.k_scale[i] if fp8 else None, self.v_scale[i] if fp8 else None)
+                         self.k_scale[i] if fp8 else None, self.v_scale[i] if fp8 else None,
+                         scales_multiply=fp8 and self.scales_inverted[i])
+
+    def set_kv_buffer_prefill(self, layer, loc: Tensor, cache_k: Tensor, cache_v: Tensor) -> None:
+        """Store a prefill chunk's tokens [T, head_num, head_dim] (bf16) at ``loc`` as the reference's prefill writers
+        do: divided by the layer's dequantization scales, which for GPT-OSS multipliers m are bf16(1 / m)
+        (qkv.py:69-70 with model_prefill.py:41-43). For a layer of dequantization scales this is set_kv_buffer."""
+        i = self._idx(_layer_id(layer))
+        fp8 = self.store_dtype == FP8
+        ks, vs = self.prefill_kv_scales(_layer_id(layer)) if fp8 else (None, None)
+        ops.kv_store_mha(cache_k.reshape(-1, self.head_num, self.head_dim),
+                         cache_v.reshape(-1, self.head_num, self.head_dim), loc, self.k_buffer[i], self.v_buffer[i],
+                         ks, vs)
 
     # bookkeeping (memory_pool.py:182-202)
     def get_kv_size_bytes(self) -> int:

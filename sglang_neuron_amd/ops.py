@@ -60,12 +60,29 @@ def _contig(t: Tensor, name: str, dtype: Optional[torch.dtype] = None) -> Tensor
     return t if t.is_contiguous() else t.contiguous()
 
 
-def cache_dtype_code(dtype: torch.dtype) -> int:
+def cache_dtype_code(dtype: torch.dtype, scales_multiply: bool = False) -> int:
+    """The C ABI's cache dtype code. ``scales_multiply``: an FP8 cache whose scales are the GPT-OSS quantization
+    multipliers m (SNA_DTYPE_FP8_E4M3FN_MUL) rather than dequantization scales."""
     if dtype == torch.bfloat16:
         return _lib.DTYPE_BF16
     if dtype in (FP8, torch.uint8):
-        return _lib.DTYPE_FP8_E4M3FN
+        return _lib.DTYPE_FP8_E4M3FN_MUL if scales_multiply else _lib.DTYPE_FP8_E4M3FN
     raise ValueError(f"unsupported cache dtype {dtype} (bf16 or float8_e4m3fn)")
+
+
+def inverted_kv_scale(scale: Union[float, Tensor]) -> Tensor:
+    """The GPT-OSS quantization multiplier of a checkpoint's dequantization scale, as the reference's loader makes it:
+    ``1.0 / scale.to(bfloat16)``, a bf16 value (models/gpt_oss/mxfp4/common.py:481-485), returned as fp32. Computed on
+    the host, so every device gets the same bits."""
+    s = torch.as_tensor(scale).detach().to("cpu", torch.float32)
+    return (1.0 / s.to(torch.bfloat16)).float()
+
+
+def prefill_write_scale(multiplier: Union[float, Tensor]) -> Tensor:
+    """The dequantization scale the reference's GPT-OSS prefill writes with, from the decode's multiplier m:
+    ``1.0 / m`` as bf16 (models/gpt_oss/mxfp4/model_prefill.py:41-43), returned as fp32 (host)."""
+    m = torch.as_tensor(multiplier).detach().to("cpu", torch.float32)
+    return (1.0 / m.to(torch.bfloat16)).float()
 
 
 # ------------------------------------------------------------------------------------------------------------------
@@ -73,10 +90,12 @@ def cache_dtype_code(dtype: torch.dtype) -> int:
 # ------------------------------------------------------------------------------------------------------------------
 
 def kv_store_mha(k: Tensor, v: Tensor, slots: Tensor, k_cache: Tensor, v_cache: Tensor,
-                 k_scale: Optional[Tensor] = None, v_scale: Optional[Tensor] = None) -> None:
+                 k_scale: Optional[Tensor] = None, v_scale: Optional[Tensor] = None,
+                 scales_multiply: bool = False) -> None:
     """Write the tokens' K/V [T, kv_heads, d] bf16 into one layer's caches [blocks, kv_heads, page, d] at ``slots``
-    [T] (int64); FP8 caches quantize with the per-head dequantization scales [kv_heads]. Out-of-pool slots write slot
-    0, as the reference's write does (ops/attention/attention_decode.py:288-300)."""
+    [T] (int64); FP8 caches quantize with the per-head dequantization scales [kv_heads] (e4m3fn(x / s), qkv.py:69-70),
+    or, with ``scales_multiply``, with the GPT-OSS multipliers m (e4m3fn(bf16(x * m)), attention_decode.py:259-260).
+    Out-of-pool slots write slot 0, as the reference's write does (ops/attention/attention_decode.py:288-300)."""
     dev = _on_gpu(k, v, slots, k_cache, v_cache, k_scale, v_scale)
     nb, G, P, d = k_cache.shape
     _need(v_cache.shape == k_cache.shape and v_cache.dtype == k_cache.dtype, "K and V caches differ")
@@ -85,8 +104,8 @@ def kv_store_mha(k: Tensor, v: Tensor, slots: Tensor, k_cache: Tensor, v_cache: 
     _need(k.shape == v.shape, f"k {tuple(k.shape)} and v {tuple(v.shape)} differ")
     slots = _contig(slots.reshape(-1).to(torch.int64), "slots")
     _need(slots.numel() == k.shape[0], f"{slots.numel()} slots for {k.shape[0]} tokens")
-    code = cache_dtype_code(k_cache.dtype)
-    if code == _lib.DTYPE_FP8_E4M3FN:
+    code = cache_dtype_code(k_cache.dtype, scales_multiply)
+    if code != _lib.DTYPE_BF16:
         _need(k_scale is not None and v_scale is not None, "an FP8 cache needs k_scale and v_scale")
         k_scale = _contig(k_scale.reshape(-1).float(), "k_scale")
         v_scale = _contig(v_scale.reshape(-1).float(), "v_scale")
@@ -255,14 +274,16 @@ def check_plan_lengths(plan: _lib.SplitPlan, kind: int, host_seq_lens, window: i
 
 
 def check_decode_operands(seq_lens: Tensor, block_table: Tensor, new_slots: Optional[Tensor], page_size: int,
-                          num_blocks: int) -> None:
+                          num_blocks: int, active: Optional[Tensor] = None) -> None:
     """Refuse a decode batch whose host operands the kernels cannot serve (sna_check_decode_operands): a seq_len
     outside [1, 2^31 - 1], a block table too narrow for a row or naming a page outside the pool inside a row's pages,
-    a live row's new slot that is not at its position on its last page, two live rows writing one slot. Host (CPU)
-    tensors: seq_lens [B] int, block_table [B, W] int32, new_slots [B] int or None. Raises ValueError naming the row.
+    a live row's new slot that is outside the pool, on the reserved page 0, or not at its position on its last page,
+    two live rows writing one slot. Host (CPU) tensors: seq_lens [B] int, block_table [B, W] int32, new_slots [B] int
+    or None, active [B] (1 = live) or None (then a row is live unless it is a padding row: seq_len 1 written to page 0
+    or outside the pool). Raises ValueError naming the row.
 
-    The refusals of the reference's decode_operands (attention/mla_operands.py:64-97)."""
-    for t in (seq_lens, block_table, new_slots):
+    The refusals of the reference's decode_operands (attention/mla_operands.py:54-97)."""
+    for t in (seq_lens, block_table, new_slots, active):
         _need(t is None or not t.is_cuda, "check_decode_operands takes host copies of the operands")
     lens = seq_lens.reshape(-1).to(torch.int64).contiguous()
     B = lens.numel()
@@ -270,8 +291,11 @@ def check_decode_operands(seq_lens: Tensor, block_table: Tensor, new_slots: Opti
     table = block_table.to(torch.int32).contiguous()
     slots = None if new_slots is None else new_slots.reshape(-1).to(torch.int64).contiguous()
     _need(slots is None or slots.numel() == B, f"new_slots must have {B} entries")
+    act = None if active is None else active.reshape(-1).to(torch.int32).contiguous()
+    _need(act is None or act.numel() == B, f"active must have {B} entries")
     rc = _lib.load().sna_check_decode_operands(lens.data_ptr(), table.data_ptr(), table.stride(0), table.shape[1],
-                                               None if slots is None else slots.data_ptr(), B, int(page_size),
+                                               None if slots is None else slots.data_ptr(),
+                                               None if act is None else act.data_ptr(), B, int(page_size),
                                                int(num_blocks))
     _lib.check(rc, "check_decode_operands")
 
@@ -288,6 +312,21 @@ def _stream_workspace_arg(ws: Optional[Tensor], plan: _lib.SplitPlan, heads: int
     _need(ws.numel() >= workspace_bytes(plan, heads, 512), f"workspace of {ws.numel()} bytes, the plan needs "
           f"{workspace_bytes(plan, heads, 512)}")
     return ws
+
+
+def stream_row_chunks(kind: int, B: int, heads: int, n_keys_per_row: int = 0) -> list[tuple[int, int]]:
+    """Row ranges [r0, r1) that split an MLA / DSA batch into launches each one plan can hold: at most MAX_PLAN_ROWS
+    rows, at most STREAM_MAX_COUNTERS merge counters (rows x 16-head groups), and for DSA at most MAX_CTAS workgroups
+    of at most SPARSE_MAX_RANGE_KEYS indices (a row of K indices takes ceil(K / 2048) of them). One range for the
+    batches of the measured configurations; the launches of a split batch run one after another on the stream."""
+    groups = (heads + 15) // 16
+    rows = min(_lib.MAX_PLAN_ROWS, _lib.STREAM_MAX_COUNTERS // groups)
+    if kind == _lib.KIND_DSA:
+        pieces = max(1, -(-int(n_keys_per_row) // _lib.SPARSE_MAX_RANGE_KEYS))
+        _need(pieces <= _lib.MAX_CTAS, f"a DSA row of {n_keys_per_row} indices needs more than {_lib.MAX_CTAS} "
+              "workgroups")
+        rows = min(rows, _lib.MAX_CTAS // pieces)
+    return [(r0, min(B, r0 + rows)) for r0 in range(0, B, rows)] or [(0, 0)]
 
 
 def stream_workspace(plan: _lib.SplitPlan, heads: int, device: torch.device) -> Tensor:
@@ -334,10 +373,12 @@ def prepare_paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_
                              v_scale: Optional[Tensor] = None, sinks: Optional[Tensor] = None, window: int = 0,
                              new_slots: Optional[Tensor] = None, out: Optional[Tensor] = None,
                              host_seq_lens=None, plan: Optional[_lib.SplitPlan] = None,
-                             library_scratch: bool = False) -> Prepared:
+                             library_scratch: bool = False, scales_multiply: bool = False) -> Prepared:
     """paged_decode_gqa's checks and argument binding, launched by calling the result. With ``library_scratch`` the
     call is sna_paged_decode_gqa_noalloc: no workspace tensor is allocated, the split partials go to the library's
-    per-GPU scratch array (at most NOALLOC_SCRATCH_BYTES; calls that overlap on one GPU race)."""
+    per-GPU scratch array (at most NOALLOC_SCRATCH_BYTES; calls that overlap on one GPU race). With
+    ``scales_multiply`` the FP8 scales are the GPT-OSS quantization multipliers m (a cached byte is worth byte / m,
+    and the step's token is stored as e4m3fn(bf16(x * m)), attention_decode.py:259-260)."""
     dev = _on_gpu(q, k_cache, v_cache, block_table, seq_lens, k_new, v_new, k_scale, v_scale, sinks, new_slots, out)
     _need(q.dim() == 3, f"q must be [B, H, d], got {tuple(q.shape)}")
     B, H, d = q.shape
@@ -346,7 +387,7 @@ def prepare_paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_
           f"caches {tuple(k_cache.shape)} / {tuple(v_cache.shape)} do not match q's head_dim {d}")
     _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
     _need(H % G == 0, f"{H} query heads over {G} KV heads")
-    code = cache_dtype_code(k_cache.dtype)
+    code = cache_dtype_code(k_cache.dtype, scales_multiply)
     q = _contig(q, "q", torch.bfloat16)
     k_new = _contig(k_new.reshape(B, G, d), "k_new", torch.bfloat16)
     v_new = _contig(v_new.reshape(B, G, d), "v_new", torch.bfloat16)
@@ -355,7 +396,7 @@ def prepare_paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_
     _need(table.stride(1) == 1, "block_table rows must be contiguous")
     lens = _contig(seq_lens.reshape(-1).to(torch.int32), "seq_lens")
     _need(lens.numel() == B, f"{lens.numel()} seq_lens for {B} rows")
-    if code == _lib.DTYPE_FP8_E4M3FN:
+    if code != _lib.DTYPE_BF16:
         _need(k_scale is not None and v_scale is not None, "an FP8 cache needs k_scale and v_scale")
         k_scale = _contig(k_scale.reshape(-1).float(), "k_scale")
         v_scale = _contig(v_scale.reshape(-1).float(), "v_scale")
@@ -392,7 +433,8 @@ def paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: T
                      k_new: Tensor, v_new: Tensor, **kw) -> Tensor:
     """GQA decode of q [B, H, d] over a layer's paged caches [blocks, G, page, d], the step's token k_new / v_new
     [B, G, d] attended in-band (and stored at ``new_slots`` when given). Keyword arguments: sm_scale, k_scale,
-    v_scale (FP8), sinks, window, new_slots, out, host_seq_lens, plan. Returns [B, H, d] bf16.
+    v_scale (FP8), scales_multiply (the scales are GPT-OSS multipliers), sinks, window, new_slots, out,
+    host_seq_lens, plan. Returns [B, H, d] bf16.
 
     Stands in for the attention core of _torch_attention_decode_paged (ops/attention/attention_decode_paged.py:
     159-177) and _torch_attention_decode (ops/attention/attention_decode.py:259-300)."""
@@ -435,19 +477,27 @@ def prepare_mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: 
         out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
     _need(out.shape == (B, H, 512) and out.dtype == torch.bfloat16 and out.is_contiguous(), "bad out tensor")
     hl = _host_lens(seq_lens, host_seq_lens)
-    if plan is None:
+    if plan is not None:
+        if hl is not None:
+            check_plan_lengths(plan, _lib.KIND_MLA, hl)
+        chunks, plans = [(0, B)], [plan]
+    else:
         # the launch runs on host lengths: read the device's once when the caller has no host copy
-        plan = plan_decode(_lib.KIND_MLA, B, host_seq_lens=hl if hl is not None else lens.cpu(),
-                           ctas_per_item=(H + 15) // 16, num_cus=_num_cus(dev))
-    elif hl is not None:
-        check_plan_lengths(plan, _lib.KIND_MLA, hl)
-    ws = _stream_workspace_arg(workspace, plan, H, dev)
+        hl = hl if hl is not None else lens.cpu()
+        chunks = stream_row_chunks(_lib.KIND_MLA, B, H)
+        plans = [plan_decode(_lib.KIND_MLA, r1 - r0, host_seq_lens=hl[r0:r1], ctas_per_item=(H + 15) // 16,
+                             num_cus=_num_cus(dev)) for r0, r1 in chunks]
+    ws = _stream_workspace_arg(workspace, max(plans, key=lambda p: workspace_bytes(p, H, 512)), H, dev)
     lib = _lib.load()
-    args = (_ptr(ql_nope), _ptr(q_pe), _ptr(cache), _ptr(row_scale), _ptr(table), table.stride(0), table.shape[1],
-            _ptr(lens), _ptr(compact_new), _ptr(new_slots), float(sm_scale), _ptr(out), B, H, P, nb, code, plan,
-            _ptr(ws), ws.numel(), _stream(dev))
-    keep = (ql_nope, q_pe, cache, row_scale, table, lens, compact_new, new_slots, out, ws, plan)
-    return Prepared([(lib.sna_mla_decode, args)], keep, out, "mla_decode")
+    calls = []
+    for (r0, r1), pl in zip(chunks, plans):
+        calls.append((lib.sna_mla_decode, (
+            _ptr(ql_nope[r0:r1]), _ptr(q_pe[r0:r1]), _ptr(cache), _ptr(row_scale), _ptr(table[r0:r1]),
+            table.stride(0), table.shape[1], _ptr(lens[r0:r1]), _ptr(compact_new[r0:r1]),
+            None if new_slots is None else _ptr(new_slots[r0:r1]), float(sm_scale), _ptr(out[r0:r1]), r1 - r0, H, P,
+            nb, code, pl, _ptr(ws), ws.numel(), _stream(dev))))
+    keep = (ql_nope, q_pe, cache, row_scale, table, lens, compact_new, new_slots, out, ws, plans)
+    return Prepared(calls, keep, out, "mla_decode")
 
 
 def mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: Tensor, block_table: Tensor,
@@ -484,20 +534,35 @@ def prepare_mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, k
     _need(table.dim() == 2 and table.shape[0] == B and table.stride(1) == 1, f"block_table must be [{B}, width]")
     pos = _contig(positions.reshape(-1).to(torch.int32), "positions")
     _need(pos.numel() == B, f"{pos.numel()} positions for {B} rows")
-    if plan is None:
-        plan = plan_decode(_lib.KIND_DSA, B, n_keys_per_row=K, ctas_per_item=(H + 15) // 16, num_cus=_num_cus(dev))
-    ws = _stream_workspace_arg(workspace, plan, H, dev)
+    if plan is not None:
+        chunks, plans = [(0, B)], [plan]
+    else:
+        chunks = stream_row_chunks(_lib.KIND_DSA, B, H, K)
+        plans = [plan_decode(_lib.KIND_DSA, r1 - r0, n_keys_per_row=K, ctas_per_item=(H + 15) // 16,
+                             num_cus=_num_cus(dev)) for r0, r1 in chunks]
+    ws = _stream_workspace_arg(workspace, max(plans, key=lambda p: workspace_bytes(p, H, 512)), H, dev)
     ctx = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
     lse = torch.empty(B, H, dtype=torch.float32, device=dev)
     lib = _lib.load()
+    calls = []
+    fused_slots = new_slots
     if new_slots is not None:
         new_slots = _contig(new_slots.reshape(-1).to(torch.int64), "new_slots")
         _need(new_slots.numel() == B, f"{new_slots.numel()} new slots for {B} rows")
-    calls = [(lib.sna_mla_decode_sparse, (
-        _ptr(q_absorbed), _ptr(q_pe), _ptr(cache), float(kv_scale), _ptr(idx), K, _ptr(table), table.stride(0),
-        table.shape[1], _ptr(pos), _ptr(own_rows), _ptr(new_slots), float(sm_scale), _ptr(ctx), _ptr(lse), B, H, P,
-        n_rows // P, plan, _ptr(ws), ws.numel(), _stream(dev)))]
-    keep = (q_absorbed, q_pe, cache, idx, table, pos, own_rows, new_slots, ctx, lse, ws, plan)
+        fused_slots = new_slots
+        if len(chunks) > 1:
+            # The reference stores every own row before any gather (mla_decode_attention_torch.py steps 0-1): one
+            # launch keeps that order in itself, several store the whole batch's rows first
+            calls.append((lib.sna_kv_store_dsa, (_ptr(own_rows), _ptr(new_slots), B, float(kv_scale), _ptr(cache),
+                                                 n_rows, _stream(dev))))
+            fused_slots = None
+    for (r0, r1), pl in zip(chunks, plans):
+        calls.append((lib.sna_mla_decode_sparse, (
+            _ptr(q_absorbed[r0:r1]), _ptr(q_pe[r0:r1]), _ptr(cache), float(kv_scale), _ptr(idx[r0:r1]), K,
+            _ptr(table[r0:r1]), table.stride(0), table.shape[1], _ptr(pos[r0:r1]), _ptr(own_rows[r0:r1]),
+            None if fused_slots is None else _ptr(fused_slots[r0:r1]), float(sm_scale), _ptr(ctx[r0:r1]),
+            _ptr(lse[r0:r1]), r1 - r0, H, P, n_rows // P, pl, _ptr(ws), ws.numel(), _stream(dev))))
+    keep = (q_absorbed, q_pe, cache, idx, table, pos, own_rows, new_slots, ctx, lse, ws, plans)
     return Prepared(calls, keep, (ctx, lse), "mla_decode_sparse")
 
 
@@ -537,10 +602,11 @@ def lse_combine(o_parts: Tensor, lse_parts: Tensor) -> tuple[Tensor, Tensor]:
 def prefill_attention(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: Tensor, q_start: Tensor,
                       prior_lens: Tensor, *, max_q_len: int, sm_scale: float, k_scale: Optional[Tensor] = None,
                       v_scale: Optional[Tensor] = None, sinks: Optional[Tensor] = None, window: int = 0,
-                      out: Optional[Tensor] = None, host_q_start=None) -> Tensor:
+                      out: Optional[Tensor] = None, host_q_start=None, scales_multiply: bool = False) -> Tensor:
     """Prefill attention of a batch of chunks: q [T, H, d] bf16 (request r's rows q_start[r] .. q_start[r + 1], at
     positions prior_lens[r] + i), every key read from one layer's caches [blocks, G, page, d] (FP8 with per-KV-head
-    scales k_scale / v_scale [G], or bf16) through ``block_table`` [R, width] (store the chunk's K/V first, with
+    scales k_scale / v_scale [G], dequantization scales or, with ``scales_multiply``, GPT-OSS multipliers m whose
+    bytes are worth byte / m; or bf16) through ``block_table`` [R, width] (store the chunk's K/V first, with
     kv_store_mha). Causal, optionally windowed (keys
     (p - window, p]) and with sinks [H]. ``max_q_len`` bounds the chunk lengths (a host int). Returns [T, H, d] bf16.
     ``host_q_start``: a host copy of q_start; with it the offsets are checked (0 first, non-decreasing, T last, no
@@ -567,9 +633,9 @@ def prefill_attention(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: 
         lens = [hq[r + 1] - hq[r] for r in range(R)]
         _need(min(lens, default=0) >= 0, "q_start must not decrease")
         _need(max(lens, default=0) <= int(max_q_len), f"a chunk of {max(lens)} queries exceeds max_q_len {max_q_len}")
-    code = cache_dtype_code(k_cache.dtype)
+    code = cache_dtype_code(k_cache.dtype, scales_multiply)
     ks = vs = None
-    if code == _lib.DTYPE_FP8_E4M3FN:
+    if code != _lib.DTYPE_BF16:
         _need(k_scale is not None and v_scale is not None, "an FP8 pool needs k_scale and v_scale")
         ks = _contig(k_scale.reshape(-1).float(), "k_scale")
         vs = _contig(v_scale.reshape(-1).float(), "v_scale")

@@ -26,8 +26,12 @@ GQA_CONFIGS = {
     2: dict(name="qwen3-8b-gqa-fp8", B=64, H=32, G=8, d=128, P=16, fp8=True, lens=(4096, 4096), window=0,
             sinks=False),
     4: dict(name="gpt-oss-120b-share-fp8", B=128, H=8, G=1, d=64, P=16, fp8=True, lens=(2048, 8192), window=0,
-            sinks=True),
+            sinks=True, scales_multiply=True),
 }
+# cfg4's FP8 write is the GPT-OSS decode's own: k * k_scale with the bf16 inverted checkpoint scale, rounded to bf16
+# before the cast (ops/attention/attention_decode.py:259-260; models/gpt_oss/mxfp4/common.py:481-485). Its
+# "checkpoint" scale is the absmax / 448 of the case's tokens. cfg2's per-KV-head scales are this path's extension
+# and divide (qkv.py:69-70).
 MLA_CONFIG = dict(name="deepseek-v2-lite-mla-fp8", B=32, H=16, P=64, lens=(1024, 16384), latent_scale=0.5,
                   sm_scale=1.0 / math.sqrt(192.0))
 DSA_CONFIG = dict(name="glm5-dsa-mla-fp8", B=16, H=16, P=64, pool_positions=131072, n_indices=2048, recent=128,
@@ -90,6 +94,7 @@ class GqaCase:
     new_slots: Tensor         # [B] int64
     sinks: Optional[Tensor]   # [H] fp32
     extra: dict = field(default_factory=dict)
+    scales_multiply: bool = False  # FP8 scales are GPT-OSS multipliers (SNA_DTYPE_FP8_E4M3FN_MUL), not divisors
 
     def to(self, device) -> "GqaCase":
         out = GqaCase(**{k: getattr(self, k) for k in self.__dataclass_fields__})
@@ -149,7 +154,8 @@ def gqa_case(cfg: int, *, gen_device="cpu", overrides: Optional[dict] = None) ->
     return GqaCase(cfg=cfg, B=B, H=H, G=G, d=d, P=P, fp8=spec["fp8"], window=spec["window"],
                    sm_scale=1.0 / math.sqrt(d), seq_lens=lens.to(torch.int64), block_table=table, num_blocks=nb,
                    q=q, k_prior=k_prior, v_prior=v_prior, prior_slots=prior_slots, k_new=k_new, v_new=v_new,
-                   new_slots=new_slots, sinks=sinks, extra={"name": spec["name"]})
+                   new_slots=new_slots, sinks=sinks, extra={"name": spec["name"]},
+                   scales_multiply=bool(spec["fp8"] and spec.get("scales_multiply", False)))
 
 
 @dataclass
@@ -304,7 +310,8 @@ def dsa_case(*, gen_device="cpu", overrides: Optional[dict] = None) -> DsaCase:
 
 def gqa_pool(case: GqaCase, device="cuda"):
     """(k_cache, v_cache, k_scale, v_scale) of one layer on ``device``: per-KV-head scales calibrated over every K (V)
-    token of the case (prior and new) by the HIP absmax kernel, then the prior tokens stored by the HIP store."""
+    token of the case (prior and new) by the HIP absmax kernel (for a GPT-OSS case, inverted on the host as the
+    reference's loader inverts its checkpoint scale), then the prior tokens stored by the HIP store."""
     from . import ops
 
     dt = torch.float8_e4m3fn if case.fp8 else torch.bfloat16
@@ -315,8 +322,10 @@ def gqa_pool(case: GqaCase, device="cuda"):
     if case.fp8:
         ks = ops.kv_absmax_scale(torch.cat([kp, case.k_new.to(device)], dim=0))
         vs = ops.kv_absmax_scale(torch.cat([vp, case.v_new.to(device)], dim=0))
+        if case.scales_multiply:
+            ks, vs = ops.inverted_kv_scale(ks).to(device), ops.inverted_kv_scale(vs).to(device)
     if kp.shape[0]:
-        ops.kv_store_mha(kp, vp, case.prior_slots.to(device), kc, vc, ks, vs)
+        ops.kv_store_mha(kp, vp, case.prior_slots.to(device), kc, vc, ks, vs, scales_multiply=case.scales_multiply)
     return kc, vc, ks, vs
 
 

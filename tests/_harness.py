@@ -29,10 +29,14 @@ def assert_close_attn(got: torch.Tensor, want: torch.Tensor, what: str = "") -> 
 # ---- GQA ----
 
 def gqa_scales(case: workloads.GqaCase):
-    """Per-KV-head absmax scales over every K (V) token of the case, prior and new (oracle)."""
+    """Per-KV-head absmax scales over every K (V) token of the case, prior and new (oracle); for a GPT-OSS case
+    (``scales_multiply``) the multipliers the reference's loader makes of them."""
     k_all = torch.cat([case.k_prior.cpu(), case.k_new.cpu()], dim=0)
     v_all = torch.cat([case.v_prior.cpu(), case.v_new.cpu()], dim=0)
-    return ofp8.absmax_scale(k_all, dims=(0, 2)), ofp8.absmax_scale(v_all, dims=(0, 2))
+    ks, vs = ofp8.absmax_scale(k_all, dims=(0, 2)), ofp8.absmax_scale(v_all, dims=(0, 2))
+    if case.scales_multiply:
+        return ofp8.inverted_scale(ks), ofp8.inverted_scale(vs)
+    return ks, vs
 
 
 def gqa_oracle(case: workloads.GqaCase):
@@ -44,11 +48,12 @@ def gqa_oracle(case: workloads.GqaCase):
     ks = vs = None
     if case.fp8:
         ks, vs = gqa_scales(case)
-    ost.kv_store_mha(case.k_prior.cpu(), case.v_prior.cpu(), case.prior_slots.cpu(), kc, vc, ks, vs)
+    mul = case.scales_multiply
+    ost.kv_store_mha(case.k_prior.cpu(), case.v_prior.cpu(), case.prior_slots.cpu(), kc, vc, ks, vs, mul)
     out = oatt.paged_decode_gqa(case.q.cpu(), kc, vc, case.block_table, case.seq_lens, case.k_new.cpu(),
                                 case.v_new.cpu(), sm_scale=case.sm_scale, k_scale=ks, v_scale=vs,
-                                sinks=case.sinks, window=case.window)
-    ost.kv_store_mha(case.k_new.cpu(), case.v_new.cpu(), case.new_slots.cpu(), kc, vc, ks, vs)
+                                sinks=case.sinks, window=case.window, scales_multiply=mul)
+    ost.kv_store_mha(case.k_new.cpu(), case.v_new.cpu(), case.new_slots.cpu(), kc, vc, ks, vs, mul)
     return out, kc, vc, ks, vs
 
 
@@ -62,7 +67,7 @@ def gqa_gpu_decode(case: workloads.GqaCase, kc, vc, ks, vs, dev="cuda", store_ne
                                 case.k_new.to(dev), case.v_new.to(dev), sm_scale=case.sm_scale, k_scale=ks,
                                 v_scale=vs, sinks=None if case.sinks is None else case.sinks.to(dev),
                                 window=case.window, new_slots=case.new_slots.to(dev) if store_new else None,
-                                host_seq_lens=case.seq_lens)
+                                host_seq_lens=case.seq_lens, scales_multiply=case.scales_multiply)
 
 
 def cache_bytes(c: torch.Tensor) -> torch.Tensor:

@@ -175,11 +175,46 @@ def test_dsa_stream_plan(lib):
     assert rc == 0 and p.total_tiles == 3 and p.empty_rows == 3
 
 
+@pytest.mark.parametrize("B,K,ctas", [(20, 3000, 1), (16, 2064, 1), (5, 4096, 1), (64, 4000, 1), (100, 2500, 2),
+                                      (7, 2049, 4), (256, 2048, 1), (3, 4095, 8)])
+def test_dsa_plan_ranges_fit_the_sparse_cap(lib, B, K, ctas):
+    """A sparse workgroup resolves at most 2048 indices (128 tiles) in LDS: every range of a DSA plan holds at most
+    that many, whole rows longer than it included (each gets enough pieces)."""
+    rc, p = _plan(lib, _lib.KIND_DSA, B=B, keys=K, ctas=ctas)
+    assert rc == 0, lib.sna_last_error()
+    sizes = [p.cta_start[w + 1] - p.cta_start[w] for w in range(p.n_ctas)]
+    assert max(sizes) <= 2048 // 16 and min(sizes) >= 1
+    assert p.cta_start[p.n_ctas] == p.total_tiles == B * max((K + 15) // 16, 1)
+    tiles = max((K + 15) // 16, 1)
+    if B <= p.n_ctas:  # whole rows: every range inside one row
+        assert all(p.cta_start[w] // tiles == (p.cta_start[w + 1] - 1) // tiles for w in range(p.n_ctas))
+
+
+def test_stream_row_chunks_fit_one_plan_each(lib):
+    """ops.stream_row_chunks splits a batch past one launch's limits (rows, merge counters, sparse workgroups) into
+    row ranges each of which plans."""
+    from sglang_neuron_amd import ops
+    for kind, B, H, K in ((_lib.KIND_MLA, 300, 16, 0), (_lib.KIND_MLA, 600, 128, 0), (_lib.KIND_DSA, 300, 16, 3000),
+                          (_lib.KIND_DSA, 90, 64, 9000), (_lib.KIND_MLA, 40, 16, 0)):
+        chunks = ops.stream_row_chunks(kind, B, H, K)
+        assert chunks[0][0] == 0 and chunks[-1][1] == B
+        assert all(a[1] == b[0] for a, b in zip(chunks, chunks[1:]))
+        for r0, r1 in chunks:
+            lens = [1000 + 37 * i for i in range(r1 - r0)] if kind == _lib.KIND_MLA else None
+            rc, _ = _plan(lib, kind, lens, B=r1 - r0, keys=K, ctas=(H + 15) // 16)
+            assert rc == 0, (kind, B, H, K, r0, r1, lib.sna_last_error())
+    assert ops.stream_row_chunks(_lib.KIND_MLA, 40, 16) == [(0, 40)]
+
+
 def test_stream_plan_refusals(lib):
     assert _plan(lib, _lib.KIND_MLA, None, B=4, max_len=3000)[0] == _lib.SNA_ERR_INVALID_ARGUMENT  # no host lengths
     assert _plan(lib, _lib.KIND_MLA, [100] * 257)[0] == _lib.SNA_ERR_UNSUPPORTED  # past SNA_MAX_PLAN_ROWS
     assert _plan(lib, _lib.KIND_MLA, [16 * 65536])[0] == _lib.SNA_ERR_UNSUPPORTED  # a row past 65535 tiles
     assert _plan(lib, _lib.KIND_MLA, [0, 5])[0] == _lib.SNA_ERR_INVALID_ARGUMENT  # seq_len 0
+    # more (row, head group) pairs than a launch's merge counters
+    assert _plan(lib, _lib.KIND_MLA, [100] * 256, ctas=8)[0] == _lib.SNA_ERR_UNSUPPORTED
+    assert b"merge counters" in lib.sna_last_error()
+    assert _plan(lib, _lib.KIND_DSA, B=200, keys=3000)[0] == _lib.SNA_ERR_UNSUPPORTED  # 400 sparse workgroups
 
 
 def test_plan_rejects_bad_arguments(lib):

@@ -11,6 +11,7 @@ import torch
 from conftest import announce
 from _harness import assert_close_attn, dsa_oracle, gqa_oracle, mla_oracle
 from oracle import attention as oatt
+from oracle import fp8 as ofp8
 from oracle import store as ost
 from sglang_neuron_amd import workloads
 from sglang_neuron_amd.attention import NeuronAttnBackend
@@ -68,8 +69,10 @@ def test_backend_gqa_decode(name, cfg, over):
                             scaling=case.sm_scale, sliding_window_size=case.window if case.window else -1,
                             sinks=None if case.sinks is None else case.sinks.to(DEV))
     if case.fp8:
+        # cfg4: the GPT-OSS model's inverted scales (the layer's decode multiplies by them)
         pool.calibrate_kv_scales(1, torch.cat([case.k_prior, case.k_new]).to(DEV),
-                                 torch.cat([case.v_prior, case.v_new]).to(DEV))
+                                 torch.cat([case.v_prior, case.v_new]).to(DEV), inverted=case.scales_multiply)
+        assert pool.kv_scales_inverted(1) == case.scales_multiply
     pool.set_kv_buffer(layer, case.prior_slots.to(DEV), case.k_prior.to(DEV), case.v_prior.to(DEV))
     backend = _backend(pool, case.block_table, case.seq_lens, case.P)
     fb = _batch(case.seq_lens, case.new_slots)
@@ -188,7 +191,7 @@ def test_backend_gqa_device_metadata(name, cfg, over, host_lens):
                             scaling=case.sm_scale, sliding_window_size=case.window if case.window else -1,
                             sinks=None if case.sinks is None else case.sinks.to(DEV))
     pool.calibrate_kv_scales(0, torch.cat([case.k_prior, case.k_new]).to(DEV),
-                             torch.cat([case.v_prior, case.v_new]).to(DEV))
+                             torch.cat([case.v_prior, case.v_new]).to(DEV), inverted=case.scales_multiply)
     pool.set_kv_buffer(layer, case.prior_slots.to(DEV), case.k_prior.to(DEV), case.v_prior.to(DEV))
     args = (case.q.reshape(case.B, -1).to(DEV), case.k_new.to(DEV), case.v_new.to(DEV), layer)
     host = _backend(pool, case.block_table, case.seq_lens, case.P).forward_decode(*args, _batch(case.seq_lens,
@@ -234,16 +237,18 @@ class _Extend:
         return False
 
 
-EXTEND = [("qwen3-8b-shape", 21, dict(H=32, G=8, d=128, P=16), (50, 0, 300), (40, 70, 5), 0, False),
-          ("gpt-oss-share-swa-sinks", 22, dict(H=8, G=1, d=64, P=16), (200, 17), (150, 33), 128, True)]
+EXTEND = [("qwen3-8b-shape", 21, dict(H=32, G=8, d=128, P=16), (50, 0, 300), (40, 70, 5), 0, False, False),
+          ("gpt-oss-share-swa-sinks", 22, dict(H=8, G=1, d=64, P=16), (200, 17), (150, 33), 128, True, True)]
 
 
 @pytest.mark.parametrize("device_r2t", [False, True], ids=["host-r2t", "device-r2t"])
-@pytest.mark.parametrize("name,seed,shape,priors,ext,window,sinks", EXTEND, ids=[e[0] for e in EXTEND])
-def test_backend_extend_then_decode(name, seed, shape, priors, ext, window, sinks, device_r2t):
+@pytest.mark.parametrize("name,seed,shape,priors,ext,window,sinks,inverted", EXTEND, ids=[e[0] for e in EXTEND])
+def test_backend_extend_then_decode(name, seed, shape, priors, ext, window, sinks, inverted, device_r2t):
     """An extend batch through forward_extend (its K/V stored, then segmented prefill attention over the pool), then
     one decode step through forward_decode over the pool the extend wrote: attention within the bar against the
-    oracle's segmented prefill and decode on the pool's bytes, the pool bit-exact against the oracle's store."""
+    oracle's segmented prefill and decode on the pool's bytes, the pool bit-exact against the oracle's store. The
+    GPT-OSS case keeps the model's inverted scales m: its prior and decoded tokens are written as the decode writes
+    them (bf16(x * m)), its extend chunk as the prefill writes it (x / bf16(1 / m), model_prefill.py:41-43)."""
     H, G, d, P = shape["H"], shape["G"], shape["d"], shape["P"]
     R = len(priors)
     announce(f"backend extend+decode {name} device_r2t={device_r2t}")
@@ -261,7 +266,8 @@ def test_backend_extend_then_decode(name, seed, shape, priors, ext, window, sink
     ks_tok = [torch.randn(x, G, d, generator=g).to(torch.bfloat16) for x in totals]
     vs_tok = [torch.randn(x, G, d, generator=g).to(torch.bfloat16) for x in totals]
     pool = NeuronMHATokenToKVPool((nb - 1) * P, P, torch.float8_e4m3fn, G, d, 1, DEV)
-    kscale, vscale = pool.calibrate_kv_scales(0, torch.cat(ks_tok).to(DEV), torch.cat(vs_tok).to(DEV))
+    kscale, vscale = pool.calibrate_kv_scales(0, torch.cat(ks_tok).to(DEV), torch.cat(vs_tok).to(DEV),
+                                              inverted=inverted)
     sk = torch.randn(H, generator=g) if sinks else None
     layer = SimpleNamespace(layer_id=0, tp_q_head_num=H, tp_k_head_num=G, head_dim=d, scaling=d ** -0.5,
                             sliding_window_size=window if window else -1, sinks=None if sk is None else sk.to(DEV))
@@ -288,15 +294,19 @@ def test_backend_extend_then_decode(name, seed, shape, priors, ext, window, sink
     torch.cuda.synchronize()
     kc_o = torch.zeros(nb, G, P, d, dtype=torch.uint8)
     vc_o = torch.zeros_like(kc_o)
-    all_slots = torch.cat([prior_slots, ext_slots])
-    ost.kv_store_mha(torch.cat([torch.cat([ks_tok[r][:priors[r]] for r in range(R)]), k_ext]),
-                     torch.cat([torch.cat([vs_tok[r][:priors[r]] for r in range(R)]), v_ext]), all_slots, kc_o, vc_o,
-                     kscale.cpu(), vscale.cpu())
+    ost.kv_store_mha(torch.cat([ks_tok[r][:priors[r]] for r in range(R)]),
+                     torch.cat([vs_tok[r][:priors[r]] for r in range(R)]), prior_slots, kc_o, vc_o, kscale.cpu(),
+                     vscale.cpu(), inverted)
+    # the chunk: divided by the prefill's scales (the multipliers' bf16 inverses for the GPT-OSS layer)
+    pk = ofp8.inverted_scale(kscale.cpu()) if inverted else kscale.cpu()
+    pv = ofp8.inverted_scale(vscale.cpu()) if inverted else vscale.cpu()
+    ost.kv_store_mha(k_ext, v_ext, ext_slots, kc_o, vc_o, pk, pv)
     k_pool, v_pool = (t.cpu().view(torch.uint8) for t in pool.get_kv_buffer(0))
     assert torch.equal(k_pool, kc_o) and torch.equal(v_pool, vc_o), "pool after extend differs"
     q_start = torch.tensor([0] + torch.tensor(ext).cumsum(0).tolist(), dtype=torch.int32)
     want = oatt.segmented_prefill(q_ext, k_pool, v_pool, table, q_start, torch.tensor(priors), sm_scale=d ** -0.5,
-                                  k_scale=kscale.cpu(), v_scale=vscale.cpu(), sinks=sk, window=window)
+                                  k_scale=kscale.cpu(), v_scale=vscale.cpu(), sinks=sk, window=window,
+                                  scales_multiply=inverted)
     assert_close_attn(out.reshape(T, H, d).cpu(), want, f"{name} extend")
 
     # one decode step over the pool the extend wrote
@@ -309,5 +319,10 @@ def test_backend_extend_then_decode(name, seed, shape, priors, ext, window, sink
                                    v_new.reshape(R, G * d).to(DEV), layer, _batch(L, new_slots))
     torch.cuda.synchronize()
     want_d = oatt.paged_decode_gqa(q_dec, k_pool, v_pool, table, L, k_new, v_new, sm_scale=d ** -0.5,
-                                   k_scale=kscale.cpu(), v_scale=vscale.cpu(), sinks=sk, window=window)
+                                   k_scale=kscale.cpu(), v_scale=vscale.cpu(), sinks=sk, window=window,
+                                   scales_multiply=inverted)
     assert_close_attn(out_d.reshape(R, H, d).cpu(), want_d, f"{name} decode after extend")
+    # the decode's fused store wrote the new tokens as the layer's decode does
+    ost.kv_store_mha(k_new, v_new, new_slots, kc_o, vc_o, kscale.cpu(), vscale.cpu(), inverted)
+    k_pool, v_pool = (t.cpu().view(torch.uint8) for t in pool.get_kv_buffer(0))
+    assert torch.equal(k_pool, kc_o) and torch.equal(v_pool, vc_o), "pool after the decode differs"

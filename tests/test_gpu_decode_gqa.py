@@ -26,6 +26,9 @@ CASES = [
     ("cfg4-page128-sinks", 4, {"B": 6, "P": 128, "lens": (1000, 5000)}),
     ("cfg2-32-splits", 2, {"B": 2, "lens": (8192, 8192)}),                # the combine's second chunk of 16 splits
     ("cfg4-64-splits", 4, {"B": 2, "lens": (8000, 8192)}),                # 4 chunks, sinks
+    # GPT-OSS multipliers on other shapes (cfg4 itself runs with them): 8 KV heads, d128, and no sinks
+    ("multiplier-g8-d128", 2, {"B": 4, "lens": (300, 1500), "scales_multiply": True}),
+    ("multiplier-cfg4-no-sinks", 4, {"B": 5, "lens": (1, 900), "sinks": False}),
     # the bench workloads at their full sizes (the metric's cfg2 included): same seeds, same split plans
     ("cfg2-full", 2, {}),
     ("cfg4-full-size", 4, {}),

@@ -23,6 +23,8 @@ MLA_CASES = [
     ("cfg3-full", {}),                                                   # the bench workload at its full size
     # more rows than workgroups (20 heads: two head groups of 128 workgroups): ranges span several rows
     ("multi-row-ranges", {"B": 200, "H": 20, "lens": (1, 200)}),
+    # more rows than one launch's plan holds (256): two launches, one after the other
+    ("batch-past-one-launch", {"B": 300, "lens": (1, 120)}),
 ]
 
 
@@ -72,6 +74,12 @@ DSA_CASES = [
     # a block table past the prologue's LDS copy (20000 one-slot pages): indices resolve entry by entry
     ("page-1-wide-table", {"B": 2, "P": 1, "pool_positions": 20000, "n_indices": 256, "recent": 16,
                            "short_rows": ()}),
+    # index lists past one workgroup's 2048 (each row in pieces of at most 2048 indices)
+    ("indices-past-one-range", {"B": 6, "pool_positions": 8192, "n_indices": 3000, "recent": 128,
+                                "short_rows": (2000,)}),
+    # rows whose pieces need more than one launch's 256 workgroups: the own rows stored first, then two launches
+    ("batch-past-one-launch", {"B": 130, "pool_positions": 2600, "n_indices": 2500, "recent": 64,
+                               "short_rows": (1000,)}),
 ]
 
 

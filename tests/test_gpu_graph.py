@@ -55,7 +55,7 @@ def test_graph_gqa_split_and_combine():
     assert plan.max_splits > 1 and plan.work_n == 0
     _replay_matches(lambda: ops.prepare_paged_decode_gqa(q, kc, vc, table, lens, kn, vn, sm_scale=case.sm_scale,
                                                          k_scale=ks, v_scale=vs, sinks=sinks, new_slots=slots,
-                                                         plan=plan),
+                                                         plan=plan, scales_multiply=case.scales_multiply),
                     lambda out: [out])
 
 

@@ -66,6 +66,32 @@ def test_qkv_writer_matches_oracle(name, T, Hq, Hkv, d, P, fp8, norm):
     assert torch.equal(kb, kc_o), "K pool differs"
 
 
+def test_qkv_writer_norm_within_a_bf16_step_of_the_reference_formula():
+    """The writer's normed Q (no RoPE: angle 0) against the reference's literal _rms, gamma * (x32 *
+    torch.rsqrt(x32.pow(2).mean(-1) + eps)).to(bf16) (qkv_paged.py:40-42): at most one bf16 step of the normed value
+    (times gamma) apart, so the writer cannot drift from the reference's normalisation."""
+    announce("qkv norm vs the literal reference formula")
+    T, Hq, Hkv, d, P = 200, 8, 2, 128, 16
+    g = torch.Generator().manual_seed(31)
+    qkv = (torch.randn(T, (Hq + 2 * Hkv) * d, generator=g) * 2.0).to(torch.bfloat16)
+    cos, sin = torch.ones(T, d, dtype=torch.bfloat16), torch.zeros(T, d, dtype=torch.bfloat16)
+    qn = (1.0 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    kn = torch.ones(d, dtype=torch.bfloat16)
+    nb = T // P + 2
+    dev = "cuda"
+    kc = torch.zeros(nb, Hkv, P, d, dtype=torch.bfloat16, device=dev)
+    q = ops.qkv_norm_rope_store(qkv.to(dev), cos=cos.to(dev), sin=sin.to(dev), num_q_heads=Hq, num_kv_heads=Hkv,
+                                d_head=d, k_cache=kc, v_cache=torch.zeros_like(kc),
+                                slot_mapping=(torch.arange(T) + P).to(dev), q_norm=qn.to(dev), k_norm=kn.to(dev),
+                                norm_eps=1e-6).cpu()
+    x32 = qkv[:, :Hq * d].reshape(T, Hq, d).float()
+    normed = (x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+    want = qn * normed
+    step = torch.exp2(torch.floor(torch.log2(normed.float().abs().clamp(min=1e-30))) - 7) * qn.float().abs()
+    assert bool(((q.float() - want.float()).abs() <= 2 * step + 1e-30).all())
+    assert float((q != want).float().mean()) < 0.05
+
+
 def test_qkv_writer_rejects_bad_arguments():
     dev = "cuda"
     kc = torch.zeros(4, 2, 16, 64, dtype=torch.bfloat16, device=dev)

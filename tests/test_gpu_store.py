@@ -46,6 +46,35 @@ def test_mha_store_every_bf16_pattern(scales):
     assert torch.equal(cache_bytes(vg), vc)
 
 
+@pytest.mark.parametrize("ckpt", [(0.0123, 3.0 / 448.0, 0.02931, 2 ** -6), (1 / 448, 4.67 / 448, 0.5, 7.5)])
+def test_mha_store_multiplier_mode_every_bf16_pattern(ckpt):
+    """The GPT-OSS decode write (SNA_DTYPE_FP8_E4M3FN_MUL): e4m3fn(bf16(x * m)) with m the loader's inverted bf16
+    scales, every bf16 pattern (NaN included: both write 0x7F) against the oracle, bit for bit."""
+    announce(f"kv_store_mha multiplier mode all bf16 patterns ckpt={ckpt}")
+    G, d, P = 4, 128, 16
+    T = (1 << 16) // (G * d)
+    k = ALL_BF16.reshape(T, G, d)
+    v = ALL_BF16.flip(0).reshape(T, G, d)
+    nb = T // P + 3
+    g = torch.Generator().manual_seed(15)
+    slots = torch.randperm((nb - 1) * P, generator=g)[:T] + P
+    km = ofp8.inverted_scale(torch.tensor(ckpt, dtype=torch.float32))
+    vm = km.flip(0).contiguous()
+    kc = torch.zeros(nb, G, P, d, dtype=torch.uint8)
+    vc = torch.zeros_like(kc)
+    ost.kv_store_mha(k, v, slots, kc, vc, km, vm, scales_multiply=True)
+    kg = torch.zeros(nb, G, P, d, dtype=torch.float8_e4m3fn, device="cuda")
+    vg = torch.zeros_like(kg)
+    ops.kv_store_mha(k.cuda(), v.cuda(), slots.cuda(), kg, vg, km.cuda(), vm.cuda(), scales_multiply=True)
+    assert torch.equal(cache_bytes(kg), kc)
+    assert torch.equal(cache_bytes(vg), vc)
+    # and the divide with the same heads' dequantization scales writes other bytes somewhere (the modes differ)
+    kd = torch.zeros_like(kg)
+    ops.kv_store_mha(k.cuda(), v.cuda(), slots.cuda(), kd, torch.zeros_like(kg),
+                     torch.tensor(ckpt, dtype=torch.float32).cuda(), torch.tensor(ckpt, dtype=torch.float32).cuda())
+    assert not torch.equal(cache_bytes(kd), kc)
+
+
 def test_mha_store_bf16_and_redirect():
     announce("kv_store_mha bf16 + out-of-pool slot")
     G, d, P, nb = 2, 64, 16, 5

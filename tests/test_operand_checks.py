@@ -58,6 +58,32 @@ def test_each_bad_operand_is_refused(what, edit, match):
         ops.check_decode_operands(lens, table, slots, P, NB)
 
 
+@pytest.mark.parametrize("slot,match", [(0, "on the reserved page 0"), (5, "on the reserved page 0"), (NB * P + 7, "outside the pool"),
+                                        (-1, "outside the pool")])
+def test_live_row_slot_off_the_pool_is_refused(slot, match):
+    """A live row (seq_len > 1) whose write would be redirected to the reserved slot 0 would lose its token: refused.
+    The same slot on a padding row (seq_len 1) passes."""
+    lens, table, slots = _ok_batch()
+    slots[3] = slot
+    with pytest.raises(ValueError, match=f"row 3: live row's new slot {slot} is {match}"):
+        ops.check_decode_operands(lens, table, slots, P, NB)
+    slots[2] = slot  # row 2 is a padding row
+    slots[3] = 14 * P + 1
+    ops.check_decode_operands(lens, table, slots, P, NB)
+
+
+def test_explicit_active_flags():
+    """With the reference's active flags, an inactive row is not checked and a live row is, whatever its length."""
+    lens, table, slots = _ok_batch()
+    slots[0] = 3 * P + 1  # would disagree with row 0's position and page
+    with pytest.raises(ValueError, match="row 0"):
+        ops.check_decode_operands(lens, table, slots, P, NB)
+    ops.check_decode_operands(lens, table, slots, P, NB, active=torch.tensor([0, 1, 0, 1]))
+    slots[2] = 0  # the padding row, flagged live: its slot on page 0 is refused
+    with pytest.raises(ValueError, match="row 2"):
+        ops.check_decode_operands(lens, table, slots, P, NB, active=torch.tensor([0, 1, 1, 1]))
+
+
 def test_refusals_name_the_row():
     lens, table, slots = _ok_batch()
     slots[3] = 14 * P + 2

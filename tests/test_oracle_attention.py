@@ -28,7 +28,7 @@ def _softmax_attend(q, keys, vals, scale, sink=None):
     return [sum(e[j] * float(vals[j][i]) for j in range(len(keys))) / den for i in range(len(vals[0]))]
 
 
-def _gqa_case(seed, B=3, H=4, G=2, d=8, P=4, fp8=False, window=0, sinks=False):
+def _gqa_case(seed, B=3, H=4, G=2, d=8, P=4, fp8=False, window=0, sinks=False, mul=False):
     g = torch.Generator().manual_seed(seed)
     lens = [1, 6, 11][:B]
     pages = [(L + P - 1) // P for L in lens]
@@ -51,11 +51,13 @@ def _gqa_case(seed, B=3, H=4, G=2, d=8, P=4, fp8=False, window=0, sinks=False):
     kp, vp = _bf16((T, G, d), g), _bf16((T, G, d), g)
     ks = torch.rand(G, generator=g) * 0.01 + 0.004 if fp8 else None
     vs = torch.rand(G, generator=g) * 0.01 + 0.004 if fp8 else None
-    ost.kv_store_mha(kp, vp, torch.tensor(slots), kc, vc, ks, vs)
+    if mul:  # GPT-OSS multipliers: the bf16 inverses of the scales
+        ks, vs = ofp8.inverted_scale(ks), ofp8.inverted_scale(vs)
+    ost.kv_store_mha(kp, vp, torch.tensor(slots), kc, vc, ks, vs, mul)
     q, kn, vn = _bf16((B, H, d), g), _bf16((B, G, d), g), _bf16((B, G, d), g)
     sk = torch.randn(H, generator=g) if sinks else None
     return dict(q=q, kc=kc, vc=vc, table=table, lens=torch.tensor(lens), kn=kn, vn=vn, ks=ks, vs=vs, sinks=sk,
-                P=P, G=G, window=window, slots=slots)
+                P=P, G=G, window=window, slots=slots, mul=mul)
 
 
 def _brute_gqa(c, scale):
@@ -75,14 +77,23 @@ def _brute_gqa(c, scale):
                 page = int(c["table"][b, p // P])
                 kb, vb = c["kc"][page, g, p % P], c["vc"][page, g, p % P]
                 if c["ks"] is not None:
-                    kb = ofp8.dequantize(kb, float(c["ks"][g]))
-                    vb = ofp8.dequantize(vb, float(c["vs"][g]))
+                    # float64 values: byte * s, or for multipliers byte / m
+                    kf = kb.view(torch.float8_e4m3fn).double()
+                    vf = vb.view(torch.float8_e4m3fn).double()
+                    kms, vms = float(c["ks"][g]), float(c["vs"][g])
+                    kb, vb = (kf / kms, vf / vms) if c["mul"] else (kf * kms, vf * vms)
                 keys.append(kb.double())
                 vals.append(vb.double())
             kn, vn = c["kn"][b, g], c["vn"][b, g]
             if c["ks"] is not None:
-                kn = ofp8.dequantize(ofp8.quantize(kn, float(c["ks"][g])), float(c["ks"][g]))
-                vn = ofp8.dequantize(ofp8.quantize(vn, float(c["vs"][g])), float(c["vs"][g]))
+                kms, vms = float(c["ks"][g]), float(c["vs"][g])
+                if c["mul"]:
+                    # the decode write of the new token: the bf16 product, cast (attention_decode.py:259-260)
+                    kn = torch.tensor(ofp8.e4m3fn_values()[_mul_bytes(kn, kms)]) / kms
+                    vn = torch.tensor(ofp8.e4m3fn_values()[_mul_bytes(vn, vms)]) / vms
+                else:
+                    kn = ofp8.dequantize(ofp8.quantize(kn, kms), kms)
+                    vn = ofp8.dequantize(ofp8.quantize(vn, vms), vms)
             keys.append(kn.double())
             vals.append(vn.double())
             sink = None if c["sinks"] is None else float(c["sinks"][h])
@@ -90,15 +101,24 @@ def _brute_gqa(c, scale):
     return out
 
 
+def _mul_bytes(x, m: float) -> np.ndarray:
+    """e4m3fn codes of bf16 x written with multiplier m, from the definitions: the exact product rounded to bf16's 8
+    significant bits, clamped, cast by nearest-value search."""
+    r = ofp8.bf16_round_spec(x.double().numpy() * m)
+    return ofp8.e4m3fn_rne_spec(np.clip(r, -448.0, 448.0).astype(np.float32)).astype(np.int64)
+
+
 def _oracle_gqa(c, scale):
     return oatt.paged_decode_gqa(c["q"], c["kc"], c["vc"], c["table"], c["lens"], c["kn"], c["vn"], sm_scale=scale,
-                                 k_scale=c["ks"], v_scale=c["vs"], sinks=c["sinks"], window=c["window"])
+                                 k_scale=c["ks"], v_scale=c["vs"], sinks=c["sinks"], window=c["window"],
+                                 scales_multiply=c["mul"])
 
 
-@pytest.mark.parametrize("fp8,window,sinks", [(False, 0, False), (True, 0, False), (True, 0, True), (False, 3, False),
-                                              (True, 4, True)])
-def test_gqa_matches_float64_brute_force(fp8, window, sinks):
-    c = _gqa_case(11, fp8=fp8, window=window, sinks=sinks)
+@pytest.mark.parametrize("fp8,window,sinks,mul", [(False, 0, False, False), (True, 0, False, False),
+                                                  (True, 0, True, False), (False, 3, False, False),
+                                                  (True, 4, True, False), (True, 0, True, True), (True, 4, True, True)])
+def test_gqa_matches_float64_brute_force(fp8, window, sinks, mul):
+    c = _gqa_case(11, fp8=fp8, window=window, sinks=sinks, mul=mul)
     scale = 1 / math.sqrt(8)
     got = _oracle_gqa(c, scale).double()
     want = _brute_gqa(c, scale)

@@ -3,6 +3,7 @@ rounding steps."""
 
 import math
 
+import pytest
 import torch
 
 from oracle import qkv as oqkv
@@ -124,3 +125,27 @@ def test_recip_sqrt_rounds_each_step_to_the_nearest_float32():
         rr = 1 / Fraction(float(root))
         for cand in (np.nextafter(r, np.float32(0)), np.nextafter(r, np.float32(np.inf))):
             assert abs(Fraction(float(r)) - rr) <= abs(Fraction(float(cand)) - rr), (vi, ri)
+
+
+def _literal_rms(x, gamma, eps):
+    """The reference's _rms exactly as written (ops/attention/qkv_paged.py:40-42), in torch's own order."""
+    x32 = x.float()
+    return gamma.reshape(-1) * (x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype)
+
+
+@pytest.mark.parametrize("d,scale", [(128, 1.0), (64, 3.0), (128, 1e-3)])
+def test_rms_matches_the_reference_formula_within_a_bf16_step(d, scale):
+    """oracle.rms fixes the sum order and rounds sqrt and 1 / sqrt once each; against the reference's literal
+    torch.rsqrt(x32.pow(2).mean(-1) + eps) the normed value may move by at most one bf16 step (before gamma's product,
+    which both round the same way), and most values are equal."""
+    g = torch.Generator().manual_seed(d)
+    x = (torch.randn(400, 8, d, generator=g) * scale).to(torch.bfloat16)
+    gamma = (1.0 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    ones = torch.ones(d, dtype=torch.bfloat16)
+    got, want = oqkv.rms(x, ones, 1e-6), _literal_rms(x, ones, 1e-6)
+    step = torch.exp2(torch.floor(torch.log2(want.float().abs().clamp(min=1e-30))) - 7)  # one bf16 ulp at |want|
+    assert bool(((got.float() - want.float()).abs() <= step).all())
+    assert float((got != want).float().mean()) < 0.05
+    with_gamma = oqkv.rms(x, gamma, 1e-6)
+    assert bool(((with_gamma.float() - _literal_rms(x, gamma, 1e-6).float()).abs()
+                 <= 2 * step * gamma.float().abs().max()).all())

@@ -53,6 +53,37 @@ def test_mha_store_slot_arithmetic_by_loop(fp8):
     assert any(torch.equal(kc[0, :, 0], c) for c in cands)
 
 
+def test_mha_store_multiplier_mode_by_loop():
+    """The GPT-OSS decode write (scales_multiply): every byte against the definition of its element, e4m3fn of the
+    exact product rounded to bf16 and clamped, at (slot // page, head, slot % page)."""
+    nb, G, P, d, T = 4, 2, 4, 8, 6
+    k, v = _rand_bf16((T, G, d), 5) * 7, _rand_bf16((T, G, d), 6)
+    slots = torch.tensor([4, 9, 15, 5, 12, 6])
+    m = ofp8.inverted_scale(torch.tensor([0.0123, 3.0 / 448.0]))
+    kc = torch.zeros(nb, G, P, d, dtype=torch.uint8)
+    vc = torch.zeros_like(kc)
+    ost.kv_store_mha(k, v, slots, kc, vc, m, m.flip(0), scales_multiply=True)
+    vals = ofp8.e4m3fn_values()
+    for t in range(T):
+        s = int(slots[t])
+        for h in range(G):
+            for src, cache, mh in ((k, kc, float(m[h])), (v, vc, float(m.flip(0)[h]))):
+                for i in range(d):
+                    p = float(src[t, h, i]) * mh
+                    r = float(ofp8.bf16_round_spec(np.array([p]))[0])
+                    r = min(max(r, -448.0), 448.0)
+                    byte = int(cache[s // P, h, s % P, i])
+                    # the nearest code (ties are rare enough at these values to be checked by the spec's search)
+                    assert byte == int(ofp8.e4m3fn_rne_spec(np.array([r], dtype=np.float32))[0]), (t, h, i)
+                    assert abs(vals[byte] - r) <= abs(r) * 2 ** -4 + 2 ** -10
+    # untouched elsewhere
+    written = {(int(s) // P, int(s) % P) for s in slots}
+    for pg in range(nb):
+        for off in range(P):
+            if (pg, off) not in written:
+                assert int(kc[pg, :, off].abs().sum()) == 0
+
+
 def test_mla_store_per_token_scale_by_loop():
     n, T = 12, 5
     rows = _rand_bf16((T, 576), 4) * 3

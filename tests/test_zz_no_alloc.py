@@ -30,7 +30,8 @@ def _noalloc_call(case, kc, vc, ks, vs, plan):
     rc = lib.sna_paged_decode_gqa_noalloc(
         ptr(q), ptr(kc), ptr(vc), ptr(ks), ptr(vs), ptr(table), table.stride(0), table.shape[1], ptr(lens), ptr(kn),
         ptr(vn), ptr(slots), ptr(sinks), case.window, case.sm_scale, ptr(out), case.B, case.H, case.G, case.d, case.P,
-        kc.shape[0], ops.cache_dtype_code(kc.dtype), ctypes.byref(plan), torch.cuda.current_stream().cuda_stream)
+        kc.shape[0], ops.cache_dtype_code(kc.dtype, case.scales_multiply), ctypes.byref(plan),
+        torch.cuda.current_stream().cuda_stream)
     _lib.check(rc, "paged_decode_gqa_noalloc")
     return out
 
@@ -39,7 +40,7 @@ def _workspace_call(case, kc, vc, ks, vs, plan):
     return ops.paged_decode_gqa(case.q.cuda(), kc, vc, case.block_table.cuda(), case.seq_lens.cuda(),
                                 case.k_new.cuda(), case.v_new.cuda(), sm_scale=case.sm_scale, k_scale=ks, v_scale=vs,
                                 sinks=None if case.sinks is None else case.sinks.cuda(), window=case.window,
-                                new_slots=case.new_slots.cuda(), plan=plan)
+                                new_slots=case.new_slots.cuda(), plan=plan, scales_multiply=case.scales_multiply)
 
 
 # the first call spreads its rows over many splits (a large partial workspace); the second is smaller

@@ -199,6 +199,14 @@ def setup_gqa(cfg: int, window: int, dev):
                                                     v_scale=vs, sinks=sinks, window=case.window, out=out, plan=plan,
                                                     scales_multiply=mul)
                        for (k, v) in pools]}
+    # the step under a plan from a bound (the block table's width), as a serving graph captured once for growing
+    # lengths runs it: the kernels locate their items from the device's seq_lens
+    plan_b = ops.plan_decode(0, case.B, max_seq_len=table.shape[1] * case.P, window=case.window, ctas_per_item=case.G,
+                             num_cus=ops._num_cus(q.device))
+    legs["bound_plan"] = [ops.prepare_paged_decode_gqa(q, k, v, table, lens, kn, vn, sm_scale=case.sm_scale,
+                                                       k_scale=ks, v_scale=vs, sinks=sinks, window=case.window,
+                                                       new_slots=slots, out=out, plan=plan_b, scales_multiply=mul)
+                          for (k, v) in pools]
     tiles = 0
     for L in case.seq_lens.tolist():
         hi = L - 1
@@ -258,13 +266,22 @@ def setup_mla(dev, bf16: bool = False):
     plan = ops.plan_decode(1, case.B, host_seq_lens=case.seq_lens, ctas_per_item=1, num_cus=ops._num_cus(table.device))
     out = torch.empty(case.B, case.H, 512, dtype=torch.bfloat16, device=dev)
     new_slots = case.new_slots.to(dev)
+    hl = case.seq_lens
     steps = [ops.prepare_mla_decode(case.ql_nope, case.q_pe, c, s, table, lens, case.compact_new,
                                     sm_scale=case.sm_scale, page_size=case.P, new_slots=new_slots,
-                                    out=out, plan=plan) for (c, s) in pools]
+                                    out=out, plan=plan, host_seq_lens=hl) for (c, s) in pools]
     legs = {"store": [functools.partial(ops.kv_store_mla, case.compact_new, new_slots, c, s) for (c, s) in pools],
             "decode": [ops.prepare_mla_decode(case.ql_nope, case.q_pe, c, s, table, lens, case.compact_new,
-                                              sm_scale=case.sm_scale, page_size=case.P, out=out, plan=plan)
+                                              sm_scale=case.sm_scale, page_size=case.P, out=out, plan=plan,
+                                              host_seq_lens=hl)
                        for (c, s) in pools]}
+    # the step under a device-split plan from a bound (the block table's width): the launch cuts its split from the
+    # device's seq_lens, as a serving graph captured once for growing lengths runs it
+    plan_b = ops.plan_decode(1, case.B, max_seq_len=table.shape[1] * case.P, ctas_per_item=1,
+                             num_cus=ops._num_cus(table.device))
+    legs["bound_plan"] = [ops.prepare_mla_decode(case.ql_nope, case.q_pe, c, s, table, lens, case.compact_new,
+                                                 sm_scale=case.sm_scale, page_size=case.P, new_slots=new_slots,
+                                                 out=out, plan=plan_b) for (c, s) in pools]
     tiles = int(((case.seq_lens - 1 + 15) // 16).sum())
     # bf16 rows: 18 QK steps of 16x16x32 and 32 PV steps of 16x16x16 (bf16); FP8 rows: the latent QK as 8 scaled FP8
     # 16x16x128 (4 blocks, the query's two parts), the rope as 2 bf16 16x16x32, PV as 32 bf16 16x16x16
@@ -817,13 +834,17 @@ def measure_decode(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: f
     log(f"{wl}: {us:.2f} us/step over {steps_n} steps replayed from a HIP graph ({gbs:.0f} GB/s, {gbs / PEAK_HBM_GBS:.1%} "
         f"of HBM peak); {us_eager:.2f} us/step launched one by one ({wall * 1e6 / (steps_n + warmup):.1f} us/step by "
         f"the host clock); kernels {kernels}; apart: store {apart['store_us']:.2f} us, decode without it "
-        f"{apart['decode_us']:.2f} us")
+        f"{apart['decode_us']:.2f} us" + (f"; the step under a plan from a bound {apart['bound_plan_us']:.2f} us"
+                                           if "bound_plan_us" in apart else ""))
     out = {
         "config": desc,
         "us_per_step": round(us, 3),
         "us_per_step_launched": round(us_eager, 3),
         "apart": dict(apart, note="the step's store kernel alone and its decode without the fused store, each replayed "
-                                  "from a HIP graph of the same steps; us_per_step is both together (fused)"),
+                                  "from a HIP graph of the same steps; us_per_step is both together (fused); "
+                                  "bound_plan_us: the whole step under a plan from a bound (the block table's width), "
+                                  "which locates (GQA) or cuts (MLA) its work from the device's seq_lens, as a serving "
+                                  "graph captured once for growing lengths runs it"),
         "step_alg_bytes": step_bytes,
         "roofline": {
             "bound": "hbm",

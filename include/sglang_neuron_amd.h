@@ -163,7 +163,8 @@ int sna_kv_store_dsa(const void *rows, const int64_t *slots, int64_t n_tokens, f
  * starting in row cta_row[w] at tile cta_off[w] of that row. A workgroup whose range holds a whole row writes its
  * output; a row split over several workgroups is merged inside the same launch (its workgroups publish partials and
  * the last to arrive, with those still waiting for it, merges them), so one launch is the whole decode. row_keys[b] is
- * row b's key count: an MLA or DSA launch uses these host lengths, not the device's seq_lens. */
+ * row b's key count: an MLA or DSA launch uses these host lengths, not the device's seq_lens, unless the MLA plan is a
+ * device split (device_split = 1: planned from a bound, its launch cuts the split from the device's seq_lens). */
 #define SNA_MAX_WORK_MAP 512
 #define SNA_MAX_CTAS 256      /* workgroups of an MLA / DSA stream split */
 #define SNA_MAX_PLAN_ROWS 256 /* rows of an MLA / DSA plan */
@@ -195,10 +196,15 @@ typedef struct {
   uint16_t cta_row[SNA_MAX_CTAS];
   uint16_t cta_off[SNA_MAX_CTAS];
   int32_t row_keys[SNA_MAX_PLAN_ROWS];
+  int32_t device_split; /* MLA: 1 for a plan from a bound. Its launch cuts the stream split from the device's seq_lens
+                           (the same apportionment, by bisection of the longest piece), so one captured launch serves
+                           every length up to the bound; n_ctas is the launch's workgroups per head group (the bound
+                           the workspace is sized for), row_keys the bound's key count, and cta_* are unused. */
 } sna_split_plan;
 
 /* Plan a decode from host copies of seq_lens (exact) or, with host_seq_lens == NULL, from an upper bound
- * max_seq_len for every row (then n_work bounds the device's count and the workspace is sized for it; GQA only).
+ * max_seq_len for every row (GQA: n_work bounds the device's count and the workspace is sized for it; MLA: a
+ * device-split plan, whose launch reads the device's seq_lens, each held to the block table's width).
  * `kind`: 0 GQA, 1 MLA, 2 DSA. For DSA, seq_lens are ignored: `n_keys_per_row` (the index-list length) is the
  * row's key count. `window` is the sliding window (0 = full). `ctas_per_item` is the number of workgroups that
  * one (sequence, split) item launches: num_kv_heads for GQA, and 1 for MLA and DSA. `num_cus` is the device's CU

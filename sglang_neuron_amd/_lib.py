@@ -46,7 +46,7 @@ class SplitPlan(ctypes.Structure):
                 ("work", ctypes.c_uint32 * 512), ("n_ctas", ctypes.c_int32), ("total_tiles", ctypes.c_int32),
                 ("wait_polls", ctypes.c_int32), ("cta_start", ctypes.c_uint32 * (MAX_CTAS + 1)),
                 ("cta_row", ctypes.c_uint16 * MAX_CTAS), ("cta_off", ctypes.c_uint16 * MAX_CTAS),
-                ("row_keys", ctypes.c_int32 * MAX_PLAN_ROWS)]
+                ("row_keys", ctypes.c_int32 * MAX_PLAN_ROWS), ("device_split", ctypes.c_int32)]
 
     def __repr__(self) -> str:
         return (f"SplitPlan(split_tiles={self.split_tiles}, n_work={self.n_work}, tile={self.tile}, "

@@ -335,15 +335,21 @@ class NeuronAttnBackend:
         q = q.reshape(bs, H, 576)
         key = ("mla", H)
         if key not in st.plans:
-            # the MLA launch runs on host lengths: without a host copy the device's are read once per forward
-            lens = st.host_lens if st.host_lens is not None else st.seq_lens.cpu()
-            st.plans[key] = ops.plan_decode(_lib.KIND_MLA, bs, host_seq_lens=lens, ctas_per_item=(H + 15) // 16,
-                                            num_cus=ops._num_cus(q.device))
-            st.plans[key + ("ws",)] = ops.stream_workspace(st.plans[key], H, q.device)
+            # exact plans from host lengths; without a host copy, a device split bounded by the table's width (the
+            # launch reads the device's lengths, nothing is read back)
+            chunks = ops.stream_row_chunks(_lib.KIND_MLA, bs, H)
+            bound = st.table.shape[1] * pool.page_size
+            plans = [ops.plan_decode(_lib.KIND_MLA, r1 - r0,
+                                     host_seq_lens=None if st.host_lens is None else st.host_lens[r0:r1],
+                                     max_seq_len=bound, ctas_per_item=(H + 15) // 16, num_cus=ops._num_cus(q.device))
+                     for r0, r1 in chunks]
+            ws = ops.stream_workspace(max(plans, key=lambda p: ops.workspace_bytes(p, H, 512)), H, q.device)
+            st.plans[key] = (plans, ws)
+        plans, ws = st.plans[key]
         out = ops.mla_decode(
             q[..., :512], q[..., 512:], pool.get_key_buffer(layer_id), pool.get_row_scale(layer_id), st.table,
             st.seq_lens, k.reshape(bs, 576), sm_scale=float(layer.scaling), page_size=pool.page_size,
-            new_slots=st.slots if save else None, plan=st.plans[key], workspace=st.plans[key + ("ws",)])
+            new_slots=st.slots if save else None, plan=plans, workspace=ws, host_seq_lens=st.host_lens)
         return out.reshape(bs, H * 512)
 
     def _decode_dsa(self, q, k, layer, layer_id, st, bs, save, topk_indices):
@@ -355,12 +361,15 @@ class NeuronAttnBackend:
         idx = topk_indices.reshape(bs, -1)
         key = ("dsa", H, idx.shape[1])
         if key not in st.plans:
-            st.plans[key] = ops.plan_decode(_lib.KIND_DSA, bs, n_keys_per_row=idx.shape[1],
-                                            ctas_per_item=(H + 15) // 16, num_cus=ops._num_cus(q.device))
-            st.plans[key + ("ws",)] = ops.stream_workspace(st.plans[key], H, q.device)
+            chunks = ops.stream_row_chunks(_lib.KIND_DSA, bs, H, idx.shape[1])
+            plans = [ops.plan_decode(_lib.KIND_DSA, r1 - r0, n_keys_per_row=idx.shape[1], ctas_per_item=(H + 15) // 16,
+                                     num_cus=ops._num_cus(q.device)) for r0, r1 in chunks]
+            ws = ops.stream_workspace(max(plans, key=lambda p: ops.workspace_bytes(p, H, 512)), H, q.device)
+            st.plans[key] = (plans, ws)
+        plans, ws = st.plans[key]
         ctx, lse = ops.mla_decode_sparse(
             q[..., :512], q[..., 512:], pool.get_key_buffer(layer_id), pool.get_kv_scale(layer_id), idx, st.table,
             st.positions, k.reshape(bs, 576), sm_scale=float(layer.scaling), page_size=pool.page_size,
-            new_slots=st.slots if save else None, plan=st.plans[key], workspace=st.plans[key + ("ws",)])
+            new_slots=st.slots if save else None, plan=plans, workspace=ws)
         self.last_lse = lse
         return ctx.reshape(bs, H * 512)

@@ -33,10 +33,9 @@ int32_t host_tiles(int32_t seq_len, int32_t window, int32_t tile) { return host_
 // most kMlaMaxSplitKeys indices in LDS, and sparse rows are latency-bound gathers, so a sparse plan aims for 8 tiles
 // per workgroup (two per wave: every tile's gathers go out at once; measured on cfg5, 16 workgroups per 2048-index
 // row beat 8 by ~1.3 us and 4 by ~8 us).
-int plan_stream(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32_t n_keys_per_row, int32_t groups,
-                int32_t num_cus, sna_split_plan* plan) {
-  if (kind == 1 && !host_seq_lens)
-    return fail(SNA_ERR_INVALID_ARGUMENT, "plan_decode: an MLA plan needs host seq_lens (its launch uses them)");
+int plan_stream(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32_t max_seq_len, int32_t n_keys_per_row,
+                int32_t groups, int32_t num_cus, sna_split_plan* plan) {
+  plan->device_split = 0;
   if (B > SNA_MAX_PLAN_ROWS)
     return fail(SNA_ERR_UNSUPPORTED, "plan_decode: an MLA / DSA plan holds at most %d rows, not %d (split the batch)",
                 SNA_MAX_PLAN_ROWS, B);
@@ -44,6 +43,27 @@ int plan_stream(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32_t n
     return fail(SNA_ERR_UNSUPPORTED, "plan_decode: %d rows x %d head groups exceed the %d merge counters of a launch "
                 "(split the batch)", B, groups, kStreamMaxCounters);
   constexpr int32_t kSparseCap = kMlaMaxSplitKeys / 16;  // a sparse range's tiles: its indices resolve in LDS
+  if (kind == 1 && !host_seq_lens) {
+    // a plan from a bound: the launch cuts its split from the device's lengths, with a workgroup per CU and head
+    // group (whole rows while B fits them, equal ranges otherwise); only the workspace and the grid are fixed here
+    if (max_seq_len < 1 || max_seq_len - 1 > 65535 * 16)
+      return fail(SNA_ERR_UNSUPPORTED, "plan_decode: an MLA bound of %d (1 .. %d keys + 1)", max_seq_len, 65535 * 16);
+    const int32_t cus = std::max(1, std::min((num_cus > 0 ? num_cus : 256) / groups, SNA_MAX_CTAS));
+    plan->device_split = 1;
+    plan->tile = 16;
+    plan->batch = B;
+    plan->n_ctas = plan->n_work = plan->target_ctas = plan->max_splits = cus;
+    plan->total_tiles = 0;
+    plan->split_tiles = (max_seq_len - 1 + 15) / 16;
+    plan->empty_rows = -1;
+    plan->depth = 0;
+    plan->work_n = 0;
+    plan->wait_polls = kStreamWaitPolls;
+    for (int32_t w = 0; w <= SNA_MAX_CTAS; ++w) plan->cta_start[w] = 0;
+    for (int32_t w = 0; w < SNA_MAX_CTAS; ++w) plan->cta_row[w] = plan->cta_off[w] = 0;
+    for (int32_t b = 0; b < B; ++b) plan->row_keys[b] = max_seq_len - 1;
+    return SNA_OK;
+  }
   int64_t total = 0, min_pieces = 0;
   int32_t empty = 0, max_tiles = 0;
   for (int32_t b = 0; b < B; ++b) {
@@ -199,6 +219,7 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
   ApiGuard guard;
   const int32_t gqa_depth = plan ? plan->depth : 0;  // a caller may preset the plan shape it wants (2 or 3)
   if (!plan) return fail(SNA_ERR_INVALID_ARGUMENT, "plan_decode: null plan");
+  plan->device_split = 0;
   if (kind < 0 || kind > 2) return fail(SNA_ERR_INVALID_ARGUMENT, "plan_decode: unknown kind %d", kind);
   if (B < 0 || ctas_per_item < 1 || window < 0)
     return fail(SNA_ERR_INVALID_ARGUMENT, "plan_decode: bad arguments (B %d, ctas_per_item %d, window %d)", B,
@@ -207,7 +228,8 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
     return fail(SNA_ERR_INVALID_ARGUMENT, "plan_decode: negative index count %d", n_keys_per_row);
   if (kind != 2 && !host_seq_lens && max_seq_len < 0)
     return fail(SNA_ERR_INVALID_ARGUMENT, "plan_decode: need host seq_lens or max_seq_len >= 0");
-  if (kind != 0) return plan_stream(kind, host_seq_lens, B, n_keys_per_row, ctas_per_item, num_cus, plan);
+  if (kind != 0)
+    return plan_stream(kind, host_seq_lens, B, max_seq_len, n_keys_per_row, ctas_per_item, num_cus, plan);
   const int32_t tile = kind == 0 ? 32 : 16;
   const int32_t waves = 4;
   const int32_t cus = num_cus > 0 ? num_cus : 256;

@@ -69,6 +69,7 @@ struct MlaArgs {
   float* ws_o;         // [2 n_ctas, H, 512] partial contexts (unnormalized; ROWS640 in latent-byte order)
   float* ws_ml;        // [2 n_ctas, H, 2] their (max, sum), log2 domain
   int32_t* ws_cnt;     // arrival words [kStreamMaxCounters], (unused) [kStreamMaxCounters], finished workgroups [1]
+  const int32_t* seq_lens;  // paged [B] (device): a device-split launch cuts its stream from them
   uint16_t* out;
   float* lse_out;
   uint32_t cta_start[SNA_MAX_CTAS + 1];  // the stream split (sna_split_plan)
@@ -200,15 +201,19 @@ __device__ __forceinline__ float2 load_dev8(__amdgpu_buffer_rsrc_t r, uint32_t o
 }
 
 // The numbers of workgroups (of n) whose range starts at or before global tiles x0 and x1: the stream split's
-// starts, one per lane in four independent loads (so one memory round trip), counted by ballots.
-__device__ __forceinline__ void ctas_starting_by(const MlaArgs& a, uint32_t x0, uint32_t x1, int32_t& n0, int32_t& n1) {
+// starts, one per lane in four independent loads (so one memory round trip; a device split's from LDS, where the
+// entries past its ranges hold the stream's end), counted by ballots.
+template <bool DEV>
+__device__ __forceinline__ void ctas_starting_by(const MlaArgs& a, const uint32_t* dev_starts, uint32_t x0, uint32_t x1,
+                                                 int32_t& n0, int32_t& n1) {
   static_assert(SNA_MAX_CTAS <= 256, "four loads of 64 starts");
   const int lane = threadIdx.x & 63;
   uint32_t c[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int k = 64 * i + lane;
-    c[i] = k < a.n_ctas ? a.cta_start[k] : 0xffffffffu;
+    if constexpr (DEV) c[i] = dev_starts[k];
+    else c[i] = k < a.n_ctas ? a.cta_start[k] : 0xffffffffu;
   }
   int32_t s0 = 0, s1 = 0;
 #pragma unroll
@@ -218,6 +223,160 @@ __device__ __forceinline__ void ctas_starting_by(const MlaArgs& a, uint32_t x0, 
   }
   n0 = __builtin_amdgcn_readfirstlane(s0);
   n1 = __builtin_amdgcn_readfirstlane(s1);
+}
+
+// ---- the stream split cut on the device (a plan from a bound), so that one captured launch serves any lengths ----
+
+// Inclusive prefix sums over the wave's 64 lanes of four values per lane, scanned together (shuffles up).
+__device__ __forceinline__ void wave_incl_scan4(uint32_t (&v)[4]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    uint32_t t[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[i] = (uint32_t)__shfl_up((int)v[i], d, 64);
+    if (lane >= d) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] += t[i];
+    }
+  }
+}
+
+// ceil(x / t) for x < 2^17 and 1 <= t < 2^17, with rt = 1 / t: the float quotient is within one of the exact one,
+// and one correction each way makes it exact.
+__device__ __forceinline__ uint32_t ceil_div_small(uint32_t x, uint32_t t, float rt) {
+  uint32_t q = (uint32_t)((float)x * rt);
+  if (q * t > x) --q;
+  else if ((q + 1) * t <= x) ++q;
+  return q + (q * t < x ? 1u : 0u);
+}
+
+// Wave 0 of every workgroup of a device-split launch cuts the same stream split from the device's seq_lens (the
+// arithmetic is deterministic, so every workgroup gets the same one): the rows' key counts (seq_len - 1, held to the
+// table's width and the stream's 65535 tiles per row) into keys[b]; the ranges' starts into cs[w] (cs[w] = the
+// stream's end for w at or past the split's n, and cs[256] too); row << 16 | tile offset into cro[w]; n into *n_out.
+// With a workgroup for every row (B <= n, n = min(launched workgroups, tiles)) rows are apportioned whole: the least
+// piece length T with sum_b ceil(tiles_b / T) <= n is found by bisection, and row b is cut into ceil(tiles_b / T)
+// equal pieces (the same longest piece as the host planner's greedy apportionment, within a tile); otherwise the
+// stream is cut into n equal ranges. tmp: 5 x 256 words of LDS scratch.
+__device__ void device_split(const MlaArgs& a, uint32_t* cs, uint32_t* cro, int32_t* keys, int32_t* n_out,
+                             uint32_t* tmp) {
+  const int lane = threadIdx.x & 63;
+  const int32_t B = a.B;
+  const int32_t kmax = (int32_t)min((int64_t)a.table_width * a.P, (int64_t)65535 * 16);
+  uint32_t tiles[4], first[4], mx = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int32_t r = lane + 64 * i;
+    tiles[i] = 0;
+    if (r < B) {
+      const int32_t k = min(max(a.seq_lens[r] - 1, 0), kmax);
+      keys[r] = k;
+      tiles[i] = (uint32_t)max((k + 15) >> 4, 1);
+    }
+    first[i] = tiles[i];
+    mx = max(mx, tiles[i]);
+  }
+  wave_incl_scan4(first);
+  uint32_t total = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t part = (uint32_t)__shfl((int)first[i], 63, 64);
+    first[i] = total + first[i] - tiles[i];
+    total += part;
+  }
+  const uint32_t n = min((uint32_t)gridDim.x, total);
+  uint32_t* t_first = tmp;
+  uint32_t* t_tiles = tmp + 256;
+  uint32_t* t_pieces = tmp + 512;
+  uint32_t* t_pfirst = tmp + 768;
+  uint32_t* mark = tmp + 1024;  // row + 1 at the first workgroup of a row (0 elsewhere)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int32_t r = lane + 64 * i;
+    mark[r] = 0;
+    if (r < B) {
+      t_first[r] = first[i];
+      t_tiles[r] = tiles[i];
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  const bool whole = (uint32_t)B <= n;
+  uint32_t n_split = n;
+  if (whole) {
+    mx = (uint32_t)wave_max((float)mx);
+    uint32_t lo = max(1u, (total + n - 1) / n), hi = mx;
+    if (n > (uint32_t)B) hi = min(hi, (total + (n - B) - 1) / (n - B));  // feasible: sum <= total / T + B <= n
+    lo = min(lo, hi);
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi) >> 1;
+      const float rt = 1.0f / (float)mid;
+      uint32_t sum = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sum += ceil_div_small(tiles[i], mid, rt);
+      if ((uint32_t)wave_sum((float)sum) <= n) hi = mid;
+      else lo = mid + 1;
+    }
+    const float rt = 1.0f / (float)lo;
+    uint32_t pieces[4], pf[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pf[i] = pieces[i] = ceil_div_small(tiles[i], lo, rt);
+    wave_incl_scan4(pf);
+    n_split = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t part = (uint32_t)__shfl((int)pf[i], 63, 64);
+      pf[i] = n_split + pf[i] - pieces[i];
+      n_split += part;
+      const int32_t r = lane + 64 * i;
+      if (r < B) {
+        t_pieces[r] = pieces[i];
+        t_pfirst[r] = pf[i];
+        mark[pf[i]] = (uint32_t)r + 1;  // every row has a piece, so the firsts are distinct
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int32_t r = lane + 64 * i;
+      // the first range starting at or after the row's first tile: ceil(first * n / total)
+      const uint32_t w0 = r < B ? (uint32_t)(((uint64_t)first[i] * n + total - 1) / total) : n;
+      if (w0 < n) atomicMax(&mark[w0], (uint32_t)r + 1);
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  // a workgroup's row: the prefix maximum of the marks (lane l holds workgroups 4 l .. 4 l + 3)
+  uint32_t m[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) m[j] = mark[4 * lane + j];
+#pragma unroll
+  for (int j = 1; j < 4; ++j) m[j] = max(m[j], m[j - 1]);
+  uint32_t run = m[3];
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t t = (uint32_t)__shfl_up((int)run, d, 64);
+    if (lane >= d) run = max(run, t);
+  }
+  uint32_t before = (uint32_t)__shfl_up((int)run, 1, 64);
+  if (lane == 0) before = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t w = 4 * lane + j;
+    if (w < n_split) {
+      const uint32_t r = max(m[j], before) - 1;
+      const uint32_t off = whole ? (w - t_pfirst[r]) * t_tiles[r] / t_pieces[r]
+                                 : (uint32_t)((uint64_t)w * total / n) - t_first[r];
+      cs[w] = t_first[r] + off;
+      cro[w] = r << 16 | off;
+    } else {
+      cs[w] = total;
+      cro[w] = 0;
+    }
+  }
+  if (lane == 0) {
+    cs[256] = total;
+    *n_out = (int32_t)n_split;
+  }
 }
 
 // Merge of up to NC latent blocks (chunks[i]: dims 64 c .. 64 c + 63; -1 = none) of row b, head group hg, over its S
@@ -330,8 +489,10 @@ __device__ void merge_mask(const MlaArgs& a, __amdgpu_buffer_rsrc_t ro, __amdgpu
 // WIDE: a sparse pool past 4 GiB, whose rows take 64-bit addresses (every other pool is read through 32-bit buffer
 // offsets). MULTI: some workgroup's range spans several rows (a plan with more rows than workgroups); without it each
 // range is one segment, and the kernel is the segment loop's body once (the loop's carried state costs the one-segment
-// kernel its scalar registers).
-template <int FMT, bool WIDE, bool MULTI>
+// kernel its scalar registers). DEV: the stream split is cut from the device's seq_lens at the start of the launch
+// (device_split), not taken from the plan; the grid is the plan's bound, and workgroups past the split's ranges only
+// count themselves finished.
+template <int FMT, bool WIDE, bool MULTI, bool DEV = false>
 __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
   constexpr int WAVES = 4;
   using Geo = TileGeo<FMT>;
@@ -392,12 +553,33 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
       (void*)a.cache, (short)0, WIDE ? 0 : (int)(uint32_t)(a.num_blocks * a.P * ROWB), kBufferFlags);
   const float base_scale = a.sm_scale * kLog2e * (SPARSE ? a.kv_scale : 1.0f);
 
+  // ---- a device split: cut by wave 0 into LDS (the ring is scratch until the first DMA) ----
+  __shared__ uint32_t sm_cs[DEV ? SNA_MAX_CTAS + 1 : 1];
+  __shared__ uint32_t sm_cro[DEV ? SNA_MAX_CTAS : 1];
+  __shared__ int32_t sm_keys[DEV ? SNA_MAX_PLAN_ROWS : 1];
+  __shared__ int32_t sm_nsplit;
+  if constexpr (DEV) {
+    static_assert(sizeof(sm_ring) >= 5 * 256 * 4, "the split's scratch fits the ring");
+    if (wave == 0)
+      device_split(a, sm_cs, sm_cro, sm_keys, &sm_nsplit, reinterpret_cast<uint32_t*>(&sm_ring[0][0][0]));
+    __syncthreads();
+  }
+  auto cta_start = [&](int32_t k) -> uint32_t {
+    if constexpr (DEV) return __builtin_amdgcn_readfirstlane(sm_cs[k]);
+    else return a.cta_start[k];
+  };
+  auto row_keys = [&](int32_t r) -> int32_t {
+    if constexpr (DEV) return __builtin_amdgcn_readfirstlane(sm_keys[r]);
+    else return a.row_keys[r];
+  };
+  const uint32_t cro_w = DEV ? __builtin_amdgcn_readfirstlane(sm_cro[w]) : a.cta_row_off[w];
+
   // ---- the workgroup's range of the stream, one segment (a piece of one row) at a time ----
-  const uint32_t g_lo = a.cta_start[w], g_hi = a.cta_start[w + 1];
-  int32_t b = (int32_t)(a.cta_row_off[w] >> 16);
-  uint32_t row_t0 = g_lo - (a.cta_row_off[w] & 0xffffu);  // the global index of row b's first tile
+  const uint32_t g_lo = cta_start(w), g_hi = cta_start(w + 1);
+  int32_t b = (int32_t)(cro_w >> 16);
+  uint32_t row_t0 = g_lo - (cro_w & 0xffffu);  // the global index of row b's first tile
   for (uint32_t g = g_lo; g < g_hi; ++b) {
-    const int32_t khi = a.row_keys[b];  // the row's keys: positions [0, khi) (paged) or index entries (sparse)
+    const int32_t khi = row_keys(b);  // the row's keys: positions [0, khi) (paged) or index entries (sparse)
     const uint32_t row_t1 = row_t0 + (uint32_t)max((khi + 15) >> 4, 1);
     const uint32_t s_hi = min(g_hi, row_t1);
     const int32_t t_first = (int32_t)(g - row_t0);
@@ -407,7 +589,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     const bool first_seg = g == g_lo;                    // the partial slot: 2 w for the first segment, 2 w + 1 after
     // the row's first and last workgroups (for the merge of a split row), found with the prologue's loads
     int32_t wa, wb;
-    ctas_starting_by(a, row_t0, row_t1 - 1, wa, wb);
+    ctas_starting_by<DEV>(a, sm_cs, row_t0, row_t1 - 1, wa, wb);
     --wa;
     --wb;
     const int32_t kbase = t_first * 16;
@@ -1275,7 +1457,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     // (A workgroup whose range goes on into another row retracts at once.)
     if (!whole) {
       const int32_t S = wb - wa + 1;
-      const bool wa_second = a.cta_start[wa] != row_t0;        // the row is not wa's first segment
+      const bool wa_second = cta_start(wa) != row_t0;          // the row is not wa's first segment
       const int32_t pair = b * a.groups + hg;
       int32_t* arrive = a.ws_cnt + kCounterStride * pair;
       wait_vmcnt<0>();  // this wave's partial stores are complete (written through) before the count
@@ -1336,7 +1518,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
   if (tid == 0) {
     const int32_t done = __hip_atomic_fetch_add(a.ws_cnt + kCounterStride * 2 * kStreamMaxCounters, 1,
                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sm_word = done == a.n_ctas * a.groups - 1;
+    sm_word = done == (int32_t)(gridDim.x * gridDim.y) - 1;
   }
   __syncthreads();
   if (sm_word) {
@@ -1387,7 +1569,8 @@ static void fill_stream_args(MlaArgs& a, const sna_split_plan* plan, float* ws) 
   for (int32_t w = 0; w < plan->n_ctas; ++w) {
     a.cta_row_off[w] = (uint32_t)plan->cta_row[w] << 16 | plan->cta_off[w];
   }
-  for (int32_t b = 0; b < plan->batch; ++b) a.row_keys[b] = plan->row_keys[b];
+  if (!plan->device_split)
+    for (int32_t b = 0; b < plan->batch; ++b) a.row_keys[b] = plan->row_keys[b];
 }
 
 }  // namespace sna
@@ -1411,12 +1594,24 @@ extern "C" int sna_mla_decode(const void* ql_nope, const void* q_pe, const void*
                 (long long)table_stride);
   const int32_t groups = (num_heads + 15) / 16;
   bool multi = false;
-  if (int rc = check_plan(plan, B, groups, "mla_decode", &multi)) return rc;
+  const bool dev = plan && plan->device_split;
+  if (dev) {
+    // a plan from a bound: the launch cuts its stream from the device's seq_lens; whole rows when every row can have
+    // a workgroup, equal ranges across rows otherwise
+    if (plan->tile != 16 || plan->batch != B || plan->n_ctas < 1 || plan->n_ctas > SNA_MAX_CTAS)
+      return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode: missing or foreign split plan (made for %d rows)", plan->batch);
+    if (B > SNA_MAX_PLAN_ROWS || (int64_t)B * groups > kStreamMaxCounters)
+      return fail(SNA_ERR_UNSUPPORTED, "mla_decode: %d rows x %d head groups exceed the stream split's counters", B,
+                  groups);
+    multi = B > plan->n_ctas;
+  } else if (int rc = check_plan(plan, B, groups, "mla_decode", &multi)) {
+    return rc;
+  }
   if (B == 0) return SNA_OK;
   const int64_t need = sna_decode_workspace_bytes(plan, num_heads, kLatent);
-  if (!ql_nope || !q_pe || !cache || (!bf16 && !row_scale) || !block_table || !compact_new || !out || !workspace)
+  if (!ql_nope || !q_pe || !cache || (!bf16 && !row_scale) || !block_table || !compact_new || !out || !workspace ||
+      (dev && !seq_lens))
     return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode: null pointer");
-  (void)seq_lens;  // the plan's host lengths drive the launch
   if (!aligned(ql_nope, 16) || !aligned(q_pe, 16) || !aligned(cache, 16) || !aligned(compact_new, 16) ||
       (!bf16 && !aligned(row_scale, 16)) || !aligned(workspace, 256))
     return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode: q, cache and row_scale must be 16-byte aligned, the workspace "
@@ -1443,16 +1638,21 @@ extern "C" int sna_mla_decode(const void* ql_nope, const void* q_pe, const void*
   a.sm_scale = sm_scale;
   a.out = (uint16_t*)out;
   a.lse_out = nullptr;
+  a.seq_lens = seq_lens;  // read by a device-split launch only: an exact plan's host lengths drive the others
   fill_stream_args(a, plan, (float*)workspace);
   const dim3 grid(plan->n_ctas, groups);
   hipStream_t s = (hipStream_t)stream;
+#define SNA_MLA_LAUNCH(F, M, D) hipLaunchKernelGGL((mla_decode_kernel<F, false, M, D>), grid, dim3(256), 0, s, a)
   if (bf16) {
-    if (multi) hipLaunchKernelGGL((mla_decode_kernel<ROWS1152, false, true>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((mla_decode_kernel<ROWS1152, false, false>), grid, dim3(256), 0, s, a);
+    if (dev) { if (multi) SNA_MLA_LAUNCH(ROWS1152, true, true); else SNA_MLA_LAUNCH(ROWS1152, false, true); }
+    else if (multi) SNA_MLA_LAUNCH(ROWS1152, true, false);
+    else SNA_MLA_LAUNCH(ROWS1152, false, false);
   } else {
-    if (multi) hipLaunchKernelGGL((mla_decode_kernel<ROWS576, false, true>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((mla_decode_kernel<ROWS576, false, false>), grid, dim3(256), 0, s, a);
+    if (dev) { if (multi) SNA_MLA_LAUNCH(ROWS576, true, true); else SNA_MLA_LAUNCH(ROWS576, false, true); }
+    else if (multi) SNA_MLA_LAUNCH(ROWS576, true, false);
+    else SNA_MLA_LAUNCH(ROWS576, false, false);
   }
+#undef SNA_MLA_LAUNCH
   return check_launch("mla_decode");
 }
 
@@ -1472,6 +1672,9 @@ extern "C" int sna_mla_decode_sparse(const void* q_absorbed, const void* q_pe, c
                 table_width, (long long)table_stride, (double)kv_scale);
   const int32_t groups = (num_heads + 15) / 16;
   bool multi = false;
+  if (plan && plan->device_split)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode_sparse: a sparse plan is exact (its rows' key counts are the "
+                "index list's length); a device-split plan is for the paged MLA decode");
   if (int rc = check_plan(plan, B, groups, "mla_decode_sparse", &multi)) return rc;
   if (B == 0) return SNA_OK;
   for (int32_t b = 0; b < B; ++b)

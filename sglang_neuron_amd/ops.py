@@ -269,6 +269,9 @@ def check_plan_lengths(plan: _lib.SplitPlan, kind: int, host_seq_lens, window: i
         _need(sum(need) <= plan.n_work, f"the lengths need {sum(need)} split items, the plan runs {plan.n_work}")
     elif kind == _lib.KIND_MLA:
         for b, L in enumerate(lens):
+            if plan.device_split:  # a bound: the launch cuts its split from the device's lengths
+                _need(L - 1 <= plan.row_keys[b], f"row {b}: seq_len {L} is past the plan's bound {plan.row_keys[b] + 1}")
+                continue
             _need(plan.row_keys[b] == max(L - 1, 0),
                   f"row {b}: seq_len {L}, the plan was made for {plan.row_keys[b] + 1} (its launch is cut by them)")
 
@@ -327,6 +330,17 @@ def stream_row_chunks(kind: int, B: int, heads: int, n_keys_per_row: int = 0) ->
               "workgroups")
         rows = min(rows, _lib.MAX_CTAS // pieces)
     return [(r0, min(B, r0 + rows)) for r0 in range(0, B, rows)] or [(0, 0)]
+
+
+def _plans_of(plan, kind: int, B: int, heads: int, n_keys: int = 0):
+    """(row chunks, plans) of a caller's plan argument: one plan for the whole batch, or a list with one plan per
+    range of stream_row_chunks."""
+    if isinstance(plan, _lib.SplitPlan):
+        return [(0, B)], [plan]
+    chunks = stream_row_chunks(kind, B, heads, n_keys)
+    plans = list(plan)
+    _need(len(plans) == len(chunks), f"{len(plans)} plans for the {len(chunks)} launches a batch of {B} rows takes")
+    return chunks, plans
 
 
 def stream_workspace(plan: _lib.SplitPlan, heads: int, device: torch.device) -> Tensor:
@@ -446,7 +460,13 @@ def prepare_mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: 
                        new_slots: Optional[Tensor] = None, out: Optional[Tensor] = None, host_seq_lens=None,
                        plan: Optional[_lib.SplitPlan] = None, workspace: Optional[Tensor] = None) -> Prepared:
     """mla_decode's checks and argument binding, launched by calling the result. ``workspace``: a uint8 tensor from
-    stream_workspace (zeroed once, reused by calls ordered on one stream), or None for a new one."""
+    stream_workspace (zeroed once, reused by calls ordered on one stream), or None for a new one.
+
+    The plan: an exact one (from host lengths: ``host_seq_lens``, or seq_lens on the host) cuts the launch by those
+    lengths, so a call with one must carry the host lengths it is checked against; a device-split plan
+    (plan_decode(KIND_MLA, B, max_seq_len=bound)) lets the launch cut its split from the device's seq_lens, so one
+    prepared (or captured) launch serves any lengths up to the bound. Without a plan: exact from host lengths when
+    there are any, else a device split bounded by the block table's width."""
     dev = _on_gpu(ql_nope, q_pe, cache, row_scale, block_table, seq_lens, compact_new, new_slots, out)
     B, H, lat = ql_nope.shape
     _need(lat == 512 and q_pe.shape == (B, H, 64), "ql_nope [B, H, 512] and q_pe [B, H, 64]")
@@ -478,15 +498,20 @@ def prepare_mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: 
     _need(out.shape == (B, H, 512) and out.dtype == torch.bfloat16 and out.is_contiguous(), "bad out tensor")
     hl = _host_lens(seq_lens, host_seq_lens)
     if plan is not None:
-        if hl is not None:
-            check_plan_lengths(plan, _lib.KIND_MLA, hl)
-        chunks, plans = [(0, B)], [plan]
+        chunks, plans = _plans_of(plan, _lib.KIND_MLA, B, H)
+        for (r0, r1), pl in zip(chunks, plans):
+            if hl is not None:
+                check_plan_lengths(pl, _lib.KIND_MLA, hl[r0:r1])
+            else:
+                _need(bool(pl.device_split), "an exact MLA plan is cut by host lengths: pass host_seq_lens (or use a "
+                      "device-split plan, plan_decode(KIND_MLA, B, max_seq_len=...), for lengths only the device "
+                      "holds)")
     else:
-        # the launch runs on host lengths: read the device's once when the caller has no host copy
-        hl = hl if hl is not None else lens.cpu()
         chunks = stream_row_chunks(_lib.KIND_MLA, B, H)
-        plans = [plan_decode(_lib.KIND_MLA, r1 - r0, host_seq_lens=hl[r0:r1], ctas_per_item=(H + 15) // 16,
-                             num_cus=_num_cus(dev)) for r0, r1 in chunks]
+        bound = table.shape[1] * P
+        plans = [plan_decode(_lib.KIND_MLA, r1 - r0, host_seq_lens=None if hl is None else hl[r0:r1],
+                             max_seq_len=bound, ctas_per_item=(H + 15) // 16, num_cus=_num_cus(dev))
+                 for r0, r1 in chunks]
     ws = _stream_workspace_arg(workspace, max(plans, key=lambda p: workspace_bytes(p, H, 512)), H, dev)
     lib = _lib.load()
     calls = []
@@ -535,7 +560,7 @@ def prepare_mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, k
     pos = _contig(positions.reshape(-1).to(torch.int32), "positions")
     _need(pos.numel() == B, f"{pos.numel()} positions for {B} rows")
     if plan is not None:
-        chunks, plans = [(0, B)], [plan]
+        chunks, plans = _plans_of(plan, _lib.KIND_DSA, B, H, K)
     else:
         chunks = stream_row_chunks(_lib.KIND_DSA, B, H, K)
         plans = [plan_decode(_lib.KIND_DSA, r1 - r0, n_keys_per_row=K, ctas_per_item=(H + 15) // 16,

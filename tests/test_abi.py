@@ -206,8 +206,24 @@ def test_stream_row_chunks_fit_one_plan_each(lib):
     assert ops.stream_row_chunks(_lib.KIND_MLA, 40, 16) == [(0, 40)]
 
 
+def test_mla_plan_from_a_bound_is_a_device_split(lib):
+    """Without host lengths an MLA plan is a device split: the launch cuts its stream from the device's seq_lens, so
+    the plan fixes only the grid (a workgroup per CU and head group) and the workspace it is sized for."""
+    rc, p = _plan(lib, _lib.KIND_MLA, None, B=4, max_len=3000, ctas=2, cus=256)
+    assert rc == 0 and p.device_split == 1 and p.n_ctas == 128 and p.batch == 4 and p.tile == 16
+    assert list(p.row_keys[:4]) == [2999] * 4
+    assert lib.sna_decode_workspace_bytes(ctypes.byref(p), 32, 512) == 262144 + 2 * 128 * 32 * 514 * 4
+    rc, q = _plan(lib, _lib.KIND_MLA, [100, 200])
+    assert rc == 0 and q.device_split == 0
+    assert _plan(lib, _lib.KIND_MLA, None, B=4, max_len=16 * 65535 + 2)[0] == _lib.SNA_ERR_UNSUPPORTED
+    assert _plan(lib, _lib.KIND_MLA, None, B=4, max_len=0)[0] == _lib.SNA_ERR_UNSUPPORTED
+    # a sparse decode refuses it
+    rc = lib.sna_mla_decode_sparse(None, None, None, 1.0, None, 16, None, 0, 0, None, None, None, 0.1, None, None, 4,
+                                   16, 64, 10, ctypes.byref(p), None, 0, None)
+    assert rc == _lib.SNA_ERR_INVALID_ARGUMENT and b"device-split" in lib.sna_last_error()
+
+
 def test_stream_plan_refusals(lib):
-    assert _plan(lib, _lib.KIND_MLA, None, B=4, max_len=3000)[0] == _lib.SNA_ERR_INVALID_ARGUMENT  # no host lengths
     assert _plan(lib, _lib.KIND_MLA, [100] * 257)[0] == _lib.SNA_ERR_UNSUPPORTED  # past SNA_MAX_PLAN_ROWS
     assert _plan(lib, _lib.KIND_MLA, [16 * 65536])[0] == _lib.SNA_ERR_UNSUPPORTED  # a row past 65535 tiles
     assert _plan(lib, _lib.KIND_MLA, [0, 5])[0] == _lib.SNA_ERR_INVALID_ARGUMENT  # seq_len 0

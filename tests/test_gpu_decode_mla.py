@@ -41,6 +41,41 @@ def test_mla_decode_matches_oracle(name, over):
     assert torch.equal(scale.cpu(), scale_o), "row scales differ"
 
 
+# device-split plans (a bound: the block table's width): the launch cuts its split from the device's seq_lens
+DEVICE_SPLIT_CASES = [
+    ("ds-cfg3-small", {"B": 4, "lens": (1024, 4096)}, False),
+    ("ds-ragged", {"B": 9, "lens": (1, 300)}, False),
+    ("ds-cfg3-full", {}, False),
+    ("ds-one-row", {"B": 1, "lens": (7000, 7000)}, False),
+    # 128 heads: 8 head groups of 32 workgroups, fewer than the 40 rows: equal ranges across rows
+    ("ds-ranges-across-rows", {"B": 40, "H": 128, "lens": (1, 1500)}, False),
+    ("ds-bf16-page128", {"B": 6, "P": 128, "lens": (1024, 16384)}, True),
+]
+
+
+@pytest.mark.parametrize("name,over,bf16", DEVICE_SPLIT_CASES, ids=[c[0] for c in DEVICE_SPLIT_CASES])
+def test_mla_device_split_matches_oracle(name, over, bf16):
+    dev = torch.device("cuda", 0)
+    case = workloads.mla_case(overrides=over)
+    want, cache_o, scale_o = mla_oracle(case, bf16=bf16)
+    cache, scale = mla_gpu_pool(case, bf16=bf16)
+    table = case.block_table.to(dev)
+    groups = (case.H + 15) // 16
+    plan = ops.plan_decode(1, case.B, max_seq_len=table.shape[1] * case.P, ctas_per_item=groups,
+                           num_cus=ops._num_cus(dev))
+    announce(f"mla device split {name}: B={case.B} H={case.H} P={case.P} n_ctas={plan.n_ctas} "
+             f"lens={case.seq_lens.tolist()[:8]}")
+    assert plan.device_split == 1
+    out = ops.mla_decode(case.ql_nope.to(dev), case.q_pe.to(dev), cache, scale, table, case.seq_lens.to(dev),
+                         case.compact_new.to(dev), sm_scale=case.sm_scale, page_size=case.P,
+                         new_slots=case.new_slots.to(dev), plan=plan)
+    torch.cuda.synchronize()
+    assert_close_attn(out, want, name)
+    assert torch.equal(cache.cpu().view(torch.uint8), cache_o.view(torch.uint8)), "row pool differs"
+    if not bf16:
+        assert torch.equal(scale.cpu(), scale_o), "row scales differ"
+
+
 # bf16 rows, the reference's DeepSeek-V2 pool (models/catalog.py:230-231: bf16 KV at page 128)
 MLA_BF16_CASES = [
     ("bf16-cfg3-page128", {"B": 8, "P": 128, "lens": (1024, 16384)}),

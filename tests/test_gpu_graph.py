@@ -6,9 +6,11 @@ gives the eager call's bits; the library issues no memset or copy, so nothing el
 import pytest
 import torch
 
+from oracle import attention as oatt
+from oracle import store as ost
 from sglang_neuron_amd import ops, workloads
 from tests.conftest import announce
-from tests._harness import dsa_gpu_pool, mla_gpu_pool
+from tests._harness import assert_close_attn, dsa_gpu_pool, mla_gpu_pool
 
 pytestmark = pytest.mark.gpu
 REPLAYS = 4
@@ -70,8 +72,76 @@ def test_graph_mla():
     ql, qp, cn, slots = case.ql_nope.to("cuda"), case.q_pe.to("cuda"), case.compact_new.to("cuda"), \
         case.new_slots.to("cuda")
     _replay_matches(lambda: ops.prepare_mla_decode(ql, qp, cache, scale, table, lens, cn, sm_scale=case.sm_scale,
-                                                   page_size=case.P, new_slots=slots, plan=plan, workspace=ws),
+                                                   page_size=case.P, new_slots=slots, plan=plan, workspace=ws,
+                                                   host_seq_lens=case.seq_lens),
                     lambda out: [out])
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["fp8-rows", "bf16-rows"])
+def test_graph_mla_device_split_replays_growing_lengths(bf16):
+    """One MLA decode captured once with a device-split plan (a bound: the table's width), then replayed for three
+    steps in which every row grows by one token: before each replay the step's own rows and slots are copied into the
+    captured inputs and the device's seq_lens are incremented, nothing is planned again. Each step's output against
+    oracle.mla_decode over the pool as the oracle has it by then, and the pool (rows and scales) bit-exact after
+    every step."""
+    dev = torch.device("cuda", 0)
+    steps = 3
+    case = workloads.mla_case(overrides={"B": 5, "lens": (900, 5000)})
+    L0 = case.seq_lens - (steps - 1)  # the first step's lengths; the case's prior covers every later step's rows
+    P = case.P
+    rows_of = {}  # (row, position) -> its compact row
+    k = 0
+    for b, L in enumerate(case.seq_lens.tolist()):
+        for pos in range(L - 1):
+            rows_of[(b, pos)] = case.prior_rows[k]
+            k += 1
+    for b in range(case.B):
+        rows_of[(b, int(case.seq_lens[b]) - 1)] = case.compact_new[b]
+    slot_of = lambda b, pos: int(case.block_table[b, pos // P]) * P + pos % P  # noqa: E731
+    n = case.num_blocks * P
+    cache_o = torch.zeros(n, 576, dtype=torch.bfloat16 if bf16 else torch.uint8)
+    scale_o = None if bf16 else torch.zeros(n, dtype=torch.float32)
+    first = [(b, pos) for b in range(case.B) for pos in range(int(L0[b]) - 1)]
+    first_rows = torch.stack([rows_of[x] for x in first])
+    first_slots = torch.tensor([slot_of(*x) for x in first])
+    ost.kv_store_mla(first_rows, first_slots, cache_o, scale_o)
+    cache = torch.zeros(n, 576, dtype=cache_o.dtype, device=dev)
+    scale = None if bf16 else torch.zeros(n, dtype=torch.float32, device=dev)
+    ops.kv_store_mla(first_rows.to(dev), first_slots.to(dev), cache, scale)
+    table = case.block_table.to(dev)
+    lens = L0.to(torch.int32).to(dev)
+    ql, qp = case.ql_nope.to(dev), case.q_pe.to(dev)
+    new_rows = torch.zeros(case.B, 576, dtype=torch.bfloat16, device=dev)
+    new_slots = torch.zeros(case.B, dtype=torch.int64, device=dev)
+    plan = ops.plan_decode(1, case.B, max_seq_len=table.shape[1] * P, ctas_per_item=1, num_cus=ops._num_cus(dev))
+    assert plan.device_split == 1
+    ws = ops.stream_workspace(plan, case.H, dev)
+    announce(f"graph mla device split bf16={bf16}: B={case.B} n_ctas={plan.n_ctas} lens0={L0.tolist()}")
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        prep = ops.prepare_mla_decode(ql, qp, cache, scale, table, lens, new_rows, sm_scale=case.sm_scale, page_size=P,
+                                      new_slots=new_slots, plan=plan, workspace=ws)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            out = prep()
+    torch.cuda.synchronize()
+    for s_ in range(steps):
+        L = L0 + s_
+        rows = torch.stack([rows_of[(b, int(L[b]) - 1)] for b in range(case.B)])
+        slots = torch.tensor([slot_of(b, int(L[b]) - 1) for b in range(case.B)])
+        new_rows.copy_(rows.to(dev))
+        new_slots.copy_(slots.to(dev))
+        lens.copy_(L.to(torch.int32).to(dev))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        want = oatt.mla_decode(case.ql_nope, case.q_pe, cache_o, scale_o, case.block_table, L, rows,
+                               sm_scale=case.sm_scale, page_size=P)
+        ost.kv_store_mla(rows, slots, cache_o, scale_o)
+        assert_close_attn(out, want, f"device split step {s_}")
+        assert torch.equal(cache.cpu().view(torch.uint8), cache_o.view(torch.uint8)), f"step {s_}: row pool differs"
+        if not bf16:
+            assert torch.equal(scale.cpu(), scale_o), f"step {s_}: row scales differ"
 
 
 def test_graph_dsa():

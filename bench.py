@@ -19,11 +19,12 @@ One JSON line on stdout:
                 rocprofv3 counter summary (traffic_source says which), else null.
   cpu_baseline  the CPU oracle (a torch restatement of the reference's torch path) on a bounded sample of the same
                 workload, timed on this host's cores (2 warm-ups, median of 5 runs).
-  per_config    cfg1, cfg3, cfg4 (full and sliding-window layers), cfg5 and cfg3 over bf16 rows, each with
-                us_per_step, its roofline and cpu_baseline.
+  per_config    cfg1, cfg3, cfg4 (full and sliding-window layers), cfg5, cfg3 over bf16 rows and cfg5 as an MTP
+                verify step (8 query tokens per sequence), each with us_per_step, its roofline and cpu_baseline.
 
-Options: --config {1,2,3,4,4swa,5,3bf16} prints that workload's line alone (3bf16: cfg3 over bf16 rows, the
-reference's served DeepSeek-V2 pool); --config meta times the device-side decode
+Options: --config {1,2,3,4,4swa,5,3bf16,5mtp} prints that workload's line alone (3bf16: cfg3 over bf16 rows, the
+reference's served DeepSeek-V2 pool; 5mtp: cfg5 as GLM's MTP verify, 8 query tokens per sequence); --config meta
+times the device-side decode
 metadata (block table, window trim) instead, --config prefill the segmented prefill attention, --config indexer the
 DSA indexer, --config qkv the QKV writer, --config wire the PD page items; --all prints one line per workload;
 --no-per-config drops the per_config map; --gpus above 1 is refused, because this build measures one GPU.
@@ -313,34 +314,38 @@ def setup_mla(dev, bf16: bool = False):
     return steps, desc, case.kv_bytes_per_step(bf16), ["mla_decode_kernel"], mfma_flops, cpu_baseline, legs
 
 
-def setup_dsa(dev):
+def setup_dsa(dev, spec: int = 1):
     import torch
 
     from sglang_neuron_amd import ops, workloads
 
     t0 = time.time()
-    case = workloads.dsa_case(gen_device=dev)
+    case = workloads.dsa_case(gen_device=dev, overrides={"spec": spec})
     cache = workloads.dsa_pool(case, dev, gen_device=dev)
     pool_bytes = cache.numel()
     n = _copies(case.kv_bytes_per_step(), pool_bytes, 16)
     pools = [cache] + [cache.clone() for _ in range(n - 1)]
     torch.cuda.synchronize()
-    log(f"cfg5: B={case.B} H={case.H} K={case.indices.shape[1]} pool={pool_bytes / 1e9:.2f} GB x {n} copies, "
-        f"built in {time.time() - t0:.1f}s")
+    wl = "cfg5" if spec == 1 else f"cfg5-mtp{spec}"
+    log(f"{wl}: B={case.B} spec={spec} H={case.H} K={case.indices.shape[1]} pool={pool_bytes / 1e9:.2f} GB x {n} "
+        f"copies, built in {time.time() - t0:.1f}s")
     idx, table, pos = case.indices.to(dev), case.block_table.to(dev), case.positions.to(dev)
-    plan = ops.plan_decode(2, case.B, n_keys_per_row=case.indices.shape[1], ctas_per_item=1,
-                           num_cus=ops._num_cus(idx.device))
+    T = case.B * spec
+    keys = case.indices.shape[1] + spec - 1  # a token's keys: its index list, then its siblings' own rows
+    plan = ops.plan_decode(2, T, n_keys_per_row=keys, ctas_per_item=1, num_cus=ops._num_cus(idx.device))
     new_slots = case.new_slots.to(dev)
     steps = [ops.prepare_mla_decode_sparse(case.q_absorbed, case.q_pe, c, case.kv_scale, idx, table, pos,
                                            case.own_rows, sm_scale=case.sm_scale, page_size=case.P,
-                                           new_slots=new_slots, plan=plan) for c in pools]
+                                           new_slots=new_slots, plan=plan, spec=spec) for c in pools]
     legs = {"store": [functools.partial(ops.kv_store_dsa, case.own_rows, new_slots, c, case.kv_scale) for c in pools],
             "decode": [ops.prepare_mla_decode_sparse(case.q_absorbed, case.q_pe, c, case.kv_scale, idx, table, pos,
                                                      case.own_rows, sm_scale=case.sm_scale, page_size=case.P,
-                                                     plan=plan) for c in pools]}
-    tiles = case.B * (-(-case.indices.shape[1] // 16))
+                                                     plan=plan, spec=spec) for c in pools]}
+    tiles = T * (-(-keys // 16))
     mfma_flops = tiles * (18 * 16 * 16 * 32 * 2 + 32 * 16 * 16 * 16 * 2)
-    desc = {"workload": "cfg5: glm-5.2-style DSA absorbed MLA", "batch": case.B, "q_heads": case.H,
+    desc = {"workload": f"{wl}: glm-5.2-style DSA absorbed MLA" + (f", MTP verify ({spec} query tokens per sequence)"
+                                                                    if spec > 1 else ""),
+            "batch": case.B, "query_tokens_per_seq": spec, "q_heads": case.H,
             "indices_per_row": case.indices.shape[1], "pool_positions_per_seq": case.pool_positions,
             "page_size": case.P, "kv_dtype": "fp8_e4m3fn latent + bf16 rope, 640-byte rows, kv_scale 2^-6",
             "short_rows": list(workloads.DSA_CONFIG["short_rows"]), "pool_copies": n,
@@ -352,10 +357,11 @@ def setup_dsa(dev):
         c0 = pools[0].cpu()
         qa, qp, own = case.q_absorbed.cpu(), case.q_pe.cpu(), case.own_rows.cpu()
 
-        def run(nrows):
-            oatt.mla_decode_sparse(qa[:nrows], qp[:nrows], c0, case.kv_scale, case.indices[:nrows],
-                                   case.block_table[:nrows], case.positions[:nrows], own[:nrows],
-                                   case.new_slots[:nrows], sm_scale=case.sm_scale, page_size=case.P, inplace=True)
+        def run(nseq):  # the first nseq sequences (their spec tokens each)
+            t = nseq * spec
+            oatt.mla_decode_sparse(qa[:t], qp[:t], c0, case.kv_scale, case.indices[:t], case.block_table[:nseq],
+                                   case.positions[:t], own[:t], case.new_slots[:t], sm_scale=case.sm_scale,
+                                   page_size=case.P, inplace=True, spec=spec)
 
         return _time_rows(run, case.B, budget_s)
 
@@ -785,7 +791,7 @@ def run_prefill(steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) ->
     return line
 
 
-DECODE_CONFIGS = ("2", "1", "3", "4", "4swa", "5", "3bf16")
+DECODE_CONFIGS = ("2", "1", "3", "4", "4swa", "5", "3bf16", "5mtp")
 
 
 def setup(key: str, dev):
@@ -799,6 +805,10 @@ def setup(key: str, dev):
         return setup_mla(dev, key == "3bf16")
     if key == "5":
         return setup_dsa(dev)
+    if key == "5mtp":
+        from sglang_neuron_amd import workloads
+
+        return setup_dsa(dev, workloads.DSA_MTP_SPEC)
     raise SystemExit(f"unknown config {key}")
 
 
@@ -911,7 +921,7 @@ def run_one(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: float, d
         line["per_config"] = {}
         for k in per_config:
             pm = measure_decode(k, steps_n, warmup, cpu, cpu_budget * 2 / 3, dev)
-            name = "cfg" + k.replace("swa", "-swa128").replace("bf16", "-bf16")
+            name = "cfg" + k.replace("swa", "-swa128").replace("bf16", "-bf16").replace("mtp", "-mtp8")
             pm["workload"] = pm["config"]["workload"]
             line["per_config"][name] = pm
     return line

@@ -315,14 +315,18 @@ int sna_mla_decode(const void *ql_nope, const void *q_pe, const void *cache, con
                    int32_t num_heads, int32_t page_size, int64_t num_blocks, int32_t cache_dtype,
                    const sna_split_plan *plan, void *workspace, int64_t workspace_bytes, void *stream);
 
-/* DSA sparse absorbed-MLA decode over 640-byte packed rows (one query token per sequence, one CP rank).
+/* DSA sparse absorbed-MLA decode over 640-byte packed rows (spec query tokens per sequence, one CP rank).
+ *   B            query tokens: B / spec sequences of spec tokens each (spec 1: one per sequence; GLM's MTP verify
+ *                runs spec 8), sequence s owning rows s * spec .. s * spec + spec - 1.
  *   q_absorbed   [B, num_heads, 512] bf16; q_pe [B, num_heads, 64] bf16.
  *   cache        [num_blocks * page_size, 640] uint8 (sna_kv_store_dsa's layout); kv_scale is per tensor.
- *   indices      [B, n_indices] int32 global token positions; < 0 entries are empty.
- *   block_table  [B, table_stride] int32 (logical block -> physical block); `table_width` valid columns.
- *   positions    [B] int32, the query token's absolute position.
- *   own_rows     [B, 576] bf16 in [k_pe | latent] order: the step's rows, attended in-band from their packed bytes
- *                (mla_decode_attention_torch.py:181-190).
+ *   indices      [B, n_indices] int32 global token positions, per query token; < 0 entries are empty.
+ *   block_table  [B / spec, table_stride] int32 per sequence (logical block -> physical block); `table_width` valid
+ *                columns.
+ *   positions    [B] int32, each query token's absolute position.
+ *   own_rows     [B, 576] bf16 in [k_pe | latent] order: the step's rows. Each token attends its own row and its
+ *                sequence's other spec - 1 rows from their packed bytes, at their positions (kept iff <= its own),
+ *                whatever their slots or table entries (mla_decode_attention_torch.py:89-103, 181-190).
  *   new_slots    [B] int64 or NULL: the cache rows the own rows are stored to in this launch, bit-exact with
  *                sna_kv_store_dsa (a slot < 0 or past the cache is skipped; of rows sharing a slot the last one's
  *                bytes land). As in the reference, where steps 0-1 store every own row before any gather, an index
@@ -332,13 +336,15 @@ int sna_mla_decode(const void *ql_nope, const void *q_pe, const void *cache, con
  * Position pos resolves to row table[pos / page_size] * page_size + pos % page_size. It is dropped when pos < 0,
  * its block is outside the table or unallocated, or the row is outside the cache. A resolved key is kept iff
  * pos <= position, and the own row always is.
- * Replaces: mla_decode_attention_torch_ref with spec = 1, cp_degree = 1 (mla_decode_attention_torch.py:38-130).
+ * plan: from sna_plan_decode(kind 2) with n_keys_per_row = n_indices + spec - 1 (a row's keys: its index list, then
+ * its siblings' rows).
+ * Replaces: mla_decode_attention_torch_ref with cp_degree = 1 (mla_decode_attention_torch.py:38-130).
  * On Trainium that is mla_decode_attention (models/glm52/kernels/decode/attention/mla/mla_decode_attention.py:207). */
 int sna_mla_decode_sparse(const void *q_absorbed, const void *q_pe, const void *cache, float kv_scale,
                           const int32_t *indices, int32_t n_indices, const int32_t *block_table, int64_t table_stride,
                           int32_t table_width, const int32_t *positions, const void *own_rows,
                           const int64_t *new_slots, float sm_scale, void *ctx_out, float *lse_out, int32_t B,
-                          int32_t num_heads, int32_t page_size,
+                          int32_t spec, int32_t num_heads, int32_t page_size,
                           int64_t num_blocks, const sna_split_plan *plan, void *workspace, int64_t workspace_bytes,
                           void *stream);
 

@@ -180,18 +180,21 @@ def mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: Optional
 
 def mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, kv_scale: float, indices: Tensor,
                       block_table: Tensor, positions: Tensor, own_rows: Tensor, new_slots: Tensor, *,
-                      sm_scale: float, page_size: int, inplace: bool = False) -> tuple[Tensor, Tensor, Tensor]:
-    """(ctx [B, H, 512] bf16, lse [B, H] fp32, cache) of the DSA absorbed-MLA decode with one query token per
-    sequence and one CP rank: mla_decode_attention_torch_ref (models/glm52/kernels/decode/attention/mla/
-    mla_decode_attention_torch.py:38-130) with spec = 1, cp_degree = 1, cp_rank = 0.
+                      sm_scale: float, page_size: int, inplace: bool = False,
+                      spec: int = 1) -> tuple[Tensor, Tensor, Tensor]:
+    """(ctx [B, H, 512] bf16, lse [B, H] fp32, cache) of the DSA absorbed-MLA decode of B query tokens, ``spec`` per
+    sequence (sequence s owns tokens s * spec .. s * spec + spec - 1 and table row s), on one CP rank:
+    mla_decode_attention_torch_ref (models/glm52/kernels/decode/attention/mla/mla_decode_attention_torch.py:38-130)
+    with cp_degree = 1, cp_rank = 0.
 
     Steps 0-1 pack ``own_rows`` [B, 576] ([k_pe | latent] order) and scatter them at ``new_slots`` into a copy of
-    ``cache`` [rows, 640] before any read. Step 2 resolves each index pos >= 0 to row table[pos // P] * P + pos % P
-    (_gather_token_keys, :162-179; dropped when its block is past the table, unallocated, or the row is outside the
-    cache), and appends the own row from its packed bytes (:185-189). Step 4 keeps key_pos <= position. Step 5 gives
-    ctx = softmax . latent and lse = max + log(sum) (:117-121); a row with no kept key gives ctx 0 and lse -inf
-    (:122-128). ``inplace`` writes the own rows into ``cache`` itself instead of a copy (the reference copies,
-    :193-196; the CPU baseline times the in-place form)."""
+    ``cache`` [rows, 640] before any read. Step 2, per token: each index pos >= 0 resolves to row
+    table[s, pos // P] * P + pos % P (_gather_token_keys, :162-179; dropped when its block is past the table,
+    unallocated, or the row is outside the cache), and the sequence's spec own rows are appended from their packed
+    bytes at their positions (:185-189). Step 4 keeps key_pos <= the token's position (its own row and its earlier
+    siblings). Step 5 gives ctx = softmax . latent and lse = max + log(sum) (:117-121); a token with no kept key gives
+    ctx 0 and lse -inf (:122-128). ``inplace`` writes the own rows into ``cache`` itself instead of a copy (the
+    reference copies, :193-196; the CPU baseline times the in-place form)."""
     B, H, _ = q_absorbed.shape
     P = page_size
     if not inplace:
@@ -204,11 +207,12 @@ def mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, kv_scale:
     lse = torch.empty(B, H, dtype=torch.float32)
     Wt = block_table.shape[1]
     for b in range(B):
+        seq = b // spec
         sel = indices[b].to(torch.int64)
         pos_q = int(positions[b])
         blk = torch.where(sel >= 0, sel // P, torch.full_like(sel, -1))
         in_table = (blk >= 0) & (blk < Wt)
-        tab = torch.where(in_table, block_table[b].to(torch.int64)[blk.clamp(min=0, max=Wt - 1)],
+        tab = torch.where(in_table, block_table[seq].to(torch.int64)[blk.clamp(min=0, max=Wt - 1)],
                           torch.full_like(sel, -1))
         row = tab * P + sel % P
         resident = in_table & (tab >= 0) & (row >= 0) & (row < n_rows)
@@ -216,9 +220,9 @@ def mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, kv_scale:
         keys = torch.zeros(sel.numel(), 576)
         if bool(resident.any()):
             keys[resident] = st.unpack_kv_row(flat[row[resident]], kv_scale)
-        own = st.unpack_kv_row(packed_own[b:b + 1], kv_scale)
+        own = st.unpack_kv_row(packed_own[seq * spec:(seq + 1) * spec], kv_scale)  # the sequence's own rows
         keys = torch.cat([keys, own], dim=0)
-        key_pos = torch.cat([key_pos, torch.tensor([float(pos_q)])])
+        key_pos = torch.cat([key_pos, positions[seq * spec:(seq + 1) * spec].float()])
         k_pe, latent = keys[:, :64], keys[:, 64:]
         scores = sm_scale * (q_absorbed[b].float() @ latent.T + q_pe[b].float() @ k_pe.T)  # [H, K+1]
         keep = key_pos <= float(pos_q)

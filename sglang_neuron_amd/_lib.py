@@ -80,7 +80,7 @@ SIGNATURES = {
     "sna_mla_decode": (_I32, [_P, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _F32, _P, _I32, _I32, _I32, _I64, _I32,
                               ctypes.POINTER(SplitPlan), _P, _I64, _P]),
     "sna_mla_decode_sparse": (_I32, [_P, _P, _P, _F32, _P, _I32, _P, _I64, _I32, _P, _P, _P, _F32, _P, _P, _I32,
-                                     _I32, _I32, _I64, ctypes.POINTER(SplitPlan), _P, _I64, _P]),
+                                     _I32, _I32, _I32, _I64, ctypes.POINTER(SplitPlan), _P, _I64, _P]),
     "sna_lse_combine": (_I32, [_P, _P, _I32, _I64, _I32, _P, _P, _P]),
     "sna_prefill_attention": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P, _I32, _I32, _P, _F32, _I32, _P,
                                      _I32, _I32, _I32, _I32, _I64, _I32, _P]),

@@ -58,6 +58,7 @@ struct MlaArgs {
   int32_t table_width;
   const int32_t* indices;    // sparse [B, n_indices]
   int32_t n_indices;
+  int32_t spec;              // sparse: query tokens per sequence (rows s * spec .. + spec - 1 share table row s)
   const int32_t* positions;  // sparse [B]
   const uint16_t* own;       // [B, 576] bf16: ROWS576 [latent | rope], ROWS640 [rope | latent]
   const int64_t* new_slots;  // store the own rows there (NULL: the caller has stored them)
@@ -593,7 +594,9 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     --wa;
     --wb;
     const int32_t kbase = t_first * 16;
-    const int32_t* trow = a.table + (int64_t)b * a.table_stride;
+    // the row's sequence: its table row (sparse: spec query tokens per sequence)
+    const int32_t seq = SPARSE ? b / a.spec : b;
+    const int32_t* trow = a.table + (int64_t)seq * a.table_stride;
     const int32_t ntiles = t_last - t_first;
 
     // ---- prologue: the segment's block-table entries (paged), the query operand, the own row ----
@@ -722,16 +725,31 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     // Sparse: every index of the segment to a row id (-1: skipped), all loads of a stage in flight together. With
     // new_slots, a row that some batch row's own row is stored to in this launch becomes -2 - (that batch row): its
     // bytes are packed from the source row after the tile lands, so no gather depends on when the store lands.
+    // With spec query tokens per sequence, a row's keys are its index list and then its spec - 1 siblings' own rows
+    // (the other tokens of its sequence, in order), each -2 - (the sibling's batch row) at the sibling's position and
+    // kept iff that position <= the row's: the reference appends every sibling's packed row
+    // (mla_decode_attention_torch.py:89-103, 185-190) whatever its slot or table entry.
     if constexpr (SPARSE) {
       constexpr int KPT = kMlaMaxSplitKeys / NT;
       const int32_t nkeys = ntiles * 16;
       const int32_t qpos = a.positions[b];
       const int64_t n_rows = a.num_blocks * a.P;
-      int32_t pos[KPT];
+      const int32_t jj = b - seq * a.spec;  // the row's token within its sequence
+      int32_t pos[KPT], sib[KPT];
 #pragma unroll
       for (int i = 0; i < KPT; ++i) {
         const int32_t k = tid + i * NT, key = kbase + k;
-        pos[i] = (k < nkeys && key < khi) ? a.indices[(int64_t)b * a.n_indices + key] : -1;
+        pos[i] = -1;
+        sib[i] = -1;
+        if (k < nkeys && key < khi) {
+          if (key < a.n_indices) {
+            pos[i] = a.indices[(int64_t)b * a.n_indices + key];
+          } else {
+            const int32_t e = key - a.n_indices;
+            sib[i] = seq * a.spec + e + (e >= jj ? 1 : 0);
+            pos[i] = a.positions[sib[i]];
+          }
+        }
       }
       // thread e's row's new slot (B <= SNA_MAX_PLAN_ROWS = NT), loaded beside the indices: the barriers below wait
       // for every load in flight, so a load issued after one costs a round trip of its own
@@ -779,20 +797,24 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
 #pragma unroll
       for (int i = 0; i < KPT; ++i) {
         ent[i] = -1;
-        if (pos[i] >= 0 && pos[i] <= qpos && pos[i] / a.P < a.table_width) ent[i] = trow[pos[i] / a.P];
+        if (sib[i] < 0 && pos[i] >= 0 && pos[i] <= qpos && pos[i] / a.P < a.table_width) ent[i] = trow[pos[i] / a.P];
       }
 #pragma unroll
       for (int i = 0; i < KPT; ++i) {
         const int32_t k = tid + i * NT;
         if (k >= nkeys) continue;
         int32_t row = -1;
-        if (ent[i] >= 0 && (int64_t)ent[i] < a.num_blocks) {
-          const int64_t r = (int64_t)ent[i] * a.P + pos[i] % a.P;
-          if (r < n_rows) row = (int32_t)r;
-        }
-        if (row >= 0 && a.new_slots) {
-          const int32_t src = slot_lookup(hkey, hval, row);
-          if (src >= 0) row = -2 - src;
+        if (sib[i] >= 0) {
+          if (pos[i] <= qpos) row = -2 - sib[i];  // a sibling's own row, packed from its source
+        } else {
+          if (ent[i] >= 0 && (int64_t)ent[i] < a.num_blocks) {
+            const int64_t r = (int64_t)ent[i] * a.P + pos[i] % a.P;
+            if (r < n_rows) row = (int32_t)r;
+          }
+          if (row >= 0 && a.new_slots) {
+            const int32_t src = slot_lookup(hkey, hval, row);
+            if (src >= 0) row = -2 - src;
+          }
         }
         sm_rowid[k] = row;
       }
@@ -1332,7 +1354,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
             vm = tile_mask(t0 + i * WAVES);
             if constexpr (SPARSE) {
               // rare: the gathers read a slot this launch stores an own row to (the loads drain first)
-              if (const uint32_t al = a.new_slots ? tile_aliases(t0 + i * WAVES) : 0u) {
+              if (const uint32_t al = (a.new_slots || a.spec > 1) ? tile_aliases(t0 + i * WAVES) : 0u) {
                 wait_vmcnt<0>();
                 patch_aliases(T, t0 + i * WAVES, al);
               }
@@ -1630,6 +1652,7 @@ extern "C" int sna_mla_decode(const void* ql_nope, const void* q_pe, const void*
   a.table_width = table_width;
   a.own = (const uint16_t*)compact_new;
   a.new_slots = new_slots;
+  a.spec = 1;
   a.B = B;
   a.H = num_heads;
   a.P = page_size;
@@ -1660,7 +1683,7 @@ extern "C" int sna_mla_decode_sparse(const void* q_absorbed, const void* q_pe, c
                                      const int32_t* indices, int32_t n_indices, const int32_t* block_table,
                                      int64_t table_stride, int32_t table_width, const int32_t* positions,
                                      const void* own_rows, const int64_t* new_slots, float sm_scale, void* ctx_out,
-                                     float* lse_out, int32_t B,
+                                     float* lse_out, int32_t B, int32_t spec,
                                      int32_t num_heads, int32_t page_size, int64_t num_blocks,
                                      const sna_split_plan* plan, void* workspace, int64_t workspace_bytes,
                                      void* stream) {
@@ -1670,6 +1693,10 @@ extern "C" int sna_mla_decode_sparse(const void* q_absorbed, const void* q_pe, c
     return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode_sparse: bad sizes (B %d, heads %d, indices %d, page %d, blocks "
                 "%lld, table %d/%lld, kv_scale %g)", B, num_heads, n_indices, page_size, (long long)num_blocks,
                 table_width, (long long)table_stride, (double)kv_scale);
+  if (spec < 1 || B % spec)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode_sparse: %d query tokens are not whole sequences of spec %d", B,
+                spec);
+  const int32_t row_keys = n_indices + spec - 1;  // the index list, then the spec - 1 siblings' own rows
   const int32_t groups = (num_heads + 15) / 16;
   bool multi = false;
   if (plan && plan->device_split)
@@ -1678,9 +1705,9 @@ extern "C" int sna_mla_decode_sparse(const void* q_absorbed, const void* q_pe, c
   if (int rc = check_plan(plan, B, groups, "mla_decode_sparse", &multi)) return rc;
   if (B == 0) return SNA_OK;
   for (int32_t b = 0; b < B; ++b)
-    if (plan->row_keys[b] != n_indices)
-      return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode_sparse: the plan was made for %d indices per row, not %d",
-                  plan->row_keys[b], n_indices);
+    if (plan->row_keys[b] != row_keys)
+      return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode_sparse: the plan was made for %d keys per row, not %d (%d "
+                  "indices and %d siblings)", plan->row_keys[b], row_keys, n_indices, spec - 1);
   for (int32_t w = 0; w < plan->n_ctas; ++w)
     if (plan->cta_start[w + 1] - plan->cta_start[w] > (uint32_t)(kMlaMaxSplitKeys / 16))
       return fail(SNA_ERR_INVALID_ARGUMENT, "mla_decode_sparse: plan workgroup %d holds more than %d index tiles", w,
@@ -1706,6 +1733,7 @@ extern "C" int sna_mla_decode_sparse(const void* q_absorbed, const void* q_pe, c
   a.table_width = table_width;
   a.indices = indices;
   a.n_indices = n_indices;
+  a.spec = spec;
   a.positions = positions;
   a.own = (const uint16_t*)own_rows;
   a.new_slots = new_slots;

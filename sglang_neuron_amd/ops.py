@@ -317,27 +317,30 @@ def _stream_workspace_arg(ws: Optional[Tensor], plan: _lib.SplitPlan, heads: int
     return ws
 
 
-def stream_row_chunks(kind: int, B: int, heads: int, n_keys_per_row: int = 0) -> list[tuple[int, int]]:
+def stream_row_chunks(kind: int, B: int, heads: int, n_keys_per_row: int = 0, spec: int = 1) -> list[tuple[int, int]]:
     """Row ranges [r0, r1) that split an MLA / DSA batch into launches each one plan can hold: at most MAX_PLAN_ROWS
     rows, at most STREAM_MAX_COUNTERS merge counters (rows x 16-head groups), and for DSA at most MAX_CTAS workgroups
-    of at most SPARSE_MAX_RANGE_KEYS indices (a row of K indices takes ceil(K / 2048) of them). One range for the
-    batches of the measured configurations; the launches of a split batch run one after another on the stream."""
+    of at most SPARSE_MAX_RANGE_KEYS keys (a row of K keys takes ceil(K / 2048) of them), whole sequences of ``spec``
+    query tokens each (a token attends its siblings' rows in its own launch). One range for the batches of the
+    measured configurations; the launches of a split batch run one after another on the stream."""
     groups = (heads + 15) // 16
     rows = min(_lib.MAX_PLAN_ROWS, _lib.STREAM_MAX_COUNTERS // groups)
     if kind == _lib.KIND_DSA:
         pieces = max(1, -(-int(n_keys_per_row) // _lib.SPARSE_MAX_RANGE_KEYS))
-        _need(pieces <= _lib.MAX_CTAS, f"a DSA row of {n_keys_per_row} indices needs more than {_lib.MAX_CTAS} "
+        _need(pieces <= _lib.MAX_CTAS, f"a DSA row of {n_keys_per_row} keys needs more than {_lib.MAX_CTAS} "
               "workgroups")
         rows = min(rows, _lib.MAX_CTAS // pieces)
+    rows -= rows % spec
+    _need(rows >= spec, f"a sequence of {spec} query tokens does not fit one launch")
     return [(r0, min(B, r0 + rows)) for r0 in range(0, B, rows)] or [(0, 0)]
 
 
-def _plans_of(plan, kind: int, B: int, heads: int, n_keys: int = 0):
+def _plans_of(plan, kind: int, B: int, heads: int, n_keys: int = 0, spec: int = 1):
     """(row chunks, plans) of a caller's plan argument: one plan for the whole batch, or a list with one plan per
     range of stream_row_chunks."""
     if isinstance(plan, _lib.SplitPlan):
         return [(0, B)], [plan]
-    chunks = stream_row_chunks(kind, B, heads, n_keys)
+    chunks = stream_row_chunks(kind, B, heads, n_keys, spec)
     plans = list(plan)
     _need(len(plans) == len(chunks), f"{len(plans)} plans for the {len(chunks)} launches a batch of {B} rows takes")
     return chunks, plans
@@ -540,7 +543,8 @@ def mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: Tensor, 
 def prepare_mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, kv_scale: float, indices: Tensor,
                               block_table: Tensor, positions: Tensor, own_rows: Tensor, *, sm_scale: float,
                               page_size: int, new_slots: Optional[Tensor] = None,
-                              plan: Optional[_lib.SplitPlan] = None, workspace: Optional[Tensor] = None) -> Prepared:
+                              plan: Optional[_lib.SplitPlan] = None, workspace: Optional[Tensor] = None,
+                              spec: int = 1) -> Prepared:
     """mla_decode_sparse's checks and argument binding (with ``new_slots``, the own rows are stored by the same launch),
     launched by calling the result."""
     dev = _on_gpu(q_absorbed, q_pe, cache, indices, block_table, positions, own_rows, new_slots)
@@ -555,15 +559,20 @@ def prepare_mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, k
     own_rows = _contig(own_rows.reshape(B, 576), "own_rows", torch.bfloat16)
     idx = _contig(indices.reshape(B, -1).to(torch.int32), "indices")
     K = idx.shape[1]
+    spec = int(spec)
+    _need(spec >= 1 and B % spec == 0, f"{B} query tokens are not whole sequences of {spec}")
+    S = B // spec
     table = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
-    _need(table.dim() == 2 and table.shape[0] == B and table.stride(1) == 1, f"block_table must be [{B}, width]")
+    _need(table.dim() == 2 and table.shape[0] == S and table.stride(1) == 1,
+          f"block_table must be [{S}, width] (one row per sequence)")
     pos = _contig(positions.reshape(-1).to(torch.int32), "positions")
     _need(pos.numel() == B, f"{pos.numel()} positions for {B} rows")
+    nkeys = K + spec - 1  # a row's keys: its index list, then its spec - 1 siblings' own rows
     if plan is not None:
-        chunks, plans = _plans_of(plan, _lib.KIND_DSA, B, H, K)
+        chunks, plans = _plans_of(plan, _lib.KIND_DSA, B, H, nkeys, spec)
     else:
-        chunks = stream_row_chunks(_lib.KIND_DSA, B, H, K)
-        plans = [plan_decode(_lib.KIND_DSA, r1 - r0, n_keys_per_row=K, ctas_per_item=(H + 15) // 16,
+        chunks = stream_row_chunks(_lib.KIND_DSA, B, H, nkeys, spec)
+        plans = [plan_decode(_lib.KIND_DSA, r1 - r0, n_keys_per_row=nkeys, ctas_per_item=(H + 15) // 16,
                              num_cus=_num_cus(dev)) for r0, r1 in chunks]
     ws = _stream_workspace_arg(workspace, max(plans, key=lambda p: workspace_bytes(p, H, 512)), H, dev)
     ctx = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
@@ -584,9 +593,10 @@ def prepare_mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, k
     for (r0, r1), pl in zip(chunks, plans):
         calls.append((lib.sna_mla_decode_sparse, (
             _ptr(q_absorbed[r0:r1]), _ptr(q_pe[r0:r1]), _ptr(cache), float(kv_scale), _ptr(idx[r0:r1]), K,
-            _ptr(table[r0:r1]), table.stride(0), table.shape[1], _ptr(pos[r0:r1]), _ptr(own_rows[r0:r1]),
-            None if fused_slots is None else _ptr(fused_slots[r0:r1]), float(sm_scale), _ptr(ctx[r0:r1]),
-            _ptr(lse[r0:r1]), r1 - r0, H, P, n_rows // P, pl, _ptr(ws), ws.numel(), _stream(dev))))
+            _ptr(table[r0 // spec:r1 // spec]), table.stride(0), table.shape[1], _ptr(pos[r0:r1]),
+            _ptr(own_rows[r0:r1]), None if fused_slots is None else _ptr(fused_slots[r0:r1]), float(sm_scale),
+            _ptr(ctx[r0:r1]), _ptr(lse[r0:r1]), r1 - r0, spec, H, P, n_rows // P, pl, _ptr(ws), ws.numel(),
+            _stream(dev))))
     keep = (q_absorbed, q_pe, cache, idx, table, pos, own_rows, new_slots, ctx, lse, ws, plans)
     return Prepared(calls, keep, (ctx, lse), "mla_decode_sparse")
 
@@ -594,10 +604,12 @@ def prepare_mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, k
 def mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, kv_scale: float, indices: Tensor,
                       block_table: Tensor, positions: Tensor, own_rows: Tensor, **kw) -> tuple[Tensor, Tensor]:
     """DSA sparse decode: q_absorbed [B, H, 512], q_pe [B, H, 64], the 640-byte row cache, ``indices`` [B, K] int32
-    global positions (-1 empty), ``block_table`` [B, W], ``positions`` [B], own rows [B, 576] ([k_pe | latent]).
-    With ``new_slots`` the launch also stores the own rows there, and a gather of such a slot attends the stored bytes
+    global positions (-1 empty), ``block_table`` [B / spec, W] (one row per sequence), ``positions`` [B], own rows
+    [B, 576] ([k_pe | latent]); ``spec`` query tokens per sequence (default 1; GLM's MTP verify runs 8): each token
+    also attends its sequence's other own rows at their positions (kept iff at or before its own). With
+    ``new_slots`` the launch also stores the own rows there, and a gather of such a slot attends the stored bytes
     (the reference stores them first, steps 0-1); without, the caller has stored them. Keyword arguments: sm_scale,
-    page_size, new_slots, plan. Returns (ctx [B, H, 512] bf16, lse [B, H] fp32).
+    page_size, new_slots, plan, spec. Returns (ctx [B, H, 512] bf16, lse [B, H] fp32).
 
     Stands in for mla_decode_attention_torch_ref with one token per sequence and one CP rank
     (models/glm52/kernels/decode/attention/mla/mla_decode_attention_torch.py:38-130)."""

@@ -35,7 +35,9 @@ GQA_CONFIGS = {
 MLA_CONFIG = dict(name="deepseek-v2-lite-mla-fp8", B=32, H=16, P=64, lens=(1024, 16384), latent_scale=0.5,
                   sm_scale=1.0 / math.sqrt(192.0))
 DSA_CONFIG = dict(name="glm5-dsa-mla-fp8", B=16, H=16, P=64, pool_positions=131072, n_indices=2048, recent=128,
-                  kv_scale=2.0 ** -6, sm_scale=0.0625, short_rows=(1000, 2000))
+                  kv_scale=2.0 ** -6, sm_scale=0.0625, short_rows=(1000, 2000), spec=1)
+# GLM-5.2's MTP verify decodes 8 query tokens per sequence (the token and 7 drafts; docs/model-recipes/glm52.md)
+DSA_MTP_SPEC = 8
 SWA_WINDOW = 128  # GPT-OSS sliding layers (models/gpt_oss/config.py)
 
 
@@ -223,20 +225,21 @@ def mla_case(*, gen_device="cpu", overrides: Optional[dict] = None) -> MlaCase:
 
 @dataclass
 class DsaCase:
-    B: int
+    B: int                # sequences
     H: int
     P: int
     kv_scale: float
     sm_scale: float
-    positions: Tensor     # [B] int32: the query token's position (its row's live length - 1)
-    block_table: Tensor   # [B, W] int32
+    positions: Tensor     # [B * spec] int32: each query token's position (the last is its sequence's live length - 1)
+    block_table: Tensor   # [B, W] int32, one row per sequence
     num_blocks: int
-    indices: Tensor       # [B, K] int32, -1 padded
-    q_absorbed: Tensor    # [B, H, 512]
-    q_pe: Tensor          # [B, H, 64]
-    own_rows: Tensor      # [B, 576] [k_pe | latent]
-    new_slots: Tensor     # [B]
+    indices: Tensor       # [B * spec, K] int32, -1 padded
+    q_absorbed: Tensor    # [B * spec, H, 512]
+    q_pe: Tensor          # [B * spec, H, 64]
+    own_rows: Tensor      # [B * spec, 576] [k_pe | latent]
+    new_slots: Tensor     # [B * spec]
     pool_positions: int
+    spec: int = 1         # query tokens per sequence (sequence s owns tokens s * spec .. s * spec + spec - 1)
 
     def to(self, device) -> "DsaCase":
         out = DsaCase(**{k: getattr(self, k) for k in self.__dataclass_fields__})
@@ -245,11 +248,12 @@ class DsaCase:
         return out
 
     def kv_bytes_per_step(self) -> int:
+        T = self.B * self.spec
         valid = int((self.indices >= 0).sum())
         b = valid * (640 + 4)                              # gathered rows + their index
         b += (self.indices < 0).sum().item() * 4
-        b += self.B * (576 * 2 + 640)                       # own rows: bf16 in, packed row out
-        b += self.B * self.H * (512 + 64) * 2 + self.B * self.H * (512 * 2 + 4)
+        b += T * (576 * 2 + 640)                            # own rows: bf16 in, packed row out
+        b += T * self.H * (512 + 64) * 2 + T * self.H * (512 * 2 + 4)
         b += valid * 4                                      # table entries
         return int(b)
 
@@ -273,37 +277,41 @@ def dsa_case(*, gen_device="cpu", overrides: Optional[dict] = None) -> DsaCase:
     """cfg5. Every row's pool holds ``pool_positions`` positions; most rows decode at the pool's last position, and
     the rows named by ``short_rows`` (a builder choice) decode at those shorter lengths, so their index lists are all
     their prior positions padded with -1. Indices: the last ``recent`` prior positions + uniform draws without
-    replacement from the rest."""
-    spec = dict(DSA_CONFIG)
-    spec.update(overrides or {})
-    B, H, P, K = spec["B"], spec["H"], spec["P"], spec["n_indices"]
-    per = spec["pool_positions"]
+    replacement from the rest. With ``spec`` > 1 a sequence decodes spec query tokens at its last spec positions
+    (MTP verify); each token draws its own index list over the sequence's prior (the positions before its first
+    token)."""
+    cfg = dict(DSA_CONFIG)
+    cfg.update(overrides or {})
+    B, H, P, K, spec = cfg["B"], cfg["H"], cfg["P"], cfg["n_indices"], cfg["spec"]
+    per = cfg["pool_positions"]
     g_cpu = gen(5)
     lens = [per] * B
-    for i, L in enumerate(spec["short_rows"]):
+    for i, L in enumerate(cfg["short_rows"]):
         if i < B:
             lens[B - 1 - i] = min(L, per)
     # extra_pages: unused pages mixed into the permutation (a larger pool, e.g. one past 4 GiB)
-    table, nb = _page_layout([per] * B, P, g_cpu, spec.get("extra_pages", 0))
-    idx = torch.full((B, K), -1, dtype=torch.int32)
+    table, nb = _page_layout([per] * B, P, g_cpu, cfg.get("extra_pages", 0))
+    T = B * spec
+    idx = torch.full((T, K), -1, dtype=torch.int32)
     for b, L in enumerate(lens):
-        prior = L - 1
-        if prior <= K:
-            sel = torch.arange(prior)
-        else:
-            recent = torch.arange(prior - spec["recent"], prior)
-            rest = torch.randperm(prior - spec["recent"], generator=g_cpu)[: K - spec["recent"]]
-            sel = torch.cat([recent, torch.sort(rest).values])
-        idx[b, : sel.numel()] = sel.to(torch.int32)
+        prior = L - spec
+        for j in range(spec):
+            if prior <= K:
+                sel = torch.arange(prior)
+            else:
+                recent = torch.arange(prior - cfg["recent"], prior)
+                rest = torch.randperm(prior - cfg["recent"], generator=g_cpu)[: K - cfg["recent"]]
+                sel = torch.cat([recent, torch.sort(rest).values])
+            idx[b * spec + j, : sel.numel()] = sel.to(torch.int32)
     g = gen(5, gen_device)
-    qa = _randn_bf16((B, H, 512), g, gen_device)
-    qpe = _randn_bf16((B, H, 64), g, gen_device)
-    own = _randn_bf16((B, 576), g, gen_device)
-    positions = torch.tensor([L - 1 for L in lens], dtype=torch.int32)
-    new_slots = _slots_of(table, positions.to(torch.int64), torch.arange(B), P)
-    return DsaCase(B=B, H=H, P=P, kv_scale=spec["kv_scale"], sm_scale=spec["sm_scale"], positions=positions,
+    qa = _randn_bf16((T, H, 512), g, gen_device)
+    qpe = _randn_bf16((T, H, 64), g, gen_device)
+    own = _randn_bf16((T, 576), g, gen_device)
+    positions = torch.tensor([L - spec + j for L in lens for j in range(spec)], dtype=torch.int32)
+    new_slots = _slots_of(table, positions.to(torch.int64), torch.arange(T) // spec, P)
+    return DsaCase(B=B, H=H, P=P, kv_scale=cfg["kv_scale"], sm_scale=cfg["sm_scale"], positions=positions,
                    block_table=table, num_blocks=nb, indices=idx, q_absorbed=qa, q_pe=qpe, own_rows=own,
-                   new_slots=new_slots, pool_positions=per)
+                   new_slots=new_slots, pool_positions=per, spec=spec)
 
 
 # ---- pools on the GPU, filled through the HIP store kernels ----

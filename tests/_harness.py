@@ -108,7 +108,8 @@ def dsa_oracle(case: workloads.DsaCase):
     case.fill_rows(lambda v, s: ost.kv_store_dsa(v, s, cache, case.kv_scale))
     ctx, lse, cache2 = oatt.mla_decode_sparse(case.q_absorbed.cpu(), case.q_pe.cpu(), cache, case.kv_scale,
                                               case.indices, case.block_table, case.positions, case.own_rows.cpu(),
-                                              case.new_slots.cpu(), sm_scale=case.sm_scale, page_size=case.P)
+                                              case.new_slots.cpu(), sm_scale=case.sm_scale, page_size=case.P,
+                                              spec=case.spec)
     return ctx, lse, cache2
 
 
@@ -125,4 +126,4 @@ def dsa_gpu_step(case: workloads.DsaCase, cache, dev="cuda", fused=True):
     return ops.mla_decode_sparse(case.q_absorbed.to(dev), case.q_pe.to(dev), cache, case.kv_scale,
                                  case.indices.to(dev), case.block_table.to(dev), case.positions.to(dev),
                                  case.own_rows.to(dev), sm_scale=case.sm_scale, page_size=case.P,
-                                 new_slots=slots if fused else None)
+                                 new_slots=slots if fused else None, spec=case.spec)

@@ -219,7 +219,7 @@ def test_mla_plan_from_a_bound_is_a_device_split(lib):
     assert _plan(lib, _lib.KIND_MLA, None, B=4, max_len=0)[0] == _lib.SNA_ERR_UNSUPPORTED
     # a sparse decode refuses it
     rc = lib.sna_mla_decode_sparse(None, None, None, 1.0, None, 16, None, 0, 0, None, None, None, 0.1, None, None, 4,
-                                   16, 64, 10, ctypes.byref(p), None, 0, None)
+                                   1, 16, 64, 10, ctypes.byref(p), None, 0, None)
     assert rc == _lib.SNA_ERR_INVALID_ARGUMENT and b"device-split" in lib.sna_last_error()
 
 

@@ -115,6 +115,12 @@ DSA_CASES = [
     # rows whose pieces need more than one launch's 256 workgroups: the own rows stored first, then two launches
     ("batch-past-one-launch", {"B": 130, "pool_positions": 2600, "n_indices": 2500, "recent": 64,
                                "short_rows": (1000,)}),
+    # MTP verify: spec query tokens per sequence, each attending its index list and its earlier siblings' own rows
+    ("spec-3-small", {"B": 3, "pool_positions": 2048, "n_indices": 256, "recent": 32, "short_rows": (300,),
+                      "spec": 3}),
+    ("cfg5-mtp-spec8", {"spec": workloads.DSA_MTP_SPEC}),               # GLM's MTP K7 on the full cfg5 pool
+    ("spec8-three-launches", {"B": 40, "pool_positions": 3000, "n_indices": 2500, "recent": 64,
+                              "short_rows": (900,), "spec": 8}),
 ]
 
 
@@ -122,7 +128,7 @@ DSA_CASES = [
 def test_dsa_decode_matches_oracle(name, over):
     case = workloads.dsa_case(overrides=over)
     want_ctx, want_lse, cache_o = dsa_oracle(case)
-    announce(f"dsa {name}: B={case.B} H={case.H} P={case.P} K={case.indices.shape[1]}")
+    announce(f"dsa {name}: B={case.B} spec={case.spec} H={case.H} P={case.P} K={case.indices.shape[1]}")
     cache = dsa_gpu_pool(case)
     ctx, lse = dsa_gpu_step(case, cache)
     torch.cuda.synchronize()

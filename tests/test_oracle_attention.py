@@ -272,6 +272,54 @@ def test_dsa_all_prior_indices_match_a_dense_brute_force():
             assert float(lse[b, h]) == pytest.approx(float(torch.logsumexp(torch.tensor(s), 0)), abs=1e-4)
 
 
+@pytest.mark.parametrize("spec", [1, 3])
+def test_dsa_speculative_tokens_match_a_float64_brute_force(spec):
+    """spec query tokens per sequence (MTP verify): token j of sequence s attends its own index list through table
+    row s, then every own row of its sequence at that token's position, kept iff at or before its own (so its
+    earlier siblings and itself), each key decoded from its packed bytes; by explicit float64 loops over keys."""
+    g = torch.Generator().manual_seed(40 + spec)
+    S, H, P, K, kv = 2, 2, 4, 6, 0.25
+    B = S * spec
+    table = torch.tensor([[3, 1, 5, 8], [2, 6, 4, 7]], dtype=torch.int32)
+    cache = torch.zeros(9 * P, 640, dtype=torch.uint8)
+    base = [9, 5]  # each sequence's first speculative position; its prior is positions < base
+    for s_ in range(S):
+        slots = torch.tensor([int(table[s_, p // P]) * P + p % P for p in range(base[s_])])
+        ost.kv_store_dsa(_bf16((base[s_], 576), g), slots, cache, kv)
+    positions = torch.tensor([base[b // spec] + b % spec for b in range(B)], dtype=torch.int32)
+    idx = torch.full((B, K), -1, dtype=torch.int32)
+    for b in range(B):
+        prior = base[b // spec]
+        sel = torch.randperm(prior, generator=g)[:K - 1]
+        idx[b, :sel.numel()] = sel.to(torch.int32)
+    idx[0, K - 1] = 30  # a block past the table's width: dropped
+    own = _bf16((B, 576), g)
+    new_slots = torch.tensor([int(table[b // spec, int(positions[b]) // P]) * P + int(positions[b]) % P
+                              for b in range(B)])
+    qa, qpe = _bf16((B, H, 512), g), _bf16((B, H, 64), g)
+    ctx, lse, cache2 = oatt.mla_decode_sparse(qa, qpe, cache, kv, idx, table, positions, own, new_slots,
+                                              sm_scale=0.0625, page_size=P, spec=spec)
+    packed = ost.pack_kv_rows(own, kv)
+    for b in range(B):
+        s_, qpos = b // spec, int(positions[b])
+        keys = []
+        for e in idx[b].tolist():
+            if e < 0 or e // P >= table.shape[1] or e > qpos:
+                continue
+            r = int(table[s_, e // P]) * P + e % P
+            keys.append(ost.unpack_kv_row(cache2[r][None], kv)[0].double())
+        for i in range(spec):  # the sequence's own rows, at their positions
+            if int(positions[s_ * spec + i]) <= qpos:
+                keys.append(ost.unpack_kv_row(packed[s_ * spec + i][None], kv)[0].double())
+        assert len(keys) == sum(1 for e in idx[b].tolist() if 0 <= e <= qpos and e // P < 4) + b % spec + 1
+        for h in range(H):
+            q = torch.cat([qpe[b, h], qa[b, h]]).double()
+            want = _softmax_attend(q, keys, [k[64:] for k in keys], 0.0625)
+            assert torch.allclose(ctx[b, h].double(), torch.tensor(want, dtype=torch.float64), atol=1e-2, rtol=8e-3)
+            sc = [float((q * k).sum()) * 0.0625 for k in keys]
+            assert float(lse[b, h]) == pytest.approx(float(torch.logsumexp(torch.tensor(sc), 0)), abs=1e-4)
+
+
 def test_block_table_by_hand():
     page = 4
     r2t = np.arange(6 * 40, dtype=np.int64).reshape(6, 40) * 3 % 997

@@ -87,6 +87,66 @@ def paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: T
     return out
 
 
+def paged_decode_gqa_multi(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: Tensor, seq_lens: Tensor,
+                           k_new: Tensor, v_new: Tensor, *, sm_scale: float, k_scale=None, v_scale=None,
+                           sinks: Optional[Tensor] = None, window: int = 0,
+                           scales_multiply: bool = False) -> Tensor:
+    """[B, S, H, d] bf16 GQA decode of S active tokens per row: q [B, S, H, d], the step's K/V k_new / v_new
+    [B, S, G, d], seq_lens [B] counting the prior and the S tokens, so token j sits at position L - S + j.
+
+    Follows _torch_attention_decode (ops/attention/attention_decode.py:226-276) for X [B, S, Hd]: the prior is
+    gathered through the row's table (positions < L - S, pages >= 0), the S tokens go in the last S slots as their
+    FP8-rounded values (:259-269), and token j sees the prior (within its window: positions >= L - S + j - W + 1,
+    gpt_oss/attention_masks.py:47-52) and active tokens 0 .. j (the mask's triu over the active slots,
+    attention_decode_mask.py:64-81); a sink column per head joins the softmax and is dropped (:274-275)."""
+    B, S, H, d = q.shape
+    nb, G, P, _ = k_cache.shape
+    group = H // G
+    Wt = block_table.shape[1]
+    table = block_table.to(torch.int64)
+    fp8_cache = k_cache.dtype == torch.uint8
+    out = torch.empty(B, S, H, d, dtype=torch.bfloat16)
+    key_pos = torch.arange(Wt * P)
+    for b in range(B):
+        L = int(seq_lens[b])
+        tb = table[b]
+        page_ok = (tb >= 0) & (tb < nb)
+        rows = tb.clamp(min=0, max=nb - 1)
+        keys = _dequant_cache(k_cache[rows], k_scale, G, scales_multiply).permute(1, 0, 2, 3).reshape(G, Wt * P, d)
+        vals = _dequant_cache(v_cache[rows], v_scale, G, scales_multiply).permute(1, 0, 2, 3).reshape(G, Wt * P, d)
+        prior_vis = page_ok.repeat_interleave(P) & (key_pos < L - S)
+        if fp8_cache:
+            ks = torch.as_tensor(k_scale, dtype=torch.float32).reshape(1, G, 1)
+            vs = torch.as_tensor(v_scale, dtype=torch.float32).reshape(1, G, 1)
+            if scales_multiply:
+                kn = fp8.dequantize_mul(fp8.quantize_mul(k_new[b], ks), ks)
+                vn = fp8.dequantize_mul(fp8.quantize_mul(v_new[b], vs), vs)
+            else:
+                kn = fp8.dequantize(fp8.quantize(k_new[b], ks), ks)
+                vn = fp8.dequantize(fp8.quantize(v_new[b], vs), vs)
+        else:
+            kn, vn = k_new[b].float(), v_new[b].float()
+        keys = torch.cat([keys, kn.permute(1, 0, 2)], dim=1)  # [G, W*P + S, d]
+        vals = torch.cat([vals, vn.permute(1, 0, 2)], dim=1)
+        for j in range(S):
+            pos = L - S + j
+            vis = prior_vis.clone()
+            if window > 0:
+                vis &= key_pos >= pos - window + 1
+            act = torch.arange(S) <= j
+            vis = torch.cat([vis, act])
+            qb = q[b, j].float().reshape(G, group, d)
+            scores = torch.einsum("gjd,gsd->gjs", qb, keys) * sm_scale
+            scores = scores.masked_fill(~vis[None, None, :], float("-inf"))
+            if sinks is not None:
+                scores = torch.cat([scores, sinks.float().reshape(G, group, 1)], dim=-1)
+                probs = torch.softmax(scores, dim=-1)[..., :-1]
+            else:
+                probs = torch.softmax(scores, dim=-1)
+            out[b, j] = torch.einsum("gjs,gsd->gjd", probs, vals).reshape(H, d).to(torch.bfloat16)
+    return out
+
+
 def segmented_prefill(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: Tensor, q_start, prior_lens, *,
                       sm_scale: float, k_scale=None, v_scale=None, sinks: Optional[Tensor] = None,
                       window: int = 0, scales_multiply: bool = False) -> Tensor:

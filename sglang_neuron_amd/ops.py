@@ -458,6 +458,43 @@ def paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: T
     return prepare_paged_decode_gqa(q, k_cache, v_cache, block_table, seq_lens, k_new, v_new, **kw)()
 
 
+def paged_decode_gqa_multi(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: Tensor, seq_lens: Tensor,
+                           k_new: Tensor, v_new: Tensor, *, sm_scale: float, new_slots: Tensor,
+                           k_scale: Optional[Tensor] = None, v_scale: Optional[Tensor] = None,
+                           sinks: Optional[Tensor] = None, window: int = 0, scales_multiply: bool = False,
+                           host_seq_lens=None) -> Tensor:
+    """GQA decode of S active tokens per row: q [B, S, H, d], the step's K/V k_new / v_new [B, S, G, d] stored at
+    new_slots [B, S], seq_lens [B] counting the prior and the S tokens (token j at position L - S + j). Token j
+    attends the row's prior and active tokens 0 .. j. Returns [B, S, H, d] bf16.
+
+    The S tokens are stored first (kv_store_mha), then each (row, token) decodes as a row of its own whose length
+    ends at that token: its earlier active tokens are then pool keys holding the bytes the store wrote, which are the
+    values the reference attends in its last S slots (dequantized FP8 or bf16), so this is the reference's triu mask
+    over the active slots. A window must hold the S tokens (S <= window), as the reference's mask does not window
+    them. Stands in for _torch_attention_decode with X [B, S, Hd] (ops/attention/attention_decode.py:226-300)."""
+    dev = _on_gpu(q, k_cache, v_cache, block_table, seq_lens, k_new, v_new, new_slots, k_scale, v_scale, sinks)
+    _need(q.dim() == 4, f"q must be [B, S, H, d], got {tuple(q.shape)}")
+    B, S, H, d = q.shape
+    nb, G, P, _ = k_cache.shape
+    _need(k_new.shape == (B, S, G, d) and v_new.shape == (B, S, G, d), f"k_new / v_new must be [{B}, {S}, {G}, {d}]")
+    _need(new_slots.numel() == B * S, f"new_slots must be [{B}, {S}]")
+    _need(window <= 0 or S <= window, f"{S} active tokens do not fit a window of {window}")
+    hl = _host_lens(seq_lens, host_seq_lens)
+    if hl is not None:
+        _need(int(hl.min()) >= S if B else True, f"a row holds its {S} active tokens: seq_lens >= {S}")
+    kv_store_mha(k_new.reshape(B * S, G, d), v_new.reshape(B * S, G, d), new_slots.reshape(-1), k_cache, v_cache,
+                 k_scale, v_scale, scales_multiply=scales_multiply)
+    j = torch.arange(S, device=dev, dtype=torch.int32)
+    lens = (seq_lens.reshape(B, 1).to(torch.int32) - S + 1 + j).reshape(-1)
+    rows = torch.arange(B, device=dev).repeat_interleave(S)
+    table = block_table.index_select(0, rows)
+    host_rows = None if hl is None else (hl.reshape(B, 1).to(torch.int32) - S + 1 + j.cpu()).reshape(-1)
+    out = paged_decode_gqa(q.reshape(B * S, H, d), k_cache, v_cache, table, lens, k_new.reshape(B * S, G, d),
+                           v_new.reshape(B * S, G, d), sm_scale=sm_scale, k_scale=k_scale, v_scale=v_scale,
+                           sinks=sinks, window=window, scales_multiply=scales_multiply, host_seq_lens=host_rows)
+    return out.reshape(B, S, H, d)
+
+
 def prepare_mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: Optional[Tensor], block_table: Tensor,
                        seq_lens: Tensor, compact_new: Tensor, *, sm_scale: float, page_size: int,
                        new_slots: Optional[Tensor] = None, out: Optional[Tensor] = None, host_seq_lens=None,

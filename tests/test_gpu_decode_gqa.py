@@ -121,3 +121,64 @@ def test_plan_for_longer_rows_still_attends_and_stores_the_own_token(mapped):
     assert_close_attn(out, want, "plan for longer rows")
     assert torch.equal(cache_bytes(kc), cache_bytes(kc_o)), "K pool differs"
     assert torch.equal(cache_bytes(vc), cache_bytes(vc_o)), "V pool differs"
+
+
+MULTI = [("cfg4-s4", 4, {"B": 8, "lens": (100, 3000)}, 4),                  # GPT-OSS multipliers, sinks
+         ("cfg4-swa-s8", 4, {"B": 6, "lens": (2, 900), "window": 128}, 8),
+         ("cfg2-s3", 2, {"B": 4, "lens": (40, 1000)}, 3),
+         ("cfg1-bf16-s2", 1, {"B": 3, "lens": (30, 400)}, 2)]
+
+
+@pytest.mark.parametrize("name,cfg,over,S", MULTI, ids=[m[0] for m in MULTI])
+def test_gqa_multi_token_decode_matches_oracle(name, cfg, over, S):
+    """S active tokens per row (the GPT-OSS decode's X [B, S, Hd]): the last S positions of each row are the step's
+    tokens, stored by the call and attended causally; against oracle.paged_decode_gqa_multi, pools bit-exact."""
+    from oracle import attention as oatt
+    from oracle import store as ost
+    from sglang_neuron_amd import ops
+
+    case = workloads.gqa_case(cfg, overrides=over)
+    B, G, d, P, H = case.B, case.G, case.d, case.P, case.H
+    lens = case.seq_lens.clamp(min=S)
+    # the prior tokens by (row, position); each row's last S positions become its active tokens
+    k_at, v_at, k = {}, {}, 0
+    for b, L in enumerate(case.seq_lens.tolist()):
+        for pos in range(L - 1):
+            k_at[(b, pos)], v_at[(b, pos)] = case.k_prior[k], case.v_prior[k]
+            k += 1
+        k_at[(b, L - 1)], v_at[(b, L - 1)] = case.k_new[b], case.v_new[b]
+    g = torch.Generator().manual_seed(77)
+    z = torch.zeros(G, d, dtype=torch.bfloat16)
+    k_act = torch.stack([torch.stack([k_at.get((b, int(L) - S + j), z) for j in range(S)]) for b, L in enumerate(lens)])
+    v_act = torch.stack([torch.stack([v_at.get((b, int(L) - S + j), z) for j in range(S)]) for b, L in enumerate(lens)])
+    q = torch.randn(B, S, H, d, generator=g).to(torch.bfloat16)
+    slot_of = lambda b, pos: int(case.block_table[b, pos // P]) * P + pos % P  # noqa: E731
+    prior = [(b, pos) for b, L in enumerate(lens.tolist()) for pos in range(L - S)]
+    pk = torch.stack([k_at[x] for x in prior]) if prior else torch.zeros(0, G, d, dtype=torch.bfloat16)
+    pv = torch.stack([v_at[x] for x in prior]) if prior else torch.zeros(0, G, d, dtype=torch.bfloat16)
+    ps = torch.tensor([slot_of(*x) for x in prior], dtype=torch.int64)
+    new_slots = torch.tensor([[slot_of(b, int(L) - S + j) for j in range(S)] for b, L in enumerate(lens)])
+    from tests._harness import gqa_scales
+    ks, vs = gqa_scales(case) if case.fp8 else (None, None)
+    mul = case.scales_multiply
+    dt = torch.uint8 if case.fp8 else torch.bfloat16
+    kc_o = torch.zeros(case.num_blocks, G, P, d, dtype=dt)
+    vc_o = torch.zeros_like(kc_o)
+    ost.kv_store_mha(pk, pv, ps, kc_o, vc_o, ks, vs, mul)
+    kc = (kc_o.view(torch.float8_e4m3fn) if case.fp8 else kc_o).cuda().contiguous()
+    vc = (vc_o.view(torch.float8_e4m3fn) if case.fp8 else vc_o).cuda().contiguous()
+    want = oatt.paged_decode_gqa_multi(q, kc_o, vc_o, case.block_table, lens, k_act, v_act, sm_scale=case.sm_scale,
+                                       k_scale=ks, v_scale=vs, sinks=case.sinks, window=case.window,
+                                       scales_multiply=mul)
+    ost.kv_store_mha(k_act.reshape(B * S, G, d), v_act.reshape(B * S, G, d), new_slots.reshape(-1), kc_o, vc_o, ks,
+                     vs, mul)
+    announce(f"gqa multi-token {name}: B={B} S={S} H={H} G={G} d={d} window={case.window}")
+    out = ops.paged_decode_gqa_multi(q.cuda(), kc, vc, case.block_table.cuda(), lens.cuda(), k_act.cuda(),
+                                     v_act.cuda(), sm_scale=case.sm_scale, new_slots=new_slots.cuda(),
+                                     k_scale=None if ks is None else ks.cuda(), v_scale=None if vs is None else vs.cuda(),
+                                     sinks=None if case.sinks is None else case.sinks.cuda(), window=case.window,
+                                     scales_multiply=mul, host_seq_lens=lens)
+    torch.cuda.synchronize()
+    assert_close_attn(out, want, name)
+    assert torch.equal(cache_bytes(kc), cache_bytes(kc_o)), "K pool differs"
+    assert torch.equal(cache_bytes(vc), cache_bytes(vc_o)), "V pool differs"

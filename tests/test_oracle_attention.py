@@ -429,3 +429,109 @@ def test_segmented_prefill_is_chunking_invariant():
     two = oatt.segmented_prefill(q, kc, vc, table.repeat(2, 1), torch.tensor([0, 4, 9]), torch.tensor([6, 10]),
                                  sm_scale=0.5, window=4)
     assert torch.equal(whole, two)
+
+
+def _multi_case(seed, B=2, S=3, H=4, G=2, d=8, P=4, mul=True):
+    """Rows of S active tokens over a small FP8 pool (GPT-OSS multipliers) or a bf16 one."""
+    g = torch.Generator().manual_seed(seed)
+    lens = [9, 14][:B]
+    pages = [(L + P - 1) // P for L in lens]
+    nb = sum(pages) + 2
+    perm = (torch.randperm(nb - 1, generator=g) + 1).tolist()
+    table = torch.full((B, max(pages)), -1, dtype=torch.int32)
+    o = 0
+    for b, n in enumerate(pages):
+        table[b, :n] = torch.tensor(perm[o:o + n], dtype=torch.int32)
+        o += n
+    fp8 = mul is not None
+    ks = torch.rand(G, generator=g) * 0.01 + 0.004 if fp8 else None
+    vs = torch.rand(G, generator=g) * 0.01 + 0.004 if fp8 else None
+    if mul:
+        ks, vs = ofp8.inverted_scale(ks), ofp8.inverted_scale(vs)
+    dt = torch.uint8 if fp8 else torch.bfloat16
+    kc, vc = torch.zeros(nb, G, P, d, dtype=dt), torch.zeros(nb, G, P, d, dtype=dt)
+    slots = [int(table[b, p // P]) * P + p % P for b, L in enumerate(lens) for p in range(L - S)]
+    T = len(slots)
+    ost.kv_store_mha(_bf16((T, G, d), g), _bf16((T, G, d), g), torch.tensor(slots), kc, vc, ks, vs, bool(mul))
+    q, kn, vn = _bf16((B, S, H, d), g), _bf16((B, S, G, d), g), _bf16((B, S, G, d), g)
+    new = torch.tensor([[int(table[b, p // P]) * P + p % P for p in range(L - S, L)] for b, L in enumerate(lens)])
+    return dict(q=q, kc=kc, vc=vc, table=table, lens=torch.tensor(lens), kn=kn, vn=vn, ks=ks, vs=vs, new=new,
+                P=P, G=G, mul=bool(mul))
+
+
+@pytest.mark.parametrize("mul,window,sinks", [(True, 0, True), (True, 5, True), (None, 0, False), (False, 6, False)])
+def test_gqa_multi_token_matches_float64_brute_force(mul, window, sinks):
+    """S active tokens per row (attention_decode.py with X [B, S, Hd]): token j of row b (position L - S + j) attends
+    the prior positions < L - S on the row's pages (within its window) and active tokens 0 .. j as their FP8-rounded
+    values; explicit float64 loops over keys."""
+    c = _multi_case(51, mul=mul)
+    B, S, H, d = c["q"].shape
+    G, P = c["G"], c["P"]
+    sk = torch.randn(H, generator=torch.Generator().manual_seed(3)) if sinks else None
+    got = oatt.paged_decode_gqa_multi(c["q"], c["kc"], c["vc"], c["table"], c["lens"], c["kn"], c["vn"],
+                                      sm_scale=0.35, k_scale=c["ks"], v_scale=c["vs"], sinks=sk, window=window,
+                                      scales_multiply=c["mul"])
+    vals = ofp8.e4m3fn_values()
+    for b in range(B):
+        L = int(c["lens"][b])
+        for j in range(S):
+            pos = L - S + j
+            for h in range(H):
+                g_ = h // (H // G)
+                keys, vv = [], []
+                for p in range(L - S):
+                    if window and p < pos - window + 1:
+                        continue
+                    pg = int(c["table"][b, p // P])
+                    kb, vb = c["kc"][pg, g_, p % P], c["vc"][pg, g_, p % P]
+                    if c["ks"] is not None:  # byte / m for multipliers, byte * s for dequantization scales
+                        kms, vms = float(c["ks"][g_]), float(c["vs"][g_])
+                        kf, vf = torch.tensor(vals[kb.long().numpy()]), torch.tensor(vals[vb.long().numpy()])
+                        kb, vb = (kf / kms, vf / vms) if c["mul"] else (kf * kms, vf * vms)
+                    keys.append(kb.double())
+                    vv.append(vb.double())
+                for i in range(j + 1):  # the active tokens up to this one, as the cache holds them
+                    kn, vn = c["kn"][b, i, g_], c["vn"][b, i, g_]
+                    if c["ks"] is not None:
+                        kms, vms = float(c["ks"][g_]), float(c["vs"][g_])
+                        if c["mul"]:
+                            kn = torch.tensor(vals[_mul_bytes(kn, kms)]) / kms
+                            vn = torch.tensor(vals[_mul_bytes(vn, vms)]) / vms
+                        else:
+                            kn = torch.tensor(vals[ofp8.e4m3fn_rne_spec(np.clip(kn.float().numpy() / np.float32(kms),
+                                                                                 -448, 448)).astype(np.int64)]) * kms
+                            vn = torch.tensor(vals[ofp8.e4m3fn_rne_spec(np.clip(vn.float().numpy() / np.float32(vms),
+                                                                                 -448, 448)).astype(np.int64)]) * vms
+                    keys.append(kn.double())
+                    vv.append(vn.double())
+                want = _softmax_attend(c["q"][b, j, h].double(), keys, vv, 0.35,
+                                       None if sk is None else float(sk[h]))
+                assert torch.allclose(got[b, j, h].double(), torch.tensor(want, dtype=torch.float64), atol=1e-2, rtol=8e-3), (b, j, h)
+
+
+def test_gqa_multi_token_is_stored_tokens_then_one_row_per_token():
+    """The decomposition the HIP path runs: store the S tokens, then decode token j as a row whose length ends at it
+    (its earlier active tokens read back from the pool) gives the multi-token oracle's outputs."""
+    c = _multi_case(52, mul=True)
+    B, S, H, d = c["q"].shape
+    want = oatt.paged_decode_gqa_multi(c["q"], c["kc"], c["vc"], c["table"], c["lens"], c["kn"], c["vn"],
+                                       sm_scale=0.35, k_scale=c["ks"], v_scale=c["vs"], window=7, scales_multiply=True)
+    kc, vc = c["kc"].clone(), c["vc"].clone()
+    ost.kv_store_mha(c["kn"].reshape(B * S, c["G"], d), c["vn"].reshape(B * S, c["G"], d), c["new"].reshape(-1), kc,
+                     vc, c["ks"], c["vs"], True)
+    lens = (c["lens"].reshape(B, 1) - S + 1 + torch.arange(S)).reshape(-1)
+    got = oatt.paged_decode_gqa(c["q"].reshape(B * S, H, d), kc, vc, c["table"].repeat_interleave(S, 0), lens,
+                                c["kn"].reshape(B * S, c["G"], d), c["vn"].reshape(B * S, c["G"], d), sm_scale=0.35,
+                                k_scale=c["ks"], v_scale=c["vs"], window=7, scales_multiply=True)
+    assert torch.allclose(got.reshape(B, S, H, d).float(), want.float(), atol=1e-2)
+    assert float((got.reshape(B, S, H, d).float() - want.float()).abs().max()) <= 2 ** -7
+
+
+def test_gqa_multi_token_with_one_token_is_the_single_token_decode():
+    c = _multi_case(53, S=1, mul=True)
+    B, S, H, d = c["q"].shape
+    a = oatt.paged_decode_gqa_multi(c["q"], c["kc"], c["vc"], c["table"], c["lens"], c["kn"], c["vn"], sm_scale=0.35,
+                                    k_scale=c["ks"], v_scale=c["vs"], scales_multiply=True)
+    b = oatt.paged_decode_gqa(c["q"][:, 0], c["kc"], c["vc"], c["table"], c["lens"], c["kn"][:, 0], c["vn"][:, 0],
+                              sm_scale=0.35, k_scale=c["ks"], v_scale=c["vs"], scales_multiply=True)
+    assert torch.equal(a[:, 0], b)

@@ -201,7 +201,7 @@ def setup_gqa(cfg: int, window: int, dev):
                                                     scales_multiply=mul)
                        for (k, v) in pools]}
     # the step under a plan from a bound (the block table's width), as a serving graph captured once for growing
-    # lengths runs it: the kernels locate their items from the device's seq_lens
+    # lengths runs it: a device split, whose launch sizes its splits and locates its items from the device's seq_lens
     plan_b = ops.plan_decode(0, case.B, max_seq_len=table.shape[1] * case.P, window=case.window, ctas_per_item=case.G,
                              num_cus=ops._num_cus(q.device))
     legs["bound_plan"] = [ops.prepare_paged_decode_gqa(q, k, v, table, lens, kn, vn, sm_scale=case.sm_scale,

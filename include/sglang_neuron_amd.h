@@ -176,7 +176,8 @@ typedef struct {
   int32_t target_ctas;  /* the workgroup count the plan aimed for */
   int32_t max_splits;   /* GQA: the most splits any row has; MLA / DSA: the most workgroups any row spans */
   int32_t batch;        /* rows the plan was made for */
-  int32_t empty_rows;   /* rows with no prior key (seq_len 1), or -1 when planned from a bound */
+  int32_t empty_rows;   /* rows with no prior key (seq_len 1), or -1 when planned from a bound (0 for a GQA device
+                           split, which gives every row a split) */
   int32_t depth;        /* GQA: the plan's shape (3: one round of two 4-wave workgroups per CU, for launches with
                            enough work to fill the chip with long splits; 2: small launches of several rounds). The
                            kernels keep two tiles per wave in their register rings either way. The planner picks it;
@@ -196,15 +197,21 @@ typedef struct {
   uint16_t cta_row[SNA_MAX_CTAS];
   uint16_t cta_off[SNA_MAX_CTAS];
   int32_t row_keys[SNA_MAX_PLAN_ROWS];
-  int32_t device_split; /* MLA: 1 for a plan from a bound. Its launch cuts the stream split from the device's seq_lens
-                           (the same apportionment, by bisection of the longest piece), so one captured launch serves
-                           every length up to the bound; n_ctas is the launch's workgroups per head group (the bound
-                           the workspace is sized for), row_keys the bound's key count, and cta_* are unused. */
+  int32_t device_split; /* 1 for a plan from a bound whose launch splits from the device's seq_lens, so one captured
+                           launch serves every length up to the bound (0: the plan's own split). MLA: the stream split
+                           (the same apportionment, by bisection of the longest piece); n_ctas is the launch's
+                           workgroups per head group (the bound the workspace is sized for), row_keys the bound's key
+                           count, and cta_* are unused. GQA (B <= 512 rows of at most 2^17 - 1 tiles): the split size,
+                           by the planner's one-round rule on the device's lengths, to fit n_work items (the bound's
+                           own item count, at least B); every row gets at least one split (a row with no prior key
+                           attends and stores its own token in a split of no tile), max_splits bounds any row's, and
+                           split_tiles is unused. */
 } sna_split_plan;
 
 /* Plan a decode from host copies of seq_lens (exact) or, with host_seq_lens == NULL, from an upper bound
- * max_seq_len for every row (GQA: n_work bounds the device's count and the workspace is sized for it; MLA: a
- * device-split plan, whose launch reads the device's seq_lens, each held to the block table's width).
+ * max_seq_len for every row (a device-split plan, whose launch reads the device's seq_lens: GQA up to 512 rows of at
+ * most 2^17 - 1 tiles of 32 keys, else the bound's own split with n_work bounding the device's count; MLA, each length held to
+ * the block table's width).
  * `kind`: 0 GQA, 1 MLA, 2 DSA. For DSA, seq_lens are ignored: `n_keys_per_row` (the index-list length) is the
  * row's key count. `window` is the sliding window (0 = full). `ctas_per_item` is the number of workgroups that
  * one (sequence, split) item launches: num_kv_heads for GQA, and 1 for MLA and DSA. `num_cus` is the device's CU
@@ -215,8 +222,8 @@ typedef struct {
 int sna_plan_decode(int32_t kind, const int32_t *host_seq_lens, int32_t B, int32_t max_seq_len, int32_t window,
                     int32_t n_keys_per_row, int32_t ctas_per_item, int32_t num_cus, sna_split_plan *plan);
 
-/* Workspace bytes a decode with this plan needs. GQA: batch * max_splits * heads * (head_dim_v + 2) * 4, or 0 when
- * max_splits <= 1. MLA / DSA: a 256 KiB block of counters, then 2 * n_ctas partials of heads * (head_dim_v + 2) fp32.
+/* Workspace bytes a decode with this plan needs. GQA: batch * max_splits * heads * (head_dim_v + 2) * 4 (+ 256 for
+ * a device split: the launch's split size, for its combine pass), or 0 when max_splits <= 1. MLA / DSA: a 256 KiB block of counters, then 2 * n_ctas partials of heads * (head_dim_v + 2) fp32.
  * The counters must be zero before the first call on a workspace (allocate it zeroed); every completed call leaves
  * them zero. Calls that share a workspace must be ordered (one stream). */
 int64_t sna_decode_workspace_bytes(const sna_split_plan *plan, int32_t num_q_heads, int32_t head_dim_v);

@@ -304,8 +304,19 @@ int sna_plan_decode(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32
   plan->target_ctas = (int32_t)target;
   plan->max_splits = max_splits;
   plan->batch = B;
-  // a plan from a bound cannot know which rows are only their new token
-  plan->empty_rows = (kind != 2 && !host_seq_lens) ? -1 : empty;
+  if (kind == 0 && !host_seq_lens && B <= kGqaDevSplitRows && bound_tiles <= kGqaDevSplitMaxTiles) {
+    // A GQA plan from a bound splits on the device: every launch sizes its splits from the device's lengths by the
+    // one-round rule above to fit the items the bound's own split runs, and gives every row a split (a row with no
+    // prior key attends its own token there: no lone-token pass). A split holds at least 4 tiles and at least
+    // min(longest row, 8), so a row of up to 8 tiles is one split and a longer one at most ceil(tiles / 8); and as
+    // every other row takes an item, a row gets at most n_work - B + 1 (one, when the bound's split is whole rows).
+    plan->device_split = 1;
+    plan->n_work = (int32_t)std::max<int64_t>(n_work, B);
+    plan->max_splits = std::min(bound_tiles <= 8 ? 1 : std::min(kMaxSplits, (bound_tiles + 7) / 8),
+                                plan->n_work - B + 1);
+  }
+  // a plan from a bound cannot know which rows are only their new token (a device split gives every row a split)
+  plan->empty_rows = plan->device_split ? 0 : (kind != 2 && !host_seq_lens) ? -1 : empty;
   plan->depth = kind == 0 ? depth : 0;
   // the item -> (row, split) map, when the lengths are exact and the items fit it (the order locate_work finds)
   plan->work_n = 0;
@@ -385,7 +396,9 @@ int64_t sna_decode_workspace_bytes(const sna_split_plan* plan, int32_t num_q_hea
            2ll * plan->n_ctas * num_q_heads * ((int64_t)head_dim_v + 2) * (int64_t)sizeof(float);
   }
   if (plan->max_splits <= 1) return 0;
-  return (int64_t)plan->batch * plan->max_splits * num_q_heads * ((int64_t)head_dim_v + 2) * (int64_t)sizeof(float);
+  // partials, then (a device split) the launch's split size for its combine, in a 256-byte line
+  return (int64_t)plan->batch * plan->max_splits * num_q_heads * ((int64_t)head_dim_v + 2) * (int64_t)sizeof(float) +
+         (plan->device_split ? 256 : 0);
 }
 
 int sna_lse_combine(const float* o_parts, const float* lse_parts, int32_t n_parts, int64_t n_rows, int32_t dim,

@@ -51,22 +51,130 @@ struct GqaArgs {
   int64_t num_blocks;
   int32_t window;
   float sm_scale;
-  int32_t split_tiles;
+  int32_t split_tiles;  // a device-split launch sizes its splits from the device's seq_lens (gqa_device_item)
   int32_t n_work;
   int32_t max_splits;
+  int32_t dev_split;    // 1: a plan from a bound whose split size the launch computes (n_work: the items it may run)
   int32_t work_n;                       // entries of work (0: locate items from seq_lens)
   uint32_t work[SNA_MAX_WORK_MAP];      // item -> row << 6 | split (| kWorkLastSplit on a row's last), from the plan
   uint8_t row_splits[SNA_MAX_WORK_MAP]; // with a map (B <= SNA_MAX_WORK_MAP): the map's items per row
   float* ws_o;   // [B, max_splits, H, D]  unnormalized partials (V dequantized)
   float* ws_ml;  // [B, max_splits, H, 2]  reference max (log2 domain) and softmax sum
+  int32_t* ws_st;  // a device split's split size, written by the decode launch for its combine (after ws_ml)
   uint16_t* out;
 };
 
 // The splits this launch runs for row b: its entries in the plan's item map (counted on the host), or (no map: items
-// located from seq_lens) the device length's split count up to the plan's.
-__device__ __forceinline__ int32_t launched_splits(const GqaArgs& a, int32_t b, int32_t seq_len) {
+// located from seq_lens) the device length's split count, with split size st, up to the plan's.
+// A device split gives every row at least one split: a row with no prior key attends and stores its own token in a
+// split of no tile (so no lone-token pass is needed).
+__device__ __forceinline__ int32_t launched_splits(const GqaArgs& a, int32_t b, int32_t seq_len, int32_t st) {
   if (a.work_n > 0) return a.row_splits[b];
-  return min(splits_of<32>(seq_len, a.window, a.split_tiles), max(a.max_splits, 1));
+  const int32_t n = splits_of<32>(seq_len, a.window, st);
+  return min(a.dev_split ? max(n, 1) : n, max(a.max_splits, 1));
+}
+
+template <int CTRL>
+__device__ __forceinline__ int32_t dpp_i32(int32_t v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+// Inclusive prefix sum of v over the wave's 64 lanes (lane l gets v[0] + ... + v[l]), and the wave's sum in *total
+// (uniform). Within each 16-lane row by row_shr 1, 2, 4 and 8 (a lane whose source lies before its row's start adds
+// 0: the move leaves it the old value, 0), then each row adds the sums of the rows before it, read from their last
+// lanes. VALU moves and lane reads, no LDS round trip.
+__device__ __forceinline__ int32_t wave_incl_scan_i32(int32_t v, int32_t* total) {
+  v += dpp_i32<0x111>(v);
+  v += dpp_i32<0x112>(v);
+  v += dpp_i32<0x114>(v);
+  v += dpp_i32<0x118>(v);
+  const int32_t r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31);
+  const int32_t r2 = __builtin_amdgcn_readlane(v, 47), r3 = __builtin_amdgcn_readlane(v, 63);
+  const int row = (threadIdx.x & 63) >> 4;
+  *total = r0 + r1 + r2 + r3;
+  return v + (row > 0 ? r0 : 0) + (row > 1 ? r1 : 0) + (row > 2 ? r2 : 0);
+}
+// The wave's largest v (uniform) for v >= 0: running maxima within each row the same way, then the rows' last lanes.
+__device__ __forceinline__ int32_t wave_max_nonneg_i32(int32_t v) {
+  v = max(v, dpp_i32<0x111>(v));
+  v = max(v, dpp_i32<0x112>(v));
+  v = max(v, dpp_i32<0x114>(v));
+  v = max(v, dpp_i32<0x118>(v));
+  return max(max(__builtin_amdgcn_readlane(v, 15), __builtin_amdgcn_readlane(v, 31)),
+             max(__builtin_amdgcn_readlane(v, 47), __builtin_amdgcn_readlane(v, 63)));
+}
+
+// A device split's item (every lane of the calling wave gets the same values): the launch's split size st and, for
+// item w, its row b (-1 past the last item), split and the row's seq_len L, from one load of every row's length.
+// Every row has at least one split (launched_splits). The split size is the host planner's one-round rule applied
+// to the device's lengths: at least 4 tiles and ceil(total tiles / items), at least min(longest row, 8) tiles, at
+// most the longest row, grown to the least size whose items (sum over rows of max(1, ceil(tiles / size))) fit the
+// launch's n_work, and at least a 64th of the longest row (a row's splits fit the combine's 64 weights). The least
+// size is bisected between that start and ceil(total / (items - B)), which fits (each row's count is below
+// tiles / size + 1). The rows' lengths and tile counts stay in registers: B <= kGqaDevSplitRows, n_work >= B (so the
+// longest row's size fits) and a row spans at most kGqaDevSplitMaxTiles tiles (the planner's bound). Items are
+// numbered row by row, splits in order, as locate_work numbers them.
+__device__ void gqa_device_item(const GqaArgs& a, int32_t w, int32_t& b_out, int32_t& split_out, int32_t& st_out,
+                                int32_t& len_out) {
+  constexpr int R = kGqaDevSplitRows / 64;
+  const int lane = threadIdx.x & 63;
+  const int chunks = (a.B + 63) / 64;
+  int32_t lens[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+    if (i < chunks) lens[i] = ld_const(a.seq_lens + min(lane + 64 * i, a.B - 1));  // uniform branch: all in flight
+  uint32_t tiles[R];
+  int32_t lane_total = 0, lane_max = 0;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    tiles[i] = 0;
+    if (i < chunks && lane + 64 * i < a.B)
+      tiles[i] = (uint32_t)min(splits_of<32>(lens[i], a.window, 1), kGqaDevSplitMaxTiles);
+    lane_total += (int32_t)tiles[i];
+    lane_max = max(lane_max, (int32_t)tiles[i]);
+  }
+  int32_t total;
+  wave_incl_scan_i32(lane_total, &total);
+  const int32_t mx = wave_max_nonneg_i32(lane_max);
+  const int32_t items = max(a.n_work, a.B);
+  const int32_t cap = max(mx, 4);
+  int32_t lo = min(max(max(4, (total + items - 1) / items), min(mx, 8)), cap);
+  int32_t hi = items > a.B ? min(cap, max(lo, (total + items - a.B - 1) / (items - a.B))) : cap;
+  while (lo < hi) {  // uniform
+    const uint32_t mid = (uint32_t)((lo + hi) >> 1);
+    const float rmid = 1.0f / (float)mid;
+    int32_t lane_n = 0;
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+      if (i < chunks && lane + 64 * i < a.B) lane_n += (int32_t)max(ceil_div_small(tiles[i], mid, rmid), 1u);
+    int32_t n;
+    wave_incl_scan_i32(lane_n, &n);
+    if (n <= items) hi = (int32_t)mid;
+    else lo = (int32_t)mid + 1;
+  }
+  const uint32_t st = (uint32_t)__builtin_amdgcn_readfirstlane(max(lo, (mx + kMaxSplits - 1) / kMaxSplits));
+  const float rst = 1.0f / (float)st;
+  st_out = (int32_t)st;
+  b_out = -1;
+  split_out = 0;
+  len_out = 0;
+  int32_t base = 0;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    if (i < chunks && b_out < 0) {  // uniform
+      const int32_t n = lane + 64 * i < a.B ? (int32_t)max(ceil_div_small(tiles[i], st, rst), 1u) : 0;
+      int32_t part;
+      const int32_t incl = wave_incl_scan_i32(n, &part);
+      if (w < base + part) {
+        const int32_t excl = incl - n;
+        const uint64_t mine = __ballot(w >= base + excl && w < base + incl);
+        const int32_t src = (int32_t)__builtin_amdgcn_readfirstlane(__ffsll((long long)mine) - 1);
+        b_out = 64 * i + src;
+        split_out = w - base - __builtin_amdgcn_readlane(excl, src);
+        len_out = __builtin_amdgcn_readlane(lens[i], src);
+      }
+      base += part;
+    }
+  }
 }
 
 template <int NB>
@@ -121,24 +229,31 @@ void gqa_decode_kernel(GqaArgs a) {
   const int li = lane & 15;
   const int g = blockIdx.y;
 
-  int32_t b, split;
-  if ((int32_t)blockIdx.x < a.work_n) {  // the plan's map, from the kernel arguments
-    const uint32_t e = a.work[blockIdx.x];
-    b = (int32_t)((e & ~kWorkLastSplit) >> 6);
-    split = (int32_t)(e & 63u);
+  int32_t b, split, st, L = 0;
+  if (a.dev_split) {  // the split size and the item, from the device's lengths
+    gqa_device_item(a, (int32_t)blockIdx.x, b, split, st, L);
+    if (!FINAL && blockIdx.x == 0 && blockIdx.y == 0 && tid == 0) *a.ws_st = st;  // for the combine
   } else {
-    locate_work<32>(a.seq_lens, a.B, a.window, a.split_tiles, (int32_t)blockIdx.x, b, split);
+    st = a.split_tiles;
+    if ((int32_t)blockIdx.x < a.work_n) {  // the plan's map, from the kernel arguments
+      const uint32_t e = a.work[blockIdx.x];
+      b = (int32_t)((e & ~kWorkLastSplit) >> 6);
+      split = (int32_t)(e & 63u);
+    } else {
+      locate_work<32>(a.seq_lens, a.B, a.window, st, (int32_t)blockIdx.x, b, split);
+    }
   }
   b = __builtin_amdgcn_readfirstlane(b);
   split = __builtin_amdgcn_readfirstlane(split);
+  st = __builtin_amdgcn_readfirstlane(st);
   // uniform across the workgroup; a split past the plan's count (a length beyond the plan's bound) is dropped, so no
   // write leaves the workspace
-  if (b < 0 || split >= max(a.max_splits, 1)) return;
-
-  const int32_t L = ld_const(a.seq_lens + b);
+  if (b < 0 || b >= a.B || split >= max(a.max_splits, 1)) return;
+  if (!a.dev_split) L = ld_const(a.seq_lens + b);
+  L = __builtin_amdgcn_readfirstlane(L);
   const KeyRange kr = key_range(L, a.window);
-  const int32_t t_first = kr.lo / 32 + split * a.split_tiles;
-  const int32_t t_last = min(t_first + a.split_tiles, (kr.hi + 31) / 32);
+  const int32_t t_first = kr.lo / 32 + split * st;
+  const int32_t t_last = min(t_first + st, (kr.hi + 31) / 32);
 
   // Query operand: in step s lane (g4, li) holds head li's 8 elements from dim CE (4 c + g4) + w, with CE the
   // elements of a 16-byte cache chunk and 8 s = CE c + w: the dims of the key bytes it feeds in that step.
@@ -315,7 +430,7 @@ void gqa_decode_kernel(GqaArgs a) {
   // when the device's length disagrees with the plan's.
   // (with a map the item's own flag says it, from the entry already loaded)
   const bool own = (int32_t)blockIdx.x < a.work_n ? (a.work[blockIdx.x] & kWorkLastSplit) != 0
-                                                   : split == launched_splits(a, b, L) - 1;  // uniform
+                                                   : split == launched_splits(a, b, L, st) - 1;  // uniform
   constexpr int OWN_J = (16 + WAVES - 1) / WAVES;  // query heads per wave in the own token's score
   uint32_t own_kb = 0, own_vb = 0;
   int64_t own_dst = -1;
@@ -476,7 +591,7 @@ __global__ __launch_bounds__(64) void gqa_combine_kernel(GqaArgs a) {
     for (int v = 0; v < V; ++v) x[k][v] = k < S ? ob[k * sstride + v] : 0.0f;
   float2 ml = make_float2(-INFINITY, 0.0f);
   if (lane < S) ml = *reinterpret_cast<const float2*>(a.ws_ml + (row0 + (int64_t)lane * a.H) * 2);
-  const int32_t n = min(launched_splits(a, b, ld_const(a.seq_lens + b)), S);
+  const int32_t n = min(launched_splits(a, b, ld_const(a.seq_lens + b), a.dev_split ? *a.ws_st : a.split_tiles), S);
   if (n == 0) return;  // a row with no prior key: the lone-token kernel writes it
   const float m = lane < n ? ml.x : -INFINITY, l = lane < n ? ml.y : 0.0f;
   const float sink = a.sinks ? a.sinks[h] * kLog2e : -INFINITY;
@@ -512,7 +627,8 @@ __global__ __launch_bounds__(64) void gqa_combine_kernel(GqaArgs a) {
 template <int D, bool FP8>
 __global__ __launch_bounds__(128) void gqa_lone_token_kernel(GqaArgs a) {
   const int b = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
-  if (launched_splits(a, b, a.seq_lens[b]) > 0) return;
+  // any split size counts the row's splits as nonzero iff it has a prior key
+  if (launched_splits(a, b, a.seq_lens[b], a.split_tiles) > 0) return;
   __shared__ float sm_kn[D], sm_vn[D];
   const float kstored = FP8 ? a.k_scale[g] : 1.0f, vstored = FP8 ? a.v_scale[g] : 1.0f;
   const float kscale = (FP8 && a.mul_scale) ? 1.0f / kstored : kstored;
@@ -614,6 +730,9 @@ int decode_gqa(const char* what, const void* q, const void* k_cache, const void*
     return fail(SNA_ERR_INVALID_ARGUMENT, "%s: missing or foreign split plan (made for %d rows)", what,
                 plan ? plan->batch : -1);
   if (const int rc = check_work_map(plan, B, what)) return rc;
+  if (plan->device_split && (plan->work_n > 0 || B > kGqaDevSplitRows))
+    return fail(SNA_ERR_INVALID_ARGUMENT, "%s: a device-split plan has no item map and at most %d rows (%d)", what,
+                kGqaDevSplitRows, B);
   if (B == 0) return SNA_OK;
   const bool fp8 = cache_dtype != SNA_DTYPE_BF16;
   const int64_t need = sna_decode_workspace_bytes(plan, num_q_heads, head_dim);
@@ -651,6 +770,7 @@ int decode_gqa(const char* what, const void* q, const void* k_cache, const void*
   a.window = window;
   a.sm_scale = sm_scale;
   a.split_tiles = plan->split_tiles;
+  a.dev_split = plan->device_split;
   a.n_work = plan->n_work;
   a.max_splits = plan->max_splits;
   a.work_n = plan->work_n;
@@ -662,9 +782,10 @@ int decode_gqa(const char* what, const void* q, const void* k_cache, const void*
   float* ws = (float*)workspace;
   a.ws_o = need > 0 ? ws : nullptr;
   a.ws_ml = need > 0 ? ws + (int64_t)B * plan->max_splits * num_q_heads * head_dim : nullptr;
+  a.ws_st = need > 0 ? (int32_t*)(a.ws_ml + (int64_t)B * plan->max_splits * num_q_heads * 2) : nullptr;
   a.out = (uint16_t*)out;
   // a row with no prior key has no split: the lone-token pass writes it (launched unless the plan rules it out)
-  const bool any_lone = plan->empty_rows != 0;
+  const bool any_lone = !plan->device_split && plan->empty_rows != 0;
 
   hipStream_t s = (hipStream_t)stream;
   if (head_dim == 128) {

@@ -243,15 +243,6 @@ __device__ __forceinline__ void wave_incl_scan4(uint32_t (&v)[4]) {
   }
 }
 
-// ceil(x / t) for x < 2^17 and 1 <= t < 2^17, with rt = 1 / t: the float quotient is within one of the exact one,
-// and one correction each way makes it exact.
-__device__ __forceinline__ uint32_t ceil_div_small(uint32_t x, uint32_t t, float rt) {
-  uint32_t q = (uint32_t)((float)x * rt);
-  if (q * t > x) --q;
-  else if ((q + 1) * t <= x) ++q;
-  return q + (q * t < x ? 1u : 0u);
-}
-
 // Wave 0 of every workgroup of a device-split launch cuts the same stream split from the device's seq_lens (the
 // arithmetic is deterministic, so every workgroup gets the same one): the rows' key counts (seq_len - 1, held to the
 // table's width and the stream's 65535 tiles per row) into keys[b]; the ranges' starts into cs[w] (cs[w] = the

@@ -19,6 +19,10 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegBig = -1.0e30f;
 // The most splits a row may have (the combine passes hold one weight per split in LDS); the planner keeps to it.
 constexpr int kMaxSplits = 64;
+// The most rows of a GQA launch that sizes its splits on the device (their tile counts stay in one wave's registers),
+// and the most 32-key tiles one of its rows may span (its split arithmetic divides through floats: ceil_div_small).
+constexpr int kGqaDevSplitRows = 512;
+constexpr int kGqaDevSplitMaxTiles = (1 << 17) - 1;
 // The most keys one sparse (DSA) workgroup may resolve (their row ids live in the kernel's LDS); the planner keeps to it.
 constexpr int kMlaMaxSplitKeys = 2048;
 // The MLA / DSA stream split's counter block at the start of its workspace: per (row, head group) an arrival counter
@@ -324,6 +328,15 @@ __device__ __forceinline__ float row16_max(float v) {
 // Whole-wave reductions: across the four row groups, then within the row.
 __device__ __forceinline__ float wave_max(float v) { return row16_max(max_across_groups(v)); }
 __device__ __forceinline__ float wave_sum(float v) { return row16_sum(sum_across_groups(v)); }
+
+// ceil(x / t) for x < 2^17 and 1 <= t < 2^17, with rt = 1 / t: the float quotient is within one of the exact one,
+// and one correction each way makes it exact.
+__device__ __forceinline__ uint32_t ceil_div_small(uint32_t x, uint32_t t, float rt) {
+  uint32_t q = (uint32_t)((float)x * rt);
+  if (q * t > x) --q;
+  else if ((q + 1) * t <= x) ++q;
+  return q + (q * t < x ? 1u : 0u);
+}
 
 // ---- split-K work decomposition ----
 // Sequence b's keys from the pool are positions [lo_b, hi_b): hi_b = seq_len_b - 1 (the step's own token is attended

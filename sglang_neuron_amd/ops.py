@@ -250,6 +250,25 @@ def _row_splits(L: int, window: int, split_tiles: int) -> int:
     return (-(-hi // 32) - lo // 32 + split_tiles - 1) // split_tiles
 
 
+def _gqa_device_split_tiles(tiles, n_work: int) -> int:
+    """The split size a device-split GQA launch computes from its rows' tile counts (gqa_device_item): the least size
+    at least 4, ceil(total / items) and min(longest, 8) (at most max(longest, 4)) whose items, max(1, ceil(tiles /
+    size)) a row, fit items = max(n_work, B); then at least a 64th of the longest row."""
+    B = len(tiles)
+    items = max(n_work, B, 1)
+    total, mx = sum(tiles), max(tiles, default=0)
+    cap = max(mx, 4)
+    lo = min(max(4, -(-total // items), min(mx, 8)), cap)
+    hi = min(cap, max(lo, -(-total // (items - B)))) if items > B else cap
+    while lo < hi:
+        mid = (lo + hi) // 2
+        if sum(max(1, -(-t // mid)) for t in tiles) <= items:
+            hi = mid
+        else:
+            lo = mid + 1
+    return max(lo, -(-mx // 64))
+
+
 def check_plan_lengths(plan: _lib.SplitPlan, kind: int, host_seq_lens, window: int = 0) -> None:
     """Refuse a plan that cannot serve these lengths (host copies): a GQA plan whose item map or split count misses a
     split some row needs (those keys would be dropped), an MLA plan made for other key counts (its launch is cut by
@@ -257,6 +276,15 @@ def check_plan_lengths(plan: _lib.SplitPlan, kind: int, host_seq_lens, window: i
     lens = [int(x) for x in torch.as_tensor(host_seq_lens).reshape(-1).tolist()]
     _need(len(lens) == plan.batch, f"a plan for {plan.batch} rows, {len(lens)} lengths")
     if kind == _lib.KIND_GQA:
+        if plan.device_split:
+            # the launch sizes its splits from the device's lengths (gqa_device_item): a row must fit the plan's
+            # split count
+            tiles = [_row_splits(L, window, 1) for L in lens]
+            st = _gqa_device_split_tiles(tiles, plan.n_work)
+            for b, t in enumerate(tiles):
+                _need(max(1, -(-t // st)) <= max(plan.max_splits, 1),
+                      f"row {b}: seq_len {lens[b]} is past the plan's bound (at most {plan.max_splits} splits)")
+            return
         need = [_row_splits(L, window, plan.split_tiles) for L in lens]
         if plan.work_n > 0:
             have = [0] * len(lens)

@@ -99,8 +99,10 @@ def test_plan_invariants(lib, kind, lens, window, ctas):
 
 
 def test_plan_from_a_bound_marks_empty_rows_unknown(lib):
-    rc, p = _plan(lib, _lib.KIND_GQA, B=4, max_len=900)
-    assert rc == 0 and p.empty_rows == -1 and p.work_n == 0  # no map: the kernels search the device's seq_lens
+    # past the device split's 512 rows a GQA plan from a bound keeps the bound's split: no map (the kernels search the
+    # device's seq_lens), and which rows hold only their new token is unknown
+    rc, p = _plan(lib, _lib.KIND_GQA, B=600, max_len=900)
+    assert rc == 0 and p.empty_rows == -1 and p.work_n == 0 and p.device_split == 0
 
 
 @pytest.mark.parametrize("kind,window,max_len,B", [
@@ -108,11 +110,74 @@ def test_plan_from_a_bound_marks_empty_rows_unknown(lib):
     (_lib.KIND_GQA, 1, 300, 2), (_lib.KIND_GQA, 0, 4000, 9)])
 def test_plan_from_a_bound_holds_every_length_up_to_it(lib, kind, window, max_len, B):
     """Every length L <= max_len: its split count fits the plan (max_splits, and n_work for B such rows), whatever
-    tile offset a window starts at."""
+    tile offset a window starts at. A GQA plan from a bound is a device split: the launch sizes its splits from the
+    device's lengths (_device_split_tiles), so the check runs that rule on batches of B rows at each length and on
+    ragged batches below the bound."""
     rc, p = _plan(lib, kind, B=B, max_len=max_len, window=window, ctas=8 if kind == _lib.KIND_GQA else 1)
     assert rc == 0, lib.sna_last_error()
-    worst = max(_splits(L, window, p.tile, p.split_tiles) for L in range(1, max_len + 1))
-    assert worst <= p.max_splits and B * worst <= p.n_work, (worst, p)
+    if not p.device_split:
+        worst = max(_splits(L, window, p.tile, p.split_tiles) for L in range(1, max_len + 1))
+        assert worst <= p.max_splits and B * worst <= p.n_work, (worst, p)
+        return
+    import random
+
+    import torch
+
+    from sglang_neuron_amd import ops
+    # every row gets an item (the own token of a row with no prior key is attended in a split of no tile)
+    assert kind == _lib.KIND_GQA and p.work_n == 0 and p.empty_rows == 0 and p.n_work >= B and p.max_splits >= 1
+    rng = random.Random(max_len * 31 + B)
+    batches = [[L] * B for L in range(1, max_len + 1)]
+    batches += [[rng.randint(1, max_len) for _ in range(B)] for _ in range(200)]
+    for lens in batches:
+        tiles = [_splits(L, window, 32, 1) for L in lens]
+        st = _device_split_tiles(tiles, p.n_work)
+        counts = [max(1, -(-t // st)) for t in tiles]
+        assert max(counts) <= p.max_splits and sum(counts) <= p.n_work, (lens, st, p.max_splits, p.n_work)
+        ops.check_plan_lengths(p, _lib.KIND_GQA, torch.tensor(lens), window=window)
+
+
+def _device_split_tiles(tiles, items):
+    """The split size a device-split GQA launch computes from its rows' tile counts (gqa_device_item in
+    decode_gqa.hip): the least size in [start, max(longest, 4)] whose items (max(1, ceil(tiles / size)) a row) fit
+    `items`, with start = ceil(total / items) and at least 4 and min(longest, 8) tiles, then at least a 64th of the
+    longest row. Found here by a linear scan over the whole range, so the kernel's bisection bracket (its upper end
+    ceil(total / (items - B))) is checked against the definition."""
+    B = len(tiles)
+    items = max(items, B)
+    total, mx = sum(tiles), max(tiles, default=0)
+    cap = max(mx, 4)
+    st = min(max(4, -(-total // items), min(mx, 8)), cap)
+    fits = [s for s in range(st, cap + 1) if sum(max(1, -(-t // s)) for t in tiles) <= items]
+    least = fits[0]
+    if items > B:
+        assert least <= min(cap, max(st, -(-total // (items - B))))
+    return max(least, -(-mx // 64))
+
+
+def test_gqa_plan_from_a_bound_is_a_device_split(lib):
+    """Up to 512 rows a GQA plan from a bound splits on the device (n_work items, one per row at least, and room for
+    4-tile splits of the bound); past 512 it keeps the bound's own split; with host lengths it is exact."""
+    rc, p = _plan(lib, _lib.KIND_GQA, B=128, max_len=8192, ctas=1, cus=256)
+    assert rc == 0 and p.device_split == 1 and p.n_work == 512 and p.max_splits == 32 and p.work_n == 0
+    assert p.empty_rows == 0  # every row gets a split: no lone-token pass
+    # 64 rows of the bound: the bound's split is whole rows, so every launch's is (n_work = B): one split a row
+    rc, p = _plan(lib, _lib.KIND_GQA, B=64, max_len=4096, ctas=8, cus=256)
+    assert rc == 0 and p.device_split == 1 and p.n_work == 64 and p.max_splits == 1
+    rc, p = _plan(lib, _lib.KIND_GQA, B=600, max_len=8192, ctas=1, cus=256)
+    assert rc == 0 and p.device_split == 0 and p.n_work >= 600
+    rc, p = _plan(lib, _lib.KIND_GQA, [100, 4000, 9000], ctas=1, cus=256)
+    assert rc == 0 and p.device_split == 0
+    rc, p = _plan(lib, _lib.KIND_GQA, B=3, max_len=40, ctas=8, cus=256)
+    assert rc == 0 and p.device_split == 1 and p.max_splits == 1 and p.n_work >= 3
+    rc, p = _plan(lib, _lib.KIND_GQA, B=5, max_len=1, ctas=8, cus=256)  # own tokens only: a split each, no tile
+    assert rc == 0 and p.device_split == 1 and p.max_splits == 1 and p.n_work == 5
+    # a sliding window of 128 keys spans at most 5 tiles: one split a row, written without a combine pass
+    rc, p = _plan(lib, _lib.KIND_GQA, B=128, max_len=8192, window=128, ctas=1, cus=256)
+    assert rc == 0 and p.device_split == 1 and p.max_splits == 1
+    assert lib.sna_decode_workspace_bytes(ctypes.byref(p), 8, 64) == 0
+    rc, p = _plan(lib, _lib.KIND_GQA, B=2, max_len=32 * (1 << 17) + 64, ctas=1, cus=256)  # past the device bound
+    assert rc == 0 and p.device_split == 0
 
 
 def _row_tiles(keys):

@@ -123,6 +123,41 @@ def test_plan_for_longer_rows_still_attends_and_stores_the_own_token(mapped):
     assert torch.equal(cache_bytes(vc), cache_bytes(vc_o)), "V pool differs"
 
 
+BOUND = [("cfg4-full-size", 4, {}, 8192),                                   # the bench's bound plan: 128 rows
+         ("cfg4-swa", 4, {"B": 40, "window": workloads.SWA_WINDOW}, 8192),
+         ("cfg2-ragged", 2, {"B": 20, "lens": (1, 3000)}, 4096),
+         ("cfg1", 1, {}, 1024),
+         ("cfg2-one-row-at-bound", 2, {"B": 3, "lens": (16, 16)}, 16),
+         ("cfg4-300-rows", 4, {"B": 300, "lens": (1, 600)}, 2048),
+         # rows of their own token only (no prior key: a split of no tile), beside rows of one tile
+         ("cfg2-own-token-rows", 2, {"B": 70, "lens": (1, 3)}, 64),
+         ("cfg1-short-final", 1, {"B": 9, "lens": (1, 200)}, 256)]                # one split a row, no combine
+
+
+@pytest.mark.parametrize("name,cfg,over,bound", BOUND, ids=[b[0] for b in BOUND])
+def test_gqa_device_split_plan_matches_oracle(name, cfg, over, bound):
+    """A plan from a length bound splits on the device: every launch sizes its splits from the device's seq_lens
+    (gqa_split_tiles). Against the oracle, pools bit-exact, on full, sliding-window, ragged and single-tile rows."""
+    from sglang_neuron_amd import ops
+
+    case = workloads.gqa_case(cfg, overrides=over)
+    want, kc_o, vc_o, ks_o, vs_o = gqa_oracle(case)
+    plan = ops.plan_decode(0, case.B, max_seq_len=bound, window=case.window, ctas_per_item=case.G,
+                           num_cus=ops._num_cus(torch.device("cuda", 0)))
+    announce(f"gqa device split {name}: B={case.B} bound={bound} n_work={plan.n_work} max_splits={plan.max_splits}")
+    assert plan.device_split == 1 and plan.work_n == 0
+    kc, vc, ks, vs = gqa_gpu_pool(case)
+    out = ops.paged_decode_gqa(case.q.cuda(), kc, vc, case.block_table.cuda(), case.seq_lens.cuda(), case.k_new.cuda(),
+                               case.v_new.cuda(), sm_scale=case.sm_scale, k_scale=ks, v_scale=vs,
+                               sinks=None if case.sinks is None else case.sinks.cuda(), window=case.window,
+                               new_slots=case.new_slots.cuda(), plan=plan, host_seq_lens=case.seq_lens,
+                               scales_multiply=case.scales_multiply)
+    torch.cuda.synchronize()
+    assert_close_attn(out, want, name)
+    assert torch.equal(cache_bytes(kc), cache_bytes(kc_o)), "K pool differs"
+    assert torch.equal(cache_bytes(vc), cache_bytes(vc_o)), "V pool differs"
+
+
 MULTI = [("cfg4-s4", 4, {"B": 8, "lens": (100, 3000)}, 4),                  # GPT-OSS multipliers, sinks
          ("cfg4-swa-s8", 4, {"B": 6, "lens": (2, 900), "window": 128}, 8),
          ("cfg2-s3", 2, {"B": 4, "lens": (40, 1000)}, 3),

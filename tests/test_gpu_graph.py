@@ -61,6 +61,79 @@ def test_graph_gqa_split_and_combine():
                     lambda out: [out])
 
 
+@pytest.mark.parametrize("window", [0, workloads.SWA_WINDOW], ids=["full", "swa"])
+def test_graph_gqa_device_split_replays_growing_lengths(window):
+    """One GQA decode (GPT-OSS shape: sinks, FP8 multipliers) captured once with a plan from a bound, which sizes its
+    splits on the device, then replayed for three steps in which every row grows by one token: before each replay
+    the step's K/V, slots and lengths are copied into the captured inputs, nothing is planned again. Each step's
+    output against oracle.paged_decode_gqa over the pool as the oracle has it by then, and both pools bit-exact after
+    every step."""
+    dev = torch.device("cuda", 0)
+    steps = 3
+    case = workloads.gqa_case(4, overrides={"B": 7, "lens": (40, 5000), "window": window})
+    L0 = case.seq_lens - (steps - 1)
+    P, G, d = case.P, case.G, case.d
+    kv_of = {}  # (row, position) -> (k, v) [G, d]
+    k = 0
+    for b, L in enumerate(case.seq_lens.tolist()):
+        for pos in range(L - 1):
+            kv_of[(b, pos)] = (case.k_prior[k], case.v_prior[k])
+            k += 1
+        kv_of[(b, L - 1)] = (case.k_new[b], case.v_new[b])
+    slot_of = lambda b, pos: int(case.block_table[b, pos // P]) * P + pos % P  # noqa: E731
+    ks = ops.inverted_kv_scale(ops.kv_absmax_scale(torch.cat([case.k_prior, case.k_new]).to(dev))).to(dev)
+    vs = ops.inverted_kv_scale(ops.kv_absmax_scale(torch.cat([case.v_prior, case.v_new]).to(dev))).to(dev)
+    ks_o, vs_o = ks.cpu(), vs.cpu()
+    first = [(b, pos) for b in range(case.B) for pos in range(int(L0[b]) - 1)]
+    k_first = torch.stack([kv_of[x][0] for x in first])
+    v_first = torch.stack([kv_of[x][1] for x in first])
+    s_first = torch.tensor([slot_of(*x) for x in first])
+    kc_o = torch.zeros(case.num_blocks, G, P, d, dtype=torch.uint8)
+    vc_o = torch.zeros_like(kc_o)
+    ost.kv_store_mha(k_first, v_first, s_first, kc_o, vc_o, ks_o, vs_o, scales_multiply=True)
+    kc = torch.zeros(case.num_blocks, G, P, d, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.zeros_like(kc)
+    ops.kv_store_mha(k_first.to(dev), v_first.to(dev), s_first.to(dev), kc, vc, ks, vs, scales_multiply=True)
+    table = case.block_table.to(dev)
+    lens = L0.to(torch.int32).to(dev)
+    q, sinks = case.q.to(dev), case.sinks.to(dev)
+    k_step = torch.zeros(case.B, G, d, dtype=torch.bfloat16, device=dev)
+    v_step = torch.zeros_like(k_step)
+    slots = torch.zeros(case.B, dtype=torch.int64, device=dev)
+    plan = ops.plan_decode(0, case.B, max_seq_len=table.shape[1] * P, window=window, ctas_per_item=G,
+                           num_cus=ops._num_cus(dev))
+    assert plan.device_split == 1 and plan.work_n == 0
+    announce(f"graph gqa device split window={window}: B={case.B} n_work={plan.n_work} lens0={L0.tolist()}")
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        prep = ops.prepare_paged_decode_gqa(q, kc, vc, table, lens, k_step, v_step, sm_scale=case.sm_scale,
+                                            k_scale=ks, v_scale=vs, sinks=sinks, window=window, new_slots=slots,
+                                            plan=plan, scales_multiply=True)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            out = prep()
+    torch.cuda.synchronize()
+    for s_ in range(steps):
+        L = L0 + s_
+        kn = torch.stack([kv_of[(b, int(L[b]) - 1)][0] for b in range(case.B)])
+        vn = torch.stack([kv_of[(b, int(L[b]) - 1)][1] for b in range(case.B)])
+        sl = torch.tensor([slot_of(b, int(L[b]) - 1) for b in range(case.B)])
+        k_step.copy_(kn.to(dev))
+        v_step.copy_(vn.to(dev))
+        slots.copy_(sl.to(dev))
+        lens.copy_(L.to(torch.int32).to(dev))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        want = oatt.paged_decode_gqa(case.q, kc_o, vc_o, case.block_table, L, kn, vn, sm_scale=case.sm_scale,
+                                     k_scale=ks_o, v_scale=vs_o, sinks=case.sinks, window=window,
+                                     scales_multiply=True)
+        ost.kv_store_mha(kn, vn, sl, kc_o, vc_o, ks_o, vs_o, scales_multiply=True)
+        assert_close_attn(out, want, f"gqa device split step {s_}")
+        assert torch.equal(kc.cpu().view(torch.uint8), kc_o), f"step {s_}: K pool differs"
+        assert torch.equal(vc.cpu().view(torch.uint8), vc_o), f"step {s_}: V pool differs"
+
+
 def test_graph_mla():
     case = workloads.mla_case(overrides={"B": 4, "lens": (1024, 4096)})
     cache, scale = mla_gpu_pool(case)

@@ -812,25 +812,30 @@ def setup(key: str, dev):
     raise SystemExit(f"unknown config {key}")
 
 
-def measure_decode(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev) -> dict:
+def measure_decode(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev,
+                   graph_only: bool = False) -> dict:
     """One decode config: its step time, the roofline of the step's kernels, and (cpu) the CPU baseline. The step time
     is the steps_n steps captured in one HIP graph and replayed (one event pair around the replay); the same steps
     launched one by one from the host (one event pair around steps_n back-to-back calls, after warmup calls) are
-    reported beside it: for the small steps that number is the host's launch rate, not the GPU's. The pools are freed
-    before returning."""
+    reported beside it: for the small steps that number is the host's launch rate, not the GPU's. ``graph_only``
+    (a profiling run): the graph replays alone, so a kernel trace of the run holds the step's kernels from the two
+    replays only (no launches one by one, no halves apart, no bound-plan leg). The pools are freed before
+    returning."""
     import torch
 
     stream = torch.cuda.Stream()  # a side stream: the steps are bound to it, and a graph captures it
     with torch.cuda.stream(stream):
         steps, desc, step_bytes, kernels, mfma_flops, cpu_fn, legs = setup(key, dev)
         n = len(steps)
-        wall = time.perf_counter()
-        us_eager = time_us(lambda i: steps[i % n](), steps_n, warmup)
-        wall = time.perf_counter() - wall
+        us_eager, wall = None, 0.0
+        if not graph_only:
+            wall = time.perf_counter()
+            us_eager = time_us(lambda i: steps[i % n](), steps_n, warmup)
+            wall = time.perf_counter() - wall
         us = time_us_graph(lambda i: steps[i % n](), steps_n)
         # the step's halves apart, the same way (the decode without its store, and the store kernel alone)
         apart = {}
-        for leg, fns in legs.items():
+        for leg, fns in ({} if graph_only else legs).items():
             time_us(lambda i: fns[i % n](), min(warmup, 5), 0)
             apart[f"{leg}_us"] = round(time_us_graph(lambda i: fns[i % n](), steps_n), 3)
     gbs = step_bytes / (us * 1e-6) / 1e9
@@ -841,15 +846,19 @@ def measure_decode(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: f
     mf = mfma_flops if isinstance(mfma_flops, dict) else {"bf16": mfma_flops, "fp8": 0}
     mfma_tflops = (mf["bf16"] + mf["fp8"]) / (us * 1e-6) / 1e12
     mfma_frac = (mf["bf16"] / PEAK_BF16_TFLOPS + mf["fp8"] / PEAK_FP8_TFLOPS) / (us * 1e-6) / 1e12
-    log(f"{wl}: {us:.2f} us/step over {steps_n} steps replayed from a HIP graph ({gbs:.0f} GB/s, {gbs / PEAK_HBM_GBS:.1%} "
-        f"of HBM peak); {us_eager:.2f} us/step launched one by one ({wall * 1e6 / (steps_n + warmup):.1f} us/step by "
-        f"the host clock); kernels {kernels}; apart: store {apart['store_us']:.2f} us, decode without it "
-        f"{apart['decode_us']:.2f} us" + (f"; the step under a plan from a bound {apart['bound_plan_us']:.2f} us"
-                                           if "bound_plan_us" in apart else ""))
+    if graph_only:
+        log(f"{wl}: {us:.2f} us/step over {steps_n} steps replayed from a HIP graph ({gbs:.0f} GB/s, "
+            f"{gbs / PEAK_HBM_GBS:.1%} of HBM peak); graph replays only; kernels {kernels}")
+    else:
+        log(f"{wl}: {us:.2f} us/step over {steps_n} steps replayed from a HIP graph ({gbs:.0f} GB/s, "
+            f"{gbs / PEAK_HBM_GBS:.1%} of HBM peak); {us_eager:.2f} us/step launched one by one "
+            f"({wall * 1e6 / (steps_n + warmup):.1f} us/step by the host clock); kernels {kernels}; apart: store "
+            f"{apart['store_us']:.2f} us, decode without it {apart['decode_us']:.2f} us" +
+            (f"; the step under a plan from a bound {apart['bound_plan_us']:.2f} us" if "bound_plan_us" in apart else ""))
     out = {
         "config": desc,
         "us_per_step": round(us, 3),
-        "us_per_step_launched": round(us_eager, 3),
+        "us_per_step_launched": None if us_eager is None else round(us_eager, 3),
         "apart": dict(apart, note="the step's store kernel alone and its decode without the fused store, each replayed "
                                   "from a HIP graph of the same steps; us_per_step is both together (fused); "
                                   "bound_plan_us: the whole step under a plan from a bound (the block table's width), "
@@ -897,8 +906,9 @@ def measure_decode(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: f
     return out
 
 
-def run_one(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev, per_config=()) -> dict:
-    m = measure_decode(key, steps_n, warmup, cpu, cpu_budget, dev)
+def run_one(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: float, dev, per_config=(),
+            graph_only: bool = False) -> dict:
+    m = measure_decode(key, steps_n, warmup, cpu, cpu_budget, dev, graph_only)
     us = m["us_per_step"]
     desc = m.pop("config")
     line = {
@@ -920,7 +930,7 @@ def run_one(key: str, steps_n: int, warmup: int, cpu: bool, cpu_budget: float, d
     if per_config:
         line["per_config"] = {}
         for k in per_config:
-            pm = measure_decode(k, steps_n, warmup, cpu, cpu_budget * 2 / 3, dev)
+            pm = measure_decode(k, steps_n, warmup, cpu, cpu_budget * 2 / 3, dev, graph_only)
             name = "cfg" + k.replace("swa", "-swa128").replace("bf16", "-bf16").replace("mtp", "-mtp8")
             pm["workload"] = pm["config"]["workload"]
             line["per_config"][name] = pm
@@ -933,7 +943,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="2",
-                    help="1, 2, 3, 4, 4swa, 5 or 3bf16 (default 2, the metric's workload); meta: the device-side metadata; "
+                    help="1, 2, 3, 4, 4swa, 5, 5mtp or 3bf16 (default 2, the metric's workload); meta: the device-side metadata; "
                          "prefill: the segmented prefill attention; indexer: the DSA indexer; wire: the PD page-item "
                          "transfer")
     ap.add_argument("--all", action="store_true", help="one line per workload")
@@ -941,6 +951,9 @@ def main() -> int:
                     help="the cfg2 line without the other decode configs under per_config")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work for the baseline sample")
+    ap.add_argument("--graph-only", action="store_true",
+                    help="decode configs: time the graph replays alone (a profiling run: no launches one by one, no "
+                         "halves apart), so a kernel trace holds the step's kernels from the replays only")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one plain device copy of 1 GiB (the reference dispatch for HBM counter scaling)")
     args = ap.parse_args()
@@ -978,7 +991,8 @@ def main() -> int:
             line = run_qkv(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev)
         else:
             extra = () if (args.all or args.no_per_config or k != "2") else DECODE_CONFIGS[1:]
-            line = run_one(k, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev, extra)
+            line = run_one(k, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget, dev, extra,
+                           args.graph_only)
         print(json.dumps(line), flush=True)
         torch.cuda.empty_cache()
     return 0

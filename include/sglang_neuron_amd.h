@@ -228,6 +228,21 @@ int sna_plan_decode(int32_t kind, const int32_t *host_seq_lens, int32_t B, int32
  * them zero. Calls that share a workspace must be ordered (one stream). */
 int64_t sna_decode_workspace_bytes(const sna_split_plan *plan, int32_t num_q_heads, int32_t head_dim_v);
 
+/* The MLA / DSA workspace's counter block, checked and repaired. It has no counterpart in the reference (its NKI
+ * kernels keep no state across launches); it is for callers that want to know a merge could not be trusted. A launch
+ * that finds a counter past what a zeroed block allows sets a sticky status bit: SNA_WS_DIRTY_ARRIVAL (a row's
+ * arrival count past its workgroups: the block was not zero on entry, or two launches overlapped on it; that row's
+ * output is unreliable) or SNA_WS_DIRTY_DONE (the finished-workgroups count past the grid: the counters may no longer
+ * return to zero by themselves).
+ * sna_stream_workspace_status waits for `stream`, returns the status word in *status (0: every launch since the last
+ * call found the block clean) and clears it. sna_stream_workspace_reset zeroes the counter block on `stream` (a fill
+ * kernel, no memset, so it may be captured); launches ordered after it find it clean. workspace_bytes is the
+ * workspace's size (at least the counter block). */
+#define SNA_WS_DIRTY_ARRIVAL 1
+#define SNA_WS_DIRTY_DONE 2
+int sna_stream_workspace_status(void *workspace, int64_t workspace_bytes, int32_t *status, void *stream);
+int sna_stream_workspace_reset(void *workspace, int64_t workspace_bytes, void *stream);
+
 /* Host check of one decode batch's operands, before any launch (host copies of every array):
  *   seq_lens     [B] int64, prefix plus the new token: each in [1, INT32_MAX] (positions are int32 in the kernels).
  *   block_table  [B, table_stride] int32, table_width valid columns: a row's ceil(seq_len / page_size) pages must fit

@@ -30,6 +30,8 @@ DTYPE_FP8_E4M3FN_MUL = 2  # FP8 bytes; the scales are the GPT-OSS quantization m
 MAX_CTAS = 256       # SNA_MAX_CTAS
 MAX_PLAN_ROWS = 256  # SNA_MAX_PLAN_ROWS
 STREAM_MAX_COUNTERS = 2047  # (row, head group) merge counters of one MLA / DSA launch
+WS_DIRTY_ARRIVAL = 1  # SNA_WS_DIRTY_ARRIVAL: a launch found a row's arrival count past its workgroups
+WS_DIRTY_DONE = 2     # SNA_WS_DIRTY_DONE: a launch found the finished-workgroups count past its grid
 SPARSE_MAX_RANGE_KEYS = 2048  # indices one DSA workgroup resolves
 
 KIND_GQA = 0
@@ -73,6 +75,8 @@ SIGNATURES = {
     "sna_plan_decode": (_I32, [_I32, _P, _I32, _I32, _I32, _I32, _I32, _I32, ctypes.POINTER(SplitPlan)]),
     "sna_decode_workspace_bytes": (_I64, [ctypes.POINTER(SplitPlan), _I32, _I32]),
     "sna_check_decode_operands": (_I32, [_P, _P, _I64, _I32, _P, _P, _I32, _I32, _I64]),
+    "sna_stream_workspace_status": (_I32, [_P, _I64, _P, _P]),
+    "sna_stream_workspace_reset": (_I32, [_P, _I64, _P]),
     "sna_paged_decode_gqa": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _I32, _F32, _P, _I32,
                                     _I32, _I32, _I32, _I32, _I64, _I32, ctypes.POINTER(SplitPlan), _P, _I64, _P]),
     "sna_paged_decode_gqa_noalloc": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _I32, _F32, _P,

@@ -69,7 +69,8 @@ struct MlaArgs {
   int32_t wait_polls;  // polls of a row's arrival counter by a workgroup that published a partial
   float* ws_o;         // [2 n_ctas, H, 512] partial contexts (unnormalized; ROWS640 in latent-byte order)
   float* ws_ml;        // [2 n_ctas, H, 2] their (max, sum), log2 domain
-  int32_t* ws_cnt;     // arrival words [kStreamMaxCounters], (unused) [kStreamMaxCounters], finished workgroups [1]
+  int32_t* ws_cnt;     // arrival words [kStreamMaxCounters], (unused) [kStreamMaxCounters], finished workgroups,
+                       // status (each a 64-byte line)
   const int32_t* seq_lens;  // paged [B] (device): a device-split launch cuts its stream from them
   uint16_t* out;
   float* lse_out;
@@ -1479,6 +1480,11 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
         const int32_t nown = min(S, 8);
         const int32_t old = __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int32_t k = old & 0xffff;
+        // a clean block counts the row's S arrivals 0 .. S - 1: anything else was left by an earlier launch (or one
+        // overlapping this one on the workspace), and this row's merge cannot be trusted
+        if (k >= S || ((uint32_t)old >> 24) != 0)
+          __hip_atomic_fetch_or(a.ws_cnt + kStreamStatusWord, SNA_WS_DIRTY_ARRIVAL, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
         uint32_t mine = 0;
         for (int32_t c = k; k < nown && c < 8; c += nown) mine |= 1u << c;
         uint32_t todo = 0;
@@ -1529,17 +1535,18 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
   // atomics on them have returned; its output stores need not have landed, so none is waited for here) ----
   __syncthreads();
   if (tid == 0) {
-    const int32_t done = __hip_atomic_fetch_add(a.ws_cnt + kCounterStride * 2 * kStreamMaxCounters, 1,
-                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int32_t done = __hip_atomic_fetch_add(a.ws_cnt + kStreamDoneWord, 1, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    if (done < 0 || done >= (int32_t)(gridDim.x * gridDim.y))
+      __hip_atomic_fetch_or(a.ws_cnt + kStreamStatusWord, SNA_WS_DIRTY_DONE, __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
     sm_word = done == (int32_t)(gridDim.x * gridDim.y) - 1;
   }
   __syncthreads();
   if (sm_word) {
     for (int32_t i = tid; i < a.B * a.groups; i += NT)
       __hip_atomic_store(a.ws_cnt + kCounterStride * i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (tid == 0)
-      __hip_atomic_store(a.ws_cnt + kCounterStride * 2 * kStreamMaxCounters, 0, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(a.ws_cnt + kStreamDoneWord, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1748,4 +1755,40 @@ extern "C" int sna_mla_decode_sparse(const void* q_absorbed, const void* q_pe, c
     else hipLaunchKernelGGL((mla_decode_kernel<ROWS640, false, false>), grid, dim3(256), 0, s, a);
   }
   return check_launch("mla_decode_sparse");
+}
+
+namespace {
+__global__ __launch_bounds__(256) void zero_words_kernel(int32_t* p, int32_t n) {
+  for (int32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0;
+}
+}  // namespace
+
+extern "C" int sna_stream_workspace_status(void* workspace, int64_t workspace_bytes, int32_t* status, void* stream) {
+  ApiGuard guard;
+  if (!workspace || !status || workspace_bytes < kStreamCounterBytes)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "stream_workspace_status: null pointer or a workspace of %lld bytes "
+                "(the counter block is %lld)", (long long)workspace_bytes, (long long)kStreamCounterBytes);
+  hipStream_t s = (hipStream_t)stream;
+  int32_t* word = (int32_t*)workspace + kStreamStatusWord;
+  int32_t v = 0;
+  static const int32_t zero = 0;
+  if (hipMemcpyAsync(&v, word, sizeof(v), hipMemcpyDeviceToHost, s) != hipSuccess || hipStreamSynchronize(s) != hipSuccess)
+    return fail(SNA_ERR_LAUNCH, "stream_workspace_status: reading the status word failed: %s",
+                hipGetErrorString(hipGetLastError()));
+  if (v != 0 && (hipMemcpyAsync(word, &zero, sizeof(zero), hipMemcpyHostToDevice, s) != hipSuccess ||
+                 hipStreamSynchronize(s) != hipSuccess))
+    return fail(SNA_ERR_LAUNCH, "stream_workspace_status: clearing the status word failed: %s",
+                hipGetErrorString(hipGetLastError()));
+  *status = v;
+  return SNA_OK;
+}
+
+extern "C" int sna_stream_workspace_reset(void* workspace, int64_t workspace_bytes, void* stream) {
+  ApiGuard guard;
+  if (!workspace || workspace_bytes < kStreamCounterBytes)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "stream_workspace_reset: null pointer or a workspace of %lld bytes "
+                "(the counter block is %lld)", (long long)workspace_bytes, (long long)kStreamCounterBytes);
+  const int32_t n = (int32_t)(kStreamCounterBytes / 4);
+  hipLaunchKernelGGL(zero_words_kernel, dim3(64), dim3(256), 0, (hipStream_t)stream, (int32_t*)workspace, n);
+  return check_launch("stream_workspace_reset");
 }

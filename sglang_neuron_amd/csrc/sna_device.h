@@ -27,11 +27,15 @@ constexpr int kGqaDevSplitMaxTiles = (1 << 17) - 1;
 constexpr int kMlaMaxSplitKeys = 2048;
 // The MLA / DSA stream split's counter block at the start of its workspace: per (row, head group) an arrival counter
 // and a mask of merged latent blocks, then one count of finished workgroups, each in a 64-byte line of its own; zero
-// at rest.
+// at rest. The last line holds a sticky status word: a launch that finds a counter past what a clean block allows
+// (an arrival past its row's count, or more finished workgroups than its grid) sets a bit there, and only the host's
+// sna_stream_workspace_status clears it.
 constexpr int kCounterStride = 16;        // int32 words between counters
 constexpr int kStreamMaxCounters = 2047;  // (row, head group) pairs the block holds
-constexpr int64_t kStreamCounterBytes = 256 * 1024;  // (2 * kStreamMaxCounters + 1) lines of 64 bytes, rounded up
-static_assert((2 * kStreamMaxCounters + 1) * kCounterStride * 4 <= kStreamCounterBytes, "the counters fit");
+constexpr int64_t kStreamCounterBytes = 256 * 1024;  // (2 * kStreamMaxCounters + 2) lines of 64 bytes
+constexpr int kStreamDoneWord = kCounterStride * 2 * kStreamMaxCounters;
+constexpr int kStreamStatusWord = kCounterStride * (2 * kStreamMaxCounters + 1);
+static_assert((2 * kStreamMaxCounters + 2) * kCounterStride * 4 <= kStreamCounterBytes, "the counters fit");
 // Polls of a row's arrival counter by a workgroup that published a partial, before it leaves the merge to others.
 constexpr int kStreamWaitPolls = 96;
 // A GQA plan's item map entry: row << 6 | split, with this bit set on a row's last item (its own token's split).

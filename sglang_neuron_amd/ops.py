@@ -380,6 +380,28 @@ def stream_workspace(plan: _lib.SplitPlan, heads: int, device: torch.device) -> 
     return torch.zeros(max(workspace_bytes(plan, heads, 512), 256), dtype=torch.uint8, device=device)
 
 
+def stream_workspace_status(ws: Tensor) -> int:
+    """The status word of an MLA / DSA workspace, cleared as it is read (sna_stream_workspace_status): 0 when every
+    launch on it since the last read found its counter block clean, else WS_DIRTY_ARRIVAL (a row's merge could not be
+    trusted) and / or WS_DIRTY_DONE (the counters may not return to zero by themselves: reset_stream_workspace).
+    Waits for the current stream."""
+    _need(ws.is_cuda and ws.dtype == torch.uint8 and ws.is_contiguous(), "workspace must be a contiguous uint8 GPU "
+          "tensor")
+    status = ctypes.c_int32(0)
+    rc = _lib.load().sna_stream_workspace_status(_ptr(ws), ws.numel(), ctypes.addressof(status), _stream(ws.device))
+    _lib.check(rc, "stream_workspace_status")
+    return int(status.value)
+
+
+def reset_stream_workspace(ws: Tensor) -> None:
+    """Zero an MLA / DSA workspace's counter block on the current stream (sna_stream_workspace_reset: a fill kernel,
+    so it may be captured in a graph)."""
+    _need(ws.is_cuda and ws.dtype == torch.uint8 and ws.is_contiguous(), "workspace must be a contiguous uint8 GPU "
+          "tensor")
+    _lib.check(_lib.load().sna_stream_workspace_reset(_ptr(ws), ws.numel(), _stream(ws.device)),
+               "stream_workspace_reset")
+
+
 def _host_lens(seq_lens: Tensor, host_seq_lens) -> Optional[Tensor]:
     if host_seq_lens is not None:
         return torch.as_tensor(host_seq_lens, dtype=torch.int32).reshape(-1)

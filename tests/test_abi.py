@@ -271,6 +271,17 @@ def test_stream_row_chunks_fit_one_plan_each(lib):
     assert ops.stream_row_chunks(_lib.KIND_MLA, 40, 16) == [(0, 40)]
 
 
+def test_stream_workspace_calls_refuse_bad_arguments(lib):
+    """The workspace status and reset calls refuse a null workspace or one smaller than the counter block before
+    touching a device."""
+    st = ctypes.c_int32(0)
+    assert lib.sna_stream_workspace_status(None, 1 << 20, ctypes.addressof(st), None) == _lib.SNA_ERR_INVALID_ARGUMENT
+    assert lib.sna_stream_workspace_status(ctypes.c_void_p(64), 4096, ctypes.addressof(st), None) == \
+        _lib.SNA_ERR_INVALID_ARGUMENT
+    assert lib.sna_stream_workspace_reset(ctypes.c_void_p(64), 4096, None) == _lib.SNA_ERR_INVALID_ARGUMENT
+    assert b"counter block" in lib.sna_last_error()
+
+
 def test_mla_plan_from_a_bound_is_a_device_split(lib):
     """Without host lengths an MLA plan is a device split: the launch cuts its stream from the device's seq_lens, so
     the plan fixes only the grid (a workgroup per CU and head group) and the workspace it is sized for."""

@@ -4,7 +4,7 @@ oracle on seeded cases, with the pools compared bit-exact after the step."""
 import pytest
 import torch
 
-from sglang_neuron_amd import ops, workloads
+from sglang_neuron_amd import _lib, ops, workloads
 from tests.conftest import announce
 from tests._harness import (assert_close_attn, dsa_gpu_pool, dsa_gpu_step, dsa_oracle, mla_gpu_decode, mla_gpu_pool,
                             mla_oracle)
@@ -230,6 +230,47 @@ def test_split_merge_when_polls_run_out(polls):
         torch.cuda.synchronize()
         assert torch.equal(ctx, base_ctx) and torch.equal(lse, base_lse), "DSA output differs from the default plan's"
     assert_close_attn(ctx, want_ctx, f"dsa polls={polls}")
+
+
+def test_dirty_counter_block_is_detected_and_reset():
+    """A workspace whose counter block is not zero on entry (planted from the host: a row's arrival count, then the
+    finished-workgroups count) sets the launch's sticky status bit, which stream_workspace_status reports and clears.
+    A clean block reads 0; after a dirty arrival the launch's own end returns the counters to zero, so the next call
+    is clean and matches the oracle; after a dirty finished count the counters stay dirty until
+    reset_stream_workspace, after which the call is clean and matches again. Every wait in the merge is bounded, so
+    each launch ends."""
+    dev = torch.device("cuda", 0)
+    case = workloads.mla_case(overrides={"B": 2, "lens": (3000, 4096)})
+    want, _, _ = mla_oracle(case)
+    cache, scale = mla_gpu_pool(case)
+    args = (case.ql_nope.to(dev), case.q_pe.to(dev), cache, scale, case.block_table.to(dev), case.seq_lens.to(dev),
+            case.compact_new.to(dev))
+    plan = ops.plan_decode(1, case.B, host_seq_lens=case.seq_lens, ctas_per_item=1, num_cus=ops._num_cus(dev))
+    assert plan.max_splits > 3
+    ws = ops.stream_workspace(plan, case.H, dev)
+    kw = dict(sm_scale=case.sm_scale, page_size=case.P, new_slots=case.new_slots.to(dev), host_seq_lens=case.seq_lens,
+              plan=plan, workspace=ws)
+    words = ws.view(torch.int32)
+    announce(f"mla dirty counters: B={case.B} n_ctas={plan.n_ctas} max_splits={plan.max_splits}")
+
+    def clean_call():
+        out = ops.mla_decode(*args, **kw)
+        assert ops.stream_workspace_status(ws) == 0
+        assert_close_attn(out, want, "clean call")
+
+    clean_call()
+    words[0] = 3  # row 0's arrival word (head group 0)
+    ops.mla_decode(*args, **kw)
+    assert ops.stream_workspace_status(ws) & _lib.WS_DIRTY_ARRIVAL
+    assert ops.stream_workspace_status(ws) == 0  # read and cleared
+    clean_call()  # the dirty launch's end zeroed the counters
+    words[16 * 2 * _lib.STREAM_MAX_COUNTERS] = 1 << 20  # the finished-workgroups count
+    ops.mla_decode(*args, **kw)
+    assert ops.stream_workspace_status(ws) & _lib.WS_DIRTY_DONE
+    ops.reset_stream_workspace(ws)
+    torch.cuda.synchronize()
+    assert int(words[:16 * 2 * _lib.STREAM_MAX_COUNTERS + 16].abs().sum()) == 0
+    clean_call()
 
 
 def test_dsa_pool_past_4gib():

@@ -51,11 +51,9 @@ __global__ __launch_bounds__(256) void kv_store_mha_kernel(const uint16_t* __res
     } else if (rcp_scale_ok(ks) && rcp_scale_ok(vs)) {
       const float rks = 1.0f / ks, rvs = 1.0f / vs;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t kb = (kw[i >> 1] >> ((i & 1) * 16)) & 0xffffu;
-        const uint32_t vb = (vw[i >> 1] >> ((i & 1) * 16)) & 0xffffu;
-        ko[i >> 2] |= quantize_e4m3fn_rcp(kb, ks, rks) << ((i & 3) * 8);
-        vo[i >> 2] |= quantize_e4m3fn_rcp(vb, vs, rvs) << ((i & 3) * 8);
+      for (int i = 0; i < 4; ++i) {
+        ko[i >> 1] |= quantize_pair_e4m3fn_hw(kw[i], ks, rks) << ((i & 1) * 16);
+        vo[i >> 1] |= quantize_pair_e4m3fn_hw(vw[i], vs, rvs) << ((i & 1) * 16);
       }
     } else {
 #pragma unroll

@@ -3,23 +3,26 @@
 // pass over the projection's output.
 //
 // Heads are ordered [Q 0 .. Hq) [K 0 .. Hkv) [V 0 .. Hkv) as the fused projection lays them out. Every rounding step
-// of the reference's torch path is kept: the norm rounds x * rsqrt(mean + eps) to bf16 and multiplies by the bf16 gamma with a bf16 result; RoPE rounds each product and the
-// sum to bf16. The sum of squares is fp32 in a wave-reduction order, so with the norm on a value can differ from the
-// reference's by one bf16 step where that order changes the sum's last bit; without the norm the path is bit-exact.
+// of the reference's torch path is kept: the norm rounds x * rsqrt(mean + eps) to bf16 and multiplies by the bf16
+// gamma with a bf16 result; RoPE rounds each product and the sum to bf16. The sum of squares is fp32 in a fixed
+// order (each square rounded, a lane's 8 in sequence, the head's lanes folded in halves) and 1 / sqrt is correctly
+// rounded, the order and roundings the oracle states, so Q and both pools are bit-exact with it; a NaN output is a NaN
+// where the reference's is (its bits are not fixed, there or here).
 #include "sna_device.h"
 #include "sna_host.h"
 
 namespace sna {
 
-// x rounded to bf16 (nearest even) and back, by the hardware conversion (v_cvt_pk_bf16_f32). It equals
-// f32_to_bf16_bits for every non-NaN input; a NaN stays a NaN, and the final conversion of each output writes the
-// canonical NaN, as torch does.
-__device__ __forceinline__ float bf16_round(float x) { return (float)(__bf16)x; }
-
-// Two floats that are already bf16 values, packed (lo in the low half) by one byte permute.
-__device__ __forceinline__ uint32_t pack_exact(float lo, float hi) {
-  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+// Two floats each rounded to bf16 (nearest even) and packed, lo in the low half, by one hardware conversion
+// (v_cvt_pk_bf16_f32). Each half equals f32_to_bf16_bits of its input for every non-NaN input; a NaN stays a NaN
+// (with its sign and leading payload bits: a NaN's bits are not fixed by the reference either, whose float to bf16
+// conversion writes 0x7FC0 or 0xFFFF depending on the code path torch takes).
+__device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
+// The halves of a bf16 pair as floats.
+__device__ __forceinline__ float lo_f(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float hi_f(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
 
 // The value of the lane `half` lanes away inside the head's lane group (lane ^ half). A 16-lane group (D = 128) is one
 // DPP row, where a rotation by 8 is that exchange; other widths go through the LDS crossbar.
@@ -47,21 +50,15 @@ __device__ __forceinline__ float group_sum(float v) {
   }
 }
 
-// Two floats rounded to bf16 (nearest even) and packed by one conversion, each NaN written as the canonical 0x7FC0
-// (f32_to_bf16_bits' and torch's NaN).
-__device__ __forceinline__ uint32_t round_pack(float lo, float hi) {
-  const bf16x2_t v = __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t);
-  uint32_t r = __builtin_bit_cast(uint32_t, v);
-  if (lo != lo) r = (r & 0xffff0000u) | 0x7fc0u;
-  if (hi != hi) r = (r & 0x0000ffffu) | 0x7fc00000u;
-  return r;
-}
 
 // Lane layout: a head row of D bf16 is D / 8 lanes of 16 bytes (LPH lanes per head, 64 / LPH heads per wave), so
 // every load and store is a 16-byte vector access. Lane j of a head holds elements 8 j .. 8 j + 7; its rotate-half
-// partner (the lane LPH / 2 away) holds the elements D / 2 further on, fetched by one xor shuffle per dword. A unit is
-// (token, a wave's worth of consecutive heads); a head's type (Q, K, V) is fixed per LPH-lane group.
-template <bool FP8, int D>
+// partner (the lane LPH / 2 away) holds the elements D / 2 further on, fetched by one xor shuffle per dword. A
+// workgroup takes one group of 64 / LPH consecutive heads (blockIdx.y; a head's type, Q, K or V, is fixed per
+// LPH-lane group) over 4 U consecutive tokens (blockIdx.x), U per wave: the loads of the wave's U tokens are all issued
+// before any is computed, and what depends only on the head (its gamma, its scale and that scale's reciprocal, its
+// cache) is fetched once per wave.
+template <bool FP8, int D, int U>
 __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
     const uint16_t* __restrict__ qkv, int64_t qkv_stride, int64_t n_tokens, int32_t Hq, int32_t Hkv,
     const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm, float eps,
@@ -72,23 +69,55 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
   constexpr int LPH = D / 8, HPW = 64 / LPH, HALF = LPH / 2;
   const int lane = threadIdx.x & 63, sub = lane % LPH;
   const int32_t heads = Hq + 2 * Hkv;
-  const int32_t groups = (heads + HPW - 1) / HPW;
-  const int64_t units = n_tokens * groups;
+  const int32_t head = (int32_t)blockIdx.y * HPW + lane / LPH;
+  const bool head_ok = head < heads;
+  const bool is_q = head < Hq, is_k = !is_q && head < Hq + Hkv, roped = head < Hq + Hkv;
   const bool first = sub < HALF;
-  // U units per wave per pass: the loads of all U are issued before any is computed
-  constexpr int U = 1;
-  auto process = [&](int64_t u, const uint4& w, const uint4& cw, const uint4& sw) {
-    const int64_t t = u / groups;
-    const int32_t head = (int32_t)(u % groups) * HPW + lane / LPH;
-    const bool live = u < units && head < heads;
-    const bool is_q = head < Hq, is_k = !is_q && head < Hq + Hkv;
-    float x[8];
-    {
-      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+  const int64_t t0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * U;
+
+  // this wave's U tokens: the head rows, the rotation rows (Q and K) and the slots (K and V), all loads in flight
+  uint4 w[U], cw[U], sw[U];
+  int64_t slot[U];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = bf16_bits_to_f32((ww[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+  for (int k = 0; k < U; ++k) {
+    const int64_t t = t0 + k;
+    const bool live = t < n_tokens && head_ok;
+    w[k] = live ? ld16(qkv + t * qkv_stride + (int64_t)head * D + 8 * sub) : make_uint4(0, 0, 0, 0);
+    cw[k] = sw[k] = make_uint4(0, 0, 0, 0);
+    if (live && roped) {
+      cw[k] = ld16(cosv + t * rope_stride + 8 * sub);
+      sw[k] = ld16(sinv + t * rope_stride + 8 * sub);
     }
-    if (q_norm) {  // uniform: both gammas or neither
+    slot[k] = (live && !is_q) ? slots[t] : 0;
+  }
+  // per head: the gamma (Q and K with the norm), the cache and its scale (K and V)
+  uint32_t gg[4] = {0, 0, 0, 0};
+  if (q_norm && head_ok && roped) {  // q_norm: uniform, both gammas or neither
+    const uint4 gw = ld16((is_q ? q_norm : k_norm) + 8 * sub);
+    gg[0] = gw.x;
+    gg[1] = gw.y;
+    gg[2] = gw.z;
+    gg[3] = gw.w;
+  }
+  const int32_t h = head - Hq - (is_k ? 0 : Hkv);  // the KV head (K and V lanes)
+  float scl = 1.0f, rs = 1.0f;
+  bool rcp_ok = false;
+  if (FP8 && head_ok && !is_q) {
+    scl = is_k ? k_scale[h] : v_scale[h];
+    rcp_ok = rcp_scale_ok(scl);
+    rs = rcp_ok ? 1.0f / scl : 1.0f;
+  }
+  uint8_t* const cache = is_k ? kc : vc;
+  const bool p_pow2 = (P & (P - 1)) == 0;  // uniform: the slot's page and offset by shifts
+  const int p_shift = __builtin_ctz((uint32_t)P);
+
+  const float sgn = first ? -1.0f : 1.0f;  // rotate-half: the first half takes the partner's value negated
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    const int64_t t = t0 + k;
+    const bool live = t < n_tokens && head_ok;
+    uint32_t xp[4] = {w[k].x, w[k].y, w[k].z, w[k].w};  // the lane's 8 elements as bf16 pairs
+    if (q_norm) {  // uniform
       // _rms: gamma * (x32 * rsqrt(mean(x32^2) + eps)).to(bf16), rsqrt as 1 / sqrt (both correctly rounded). The
       // sum of squares: each square rounded (pow(2)), a lane's 8 summed in sequence, then the head's LPH lane sums
       // folded in halves (group_sum; every lane takes part in the shuffles)
@@ -96,63 +125,66 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
       {
 #pragma clang fp contract(off)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ss = ss + x[e] * x[e];
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const float a = lo_f(xp[e2]), b = hi_f(xp[e2]);
+          ss = ss + a * a;
+          ss = ss + b * b;
+        }
       }
       ss = group_sum<HALF>(ss);
-      if (live && (is_q || is_k)) {
+      if (live && roped) {
         const float inv = 1.0f / sqrtf(ss / (float)D + eps);  // sqrtf: correctly rounded (__fsqrt_rn is the native one)
-        const uint4 gw = ld16((is_q ? q_norm : k_norm) + 8 * sub);
-        const uint32_t gg[4] = {gw.x, gw.y, gw.z, gw.w};
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          x[e] = bf16_round(bf16_bits_to_f32((gg[e >> 1] >> (16 * (e & 1))) & 0xffffu) * bf16_round(x[e] * inv));
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const uint32_t n = cvt_pk(lo_f(xp[e2]) * inv, hi_f(xp[e2]) * inv);
+          xp[e2] = cvt_pk(lo_f(gg[e2]) * lo_f(n), hi_f(gg[e2]) * hi_f(n));
+        }
       }
     }
     // the partner's elements (every lane takes part in the shuffles)
     uint32_t pw[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      pw[e] = partner<HALF>(pack_exact(x[2 * e], x[2 * e + 1]));
-    if (!live) return;
+    for (int e2 = 0; e2 < 4; ++e2) pw[e2] = partner<HALF>(xp[e2]);
+    if (!live) continue;
     uint32_t ob[4];
-    if (is_q || is_k) {
-      // rope(t) = t * c + cat(-t[D/2:], t[:D/2]) * s, every product and the sum rounded to bf16 (the sums by the
-      // packing conversion)
-      const uint32_t cc[4] = {cw.x, cw.y, cw.z, cw.w}, sc[4] = {sw.x, sw.y, sw.z, sw.w};
+    bool nan = false;  // a NaN among the lane's 8 output elements
+    if (roped) {
+      // rope(t) = t * c + cat(-t[D/2:], t[:D/2]) * s, every product and the sum rounded to bf16: each element's two
+      // products by one pair conversion, the sum by the output's (sgn * r exact, so the FMA rounds once, as the sum)
+      const uint32_t cc[4] = {cw[k].x, cw[k].y, cw[k].z, cw[k].w}, sc[4] = {sw[k].x, sw[k].y, sw[k].z, sw[k].w};
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
-        float y[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int e = 2 * e2 + i;
-          const float c = bf16_bits_to_f32((cc[e2] >> (16 * i)) & 0xffffu);
-          const float sn = bf16_bits_to_f32((sc[e2] >> (16 * i)) & 0xffffu);
-          const float p = bf16_bits_to_f32((pw[e2] >> (16 * i)) & 0xffffu);
-          y[i] = bf16_round(x[e] * c) + bf16_round((first ? -p : p) * sn);
-        }
-        ob[e2] = round_pack(y[0], y[1]);
+        const uint32_t r0 = cvt_pk(lo_f(xp[e2]) * lo_f(cc[e2]), lo_f(pw[e2]) * lo_f(sc[e2]));
+        const uint32_t r1 = cvt_pk(hi_f(xp[e2]) * hi_f(cc[e2]), hi_f(pw[e2]) * hi_f(sc[e2]));
+        const float y0 = fmaf(sgn, hi_f(r0), lo_f(r0)), y1 = fmaf(sgn, hi_f(r1), lo_f(r1));
+        nan |= (y0 != y0) | (y1 != y1);
+        ob[e2] = cvt_pk(y0, y1);
       }
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) ob[e] = pack_exact(x[2 * e], x[2 * e + 1]);
+      for (int e2 = 0; e2 < 4; ++e2) {
+        ob[e2] = xp[e2];
+        nan |= (lo_f(xp[e2]) != lo_f(xp[e2])) | (hi_f(xp[e2]) != hi_f(xp[e2]));
+      }
     }
     if (is_q) {
       *reinterpret_cast<uint4*>(q_out + (t * Hq + head) * D + 8 * sub) = make_uint4(ob[0], ob[1], ob[2], ob[3]);
-      return;
+      continue;
     }
     // K (rotated) or V into the pool at the token's slot, as the MHA store writes it
-    const int32_t h = head - Hq - (is_k ? 0 : Hkv);
-    const int64_t slot = redirect_slot(slots[t], num_slots);
-    const int64_t dst = (((slot / P) * Hkv + h) * P + slot % P) * D + 8 * sub;
-    uint8_t* cache = is_k ? kc : vc;
+    const int64_t sl = redirect_slot(slot[k], num_slots);
+    const int64_t page = p_pow2 ? sl >> p_shift : sl / P;
+    const int64_t off = p_pow2 ? sl & (P - 1) : sl % P;
+    const int64_t dst = ((page * Hkv + h) * P + off) * D + 8 * sub;
     if constexpr (FP8) {
-      const float scl = is_k ? k_scale[h] : v_scale[h];
       uint32_t q8[2] = {0, 0};
-      if (rcp_scale_ok(scl)) {
-        const float rs = 1.0f / scl;
+      if (rcp_ok && !__any(nan)) {  // uniform: NaNs are rare, and only a wave that holds one takes their path
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          q8[e >> 2] |= quantize_e4m3fn_rcp((ob[e >> 1] >> (16 * (e & 1))) & 0xffffu, scl, rs) << (8 * (e & 3));
+        for (int e2 = 0; e2 < 4; ++e2)
+          q8[e2 >> 1] |= quantize_pair_e4m3fn_hw_nonan(lo_f(ob[e2]), hi_f(ob[e2]), scl, rs) << (16 * (e2 & 1));
+      } else if (rcp_ok) {
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) q8[e2 >> 1] |= quantize_pair_e4m3fn_hw(ob[e2], scl, rs) << (16 * (e2 & 1));
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
@@ -162,27 +194,11 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
     } else {
       *reinterpret_cast<uint4*>(cache + 2 * dst) = make_uint4(ob[0], ob[1], ob[2], ob[3]);
     }
-  };
-  const int64_t stride = (int64_t)gridDim.x * 4 * U;
-  for (int64_t base = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * U; base < units; base += stride) {
-    uint4 w[U], cw[U], sw[U];
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const int64_t u = base + k;
-      const int64_t t = u / groups;
-      const int32_t head = (int32_t)(u % groups) * HPW + lane / LPH;
-      const bool live = u < units && head < heads;
-      w[k] = live ? ld16(qkv + t * qkv_stride + (int64_t)head * D + 8 * sub) : make_uint4(0, 0, 0, 0);
-      cw[k] = sw[k] = make_uint4(0, 0, 0, 0);
-      if (live && head < Hq + Hkv) {
-        cw[k] = ld16(cosv + t * rope_stride + 8 * sub);
-        sw[k] = ld16(sinv + t * rope_stride + 8 * sub);
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < U; ++k) process(base + k, w[k], cw[k], sw[k]);
   }
 }
+
+// Tokens per wave of a launch (their loads in flight together).
+constexpr int kQkvTokensPerWave = 2;
 
 }  // namespace sna
 
@@ -221,13 +237,21 @@ extern "C" int sna_qkv_norm_rope_store(const void* qkv, int64_t qkv_stride, int6
       !aligned(q_out, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || (q_norm && (!aligned(q_norm, 16) ||
       !aligned(k_norm, 16))))
     return fail(SNA_ERR_INVALID_ARGUMENT, "qkv_norm_rope_store: tensors and row strides must be 16-byte aligned");
+  constexpr int U = kQkvTokensPerWave;
   const int32_t hpw = 64 / (head_dim / 8);
-  const int64_t units = n_tokens * ((num_q_heads + 2 * num_kv_heads + hpw - 1) / hpw);
-  const unsigned grid = (unsigned)std::min<int64_t>((units + 4 * 1 - 1) / (4 * 1), (int64_t)1 << 22);  // 4 waves x U
+  const int64_t token_blocks = (n_tokens + 4 * U - 1) / (4 * U);  // 4 waves x U tokens
+  if (token_blocks > INT32_MAX)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "qkv_norm_rope_store: %lld tokens is too many for one launch",
+                (long long)n_tokens);
+  const int64_t head_groups = (num_q_heads + 2 * (int64_t)num_kv_heads + hpw - 1) / hpw;
+  if (head_groups > 65535)
+    return fail(SNA_ERR_INVALID_ARGUMENT, "qkv_norm_rope_store: %lld heads is too many for one launch",
+                (long long)num_q_heads + 2ll * num_kv_heads);
+  const dim3 grid((unsigned)token_blocks, (unsigned)head_groups);
   const int64_t num_slots = num_blocks * page_size;
   hipStream_t s = (hipStream_t)stream;
 #define SNA_QKV_LAUNCH(F, DD)                                                                                   \
-  hipLaunchKernelGGL((qkv_norm_rope_store_kernel<F, DD>), dim3(grid), dim3(256), 0, s, (const uint16_t*)qkv,     \
+  hipLaunchKernelGGL((qkv_norm_rope_store_kernel<F, DD, U>), grid, dim3(256), 0, s, (const uint16_t*)qkv,         \
                      qkv_stride, n_tokens, num_q_heads, num_kv_heads, (const uint16_t*)q_norm,                   \
                      (const uint16_t*)k_norm, eps, (const uint16_t*)cos, (const uint16_t*)sin, rope_stride, slots, \
                      (uint16_t*)q_out, (uint8_t*)k_cache, (uint8_t*)v_cache, k_scale, v_scale, num_slots, page_size)

@@ -107,28 +107,6 @@ __device__ __forceinline__ uint32_t quantize_e4m3fn(uint32_t bf16_bits, float s)
   return f32_to_e4m3fn(clamp_fp8(bf16_bits_to_f32(bf16_bits) / s));
 }
 
-// The same quantizer without a division per element or branches, for a scale s whose correctly rounded reciprocal rs
-// = 1 / s the caller computes once (s positive and normal; otherwise use quantize_e4m3fn). |x| / s is q0 = |x| * rs,
-// within an ulp, corrected once by its exact FMA residual (Markstein's sequence, which yields the correctly rounded
-// quotient from a correctly rounded reciprocal); an overflowing q0 (|x| infinite or the quotient past the float range)
-// stands for itself, since the clamp maps it to 448 like the exact quotient. The sign goes on last, so -0 stays -0.
-// Both e4m3fn encodings (subnormal, normal) are computed and one is selected.
-__device__ __forceinline__ uint32_t quantize_e4m3fn_rcp(uint32_t bf16_bits, float s, float rs) {
-  const float x = bf16_bits_to_f32(bf16_bits);
-  const float a = fabsf(x);
-  const float q0 = a * rs;
-  const float q1 = q0 == __builtin_inff() ? q0 : fmaf(fmaf(-q0, s, a), rs, q0);
-  const float y = clamp_fp8(copysignf(q1, x));
-  const uint32_t u = __float_as_uint(y);
-  const uint32_t sign = (u >> 24) & 0x80u;
-  const uint32_t m = u & 0x7fffffffu;
-  const uint32_t sub = (uint32_t)__builtin_rintf(__uint_as_float(m) * 512.0f);
-  const uint32_t nrm = ((m + 0x7ffffu + ((m >> 20) & 1u)) >> 20) - 960u;
-  uint32_t r = m < 0x3c800000u ? sub : nrm;
-  r = (m > 0x7f800000u || r > 0x7eu) ? 0x7fu : r;
-  return sign | r;
-}
-
 // The GPT-OSS decode write (attention_decode.py:259-260): a bf16 element times the bf16 quantization multiplier m
 // (the inverted checkpoint scale, gpt_oss/mxfp4/common.py:481-485), the product rounded to bf16 as a product of two
 // bf16 tensors is, then clamped to +-448 (exact in bf16) and cast. The fp32 product of two bf16 values is exact (two
@@ -139,7 +117,34 @@ __device__ __forceinline__ uint32_t quantize_e4m3fn_mul(uint32_t bf16_bits, floa
   return f32_to_e4m3fn(clamp_fp8(bf16_bits_to_f32(f32_to_bf16_bits(p))));
 }
 
-// Whether quantize_e4m3fn_rcp serves the scale s (a positive normal float).
+// quantize_e4m3fn of the two bf16 elements packed in `pair` (low half first), as a 16-bit pair of bytes (the low
+// element's in the low byte), without a division per element: through the hardware conversion v_cvt_pk_fp8_f32
+// (round to nearest even onto the OCP e4m3fn grid, subnormals included). The signed quotient x / s comes from x * rs held to +-1024 (beyond it the clamp
+// gives +-448 whatever the rounding), corrected once by its exact FMA residual (Markstein's sequence: the correctly
+// rounded quotient from the correctly rounded reciprocal rs = 1 / s), then clamped to +-448 by a median, so the
+// conversion never overflows, and given x's sign (the residual's exact zero is +0, which would turn -0 into +0); a
+// NaN element is written as its sign | 0x7F, as f32_to_e4m3fn writes it. s positive and normal (rcp_scale_ok).
+__device__ __forceinline__ float with_sign_of(float mag, float x) {
+  return __uint_as_float((__float_as_uint(mag) & 0x7fffffffu) | (__float_as_uint(x) & 0x80000000u));
+}
+// The bytes of two elements x0, x1 that are not NaN (bf16 values as floats): quantize_pair_e4m3fn_hw without its NaN
+// step.
+__device__ __forceinline__ uint32_t quantize_pair_e4m3fn_hw_nonan(float x0, float x1, float s, float rs) {
+  const float q0 = __builtin_amdgcn_fmed3f(x0 * rs, -1024.0f, 1024.0f);
+  const float q1 = __builtin_amdgcn_fmed3f(x1 * rs, -1024.0f, 1024.0f);
+  const float y0 = with_sign_of(__builtin_amdgcn_fmed3f(fmaf(fmaf(-q0, s, x0), rs, q0), -kFp8Max, kFp8Max), x0);
+  const float y1 = with_sign_of(__builtin_amdgcn_fmed3f(fmaf(fmaf(-q1, s, x1), rs, q1), -kFp8Max, kFp8Max), x1);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false) & 0xffffu;
+}
+__device__ __forceinline__ uint32_t quantize_pair_e4m3fn_hw(uint32_t pair, float s, float rs) {
+  const float x0 = __uint_as_float(pair << 16), x1 = __uint_as_float(pair & 0xffff0000u);
+  uint32_t b = quantize_pair_e4m3fn_hw_nonan(x0, x1, s, rs);
+  if (x0 != x0) b = (b & 0xff00u) | ((pair >> 8) & 0x80u) | 0x7fu;
+  if (x1 != x1) b = (b & 0x00ffu) | ((((pair >> 24) & 0x80u) | 0x7fu) << 8);
+  return b;
+}
+
+// Whether quantize_pair_e4m3fn_hw serves the scale s (a positive normal float; otherwise use quantize_e4m3fn).
 __device__ __forceinline__ bool rcp_scale_ok(float s) { return s >= 1.17549435e-38f && s <= 3.40282347e+38f; }
 
 // The scale rule for per-head and per-token scales: absmax / 448, or 1 for an all-zero operand (whose bytes are then

@@ -21,6 +21,9 @@ CASES = [
     # d 64 with the norm: the lane sums fold through xor shuffles instead of DPP rotations
     ("d64-bf16-norm", 129, 8, 2, 64, 16, False, True),
     ("d64-fp8-norm", 77, 4, 4, 64, 16, True, True),
+    # a page size that is not a power of two: the slot's page and offset by division
+    ("fp8-page24-norm", 61, 4, 2, 128, 24, True, True),
+    ("bf16-page24", 50, 4, 2, 64, 24, False, False),
 ]
 
 
@@ -64,6 +67,55 @@ def test_qkv_writer_matches_oracle(name, T, Hq, Hkv, d, P, fp8, norm):
     # with the QK norm too: the oracle sums the squares in the order the writer's lanes do (oracle.qkv.sum_of_squares)
     assert torch.equal(q.cpu(), q_o), "Q differs"
     assert torch.equal(kb, kc_o), "K pool differs"
+
+
+@pytest.mark.parametrize("fp8,norm", [(True, True), (True, False), (False, True), (False, False)])
+def test_qkv_writer_nan_and_inf_bits(fp8, norm):
+    """NaN (both signs, assorted payloads) and infinities in the projection output and the rotation rows: Q and K
+    against the oracle with NaN exactly where the oracle has NaN and every other value bit for bit (a NaN's bits are
+    not fixed by the reference: torch's float to bf16 conversion writes 0x7FC0 or 0xFFFF depending on its code path,
+    and an FP8 byte of a NaN is 0x7F or 0xFF by that NaN's sign); V, copied or quantized from the input, bit for bit
+    (a bf16 pool keeps the input's bits, an FP8 byte of a NaN is its sign | 0x7F). Covers the kernel's uniform NaN
+    branch (a wave with a NaN takes the exact quantizer, one without the fast one)."""
+    announce(f"qkv NaN/inf fp8={fp8} norm={norm}")
+    T, Hq, Hkv, d, P = 96, 8, 2, 128, 16
+    qkv, cos, sin, slots, qn, kn, ks, vs, nb = _inputs(T, Hq, Hkv, d, P, fp8, norm, 11)
+    g = torch.Generator().manual_seed(12)
+    i16 = lambda v: v - (1 << 16) if v >= 1 << 15 else v  # noqa: E731  (a bf16 bit pattern as int16)
+    bits = qkv.view(torch.int16)
+    specials = torch.tensor([i16(v) for v in (0x7FC0, 0xFFC0, 0x7F81, 0xFFFF, 0x7FA5, 0x7F80, 0xFF80)],
+                            dtype=torch.int16)
+    where = torch.randperm(bits.numel(), generator=g)[:60]  # a few tokens' rows, most rows clean
+    bits.view(-1)[where] = specials[torch.arange(60) % len(specials)]
+    cos.view(torch.int16)[5, 3] = i16(0x7F80)   # +inf: inf * 0 and inf - inf reach the sums
+    sin.view(torch.int16)[9, 70] = i16(0xFF80)
+    dt = torch.uint8 if fp8 else torch.bfloat16
+    kc_o, vc_o = torch.zeros(nb, Hkv, P, d, dtype=dt), torch.zeros(nb, Hkv, P, d, dtype=dt)
+    q_o = oqkv.qkv_norm_rope_store(qkv, cos, sin, Hq, Hkv, d, kc_o, vc_o, slots, qn, kn, 1e-6, ks, vs)
+    dev = "cuda"
+    gdt = torch.float8_e4m3fn if fp8 else torch.bfloat16
+    kc = torch.zeros(nb, Hkv, P, d, dtype=gdt, device=dev)
+    vc = torch.zeros(nb, Hkv, P, d, dtype=gdt, device=dev)
+    q = ops.qkv_norm_rope_store(qkv.to(dev), cos=cos.to(dev), sin=sin.to(dev), num_q_heads=Hq, num_kv_heads=Hkv,
+                                d_head=d, k_cache=kc, v_cache=vc, slot_mapping=slots.to(dev),
+                                q_norm=None if qn is None else qn.to(dev), k_norm=None if kn is None else kn.to(dev),
+                                norm_eps=1e-6, k_scale=None if ks is None else ks.to(dev),
+                                v_scale=None if vs is None else vs.to(dev))
+    torch.cuda.synchronize()
+    as_bits = lambda t: t.contiguous().view(torch.uint8)  # noqa: E731
+
+    def same_up_to_nan_bits(got, want, what):
+        if got.dtype == torch.uint8:  # FP8 bytes: 0x7F / 0xFF are NaN
+            gn, wn = (got & 0x7F) == 0x7F, (want & 0x7F) == 0x7F
+        else:
+            gn, wn = torch.isnan(got.float()), torch.isnan(want.float())
+        assert torch.equal(gn, wn), f"{what}: NaN at different places"
+        assert torch.equal(as_bits(got[~gn]), as_bits(want[~wn])), f"{what}: non-NaN values differ"
+
+    assert bool(torch.isnan(q_o.float()).any()), "the case must reach NaN outputs"
+    same_up_to_nan_bits(q.cpu(), q_o, "Q")
+    same_up_to_nan_bits(kc.cpu().view(torch.uint8) if fp8 else kc.cpu(), kc_o, "K pool")
+    assert torch.equal(as_bits(vc.cpu()), as_bits(vc_o)), "V pool bits differ"
 
 
 def test_qkv_writer_norm_within_a_bf16_step_of_the_reference_formula():

@@ -249,12 +249,6 @@ void gqa_decode_kernel(GqaArgs a) {
   // uniform across the workgroup; a split past the plan's count (a length beyond the plan's bound) is dropped, so no
   // write leaves the workspace
   if (b < 0 || b >= a.B || split >= max(a.max_splits, 1)) return;
-  if (!a.dev_split) L = ld_const(a.seq_lens + b);
-  L = __builtin_amdgcn_readfirstlane(L);
-  const KeyRange kr = key_range(L, a.window);
-  const int32_t t_first = kr.lo / 32 + split * st;
-  const int32_t t_last = min(t_first + st, (kr.hi + 31) / 32);
-
   // Query operand: in step s lane (g4, li) holds head li's 8 elements from dim CE (4 c + g4) + w, with CE the
   // elements of a 16-byte cache chunk and 8 s = CE c + w: the dims of the key bytes it feeds in that step.
   constexpr int CE = 16 / ESZ;
@@ -274,6 +268,12 @@ void gqa_decode_kernel(GqaArgs a) {
     }
   }
 
+  // The row's length by a vector load issued after the query's, so neither the kernel-argument waits nor the query's
+  // wait for it: for a full-attention row the split's block-table entries load beside it too. (mbcnt_lo(0, 0) is 0 in
+  // every lane, but not provably uniform, so the load stays a vector load.)
+  int32_t len_v = L;
+  if (!a.dev_split) len_v = a.seq_lens[b + (int32_t)__builtin_amdgcn_mbcnt_lo(0u, 0u)];
+
   // the stored scales, and the dequantization scales they give (m -> 1 / m for the GPT-OSS multipliers)
   const float kstored = FP8 ? a.k_scale[g] : 1.0f;
   const float vstored = FP8 ? a.v_scale[g] : 1.0f;
@@ -291,14 +291,33 @@ void gqa_decode_kernel(GqaArgs a) {
   auto column = [&](int32_t key) -> int32_t { return p_pow2 ? key >> p_shift : key / a.P; };
   auto in_page = [&](int32_t key) -> int32_t { return p_pow2 ? key & (a.P - 1) : key % a.P; };
   // The split's block-table entries, when they fit in 256: column col0 + 64 r + lane in pg[r], -1 past the table
-  // (then a tile's page is a readlane instead of a scalar load and its wait).
-  const int32_t col0 = column(t_first * 32);
-  const bool pre = column(t_last * 32 - 1) - col0 < 256;
+  // (then a tile's page is a readlane instead of a scalar load and its wait). Without a window the split's first
+  // tile is split * st whatever the row's length, so when a split of st tiles spans at most 256 columns the entries
+  // load before the length is known (uniform).
+  const int32_t span = (32 % a.P == 0) ? st * 32 / a.P : (st * 32 + a.P - 1) / a.P + 1;
+  const bool early = a.window == 0 && span <= 256;
+  int32_t col0 = column(split * st * 32);
   int32_t pg[4];
+  if (early) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int32_t c = col0 + 64 * r + lane;
-    pg[r] = (pre && c < a.table_width) ? trow[c] : -1;
+    for (int r = 0; r < 4; ++r) {
+      const int32_t c = col0 + 64 * r + lane;
+      pg[r] = c < a.table_width ? trow[c] : -1;
+    }
+  }
+  L = __builtin_amdgcn_readfirstlane(len_v);
+  const KeyRange kr = key_range(L, a.window);
+  const int32_t t_first = kr.lo / 32 + split * st;
+  const int32_t t_last = min(t_first + st, (kr.hi + 31) / 32);
+  bool pre = true;
+  if (!early) {
+    col0 = column(t_first * 32);
+    pre = column(t_last * 32 - 1) - col0 < 256;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int32_t c = col0 + 64 * r + lane;
+      pg[r] = (pre && c < a.table_width) ? trow[c] : -1;
+    }
   }
   auto table_entry = [&](int32_t col) -> int32_t {
     if (pre) {

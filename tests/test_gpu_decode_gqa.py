@@ -95,27 +95,33 @@ def test_gqa_invalid_pages_are_masked():
     assert_close_attn(out, want, "-1 pages")
 
 
+@pytest.mark.parametrize("window", [0, 100], ids=["full", "window100"])
 @pytest.mark.parametrize("mapped", [True, False], ids=["item-map", "located"])
-def test_plan_for_longer_rows_still_attends_and_stores_the_own_token(mapped):
+def test_plan_for_longer_rows_still_attends_and_stores_the_own_token(mapped, window):
     """A plan made for longer rows than the device holds (its last splits cover no key of the device's rows) still
     attends and stores every row's own token: the last split the launch runs for a row takes it, whether the plan
-    carries an item map (host lengths) or the items are located from the device's lengths (a bound)."""
+    carries an item map (host lengths) or the items are located from the device's lengths (a bound). The rows are
+    longer by 2048 keys, a whole number of tiles, so with a window each row spans as many tiles as the plan's rows
+    (a window's tile count depends on where it starts inside a tile; the plan is then valid for the device's lengths,
+    as check_plan_lengths confirms), while its splits start elsewhere: the launch places them by the device's
+    lengths."""
     from sglang_neuron_amd import ops
 
-    case = workloads.gqa_case(2, overrides={"B": 4, "lens": (300, 900)})
+    case = workloads.gqa_case(2, overrides={"B": 4, "lens": (300, 900), "window": window})
     want, kc_o, vc_o, ks_o, vs_o = gqa_oracle(case)
-    announce(f"gqa plan for longer rows mapped={mapped} lens={case.seq_lens.tolist()}")
+    announce(f"gqa plan for longer rows mapped={mapped} window={window} lens={case.seq_lens.tolist()}")
     kc, vc, ks, vs = gqa_gpu_pool(case)
-    longer = (case.seq_lens + 2000).tolist()
+    longer = (case.seq_lens + 2048).tolist()
     if mapped:
-        plan = ops.plan_decode(0, case.B, host_seq_lens=longer, ctas_per_item=case.G, num_cus=256)
+        plan = ops.plan_decode(0, case.B, host_seq_lens=longer, window=window, ctas_per_item=case.G, num_cus=256)
         assert plan.work_n > 0
+        ops.check_plan_lengths(plan, 0, case.seq_lens, window)
     else:
-        plan = ops.plan_decode(0, case.B, max_seq_len=max(longer), ctas_per_item=case.G, num_cus=256)
+        plan = ops.plan_decode(0, case.B, max_seq_len=max(longer), window=window, ctas_per_item=case.G, num_cus=256)
         assert plan.work_n == 0
-    assert plan.max_splits > 1
+    assert window or plan.max_splits > 1
     out = ops.paged_decode_gqa(case.q.cuda(), kc, vc, case.block_table.cuda(), case.seq_lens.cuda(), case.k_new.cuda(),
-                               case.v_new.cuda(), sm_scale=case.sm_scale, k_scale=ks, v_scale=vs,
+                               case.v_new.cuda(), sm_scale=case.sm_scale, k_scale=ks, v_scale=vs, window=window,
                                new_slots=case.new_slots.cuda(), plan=plan)
     torch.cuda.synchronize()
     assert_close_attn(out, want, "plan for longer rows")

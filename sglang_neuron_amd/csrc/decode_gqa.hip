@@ -703,9 +703,17 @@ static void launch_gqa(const GqaArgs& a, bool any_lone, hipStream_t s) {
   if (a.n_work > 0) {
     const dim3 grid(a.n_work, a.G);
     // two register tiles per wave whatever the plan's shape (rings of 3 and 4 measured 1% and 2% slower on the cfg2
-    // and cfg4 batches: fewer loads outstanding per wave stream faster)
-    if (a.max_splits <= 1) hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, true, 2>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, false, 2>), grid, dim3(256), 0, s, a);
+    // and cfg4 batches: fewer loads outstanding per wave stream faster). Splits of 5 to 64 tiles run on 8 waves, so
+    // a wave walks half as many tiles one after the other (cfg4-swa's 5-tile rows 7.98 -> 6.45 us, cfg4's 48-tile
+    // splits 24.9 -> 24.3, cfg1's 8-tile splits 12.3 -> 12.1); cfg2's whole 128-tile rows stay on 4 (91 against 94).
+    const bool eight = a.split_tiles > 4 && a.split_tiles <= 64;
+    if (a.max_splits <= 1) {
+      if (eight) hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 8, true, 2>), grid, dim3(512), 0, s, a);
+      else hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, true, 2>), grid, dim3(256), 0, s, a);
+    } else {
+      if (eight) hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 8, false, 2>), grid, dim3(512), 0, s, a);
+      else hipLaunchKernelGGL((gqa_decode_kernel<D, FP8, 4, false, 2>), grid, dim3(256), 0, s, a);
+    }
   }
   if (a.max_splits > 1) hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.B, a.H), dim3(64), 0, s, a);
   if (any_lone) hipLaunchKernelGGL((gqa_lone_token_kernel<D, FP8>), dim3(a.B, a.G), dim3(128), 0, s, a);

@@ -26,7 +26,14 @@ def _ptr(t: Optional[Tensor]) -> Optional[int]:
 
 
 def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The current HIP stream of `device` (its raw handle: torch's own accessor, a few hundred ns, where building the
+    torch.cuda.Stream object costs microseconds a call)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return _raw_stream(idx)
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None) or \
+    (lambda idx: torch.cuda.current_stream(idx).cuda_stream)
 
 
 def _num_cus(device: torch.device) -> int:
@@ -36,28 +43,41 @@ def _num_cus(device: torch.device) -> int:
     return _cu_count[idx]
 
 
-def _need(cond: bool, msg: str) -> None:
+def _need(cond: bool, msg) -> None:
+    """Raise ValueError(msg) unless cond; msg is a string or, where building it costs (a formatted message on a hot
+    path), a callable that returns it."""
     if not cond:
-        raise ValueError(msg)
+        raise ValueError(msg() if callable(msg) else msg)
 
 
 def _on_gpu(*ts: Optional[Tensor]) -> torch.device:
-    dev = None
+    """The device of the given tensors (None entries skipped): every one a GPU tensor on the same GPU, else
+    ValueError (compared by device index, which get_device gives without building a torch.device per tensor)."""
+    first = None
+    idx = -1
     for t in ts:
         if t is None:
             continue
-        _need(t.is_cuda, "the HIP path takes device tensors (got a CPU tensor); there is no CPU fallback")
-        if dev is None:
-            dev = t.device
-        _need(t.device == dev, f"tensors on {t.device} and {dev}")
-    assert dev is not None
-    return dev
+        i = t.get_device()
+        if first is None:
+            first, idx = t, i
+        if i < 0 or i != idx:
+            _need(t.is_cuda, "the HIP path takes device tensors (got a CPU tensor); there is no CPU fallback")
+            _need(False, lambda: f"tensors on {t.device} and {first.device}")
+    assert first is not None
+    _need(idx >= 0, "the HIP path takes device tensors (got a CPU tensor); there is no CPU fallback")
+    return first.device
 
 
 def _contig(t: Tensor, name: str, dtype: Optional[torch.dtype] = None) -> Tensor:
     if dtype is not None:
-        _need(t.dtype == dtype, f"{name} must be {dtype}, got {t.dtype}")
+        _need(t.dtype == dtype, lambda: f"{name} must be {dtype}, got {t.dtype}")
     return t if t.is_contiguous() else t.contiguous()
+
+
+def _as(t: Tensor, dtype: torch.dtype) -> Tensor:
+    """t converted to dtype, t itself when it already is (skipping Tensor.to's argument parsing on the hot path)."""
+    return t if t.dtype == dtype else t.to(dtype)
 
 
 def cache_dtype_code(dtype: torch.dtype, scales_multiply: bool = False) -> int:
@@ -101,15 +121,15 @@ def kv_store_mha(k: Tensor, v: Tensor, slots: Tensor, k_cache: Tensor, v_cache: 
     _need(v_cache.shape == k_cache.shape and v_cache.dtype == k_cache.dtype, "K and V caches differ")
     k = _contig(k.reshape(-1, G, d), "k", torch.bfloat16)
     v = _contig(v.reshape(-1, G, d), "v", torch.bfloat16)
-    _need(k.shape == v.shape, f"k {tuple(k.shape)} and v {tuple(v.shape)} differ")
-    slots = _contig(slots.reshape(-1).to(torch.int64), "slots")
-    _need(slots.numel() == k.shape[0], f"{slots.numel()} slots for {k.shape[0]} tokens")
+    _need(k.shape == v.shape, lambda: f"k {tuple(k.shape)} and v {tuple(v.shape)} differ")
+    slots = _contig(_as(slots.reshape(-1), torch.int64), "slots")
+    _need(slots.numel() == k.shape[0], lambda: f"{slots.numel()} slots for {k.shape[0]} tokens")
     code = cache_dtype_code(k_cache.dtype, scales_multiply)
     if code != _lib.DTYPE_BF16:
         _need(k_scale is not None and v_scale is not None, "an FP8 cache needs k_scale and v_scale")
-        k_scale = _contig(k_scale.reshape(-1).float(), "k_scale")
-        v_scale = _contig(v_scale.reshape(-1).float(), "v_scale")
-        _need(k_scale.numel() == G and v_scale.numel() == G, f"scales must have {G} entries (one per KV head)")
+        k_scale = _contig(_as(k_scale.reshape(-1), torch.float32), "k_scale")
+        v_scale = _contig(_as(v_scale.reshape(-1), torch.float32), "v_scale")
+        _need(k_scale.numel() == G and v_scale.numel() == G, lambda: f"scales must have {G} entries (one per KV head)")
     _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
     rc = _lib.load().sna_kv_store_mha(_ptr(k), _ptr(v), _ptr(slots), k.shape[0], _ptr(k_scale), _ptr(v_scale),
                                       _ptr(k_cache), _ptr(v_cache), nb, G, P, d, code, _stream(dev))
@@ -129,24 +149,25 @@ def qkv_norm_rope_store(qkv: Tensor, *, cos: Tensor, sin: Tensor, num_q_heads: i
     and FP8 write (ops/attention/qkv.py:57-85)."""
     dev = _on_gpu(qkv, cos, sin, k_cache, v_cache, slot_mapping, q_norm, k_norm, k_scale, v_scale, q_out)
     nb, G, P, d = k_cache.shape
-    _need(G == num_kv_heads and d == d_head, f"caches {tuple(k_cache.shape)} for {num_kv_heads} heads of {d_head}")
+    _need(G == num_kv_heads and d == d_head,
+          lambda: f"caches {tuple(k_cache.shape)} for {num_kv_heads} heads of {d_head}")
     _need(v_cache.shape == k_cache.shape and v_cache.dtype == k_cache.dtype, "K and V caches differ")
     _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
     width = (num_q_heads + 2 * num_kv_heads) * d_head
     qkv = qkv.reshape(-1, qkv.shape[-1])
     _need(qkv.dtype == torch.bfloat16 and qkv.shape[-1] == width and qkv.stride(-1) == 1,
-          f"qkv must be bf16 [T, {width}] with unit column stride")
+          lambda: f"qkv must be bf16 [T, {width}] with unit column stride")
     T = qkv.shape[0]
     cos = _contig(cos.reshape(-1, d_head), "cos", torch.bfloat16)
     sin = _contig(sin.reshape(-1, d_head), "sin", torch.bfloat16)
-    _need(cos.shape[0] == T and sin.shape[0] == T, f"cos/sin need {T} rows")
-    slots = _contig(slot_mapping.reshape(-1).to(torch.int64), "slot_mapping")
-    _need(slots.numel() == T, f"{slots.numel()} slots for {T} tokens")
+    _need(cos.shape[0] == T and sin.shape[0] == T, lambda: f"cos/sin need {T} rows")
+    slots = _contig(_as(slot_mapping.reshape(-1), torch.int64), "slot_mapping")
+    _need(slots.numel() == T, lambda: f"{slots.numel()} slots for {T} tokens")
     _need((q_norm is None) == (k_norm is None), "give both QK-norm gammas or neither")
     if q_norm is not None:
         q_norm = _contig(q_norm.reshape(-1), "q_norm", torch.bfloat16)
         k_norm = _contig(k_norm.reshape(-1), "k_norm", torch.bfloat16)
-        _need(q_norm.numel() == d_head and k_norm.numel() == d_head, f"QK-norm gammas need {d_head} entries")
+        _need(q_norm.numel() == d_head and k_norm.numel() == d_head, lambda: f"QK-norm gammas need {d_head} entries")
     code = cache_dtype_code(k_cache.dtype)
     if code == _lib.DTYPE_FP8_E4M3FN:
         _need(k_scale is not None and v_scale is not None, "an FP8 cache needs k_scale and v_scale")
@@ -154,7 +175,7 @@ def qkv_norm_rope_store(qkv: Tensor, *, cos: Tensor, sin: Tensor, num_q_heads: i
                           "k_scale")
         v_scale = _contig(v_scale.reshape(-1).float().expand(G) if v_scale.numel() == 1 else v_scale.reshape(-1).float(),
                           "v_scale")
-        _need(k_scale.numel() == G and v_scale.numel() == G, f"scales need 1 or {G} entries")
+        _need(k_scale.numel() == G and v_scale.numel() == G, lambda: f"scales need 1 or {G} entries")
     if q_out is None:
         q_out = torch.empty(T, num_q_heads, d_head, dtype=torch.bfloat16, device=dev)
     _need(q_out.shape == (T, num_q_heads, d_head) and q_out.dtype == torch.bfloat16 and q_out.is_contiguous(),
@@ -170,7 +191,7 @@ def qkv_norm_rope_store(qkv: Tensor, *, cos: Tensor, sin: Tensor, num_q_heads: i
 def kv_absmax_scale(x: Tensor) -> Tensor:
     """Per-head dequantization scales [H] fp32 of x [T, H, d] bf16: absmax / 448, or 1 for an all-zero head."""
     dev = _on_gpu(x)
-    _need(x.dim() == 3, f"x must be [T, H, d], got {tuple(x.shape)}")
+    _need(x.dim() == 3, lambda: f"x must be [T, H, d], got {tuple(x.shape)}")
     x = _contig(x, "x", torch.bfloat16)
     T, H, d = x.shape
     lib = _lib.load()
@@ -189,12 +210,12 @@ def kv_store_mla(rows: Tensor, slots: Tensor, cache: Tensor, row_scale: Optional
     flat = cache.reshape(cache.shape[0], -1)
     n_slots, dim = flat.shape
     rows = _contig(rows.reshape(-1, dim), "rows", torch.bfloat16)
-    slots = _contig(slots.reshape(-1).to(torch.int64), "slots")
-    _need(slots.numel() == rows.shape[0], f"{slots.numel()} slots for {rows.shape[0]} rows")
+    slots = _contig(_as(slots.reshape(-1), torch.int64), "slots")
+    _need(slots.numel() == rows.shape[0], lambda: f"{slots.numel()} slots for {rows.shape[0]} rows")
     code = cache_dtype_code(cache.dtype)
     if code == _lib.DTYPE_FP8_E4M3FN:
         _need(row_scale is not None and row_scale.numel() == n_slots and row_scale.dtype == torch.float32
-              and row_scale.is_contiguous(), f"an FP8 MLA cache needs a contiguous fp32 row_scale of {n_slots}")
+              and row_scale.is_contiguous(), lambda: f"an FP8 MLA cache needs a contiguous fp32 row_scale of {n_slots}")
     _need(cache.is_contiguous(), "cache must be contiguous")
     rc = _lib.load().sna_kv_store_mla(_ptr(rows), _ptr(slots), rows.shape[0], dim, _ptr(cache), _ptr(row_scale),
                                       n_slots, code, _stream(dev))
@@ -209,8 +230,8 @@ def kv_store_dsa(rows: Tensor, slots: Tensor, cache: Tensor, kv_scale: float) ->
     _need(cache.dtype == torch.uint8 and cache.shape[-1] == 640 and cache.is_contiguous(),
           "the DSA cache is contiguous uint8 [..., 640]")
     rows = _contig(rows.reshape(-1, 576), "rows", torch.bfloat16)
-    slots = _contig(slots.reshape(-1).to(torch.int64), "slots")
-    _need(slots.numel() == rows.shape[0], f"{slots.numel()} slots for {rows.shape[0]} rows")
+    slots = _contig(_as(slots.reshape(-1), torch.int64), "slots")
+    _need(slots.numel() == rows.shape[0], lambda: f"{slots.numel()} slots for {rows.shape[0]} rows")
     n_rows = cache.numel() // 640
     rc = _lib.load().sna_kv_store_dsa(_ptr(rows), _ptr(slots), rows.shape[0], float(kv_scale), _ptr(cache), n_rows,
                                       _stream(dev))
@@ -231,7 +252,7 @@ def plan_decode(kind: int, B: int, *, host_seq_lens: Union[Tensor, Sequence[int]
     arr = None
     if host_seq_lens is not None:
         t = torch.as_tensor(host_seq_lens, dtype=torch.int32).reshape(-1).cpu().contiguous()
-        _need(t.numel() == B, f"{t.numel()} host seq_lens for {B} rows")
+        _need(t.numel() == B, lambda: f"{t.numel()} host seq_lens for {B} rows")
         arr = t
     rc = _lib.load().sna_plan_decode(kind, None if arr is None else arr.data_ptr(), B, max_seq_len, window,
                                      n_keys_per_row, ctas_per_item, num_cus, plan)
@@ -274,7 +295,7 @@ def check_plan_lengths(plan: _lib.SplitPlan, kind: int, host_seq_lens, window: i
     split some row needs (those keys would be dropped), an MLA plan made for other key counts (its launch is cut by
     the plan's). Raises ValueError naming the first row."""
     lens = [int(x) for x in torch.as_tensor(host_seq_lens).reshape(-1).tolist()]
-    _need(len(lens) == plan.batch, f"a plan for {plan.batch} rows, {len(lens)} lengths")
+    _need(len(lens) == plan.batch, lambda: f"a plan for {plan.batch} rows, {len(lens)} lengths")
     if kind == _lib.KIND_GQA:
         if plan.device_split:
             # the launch sizes its splits from the device's lengths (gqa_device_item): a row must fit the plan's
@@ -283,7 +304,7 @@ def check_plan_lengths(plan: _lib.SplitPlan, kind: int, host_seq_lens, window: i
             st = _gqa_device_split_tiles(tiles, plan.n_work)
             for b, t in enumerate(tiles):
                 _need(max(1, -(-t // st)) <= max(plan.max_splits, 1),
-                      f"row {b}: seq_len {lens[b]} is past the plan's bound (at most {plan.max_splits} splits)")
+                      lambda: f"row {b}: seq_len {lens[b]} is past the plan's bound (at most {plan.max_splits} splits)")
             return
         need = [_row_splits(L, window, plan.split_tiles) for L in lens]
         if plan.work_n > 0:
@@ -293,15 +314,19 @@ def check_plan_lengths(plan: _lib.SplitPlan, kind: int, host_seq_lens, window: i
         else:
             have = [max(plan.max_splits, 1)] * len(lens)
         for b, (n, h) in enumerate(zip(need, have)):
-            _need(n <= h, f"row {b}: seq_len {lens[b]} needs {n} splits, the plan runs {h} (made for other lengths)")
-        _need(sum(need) <= plan.n_work, f"the lengths need {sum(need)} split items, the plan runs {plan.n_work}")
+            _need(n <= h,
+                  lambda: f"row {b}: seq_len {lens[b]} needs {n} splits, the plan runs {h} (made for other lengths)")
+        _need(sum(need) <= plan.n_work,
+              lambda: f"the lengths need {sum(need)} split items, the plan runs {plan.n_work}")
     elif kind == _lib.KIND_MLA:
         for b, L in enumerate(lens):
             if plan.device_split:  # a bound: the launch cuts its split from the device's lengths
-                _need(L - 1 <= plan.row_keys[b], f"row {b}: seq_len {L} is past the plan's bound {plan.row_keys[b] + 1}")
+                _need(L - 1 <= plan.row_keys[b],
+                      lambda: f"row {b}: seq_len {L} is past the plan's bound {plan.row_keys[b] + 1}")
                 continue
             _need(plan.row_keys[b] == max(L - 1, 0),
-                  f"row {b}: seq_len {L}, the plan was made for {plan.row_keys[b] + 1} (its launch is cut by them)")
+                  lambda: f"row {b}: seq_len {L}, the plan was made for {plan.row_keys[b] + 1} "
+                          "(its launch is cut by them)")
 
 
 def check_decode_operands(seq_lens: Tensor, block_table: Tensor, new_slots: Optional[Tensor], page_size: int,
@@ -318,12 +343,12 @@ def check_decode_operands(seq_lens: Tensor, block_table: Tensor, new_slots: Opti
         _need(t is None or not t.is_cuda, "check_decode_operands takes host copies of the operands")
     lens = seq_lens.reshape(-1).to(torch.int64).contiguous()
     B = lens.numel()
-    _need(block_table.dim() == 2 and block_table.shape[0] == B, f"block_table must be [{B}, width]")
+    _need(block_table.dim() == 2 and block_table.shape[0] == B, lambda: f"block_table must be [{B}, width]")
     table = block_table.to(torch.int32).contiguous()
     slots = None if new_slots is None else new_slots.reshape(-1).to(torch.int64).contiguous()
-    _need(slots is None or slots.numel() == B, f"new_slots must have {B} entries")
+    _need(slots is None or slots.numel() == B, lambda: f"new_slots must have {B} entries")
     act = None if active is None else active.reshape(-1).to(torch.int32).contiguous()
-    _need(act is None or act.numel() == B, f"active must have {B} entries")
+    _need(act is None or act.numel() == B, lambda: f"active must have {B} entries")
     rc = _lib.load().sna_check_decode_operands(lens.data_ptr(), table.data_ptr(), table.stride(0), table.shape[1],
                                                None if slots is None else slots.data_ptr(),
                                                None if act is None else act.data_ptr(), B, int(page_size),
@@ -340,7 +365,7 @@ def _stream_workspace_arg(ws: Optional[Tensor], plan: _lib.SplitPlan, heads: int
         return stream_workspace(plan, heads, device)
     _need(ws.dtype == torch.uint8 and ws.is_contiguous() and ws.device == device, "workspace must be contiguous uint8 "
           "on the decode's device")
-    _need(ws.numel() >= workspace_bytes(plan, heads, 512), f"workspace of {ws.numel()} bytes, the plan needs "
+    _need(ws.numel() >= workspace_bytes(plan, heads, 512), lambda: f"workspace of {ws.numel()} bytes, the plan needs "
           f"{workspace_bytes(plan, heads, 512)}")
     return ws
 
@@ -355,11 +380,11 @@ def stream_row_chunks(kind: int, B: int, heads: int, n_keys_per_row: int = 0, sp
     rows = min(_lib.MAX_PLAN_ROWS, _lib.STREAM_MAX_COUNTERS // groups)
     if kind == _lib.KIND_DSA:
         pieces = max(1, -(-int(n_keys_per_row) // _lib.SPARSE_MAX_RANGE_KEYS))
-        _need(pieces <= _lib.MAX_CTAS, f"a DSA row of {n_keys_per_row} keys needs more than {_lib.MAX_CTAS} "
+        _need(pieces <= _lib.MAX_CTAS, lambda: f"a DSA row of {n_keys_per_row} keys needs more than {_lib.MAX_CTAS} "
               "workgroups")
         rows = min(rows, _lib.MAX_CTAS // pieces)
     rows -= rows % spec
-    _need(rows >= spec, f"a sequence of {spec} query tokens does not fit one launch")
+    _need(rows >= spec, lambda: f"a sequence of {spec} query tokens does not fit one launch")
     return [(r0, min(B, r0 + rows)) for r0 in range(0, B, rows)] or [(0, 0)]
 
 
@@ -370,7 +395,8 @@ def _plans_of(plan, kind: int, B: int, heads: int, n_keys: int = 0, spec: int = 
         return [(0, B)], [plan]
     chunks = stream_row_chunks(kind, B, heads, n_keys, spec)
     plans = list(plan)
-    _need(len(plans) == len(chunks), f"{len(plans)} plans for the {len(chunks)} launches a batch of {B} rows takes")
+    _need(len(plans) == len(chunks),
+          lambda: f"{len(plans)} plans for the {len(chunks)} launches a batch of {B} rows takes")
     return chunks, plans
 
 
@@ -447,33 +473,33 @@ def prepare_paged_decode_gqa(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_
     ``scales_multiply`` the FP8 scales are the GPT-OSS quantization multipliers m (a cached byte is worth byte / m,
     and the step's token is stored as e4m3fn(bf16(x * m)), attention_decode.py:259-260)."""
     dev = _on_gpu(q, k_cache, v_cache, block_table, seq_lens, k_new, v_new, k_scale, v_scale, sinks, new_slots, out)
-    _need(q.dim() == 3, f"q must be [B, H, d], got {tuple(q.shape)}")
+    _need(q.dim() == 3, lambda: f"q must be [B, H, d], got {tuple(q.shape)}")
     B, H, d = q.shape
     nb, G, P, dk = k_cache.shape
     _need(dk == d and v_cache.shape == k_cache.shape and v_cache.dtype == k_cache.dtype,
-          f"caches {tuple(k_cache.shape)} / {tuple(v_cache.shape)} do not match q's head_dim {d}")
+          lambda: f"caches {tuple(k_cache.shape)} / {tuple(v_cache.shape)} do not match q's head_dim {d}")
     _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
-    _need(H % G == 0, f"{H} query heads over {G} KV heads")
+    _need(H % G == 0, lambda: f"{H} query heads over {G} KV heads")
     code = cache_dtype_code(k_cache.dtype, scales_multiply)
     q = _contig(q, "q", torch.bfloat16)
     k_new = _contig(k_new.reshape(B, G, d), "k_new", torch.bfloat16)
     v_new = _contig(v_new.reshape(B, G, d), "v_new", torch.bfloat16)
-    _need(block_table.dim() == 2 and block_table.shape[0] == B, f"block_table must be [{B}, width]")
+    _need(block_table.dim() == 2 and block_table.shape[0] == B, lambda: f"block_table must be [{B}, width]")
     table = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
     _need(table.stride(1) == 1, "block_table rows must be contiguous")
-    lens = _contig(seq_lens.reshape(-1).to(torch.int32), "seq_lens")
-    _need(lens.numel() == B, f"{lens.numel()} seq_lens for {B} rows")
+    lens = _contig(_as(seq_lens.reshape(-1), torch.int32), "seq_lens")
+    _need(lens.numel() == B, lambda: f"{lens.numel()} seq_lens for {B} rows")
     if code != _lib.DTYPE_BF16:
         _need(k_scale is not None and v_scale is not None, "an FP8 cache needs k_scale and v_scale")
-        k_scale = _contig(k_scale.reshape(-1).float(), "k_scale")
-        v_scale = _contig(v_scale.reshape(-1).float(), "v_scale")
+        k_scale = _contig(_as(k_scale.reshape(-1), torch.float32), "k_scale")
+        v_scale = _contig(_as(v_scale.reshape(-1), torch.float32), "v_scale")
         _need(k_scale.numel() == G and v_scale.numel() == G, "one k/v scale per KV head")
     if sinks is not None:
-        sinks = _contig(sinks.reshape(-1).float(), "sinks")
-        _need(sinks.numel() == H, f"{sinks.numel()} sinks for {H} heads")
+        sinks = _contig(_as(sinks.reshape(-1), torch.float32), "sinks")
+        _need(sinks.numel() == H, lambda: f"{sinks.numel()} sinks for {H} heads")
     if new_slots is not None:
-        new_slots = _contig(new_slots.reshape(-1).to(torch.int64), "new_slots")
-        _need(new_slots.numel() == B, f"{new_slots.numel()} new slots for {B} rows")
+        new_slots = _contig(_as(new_slots.reshape(-1), torch.int64), "new_slots")
+        _need(new_slots.numel() == B, lambda: f"{new_slots.numel()} new slots for {B} rows")
     if out is None:
         out = torch.empty(B, H, d, dtype=torch.bfloat16, device=dev)
     _need(out.shape == (B, H, d) and out.dtype == torch.bfloat16 and out.is_contiguous(), "bad out tensor")
@@ -523,15 +549,16 @@ def paged_decode_gqa_multi(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_ta
     over the active slots. A window must hold the S tokens (S <= window), as the reference's mask does not window
     them. Stands in for _torch_attention_decode with X [B, S, Hd] (ops/attention/attention_decode.py:226-300)."""
     dev = _on_gpu(q, k_cache, v_cache, block_table, seq_lens, k_new, v_new, new_slots, k_scale, v_scale, sinks)
-    _need(q.dim() == 4, f"q must be [B, S, H, d], got {tuple(q.shape)}")
+    _need(q.dim() == 4, lambda: f"q must be [B, S, H, d], got {tuple(q.shape)}")
     B, S, H, d = q.shape
     nb, G, P, _ = k_cache.shape
-    _need(k_new.shape == (B, S, G, d) and v_new.shape == (B, S, G, d), f"k_new / v_new must be [{B}, {S}, {G}, {d}]")
-    _need(new_slots.numel() == B * S, f"new_slots must be [{B}, {S}]")
-    _need(window <= 0 or S <= window, f"{S} active tokens do not fit a window of {window}")
+    _need(k_new.shape == (B, S, G, d) and v_new.shape == (B, S, G, d),
+          lambda: f"k_new / v_new must be [{B}, {S}, {G}, {d}]")
+    _need(new_slots.numel() == B * S, lambda: f"new_slots must be [{B}, {S}]")
+    _need(window <= 0 or S <= window, lambda: f"{S} active tokens do not fit a window of {window}")
     hl = _host_lens(seq_lens, host_seq_lens)
     if hl is not None:
-        _need(int(hl.min()) >= S if B else True, f"a row holds its {S} active tokens: seq_lens >= {S}")
+        _need(int(hl.min()) >= S if B else True, lambda: f"a row holds its {S} active tokens: seq_lens >= {S}")
     kv_store_mha(k_new.reshape(B * S, G, d), v_new.reshape(B * S, G, d), new_slots.reshape(-1), k_cache, v_cache,
                  k_scale, v_scale, scales_multiply=scales_multiply)
     j = torch.arange(S, device=dev, dtype=torch.int32)
@@ -561,12 +588,12 @@ def prepare_mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: 
     B, H, lat = ql_nope.shape
     _need(lat == 512 and q_pe.shape == (B, H, 64), "ql_nope [B, H, 512] and q_pe [B, H, 64]")
     # rows as the pool holds them: [slots, 576], [slots, 1, 576] or the block view [blocks, page, 576]
-    _need(cache.shape[-1] == 576 and cache.is_contiguous(), f"MLA rows must be contiguous [.., 576], got "
+    _need(cache.shape[-1] == 576 and cache.is_contiguous(), lambda: f"MLA rows must be contiguous [.., 576], got "
           f"{tuple(cache.shape)}")
     code = cache_dtype_code(cache.dtype)
     n_slots = cache.numel() // 576
     P = int(page_size)
-    _need(n_slots % P == 0, f"{n_slots} rows are not whole pages of {P}")
+    _need(n_slots % P == 0, lambda: f"{n_slots} rows are not whole pages of {P}")
     nb = n_slots // P
     if code == _lib.DTYPE_FP8_E4M3FN:
         _need(row_scale is not None and row_scale.numel() == n_slots and row_scale.dtype == torch.float32 and
@@ -577,12 +604,13 @@ def prepare_mla_decode(ql_nope: Tensor, q_pe: Tensor, cache: Tensor, row_scale: 
     q_pe = _contig(q_pe, "q_pe", torch.bfloat16)
     compact_new = _contig(compact_new.reshape(B, 576), "compact_new", torch.bfloat16)
     table = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
-    _need(table.dim() == 2 and table.shape[0] == B and table.stride(1) == 1, f"block_table must be [{B}, width]")
-    lens = _contig(seq_lens.reshape(-1).to(torch.int32), "seq_lens")
-    _need(lens.numel() == B, f"{lens.numel()} seq_lens for {B} rows")
+    _need(table.dim() == 2 and table.shape[0] == B and table.stride(1) == 1,
+          lambda: f"block_table must be [{B}, width]")
+    lens = _contig(_as(seq_lens.reshape(-1), torch.int32), "seq_lens")
+    _need(lens.numel() == B, lambda: f"{lens.numel()} seq_lens for {B} rows")
     if new_slots is not None:
-        new_slots = _contig(new_slots.reshape(-1).to(torch.int64), "new_slots")
-        _need(new_slots.numel() == B, f"{new_slots.numel()} new slots for {B} rows")
+        new_slots = _contig(_as(new_slots.reshape(-1), torch.int64), "new_slots")
+        _need(new_slots.numel() == B, lambda: f"{new_slots.numel()} new slots for {B} rows")
     if out is None:
         out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
     _need(out.shape == (B, H, 512) and out.dtype == torch.bfloat16 and out.is_contiguous(), "bad out tensor")
@@ -640,20 +668,20 @@ def prepare_mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, k
     _need(cache.dtype == torch.uint8 and cache.shape[-1] == 640 and cache.is_contiguous(), "cache [..., 640] uint8")
     n_rows = cache.numel() // 640
     P = int(page_size)
-    _need(n_rows % P == 0, f"{n_rows} rows are not whole pages of {P}")
+    _need(n_rows % P == 0, lambda: f"{n_rows} rows are not whole pages of {P}")
     q_absorbed = _contig(q_absorbed, "q_absorbed", torch.bfloat16)
     q_pe = _contig(q_pe, "q_pe", torch.bfloat16)
     own_rows = _contig(own_rows.reshape(B, 576), "own_rows", torch.bfloat16)
-    idx = _contig(indices.reshape(B, -1).to(torch.int32), "indices")
+    idx = _contig(_as(indices.reshape(B, -1), torch.int32), "indices")
     K = idx.shape[1]
     spec = int(spec)
-    _need(spec >= 1 and B % spec == 0, f"{B} query tokens are not whole sequences of {spec}")
+    _need(spec >= 1 and B % spec == 0, lambda: f"{B} query tokens are not whole sequences of {spec}")
     S = B // spec
     table = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
     _need(table.dim() == 2 and table.shape[0] == S and table.stride(1) == 1,
-          f"block_table must be [{S}, width] (one row per sequence)")
-    pos = _contig(positions.reshape(-1).to(torch.int32), "positions")
-    _need(pos.numel() == B, f"{pos.numel()} positions for {B} rows")
+          lambda: f"block_table must be [{S}, width] (one row per sequence)")
+    pos = _contig(_as(positions.reshape(-1), torch.int32), "positions")
+    _need(pos.numel() == B, lambda: f"{pos.numel()} positions for {B} rows")
     nkeys = K + spec - 1  # a row's keys: its index list, then its spec - 1 siblings' own rows
     if plan is not None:
         chunks, plans = _plans_of(plan, _lib.KIND_DSA, B, H, nkeys, spec)
@@ -668,8 +696,8 @@ def prepare_mla_decode_sparse(q_absorbed: Tensor, q_pe: Tensor, cache: Tensor, k
     calls = []
     fused_slots = new_slots
     if new_slots is not None:
-        new_slots = _contig(new_slots.reshape(-1).to(torch.int64), "new_slots")
-        _need(new_slots.numel() == B, f"{new_slots.numel()} new slots for {B} rows")
+        new_slots = _contig(_as(new_slots.reshape(-1), torch.int64), "new_slots")
+        _need(new_slots.numel() == B, lambda: f"{new_slots.numel()} new slots for {B} rows")
         fused_slots = new_slots
         if len(chunks) > 1:
             # The reference stores every own row before any gather (mla_decode_attention_torch.py steps 0-1): one
@@ -741,9 +769,9 @@ def prefill_attention(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: 
     T, H, d = q.shape
     nb, G, P, dk = k_cache.shape
     _need(dk == d and tuple(v_cache.shape) == tuple(k_cache.shape), "q, k_cache and v_cache disagree on shape")
-    _need(H % G == 0, f"{H} query heads over {G} KV heads")
+    _need(H % G == 0, lambda: f"{H} query heads over {G} KV heads")
     R = prior_lens.shape[0]
-    _need(q_start.shape == (R + 1,), f"q_start must be [{R + 1}]")
+    _need(q_start.shape == (R + 1,), lambda: f"q_start must be [{R + 1}]")
     _need(block_table.dim() == 2 and block_table.shape[0] >= R and block_table.stride(1) == 1,
           "block_table must be [R, width] with unit column stride")
     q = _contig(q, "q", torch.bfloat16)
@@ -752,21 +780,23 @@ def prefill_attention(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_table: 
     table = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32).contiguous()
     if host_q_start is not None:
         hq = [int(x) for x in torch.as_tensor(host_q_start).reshape(-1).tolist()]
-        _need(len(hq) == R + 1 and hq[0] == 0 and hq[-1] == T, f"q_start must run from 0 to T = {T} over {R + 1} "
+        _need(len(hq) == R + 1 and hq[0] == 0 and hq[-1] == T,
+              lambda: f"q_start must run from 0 to T = {T} over {R + 1} "
               f"entries, got {hq[:4]}{'...' if len(hq) > 4 else ''} ending {hq[-1] if hq else None}")
         lens = [hq[r + 1] - hq[r] for r in range(R)]
         _need(min(lens, default=0) >= 0, "q_start must not decrease")
-        _need(max(lens, default=0) <= int(max_q_len), f"a chunk of {max(lens)} queries exceeds max_q_len {max_q_len}")
+        _need(max(lens, default=0) <= int(max_q_len),
+              lambda: f"a chunk of {max(lens)} queries exceeds max_q_len {max_q_len}")
     code = cache_dtype_code(k_cache.dtype, scales_multiply)
     ks = vs = None
     if code != _lib.DTYPE_BF16:
         _need(k_scale is not None and v_scale is not None, "an FP8 pool needs k_scale and v_scale")
-        ks = _contig(k_scale.reshape(-1).float(), "k_scale")
-        vs = _contig(v_scale.reshape(-1).float(), "v_scale")
-        _need(ks.numel() == G and vs.numel() == G, f"k_scale and v_scale must have {G} entries")
-    sk = None if sinks is None else _contig(sinks.reshape(-1).float(), "sinks")
+        ks = _contig(_as(k_scale.reshape(-1), torch.float32), "k_scale")
+        vs = _contig(_as(v_scale.reshape(-1), torch.float32), "v_scale")
+        _need(ks.numel() == G and vs.numel() == G, lambda: f"k_scale and v_scale must have {G} entries")
+    sk = None if sinks is None else _contig(_as(sinks.reshape(-1), torch.float32), "sinks")
     if sk is not None:
-        _need(sk.numel() == H, f"sinks must have {H} entries")
+        _need(sk.numel() == H, lambda: f"sinks must have {H} entries")
     if out is None:
         out = torch.empty(T, H, d, dtype=torch.bfloat16, device=dev)
     _need(out.shape == (T, H, d) and out.dtype == torch.bfloat16 and out.is_contiguous(), "out must be [T, H, d] bf16")
@@ -791,7 +821,8 @@ def segmented_attention(q: Tensor, *, k_cache: Tensor, v_cache: Tensor, block_ta
     has no role here."""
     del kv_segment_size
     heads, S, d = q.shape
-    _need(block_size == k_cache.shape[2], f"block_size {block_size} differs from the cache's page {k_cache.shape[2]}")
+    _need(block_size == k_cache.shape[2],
+          lambda: f"block_size {block_size} differs from the cache's page {k_cache.shape[2]}")
     dev = q.device
     prior = int(torch.as_tensor(prior_tokens).reshape(-1)[0])
     out = prefill_attention(
@@ -831,7 +862,7 @@ def indexer_scores(q: Tensor, w: Tensor, keys: Tensor, block_table: Tensor, limi
     B, H, d = q.shape
     nb, P, dk = keys.shape
     _need(dk == d, "q and the keys disagree on head_dim")
-    _need(w.shape == (B, H) and limits.shape == (B,), f"w must be [{B}, {H}] and limits [{B}]")
+    _need(w.shape == (B, H) and limits.shape == (B,), lambda: f"w must be [{B}, {H}] and limits [{B}]")
     _need(block_table.dim() == 2 and block_table.shape[0] >= B and block_table.stride(1) == 1,
           "block_table must be [B, W] with unit column stride")
     q = _contig(q, "q", torch.bfloat16)
@@ -842,7 +873,7 @@ def indexer_scores(q: Tensor, w: Tensor, keys: Tensor, block_table: Tensor, limi
     if out is None:
         out = torch.empty(B, width, dtype=torch.bfloat16, device=dev)
     _need(out.shape[0] == B and out.shape[1] >= width and out.dtype == torch.bfloat16 and out.stride(1) == 1,
-          f"out must be [{B}, >= {width}] bf16")
+          lambda: f"out must be [{B}, >= {width}] bf16")
     rc = _lib.load().sna_indexer_scores(_ptr(q), _ptr(w), _ptr(keys), _ptr(table), table.stride(0), table.shape[1],
                                         _ptr(lim), B, H, d, P, nb, int(width), _ptr(out), out.stride(0), _stream(dev))
     _lib.check(rc, "indexer_scores")
@@ -856,7 +887,7 @@ def topk_positions(scores: Tensor, k: int) -> Tensor:
     dev = _on_gpu(scores)
     _need(scores.dim() == 2 and scores.dtype == torch.bfloat16 and scores.stride(1) == 1, "scores must be [B, N] bf16")
     B, N = scores.shape
-    _need(1 <= k <= N, f"k {k} must be in [1, {N}]")
+    _need(1 <= k <= N, lambda: f"k {k} must be in [1, {N}]")
     out = torch.empty(B, k, dtype=torch.int32, device=dev)
     lib = _lib.load()
     ws = torch.empty(max(int(lib.sna_topk_workspace_bytes(B, N)), 4), dtype=torch.uint8, device=dev)
@@ -880,13 +911,13 @@ def block_table(req_to_token: Tensor, req_pool_indices: Tensor, seq_lens: Tensor
     _need(req_to_token.dim() == 2 and req_to_token.dtype == torch.int32 and req_to_token.stride(1) == 1,
           "req_to_token must be [rows, context] int32 with unit column stride")
     B = req_pool_indices.shape[0]
-    _need(seq_lens.shape == (B,), f"seq_lens must be [{B}]")
-    _need(width >= 1 and page_size >= 1, f"width {width} and page_size {page_size} must be positive")
+    _need(seq_lens.shape == (B,), lambda: f"seq_lens must be [{B}]")
+    _need(width >= 1 and page_size >= 1, lambda: f"width {width} and page_size {page_size} must be positive")
     rows = _contig(req_pool_indices, "req_pool_indices", torch.int64)
     lens = _contig(seq_lens, "seq_lens", torch.int64)
     if seq_lens_i32 is not None:
         _need(seq_lens_i32.shape == (B,) and seq_lens_i32.dtype == torch.int32 and seq_lens_i32.is_contiguous(),
-              f"seq_lens_i32 must be a contiguous [{B}] int32 tensor")
+              lambda: f"seq_lens_i32 must be a contiguous [{B}] int32 tensor")
     table = torch.empty(B, width, dtype=torch.int32, device=dev)
     rc = _lib.load().sna_block_table(_ptr(req_to_token), req_to_token.shape[0], req_to_token.shape[1],
                                      req_to_token.stride(0), _ptr(rows), _ptr(lens), B, page_size, width, _ptr(table),
@@ -913,7 +944,7 @@ def window_table(block_table: Tensor, seq_lens: Tensor, page_size: int, n_blocks
     _need(block_table.dim() == 2 and block_table.dtype == torch.int32 and block_table.stride(1) == 1,
           "block_table must be [B, width] int32 with unit column stride")
     B, width = block_table.shape
-    _need(seq_lens.shape == (B,), f"seq_lens must be [{B}]")
+    _need(seq_lens.shape == (B,), lambda: f"seq_lens must be [{B}]")
     _need(n_blocks >= 1, "n_blocks must be >= 1")
     lens = _contig(seq_lens, "seq_lens", torch.int64)
     trimmed = torch.empty(B, n_blocks, dtype=torch.int32, device=dev)
@@ -947,14 +978,14 @@ def default_sm_scale(head_dim: int) -> float:
 def _regions(infos, what: str):
     """Host arrays (ptrs u64, lens i64, item_lens i64) of a pool's get_contiguous_buf_infos() triple."""
     ptrs, lens, items = (list(x) for x in infos)
-    _need(len(ptrs) == len(lens) == len(items), f"{what}: ptrs, lens and item_lens differ in length")
+    _need(len(ptrs) == len(lens) == len(items), lambda: f"{what}: ptrs, lens and item_lens differ in length")
     n = len(ptrs)
     return ((ctypes.c_uint64 * n)(*[int(x) for x in ptrs]), (ctypes.c_int64 * n)(*[int(x) for x in lens]),
             (ctypes.c_int64 * n)(*[int(x) for x in items]), n)
 
 
 def _pages(pages: Tensor, what: str) -> Tensor:
-    _need(pages.dim() == 1, f"{what}: pages must be 1-D")
+    _need(pages.dim() == 1, lambda: f"{what}: pages must be 1-D")
     return pages.to(torch.int32).contiguous()
 
 
@@ -1005,7 +1036,7 @@ def copy_page_items(src_infos, dst_infos, src_pages: Tensor, dst_pages: Tensor) 
     _need(sp.numel() == dp.numel(), "copy_page_items: src_pages and dst_pages differ in length")
     s_ptrs, s_lens, items, n = _regions(src_infos, "copy_page_items")
     d_ptrs, d_lens, _, n_dst = _regions((dst_infos[0], dst_infos[1], src_infos[2]), "copy_page_items")
-    _need(n == n_dst, f"copy_page_items: {n} source regions, {n_dst} destination regions")
+    _need(n == n_dst, lambda: f"copy_page_items: {n} source regions, {n_dst} destination regions")
     rc = _lib.load().sna_page_items_copy(s_ptrs, s_lens, d_ptrs, d_lens, items, n, _ptr(sp), _ptr(dp), sp.numel(),
                                          _stream(dev))
     _lib.check(rc, "page_items_copy")

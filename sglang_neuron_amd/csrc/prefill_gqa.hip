@@ -5,19 +5,21 @@
 //
 // Work: one workgroup of 4 waves per (request, block of query tokens, KV head). Its 128 query rows are (token, head)
 // pairs, token-major (row = t * group + j for the group's query head j); wave w owns rows 32 w .. 32 w + 31 as two
-// 16-row MFMA N tiles. Keys run in tiles of 32 positions (aligned to multiples of 32) from the window's first key
-// to the block's last query. A tile's K and V rows (32 x d bytes each) are DMA'd into a 3-slot LDS ring shared by
-// the 4 waves (each wave issues a share of the tile's DMAs); two tiles are in flight while one computes. The block
-// table entries of the key range are staged in LDS first.
+// 16-row MFMA N tiles. Keys run in tiles of 64 positions (FP8; 32 for bf16 pools) from the window's first key to
+// the block's last query, each tile NSUB sub-tiles of 32 keys. A tile's K and V rows are DMA'd into a 2-slot LDS
+// ring shared by the 4 waves (each wave issues a share of the tile's DMAs); one tile loads while one computes. The
+// block-table entries of the key range are staged in LDS first, and a tile's four 16-key groups' byte offsets are
+// computed by four lanes from one LDS round trip (lane reads hand them to the DMAs).
 //
-// Lane roles (lane = 16 g4 + i), all MFMAs v_mfma_f32_16x16x32_bf16:
-//   QK  S^T[key, row] = K[key, :] . Q[row, :] over d / 32 steps, per 16-key half a of the tile: lane (g4, i) feeds
-//       key 8 (i / 4) + 4 a + i % 4 (its bytes 32 s + 8 g4 .. + 7, converted to bf16) and row i's query elements
-//       32 s + 8 g4 .. + 7 (registers, loaded once). The result hands lane (g4, i) keys 8 g4 + 4 a + r (r < 4) of
-//       row i: over both halves the 8 consecutive keys 8 g4 .. 8 g4 + 7.
-//   PV  O^T[dim, row] += V^T[dim, key] . P^T[key, row] per 16-dim tile c, K = the tile's 32 keys: lane (g4, i)
-//       supplies P^T for keys 8 g4 .. + 7 of row i (its own probabilities) and, by one ds_read_b64_tr_b8, the V bytes
-//       of those keys at dim 16 c + i.
+// Lane roles (lane = 16 g4 + i), per 32-key sub-tile:
+//   QK  S^T[key, row] = K[key, :] . Q[row, :] per 16-key half a: lane (g4, i) feeds key 8 (i / 4) + 4 a + i % 4.
+//       FP8: its bytes 32 g4 .. + 31 straight from LDS into v_mfma_scale_f32_16x16x128_f8f6f4 against the query's
+//       two exact e4m3fn parts (below); bf16: elements 32 s + 8 g4 .. + 7 per step s into v_mfma_f32_16x16x32_bf16.
+//       The result hands lane (g4, i) keys 8 g4 + 4 a + r (r < 4) of row i: over both halves the 8 consecutive keys
+//       8 g4 .. 8 g4 + 7.
+//   PV  O^T[dim, row] += V^T[dim, key] . P^T[key, row] per 16-dim tile c (v_mfma_f32_16x16x32_bf16): lane (g4, i)
+//       supplies P^T for keys 8 g4 .. + 7 of row i (its own probabilities) and V^T's bf16 values of those keys at
+//       dim 16 c + i, from a V^T the 4 waves convert once per tile into LDS.
 //   acc lane (g4, i) holds row i at dims 16 c + 4 g4 + r.
 // Online softmax in the log2 domain with a lazily moved reference maximum (as the decode kernels). Keys that no row
 // of the block may see (past the chunk, or on an invalid page) have their V bytes zeroed in registers, so stale
@@ -71,9 +73,11 @@ constexpr float kPrefillRescaleSlack = 8.0f;
 constexpr int kPrefillBufferFlags = 0x00020000;  // dword 3 of a raw buffer resource (gfx9 family)
 
 // BUF: each cache is under 4 GiB, so its tiles load through a buffer resource (the page base a uniform SGPR offset);
-// otherwise through 64-bit addresses.
+// otherwise through 64-bit addresses. The buffer forms of head dim 64 and of bf16 pools fit three workgroups' waves
+// per SIMD (at most 168 VGPRs, no spill); the others take two.
 template <int D, bool BUF, int ESZ>
-__global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((BUF && (D == 64 || ESZ == 2)) ? 3 : 2)))
+void prefill_gqa_kernel(PrefillArgs a) {
   using Geo = PrefillGeo<D, ESZ>;
   constexpr int ROWB = Geo::ROWB;
   constexpr int CH = Geo::CH, STRIDE = Geo::STRIDE, RS = Geo::RS, HALF = Geo::HALF, SLOT = Geo::SLOT;
@@ -179,7 +183,8 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
   const int64_t head_stride = (int64_t)a.P * ROWB;  // bytes between KV heads of one page
 
   int32_t p0 = 0;  // first page index staged in sm_pages
-  auto page_of = [&](int32_t key) -> int32_t { return sm_pages[key / a.P - p0]; };  // -1: invalid
+  const bool p_pow2 = (a.P & (a.P - 1)) == 0;  // uniform: the page column of a key is a shift
+  const int p_shift = __builtin_ctz((uint32_t)a.P);
   // This wave's DMAs of a tile: the m-th is DMA j = wave + 4 m of the tile (K for j < NDMA, then V), whose 64 lanes
   // fill LDS chunks 64 jj .. 64 jj + 63 of the K or V rows. Its rows span at most two 16-key groups (glo and glo + 1;
   // a group lies in one page): per lane, the byte offset inside the group and whether the lane's row is in glo + 1.
@@ -206,40 +211,40 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
       (void*)a.k_cache, (short)0, BUF ? (int)(uint32_t)cache_bytes : 0, kPrefillBufferFlags);
   const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)a.v_cache, (short)0, BUF ? (int)(uint32_t)cache_bytes : 0, kPrefillBufferFlags);
-  auto issue = [&](int32_t t, int slot) {
-    const int32_t k0 = TK * t;
-    int64_t base[TK / 16 + 1];  // byte offset of each 16-key group's first row (one page), and a spare
-#pragma unroll
-    for (int u = 0; u < TK / 16; ++u)
-      base[u] =
-          ((int64_t)max(page_of(k0 + 16 * u), 0) * a.G + g) * head_stride + (int64_t)((k0 + 16 * u) % a.P) * ROWB;
-    base[TK / 16] = base[TK / 16 - 1];
+  // Tile t's DMAs, and its pages' validity (bit u: the page of keys TK t + 16 u .. + 15 is valid; uniform), which
+  // the tile's compute takes. Lane u (lanes past the tile's groups repeat its last, the spare a DMA whose rows end
+  // in the last group reads) looks up its 16-key group's page and computes the group's byte offset, so the tile's
+  // page lookups are one LDS round trip and its address arithmetic vector work; each DMA reads its two groups'
+  // offsets with lane reads.
+  auto issue = [&](int32_t t, int slot) -> uint32_t {
+    const int32_t key = TK * t + 16 * min(lane, TK / 16 - 1);
+    const int32_t col = p_pow2 ? key >> p_shift : key / a.P;
+    const int32_t pg = sm_pages[col - p0];  // -1: invalid
+    const int64_t goff = ((int64_t)max(pg, 0) * a.G + g) * head_stride + (int64_t)(key - col * a.P) * ROWB;
+    const uint32_t pg_ok = (uint32_t)__ballot(pg >= 0) & ((1u << (TK / 16)) - 1u);
 #pragma unroll
     for (int m = 0; m < MW; ++m) {
       if (m >= cnt) break;
       const int j = wave + 4 * m;
-      int64_t blo = base[0], bhi = base[1];
-#pragma unroll
-      for (int u = 1; u < TK / 16; ++u)
-        if (dma_glo[m] == u) blo = base[u], bhi = base[u + 1];
       const uint32_t lds = ring + slot * SLOT + dma_lds[m];
       if (Geo::TAIL < 64 && (dma_pk[m] >> 30 & 1u)) continue;
-      if constexpr (BUF) {
-        const uint32_t voff = (uint32_t)((dma_pk[m] >> 31) ? bhi : blo) + (dma_pk[m] & 0x3fffffffu);  // < 4 GiB
+      if constexpr (BUF) {  // offsets < 4 GiB
+        const uint32_t blo = __builtin_amdgcn_readlane((uint32_t)goff, dma_glo[m]);
+        const uint32_t bhi = __builtin_amdgcn_readlane((uint32_t)goff, dma_glo[m] + 1);
+        const uint32_t voff = ((dma_pk[m] >> 31) ? bhi : blo) + (dma_pk[m] & 0x3fffffffu);
         dma_buffer16(j < NDMA ? k_rsrc : v_rsrc, lds, voff);
       } else {
+        const int64_t blo = readlane_i64(goff, dma_glo[m]), bhi = readlane_i64(goff, dma_glo[m] + 1);
         const int64_t off = ((dma_pk[m] >> 31) ? bhi : blo) + (int64_t)(dma_pk[m] & 0x3fffffffu);
         dma_global16((j < NDMA ? a.k_cache : a.v_cache) + off, lds);
       }
     }
+    return pg_ok;
   };
 
-  auto compute = [&](int32_t t, int slot) {
+  auto compute = [&](int32_t t, int slot, uint32_t pg_ok) {  // pg_ok: the tile's page validity, from its issue
     const uint8_t* K = &sm_ring[slot * SLOT];
     const int32_t k0 = TK * t;
-    uint32_t pg_ok = 0;  // bit u: the page of keys k0 + 16 u .. + 15 is valid (uniform)
-#pragma unroll
-    for (int u = 0; u < TK / 16; ++u) pg_ok |= (uint32_t)(page_of(k0 + 16 * u) >= 0) << u;
     // a full tile: every key valid and visible to every row of the block
     const bool full = pg_ok == (1u << (TK / 16)) - 1 && k0 + TK - 1 <= pos0 &&
                       (a.window == 0 || k0 > hi - 1 - a.window);
@@ -253,9 +258,9 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
         for (int n = 0; n < 2; ++n) st[u][h][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < NSUB; ++u) {
+      if constexpr (ESZ == 2) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if constexpr (ESZ == 2) {
+        for (int h = 0; h < 2; ++h) {
           // bf16 K: elements 32 s + 8 g4 .. + 7 of the lane's key, one 16-byte LDS read per step
           const uint8_t* kr = K + (32 * u + 8 * (li >> 2) + 4 * h + (li & 3)) * RS + 16 * g4;
 #pragma unroll
@@ -265,21 +270,32 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
 #pragma unroll
             for (int n = 0; n < 2; ++n) st[u][h][n] = mfma_16x16x32_bf16(kop, qf[n][s], st[u][h][n]);
           }
-          continue;
         }
-        // the K bytes of the lane's key, dims 32 g4 .. + 31, straight from LDS (e4m3fn, no conversion)
-        uint32_t kop[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (32 * g4 < D) {
-          const uint8_t* kr = K + (32 * u + 8 * (li >> 2) + 4 * h + (li & 3)) * RS + 32 * g4;
-          const uint4 w0 = *reinterpret_cast<const uint4*>(kr), w1 = *reinterpret_cast<const uint4*>(kr + 16);
-          kop[0] = w0.x, kop[1] = w0.y, kop[2] = w0.z, kop[3] = w0.w;
-          kop[4] = w1.x, kop[5] = w1.y, kop[6] = w1.z, kop[7] = w1.w;
+      }
+      if constexpr (ESZ == 1) {
+        // the K bytes of the lane's key in each half, dims 32 g4 .. + 31, straight from LDS (e4m3fn, no
+        // conversion); the four (half, N tile) products' hi parts first, then their lo parts, so no MFMA waits on
+        // the one before it
+        uint32_t kop[2][8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) kop[h][e] = 0;
+          if (32 * g4 < D) {
+            const uint8_t* kr = K + (32 * u + 8 * (li >> 2) + 4 * h + (li & 3)) * RS + 32 * g4;
+            const uint4 w0 = *reinterpret_cast<const uint4*>(kr), w1 = *reinterpret_cast<const uint4*>(kr + 16);
+            kop[h][0] = w0.x, kop[h][1] = w0.y, kop[h][2] = w0.z, kop[h][3] = w0.w;
+            kop[h][4] = w1.x, kop[h][5] = w1.y, kop[h][6] = w1.z, kop[h][7] = w1.w;
+          }
         }
 #pragma unroll
-        for (int n = 0; n < 2; ++n) {
-          st[u][h][n] = mfma_16x16x128_fp8(kop, qhi[n], st[u][h][n], qsc_hi[n]);
-          st[u][h][n] = mfma_16x16x128_fp8(kop, qlo[n], st[u][h][n], qsc_lo[n]);
-        }
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int n = 0; n < 2; ++n) st[u][h][n] = mfma_16x16x128_fp8(kop[h], qhi[n], st[u][h][n], qsc_hi[n]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int n = 0; n < 2; ++n) st[u][h][n] = mfma_16x16x128_fp8(kop[h], qlo[n], st[u][h][n], qsc_lo[n]);
       }
     }
     // scores (log2 domain) of keys k0 + 32 u + 8 g4 + j, j = 4 h + r; a tile that is not full masks them in one block
@@ -360,15 +376,31 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
   // goes to wave e % 4, whose lane (g4, i) reads keys 32 u + 8 g4 .. + 7 at dim 16 c + i (one ds_read_b64_tr_b8),
   // converts them and stores the 16 bytes at row 16 c + i. Keys no row may see (past the chunk or on an invalid
   // page) are zeroed, since a stale NaN would survive p = 0.
-  auto convert_v = [&](int32_t t, int slot) {
+  auto convert_v = [&](int32_t t, int slot, uint32_t pg_ok) {
+    constexpr int NQ = NSUB * NC / 4;  // this wave's (sub-tile, dim tile) pairs
     const uint8_t* V = &sm_ring[slot * SLOT] + HALF;
     const int32_t k0 = TK * t;
-    uint32_t pg_ok = 0;
-#pragma unroll
-    for (int u = 0; u < TK / 16; ++u) pg_ok |= (uint32_t)(page_of(k0 + 16 * u) >= 0) << u;
     const bool clean = pg_ok == (1u << (TK / 16)) - 1 && k0 + TK <= hi;
+    // every pair's LDS reads first, then the conversions and the V^T stores: a store between two reads would hold
+    // the second read back until the first has returned (the compiler cannot tell the two arrays apart here)
+    uint32_t raw[NQ][ESZ == 2 ? 8 : 2];
 #pragma unroll
-    for (int q = 0; q < NSUB * NC / 4; ++q) {
+    for (int q = 0; q < NQ; ++q) {
+      const int e = wave + 4 * q;
+      const int u = e / NC, c = e % NC;
+      if constexpr (ESZ == 2) {
+        // bf16 V: the 8 keys' elements at dim 16 c + i, one 2-byte LDS read each
+        const uint8_t* vr = V + (32 * u + 8 * g4) * RS + 2 * (16 * c + li);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) raw[q][k] = *reinterpret_cast<const uint16_t*>(vr + k * RS);
+      } else {
+        const uint2 vw = lds_read_tr8(V + (32 * u + 8 * g4 + (li >> 1)) * RS + 8 * (li & 1) + 16 * c);
+        raw[q][0] = vw.x;
+        raw[q][1] = vw.y;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
       const int e = wave + 4 * q;
       const int u = e / NC, c = e % NC;
       uint32_t vm0 = 0xffffffffu, vm1 = 0xffffffffu;
@@ -380,21 +412,16 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
       }
       uint32_t o[4];
       if constexpr (ESZ == 2) {
-        // bf16 V: the 8 keys' elements at dim 16 c + i, one 2-byte LDS read each (the byte masks select whole values)
-        const uint8_t* vr = V + (32 * u + 8 * g4) * RS + 2 * (16 * c + li);
-        uint32_t e[8];
+        // (the byte masks select whole values)
 #pragma unroll
-        for (int k = 0; k < 8; ++k) e[k] = *reinterpret_cast<const uint16_t*>(vr + k * RS);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) o[k] = e[2 * k] | (e[2 * k + 1] << 16);
+        for (int k = 0; k < 4; ++k) o[k] = raw[q][2 * k] | (raw[q][2 * k + 1] << 16);
         o[0] &= (vm0 & 0xffu ? 0xffffu : 0u) | (vm0 & 0xff00u ? 0xffff0000u : 0u);
         o[1] &= (vm0 & 0xff0000u ? 0xffffu : 0u) | (vm0 & 0xff000000u ? 0xffff0000u : 0u);
         o[2] &= (vm1 & 0xffu ? 0xffffu : 0u) | (vm1 & 0xff00u ? 0xffff0000u : 0u);
         o[3] &= (vm1 & 0xff0000u ? 0xffffu : 0u) | (vm1 & 0xff000000u ? 0xffff0000u : 0u);
       } else {
-        const uint2 vw = lds_read_tr8(V + (32 * u + 8 * g4 + (li >> 1)) * RS + 8 * (li & 1) + 16 * c);
-        fp8x4_to_bf16x4(vw.x & vm0, o[0], o[1]);
-        fp8x4_to_bf16x4(vw.y & vm1, o[2], o[3]);
+        fp8x4_to_bf16x4(raw[q][0] & vm0, o[0], o[1]);
+        fp8x4_to_bf16x4(raw[q][1] & vm1, o[2], o[3]);
       }
       *reinterpret_cast<uint4*>(&sm_vt[(16 * c + li) * Geo::VT_RS + (32 * u + 8 * g4) * 2]) = make_uint4(o[0], o[1], o[2],
                                                                                                        o[3]);
@@ -421,14 +448,15 @@ __global__ __launch_bounds__(256) void prefill_gqa_kernel(PrefillArgs a) {
     __syncthreads();
     const int32_t n = c1 - c0;
     static_assert(DEPTH == 2, "tile i + 1 loads while tile i computes");
-    issue(c0, 0);
+    uint32_t pg_cur = issue(c0, 0);
     for (int32_t i = 0; i < n; ++i) {
       wait_vmcnt<0>();  // this wave's DMAs of tile i have landed (tile i + 1 is not issued yet)
       // every wave's DMAs of tile i have landed; every wave is done with tile i - 1 (its slot and sm_vt are free)
       __syncthreads();
-      if (i + 1 < n) issue(c0 + i + 1, (i + 1) % DEPTH);
-      convert_v(c0 + i, i % DEPTH);
-      compute(c0 + i, i % DEPTH);
+      const uint32_t pg_next = i + 1 < n ? issue(c0 + i + 1, (i + 1) % DEPTH) : 0u;
+      convert_v(c0 + i, i % DEPTH, pg_cur);
+      compute(c0 + i, i % DEPTH, pg_cur);
+      pg_cur = pg_next;
     }
   }
 

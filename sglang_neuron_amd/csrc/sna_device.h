@@ -216,6 +216,12 @@ __device__ __forceinline__ void dma_global16(const void* src, uint32_t lds) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt" ::"s"(m0), "v"(src) : "memory");
 }
+// Lane `src`'s 64-bit value (uniform), as two lane reads.
+__device__ __forceinline__ int64_t readlane_i64(int64_t v, int src) {
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)(uint64_t)v, src);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)v >> 32), src);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");

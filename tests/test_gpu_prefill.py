@@ -61,6 +61,7 @@ CASES = [
     ("bf16-qwen3-0.6b", 8, dict(H=16, G=8, d=128, P=16, priors=(0, 300, 77), lens=(128, 45, 200), bf16=True), 0, False),
     ("bf16-swa-sinks-d64", 10, dict(H=8, G=2, d=64, P=32, priors=(500, 3), lens=(70, 130), bf16=True), 96, True),
     ("bf16-long-prior", 11, dict(H=4, G=1, d=128, P=16, priors=(34000,), lens=(20,), bf16=True), 0, False),
+    ("fp8-long-window-page64", 13, dict(H=16, G=4, d=128, P=64, priors=(70000, 3000), lens=(100, 70)), 40000, True),
 ]
 
 

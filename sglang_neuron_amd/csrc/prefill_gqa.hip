@@ -19,7 +19,8 @@
 //       8 g4 .. 8 g4 + 7.
 //   PV  O^T[dim, row] += V^T[dim, key] . P^T[key, row] per 16-dim tile c (v_mfma_f32_16x16x32_bf16): lane (g4, i)
 //       supplies P^T for keys 8 g4 .. + 7 of row i (its own probabilities) and V^T's bf16 values of those keys at
-//       dim 16 c + i, from a V^T the 4 waves convert once per tile into LDS.
+//       dim 16 c + i: FP8, one ds_read_b64_tr_b8 of the ring's V rows converted in registers; bf16, from a V^T the
+//       4 waves build once per tile in LDS.
 //   acc lane (g4, i) holds row i at dims 16 c + 4 g4 + r.
 // Online softmax in the log2 domain with a lazily moved reference maximum (as the decode kernels). Keys that no row
 // of the block may see (past the chunk, or on an invalid page) have their V bytes zeroed in registers, so stale
@@ -88,7 +89,7 @@ void prefill_gqa_kernel(PrefillArgs a) {
   typedef __attribute__((address_space(3))) uint8_t lds_u8;
   __shared__ __attribute__((aligned(16))) uint8_t sm_ring[DEPTH * SLOT];
   __shared__ int32_t sm_pages[Geo::PAGES];
-  // The current tile's V, transposed and converted once (each wave a quarter): row d holds the TK keys' bf16 values.
+  // bf16 pools: the current tile's V, transposed once (each wave a quarter): row d holds the TK keys' values.
   __shared__ __attribute__((aligned(16))) uint8_t sm_vt[D * Geo::VT_RS];
 
   const int tid = threadIdx.x, lane = tid & 63, g4 = lane >> 4, li = lane & 15;
@@ -344,7 +345,9 @@ void prefill_gqa_kernel(PrefillArgs a) {
         for (int c = 0; c < NC; ++c) acc[n][c] *= alpha;
       }
     }
-    __syncthreads();  // sm_vt holds this tile's V^T (every wave's quarter)
+    if constexpr (ESZ == 2) __syncthreads();  // sm_vt holds this tile's V^T (every wave's quarter)
+    const uint8_t* Vt = &sm_ring[slot * SLOT] + HALF;
+    const bool vclean = pg_ok == (1u << (TK / 16)) - 1 && k0 + TK <= hi;
 #pragma unroll
     for (int u = 0; u < NSUB; ++u) {
       uint32_t pop[2][4];
@@ -362,67 +365,68 @@ void prefill_gqa_kernel(PrefillArgs a) {
         }
       }
       const uint8_t* Vr = &sm_vt[li * Geo::VT_RS + (32 * u + 8 * g4) * 2];
+      uint32_t vm0 = 0xffffffffu, vm1 = 0xffffffffu;
+      if (ESZ == 1 && !vclean) {
+        const bool page_ok = (pg_ok >> (2 * u + (g4 >> 1))) & 1u;
+        const int32_t nvalid = page_ok ? min(max(hi - (k0 + 32 * u + 8 * g4), 0), 8) : 0;  // keys below hi
+        vm0 = nvalid >= 4 ? 0xffffffffu : (1u << (8 * nvalid)) - 1u;
+        vm1 = nvalid >= 8 ? 0xffffffffu : nvalid <= 4 ? 0u : (1u << (8 * (nvalid - 4))) - 1u;
+      }
+      uint2 vraw[NC];
+      if constexpr (ESZ == 1) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) vraw[c] = lds_read_tr8(Vt + (32 * u + 8 * g4 + (li >> 1)) * RS + 8 * (li & 1) + 16 * c);
+      }
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        const uint4 w = *reinterpret_cast<const uint4*>(Vr + 16 * c * Geo::VT_RS);
-        const uint32_t vop[4] = {w.x, w.y, w.z, w.w};
+        uint32_t vop[4];
+        if constexpr (ESZ == 1) {
+          fp8x4_to_bf16x4(vraw[c].x & vm0, vop[0], vop[1]);
+          fp8x4_to_bf16x4(vraw[c].y & vm1, vop[2], vop[3]);
+        } else {
+          const uint4 w = *reinterpret_cast<const uint4*>(Vr + 16 * c * Geo::VT_RS);
+          vop[0] = w.x, vop[1] = w.y, vop[2] = w.z, vop[3] = w.w;
+        }
 #pragma unroll
         for (int n = 0; n < 2; ++n) acc[n][c] = mfma_16x16x32_bf16(vop, pop[n], acc[n][c]);
       }
     }
   };
 
-  // Tile t's V (ring slot `slot`) into sm_vt as bf16 V^T: pair e = (sub-tile u, dim tile c) of the tile's NSUB x NC
-  // goes to wave e % 4, whose lane (g4, i) reads keys 32 u + 8 g4 .. + 7 at dim 16 c + i (one ds_read_b64_tr_b8),
-  // converts them and stores the 16 bytes at row 16 c + i. Keys no row may see (past the chunk or on an invalid
-  // page) are zeroed, since a stale NaN would survive p = 0.
+  // bf16 pools (FP8 tiles read V^T straight from the ring): tile t's V (ring slot `slot`) into sm_vt as V^T. Pair
+  // e = (sub-tile u, dim tile c) of the tile's NSUB x NC goes to wave e % 4, whose lane (g4, i) reads keys
+  // 32 u + 8 g4 .. + 7 at dim 16 c + i and stores the 16 bytes at row 16 c + i. Keys no row may see (past the chunk
+  // or on an invalid page) are zeroed, since a stale NaN would survive p = 0.
   auto convert_v = [&](int32_t t, int slot, uint32_t pg_ok) {
     constexpr int NQ = NSUB * NC / 4;  // this wave's (sub-tile, dim tile) pairs
     const uint8_t* V = &sm_ring[slot * SLOT] + HALF;
     const int32_t k0 = TK * t;
     const bool clean = pg_ok == (1u << (TK / 16)) - 1 && k0 + TK <= hi;
-    // every pair's LDS reads first, then the conversions and the V^T stores: a store between two reads would hold
-    // the second read back until the first has returned (the compiler cannot tell the two arrays apart here)
-    uint32_t raw[NQ][ESZ == 2 ? 8 : 2];
+    // every pair's LDS reads first, then the V^T stores: a store between two reads would hold the second read back
+    // until the first has returned (the compiler cannot tell the two arrays apart here)
+    uint32_t raw[NQ][8];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int e = wave + 4 * q;
       const int u = e / NC, c = e % NC;
-      if constexpr (ESZ == 2) {
-        // bf16 V: the 8 keys' elements at dim 16 c + i, one 2-byte LDS read each
-        const uint8_t* vr = V + (32 * u + 8 * g4) * RS + 2 * (16 * c + li);
+      // the 8 keys' elements at dim 16 c + i, one 2-byte LDS read each
+      const uint8_t* vr = V + (32 * u + 8 * g4) * RS + 2 * (16 * c + li);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) raw[q][k] = *reinterpret_cast<const uint16_t*>(vr + k * RS);
-      } else {
-        const uint2 vw = lds_read_tr8(V + (32 * u + 8 * g4 + (li >> 1)) * RS + 8 * (li & 1) + 16 * c);
-        raw[q][0] = vw.x;
-        raw[q][1] = vw.y;
-      }
+      for (int k = 0; k < 8; ++k) raw[q][k] = *reinterpret_cast<const uint16_t*>(vr + k * RS);
     }
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int e = wave + 4 * q;
       const int u = e / NC, c = e % NC;
-      uint32_t vm0 = 0xffffffffu, vm1 = 0xffffffffu;
+      int32_t nvalid = 8;  // keys below hi on a valid page
       if (!clean) {
         const bool page_ok = (pg_ok >> (2 * u + (g4 >> 1))) & 1u;
-        const int32_t nvalid = page_ok ? min(max(hi - (k0 + 32 * u + 8 * g4), 0), 8) : 0;  // keys below hi
-        vm0 = nvalid >= 4 ? 0xffffffffu : (1u << (8 * nvalid)) - 1u;
-        vm1 = nvalid >= 8 ? 0xffffffffu : nvalid <= 4 ? 0u : (1u << (8 * (nvalid - 4))) - 1u;
+        nvalid = page_ok ? min(max(hi - (k0 + 32 * u + 8 * g4), 0), 8) : 0;
       }
       uint32_t o[4];
-      if constexpr (ESZ == 2) {
-        // (the byte masks select whole values)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) o[k] = raw[q][2 * k] | (raw[q][2 * k + 1] << 16);
-        o[0] &= (vm0 & 0xffu ? 0xffffu : 0u) | (vm0 & 0xff00u ? 0xffff0000u : 0u);
-        o[1] &= (vm0 & 0xff0000u ? 0xffffu : 0u) | (vm0 & 0xff000000u ? 0xffff0000u : 0u);
-        o[2] &= (vm1 & 0xffu ? 0xffffu : 0u) | (vm1 & 0xff00u ? 0xffff0000u : 0u);
-        o[3] &= (vm1 & 0xff0000u ? 0xffffu : 0u) | (vm1 & 0xff000000u ? 0xffff0000u : 0u);
-      } else {
-        fp8x4_to_bf16x4(raw[q][0] & vm0, o[0], o[1]);
-        fp8x4_to_bf16x4(raw[q][1] & vm1, o[2], o[3]);
-      }
+      for (int k = 0; k < 4; ++k)
+        o[k] = (2 * k < nvalid ? raw[q][2 * k] : 0u) | ((2 * k + 1 < nvalid ? raw[q][2 * k + 1] : 0u) << 16);
       *reinterpret_cast<uint4*>(&sm_vt[(16 * c + li) * Geo::VT_RS + (32 * u + 8 * g4) * 2]) = make_uint4(o[0], o[1], o[2],
                                                                                                        o[3]);
     }
@@ -454,7 +458,7 @@ void prefill_gqa_kernel(PrefillArgs a) {
       // every wave's DMAs of tile i have landed; every wave is done with tile i - 1 (its slot and sm_vt are free)
       __syncthreads();
       const uint32_t pg_next = i + 1 < n ? issue(c0 + i + 1, (i + 1) % DEPTH) : 0u;
-      convert_v(c0 + i, i % DEPTH, pg_cur);
+      if constexpr (ESZ == 2) convert_v(c0 + i, i % DEPTH, pg_cur);
       compute(c0 + i, i % DEPTH, pg_cur);
       pg_cur = pg_next;
     }

@@ -24,6 +24,10 @@ CASES = [
     ("cfg2-page128", 2, {"B": 8, "P": 128, "lens": (2000, 4096)}),
     ("bf16-page128", 1, {"B": 5, "P": 128, "lens": (100, 3000)}),
     ("cfg4-page128-sinks", 4, {"B": 6, "P": 128, "lens": (1000, 5000)}),
+    # page sizes that are multiples of 16 but not powers of two (columns and in-page slots by division)
+    ("fp8-page48", 2, {"B": 4, "P": 48, "lens": (50, 2000)}),
+    ("cfg4-swa-page48", 4, {"B": 5, "P": 48, "window": 128, "lens": (1, 3000)}),
+    ("bf16-page80", 1, {"B": 3, "P": 80, "lens": (2, 900)}),
     ("cfg2-32-splits", 2, {"B": 2, "lens": (8192, 8192)}),                # the combine's second chunk of 16 splits
     ("cfg4-64-splits", 4, {"B": 2, "lens": (8000, 8192)}),                # 4 chunks, sinks
     # GPT-OSS multipliers on other shapes (cfg4 itself runs with them): 8 KV heads, d128, and no sinks

@@ -18,6 +18,7 @@ MLA_CASES = [
     ("heads-8", {"B": 3, "H": 8, "lens": (20, 2000)}),
     ("heads-20", {"B": 2, "H": 20, "lens": (100, 1000)}),
     ("page-16", {"B": 3, "P": 16, "lens": (40, 900)}),
+    ("page-48", {"B": 3, "P": 48, "lens": (40, 3000)}),                 # a page that is not a power of two
     # page 128: the page the reference serves DeepSeek-V2 with (docs/model-recipes/deepseek-v2.md:122)
     ("cfg3-page128", {"B": 6, "P": 128, "lens": (1024, 16384)}),
     ("cfg3-full", {}),                                                   # the bench workload at its full size
@@ -83,6 +84,7 @@ MLA_BF16_CASES = [
     ("bf16-ragged", {"B": 6, "lens": (1, 300)}),
     ("bf16-heads-20", {"B": 2, "H": 20, "lens": (100, 1000)}),
     ("bf16-page-16", {"B": 3, "P": 16, "lens": (40, 900)}),
+    ("bf16-page-48", {"B": 3, "P": 48, "lens": (40, 3000)}),
     ("bf16-multi-row-ranges", {"B": 200, "H": 20, "lens": (1, 200)}),
 ]
 
@@ -103,6 +105,7 @@ DSA_CASES = [
     ("cfg5-small", {"B": 4, "pool_positions": 4096, "n_indices": 512, "recent": 128, "short_rows": (100, 300)}),
     ("cfg5-wide", {"B": 2, "pool_positions": 8192, "n_indices": 2048, "recent": 128, "short_rows": (1500,)}),
     ("page-16", {"B": 3, "P": 16, "pool_positions": 2048, "n_indices": 100, "recent": 16, "short_rows": (40,)}),
+    ("page-48", {"B": 3, "P": 48, "pool_positions": 4800, "n_indices": 300, "recent": 32, "short_rows": (200,)}),
     ("cfg5-page128", {"B": 4, "P": 128, "pool_positions": 8192, "n_indices": 2048, "recent": 128,
                       "short_rows": (600,)}),
     ("cfg5-full", {}),                                                   # the bench workload: 131072 positions per row

@@ -62,6 +62,9 @@ CASES = [
     ("bf16-swa-sinks-d64", 10, dict(H=8, G=2, d=64, P=32, priors=(500, 3), lens=(70, 130), bf16=True), 96, True),
     ("bf16-long-prior", 11, dict(H=4, G=1, d=128, P=16, priors=(34000,), lens=(20,), bf16=True), 0, False),
     ("fp8-long-window-page64", 13, dict(H=16, G=4, d=128, P=64, priors=(70000, 3000), lens=(100, 70)), 40000, True),
+    # pages that are multiples of 16 but not powers of two (the tile's page lookups divide)
+    ("fp8-page48-window", 14, dict(H=16, G=4, d=128, P=48, priors=(3000, 7), lens=(90, 60)), 500, False),
+    ("bf16-page48-sinks", 15, dict(H=8, G=2, d=64, P=48, priors=(100,), lens=(70,), bf16=True), 0, True),
 ]
 
 

@@ -858,14 +858,18 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
     auto issue = [&](uint32_t d, int32_t tile) {  // d: the slot's LDS address
       if constexpr (SPARSE) {
         const int32_t k0 = tile * 16 - kbase;
+        // every DMA's row id first, then the DMAs: a read between two DMAs (whose asm may touch memory) would wait
+        // for its own round trip before the next DMA could issue
+        int32_t row[NDMA];
+#pragma unroll
+        for (int j = 0; j < NDMA; ++j) row[j] = max(sm_rowid[k0 + (int32_t)(dma_src[j] >> 16)], 0);
 #pragma unroll
         for (int j = 0; j < NDMA; ++j) {
-          const int32_t row = max(sm_rowid[k0 + (int32_t)(dma_src[j] >> 16)], 0);
           if (j < NDMA - 1 || lane < Geo::TAIL) {
             if constexpr (!WIDE)
-              dma_buffer16(pool_rsrc, d + 1024 * j, (uint32_t)row * ROWB + (dma_src[j] & 0xffffu));
+              dma_buffer16(pool_rsrc, d + 1024 * j, (uint32_t)row[j] * ROWB + (dma_src[j] & 0xffffu));
             else
-              dma_global16(a.cache + (int64_t)row * ROWB + (dma_src[j] & 0xffffu), d + 1024 * j);
+              dma_global16(a.cache + (int64_t)row[j] * ROWB + (dma_src[j] & 0xffffu), d + 1024 * j);
           }
         }
       } else {

@@ -30,9 +30,11 @@ int32_t host_tiles(int32_t seq_len, int32_t window, int32_t tile) { return host_
 // The MLA / DSA stream split: every row's key tiles (at least one, so a row with no prior key still has a workgroup
 // to attend its own row) laid end to end, cut into n_ctas ranges of equal tile counts. A workgroup runs per CU (the
 // kernel's LDS holds one), so n_ctas is the CU count over the head groups, fewer when there are fewer tiles; a sparse workgroup resolves at
-// most kMlaMaxSplitKeys indices in LDS, and sparse rows are latency-bound gathers, so a sparse plan aims for 8 tiles
-// per workgroup (two per wave: every tile's gathers go out at once; measured on cfg5, 16 workgroups per 2048-index
-// row beat 8 by ~1.3 us and 4 by ~8 us).
+// most kMlaMaxSplitKeys indices in LDS, and sparse rows are latency-bound gathers, so a sparse plan aims for
+// kSparseTilesPerCta tiles per workgroup (about three per wave: every tile's gathers go out at once). Measured on
+// cfg5's 2048-index rows, 11 tiles (~12 workgroups a row) beat 8 (16 a row) by 0.5 us at 16 rows and 0.3 us at 8,
+// and tie at 4; 12 tiles and 8 workgroups a row were slower.
+constexpr int64_t kSparseTilesPerCta = 11;
 int plan_stream(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32_t max_seq_len, int32_t n_keys_per_row,
                 int32_t groups, int32_t num_cus, sna_split_plan* plan) {
   plan->device_split = 0;
@@ -85,7 +87,8 @@ int plan_stream(int32_t kind, const int32_t* host_seq_lens, int32_t B, int32_t m
   const int32_t cus = std::max(1, std::min((num_cus > 0 ? num_cus : 256) / groups, SNA_MAX_CTAS));
   int64_t n = 0;
   if (total > 0) {
-    n = kind == 1 ? std::min<int64_t>(cus, total) : std::min<int64_t>(cus, std::max<int64_t>((total + 7) / 8, 1));
+    n = kind == 1 ? std::min<int64_t>(cus, total)
+                  : std::min<int64_t>(cus, std::max<int64_t>((total + kSparseTilesPerCta - 1) / kSparseTilesPerCta, 1));
     // a sparse range holds at most kSparseCap tiles: equal ranges need ceil(total / cap) of them, and whole rows
     // (when every row gets a workgroup) need each row's ceil(tiles / cap) pieces
     if (kind == 2) {

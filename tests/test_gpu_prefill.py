@@ -3,6 +3,8 @@ the CPU oracle (oracle/attention.segmented_prefill) on the same pool bytes: with
 
 from __future__ import annotations
 
+import random
+
 import pytest
 import torch
 
@@ -85,6 +87,28 @@ def test_prefill_attention_matches_oracle(name, seed, cfg, window, sinks):
     want = oatt.segmented_prefill(q, kh, vh, table, q_start, priors, sm_scale=scale, k_scale=ks, v_scale=vs, sinks=sk,
                                   window=window)
     assert_close_attn(out.cpu(), want, name)
+
+
+def _random_shape(seed: int):
+    r = random.Random(seed)
+    G = r.choice([1, 2, 4, 8])
+    group = r.choice([g for g in (1, 2, 4, 8, 16) if G * g <= 64])
+    R = r.randint(1, 3)
+    cfg = dict(H=G * group, G=G, d=r.choice([64, 128]), P=r.choice([16, 32, 48, 64, 128]),
+               priors=tuple(r.randint(0, 3000) for _ in range(R)), lens=tuple(r.randint(1, 200) for _ in range(R)),
+               bf16=r.random() < 0.35)
+    return cfg, r.choice([0, 0, r.randint(16, 1500)]), r.random() < 0.4
+
+
+RANDOM_SEEDS = list(range(9400, 9410))
+
+
+@pytest.mark.parametrize("seed", RANDOM_SEEDS)
+def test_prefill_random_shape(seed):
+    """Seeded random shapes (groups, head dims, pages including non-powers of two, requests, windows, sinks, FP8 and
+    bf16 pools), drawn once from fixed seeds, against the oracle."""
+    cfg, window, sinks = _random_shape(seed)
+    test_prefill_attention_matches_oracle(f"random-{seed}", seed, cfg, window, sinks)
 
 
 def test_segmented_attention_reference_signature():

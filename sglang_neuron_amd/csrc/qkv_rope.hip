@@ -73,22 +73,26 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
   const bool head_ok = head < heads;
   const bool is_q = head < Hq, is_k = !is_q && head < Hq + Hkv, roped = head < Hq + Hkv;
   const bool first = sub < HALF;
-  const int64_t t0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * U;
+  // The wave's tokens are the same in every lane: from the wave index read once, every per-token address, the slot
+  // and its page are scalar work; the lanes add only their head's and their own 16-byte offsets.
+  const int32_t wave = __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
+  const int64_t t0 = ((int64_t)blockIdx.x * 4 + wave) * U;
+  const int32_t row_off = head * D + 8 * sub;  // the lane's offset in a token's projection row
 
-  // this wave's U tokens: the head rows, the rotation rows (Q and K) and the slots (K and V), all loads in flight
+  // this wave's U tokens: the head rows, the rotation rows (Q and K) and the slots, all loads in flight
   uint4 w[U], cw[U], sw[U];
   int64_t slot[U];
 #pragma unroll
   for (int k = 0; k < U; ++k) {
     const int64_t t = t0 + k;
     const bool live = t < n_tokens && head_ok;
-    w[k] = live ? ld16(qkv + t * qkv_stride + (int64_t)head * D + 8 * sub) : make_uint4(0, 0, 0, 0);
+    w[k] = live ? ld16(qkv + t * qkv_stride + row_off) : make_uint4(0, 0, 0, 0);
     cw[k] = sw[k] = make_uint4(0, 0, 0, 0);
     if (live && roped) {
       cw[k] = ld16(cosv + t * rope_stride + 8 * sub);
       sw[k] = ld16(sinv + t * rope_stride + 8 * sub);
     }
-    slot[k] = (live && !is_q) ? slots[t] : 0;
+    slot[k] = t < n_tokens ? slots[t] : 0;  // every token has a slot; a Q lane ignores it
   }
   // per head: the gamma (Q and K with the norm), the cache and its scale (K and V)
   uint32_t gg[4] = {0, 0, 0, 0};
@@ -110,6 +114,7 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
   uint8_t* const cache = is_k ? kc : vc;
   const bool p_pow2 = (P & (P - 1)) == 0;  // uniform: the slot's page and offset by shifts
   const int p_shift = __builtin_ctz((uint32_t)P);
+  const int64_t kv_off = ((int64_t)h * P) * D + 8 * sub;  // the lane's offset in a page (K and V lanes)
 
   const float sgn = first ? -1.0f : 1.0f;  // rotate-half: the first half takes the partner's value negated
 #pragma unroll
@@ -168,14 +173,15 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
       }
     }
     if (is_q) {
-      *reinterpret_cast<uint4*>(q_out + (t * Hq + head) * D + 8 * sub) = make_uint4(ob[0], ob[1], ob[2], ob[3]);
+      *reinterpret_cast<uint4*>(q_out + t * Hq * D + row_off) = make_uint4(ob[0], ob[1], ob[2], ob[3]);
       continue;
     }
-    // K (rotated) or V into the pool at the token's slot, as the MHA store writes it
+    // K (rotated) or V into the pool at the token's slot, as the MHA store writes it: element
+    // ((page * Hkv + h) * P + off) * D + 8 sub, the page's and the offset's part of it the same in every lane
     const int64_t sl = redirect_slot(slot[k], num_slots);
     const int64_t page = p_pow2 ? sl >> p_shift : sl / P;
     const int64_t off = p_pow2 ? sl & (P - 1) : sl % P;
-    const int64_t dst = ((page * Hkv + h) * P + off) * D + 8 * sub;
+    const int64_t dst = (page * Hkv * P + off) * D + kv_off;
     if constexpr (FP8) {
       uint32_t q8[2] = {0, 0};
       if (rcp_ok && !__any(nan)) {  // uniform: NaNs are rare, and only a wave that holds one takes their path

@@ -95,13 +95,17 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
     slot[k] = t < n_tokens ? slots[t] : 0;  // every token has a slot; a Q lane ignores it
   }
   // per head: the gamma (Q and K with the norm), the cache and its scale (K and V)
-  uint32_t gg[4] = {0, 0, 0, 0};
+  float gf[8];  // the lane's 8 gamma elements as floats, converted once for the wave's tokens
+#pragma unroll
+  for (int e = 0; e < 8; ++e) gf[e] = 0.0f;
   if (q_norm && head_ok && roped) {  // q_norm: uniform, both gammas or neither
     const uint4 gw = ld16((is_q ? q_norm : k_norm) + 8 * sub);
-    gg[0] = gw.x;
-    gg[1] = gw.y;
-    gg[2] = gw.z;
-    gg[3] = gw.w;
+    const uint32_t gg[4] = {gw.x, gw.y, gw.z, gw.w};
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      gf[2 * e2] = lo_f(gg[e2]);
+      gf[2 * e2 + 1] = hi_f(gg[e2]);
+    }
   }
   const int32_t h = head - Hq - (is_k ? 0 : Hkv);  // the KV head (K and V lanes)
   float scl = 1.0f, rs = 1.0f;
@@ -117,33 +121,52 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
   const int64_t kv_off = ((int64_t)h * P) * D + 8 * sub;  // the lane's offset in a page (K and V lanes)
 
   const float sgn = first ? -1.0f : 1.0f;  // rotate-half: the first half takes the partner's value negated
+  // _rms: gamma * (x32 * rsqrt(mean(x32^2) + eps)).to(bf16), rsqrt as 1 / sqrt (both correctly rounded). The sum of
+  // squares: each square rounded (pow(2)), a lane's 8 summed in sequence, then the head's LPH lane sums folded in
+  // halves (group_sum; every lane takes part in the shuffles). The U tokens' 1 / sqrt share one sequence: the head's
+  // lanes are cut into U runs of LPH / U, run k computes token k's, and the lanes fetch the other tokens' results
+  // from the runs that hold them.
+  float inv[U];
+#pragma unroll
+  for (int k = 0; k < U; ++k) inv[k] = 1.0f;
+  if (q_norm) {  // uniform
+    static_assert(U == 1 || U == 2, "the shared 1 / sqrt exchanges between U = 2 runs of a head's lanes");
+    float ss[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const uint32_t xk[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
+      float sk = 0.0f;
+      {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const float a = lo_f(xk[e2]), b = hi_f(xk[e2]);
+          sk = sk + a * a;
+          sk = sk + b * b;
+        }
+      }
+      ss[k] = group_sum<HALF>(sk);
+    }
+    // sqrtf: correctly rounded (__fsqrt_rn is the native one)
+    const float mine = 1.0f / sqrtf((U == 2 && !first ? ss[U - 1] : ss[0]) / (float)D + eps);
+    if constexpr (U == 1) {
+      inv[0] = mine;
+    } else {  // run 0 is the first half of the head's lanes, run 1 the second: the partner lane holds the other
+      const float other = __uint_as_float(partner<HALF>(__float_as_uint(mine)));
+      inv[0] = first ? mine : other;
+      inv[U - 1] = first ? other : mine;
+    }
+  }
 #pragma unroll
   for (int k = 0; k < U; ++k) {
     const int64_t t = t0 + k;
     const bool live = t < n_tokens && head_ok;
     uint32_t xp[4] = {w[k].x, w[k].y, w[k].z, w[k].w};  // the lane's 8 elements as bf16 pairs
-    if (q_norm) {  // uniform
-      // _rms: gamma * (x32 * rsqrt(mean(x32^2) + eps)).to(bf16), rsqrt as 1 / sqrt (both correctly rounded). The
-      // sum of squares: each square rounded (pow(2)), a lane's 8 summed in sequence, then the head's LPH lane sums
-      // folded in halves (group_sum; every lane takes part in the shuffles)
-      float ss = 0.0f;
-      {
-#pragma clang fp contract(off)
+    if (q_norm && live && roped) {
 #pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-          const float a = lo_f(xp[e2]), b = hi_f(xp[e2]);
-          ss = ss + a * a;
-          ss = ss + b * b;
-        }
-      }
-      ss = group_sum<HALF>(ss);
-      if (live && roped) {
-        const float inv = 1.0f / sqrtf(ss / (float)D + eps);  // sqrtf: correctly rounded (__fsqrt_rn is the native one)
-#pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-          const uint32_t n = cvt_pk(lo_f(xp[e2]) * inv, hi_f(xp[e2]) * inv);
-          xp[e2] = cvt_pk(lo_f(gg[e2]) * lo_f(n), hi_f(gg[e2]) * hi_f(n));
-        }
+      for (int e2 = 0; e2 < 4; ++e2) {
+        const uint32_t n = cvt_pk(lo_f(xp[e2]) * inv[k], hi_f(xp[e2]) * inv[k]);
+        xp[e2] = cvt_pk(gf[2 * e2] * lo_f(n), gf[2 * e2 + 1] * hi_f(n));
       }
     }
     // the partner's elements (every lane takes part in the shuffles)

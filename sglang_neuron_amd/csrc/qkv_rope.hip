@@ -28,7 +28,7 @@ __device__ __forceinline__ float hi_f(uint32_t v) { return __uint_as_float(v & 0
 // DPP row, where a rotation by 8 is that exchange; other widths go through the LDS crossbar.
 template <int HALF>
 __device__ __forceinline__ uint32_t partner(uint32_t v) {
-  if constexpr (HALF == 8) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, false);  // row_ror:8
+  if constexpr (HALF == 8) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, true);  // row_ror:8
   else return (uint32_t)__shfl_xor((int)v, HALF, 64);
 }
 
@@ -169,10 +169,12 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
         xp[e2] = cvt_pk(gf[2 * e2] * lo_f(n), gf[2 * e2 + 1] * hi_f(n));
       }
     }
-    // the partner's elements (every lane takes part in the shuffles)
-    uint32_t pw[4];
+    float xf[8];  // the lane's elements as floats
 #pragma unroll
-    for (int e2 = 0; e2 < 4; ++e2) pw[e2] = partner<HALF>(xp[e2]);
+    for (int e2 = 0; e2 < 4; ++e2) {
+      xf[2 * e2] = lo_f(xp[e2]);
+      xf[2 * e2 + 1] = hi_f(xp[e2]);
+    }
     if (!live) continue;
     uint32_t ob[4];
     bool nan = false;  // a NaN among the lane's 8 output elements
@@ -180,10 +182,15 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
       // rope(t) = t * c + cat(-t[D/2:], t[:D/2]) * s, every product and the sum rounded to bf16: each element's two
       // products by one pair conversion, the sum by the output's (sgn * r exact, so the FMA rounds once, as the sum)
       const uint32_t cc[4] = {cw[k].x, cw[k].y, cw[k].z, cw[k].w}, sc[4] = {sw[k].x, sw[k].y, sw[k].z, sw[k].w};
+      // The partner's elements: it is a lane of the same head, so it is live and roped too, and active here. The
+      // shuffles move floats, not pairs, so the partner's halves need no extraction of their own.
+      float pf[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pf[e] = __uint_as_float(partner<HALF>(__float_as_uint(xf[e])));
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
-        const uint32_t r0 = cvt_pk(lo_f(xp[e2]) * lo_f(cc[e2]), lo_f(pw[e2]) * lo_f(sc[e2]));
-        const uint32_t r1 = cvt_pk(hi_f(xp[e2]) * hi_f(cc[e2]), hi_f(pw[e2]) * hi_f(sc[e2]));
+        const uint32_t r0 = cvt_pk(xf[2 * e2] * lo_f(cc[e2]), pf[2 * e2] * lo_f(sc[e2]));
+        const uint32_t r1 = cvt_pk(xf[2 * e2 + 1] * hi_f(cc[e2]), pf[2 * e2 + 1] * hi_f(sc[e2]));
         const float y0 = fmaf(sgn, hi_f(r0), lo_f(r0)), y1 = fmaf(sgn, hi_f(r1), lo_f(r1));
         nan |= (y0 != y0) | (y1 != y1);
         ob[e2] = cvt_pk(y0, y1);
@@ -192,7 +199,7 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
         ob[e2] = xp[e2];
-        nan |= (lo_f(xp[e2]) != lo_f(xp[e2])) | (hi_f(xp[e2]) != hi_f(xp[e2]));
+        nan |= (xf[2 * e2] != xf[2 * e2]) | (xf[2 * e2 + 1] != xf[2 * e2 + 1]);
       }
     }
     if (is_q) {

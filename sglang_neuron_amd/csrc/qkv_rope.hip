@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
 #pragma unroll
   for (int k = 0; k < U; ++k) inv[k] = 1.0f;
   if (q_norm) {  // uniform
-    static_assert(U == 1 || U == 2, "the shared 1 / sqrt exchanges between U = 2 runs of a head's lanes");
+    static_assert(LPH % U == 0, "a head's lanes are cut into U equal runs");
     float ss[U];
 #pragma unroll
     for (int k = 0; k < U; ++k) {
@@ -147,14 +147,23 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
       }
       ss[k] = group_sum<HALF>(sk);
     }
+    constexpr int RUN = LPH / U;  // lanes per run
+    const int run = sub / RUN;     // this lane computes token `run`'s
+    float xs = ss[0];
+#pragma unroll
+    for (int k = 1; k < U; ++k) xs = run == k ? ss[k] : xs;
     // sqrtf: correctly rounded (__fsqrt_rn is the native one)
-    const float mine = 1.0f / sqrtf((U == 2 && !first ? ss[U - 1] : ss[0]) / (float)D + eps);
+    const float mine = 1.0f / sqrtf(xs / (float)D + eps);
     if constexpr (U == 1) {
       inv[0] = mine;
-    } else {  // run 0 is the first half of the head's lanes, run 1 the second: the partner lane holds the other
+    } else if constexpr (U == 2) {  // run 0 is the first half of the head's lanes: the partner lane holds the other
       const float other = __uint_as_float(partner<HALF>(__float_as_uint(mine)));
       inv[0] = first ? mine : other;
-      inv[U - 1] = first ? other : mine;
+      inv[1] = first ? other : mine;
+    } else {  // token k's from the lane of run k at this lane's place in its run
+      const int src = lane - sub + sub % RUN;
+#pragma unroll
+      for (int k = 0; k < U; ++k) inv[k] = __shfl(mine, src + k * RUN, 64);
     }
   }
 #pragma unroll

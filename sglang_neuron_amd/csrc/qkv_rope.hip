@@ -34,14 +34,16 @@ __device__ __forceinline__ uint32_t partner(uint32_t v) {
 
 // The sum over the head's lane group, in every lane of it, folded in halves: lane i adds the lane HALF away, then
 // HALF / 2, ..., 1 (every lane ends with the same bits, addition being commutative). DPP row rotations for a
-// 16-lane group (rotations by 8, 4, 2, 1 pair the same lanes there), xor shuffles else.
+// 16-lane group (rotations by 8, 4, 2, 1 pair the same lanes there), xor shuffles else. Every lane of the wave is
+// active where it is called, so the rotations' bound_ctrl (what a disabled source lane gives) changes nothing; set,
+// it lets each rotation fold into its add (v_add_f32_dpp).
 template <int HALF>
 __device__ __forceinline__ float group_sum(float v) {
   if constexpr (HALF == 8) {
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false));  // row_ror:8
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xf, 0xf, false));  // row_ror:4
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x122, 0xf, 0xf, false));  // row_ror:2
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x121, 0xf, 0xf, false));  // row_ror:1
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, true));  // row_ror:8
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xf, 0xf, true));  // row_ror:4
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x122, 0xf, 0xf, true));  // row_ror:2
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x121, 0xf, 0xf, true));  // row_ror:1
     return v;
   } else {
 #pragma unroll

@@ -123,6 +123,7 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
   const int64_t kv_off = ((int64_t)h * P) * D + 8 * sub;  // the lane's offset in a page (K and V lanes)
 
   const float sgn = first ? -1.0f : 1.0f;  // rotate-half: the first half takes the partner's value negated
+  const bool kv_wave = !__all(is_q);       // the wave holds K or V heads (uniform)
   // _rms: gamma * (x32 * rsqrt(mean(x32^2) + eps)).to(bf16), rsqrt as 1 / sqrt (both correctly rounded). The sum of
   // squares: each square rounded (pow(2)), a lane's 8 summed in sequence, then the head's LPH lane sums folded in
   // halves (group_sum; every lane takes part in the shuffles). The U tokens' 1 / sqrt share one sequence: the head's
@@ -198,13 +199,18 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
       float pf[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) pf[e] = __uint_as_float(partner<HALF>(__float_as_uint(xf[e])));
+      float y[8];
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
         const uint32_t r0 = cvt_pk(xf[2 * e2] * lo_f(cc[e2]), pf[2 * e2] * lo_f(sc[e2]));
         const uint32_t r1 = cvt_pk(xf[2 * e2 + 1] * hi_f(cc[e2]), pf[2 * e2 + 1] * hi_f(sc[e2]));
-        const float y0 = fmaf(sgn, hi_f(r0), lo_f(r0)), y1 = fmaf(sgn, hi_f(r1), lo_f(r1));
-        nan |= (y0 != y0) | (y1 != y1);
-        ob[e2] = cvt_pk(y0, y1);
+        y[2 * e2] = fmaf(sgn, hi_f(r0), lo_f(r0));
+        y[2 * e2 + 1] = fmaf(sgn, hi_f(r1), lo_f(r1));
+        ob[e2] = cvt_pk(y[2 * e2], y[2 * e2 + 1]);
+      }
+      if (FP8 && kv_wave) {  // uniform: only the FP8 store looks at NaNs, and a wave of Q heads stores none
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) nan |= (y[2 * e2] != y[2 * e2]) | (y[2 * e2 + 1] != y[2 * e2 + 1]);
       }
     } else {
 #pragma unroll

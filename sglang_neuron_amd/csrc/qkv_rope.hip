@@ -88,7 +88,8 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_store_kernel(
   for (int k = 0; k < U; ++k) {
     const int64_t t = t0 + k;
     const bool live = t < n_tokens && head_ok;
-    w[k] = live ? ld16(qkv + t * qkv_stride + row_off) : make_uint4(0, 0, 0, 0);
+    // the projection row is read once (non-temporal); cos / sin rows are read by every roped head group
+    w[k] = live ? ld16_stream(qkv + t * qkv_stride + row_off) : make_uint4(0, 0, 0, 0);
     cw[k] = sw[k] = make_uint4(0, 0, 0, 0);
     if (live && roped) {
       cw[k] = ld16(cosv + t * rope_stride + 8 * sub);

@@ -233,11 +233,11 @@ void prefill_gqa_kernel(PrefillArgs a) {
         const uint32_t blo = __builtin_amdgcn_readlane((uint32_t)goff, dma_glo[m]);
         const uint32_t bhi = __builtin_amdgcn_readlane((uint32_t)goff, dma_glo[m] + 1);
         const uint32_t voff = ((dma_pk[m] >> 31) ? bhi : blo) + (dma_pk[m] & 0x3fffffffu);
-        dma_buffer16(j < NDMA ? k_rsrc : v_rsrc, lds, voff);
+        dma_buffer16_cached(j < NDMA ? k_rsrc : v_rsrc, lds, voff);
       } else {
         const int64_t blo = readlane_i64(goff, dma_glo[m]), bhi = readlane_i64(goff, dma_glo[m] + 1);
         const int64_t off = ((dma_pk[m] >> 31) ? bhi : blo) + (int64_t)(dma_pk[m] & 0x3fffffffu);
-        dma_global16((j < NDMA ? a.k_cache : a.v_cache) + off, lds);
+        dma_global16_cached((j < NDMA ? a.k_cache : a.v_cache) + off, lds);
       }
     }
     return pg_ok;

@@ -197,7 +197,8 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint8_t* p) {
 // need. The buffer forms read through a buffer resource (a uniform base and size in SGPRs, a 32-bit offset per lane;
 // reads past the size return zeros). The LDS address is wave-uniform (readfirstlane keeps it in an SGPR for m0); the
 // s_nop covers the m0 write -> LDS-DMA hazard. The 16-byte forms carry the pool's pages, read once per decode: they
-// are non-temporal (nt), which measured ~5% faster on the MLA gathers.
+// are non-temporal (nt), which measured ~5% faster on the MLA gathers. The _cached forms are for pages that other
+// workgroups read again soon (prefill: every query block of a request reads the same keys), kept in the L2.
 typedef __attribute__((address_space(3))) void lds_ptr_t;
 __device__ __forceinline__ uint32_t lds_address(const lds_ptr_t* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
@@ -215,6 +216,15 @@ __device__ __forceinline__ void dma_buffer4(__amdgpu_buffer_rsrc_t r, uint32_t l
 __device__ __forceinline__ void dma_global16(const void* src, uint32_t lds) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt" ::"s"(m0), "v"(src) : "memory");
+}
+__device__ __forceinline__ void dma_buffer16_cached(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voff) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(r)
+               : "memory");
+}
+__device__ __forceinline__ void dma_global16_cached(const void* src, uint32_t lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src) : "memory");
 }
 // Lane `src`'s 64-bit value (uniform), as two lane reads.
 __device__ __forceinline__ int64_t readlane_i64(int64_t v, int src) {

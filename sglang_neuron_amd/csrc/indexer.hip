@@ -104,7 +104,8 @@ __global__ __launch_bounds__(256) void indexer_score_kernel(IndexerArgs a) {
   uint32_t ring[PD][8];
   auto fetch = [&](int t, uint32_t (&kb)[8]) {
     const uint8_t* kp = a.keys + ((int64_t)kofs[t] << 4) + 32 * g4;
-    const uint4 x0 = ld16_stream(kp), x1 = ld16_stream(kp + 16);
+    // plain loads: with the non-temporal hint the same stream measured ~3% slower
+    const uint4 x0 = ld16(kp), x1 = ld16(kp + 16);
     kb[0] = x0.x, kb[1] = x0.y, kb[2] = x0.z, kb[3] = x0.w, kb[4] = x1.x, kb[5] = x1.y, kb[6] = x1.z, kb[7] = x1.w;
   };
 #pragma unroll

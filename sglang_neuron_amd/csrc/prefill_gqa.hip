@@ -3,7 +3,9 @@
 // before the attention runs), optionally inside a sliding window and with a sink logit per head.
 //   reference: segmented_attention / _torch_segmented_attention (ops/attention/attention_segmented_cte.py:21-75)
 //
-// Work: one workgroup of 4 waves per (request, block of query tokens, KV head). Its 128 query rows are (token, head)
+// Work: one workgroup of 4 waves per (request, block of query tokens, KV head), dealt to the XCDs in contiguous runs
+// so the blocks that read one request's keys of a KV head share an L2 (the DMAs keep the default cache policy for
+// those rereads). Its 128 query rows are (token, head)
 // pairs, token-major (row = t * group + j for the group's query head j); wave w owns rows 32 w .. 32 w + 31 as two
 // 16-row MFMA N tiles. Keys run in tiles of 64 positions (FP8; 32 for bf16 pools) from the window's first key to
 // the block's last query, each tile NSUB sub-tiles of 32 keys. A tile's K and V rows are DMA'd into a 2-slot LDS

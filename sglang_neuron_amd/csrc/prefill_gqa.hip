@@ -547,7 +547,11 @@ extern "C" int sna_prefill_attention(const void* q, const void* k_cache, const v
   a.num_blocks = num_blocks;
   a.sm_scale = sm_scale;
   a.window = window;
-  const dim3 grid((unsigned)((max_q_len + a.bq - 1) / a.bq), (unsigned)R, (unsigned)num_kv_heads);
+  const int64_t qblocks = (max_q_len + a.bq - 1) / a.bq;
+  if (qblocks * R * num_kv_heads > (int64_t)UINT32_MAX)  // the kernel's XCD-aware order numbers them in 32 bits
+    return fail(SNA_ERR_INVALID_ARGUMENT, "prefill_attention: %lld query blocks x %d requests x %d KV heads exceed "
+                "the grid (split the batch)", (long long)qblocks, R, num_kv_heads);
+  const dim3 grid((unsigned)qblocks, (unsigned)R, (unsigned)num_kv_heads);
   const int esz = kv_dtype == SNA_DTYPE_BF16 ? 2 : 1;
   const bool buf = num_blocks * num_kv_heads * (int64_t)page_size * head_dim * esz < ((int64_t)1 << 32);
   const hipStream_t s = (hipStream_t)stream;

@@ -139,6 +139,13 @@ def test_prefill_rejects_bad_pages_and_missing_scales():
     kc8 = torch.zeros(3, 2, 8, 64, dtype=torch.float8_e4m3fn, device=DEV)
     with pytest.raises(ValueError):
         ops.prefill_attention(q, kc8, kc8, *args[3:], max_q_len=4, sm_scale=1.0, k_scale=one, v_scale=one)
+    # more workgroups than the kernel numbers in 32 bits: refused before any launch
+    many = 65535
+    with pytest.raises(ValueError, match="exceed the grid"):
+        ops.prefill_attention(q, kc, kc, torch.zeros(many, 2, dtype=torch.int32, device=DEV),
+                              torch.zeros(many + 1, dtype=torch.int32, device=DEV),
+                              torch.zeros(many, dtype=torch.int32, device=DEV), max_q_len=2 ** 31 - 1, sm_scale=1.0,
+                              k_scale=one, v_scale=one)
 
 
 def test_prefill_takes_int64_tables_and_checks_host_offsets():

@@ -507,7 +507,11 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
   const int li = lane & 15;
   const int hg = blockIdx.y;  // 16-head group
   const int nh = min(16, a.H - 16 * hg);
-  const int32_t w = blockIdx.x;
+  // With spec query tokens per sequence (MTP verify), sibling tokens read mostly the same rows (the recent window,
+  // overlapping index lists, each other's own rows): the XCD-aware order puts a sequence's consecutive pieces on one
+  // XCD, so those rows come from its L2 (cfg5 at spec 8: 53.6 -> 50.3-51.1 us). With one token per row it measured
+  // neutral (MLA) or slightly slower (DSA), so those keep the launch order.
+  const int32_t w = (SPARSE && a.spec > 1) ? (int32_t)xcd_order(blockIdx.x, gridDim.x) : (int32_t)blockIdx.x;
 
   // LDS: each wave's ring of DEPTH tile slots (after a segment's tile loop: the merge exchange), the sparse row ids,
   // the waves' softmax statistics, the own row, the query operand (bf16 rows: in registers, the ring takes the

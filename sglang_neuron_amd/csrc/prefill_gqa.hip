@@ -96,13 +96,10 @@ void prefill_gqa_kernel(PrefillArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, g4 = lane >> 4, li = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // XCD-aware order: workgroup i of the launch runs on XCD i mod 8, so the linear ids are dealt out so that each XCD
-  // takes a contiguous run of the (query block, request, KV head) order, and the query blocks that read the same
-  // request's keys of one KV head share that XCD's L2 (a bijection on the grid whatever the hardware's placement).
-  const uint32_t nwg = gridDim.x * gridDim.y * gridDim.z;
-  const uint32_t hw = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-  const uint32_t per = nwg / 8, extra = nwg % 8, xcd = hw % 8;
-  const uint32_t lin = (xcd < extra ? xcd * (per + 1) : extra * (per + 1) + (xcd - extra) * per) + hw / 8;
+  // XCD-aware order: each XCD takes a contiguous run of the (query block, request, KV head) order, so the query
+  // blocks that read the same request's keys of one KV head share that XCD's L2
+  const uint32_t lin = xcd_order(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z),
+                                 gridDim.x * gridDim.y * gridDim.z);
   const int32_t bx = (int32_t)(lin % gridDim.x);
   const int32_t r = (int32_t)((lin / gridDim.x) % gridDim.y), g = (int32_t)(lin / (gridDim.x * gridDim.y));
   const int32_t qa = a.q_start[r];

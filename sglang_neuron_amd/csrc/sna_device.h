@@ -226,6 +226,14 @@ __device__ __forceinline__ void dma_global16_cached(const void* src, uint32_t ld
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src) : "memory");
 }
+// XCD-aware order: workgroup i of a launch runs on XCD i mod 8 (an in-bounds probe of the XCC_ID register showed it
+// for every workgroup of 256-, 512- and 1000-workgroup launches). xcd_order(i, n) deals the ids 0 .. n - 1 out so
+// that each XCD takes a contiguous run of the logical order (the first n mod 8 XCDs one item more), so consecutive
+// logical items share one XCD's L2. A bijection on [0, n) whatever the hardware's placement.
+__device__ __forceinline__ uint32_t xcd_order(uint32_t i, uint32_t n) {
+  const uint32_t per = n / 8, extra = n % 8, xcd = i % 8;
+  return (xcd < extra ? xcd * (per + 1) : extra * (per + 1) + (xcd - extra) * per) + i / 8;
+}
 // Lane `src`'s 64-bit value (uniform), as two lane reads.
 __device__ __forceinline__ int64_t readlane_i64(int64_t v, int src) {
   const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)(uint64_t)v, src);

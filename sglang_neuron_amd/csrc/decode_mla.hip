@@ -484,8 +484,8 @@ __device__ void merge_mask(const MlaArgs& a, __amdgpu_buffer_rsrc_t ro, __amdgpu
 // range is one segment, and the kernel is the segment loop's body once (the loop's carried state costs the one-segment
 // kernel its scalar registers). DEV: the stream split is cut from the device's seq_lens at the start of the launch
 // (device_split), not taken from the plan; the grid is the plan's bound, and workgroups past the split's ranges only
-// count themselves finished.
-template <int FMT, bool WIDE, bool MULTI, bool DEV = false>
+// count themselves finished. XORD: the XCD-aware order of the pieces (below; the sparse kernel with spec > 1).
+template <int FMT, bool WIDE, bool MULTI, bool DEV = false, bool XORD = false>
 __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
   constexpr int WAVES = 4;
   using Geo = TileGeo<FMT>;
@@ -510,8 +510,8 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
   // With spec query tokens per sequence (MTP verify), sibling tokens read mostly the same rows (the recent window,
   // overlapping index lists, each other's own rows): the XCD-aware order puts a sequence's consecutive pieces on one
   // XCD, so those rows come from its L2 (cfg5 at spec 8: 53.6 -> 50.3-51.1 us). With one token per row it measured
-  // neutral (MLA) or slightly slower (DSA), so those keep the launch order.
-  const int32_t w = (SPARSE && a.spec > 1) ? (int32_t)xcd_order(blockIdx.x, gridDim.x) : (int32_t)blockIdx.x;
+  // neutral (MLA) or slightly slower (DSA), so those keep the launch order, in their own instantiations.
+  const int32_t w = XORD ? (int32_t)xcd_order(blockIdx.x, gridDim.x) : (int32_t)blockIdx.x;
 
   // LDS: each wave's ring of DEPTH tile slots (after a segment's tile loop: the merge exchange), the sparse row ids,
   // the waves' softmax statistics, the own row, the query operand (bf16 rows: in registers, the ring takes the
@@ -1744,13 +1744,19 @@ extern "C" int sna_mla_decode_sparse(const void* q_absorbed, const void* q_pe, c
   const bool wide = num_blocks * page_size * (int64_t)RowFmt<ROWS640>::kRowBytes > 0xffffffffll;
   const dim3 grid(plan->n_ctas, groups);
   hipStream_t s = (hipStream_t)stream;
+#define SNA_DSA_LAUNCH(W, M)                                                                                  \
+  do {                                                                                                        \
+    if (spec > 1) hipLaunchKernelGGL((mla_decode_kernel<ROWS640, W, M, false, true>), grid, dim3(256), 0, s, a); \
+    else hipLaunchKernelGGL((mla_decode_kernel<ROWS640, W, M>), grid, dim3(256), 0, s, a);                     \
+  } while (0)
   if (wide) {
-    if (multi) hipLaunchKernelGGL((mla_decode_kernel<ROWS640, true, true>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((mla_decode_kernel<ROWS640, true, false>), grid, dim3(256), 0, s, a);
+    if (multi) SNA_DSA_LAUNCH(true, true);
+    else SNA_DSA_LAUNCH(true, false);
   } else {
-    if (multi) hipLaunchKernelGGL((mla_decode_kernel<ROWS640, false, true>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((mla_decode_kernel<ROWS640, false, false>), grid, dim3(256), 0, s, a);
+    if (multi) SNA_DSA_LAUNCH(false, true);
+    else SNA_DSA_LAUNCH(false, false);
   }
+#undef SNA_DSA_LAUNCH
   return check_launch("mla_decode_sparse");
 }
 
